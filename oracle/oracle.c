@@ -1,0 +1,566 @@
+/*
+ * CPU oracle: plain-C restatement of the onnx-light reference arithmetic for
+ * MatMulInteger, QLinearMatMul, DequantizeLinear and the fp16/bf16 MatMul that
+ * follows DequantizeLinear.  Test infrastructure only: the shipped HIP library
+ * never links or calls it.  Written from the reference's semantics (cited per
+ * function); the loop orders that fix rounding are kept, everything else is
+ * this file's own.  Build with -ffp-contract=off so no FMA is formed, matching
+ * a baseline x86-64 build of the reference (CMakeLists.txt adds no -march).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+static uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* Round-half-to-even of x / 2^s for an unsigned integer x and 1 <= s <= 31. */
+static uint32_t shr_rne(uint32_t x, unsigned s) {
+  const uint32_t q = x >> s;
+  const uint32_t rem = x & ((1u << s) - 1u);
+  const uint32_t half = 1u << (s - 1u);
+  return (rem > half || (rem == half && (q & 1u))) ? q + 1u : q;
+}
+
+/* FLOAT -> FLOAT16, round-to-nearest-even; NaN -> sign|0x7e00; overflow ->
+ * inf; fp32 subnormals -> signed zero.  rk/cast_helper.cc:51-87. */
+uint16_t orc_f32_to_f16(float f) {
+  const uint32_t u = f2u(f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const int32_t e32 = (int32_t)((u >> 23) & 0xffu);
+  const uint32_t m32 = u & 0x7fffffu;
+  if (e32 == 0xff) return (uint16_t)(sign | 0x7c00u | (m32 ? 0x0200u : 0u));
+  const int32_t e = e32 - 127 + 15; /* fp16 biased exponent */
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return sign;
+    /* subnormal: significand (with hidden bit) in units of 2^-24 */
+    return (uint16_t)(sign | shr_rne(m32 | 0x800000u, (unsigned)(14 - e)));
+  }
+  /* normal: exponent and mantissa shifted together so a carry bumps e */
+  return (uint16_t)(sign | shr_rne(((uint32_t)e << 23) | m32, 13));
+}
+
+/* FLOAT16 -> FLOAT, exact; NaN payload kept.  rk/cast_helper.cc:89-122. */
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  const uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+  const uint32_t man = (uint32_t)h & 0x3ffu;
+  if (exp == 0x1f) return u2f(sign | 0x7f800000u | (man << 13));
+  if (exp == 0) {
+    /* zero or subnormal: man * 2^-24, exact in float */
+    const float v = ldexpf((float)man, -24);
+    return sign ? -v : v;
+  }
+  return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* FLOAT -> BFLOAT16 round-to-nearest-even; NaN keeps its upper half with the
+ * quiet bit set.  rk/cast_helper.cc:124-134. */
+uint16_t orc_f32_to_bf16(float f) {
+  const uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  const uint64_t wide = (uint64_t)u + 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)((uint32_t)wide >> 16);
+}
+
+/* rk/cast_helper.cc:136-141. */
+float orc_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* FLOAT -> FLOAT8E4M3FN, saturating round-to-nearest-even: |v| beyond the
+ * largest finite 448 (and +-inf) -> +-448, NaN -> sign|0x7f, magnitudes below
+ * half the smallest subnormal 2^-9 -> +-0, fp32 subnormals -> +-0.
+ * rk/cast_float8.cc:27-81 (used to generate fp8 weights). */
+uint8_t orc_f32_to_f8e4m3fn(float v) {
+  const uint32_t u = f2u(v);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+  if (a == 0x7f800000u) return (uint8_t)(sign | 0x7eu);
+  const int32_t e = (int32_t)(a >> 23);
+  const uint32_t m = a & 0x7fffffu;
+  if (e == 0 || e < 117) return sign;
+  const int32_t E = e - 120; /* fp8 biased exponent when normal */
+  uint32_t mag;
+  if (E >= 1) {
+    mag = shr_rne(((uint32_t)E << 23) | m, 20);
+  } else {
+    /* subnormal target: value / 2^-9 = (m|2^23) / 2^(21-E) */
+    mag = shr_rne(m | 0x800000u, (unsigned)(21 - E));
+  }
+  if (mag > 0x7eu) mag = 0x7eu;
+  return (uint8_t)(sign | mag);
+}
+
+/* FLOAT8E4M3FN -> FLOAT, exact; 0x7f/0xff are NaN.  rk/cast_float8.cc:83-118. */
+float orc_f8e4m3fn_to_f32(uint8_t c) {
+  if (c == 0xffu) return u2f(0xffc00000u);
+  if (c == 0x7fu) return u2f(0x7fc00000u);
+  const int E = (c >> 3) & 0xf;
+  const int M = c & 7;
+  const float mag = (E == 0) ? ldexpf((float)M, -9) : ldexpf((float)(8 + M), E - 10);
+  return (c & 0x80u) ? -mag : mag;
+}
+
+/* Low nibble holds the even flat index.  rk/cast_sub_byte.h:57-60. */
+uint8_t orc_read_4bit(const uint8_t *data, int64_t i) {
+  const uint8_t byte = data[i >> 1];
+  return (uint8_t)((i & 1) ? (byte >> 4) : (byte & 0x0f));
+}
+
+/* Two's-complement 4-bit sign extension.  rk/cast_sub_byte.cc:81-88. */
+int8_t orc_int4_to_i8(uint8_t nibble) {
+  const int v = nibble & 0x0f;
+  return (int8_t)(v >= 8 ? v - 16 : v);
+}
+
+void orc_f32_to_f16_n(const float *s, int64_t n, uint16_t *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_f32_to_f16(s[i]);
+}
+void orc_f16_to_f32_n(const uint16_t *s, int64_t n, float *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_f16_to_f32(s[i]);
+}
+void orc_f32_to_bf16_n(const float *s, int64_t n, uint16_t *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_f32_to_bf16(s[i]);
+}
+void orc_bf16_to_f32_n(const uint16_t *s, int64_t n, float *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_bf16_to_f32(s[i]);
+}
+void orc_f32_to_f8e4m3fn_n(const float *s, int64_t n, uint8_t *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_f32_to_f8e4m3fn(s[i]);
+}
+void orc_f8e4m3fn_to_f32_n(const uint8_t *s, int64_t n, float *d) {
+  for (int64_t i = 0; i < n; ++i) d[i] = orc_f8e4m3fn_to_f32(s[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* SplitMix64 and the reference's samplers, rk/random.cc:32-106.             */
+
+uint64_t orc_splitmix64_next(uint64_t *state) {
+  *state += 0x9E3779B97F4A7C15ull;
+  uint64_t z = *state;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static double uniform53(uint64_t x) { return (double)(x >> 11) * (1.0 / 9007199254740992.0); }
+
+void orc_rand_uniform(uint64_t seed, int64_t n, double *out) {
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) out[i] = uniform53(orc_splitmix64_next(&s));
+}
+
+/* Uniform integers in [low, high) by rejection of the top partial span. */
+int orc_rand_int(int64_t low, int64_t high, uint64_t seed, int64_t n, int64_t *out) {
+  if (high <= low) return 1;
+  const uint64_t span = (uint64_t)(high - low);
+  const uint64_t limit = 0ull - ((0ull - span) % span); /* 2^64 - 2^64 % span (mod 2^64) */
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t x;
+    do {
+      x = orc_splitmix64_next(&s);
+    } while (limit != 0 && x >= limit);
+    out[i] = (int64_t)(x % span) + low;
+  }
+  return 0;
+}
+
+/* Irwin-Hall: sum of 12 uniforms minus 6, summed in double in draw order. */
+void orc_randn(uint64_t seed, int64_t n, double *out) {
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) {
+    double acc = 0.0;
+    for (int j = 0; j < 12; ++j) acc += uniform53(orc_splitmix64_next(&s));
+    out[i] = acc - 6.0;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* MatMul shape rules, km/matmul_shape_utils.h:24-106.                       */
+
+#define ORC_MAX_RANK 16
+
+typedef struct {
+  int64_t M, K, N;
+  int batch_rank;
+  int64_t out_prefix[ORC_MAX_RANK];
+  int64_t a_bstride[ORC_MAX_RANK]; /* element stride per output batch dim (0 = broadcast) */
+  int64_t b_bstride[ORC_MAX_RANK];
+  int64_t batch_count;
+} mm_plan;
+
+/* Builds the plan; returns 0 or the error code of orc_matmul_output_shape. */
+static int mm_make_plan(const int64_t *a_shape, int a_rank, const int64_t *b_shape, int b_rank,
+                        mm_plan *p) {
+  if (a_rank <= 0 || b_rank <= 0) return 1;
+  if (a_rank > ORC_MAX_RANK || b_rank > ORC_MAX_RANK) return 3;
+  int64_t a2[ORC_MAX_RANK + 1], b2[ORC_MAX_RANK + 1];
+  int ar = a_rank, br = b_rank;
+  if (a_rank == 1) {
+    a2[0] = 1;
+    a2[1] = a_shape[0];
+    ar = 2;
+  } else {
+    memcpy(a2, a_shape, sizeof(int64_t) * (size_t)a_rank);
+  }
+  if (b_rank == 1) {
+    b2[0] = b_shape[0];
+    b2[1] = 1;
+    br = 2;
+  } else {
+    memcpy(b2, b_shape, sizeof(int64_t) * (size_t)b_rank);
+  }
+  p->M = a2[ar - 2];
+  p->K = a2[ar - 1];
+  p->N = b2[br - 1];
+  if (p->K != b2[br - 2]) return 2;
+  const int ap = ar - 2, bp = br - 2;
+  const int rank = ap > bp ? ap : bp;
+  p->batch_rank = rank;
+  /* contiguous strides of the promoted operands */
+  int64_t as[ORC_MAX_RANK + 1], bs[ORC_MAX_RANK + 1];
+  as[ar - 1] = 1;
+  for (int i = ar - 2; i >= 0; --i) as[i] = as[i + 1] * a2[i + 1];
+  bs[br - 1] = 1;
+  for (int i = br - 2; i >= 0; --i) bs[i] = bs[i + 1] * b2[i + 1];
+  p->batch_count = 1;
+  for (int i = 0; i < rank; ++i) {
+    const int ia = i - (rank - ap), ib = i - (rank - bp);
+    const int64_t da = ia >= 0 ? a2[ia] : 1;
+    const int64_t db = ib >= 0 ? b2[ib] : 1;
+    int64_t d;
+    if (da == db || da == 1) {
+      d = db;
+    } else if (db == 1) {
+      d = da;
+    } else {
+      return 3;
+    }
+    p->out_prefix[i] = d;
+    p->a_bstride[i] = (ia >= 0 && a2[ia] != 1) ? as[ia] : 0;
+    p->b_bstride[i] = (ib >= 0 && b2[ib] != 1) ? bs[ib] : 0;
+    p->batch_count *= d;
+  }
+  return 0;
+}
+
+int orc_matmul_output_shape(const int64_t *a_shape, int a_rank, const int64_t *b_shape,
+                            int b_rank, int64_t *out_shape, int *out_rank) {
+  mm_plan p;
+  const int rc = mm_make_plan(a_shape, a_rank, b_shape, b_rank, &p);
+  if (rc) return rc;
+  int r = 0;
+  for (int i = 0; i < p.batch_rank; ++i) out_shape[r++] = p.out_prefix[i];
+  if (a_rank != 1) out_shape[r++] = p.M;
+  if (b_rank != 1) out_shape[r++] = p.N;
+  *out_rank = r;
+  return 0;
+}
+
+/* Element offsets of batch `batch` (row-major over out_prefix) in A and B. */
+static void mm_batch_base(const mm_plan *p, int64_t batch, int64_t *a_base, int64_t *b_base) {
+  int64_t ab = 0, bb = 0, rem = batch;
+  for (int d = p->batch_rank - 1; d >= 0; --d) {
+    const int64_t c = rem % p->out_prefix[d];
+    rem /= p->out_prefix[d];
+    ab += c * p->a_bstride[d];
+    bb += c * p->b_bstride[d];
+  }
+  *a_base = ab;
+  *b_base = bb;
+}
+
+static int32_t read_byte_elem(const void *t, int dtype, int64_t idx) {
+  return dtype == ORC_INT8 ? (int32_t)((const int8_t *)t)[idx] : (int32_t)((const uint8_t *)t)[idx];
+}
+
+/* km/kernel_matmul_integer.cc:89-176: i, j, k loops; int32 accumulate of
+ * (a - za[i]) * (b - zb[j]); the per-row zero point is indexed by i in every
+ * batch.  Unsigned arithmetic gives the two's-complement wrap of `acc`. */
+int orc_matmul_integer(const void *a, int a_dtype, const int64_t *a_shape, int a_rank,
+                       const void *b, int b_dtype, const int64_t *b_shape, int b_rank,
+                       const int32_t *a_zp, int64_t a_zp_count, const int32_t *b_zp,
+                       int64_t b_zp_count, int32_t *y) {
+  mm_plan p;
+  const int rc = mm_make_plan(a_shape, a_rank, b_shape, b_rank, &p);
+  if (rc) return rc;
+  const int64_t M = p.M, K = p.K, N = p.N;
+  for (int64_t bt = 0; bt < p.batch_count; ++bt) {
+    int64_t ab, bb;
+    mm_batch_base(&p, bt, &ab, &bb);
+    for (int64_t i = 0; i < M; ++i) {
+      const int32_t za = a_zp_count > 1 ? a_zp[i] : a_zp[0];
+      for (int64_t j = 0; j < N; ++j) {
+        const int32_t zb = b_zp_count > 1 ? b_zp[j] : b_zp[0];
+        uint32_t acc = 0;
+        for (int64_t k = 0; k < K; ++k) {
+          const int32_t av = read_byte_elem(a, a_dtype, ab + i * K + k);
+          const int32_t bv = read_byte_elem(b, b_dtype, bb + k * N + j);
+          acc += (uint32_t)(av - za) * (uint32_t)(bv - zb);
+        }
+        y[(bt * M + i) * N + j] = (int32_t)acc;
+      }
+    }
+  }
+  return 0;
+}
+
+/* kq/kernel_qlinearmatmul.cc:115-217: int64 accumulate, combined scale
+ * a_s*b_s/y_s in fp32 (left to right), (float)acc*cs, nearbyint (ties to
+ * even, before the zero point), + (float)y_zp, clamp, cast. */
+int orc_qlinear_matmul(const void *a, int a_dtype, const int64_t *a_shape, int a_rank,
+                       int32_t a_zp, float a_scale, const void *b, int b_dtype,
+                       const int64_t *b_shape, int b_rank, int32_t b_zp, float b_scale,
+                       float y_scale, int32_t y_zp, int y_dtype, void *y, int64_t row_begin,
+                       int64_t row_end) {
+  mm_plan p;
+  const int rc = mm_make_plan(a_shape, a_rank, b_shape, b_rank, &p);
+  if (rc) return rc;
+  const int64_t M = p.M, K = p.K, N = p.N;
+  if (row_end < 0 || row_end > M) row_end = M;
+  const float cs = a_scale * b_scale / y_scale;
+  const float zy = (float)y_zp;
+  const float lo = y_dtype == ORC_INT8 ? -128.0f : 0.0f;
+  const float hi = y_dtype == ORC_INT8 ? 127.0f : 255.0f;
+  for (int64_t bt = 0; bt < p.batch_count; ++bt) {
+    int64_t ab, bb;
+    mm_batch_base(&p, bt, &ab, &bb);
+    for (int64_t i = row_begin; i < row_end; ++i) {
+      for (int64_t j = 0; j < N; ++j) {
+        int64_t acc = 0;
+        for (int64_t k = 0; k < K; ++k) {
+          const int32_t av = read_byte_elem(a, a_dtype, ab + i * K + k);
+          const int32_t bv = read_byte_elem(b, b_dtype, bb + k * N + j);
+          acc += (int64_t)(av - a_zp) * (int64_t)(bv - b_zp);
+        }
+        float v = nearbyintf((float)acc * cs) + zy;
+        if (v < lo) {
+          v = lo;
+        } else if (v > hi) {
+          v = hi;
+        }
+        const int64_t yi = (bt * M + i) * N + j;
+        if (y_dtype == ORC_INT8) {
+          ((int8_t *)y)[yi] = (int8_t)v;
+        } else {
+          ((uint8_t *)y)[yi] = (uint8_t)v;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* DequantizeLinear, kq/kernel_dequantizelinear.cc.                           */
+
+static int64_t numel(const int64_t *s, int r) {
+  int64_t n = 1;
+  for (int i = 0; i < r; ++i) n *= s[i];
+  return n;
+}
+
+/* Decoded (float) quantized element i of x. */
+static float dq_decode(const void *x, int dtype, int64_t i) {
+  switch (dtype) {
+  case ORC_UINT8: return (float)((const uint8_t *)x)[i];
+  case ORC_INT8: return (float)((const int8_t *)x)[i];
+  case ORC_UINT16: return (float)((const uint16_t *)x)[i];
+  case ORC_INT16: return (float)((const int16_t *)x)[i];
+  case ORC_INT32: return (float)((const int32_t *)x)[i];
+  case ORC_FLOAT8E4M3FN: return orc_f8e4m3fn_to_f32(((const uint8_t *)x)[i]);
+  case ORC_INT4: return (float)orc_int4_to_i8(orc_read_4bit((const uint8_t *)x, i));
+  case ORC_UINT4: return (float)orc_read_4bit((const uint8_t *)x, i);
+  default: return 0.0f;
+  }
+}
+
+static int dq_supported(int dtype) {
+  switch (dtype) {
+  case ORC_UINT8: case ORC_INT8: case ORC_UINT16: case ORC_INT16: case ORC_INT32:
+  case ORC_FLOAT8E4M3FN: case ORC_INT4: case ORC_UINT4:
+    return 1;
+  default:
+    return 0;
+  }
+}
+
+/* Per-tensor: (x - zp) * s (:65-130).  Per-axis: scale index
+ * (i / inner) % axis_size (:237-242).  Blocked (scale rank == x rank): scale
+ * index sum_d (coord_d / (x_d / s_d)) * s_stride_d (:204-235).  Each value is
+ * (decode(x) - decode(zp)) * scale in fp32, then FLOAT16 RNE or kept FLOAT
+ * (:57-63, :247-285). */
+int orc_dequantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int x_rank,
+                          const void *scale, int scale_dtype, const int64_t *s_shape,
+                          int s_rank, const void *zp, int64_t axis, void *y) {
+  if (!dq_supported(x_dtype)) return 1;
+  if (scale_dtype != ORC_FLOAT && scale_dtype != ORC_FLOAT16) return 1;
+  const int64_t n = numel(x_shape, x_rank);
+  const int64_t ns = numel(s_shape, s_rank);
+  float *sc = (float *)malloc(sizeof(float) * (size_t)(ns > 0 ? ns : 1));
+  if (!sc) return 2;
+  for (int64_t i = 0; i < ns; ++i) {
+    sc[i] = scale_dtype == ORC_FLOAT16 ? orc_f16_to_f32(((const uint16_t *)scale)[i])
+                                       : ((const float *)scale)[i];
+  }
+  int64_t repeats[ORC_MAX_RANK], sstr[ORC_MAX_RANK], coord[ORC_MAX_RANK];
+  const int blocked = ns != 1 && s_rank == x_rank;
+  int64_t inner = 1, axis_size = 1;
+  if (ns != 1) {
+    if (axis < 0 || axis >= x_rank || x_rank > ORC_MAX_RANK) {
+      free(sc);
+      return 1;
+    }
+    if (blocked) {
+      int64_t st = 1;
+      for (int d = x_rank - 1; d >= 0; --d) {
+        sstr[d] = st;
+        st *= s_shape[d];
+        repeats[d] = s_shape[d] ? x_shape[d] / s_shape[d] : 1;
+        coord[d] = 0;
+      }
+    } else {
+      for (int d = (int)axis + 1; d < x_rank; ++d) inner *= x_shape[d];
+      axis_size = x_shape[axis];
+    }
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t si = 0;
+    if (ns != 1) {
+      if (blocked) {
+        for (int d = 0; d < x_rank; ++d) si += (coord[d] / repeats[d]) * sstr[d];
+        for (int d = x_rank - 1; d >= 0; --d) {
+          if (++coord[d] < x_shape[d]) break;
+          coord[d] = 0;
+        }
+      } else {
+        si = (i / inner) % axis_size;
+      }
+    }
+    const float zpv = zp ? dq_decode(zp, x_dtype, si) : 0.0f;
+    const float v = (dq_decode(x, x_dtype, i) - zpv) * sc[si];
+    if (scale_dtype == ORC_FLOAT16) {
+      ((uint16_t *)y)[i] = orc_f32_to_f16(v);
+    } else {
+      ((float *)y)[i] = v;
+    }
+  }
+  free(sc);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MatMul, km/kernel_matmul.cc:61-147 and :206-218.                          */
+
+typedef struct {
+  const mm_plan *p;
+  const float *a, *b;
+  float *y;
+  int64_t r0, r1; /* rows of every batch matrix */
+  int64_t part, nparts;
+} mm_job;
+
+static void *mm_worker(void *arg) {
+  const mm_job *j = (const mm_job *)arg;
+  const mm_plan *p = j->p;
+  const int64_t K = p->K, N = p->N, M = p->M;
+  const int64_t rows = j->r1 - j->r0;
+  const int64_t total = p->batch_count * rows;
+  const int64_t lo = total * j->part / j->nparts, hi = total * (j->part + 1) / j->nparts;
+  for (int64_t t = lo; t < hi; ++t) {
+    const int64_t bt = t / rows, i = j->r0 + t % rows;
+    int64_t ab, bb;
+    mm_batch_base(p, bt, &ab, &bb);
+    float *yr = j->y + (bt * M + i) * N;
+    for (int64_t c = 0; c < N; ++c) yr[c] = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float av = j->a[ab + i * K + k];
+      const float *br = j->b + bb + k * N;
+      for (int64_t c = 0; c < N; ++c) yr[c] += av * br[c];
+    }
+  }
+  return NULL;
+}
+
+int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank, const float *b,
+                   const int64_t *b_shape, int b_rank, float *y, int64_t row_begin,
+                   int64_t row_end, int nthreads) {
+  mm_plan p;
+  const int rc = mm_make_plan(a_shape, a_rank, b_shape, b_rank, &p);
+  if (rc) return rc;
+  if (row_end < 0 || row_end > p.M) row_end = p.M;
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > 256) nthreads = 256;
+  mm_job jobs[256];
+  pthread_t th[256];
+  for (int t = 0; t < nthreads; ++t) {
+    jobs[t].p = &p;
+    jobs[t].a = a;
+    jobs[t].b = b;
+    jobs[t].y = y;
+    jobs[t].r0 = row_begin;
+    jobs[t].r1 = row_end;
+    jobs[t].part = t;
+    jobs[t].nparts = nthreads;
+  }
+  for (int t = 1; t < nthreads; ++t) pthread_create(&th[t], NULL, mm_worker, &jobs[t]);
+  mm_worker(&jobs[0]);
+  for (int t = 1; t < nthreads; ++t) pthread_join(th[t], NULL);
+  return 0;
+}
+
+int orc_matmul_half(const uint16_t *a, const int64_t *a_shape, int a_rank, const uint16_t *b,
+                    const int64_t *b_shape, int b_rank, int dtype, uint16_t *y,
+                    int64_t row_begin, int64_t row_end, int nthreads) {
+  mm_plan p;
+  const int rc = mm_make_plan(a_shape, a_rank, b_shape, b_rank, &p);
+  if (rc) return rc;
+  if (dtype != ORC_FLOAT16 && dtype != ORC_BFLOAT16) return 4;
+  const int64_t na = numel(a_shape, a_rank), nb = numel(b_shape, b_rank);
+  const int64_t ny = p.batch_count * p.M * p.N;
+  float *af = (float *)malloc(sizeof(float) * (size_t)(na ? na : 1));
+  float *bf = (float *)malloc(sizeof(float) * (size_t)(nb ? nb : 1));
+  float *yf = (float *)calloc((size_t)(ny ? ny : 1), sizeof(float));
+  if (!af || !bf || !yf) {
+    free(af);
+    free(bf);
+    free(yf);
+    return 5;
+  }
+  if (dtype == ORC_FLOAT16) {
+    orc_f16_to_f32_n(a, na, af);
+    orc_f16_to_f32_n(b, nb, bf);
+  } else {
+    orc_bf16_to_f32_n(a, na, af);
+    orc_bf16_to_f32_n(b, nb, bf);
+  }
+  orc_matmul_f32(af, a_shape, a_rank, bf, b_shape, b_rank, yf, row_begin, row_end, nthreads);
+  if (row_end < 0 || row_end > p.M) row_end = p.M;
+  for (int64_t bt = 0; bt < p.batch_count; ++bt) {
+    for (int64_t i = row_begin; i < row_end; ++i) {
+      const int64_t o = (bt * p.M + i) * p.N;
+      if (dtype == ORC_FLOAT16) {
+        orc_f32_to_f16_n(yf + o, p.N, y + o);
+      } else {
+        orc_f32_to_bf16_n(yf + o, p.N, y + o);
+      }
+    }
+  }
+  free(af);
+  free(bf);
+  free(yf);
+  return 0;
+}

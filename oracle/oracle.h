@@ -1,0 +1,117 @@
+/*
+ * CPU oracle for the quantized-matmul path: a plain-C restatement of the
+ * onnx-light reference arithmetic, used ONLY as the parity checker (tests,
+ * smoke) and as the reported CPU baseline (bench.py `cpu_baseline`).  Nothing
+ * in the shipped library links or calls this code.
+ *
+ * Each function cites the reference file:line whose semantics it restates.
+ * Paths are relative to the onnx-light source tree:
+ *   km/ = onnx_light/onnx_extensions/kernels/kernels/math/
+ *   kq/ = onnx_light/onnx_extensions/kernels/kernels/quantization/
+ *   rk/ = onnx_light/onnx_core/runtime/kernels/
+ *
+ * Pinning (how each function is checked independently of this restatement;
+ * the tests live in tests/test_oracle_*.py):
+ *   codecs        - exhaustive over all 2^8 / 2^16 codes against closed forms
+ *                   (numpy float16, bit arithmetic), plus the reference's
+ *                   fp8 and fp16 known-answer bit patterns.
+ *   SplitMix64    - published first outputs of canonical SplitMix64, seed 0.
+ *   MatMulInteger - reference known-answer tests + brute force in numpy int64.
+ *   QLinearMatMul - reference known-answer tests (2-D u8/s8, ties-to-even,
+ *                   saturation) + numpy float32 closed form.
+ *   DequantizeLinear - reference known-answer tests (per-tensor, per-axis,
+ *                   blocked, fp16, fp8, int4/uint4) + numpy closed form.
+ *   MatMul fp16/bf16 - reference known-answer test + float64 bound.
+ * No function is "parity unpinned".
+ */
+#ifndef ONNXL_AMD_ORACLE_H_
+#define ONNXL_AMD_ORACLE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ONNX TensorProto.DataType codes used on this path. */
+enum {
+  ORC_FLOAT = 1, ORC_UINT8 = 2, ORC_INT8 = 3, ORC_UINT16 = 4, ORC_INT16 = 5,
+  ORC_INT32 = 6, ORC_FLOAT16 = 10, ORC_BFLOAT16 = 16, ORC_FLOAT8E4M3FN = 17,
+  ORC_UINT4 = 21, ORC_INT4 = 22
+};
+
+/* ---- scalar codecs ---- */
+uint16_t orc_f32_to_f16(float f);       /* rk/cast_helper.cc:51-87  */
+float orc_f16_to_f32(uint16_t h);       /* rk/cast_helper.cc:89-122 */
+uint16_t orc_f32_to_bf16(float f);      /* rk/cast_helper.cc:124-134 */
+float orc_bf16_to_f32(uint16_t b);      /* rk/cast_helper.cc:136-141 */
+uint8_t orc_f32_to_f8e4m3fn(float v);   /* rk/cast_float8.cc:27-81  */
+float orc_f8e4m3fn_to_f32(uint8_t v);   /* rk/cast_float8.cc:83-118 */
+uint8_t orc_read_4bit(const uint8_t *data, int64_t i); /* rk/cast_sub_byte.h:57-60 */
+int8_t orc_int4_to_i8(uint8_t nibble);  /* rk/cast_sub_byte.cc:81-88 */
+
+/* Bulk codec helpers (same semantics as the scalar ones). */
+void orc_f32_to_f16_n(const float *src, int64_t n, uint16_t *dst);
+void orc_f16_to_f32_n(const uint16_t *src, int64_t n, float *dst);
+void orc_f32_to_bf16_n(const float *src, int64_t n, uint16_t *dst);
+void orc_bf16_to_f32_n(const uint16_t *src, int64_t n, float *dst);
+void orc_f32_to_f8e4m3fn_n(const float *src, int64_t n, uint8_t *dst);
+void orc_f8e4m3fn_to_f32_n(const uint8_t *src, int64_t n, float *dst);
+
+/* ---- SplitMix64 (rk/random.cc:32-106) ---- */
+uint64_t orc_splitmix64_next(uint64_t *state);
+void orc_rand_uniform(uint64_t seed, int64_t n, double *out);
+int orc_rand_int(int64_t low, int64_t high, uint64_t seed, int64_t n, int64_t *out);
+void orc_randn(uint64_t seed, int64_t n, double *out);
+
+/* ---- MatMul shape rules (km/matmul_shape_utils.h:24-106) ----
+ * Writes the broadcast output shape; returns 0, or a nonzero code for
+ * rank-0 (1), inner-dimension mismatch (2) or batch broadcast failure (3). */
+int orc_matmul_output_shape(const int64_t *a_shape, int a_rank, const int64_t *b_shape,
+                            int b_rank, int64_t *out_shape, int *out_rank);
+
+/* ---- MatMulInteger (km/kernel_matmul_integer.cc:89-176) ----
+ * a/b are UINT8 or INT8 element arrays; a_zp has a_zp_count (1 or M) int32
+ * values, b_zp has b_zp_count (1 or N) values.  int32 accumulation with
+ * two's-complement wrap (the reference's int32 `acc`). */
+int orc_matmul_integer(const void *a, int a_dtype, const int64_t *a_shape, int a_rank,
+                       const void *b, int b_dtype, const int64_t *b_shape, int b_rank,
+                       const int32_t *a_zp, int64_t a_zp_count, const int32_t *b_zp,
+                       int64_t b_zp_count, int32_t *y);
+
+/* ---- QLinearMatMul (kq/kernel_qlinearmatmul.cc:115-217) ----
+ * Row range [row_begin, row_end) of every batch matrix is computed (the full
+ * job is row_begin=0, row_end=-1); used to time a bounded CPU sample. */
+int orc_qlinear_matmul(const void *a, int a_dtype, const int64_t *a_shape, int a_rank,
+                       int32_t a_zp, float a_scale, const void *b, int b_dtype,
+                       const int64_t *b_shape, int b_rank, int32_t b_zp, float b_scale,
+                       float y_scale, int32_t y_zp, int y_dtype, void *y, int64_t row_begin,
+                       int64_t row_end);
+
+/* ---- DequantizeLinear (kq/kernel_dequantizelinear.cc:65-693) ----
+ * scale is FLOAT or FLOAT16 (the output dtype follows it); zp may be NULL
+ * (zero point 0).  scale_count==1 selects per-tensor, scale_rank==x_rank
+ * blocked, otherwise per-axis.  Returns 0 on success. */
+int orc_dequantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int x_rank,
+                          const void *scale, int scale_dtype, const int64_t *s_shape,
+                          int s_rank, const void *zp, int64_t axis, void *y);
+
+/* ---- MatMul FLOAT (km/kernel_matmul.cc:61-147): k-sequential, no FMA. ----
+ * Row range as for orc_qlinear_matmul; nthreads>1 splits rows over threads
+ * (the reference parallelises over output elements; per-element order is
+ * unchanged, so the result does not depend on the split). */
+int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank, const float *b,
+                   const int64_t *b_shape, int b_rank, float *y, int64_t row_begin,
+                   int64_t row_end, int nthreads);
+
+/* ---- MatMul FLOAT16/BFLOAT16 (km/kernel_matmul.cc:206-218):
+ * PromoteToFloat32 -> MatMulCompute<float> -> DemoteFromFloat32 ---- */
+int orc_matmul_half(const uint16_t *a, const int64_t *a_shape, int a_rank, const uint16_t *b,
+                    const int64_t *b_shape, int b_rank, int dtype, uint16_t *y,
+                    int64_t row_begin, int64_t row_end, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONNXL_AMD_ORACLE_H_ */

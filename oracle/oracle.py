@@ -1,0 +1,275 @@
+"""numpy front end of the C oracle (``oracle/liboracle.so``).
+
+Test infrastructure only: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` as the parity checker / CPU
+baseline.  The shipped library never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+FLOAT, UINT8, INT8, UINT16, INT16, INT32 = 1, 2, 3, 4, 5, 6
+FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 10, 16, 17, 21, 22
+
+_NP_OF = {UINT8: np.uint8, INT8: np.int8, UINT16: np.uint16, INT16: np.int16, INT32: np.int32,
+          FLOAT: np.float32, FLOAT16: np.uint16, BFLOAT16: np.uint16, FLOAT8E4M3FN: np.uint8,
+          INT4: np.uint8, UINT4: np.uint8}
+
+_lib = None
+
+
+def build() -> None:
+    """Compiles liboracle.so with the Makefile next to this file."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = ctypes.c_void_p
+I64P = ctypes.POINTER(ctypes.c_int64)
+
+
+def _declare(L):
+    L.orc_f32_to_f16.restype = ctypes.c_uint16
+    L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+    L.orc_f16_to_f32.restype = ctypes.c_float
+    L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_f32_to_bf16.restype = ctypes.c_uint16
+    L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+    L.orc_f32_to_f8e4m3fn.restype = ctypes.c_uint8
+    L.orc_f32_to_f8e4m3fn.argtypes = [ctypes.c_float]
+    L.orc_f8e4m3fn_to_f32.restype = ctypes.c_float
+    L.orc_f8e4m3fn_to_f32.argtypes = [ctypes.c_uint8]
+    for name in ("orc_f32_to_f16_n", "orc_f16_to_f32_n", "orc_f32_to_bf16_n", "orc_bf16_to_f32_n",
+                 "orc_f32_to_f8e4m3fn_n", "orc_f8e4m3fn_to_f32_n"):
+        getattr(L, name).restype = None
+        getattr(L, name).argtypes = [P, ctypes.c_int64, P]
+    L.orc_splitmix64_next.restype = ctypes.c_uint64
+    L.orc_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.orc_rand_uniform.restype = None
+    L.orc_rand_uniform.argtypes = [ctypes.c_uint64, ctypes.c_int64, P]
+    L.orc_rand_int.restype = ctypes.c_int
+    L.orc_rand_int.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int64, P]
+    L.orc_randn.restype = None
+    L.orc_randn.argtypes = [ctypes.c_uint64, ctypes.c_int64, P]
+    L.orc_matmul_output_shape.restype = ctypes.c_int
+    L.orc_matmul_output_shape.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P,
+                                          ctypes.POINTER(ctypes.c_int)]
+    L.orc_matmul_integer.restype = ctypes.c_int
+    L.orc_matmul_integer.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
+                                     ctypes.c_int, P, ctypes.c_int64, P, ctypes.c_int64, P]
+    L.orc_qlinear_matmul.restype = ctypes.c_int
+    L.orc_qlinear_matmul.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int32,
+                                     ctypes.c_float, P, ctypes.c_int, P, ctypes.c_int,
+                                     ctypes.c_int32, ctypes.c_float, ctypes.c_float,
+                                     ctypes.c_int32, ctypes.c_int, P, ctypes.c_int64,
+                                     ctypes.c_int64]
+    L.orc_dequantize_linear.restype = ctypes.c_int
+    L.orc_dequantize_linear.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
+                                        ctypes.c_int, P, ctypes.c_int64, P]
+    L.orc_matmul_f32.restype = ctypes.c_int
+    L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
+                                 ctypes.c_int64, ctypes.c_int]
+    L.orc_matmul_half.restype = ctypes.c_int
+    L.orc_matmul_half.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, P,
+                                  ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(P)
+
+
+def _shape(shape):
+    return np.ascontiguousarray(np.array(list(shape) or [0], dtype=np.int64))
+
+
+# ---- codecs -----------------------------------------------------------------
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(np.asarray(h, dtype=np.uint16))
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_n(_ptr(h), h.size, _ptr(out))
+    return out
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16_n(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def bf16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(np.asarray(h, dtype=np.uint16))
+    out = np.empty(h.shape, np.float32)
+    lib().orc_bf16_to_f32_n(_ptr(h), h.size, _ptr(out))
+    return out
+
+
+def f32_to_f8e4m3fn_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    out = np.empty(x.shape, np.uint8)
+    lib().orc_f32_to_f8e4m3fn_n(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def f8e4m3fn_bits_to_f32(c) -> np.ndarray:
+    c = np.ascontiguousarray(np.asarray(c, dtype=np.uint8))
+    out = np.empty(c.shape, np.float32)
+    lib().orc_f8e4m3fn_to_f32_n(_ptr(c), c.size, _ptr(out))
+    return out
+
+
+# ---- RNG --------------------------------------------------------------------
+
+def splitmix64(seed: int, n: int) -> list[int]:
+    s = ctypes.c_uint64(seed)
+    return [lib().orc_splitmix64_next(ctypes.byref(s)) for _ in range(n)]
+
+
+def rand_uniform(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float64)
+    lib().orc_rand_uniform(seed, n, _ptr(out))
+    return out
+
+
+def rand_int(low: int, high: int, seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.int64)
+    if lib().orc_rand_int(low, high, seed, n, _ptr(out)) != 0:
+        raise ValueError("high must be greater than low.")
+    return out
+
+
+def randn(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float64)
+    lib().orc_randn(seed, n, _ptr(out))
+    return out
+
+
+def pack_int4(values) -> np.ndarray:
+    """Packs 4-bit values (flat order, low nibble = even index) into bytes."""
+    v = np.asarray(values, dtype=np.int64).reshape(-1) & 0xF
+    if v.size % 2:
+        v = np.concatenate([v, np.zeros(1, np.int64)])
+    return (v[0::2] | (v[1::2] << 4)).astype(np.uint8)
+
+
+# ---- kernels ----------------------------------------------------------------
+
+def matmul_output_shape(a_shape, b_shape):
+    a_s, b_s = _shape(a_shape), _shape(b_shape)
+    out = np.zeros(40, np.int64)
+    r = ctypes.c_int(0)
+    rc = lib().orc_matmul_output_shape(_ptr(a_s), len(a_shape), _ptr(b_s), len(b_shape),
+                                       _ptr(out), ctypes.byref(r))
+    if rc:
+        raise ValueError(f"matmul shape error {rc}")
+    return tuple(int(d) for d in out[: r.value])
+
+
+def matmul_integer(a: np.ndarray, b: np.ndarray, a_zp=None, b_zp=None) -> np.ndarray:
+    """MatMulInteger with zero points given as int arrays (1 or M / 1 or N values)."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    ad = INT8 if a.dtype == np.int8 else UINT8
+    bd = INT8 if b.dtype == np.int8 else UINT8
+    za = np.ascontiguousarray(np.asarray([0] if a_zp is None else a_zp, np.int32).reshape(-1))
+    zb = np.ascontiguousarray(np.asarray([0] if b_zp is None else b_zp, np.int32).reshape(-1))
+    out_shape = matmul_output_shape(a.shape, b.shape)
+    y = np.empty(out_shape, np.int32)
+    rc = lib().orc_matmul_integer(_ptr(a), ad, _ptr(_shape(a.shape)), a.ndim, _ptr(b), bd,
+                                  _ptr(_shape(b.shape)), b.ndim, _ptr(za), za.size, _ptr(zb),
+                                  zb.size, _ptr(y))
+    if rc:
+        raise ValueError(f"matmul_integer error {rc}")
+    return y
+
+
+def qlinear_matmul(a, a_scale, a_zp, b, b_scale, b_zp, y_scale, y_zp, y_dtype=None,
+                   rows=None) -> np.ndarray:
+    """QLinearMatMul; y dtype defaults to the dtype of the y zero point (u8 or s8)."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    ad = INT8 if a.dtype == np.int8 else UINT8
+    bd = INT8 if b.dtype == np.int8 else UINT8
+    yd = y_dtype if y_dtype is not None else ad
+    out_shape = matmul_output_shape(a.shape, b.shape)
+    y = np.zeros(out_shape, np.int8 if yd == INT8 else np.uint8)
+    r0, r1 = (0, -1) if rows is None else rows
+    rc = lib().orc_qlinear_matmul(_ptr(a), ad, _ptr(_shape(a.shape)), a.ndim, int(a_zp),
+                                  float(a_scale), _ptr(b), bd, _ptr(_shape(b.shape)), b.ndim,
+                                  int(b_zp), float(b_scale), float(y_scale), int(y_zp), yd,
+                                  _ptr(y), r0, r1)
+    if rc:
+        raise ValueError(f"qlinear_matmul error {rc}")
+    return y
+
+
+def dequantize_linear(x: np.ndarray, x_dtype: int, x_shape, scale: np.ndarray, scale_dtype: int,
+                      zp=None, axis: int = 1) -> np.ndarray:
+    """DequantizeLinear.  x holds the raw storage (bytes for 4-bit types);
+    scale holds FLOAT values or FLOAT16 bit patterns; the output follows the
+    scale dtype (float32 array, or uint16 FLOAT16 bits)."""
+    x = np.ascontiguousarray(x)
+    scale = np.ascontiguousarray(scale)
+    zp_arr = None if zp is None else np.ascontiguousarray(zp)
+    n = int(np.prod(x_shape)) if len(x_shape) else 1
+    y = np.empty(tuple(x_shape), np.uint16 if scale_dtype == FLOAT16 else np.float32)
+    s_shape = scale.shape
+    rc = lib().orc_dequantize_linear(_ptr(x), x_dtype, _ptr(_shape(x_shape)), len(x_shape),
+                                     _ptr(scale), scale_dtype, _ptr(_shape(s_shape)),
+                                     len(s_shape), None if zp_arr is None else _ptr(zp_arr),
+                                     axis, _ptr(y))
+    if rc:
+        raise ValueError(f"dequantize_linear error {rc}")
+    assert y.size == n
+    return y
+
+
+def matmul_f32(a: np.ndarray, b: np.ndarray, rows=None, nthreads=1) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    y = np.zeros(matmul_output_shape(a.shape, b.shape), np.float32)
+    r0, r1 = (0, -1) if rows is None else rows
+    rc = lib().orc_matmul_f32(_ptr(a), _ptr(_shape(a.shape)), a.ndim, _ptr(b),
+                              _ptr(_shape(b.shape)), b.ndim, _ptr(y), r0, r1, nthreads)
+    if rc:
+        raise ValueError(f"matmul error {rc}")
+    return y
+
+
+def matmul_half(a_bits: np.ndarray, b_bits: np.ndarray, dtype: int, rows=None,
+                nthreads=1) -> np.ndarray:
+    """fp16 / bf16 MatMul on bit patterns (uint16 arrays); returns uint16 bits."""
+    a = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    b = np.ascontiguousarray(b_bits, dtype=np.uint16)
+    y = np.zeros(matmul_output_shape(a.shape, b.shape), np.uint16)
+    r0, r1 = (0, -1) if rows is None else rows
+    rc = lib().orc_matmul_half(_ptr(a), _ptr(_shape(a.shape)), a.ndim, _ptr(b),
+                               _ptr(_shape(b.shape)), b.ndim, dtype, _ptr(y), r0, r1, nthreads)
+    if rc:
+        raise ValueError(f"matmul_half error {rc}")
+    return y
