@@ -1,0 +1,148 @@
+/*
+ * onnxl_amd.h - C ABI of the MI355X (gfx950) quantized-matmul kernels.
+ *
+ * Each entry point is the GPU replacement of one onnx-light reference kernel
+ * overload that writes into a preallocated output (the `Tensor &output`
+ * overloads).  A reference-side adapter (KernelBase subclass registered with
+ * RegisterKernelFn) calls these functions from KernelBase::Run.  Reference
+ * paths below are relative to the onnx-light tree:
+ *   km/ = onnx_light/onnx_extensions/kernels/kernels/math/
+ *   kq/ = onnx_light/onnx_extensions/kernels/kernels/quantization/
+ *
+ * Conventions
+ * - Tensors are described by onnxl_amd_tensor: ONNX TensorProto.DataType code,
+ *   row-major dims, payload pointer and byte count.  4-bit types pack two
+ *   elements per byte, low nibble first (the ONNX / reference layout).
+ * - `location` says where the payload lives.  Device payloads are used in
+ *   place; host payloads are staged to the device (inputs) or copied back
+ *   (outputs) inside the call, which then completes before returning.
+ * - An absent optional input is a NULL pointer or a descriptor with rank -1
+ *   (the reference's empty `Tensor{}`).
+ * - Outputs are preallocated by the caller with the shape the reference
+ *   computes; a mismatch is an INVALID_ARGUMENT, as in the reference.
+ * - `stream` is a hipStream_t (NULL = default stream).  Device-only calls are
+ *   asynchronous on `stream`.
+ * - Every function returns an onnxl_amd_status; the message of the last
+ *   failure on the calling thread is returned by onnxl_amd_last_error().  The
+ *   validation failures the reference raises as std::invalid_argument map to
+ *   ONNXL_AMD_INVALID_ARGUMENT with the reference's message text.
+ * - Calls on one device share a library-owned workspace: calls on different
+ *   streams of the same device must be ordered by the caller.
+ */
+#ifndef ONNXL_AMD_H_
+#define ONNXL_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ONNXL_AMD_MAX_RANK 8
+
+typedef enum onnxl_amd_status {
+  ONNXL_AMD_OK = 0,
+  ONNXL_AMD_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument */
+  ONNXL_AMD_UNSUPPORTED = 2,      /* valid for the reference, not handled on the GPU path */
+  ONNXL_AMD_DEVICE_ERROR = 3,     /* HIP runtime failure */
+  ONNXL_AMD_NOT_INITIALIZED = 4   /* onnxl_amd_init was not called */
+} onnxl_amd_status;
+
+typedef enum onnxl_amd_location { ONNXL_AMD_DEVICE = 0, ONNXL_AMD_HOST = 1 } onnxl_amd_location;
+
+/* Mirrors the fields of the reference core::runtime::Tensor that kernels read
+ * (core/runtime/memory/simple_tensor.h:526): data_type, shape, bytes. */
+typedef struct onnxl_amd_tensor {
+  int32_t data_type;                /* ONNX TensorProto.DataType code */
+  int32_t rank;                     /* number of dims; -1 = absent optional input */
+  int64_t dims[ONNXL_AMD_MAX_RANK]; /* row-major shape */
+  void *data;                       /* payload (see location) */
+  int64_t size_bytes;               /* payload bytes */
+  int32_t location;                 /* onnxl_amd_location */
+  int32_t reserved;                 /* must be 0 */
+} onnxl_amd_tensor;
+
+/* Library lifetime.  init selects the device for all later calls on this
+ * process; shutdown releases the workspace. */
+int onnxl_amd_init(int device_ordinal);
+int onnxl_amd_shutdown(void);
+const char *onnxl_amd_last_error(void);
+const char *onnxl_amd_version(void);
+
+/* MatMul output shape (km/matmul_shape_utils.h:85-106): 1-D promotion, batch
+ * broadcasting, promoted dims dropped.  out_dims holds ONNXL_AMD_MAX_RANK. */
+int onnxl_amd_matmul_shape(const int64_t *a_dims, int32_t a_rank, const int64_t *b_dims,
+                           int32_t b_rank, int64_t *out_dims, int32_t *out_rank);
+
+/* MatMulInteger: Y = (A - a_zp) @ (B - b_zp) with int32 output.
+ * A, B: UINT8 or INT8 (independently); zero points absent, scalar, [1], or
+ * 1-D of size M (a) / N (b) with their input's dtype; Y: INT32.
+ * Replaces kernel::MatMulInteger::operator()(a, b, a_zero_point,
+ * b_zero_point, Tensor &output), km/kernel_matmul_integer.cc:231-234
+ * (validation :178-208, arithmetic :89-176). */
+int onnxl_amd_matmul_integer(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
+                             const onnxl_amd_tensor *a_zero_point,
+                             const onnxl_amd_tensor *b_zero_point, onnxl_amd_tensor *y,
+                             void *stream);
+
+/* QLinearMatMul: y = saturate(rint((float)Σ(a-za)(b-zb) * (a_s*b_s/y_s)) + zy).
+ * a, b: UINT8/INT8; scales: FLOAT or FLOAT16 scalars; zero points: scalars
+ * with their input's dtype; y dtype = y_zero_point dtype.
+ * Replaces kernel::QLinearMatMul::operator()(..., Tensor &output),
+ * kq/kernel_qlinearmatmul.cc:242-267 (arithmetic :115-217). */
+int onnxl_amd_qlinear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
+                             const onnxl_amd_tensor *a_zero_point, const onnxl_amd_tensor *b,
+                             const onnxl_amd_tensor *b_scale,
+                             const onnxl_amd_tensor *b_zero_point,
+                             const onnxl_amd_tensor *y_scale,
+                             const onnxl_amd_tensor *y_zero_point, onnxl_amd_tensor *y,
+                             void *stream);
+
+/* DequantizeLinear (opset 21 semantics of the reference): per-tensor,
+ * per-axis (1-D scale of size x.shape[axis]) or blocked (scale rank == x
+ * rank, only `axis` coarser; the block size is derived from the shapes).
+ * x: UINT8, INT8, UINT16, INT16, INT32, FLOAT8E4M3FN, UINT4, INT4;
+ * x_scale: FLOAT or FLOAT16; y dtype = x_scale dtype.
+ * Replaces kernel::DequantizeLinear::operator() with and without zero point,
+ * kq/kernel_dequantizelinear.cc:349-410, :426-502, :522-651, :670-693. */
+int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                                const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                onnxl_amd_tensor *y, void *stream);
+
+/* MatMul for FLOAT16 / BFLOAT16 operands (fp32 accumulation, output rounded
+ * to the input dtype).  Replaces kernel::MatMul::operator()(a, b, Tensor &)
+ * for those dtypes, km/kernel_matmul.cc:242-253 (compute :61-147, :206-218). */
+int onnxl_amd_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tensor *y,
+                     void *stream);
+
+/* Cast FLOAT -> FLOAT16 / BFLOAT16 (round-to-nearest-even), the Cast step
+ * between DequantizeLinear and a bf16 MatMul.
+ * Replaces the FLOAT->BFLOAT16 / FLOAT16 branch of the reference Cast kernel,
+ * ext/kernels/kernels/tensor/kernel_cast.cc:360-370. */
+int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, void *stream);
+
+/* Fused Y = MatMul(A, [Cast(to=cast_to)](DequantizeLinear(x, x_scale,
+ * x_zero_point, axis))) for a 2-D quantized weight x [K, N].  A: FLOAT16 or
+ * BFLOAT16 [..., M, K]; the dequantized weight is rounded exactly as the
+ * unfused reference chain rounds it (to x_scale's dtype, then to cast_to), so
+ * only the fp32 summation order differs from the chain of the three kernels
+ * above.  cast_to = 0 means no Cast node (the DequantizeLinear output dtype
+ * must then equal A's dtype).  Y dtype = A dtype.  x: INT4, UINT4, INT8,
+ * UINT8, FLOAT8E4M3FN; per-tensor, per-axis (axis 1) or blocked along K
+ * (axis 0) scales.  No single reference kernel: it computes the chain
+ * kq/kernel_dequantizelinear.cc:522-693 -> kernel_cast.cc:360-370 ->
+ * km/kernel_matmul.cc:181-223 that a DequantizeLinear->[Cast]->MatMul
+ * subgraph runs node by node. */
+int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
+                                       const onnxl_amd_tensor *x_scale,
+                                       const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                       int32_t cast_to, onnxl_amd_tensor *y, void *stream);
+
+/* Waits for all work queued by this library on `stream`. */
+int onnxl_amd_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONNXL_AMD_H_ */

@@ -1,0 +1,337 @@
+"""Python front end of the MI355X quantized-matmul kernels.
+
+Mirrors the onnx-light reference kernel classes for this path
+(``kernel::MatMulInteger``, ``kernel::QLinearMatMul``,
+``kernel::DequantizeLinear``, ``kernel::MatMul``) with the same argument
+meaning and error behaviour: validation failures raise :class:`InvalidArgument`
+(a ``ValueError``, the reference raises ``std::invalid_argument``) with the
+reference's message text.  Every call goes through the C ABI of
+``libonnxl_amd.so`` (``include/onnxl_amd.h``); there is no CPU fallback: if the
+library is missing, :func:`lib` raises.
+
+Tensors are ``torch.Tensor`` objects (CUDA tensors are used in place, CPU
+tensors are staged by the library) or numpy arrays (host).  4-bit tensors are
+passed as packed ``uint8`` storage together with ``dtype=INT4/UINT4`` and the
+logical ``shape``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libonnxl_amd.so")
+MAX_RANK = 8
+
+# ONNX TensorProto.DataType codes.
+FLOAT, UINT8, INT8, UINT16, INT16, INT32, INT64 = 1, 2, 3, 4, 5, 6, 7
+FLOAT16, DOUBLE, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 10, 11, 16, 17, 21, 22
+
+OK, INVALID_ARGUMENT, UNSUPPORTED, DEVICE_ERROR, NOT_INITIALIZED = 0, 1, 2, 3, 4
+DEVICE, HOST = 0, 1
+
+
+class InvalidArgument(ValueError):
+    """The reference kernel would raise std::invalid_argument."""
+
+
+class Unsupported(NotImplementedError):
+    """Valid for the reference, but this input has no GPU kernel."""
+
+
+class DeviceError(RuntimeError):
+    """HIP runtime failure, or the library was not initialised."""
+
+
+class Tensor(ctypes.Structure):
+    """onnxl_amd_tensor (include/onnxl_amd.h)."""
+    _fields_ = [("data_type", ctypes.c_int32), ("rank", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * MAX_RANK), ("data", ctypes.c_void_p),
+                ("size_bytes", ctypes.c_int64), ("location", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+TP = ctypes.POINTER(Tensor)
+_lib = None
+
+
+def build() -> str:
+    """Compiles libonnxl_amd.so in place (hipcc, gfx950)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-j8"], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C ABI library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run onnx_light_amd.build() (make -C onnx-light_amd)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.onnxl_amd_init.argtypes = [ctypes.c_int]
+        L.onnxl_amd_shutdown.argtypes = []
+        L.onnxl_amd_last_error.restype = ctypes.c_char_p
+        L.onnxl_amd_version.restype = ctypes.c_char_p
+        L.onnxl_amd_matmul_shape.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                                             ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                                             ctypes.POINTER(ctypes.c_int64),
+                                             ctypes.POINTER(ctypes.c_int32)]
+        L.onnxl_amd_matmul_integer.argtypes = [TP, TP, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_qlinear_matmul.argtypes = [TP] * 9 + [ctypes.c_void_p]
+        L.onnxl_amd_dequantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
+        L.onnxl_amd_matmul.argtypes = [TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
+                                                         ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_synchronize.argtypes = [ctypes.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = lib().onnxl_amd_last_error().decode(errors="replace")
+    if rc == INVALID_ARGUMENT:
+        raise InvalidArgument(msg)
+    if rc == UNSUPPORTED:
+        raise Unsupported(msg)
+    raise DeviceError(f"status {rc}: {msg}")
+
+
+def init(device: int = 0) -> None:
+    _check(lib().onnxl_amd_init(device))
+
+
+def shutdown() -> None:
+    _check(lib().onnxl_amd_shutdown())
+
+
+def synchronize(stream=None) -> None:
+    _check(lib().onnxl_amd_synchronize(stream))
+
+
+# ---- descriptors ------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+_TORCH_CODES = None
+
+
+def _torch_code(dt):
+    global _TORCH_CODES
+    if _TORCH_CODES is None:
+        torch = _torch()
+        _TORCH_CODES = {torch.float32: FLOAT, torch.uint8: UINT8, torch.int8: INT8,
+                        torch.int16: INT16, torch.int32: INT32, torch.int64: INT64,
+                        torch.float16: FLOAT16, torch.float64: DOUBLE, torch.bfloat16: BFLOAT16,
+                        torch.float8_e4m3fn: FLOAT8E4M3FN, torch.uint16: UINT16}
+    return _TORCH_CODES[dt]
+
+
+_NP_CODES = {np.dtype(np.float32): FLOAT, np.dtype(np.uint8): UINT8, np.dtype(np.int8): INT8,
+             np.dtype(np.uint16): UINT16, np.dtype(np.int16): INT16, np.dtype(np.int32): INT32,
+             np.dtype(np.int64): INT64, np.dtype(np.float16): FLOAT16}
+
+
+def describe(t, dtype: int | None = None, shape=None) -> Tensor:
+    """Builds an onnxl_amd_tensor for a torch tensor / numpy array / None.
+
+    ``dtype`` overrides the element type (4-bit types, FLOAT16 bits held in
+    uint16 arrays, ...); ``shape`` overrides the logical shape."""
+    d = Tensor()
+    if t is None:
+        d.rank = -1
+        return d
+    if isinstance(t, np.ndarray):
+        arr = t if t.flags["C_CONTIGUOUS"] else np.ascontiguousarray(t).reshape(t.shape)
+        d.data_type = dtype if dtype is not None else _NP_CODES[arr.dtype]
+        d.data = arr.ctypes.data if arr.nbytes else None
+        d.size_bytes = arr.nbytes
+        d.location = HOST
+        d._keep = arr
+        shp = arr.shape if shape is None else tuple(shape)
+    else:
+        torch = _torch()
+        if not t.is_contiguous():
+            raise InvalidArgument("tensors passed to the C ABI must be contiguous")
+        d.data_type = dtype if dtype is not None else _torch_code(t.dtype)
+        d.data = t.data_ptr() if t.numel() else None
+        d.size_bytes = t.numel() * t.element_size()
+        d.location = DEVICE if t.is_cuda else HOST
+        d._keep = t
+        shp = tuple(t.shape) if shape is None else tuple(shape)
+        del torch
+    if len(shp) > MAX_RANK:
+        raise InvalidArgument(f"rank {len(shp)} above {MAX_RANK}")
+    d.rank = len(shp)
+    for i, s in enumerate(shp):
+        d.dims[i] = int(s)
+    return d
+
+
+def _stream_of(*ts):
+    for t in ts:
+        if t is not None and not isinstance(t, np.ndarray) and t.is_cuda:
+            return ctypes.c_void_p(_torch().cuda.current_stream(t.device).cuda_stream)
+    return None
+
+
+def _device_of(*ts):
+    for t in ts:
+        if t is not None and not isinstance(t, np.ndarray) and t.is_cuda:
+            return t.device
+    return "cpu"
+
+
+def _describe_zp(zp, x_dtype, x_scale):
+    """Zero point descriptor: 4-bit zero points are packed storage whose
+    logical shape is the scale's shape."""
+    if zp is None:
+        return describe(None)
+    if x_dtype in (INT4, UINT4):
+        return describe(zp, x_dtype, tuple(x_scale.shape))
+    return describe(zp, x_dtype)
+
+
+def matmul_shape(a_shape, b_shape) -> tuple:
+    a = (ctypes.c_int64 * MAX_RANK)(*a_shape)
+    b = (ctypes.c_int64 * MAX_RANK)(*b_shape)
+    out = (ctypes.c_int64 * MAX_RANK)()
+    r = ctypes.c_int32(0)
+    _check(lib().onnxl_amd_matmul_shape(a, len(a_shape), b, len(b_shape), out,
+                                        ctypes.byref(r)))
+    return tuple(out[i] for i in range(r.value))
+
+
+def _shape_of(t, shape=None):
+    return tuple(shape) if shape is not None else tuple(t.shape)
+
+
+def _empty(shape, torch_dtype, device):
+    return _torch().empty(shape, dtype=torch_dtype, device=device)
+
+
+# ---- kernels (reference operator() overloads) ------------------------------
+
+def matmul_integer(a, b, a_zero_point=None, b_zero_point=None, out=None):
+    """kernel::MatMulInteger (km/kernel_matmul_integer.cc:212-234)."""
+    torch = _torch()
+    if out is None:
+        out = _empty(matmul_shape(_shape_of(a), _shape_of(b)), torch.int32, _device_of(a, b))
+    da, db = describe(a), describe(b)
+    dza, dzb, dy = describe(a_zero_point), describe(b_zero_point), describe(out)
+    _check(lib().onnxl_amd_matmul_integer(da, db, dza, dzb, dy, _stream_of(a, b, out)))
+    return out
+
+
+def qlinear_matmul(a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale, y_zero_point,
+                   out=None):
+    """kernel::QLinearMatMul (kq/kernel_qlinearmatmul.cc:221-267); output dtype
+    follows y_zero_point."""
+    torch = _torch()
+    if out is None:
+        ydt = y_zero_point.dtype
+        if isinstance(y_zero_point, np.ndarray):
+            ydt = torch.int8 if ydt == np.int8 else torch.uint8
+        out = _empty(matmul_shape(_shape_of(a), _shape_of(b)), ydt, _device_of(a, b))
+    ds = [describe(t) for t in (a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale,
+                                y_zero_point, out)]
+    _check(lib().onnxl_amd_qlinear_matmul(*ds, _stream_of(a, b, out)))
+    return out
+
+
+def dequantize_linear(x, x_scale, x_zero_point=None, axis: int = 1, x_dtype=None, x_shape=None,
+                      out=None):
+    """kernel::DequantizeLinear (kq/kernel_dequantizelinear.cc:332-693); the
+    output dtype follows x_scale (FLOAT or FLOAT16)."""
+    torch = _torch()
+    shape = _shape_of(x, x_shape)
+    if out is None:
+        odt = x_scale.dtype
+        if isinstance(x_scale, np.ndarray):
+            odt = torch.float16 if x_scale.dtype == np.float16 else torch.float32
+        out = _empty(shape, odt, _device_of(x))
+    dx = describe(x, x_dtype, shape)
+    dz = _describe_zp(x_zero_point, x_dtype, x_scale)
+    _check(lib().onnxl_amd_dequantize_linear(dx, describe(x_scale), dz, axis, describe(out),
+                                             _stream_of(x, out)))
+    return out
+
+
+def matmul(a, b, out=None):
+    """kernel::MatMul for FLOAT16 / BFLOAT16 (km/kernel_matmul.cc:181-258)."""
+    if out is None:
+        out = _empty(matmul_shape(_shape_of(a), _shape_of(b)), a.dtype, _device_of(a, b))
+    _check(lib().onnxl_amd_matmul(describe(a), describe(b), describe(out), _stream_of(a, b, out)))
+    return out
+
+
+def cast(x, to: int, out=None):
+    """FLOAT -> FLOAT16 / BFLOAT16 Cast (ext/kernels/kernels/tensor/kernel_cast.cc:360-370)."""
+    torch = _torch()
+    if out is None:
+        out = _empty(_shape_of(x), torch.bfloat16 if to == BFLOAT16 else torch.float16,
+                     _device_of(x))
+    _check(lib().onnxl_amd_cast(describe(x), to, describe(out), _stream_of(x, out)))
+    return out
+
+
+def dequantize_linear_matmul(a, x, x_scale, x_zero_point=None, axis: int = 1, cast_to: int = 0,
+                             x_dtype=None, x_shape=None, out=None):
+    """Fused MatMul(a, [Cast](DequantizeLinear(x, x_scale, x_zero_point, axis)))."""
+    shape = _shape_of(x, x_shape)
+    if out is None:
+        out = _empty(matmul_shape(_shape_of(a), shape), a.dtype, _device_of(a, x))
+    dz = _describe_zp(x_zero_point, x_dtype, x_scale)
+    _check(lib().onnxl_amd_dequantize_linear_matmul(describe(a), describe(x, x_dtype, shape),
+                                                    describe(x_scale), dz, axis, cast_to,
+                                                    describe(out), _stream_of(a, x, out)))
+    return out
+
+
+class MatMulInteger:
+    """Kernel-class mirror of kernel::MatMulInteger."""
+    name = "onnxl_amd:GPU:ai.onnx:MatMulInteger"
+
+    def __call__(self, a, b, a_zero_point=None, b_zero_point=None, out=None):
+        return matmul_integer(a, b, a_zero_point, b_zero_point, out)
+
+
+class QLinearMatMul:
+    """Kernel-class mirror of kernel::QLinearMatMul."""
+    name = "onnxl_amd:GPU:ai.onnx:QLinearMatMul"
+
+    def __call__(self, a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale, y_zero_point,
+                 out=None):
+        return qlinear_matmul(a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale,
+                              y_zero_point, out)
+
+
+class DequantizeLinear:
+    """Kernel-class mirror of kernel::DequantizeLinear (axis defaults to 1 as
+    in DequantizeLinear::Run, kq/kernel_dequantizelinear.cc:705)."""
+    name = "onnxl_amd:GPU:ai.onnx:DequantizeLinear"
+
+    def __call__(self, x, x_scale, x_zero_point=None, axis=1, x_dtype=None, x_shape=None, out=None):
+        return dequantize_linear(x, x_scale, x_zero_point, axis, x_dtype, x_shape, out)
+
+
+class MatMul:
+    """Kernel-class mirror of kernel::MatMul (FLOAT16 / BFLOAT16 inputs)."""
+    name = "onnxl_amd:GPU:ai.onnx:MatMul"
+
+    def __call__(self, a, b, out=None):
+        return matmul(a, b, out)
+
+
+# Dispatch keys "<domain>:<op_type>" as the reference table uses them
+# (core/runtime/kernels/kernel_dispatch_table.h:148-164).
+KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
+           "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul}

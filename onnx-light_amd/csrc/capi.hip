@@ -1,0 +1,838 @@
+// C ABI of the gfx950 quantized-matmul kernels (include/onnxl_amd.h).
+//
+// Host side of every entry point: the reference kernel's validation (same
+// checks, order and message text, cited per function), staging of host
+// payloads, the zero-point / scale arithmetic that the reference does on the
+// host, and the kernel launch.  No computation falls back to the CPU: a shape
+// or dtype without a GPU kernel returns ONNXL_AMD_UNSUPPORTED.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <limits>
+#include <memory>
+#include <mutex>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace onnxl_amd {
+
+// ---------------------------------------------------------------------------
+// Library state.
+
+namespace {
+DeviceContext g_ctx;
+std::atomic<bool> g_init{false};
+std::mutex g_mu;  // serialises entry points: one workspace per device
+thread_local std::string g_last_error;
+}  // namespace
+
+bool Initialized() { return g_init.load(); }
+
+DeviceContext &Ctx() {
+  if (!g_init.load()) throw NotInitialized();
+  return g_ctx;
+}
+
+void *Workspace::Get(size_t bytes) {
+  if (bytes <= cap_ && ptr_ != nullptr) return ptr_;
+  size_t want = std::max<size_t>(bytes, size_t(1) << 20);
+  want = std::max(want, cap_ * 2);
+  if (ptr_ != nullptr) {
+    OLA_HIP(hipDeviceSynchronize());
+    OLA_HIP(hipFree(ptr_));
+    ptr_ = nullptr;
+    cap_ = 0;
+  }
+  OLA_HIP(hipMalloc(&ptr_, want));
+  cap_ = want;
+  return ptr_;
+}
+
+unsigned *Workspace::Counters(size_t count) {
+  if (count <= counters_cap_ && counters_ != nullptr) return counters_;
+  size_t want = std::max<size_t>(count, 4096);
+  if (counters_ != nullptr) {
+    OLA_HIP(hipDeviceSynchronize());
+    OLA_HIP(hipFree(counters_));
+    counters_ = nullptr;
+  }
+  OLA_HIP(hipMalloc(&counters_, want * sizeof(unsigned)));
+  OLA_HIP(hipMemset(counters_, 0, want * sizeof(unsigned)));
+  counters_cap_ = want;
+  return counters_;
+}
+
+void Workspace::Release() {
+  if (ptr_) (void)hipFree(ptr_);
+  if (counters_) (void)hipFree(counters_);
+  ptr_ = nullptr;
+  counters_ = nullptr;
+  cap_ = counters_cap_ = 0;
+}
+
+// ---------------------------------------------------------------------------
+// MatMul shape rules, km/matmul_shape_utils.h:24-106.
+
+MatMulPlan MakeMatMulPlan(const Shape &a, const Shape &b, const char *kname, const char *rank0_msg,
+                          const char *inner_msg, const char *bcast_msg) {
+  OLA_ENFORCE(!a.empty() && !b.empty(), kname, rank0_msg);
+  const Shape a2 = a.size() == 1 ? Shape{1, a[0]} : a;
+  const Shape b2 = b.size() == 1 ? Shape{b[0], 1} : b;
+  MatMulPlan p;
+  p.M = a2[a2.size() - 2];
+  p.K = a2[a2.size() - 1];
+  p.N = b2[b2.size() - 1];
+  OLA_ENFORCE(p.K == b2[b2.size() - 2], kname, inner_msg);
+  const size_t ap = a2.size() - 2, bp = b2.size() - 2;
+  const size_t rank = std::max(ap, bp);
+  Shape as(a2.size()), bs(b2.size());
+  as.back() = 1;
+  for (size_t i = a2.size() - 1; i-- > 0;) as[i] = as[i + 1] * a2[i + 1];
+  bs.back() = 1;
+  for (size_t i = b2.size() - 1; i-- > 0;) bs[i] = bs[i + 1] * b2[i + 1];
+  for (size_t i = 0; i < rank; ++i) {
+    const bool ha = i + ap >= rank, hb = i + bp >= rank;
+    const int64_t da = ha ? a2[i - (rank - ap)] : 1;
+    const int64_t db = hb ? b2[i - (rank - bp)] : 1;
+    int64_t d;
+    if (da == db || da == 1) {
+      d = db;
+    } else if (db == 1) {
+      d = da;
+    } else {
+      throw InvalidArgument(Cat(kname, bcast_msg));
+    }
+    p.out_prefix.push_back(d);
+    p.a_bstride.push_back(ha && da != 1 ? as[i - (rank - ap)] : 0);
+    p.b_bstride.push_back(hb && db != 1 ? bs[i - (rank - bp)] : 0);
+    p.batch *= d;
+  }
+  for (size_t i = 0; i < ap; ++i) p.a_mats *= a2[i];
+  for (size_t i = 0; i < bp; ++i) p.b_mats *= b2[i];
+  p.out_shape = p.out_prefix;
+  if (a.size() != 1) p.out_shape.push_back(p.M);
+  if (b.size() != 1) p.out_shape.push_back(p.N);
+  return p;
+}
+
+namespace {
+
+BatchMap ToBatchMap(const MatMulPlan &p) {
+  BatchMap m;
+  // Leading broadcast dims that are 1 everywhere carry no offset; drop dims
+  // of size 1 to fit kMaxBatchRank.
+  for (size_t i = 0; i < p.out_prefix.size(); ++i) {
+    if (p.out_prefix[i] == 1) continue;
+    if (m.rank == kMaxBatchRank) throw Unsupported("MatMul batch rank above 6 (non-unit dims)");
+    m.dims[m.rank] = p.out_prefix[i];
+    m.a_stride[m.rank] = p.a_bstride[i];
+    m.b_stride[m.rank] = p.b_bstride[i];
+    ++m.rank;
+  }
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Descriptor helpers.
+
+void CheckDescriptor(const onnxl_amd_tensor *t, const char *what) {
+  if (t == nullptr) return;
+  OLA_ENFORCE(t->rank <= ONNXL_AMD_MAX_RANK, what, ": rank above ", ONNXL_AMD_MAX_RANK);
+  if (t->rank < 0) return;
+  for (int i = 0; i < t->rank; ++i) OLA_ENFORCE(t->dims[i] >= 0, what, ": negative dimension");
+  OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE || t->location == ONNXL_AMD_HOST, what,
+              ": unknown location");
+  const int64_t need = PackedBytes(t->data_type, NumElements(*t));
+  OLA_ENFORCE(t->size_bytes >= need, what, ": payload of ", t->size_bytes,
+              " bytes is smaller than its shape needs (", need, ")");
+  OLA_ENFORCE(need == 0 || t->data != nullptr, what, ": null payload");
+}
+
+// Copies `bytes` of element data from a descriptor (host or device) to host.
+void ReadBytes(const onnxl_amd_tensor &t, int64_t offset, void *dst, size_t bytes) {
+  const char *src = static_cast<const char *>(t.data) + offset;
+  if (t.location == ONNXL_AMD_HOST) {
+    std::memcpy(dst, src, bytes);
+  } else {
+    OLA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  }
+}
+
+// One call's device view of its tensors: host payloads staged into scratch.
+class Staging {
+public:
+  Staging(hipStream_t s, size_t extra_scratch, std::initializer_list<const onnxl_amd_tensor *> in,
+          std::initializer_list<onnxl_amd_tensor *> out)
+      : stream_(s) {
+    size_t total = Scratch::Round(extra_scratch) + 256;
+    for (auto *t : in)
+      if (t && t->rank >= 0 && t->location == ONNXL_AMD_HOST) total += Scratch::Round(t->size_bytes) + 256;
+    for (auto *t : out)
+      if (t && t->location == ONNXL_AMD_HOST) total += Scratch::Round(t->size_bytes) + 256;
+    scratch_ = std::make_unique<Scratch>(total);
+    extra_ = extra_scratch ? scratch_->Take(extra_scratch) : nullptr;
+    for (auto *t : in) {
+      if (t && t->rank >= 0 && t->location == ONNXL_AMD_HOST && t->size_bytes > 0) {
+        void *d = scratch_->Take(t->size_bytes);
+        OLA_HIP(hipMemcpyAsync(d, t->data, t->size_bytes, hipMemcpyHostToDevice, s));
+        dev_.push_back({t, d});
+      }
+    }
+    for (auto *t : out) {
+      if (t && t->location == ONNXL_AMD_HOST && t->size_bytes > 0) {
+        void *d = scratch_->Take(t->size_bytes);
+        dev_.push_back({t, d});
+        outs_.push_back({t, d});
+      }
+    }
+  }
+  const void *In(const onnxl_amd_tensor *t) const {
+    if (t == nullptr || t->rank < 0) return nullptr;
+    for (auto &e : dev_)
+      if (e.first == t) return e.second;
+    return t->data;
+  }
+  void *Out(onnxl_amd_tensor *t) const { return const_cast<void *>(In(t)); }
+  void *Extra() const { return extra_; }
+  // Copies host outputs back and waits when any payload was on the host.
+  void Finish() {
+    for (auto &e : outs_)
+      OLA_HIP(hipMemcpyAsync(e.first->data, e.second, e.first->size_bytes, hipMemcpyDeviceToHost,
+                             stream_));
+    if (!dev_.empty()) OLA_HIP(hipStreamSynchronize(stream_));
+    OLA_HIP(hipGetLastError());
+  }
+
+private:
+  hipStream_t stream_;
+  std::unique_ptr<Scratch> scratch_;
+  void *extra_ = nullptr;
+  std::vector<std::pair<const onnxl_amd_tensor *, void *>> dev_;
+  std::vector<std::pair<onnxl_amd_tensor *, void *>> outs_;
+};
+
+bool IsInt8OrUint8(int32_t dt) { return dt == kInt8 || dt == kUint8; }
+
+int32_t ReadIntElem(const onnxl_amd_tensor &t, int64_t idx) {
+  uint8_t b = 0;
+  ReadBytes(t, idx, &b, 1);
+  return t.data_type == kInt8 ? (int32_t)(int8_t)b : (int32_t)b;
+}
+
+float HalfBitsToFloat(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+  uint32_t f;
+  if (exp == 0x1f) {
+    f = sign | 0x7f800000u | (man << 13);
+  } else if (exp == 0) {
+    float v = std::ldexp((float)man, -24);
+    return sign ? -v : v;
+  } else {
+    f = sign | ((exp + 112u) << 23) | (man << 13);
+  }
+  float out;
+  std::memcpy(&out, &f, 4);
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// MatMulInteger, km/kernel_matmul_integer.cc.
+
+constexpr const char *kMmiName = "kernel::MatMulInteger";
+
+// ZeroPointCount, km/kernel_matmul_integer.cc:40-57.
+int64_t ZeroPointCount(const onnxl_amd_tensor *t, int32_t expected_dtype, int64_t expected_size,
+                       const char *name) {
+  if (Absent(t) || (t->rank == 0 && t->size_bytes == 0)) return 1;
+  OLA_ENFORCE(t->data_type == expected_dtype, kMmiName, ": '", name,
+              "' dtype must match its data input.");
+  OLA_ENFORCE(t->rank <= 1, kMmiName, ": '", name, "' must be a scalar or a 1-D tensor.");
+  const int64_t numel = NumElements(*t);
+  OLA_ENFORCE(numel == 1 || numel == expected_size, kMmiName, ": '", name,
+              "' must be a scalar, a one-element 1-D tensor, or a 1-D tensor whose size matches "
+              "the corresponding matrix dimension.");
+  return numel;
+}
+
+int MatMulInteger(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
+                  const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b_zp,
+                  onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(a && b && y, kMmiName, ": A, B and the output are required.");
+  CheckDescriptor(a, "A");
+  CheckDescriptor(b, "B");
+  CheckDescriptor(a_zp, "a_zero_point");
+  CheckDescriptor(b_zp, "b_zero_point");
+  CheckDescriptor(y, "Y");
+  // ComputeMatMulInteger, :178-208
+  OLA_ENFORCE(IsInt8OrUint8(a->data_type), kMmiName, ": A must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(b->data_type), kMmiName, ": B must be INT8 or UINT8.");
+  OLA_ENFORCE(y->data_type == kInt32, kMmiName, ": output dtype must be INT32.");
+  const MatMulPlan plan = MakeMatMulPlan(
+      ShapeOf(*a), ShapeOf(*b), kMmiName, ": rank-0 inputs are not accepted.",
+      ": incompatible inner dimensions.", ": inputs are not broadcast-compatible on batch dimensions.");
+  OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kMmiName, ": preallocated output has invalid shape.");
+  OLA_ENFORCE(y->size_bytes == NumElements(plan.out_shape) * 4, kMmiName,
+              ": preallocated output buffer size does not match its shape.");
+  const int64_t a_count = ZeroPointCount(a_zp, a->data_type, plan.M, "a_zero_point");
+  const int64_t b_count = ZeroPointCount(b_zp, b->data_type, plan.N, "b_zero_point");
+
+  IGemmParams p{};
+  p.M = plan.M;
+  p.N = plan.N;
+  p.K = plan.K;
+  p.batch = plan.batch;
+  p.bm = ToBatchMap(plan);
+  p.a_u8 = a->data_type == kUint8;
+  p.b_u8 = b->data_type == kUint8;
+  const int32_t ca = p.a_u8 ? 128 : 0, cb = p.b_u8 ? 128 : 0;
+  const bool a_present = !(Absent(a_zp) || (a_zp->rank == 0 && a_zp->size_bytes == 0));
+  const bool b_present = !(Absent(b_zp) || (b_zp->rank == 0 && b_zp->size_bytes == 0));
+  // The reference indexes per-row values only when more than one is given
+  // (a_per_row = a_size > 1, :118-119).
+  const bool a_vec = a_present && a_count > 1;
+  const bool b_vec = b_present && b_count > 1;
+  p.alpha_scalar = ca - ((a_present && !a_vec && a_count == 1) ? ReadIntElem(*a_zp, 0) : 0);
+  p.beta_scalar = cb - ((b_present && !b_vec && b_count == 1) ? ReadIntElem(*b_zp, 0) : 0);
+  p.need_cb = a_vec || p.alpha_scalar != 0;
+  p.need_ra = b_vec || p.beta_scalar != 0;
+  p.epilogue = kEpiInt32;
+
+  Staging st(stream, 0, {a, b, a_vec ? a_zp : nullptr, b_vec ? b_zp : nullptr}, {y});
+  p.A = static_cast<const int8_t *>(st.In(a));
+  p.B = static_cast<const int8_t *>(st.In(b));
+  p.a_zp = a_vec ? static_cast<const uint8_t *>(st.In(a_zp)) : nullptr;
+  p.b_zp = b_vec ? static_cast<const uint8_t *>(st.In(b_zp)) : nullptr;
+  p.Y = st.Out(y);
+  LaunchIGemm(p, stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// QLinearMatMul, kq/kernel_qlinearmatmul.cc.
+
+constexpr const char *kQlmName = "kernel::QLinearMatMul";
+
+int32_t QReadScalarInt(const onnxl_amd_tensor &t, const char *name) {  // :35-38
+  OLA_ENFORCE(NumElements(t) == 1, kQlmName, ": '", name, "' must be a scalar.");
+  return ReadIntElem(t, 0);
+}
+
+float QReadScalarFloat(const onnxl_amd_tensor &t, const char *name) {  // :40-51
+  OLA_ENFORCE(NumElements(t) == 1, kQlmName, ": '", name, "' must be a scalar.");
+  if (t.data_type == kFloat) {
+    float v;
+    ReadBytes(t, 0, &v, 4);
+    return v;
+  }
+  if (t.data_type == kFloat16) {
+    uint16_t h;
+    ReadBytes(t, 0, &h, 2);
+    return HalfBitsToFloat(h);
+  }
+  throw InvalidArgument(Cat(kQlmName, ": '", name,
+                            "' must be a FLOAT or FLOAT16 scalar for the reference kernel."));
+}
+
+int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
+                  const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b,
+                  const onnxl_amd_tensor *b_scale, const onnxl_amd_tensor *b_zp,
+                  const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zp,
+                  onnxl_amd_tensor *y, hipStream_t stream) {
+  const onnxl_amd_tensor *req[] = {a, a_scale, a_zp, b, b_scale, b_zp, y_scale, y_zp, y};
+  for (auto *t : req) OLA_ENFORCE(!Absent(t), kQlmName, ": all 8 inputs and the output are required.");
+  const char *names[] = {"a", "a_scale", "a_zero_point", "b", "b_scale", "b_zero_point", "y_scale",
+                         "y_zero_point", "y"};
+  for (int i = 0; i < 9; ++i) CheckDescriptor(req[i], names[i]);
+  // :225-227 (allocating overload), then :246-264
+  OLA_ENFORCE(IsInt8OrUint8(a->data_type), kQlmName, ": a must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(b->data_type), kQlmName, ": b must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(y_zp->data_type), kQlmName, ": y_zero_point must be INT8 or UINT8.");
+  OLA_ENFORCE(a_zp->data_type == a->data_type, kQlmName, ": a_zero_point dtype must match a.");
+  OLA_ENFORCE(b_zp->data_type == b->data_type, kQlmName, ": b_zero_point dtype must match b.");
+  OLA_ENFORCE(y->data_type == y_zp->data_type, kQlmName, ": output dtype must match y_zero_point.");
+  const MatMulPlan plan = MakeMatMulPlan(
+      ShapeOf(*a), ShapeOf(*b), kQlmName, ": rank-0 inputs are not accepted.",
+      ": incompatible inner dimensions.", ": inputs are not broadcast-compatible on batch dimensions.");
+  OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kQlmName, ": preallocated output has invalid shape.");
+  OLA_ENFORCE(y->size_bytes >= NumElements(plan.out_shape), kQlmName,
+              ": preallocated output buffer size does not match its shape.");
+  const int32_t za = QReadScalarInt(*a_zp, "a_zero_point");
+  const int32_t zb = QReadScalarInt(*b_zp, "b_zero_point");
+  const int32_t zy = QReadScalarInt(*y_zp, "y_zero_point");
+  const float as = QReadScalarFloat(*a_scale, "a_scale");
+  const float bs = QReadScalarFloat(*b_scale, "b_scale");
+  const float ys = QReadScalarFloat(*y_scale, "y_scale");
+  OLA_ENFORCE(ys != 0.0f, kQlmName, ": y_scale must be non-zero.");
+
+  // The reference accumulates in int64 (:187-191); the MFMA path is exact
+  // while |sum| < 2^31, guaranteed by K * max|a-za| * max|b-zb| < 2^31.
+  auto span = [](int32_t dt, int32_t z) -> int64_t {
+    const int64_t lo = dt == kInt8 ? -128 : 0, hi = dt == kInt8 ? 127 : 255;
+    return std::max<int64_t>(std::llabs(lo - z), std::llabs(hi - z));
+  };
+  const double bound = (double)plan.K * (double)span(a->data_type, za) * (double)span(b->data_type, zb);
+  if (!(bound < 2147483648.0))
+    throw Unsupported("QLinearMatMul: K too large for exact int32 accumulation on the GPU path");
+
+  IGemmParams p{};
+  p.M = plan.M;
+  p.N = plan.N;
+  p.K = plan.K;
+  p.batch = plan.batch;
+  p.bm = ToBatchMap(plan);
+  p.a_u8 = a->data_type == kUint8;
+  p.b_u8 = b->data_type == kUint8;
+  p.alpha_scalar = (p.a_u8 ? 128 : 0) - za;
+  p.beta_scalar = (p.b_u8 ? 128 : 0) - zb;
+  p.need_cb = p.alpha_scalar != 0;
+  p.need_ra = p.beta_scalar != 0;
+  // combined scale in fp32, left to right (:156)
+  const float ab = as * bs;
+  p.cs = ab / ys;
+  p.zy = (float)zy;
+  p.y_signed = y->data_type == kInt8;
+  p.qmin = p.y_signed ? -128.0f : 0.0f;
+  p.qmax = p.y_signed ? 127.0f : 255.0f;
+  p.epilogue = kEpiQuant8;
+
+  Staging st(stream, 0, {a, b}, {y});
+  p.A = static_cast<const int8_t *>(st.In(a));
+  p.B = static_cast<const int8_t *>(st.In(b));
+  p.Y = st.Out(y);
+  LaunchIGemm(p, stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// DequantizeLinear, kq/kernel_dequantizelinear.cc.
+
+constexpr const char *kDqSupportedMsg =
+    "kernel::DequantizeLinear: only UINT8, INT8, UINT16, INT16, INT32, FLOAT8E4M3FN, "
+    "FLOAT8E4M3FNUZ, FLOAT8E5M2, FLOAT8E5M2FNUZ, INT4, UINT4, INT2, UINT2 and FLOAT4E2M1 inputs "
+    "are supported.";
+
+bool IsSupportedScaleDType(int32_t dt) { return dt == kFloat || dt == kFloat16; }
+
+bool DqGpuDtype(int32_t dt) {
+  switch (dt) {
+  case kUint8: case kInt8: case kUint16: case kInt16: case kInt32: case kFloat8E4M3FN:
+  case kInt4: case kUint4:
+    return true;
+  default:
+    return false;
+  }
+}
+
+void CheckDqDtype(int32_t dt) {
+  // Types the reference accepts but this GPU path does not decode.
+  switch (dt) {
+  case 18: case 19: case 20: case 23: case 24: case 25: case 26: case 27:
+    throw Unsupported(Cat("DequantizeLinear: input dtype ", dt, " has no GPU kernel"));
+  default:
+    break;
+  }
+  if (!DqGpuDtype(dt)) throw InvalidArgument(Cat("unsupported data type ", dt, ", ", kDqSupportedMsg));
+}
+
+void CheckDqOutput(const onnxl_amd_tensor &x, const onnxl_amd_tensor &y) {
+  OLA_ENFORCE(ShapeOf(y) == ShapeOf(x),
+              "kernel::DequantizeLinear preallocated output shape must match x shape.");
+  OLA_ENFORCE(y.size_bytes == NumElements(x) * ElementSize(y.data_type),
+              "kernel::DequantizeLinear preallocated output buffer has unexpected size in bytes.");
+}
+
+int DequantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                     const onnxl_amd_tensor *x_zp, int64_t axis, onnxl_amd_tensor *y,
+                     hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && !Absent(x_scale) && y, "kernel::DequantizeLinear: x, x_scale and the "
+              "output are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(x_scale, "x_scale");
+  CheckDescriptor(x_zp, "x_zero_point");
+  CheckDescriptor(y, "y");
+  const bool has_zp = !Absent(x_zp);
+  DequantParams p{};
+  p.n = NumElements(*x);
+  p.x_dtype = x->data_type;
+  if (NumElements(*x_scale) == 1) {
+    // per-tensor, :349-410 (no zero point) and :426-502
+    OLA_ENFORCE(IsSupportedScaleDType(x_scale->data_type),
+                "kernel::DequantizeLinear: x_scale must be FLOAT or FLOAT16.");
+    if (has_zp) {
+      OLA_ENFORCE(NumElements(*x_zp) == 1,
+                  "kernel::DequantizeLinear: x_zero_point must be a scalar (per-tensor dequantization).");
+      OLA_ENFORCE(x->data_type == x_zp->data_type,
+                  "kernel::DequantizeLinear: x_zero_point data_type must match x.");
+      OLA_ENFORCE(y->data_type == x_scale->data_type,
+                  "kernel::DequantizeLinear: output dtype must match x_scale.");
+    } else {
+      OLA_ENFORCE(y->data_type == x_scale->data_type,
+                  "kernel::DequantizeLinear: output (no x_zero_point) dtype must match x_scale.");
+    }
+    CheckDqOutput(*x, *y);
+    CheckDqDtype(x->data_type);
+    p.mode = 0;
+  } else {
+    // per-axis / blocked, :522-651 (with zero point) and :670-693 (without)
+    if (!has_zp)
+      OLA_ENFORCE(axis >= 0 && axis < x->rank, "kernel::DequantizeLinear: axis out of range.");
+    OLA_ENFORCE(IsSupportedScaleDType(x_scale->data_type),
+                "kernel::DequantizeLinear: x_scale must be FLOAT or FLOAT16.");
+    if (has_zp)
+      OLA_ENFORCE(x->data_type == x_zp->data_type,
+                  "kernel::DequantizeLinear: x_zero_point data_type must match x.");
+    OLA_ENFORCE(y->data_type == x_scale->data_type,
+                "kernel::DequantizeLinear: output dtype must match x_scale.");
+    CheckDqOutput(*x, *y);
+    OLA_ENFORCE(axis >= 0 && axis < x->rank, "kernel::DequantizeLinear: axis out of range.");
+    if (has_zp)
+      OLA_ENFORCE(ShapeOf(*x_scale) == ShapeOf(*x_zp),
+                  "kernel::DequantizeLinear: x_scale and x_zero_point must have the same shape.");
+    const Shape xs = ShapeOf(*x), ss = ShapeOf(*x_scale);
+    p.inner = 1;
+    for (int d = (int)axis + 1; d < x->rank; ++d) p.inner *= xs[d];
+    p.axis_len = xs[axis];
+    if (ss.size() == xs.size()) {
+      for (size_t d = 0; d < xs.size(); ++d) {
+        const int64_t s_dim = ss[d];
+        OLA_ENFORCE(s_dim > 0 && xs[d] % s_dim == 0,
+                    "kernel::DequantizeLinear: blocked x_scale dimension must divide the matching x "
+                    "dimension.");
+        OLA_ENFORCE((int64_t)d == axis || s_dim == xs[d],
+                    "kernel::DequantizeLinear: blocked x_scale may only differ from x along the "
+                    "quantization axis.");
+      }
+      p.mode = 2;
+      p.s_axis = ss[axis];
+      p.block = xs[axis] / ss[axis];
+    } else {
+      OLA_ENFORCE(NumElements(*x_scale) == xs[axis],
+                  "kernel::DequantizeLinear: x_scale element count must equal axis dimension.");
+      p.mode = 1;
+    }
+    CheckDqDtype(x->data_type);
+  }
+  p.scale_f16 = x_scale->data_type == kFloat16;
+  Staging st(stream, 0, {x, x_scale, has_zp ? x_zp : nullptr}, {y});
+  p.x = st.In(x);
+  p.scale = st.In(x_scale);
+  p.zp = has_zp ? st.In(x_zp) : nullptr;
+  p.y = st.Out(y);
+  LaunchDequantize(p, stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Cast FLOAT -> FLOAT16 / BFLOAT16.
+
+int Cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && y, "kernel::Cast: input and output are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y, "y");
+  if (x->data_type != kFloat || (to != kFloat16 && to != kBfloat16))
+    throw Unsupported("Cast: only FLOAT -> FLOAT16 / BFLOAT16 runs on the GPU path");
+  OLA_ENFORCE(y->data_type == to, "kernel::Cast: output dtype must match 'to'.");
+  OLA_ENFORCE(ShapeOf(*y) == ShapeOf(*x), "kernel::Cast: output shape must match input shape.");
+  OLA_ENFORCE(y->size_bytes == NumElements(*x) * 2, "kernel::Cast: output size does not match.");
+  Staging st(stream, 0, {x}, {y});
+  LaunchCastF32(static_cast<const float *>(st.In(x)), st.Out(y), NumElements(*x), to == kBfloat16,
+                stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MatMul FLOAT16 / BFLOAT16, km/kernel_matmul.cc:225-253.
+
+constexpr const char *kMmName = "kernel::MatMul";
+
+int MatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tensor *y,
+           hipStream_t stream) {
+  OLA_ENFORCE(!Absent(a) && !Absent(b) && y, kMmName, ": A, B and the output are required.");
+  CheckDescriptor(a, "A");
+  CheckDescriptor(b, "B");
+  CheckDescriptor(y, "Y");
+  OLA_ENFORCE(a->data_type == b->data_type, kMmName, " inputs must share the same dtype.");
+  if (a->data_type != kFloat16 && a->data_type != kBfloat16)
+    throw Unsupported("MatMul: only FLOAT16 / BFLOAT16 run on the GPU path");
+  OLA_ENFORCE(y->data_type == a->data_type, kMmName,
+              " preallocated output must have the same dtype as input A.");
+  const MatMulPlan plan = MakeMatMulPlan(ShapeOf(*a), ShapeOf(*b), kMmName,
+                                         " does not accept rank-0 inputs.",
+                                         " got incompatible inner dimensions.",
+                                         " inputs are not broadcast-compatible on batch dimensions.");
+  OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kMmName, " preallocated output has an invalid shape.");
+  OLA_ENFORCE(y->size_bytes == NumElements(plan.out_shape) * 2, kMmName,
+              " preallocated output buffer size does not match its shape.");
+  HMatMulParams p{};
+  p.M = plan.M;
+  p.N = plan.N;
+  p.K = plan.K;
+  p.batch = plan.batch;
+  p.bm = ToBatchMap(plan);
+  p.bf16 = a->data_type == kBfloat16;
+  Staging st(stream, 0, {a, b}, {y});
+  p.A = static_cast<const uint16_t *>(st.In(a));
+  p.B = static_cast<const uint16_t *>(st.In(b));
+  p.Y = static_cast<uint16_t *>(st.Out(y));
+  LaunchHMatMul(p, stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused DequantizeLinear -> [Cast] -> MatMul.
+
+constexpr const char *kDqmName = "DequantizeLinearMatMul";
+
+int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+             const onnxl_amd_tensor *x_zp, int64_t axis, int32_t cast_to, onnxl_amd_tensor *y,
+             hipStream_t stream) {
+  OLA_ENFORCE(!Absent(a) && !Absent(x) && !Absent(x_scale) && y, kDqmName,
+              ": A, x, x_scale and the output are required.");
+  CheckDescriptor(a, "A");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(x_scale, "x_scale");
+  CheckDescriptor(x_zp, "x_zero_point");
+  CheckDescriptor(y, "Y");
+  const bool has_zp = !Absent(x_zp);
+  // The DequantizeLinear node's own checks (kq/kernel_dequantizelinear.cc:522-565).
+  OLA_ENFORCE(IsSupportedScaleDType(x_scale->data_type),
+              "kernel::DequantizeLinear: x_scale must be FLOAT or FLOAT16.");
+  if (has_zp)
+    OLA_ENFORCE(x->data_type == x_zp->data_type,
+                "kernel::DequantizeLinear: x_zero_point data_type must match x.");
+  OLA_ENFORCE(x->rank == 2, kDqmName, ": the quantized weight must be 2-D [K, N].");
+  const Shape xs = ShapeOf(*x), ss = ShapeOf(*x_scale);
+  const int64_t K = xs[0], N = xs[1];
+  DqMatMulParams p{};
+  const int64_t scount = NumElements(*x_scale);
+  if (scount == 1) {
+    if (has_zp)
+      OLA_ENFORCE(NumElements(*x_zp) == 1,
+                  "kernel::DequantizeLinear: x_zero_point must be a scalar (per-tensor dequantization).");
+    p.mode = 0;
+  } else {
+    OLA_ENFORCE(axis >= 0 && axis < 2, "kernel::DequantizeLinear: axis out of range.");
+    if (has_zp)
+      OLA_ENFORCE(ShapeOf(*x_scale) == ShapeOf(*x_zp),
+                  "kernel::DequantizeLinear: x_scale and x_zero_point must have the same shape.");
+    if (ss.size() == 2) {
+      for (size_t d = 0; d < 2; ++d) {
+        OLA_ENFORCE(ss[d] > 0 && xs[d] % ss[d] == 0,
+                    "kernel::DequantizeLinear: blocked x_scale dimension must divide the matching x "
+                    "dimension.");
+        OLA_ENFORCE((int64_t)d == axis || ss[d] == xs[d],
+                    "kernel::DequantizeLinear: blocked x_scale may only differ from x along the "
+                    "quantization axis.");
+      }
+      if (axis != 0) throw Unsupported(Cat(kDqmName, ": scales blocked along N"));
+      p.mode = 2;
+      p.block = K / ss[0];
+    } else {
+      OLA_ENFORCE(scount == xs[axis],
+                  "kernel::DequantizeLinear: x_scale element count must equal axis dimension.");
+      if (axis != 1) throw Unsupported(Cat(kDqmName, ": 1-D per-row (axis 0) scales"));
+      p.mode = 1;
+    }
+  }
+  switch (x->data_type) {
+  case kInt4: case kUint4: case kInt8: case kUint8: case kFloat8E4M3FN: break;
+  default: throw Unsupported(Cat(kDqmName, ": weight dtype ", x->data_type, " has no GPU kernel"));
+  }
+  // Rounding chain of the unfused graph: DequantizeLinear output = x_scale
+  // dtype; optional Cast; then MatMul requires both operands to share A's dtype.
+  const int32_t dq_out = x_scale->data_type;
+  const int32_t w_dtype = cast_to ? cast_to : dq_out;
+  OLA_ENFORCE(a->data_type == kFloat16 || a->data_type == kBfloat16, kDqmName,
+              ": A must be FLOAT16 or BFLOAT16.");
+  OLA_ENFORCE(w_dtype == a->data_type, kMmName, " inputs must share the same dtype.");
+  if (cast_to)
+    OLA_ENFORCE(dq_out == kFloat, kDqmName, ": the Cast step must convert a FLOAT DequantizeLinear output.");
+  OLA_ENFORCE(y->data_type == a->data_type, kMmName,
+              " preallocated output must have the same dtype as input A.");
+  const MatMulPlan plan = MakeMatMulPlan(ShapeOf(*a), xs, kMmName, " does not accept rank-0 inputs.",
+                                         " got incompatible inner dimensions.",
+                                         " inputs are not broadcast-compatible on batch dimensions.");
+  OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kMmName, " preallocated output has an invalid shape.");
+  OLA_ENFORCE(y->size_bytes == NumElements(plan.out_shape) * 2, kMmName,
+              " preallocated output buffer size does not match its shape.");
+  p.M = plan.M * plan.batch;  // A batches are contiguous rows; W is shared
+  p.N = N;
+  p.K = K;
+  p.w_dtype = x->data_type;
+  p.scale_f16 = x_scale->data_type == kFloat16;
+  p.a_bf16 = a->data_type == kBfloat16;
+  p.deq_round_f16 = dq_out == kFloat16;
+  p.cast_round = cast_to == kBfloat16 ? 16 : (cast_to == kFloat16 ? 10 : 0);
+  const size_t scratch = DqMatMulScratchBytes(p);
+  Staging st(stream, scratch, {a, x, x_scale, has_zp ? x_zp : nullptr}, {y});
+  p.A = st.In(a);
+  p.W = static_cast<const uint8_t *>(st.In(x));
+  p.scale = st.In(x_scale);
+  p.zp = has_zp ? static_cast<const uint8_t *>(st.In(x_zp)) : nullptr;
+  p.Y = st.Out(y);
+  const size_t nc = DqMatMulCounters(p);
+  unsigned *counters = nc ? Ctx().ws.Counters(nc) : nullptr;
+  if (!LaunchDqMatMul(p, st.Extra(), scratch, counters, nc, stream))
+    throw Unsupported(Cat(kDqmName, ": no GPU kernel for this shape / dtype combination"));
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// Validation runs before any device work, so argument errors are reported
+// even before onnxl_amd_init (the first device access then raises
+// NotInitialized).
+template <typename F> int Guard(F &&f) {
+  try {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (Initialized()) OLA_HIP(hipSetDevice(g_ctx.device));
+    return f();
+  } catch (const NotInitialized &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_NOT_INITIALIZED;
+  } catch (const InvalidArgument &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_INVALID_ARGUMENT;
+  } catch (const Unsupported &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_UNSUPPORTED;
+  } catch (const std::exception &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_DEVICE_ERROR;
+  }
+}
+
+}  // namespace
+}  // namespace onnxl_amd
+
+using namespace onnxl_amd;
+
+extern "C" {
+
+int onnxl_amd_init(int device_ordinal) {
+  try {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int n = 0;
+    OLA_HIP(hipGetDeviceCount(&n));
+    OLA_ENFORCE(device_ordinal >= 0 && device_ordinal < n, "onnxl_amd_init: device ", device_ordinal,
+                " out of range (", n, " devices)");
+    OLA_HIP(hipSetDevice(device_ordinal));
+    hipDeviceProp_t prop;
+    OLA_HIP(hipGetDeviceProperties(&prop, device_ordinal));
+    const std::string arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+      throw Unsupported(Cat("onnxl_amd_init: device is ", arch, ", kernels are built for gfx950"));
+    if (g_init.load() && g_ctx.device != device_ordinal) g_ctx.ws.Release();
+    g_ctx.device = device_ordinal;
+    g_ctx.num_cus = prop.multiProcessorCount;
+    g_init.store(true);
+    return ONNXL_AMD_OK;
+  } catch (const InvalidArgument &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_INVALID_ARGUMENT;
+  } catch (const Unsupported &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_UNSUPPORTED;
+  } catch (const std::exception &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_DEVICE_ERROR;
+  }
+}
+
+int onnxl_amd_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_init.load()) {
+    (void)hipSetDevice(g_ctx.device);
+    (void)hipDeviceSynchronize();
+    g_ctx.ws.Release();
+  }
+  g_init.store(false);
+  return ONNXL_AMD_OK;
+}
+
+const char *onnxl_amd_last_error(void) { return g_last_error.c_str(); }
+
+const char *onnxl_amd_version(void) { return "onnxl_amd 0.1.0 (gfx950)"; }
+
+int onnxl_amd_matmul_shape(const int64_t *a_dims, int32_t a_rank, const int64_t *b_dims,
+                           int32_t b_rank, int64_t *out_dims, int32_t *out_rank) {
+  try {
+    OLA_ENFORCE(a_rank >= 0 && b_rank >= 0 && a_rank <= ONNXL_AMD_MAX_RANK &&
+                    b_rank <= ONNXL_AMD_MAX_RANK,
+                "onnxl_amd_matmul_shape: rank out of range");
+    const MatMulPlan p = MakeMatMulPlan(Shape(a_dims, a_dims + a_rank), Shape(b_dims, b_dims + b_rank),
+                                        "kernel::MatMul", " does not accept rank-0 inputs.",
+                                        " got incompatible inner dimensions.",
+                                        " inputs are not broadcast-compatible on batch dimensions.");
+    OLA_ENFORCE((int)p.out_shape.size() <= ONNXL_AMD_MAX_RANK, "output rank too large");
+    for (size_t i = 0; i < p.out_shape.size(); ++i) out_dims[i] = p.out_shape[i];
+    *out_rank = (int32_t)p.out_shape.size();
+    return ONNXL_AMD_OK;
+  } catch (const InvalidArgument &e) {
+    g_last_error = e.what();
+    return ONNXL_AMD_INVALID_ARGUMENT;
+  }
+}
+
+int onnxl_amd_matmul_integer(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
+                             const onnxl_amd_tensor *a_zero_point,
+                             const onnxl_amd_tensor *b_zero_point, onnxl_amd_tensor *y,
+                             void *stream) {
+  return Guard([&] {
+    return MatMulInteger(a, b, a_zero_point, b_zero_point, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_qlinear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
+                             const onnxl_amd_tensor *a_zero_point, const onnxl_amd_tensor *b,
+                             const onnxl_amd_tensor *b_scale,
+                             const onnxl_amd_tensor *b_zero_point,
+                             const onnxl_amd_tensor *y_scale,
+                             const onnxl_amd_tensor *y_zero_point, onnxl_amd_tensor *y,
+                             void *stream) {
+  return Guard([&] {
+    return QLinearMatMul(a, a_scale, a_zero_point, b, b_scale, b_zero_point, y_scale, y_zero_point, y,
+                         static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                                const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeLinear(x, x_scale, x_zero_point, axis, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tensor *y,
+                     void *stream) {
+  return Guard([&] { return MatMul(a, b, y, static_cast<hipStream_t>(stream)); });
+}
+
+int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] { return Cast(x, to, y, static_cast<hipStream_t>(stream)); });
+}
+
+int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
+                                       const onnxl_amd_tensor *x_scale,
+                                       const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                       int32_t cast_to, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DqMatMul(a, x, x_scale, x_zero_point, axis, cast_to, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_synchronize(void *stream) {
+  return Guard([&] {
+    OLA_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return ONNXL_AMD_OK;
+  });
+}
+
+}  // extern "C"

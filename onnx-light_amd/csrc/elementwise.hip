@@ -1,0 +1,105 @@
+// Element-wise kernels: standalone DequantizeLinear (per-tensor, per-axis,
+// blocked; kq/kernel_dequantizelinear.cc) and the FLOAT -> FLOAT16/BFLOAT16
+// Cast (ext/kernels/kernels/tensor/kernel_cast.cc:360-370).  Both are
+// HBM-bound streams: each thread handles 8 consecutive elements so 4-bit
+// inputs are read a whole 32-bit word at a time.
+#include "common.hpp"
+#include "device_codecs.hpp"
+#include "kernels.hpp"
+
+namespace onnxl_amd {
+namespace {
+
+constexpr int kPerThread = 8;
+constexpr int kBlock = 256;
+
+template <int XT>
+__device__ __forceinline__ float Decode(const void *base, int64_t i) {
+  if constexpr (XT == kUint8) return (float)static_cast<const uint8_t *>(base)[i];
+  if constexpr (XT == kInt8) return (float)static_cast<const int8_t *>(base)[i];
+  if constexpr (XT == kUint16) return (float)static_cast<const uint16_t *>(base)[i];
+  if constexpr (XT == kInt16) return (float)static_cast<const int16_t *>(base)[i];
+  if constexpr (XT == kInt32) return (float)static_cast<const int32_t *>(base)[i];
+  if constexpr (XT == kFloat8E4M3FN) return Fp8E4M3ToF32(static_cast<const uint8_t *>(base)[i]);
+  const uint8_t byte = static_cast<const uint8_t *>(base)[i >> 1];
+  const uint32_t nib = (i & 1) ? (byte >> 4) : (byte & 0xfu);
+  if constexpr (XT == kInt4) return (float)Int4ToInt(nib);
+  return (float)nib;  // kUint4
+}
+
+template <int XT, int MODE, bool F16S>
+__global__ __launch_bounds__(kBlock) void DequantKernel(const DequantParams p) {
+  const int64_t first = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * kPerThread;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    const int64_t i = first + e;
+    if (i >= p.n) return;
+    int64_t si = 0;
+    if (MODE == 1) {
+      si = (i / p.inner) % p.axis_len;
+    } else if (MODE == 2) {
+      const int64_t outer = i / (p.axis_len * p.inner);
+      const int64_t a = (i / p.inner) % p.axis_len;
+      si = (outer * p.s_axis + a / p.block) * p.inner + i % p.inner;
+    }
+    const float s = F16S ? F16ToF32(static_cast<const uint16_t *>(p.scale)[si])
+                         : static_cast<const float *>(p.scale)[si];
+    const float z = p.zp ? Decode<XT>(p.zp, si) : 0.0f;
+    const float v = (Decode<XT>(p.x, i) - z) * s;
+    if (F16S) {
+      static_cast<uint16_t *>(p.y)[i] = F32ToF16(v);
+    } else {
+      static_cast<float *>(p.y)[i] = v;
+    }
+  }
+}
+
+template <int XT, int MODE>
+void LaunchMode(const DequantParams &p, dim3 g, hipStream_t s) {
+  if (p.scale_f16) hipLaunchKernelGGL((DequantKernel<XT, MODE, true>), g, dim3(kBlock), 0, s, p);
+  else hipLaunchKernelGGL((DequantKernel<XT, MODE, false>), g, dim3(kBlock), 0, s, p);
+}
+
+template <int XT>
+void LaunchX(const DequantParams &p, dim3 g, hipStream_t s) {
+  if (p.mode == 0) LaunchMode<XT, 0>(p, g, s);
+  else if (p.mode == 1) LaunchMode<XT, 1>(p, g, s);
+  else LaunchMode<XT, 2>(p, g, s);
+}
+
+__global__ __launch_bounds__(kBlock) void CastF32Kernel(const float *x, uint16_t *y, int64_t n,
+                                                        int to_bf16) {
+  const int64_t first = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * kPerThread;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    const int64_t i = first + e;
+    if (i >= n) return;
+    y[i] = to_bf16 ? F32ToBf16(x[i]) : F32ToF16(x[i]);
+  }
+}
+
+}  // namespace
+
+void LaunchDequantize(const DequantParams &p, hipStream_t s) {
+  if (p.n == 0) return;
+  const dim3 g((unsigned)((p.n + (int64_t)kBlock * kPerThread - 1) / ((int64_t)kBlock * kPerThread)));
+  switch (p.x_dtype) {
+  case kUint8: LaunchX<kUint8>(p, g, s); break;
+  case kInt8: LaunchX<kInt8>(p, g, s); break;
+  case kUint16: LaunchX<kUint16>(p, g, s); break;
+  case kInt16: LaunchX<kInt16>(p, g, s); break;
+  case kInt32: LaunchX<kInt32>(p, g, s); break;
+  case kFloat8E4M3FN: LaunchX<kFloat8E4M3FN>(p, g, s); break;
+  case kInt4: LaunchX<kInt4>(p, g, s); break;
+  case kUint4: LaunchX<kUint4>(p, g, s); break;
+  default: throw Unsupported("DequantizeLinear: no GPU kernel for this dtype");
+  }
+}
+
+void LaunchCastF32(const float *x, void *y, int64_t n, int to_bf16, hipStream_t s) {
+  if (n == 0) return;
+  const dim3 g((unsigned)((n + (int64_t)kBlock * kPerThread - 1) / ((int64_t)kBlock * kPerThread)));
+  hipLaunchKernelGGL(CastF32Kernel, g, dim3(kBlock), 0, s, x, static_cast<uint16_t *>(y), n, to_bf16);
+}
+
+}  // namespace onnxl_amd

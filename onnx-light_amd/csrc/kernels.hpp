@@ -1,0 +1,134 @@
+// Launch parameters and launcher declarations of the gfx950 kernels.  Plain
+// structs passed by value as kernel arguments.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace onnxl_amd {
+
+constexpr int kMaxBatchRank = 6;
+
+// Maps a flat output-batch index to element offsets of A and B under ONNX
+// MatMul broadcasting (row-major over `dims`; stride 0 = broadcast dim).
+struct BatchMap {
+  int rank = 0;
+  int64_t dims[kMaxBatchRank] = {};
+  int64_t a_stride[kMaxBatchRank] = {};
+  int64_t b_stride[kMaxBatchRank] = {};
+};
+
+__host__ __device__ inline void BatchOffsets(const BatchMap &m, int64_t batch, int64_t &a_off,
+                                             int64_t &b_off) {
+  int64_t ao = 0, bo = 0, rem = batch;
+  for (int d = m.rank - 1; d >= 0; --d) {
+    const int64_t c = rem % m.dims[d];
+    rem /= m.dims[d];
+    ao += c * m.a_stride[d];
+    bo += c * m.b_stride[d];
+  }
+  a_off = ao;
+  b_off = bo;
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA GEMM shared by MatMulInteger and QLinearMatMul.
+//
+// The MFMA runs on a' = a - ca and b' = b - cb as signed bytes (ca = 128 for
+// UINT8 A, i.e. a ^ 0x80, else 0; cb likewise).  With alpha_i = ca - za_i and
+// beta_j = cb - zb_j the exact result is
+//   Y_ij = sum_k a'b' + beta_j*RA_i + alpha_i*CB_j + K*alpha_i*beta_j,
+// RA_i = sum_k a'_ik, CB_j = sum_k b'_kj, evaluated modulo 2^32 (which is the
+// int32 wrap of the reference's accumulator).
+
+enum IGemmEpilogue : int { kEpiInt32 = 0, kEpiQuant8 = 1 };
+
+struct IGemmParams {
+  const int8_t *A;  // [.., M, K] row-major
+  const int8_t *B;  // [.., K, N] row-major
+  void *Y;          // [batch, M, N]
+  int64_t M, N, K;
+  int64_t batch;
+  BatchMap bm;
+  int a_u8, b_u8;
+  // Per-row / per-column zero points (M / N bytes in A's / B's dtype), or
+  // nullptr when the zero point is a single value: alpha_scalar / beta_scalar
+  // then hold ca - za / cb - zb.
+  const uint8_t *a_zp;
+  const uint8_t *b_zp;
+  int32_t alpha_scalar, beta_scalar;
+  int need_ra, need_cb;  // beta != 0 anywhere / alpha != 0 anywhere
+  // kEpiQuant8: v = rint((float)acc * cs) + zy, clamped to [qmin, qmax]
+  float cs, zy, qmin, qmax;
+  int y_signed;
+  int epilogue;
+};
+
+void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// DequantizeLinear (standalone, element-wise).
+
+struct DequantParams {
+  const void *x;
+  const void *scale;  // FLOAT or FLOAT16 values
+  const void *zp;     // same storage type as x, or nullptr
+  void *y;            // FLOAT or FLOAT16 (= scale dtype)
+  int64_t n;          // elements of x
+  int x_dtype, scale_f16;
+  // scale index of flat element i: ((i / inner) / block) % ... computed as
+  //   outer = i / (axis_len * inner); a = (i / inner) % axis_len; in = i % inner
+  //   si = (outer * s_axis + a / block) * inner + in      (blocked, s_axis = axis_len / block)
+  //   si = a                                                (per-axis)
+  //   si = 0                                                (per-tensor)
+  int mode;           // 0 per-tensor, 1 per-axis, 2 blocked
+  int64_t inner, axis_len, block, s_axis;
+};
+
+void LaunchDequantize(const DequantParams &p, hipStream_t stream);
+
+// Cast FLOAT -> FLOAT16 / BFLOAT16 (round to nearest even).
+void LaunchCastF32(const float *x, void *y, int64_t n, int to_bf16, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Dequantize-fused MatMul: Y[M,N] = A[M,K] @ W[K,N], W = round(deq(x)).
+
+struct DqMatMulParams {
+  const void *A;     // FLOAT16 / BFLOAT16 activations [batch*M, K] (contiguous rows)
+  const uint8_t *W;  // quantized weight [K, N] (4-bit: N/2 bytes per row)
+  const void *scale; // FLOAT or FLOAT16
+  const uint8_t *zp; // same storage as W (per scale entry) or nullptr
+  void *Y;           // activations dtype [batch*M, N]
+  int64_t M, N, K;
+  int w_dtype;       // kInt4, kUint4, kInt8, kUint8, kFloat8E4M3FN
+  int scale_f16;     // scale storage is FLOAT16 (else FLOAT)
+  int a_bf16;        // activations/output are BFLOAT16 (else FLOAT16)
+  int mode;          // 0 per-tensor, 1 per-column (axis 1), 2 blocked along K (axis 0)
+  int64_t block;     // rows of K per scale row (mode 2)
+  // Rounding of the dequantized weight, as the unfused chain does it:
+  //   deq_round: 1 = to FLOAT16 (x_scale FLOAT16), 0 = stays FLOAT
+  //   cast_round: 16 = to BFLOAT16, 10 = to FLOAT16, 0 = none
+  int deq_round_f16;
+  int cast_round;
+};
+
+// Returns false when the shape/dtype combination has no GPU kernel.
+bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes,
+                    unsigned *counters, size_t n_counters, hipStream_t stream);
+size_t DqMatMulScratchBytes(const DqMatMulParams &p);
+size_t DqMatMulCounters(const DqMatMulParams &p);
+
+// Plain FLOAT16 / BFLOAT16 MatMul (fp32 accumulate).
+struct HMatMulParams {
+  const uint16_t *A;
+  const uint16_t *B;
+  uint16_t *Y;
+  int64_t M, N, K;
+  int64_t batch;
+  BatchMap bm;
+  int bf16;
+};
+void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream);
+
+}  // namespace onnxl_amd

@@ -1,0 +1,186 @@
+"""C-ABI host logic without a GPU: the library loads, exports every symbol the
+header declares, and reproduces the reference kernels' validation (same
+checks and message text) before touching the device.  Calls whose arguments
+are valid stop at NOT_INITIALIZED (no GPU here): no kernel runs on the CPU."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    with open(os.path.join(ROOT, "include", "onnxl_amd.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(onnxl_amd_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol(olamd):
+    names = _header_functions()
+    assert len(names) >= 11
+    L = olamd.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.onnxl_amd_version().startswith(b"onnxl_amd")
+
+
+def test_library_carries_gfx950_code_objects():
+    with open(os.path.join(ROOT, "onnx-light_amd", "libonnxl_amd.so"), "rb") as f:
+        blob = f.read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+
+
+def _call(olamd, fn, *args):
+    rc = getattr(olamd.lib(), fn)(*args)
+    return rc, olamd.lib().onnxl_amd_last_error().decode()
+
+
+def test_matmul_integer_validation(olamd):
+    d = olamd.describe
+    a = np.zeros((4, 3), np.uint8)
+    b = np.zeros((3, 2), np.uint8)
+    y = np.zeros((4, 2), np.int32)
+    cases = [
+        ((np.zeros((4, 3), np.int32), b, None, None, y), "A must be INT8 or UINT8."),  # :2268-2276
+        ((a, np.zeros((3, 2), np.float32), None, None, y), "B must be INT8 or UINT8."),
+        ((a, b, None, None, np.zeros((4, 2), np.float32)), "output dtype must be INT32."),
+        ((a, np.zeros((4, 2), np.uint8), None, None, y), "incompatible inner dimensions."),
+        ((a, b, None, None, np.zeros((4, 3), np.int32)), "preallocated output has invalid shape."),
+        ((a, b, np.zeros(1, np.int8), None, y), "'a_zero_point' dtype must match its data input."),
+        ((a, b, np.zeros((2, 2), np.uint8), None, y), "'a_zero_point' must be a scalar or a 1-D tensor."),
+        ((a, b, np.zeros(3, np.uint8), None, y), "'a_zero_point' must be a scalar, a one-element 1-D"),
+        ((a, b, None, np.zeros(4, np.uint8), y), "'b_zero_point' must be a scalar, a one-element 1-D"),
+        ((np.zeros((2, 4, 3), np.uint8), np.zeros((3, 3, 2), np.uint8), None, None,
+          np.zeros((3, 4, 2), np.int32)), "not broadcast-compatible on batch dimensions."),
+    ]
+    for args, msg in cases:
+        rc, err = _call(olamd, "onnxl_amd_matmul_integer", *[d(t) for t in args], None)
+        assert rc == olamd.INVALID_ARGUMENT, (msg, err)
+        assert err.startswith("[onnx-light] kernel::MatMulInteger")
+        assert msg in err, (msg, err)
+    # rank-0 input
+    rc, err = _call(olamd, "onnxl_amd_matmul_integer", d(np.zeros((), np.uint8)), d(b), d(None), d(None),
+                    d(y), None)
+    assert rc == olamd.INVALID_ARGUMENT and "rank-0 inputs are not accepted." in err
+    # valid arguments stop at the device
+    rc, _ = _call(olamd, "onnxl_amd_matmul_integer", d(a), d(b), d(np.array([1, 2, 3, 4], np.uint8)),
+                  d(np.array(3, np.uint8)), d(y), None)
+    assert rc == olamd.NOT_INITIALIZED
+
+
+def test_qlinear_validation(olamd):
+    d = olamd.describe
+    a = np.zeros((2, 4), np.uint8)
+    b = np.zeros((4, 3), np.int8)
+    f = lambda v: np.array(v, np.float32)
+    u = lambda v: np.array(v, np.uint8)
+    s = lambda v: np.array(v, np.int8)
+    y = np.zeros((2, 3), np.uint8)
+    base = [a, f(0.1), u(1), b, f(0.2), s(0), f(0.3), u(2), y]
+
+    def run(**over):
+        args = list(base)
+        for k, v in over.items():
+            args[int(k[1:])] = v
+        return _call(olamd, "onnxl_amd_qlinear_matmul", *[d(t) for t in args], None)
+
+    rc, err = run(i0=np.zeros((2, 4), np.int16))
+    assert rc == olamd.INVALID_ARGUMENT and "a must be INT8 or UINT8." in err
+    rc, err = run(i2=s(1))
+    assert rc == olamd.INVALID_ARGUMENT and "a_zero_point dtype must match a." in err
+    rc, err = run(i5=u(1))
+    assert rc == olamd.INVALID_ARGUMENT and "b_zero_point dtype must match b." in err
+    rc, err = run(i7=np.array(1, np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "y_zero_point must be INT8 or UINT8." in err
+    rc, err = run(i8=np.zeros((2, 3), np.int8))
+    assert rc == olamd.INVALID_ARGUMENT and "output dtype must match y_zero_point." in err
+    rc, err = run(i1=np.array([0.1, 0.2], np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "'a_scale' must be a scalar." in err
+    rc, err = run(i4=np.array(1, np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "'b_scale' must be a FLOAT or FLOAT16 scalar" in err
+    rc, err = run(i6=f(0.0))
+    assert rc == olamd.INVALID_ARGUMENT and "y_scale must be non-zero." in err  # :264
+    rc, err = run(i8=np.zeros((3, 2), np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "preallocated output has invalid shape." in err
+    rc, err = run()
+    assert rc == olamd.NOT_INITIALIZED
+    # FLOAT16 scales are accepted (bits 0x2e66 ~ 0.1)
+    rc, err = run(i1=np.array(0x2E66, np.uint16), i4=np.array(0x2E66, np.uint16))
+    assert rc == olamd.INVALID_ARGUMENT  # uint16 is not a scale dtype
+    h = np.array(0.1, np.float16)
+    rc, _ = _call(olamd, "onnxl_amd_qlinear_matmul", d(a), d(h), d(u(1)), d(b), d(h), d(s(0)), d(h),
+                  d(u(2)), d(y), None)
+    assert rc == olamd.NOT_INITIALIZED
+
+
+def test_qlinear_rejects_inexact_int32_accumulation(olamd):
+    d = olamd.describe
+    K = 70000  # 70000 * 255 * 255 > 2^31
+    a = np.zeros((1, K), np.uint8)
+    b = np.zeros((K, 1), np.uint8)
+    rc, err = _call(olamd, "onnxl_amd_qlinear_matmul", d(a), d(np.array(1, np.float32)),
+                    d(np.array(0, np.uint8)), d(b), d(np.array(1, np.float32)),
+                    d(np.array(0, np.uint8)), d(np.array(1, np.float32)), d(np.array(0, np.uint8)),
+                    d(np.zeros((1, 1), np.uint8)), None)
+    assert rc == olamd.UNSUPPORTED and "int32 accumulation" in err
+
+
+def test_dequantize_validation(olamd):
+    d = olamd.describe
+    x = np.zeros((2, 3), np.uint8)
+    sc = np.array([1.0, 2.0, 3.0], np.float32)
+    y = np.zeros((2, 3), np.float32)
+    L = olamd.lib()
+
+    def run(x=x, s=sc, z=None, axis=1, y=y):
+        rc = L.onnxl_amd_dequantize_linear(d(x), d(s), d(z), axis, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    rc, err = run(s=np.array([1.0, 2.0], np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "x_scale element count must equal axis dimension." in err
+    rc, err = run(z=np.zeros(3, np.int8))
+    assert rc == olamd.INVALID_ARGUMENT and "x_zero_point data_type must match x." in err
+    rc, err = run(axis=2)
+    assert rc == olamd.INVALID_ARGUMENT and "axis out of range." in err
+    rc, err = run(axis=-1)  # the reference does not normalise negative axes
+    assert rc == olamd.INVALID_ARGUMENT and "axis out of range." in err
+    rc, err = run(y=np.zeros((2, 3), np.float16))
+    assert rc == olamd.INVALID_ARGUMENT and "output dtype must match x_scale." in err
+    rc, err = run(s=np.array(1.0, np.float32), y=np.zeros((2, 3), np.float16))
+    assert rc == olamd.INVALID_ARGUMENT and "output (no x_zero_point) dtype must match x_scale." in err
+    rc, err = run(s=np.array(1.0, np.float32), z=np.zeros(2, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "x_zero_point must be a scalar (per-tensor" in err
+    rc, err = run(s=np.array([1, 2, 3], np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "x_scale must be FLOAT or FLOAT16." in err
+    rc, err = run(x=np.zeros((2, 3), np.float32), s=np.array(1.0, np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "unsupported data type 1" in err  # :295-309
+    rc, err = run(s=np.ones((2, 2), np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "blocked x_scale dimension must divide" in err
+    rc, err = run(s=np.ones((1, 3), np.float32))  # dim 0 differs and is not the axis
+    assert rc == olamd.INVALID_ARGUMENT and "may only differ from x along the quantization axis" in err
+    rc, err = run(x=np.zeros((4, 6), np.uint8), s=np.ones((2, 3), np.float32), y=np.zeros((4, 6), np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "may only differ from x along the quantization axis" in err
+    rc, err = run(z=np.zeros(2, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "must have the same shape" in err
+    rc, err = run(y=np.zeros((3, 2), np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "preallocated output shape must match x shape." in err
+    rc, _ = run()
+    assert rc == olamd.NOT_INITIALIZED
+    # a dtype the reference decodes but this GPU path does not (FLOAT8E5M2)
+    rc = L.onnxl_amd_dequantize_linear(d(x, 19), d(np.array(1.0, np.float32)), d(None), 1, d(y), None)
+    assert rc == olamd.UNSUPPORTED
+
+
+def test_matmul_shape_rules(olamd, golden):
+    for c in golden["matmul_shapes"]:
+        assert list(olamd.matmul_shape(c["a_shape"], c["b_shape"])) == c["y_shape"]
+    with pytest.raises(olamd.InvalidArgument):
+        olamd.matmul_shape((2, 3), (4, 2))
+
+
+def test_not_initialized_before_device_work(olamd):
+    with pytest.raises(olamd.DeviceError):
+        olamd.matmul_integer(np.zeros((2, 2), np.uint8), np.zeros((2, 2), np.uint8),
+                             out=np.zeros((2, 2), np.int32))
