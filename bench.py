@@ -1,0 +1,288 @@
+"""Benchmark of the MI355X quantized-matmul kernels (one GPU).
+
+Default workload (the JSON line's `value`): configuration 2, QLinearMatMul
+prefill u8[2048,4096] x s8[4096,4096] -> u8[2048,4096], int8 MFMA.  A step is
+one QLinearMatMul over device-resident inputs; `value` is whole-job TOPS
+(2*M*N*K ops / time per step).  `roofline.achieved` uses the same algorithmic
+ops over the kernel time measured with HIP events on the launch stream.
+`cpu_baseline` times the serial CPU oracle (a restatement of the reference
+kernel, single core as the reference runs it) on a bounded row sample.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
+                  [--extra] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "int8/fp8 GEMM TOPS + GEMV GB/s (% of MI355X roofline), 1 GPU"
+PEAK = {"hbm_GBps": 8000.0, "int8_TOPs": 5000.0, "bf16_TFLOPs": 2500.0, "fp8_TFLOPs": 5000.0}
+
+
+def load_package():
+    if "onnx_light_amd" in sys.modules:
+        return sys.modules["onnx_light_amd"]
+    path = os.path.join(ROOT, "onnx-light_amd", "__init__.py")
+    spec = importlib.util.spec_from_file_location("onnx_light_amd", path,
+                                                  submodule_search_locations=[os.path.dirname(path)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["onnx_light_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _t(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+class Workload:
+    """One configuration: inputs on the GPU, a prepared call per replica."""
+    name = ""
+    unit = ""
+    dtype = ""
+    bound = ""
+    work = 0.0     # algorithmic ops/flops (mfma) or bytes (hbm) per launch
+    nbytes = 0     # algorithmic HBM bytes per launch
+
+    def step(self, i):
+        self.calls[i % len(self.calls)]()
+
+
+def make_c2(olamd, dev):
+    import importlib
+    syn = importlib.import_module("onnx_light_amd.synth")
+    x = syn.config_inputs(2)
+    w = Workload()
+    w.name = "C2 QLinearMatMul prefill u8[2048,4096] x s8[4096,4096] -> u8[2048,4096] (a_zp=128, b_zp=0, y_zp=128)"
+    w.key, w.unit, w.dtype, w.bound = "c2", "TOPS", "int8", "mfma"
+    M, K, N = 2048, 4096, 4096
+    w.work = 2.0 * M * N * K
+    w.nbytes = M * K + K * N + M * N
+    a, b = _t(x["a"], dev), _t(x["b"], dev)
+    import torch
+    y = torch.empty((M, N), dtype=torch.uint8, device=dev)
+    w.calls = [olamd.prepare("qlinear_matmul", a, x["a_scale"], x["a_zp"], b, x["b_scale"], x["b_zp"],
+                             x["y_scale"], x["y_zp"], y)]
+    w.inputs = x
+    return w
+
+
+def make_c3(olamd, dev, replicas):
+    import importlib
+    import torch
+    syn = importlib.import_module("onnx_light_amd.synth")
+    x = syn.config_inputs(3)
+    w = Workload()
+    w.name = ("C3 decode GEMV fp16[8,4096] x DequantizeLinear(int4[4096,11008], block 32 on K, fp16 "
+              "scales) -> fp16[8,11008]")
+    w.key, w.unit, w.dtype, w.bound = "c3", "GB/s", "fp16 x int4 (fp32 accumulate)", "hbm"
+    K, N = x["w_shape"]
+    w.nbytes = K * N // 2 + (K // 32) * N * 2 + 8 * K * 2 + 8 * N * 2
+    w.work = float(w.nbytes)
+    a = _t(x["a"], dev)
+    w.calls = []
+    for _ in range(replicas):
+        wq = _t(x["w"], dev)
+        sc = _t(x["scale"], dev)
+        y = torch.empty((8, N), dtype=torch.float16, device=dev)
+        w.calls.append(olamd.prepare("dequantize_linear_matmul", a, wq, sc, None, 0, 0, y,
+                                     descs={1: olamd.describe(wq, olamd.INT4, (K, N))}))
+    w.inputs = x
+    return w
+
+
+def make_c4(olamd, dev):
+    import importlib
+    import torch
+    syn = importlib.import_module("onnx_light_amd.synth")
+    x = syn.config_inputs(4)
+    w = Workload()
+    w.name = ("C4 fp8 per-axis prefill bf16[4096,4096] x Cast(bf16, DequantizeLinear(fp8e4m3fn"
+              "[4096,14336], fp32 per-column scale)) -> bf16[4096,14336]")
+    w.key, w.unit, w.dtype, w.bound = "c4", "TFLOPS", "bf16 (fp32 accumulate)", "mfma"
+    M, K, N = 4096, 4096, 14336
+    w.work = 2.0 * M * N * K
+    w.nbytes = M * K * 2 + K * N + N * 4 + M * N * 2
+    a = _t(x["a_bits"], dev).view(torch.bfloat16)
+    wq = _t(x["w"], dev)
+    sc = _t(x["scale"], dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    w.calls = [olamd.prepare("dequantize_linear_matmul", a, wq, sc, None, 1, olamd.BFLOAT16, y,
+                             descs={1: olamd.describe(wq, olamd.FLOAT8E4M3FN)})]
+    w.inputs = x
+    return w
+
+
+def make_c5(olamd, dev, replicas):
+    import importlib
+    import torch
+    syn = importlib.import_module("onnx_light_amd.synth")
+    x = syn.config_inputs(5)
+    w = Workload()
+    w.name = ("C5 batched MatMulInteger s8[32,512,64] x s8[32,64,512], per-row / per-column int8 "
+              "zero points -> i32[32,512,512]")
+    w.key, w.unit, w.dtype, w.bound = "c5", "GB/s", "int8 (int32 accumulate)", "hbm"
+    w.nbytes = 32 * 512 * 64 * 2 + 1024 + 32 * 512 * 512 * 4
+    w.work = float(w.nbytes)
+    a, b = _t(x["a"], dev), _t(x["b"], dev)
+    za, zb = _t(x["a_zp"], dev), _t(x["b_zp"], dev)
+    w.calls = []
+    for _ in range(replicas):
+        y = torch.empty((32, 512, 512), dtype=torch.int32, device=dev)
+        w.calls.append(olamd.prepare("matmul_integer", a, b, za, zb, y))
+    w.inputs = x
+    return w
+
+
+def time_workload(w, steps, warmup):
+    """Warm-up, then `steps` launches bracketed by synchronisations; per-launch
+    kernel time from events recorded around each launch on the launch stream."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        w.step(i)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(steps):
+        w.step(i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]  # ms
+    return wall / steps * 1e3, statistics.mean(per), statistics.median(per)
+
+
+def cpu_baseline_c2(w, budget_s=20.0):
+    """Serial oracle QLinearMatMul (the reference kernel restated, 1 core) on a
+    row sample of configuration 2; median of repeated timed runs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    x = w.inputs
+    rows = 16
+    orc.qlinear_matmul(x["a"], x["a_scale"], 128, x["b"], x["b_scale"], 0, x["y_scale"], 128,
+                       rows=(0, 2))  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    r0 = 0
+    while len(times) < 5 and time.perf_counter() - t_start < budget_s:
+        t = time.perf_counter()
+        orc.qlinear_matmul(x["a"], x["a_scale"], 128, x["b"], x["b_scale"], 0, x["y_scale"], 128,
+                           rows=(r0, r0 + rows))
+        times.append(time.perf_counter() - t)
+        r0 += rows
+    sec_per_row = statistics.median(times) / rows
+    ops = 2.0 * 2048 * 4096 * 4096
+    full_s = sec_per_row * 2048
+    return {"value": ops / full_s / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} timed runs of {rows} rows (of 2048) through the serial oracle "
+                      f"QLinearMatMul (oracle/oracle.c, int64 accumulate, column-strided B), median, "
+                      f"extrapolated linearly to the full 2048 rows ({full_s:.1f} s per job)",
+            "nproc": os.cpu_count()}
+
+
+def roofline(w, kernel_ms, traffic):
+    if w.bound == "mfma":
+        peak = PEAK["int8_TOPs"] if w.key == "c2" else PEAK["bf16_TFLOPs"]
+        achieved = w.work / (kernel_ms * 1e-3) / 1e12
+        unit = "TOP/s" if w.key == "c2" else "TFLOP/s"
+    else:
+        peak = PEAK["hbm_GBps"]
+        achieved = w.nbytes / (kernel_ms * 1e-3) / 1e9
+        unit = "GB/s"
+    out = {"bound": w.bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "traffic": traffic}
+    if w.key == "c4":
+        out["frac_of_fp8_peak"] = round(achieved / PEAK["fp8_TFLOPs"], 4)
+    return out
+
+
+def load_traffic(key):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(key, {}).get("hbm_bytes_per_launch")
+
+
+def value_of(w, ms):
+    if w.bound == "mfma":
+        return w.work / (ms * 1e-3) / 1e12
+    return w.nbytes / (ms * 1e-3) / 1e9
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--extra", action="store_true", help="also time the other configurations")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--replicas", type=int, default=0,
+                    help="buffer replicas for HBM-bound configs (0 = enough to exceed 512 MB)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the quantized-matmul kernels "
+                                   "are single-device (see DESIGN.md for how they would shard)",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+    olamd = load_package()
+    olamd.init(0)
+    dev = torch.device("cuda:0")
+
+    def build(key):
+        if key == "c2":
+            return make_c2(olamd, dev)
+        if key == "c3":
+            return make_c3(olamd, dev, args.replicas or 24)
+        if key == "c4":
+            return make_c4(olamd, dev)
+        return make_c5(olamd, dev, args.replicas or 16)
+
+    w = build(args.workload)
+    ms, kern_mean, kern_med = time_workload(w, args.steps, args.warmup)
+    line = {"metric": METRIC, "value": round(value_of(w, ms), 3), "unit": w.unit, "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w.dtype,
+            "data": "synthetic (SplitMix64 inputs of the reference's generator, device-resident)",
+            "config": {"workload": w.name, "replicas": len(w.calls)},
+            "kernel_ms_mean": round(kern_mean, 5), "kernel_ms_median": round(kern_med, 5),
+            "roofline": roofline(w, kern_mean, load_traffic(w.key))}
+    if args.extra:
+        extra = {}
+        for key in ("c2", "c3", "c4", "c5"):
+            if key == args.workload:
+                continue
+            try:
+                ew = build(key)
+                e_ms, e_mean, _ = time_workload(ew, max(20, args.steps // 4), max(3, args.warmup // 4))
+                extra[key] = {"workload": ew.name, "value": round(value_of(ew, e_ms), 3), "unit": ew.unit,
+                              "ms_per_step": round(e_ms, 5), "kernel_ms_mean": round(e_mean, 5),
+                              "roofline": roofline(ew, e_mean, load_traffic(key))}
+                del ew
+                torch.cuda.empty_cache()
+            except olamd.Unsupported as e:
+                extra[key] = {"unsupported": str(e)}
+        line["extra"] = extra
+    if not args.no_cpu_baseline and args.workload == "c2":
+        line["cpu_baseline"] = cpu_baseline_c2(w)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

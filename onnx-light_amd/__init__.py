@@ -335,3 +335,34 @@ class MatMul:
 # (core/runtime/kernels/kernel_dispatch_table.h:148-164).
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
            "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul}
+
+
+class Prepared:
+    """A C-ABI call with its descriptors built once (what a session adapter
+    keeps per node): calling it re-runs the kernel on the same buffers."""
+
+    def __init__(self, fn_name: str, descs: list, extra: tuple, stream):
+        self._fn = getattr(lib(), fn_name)
+        self._descs = descs
+        self._args = [ctypes.byref(d) if isinstance(d, Tensor) else d for d in descs]
+        self._extra = extra
+        self._stream = stream
+
+    def __call__(self) -> None:
+        _check(self._fn(*self._args, self._stream))
+
+
+def prepare(fn_name: str, *tensors, descs=None, **kw):
+    """Prepared call of `onnxl_amd_<fn_name>`: tensors are described in order
+    (None = absent); `descs` overrides individual descriptors by position and
+    scalar (non-tensor) arguments are passed through unchanged."""
+    out = []
+    for i, t in enumerate(tensors):
+        if descs and i in descs:
+            out.append(descs[i])
+        elif isinstance(t, (int, float)) and not isinstance(t, bool):
+            out.append(t)
+        else:
+            out.append(describe(t))
+    return Prepared("onnxl_amd_" + fn_name, out, (), _stream_of(*[t for t in tensors
+                                                                  if not isinstance(t, (int, float))]))
