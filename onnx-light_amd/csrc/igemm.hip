@@ -26,6 +26,8 @@
 //  - Workgroup ids are remapped so each XCD (8 on MI355X, ids dealt
 //    round-robin) owns a contiguous run of tiles, grouped 8 tile-rows high,
 //    so tiles sharing A rows / B columns share that XCD's L2.
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace onnxl_amd {
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmKernel(const IGemmParams p) 
 //  - The UINT8 flip is applied to the fragments in registers; padding (rows
 //    >= M, columns >= N) only feeds outputs that are never stored, and there
 //    is no K padding on this path.
-constexpr int kStages = 3;
+constexpr int kMaxStages = 6;
 constexpr int kAStage = kBM * kBK;  // 16 KB
 constexpr int kBStage = kBK * kBN;  //  8 KB
 
@@ -349,15 +351,31 @@ typedef int v2iL __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef __attribute__((address_space(3))) v2iL *lds_v2i_t;
 
-template <int EPI, bool NEED_RA, bool NEED_CB>
+// Waits until the oldest outstanding K step (six direct loads per thread) has
+// landed, retires this wave's LDS reads, then joins the workgroup barrier.
+// A plain __syncthreads() would drain every outstanding load (vmcnt(0)) and
+// serialise the ring; the "memory" clobber keeps the compiler from moving LDS
+// accesses across.
+template <int S> __device__ __forceinline__ void RingBarrier() {
+  static_assert(S >= 3 && S <= kMaxStages, "ring depth");
+  if constexpr (S == 3) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (S == 4) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (S == 5) asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (S == 6) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int EPI, bool NEED_RA, bool NEED_CB, int S>
 __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams p) {
   // One object per ring stage: the compiler's LDS-DMA wait tracking can then
   // tell a read of stage s from a direct load into another stage (with a
   // single array it waits for every outstanding load before each read).
-  __shared__ __align__(16) int8_t lds_a0[kAStage], lds_a1[kAStage], lds_a2[kAStage];
-  __shared__ __align__(16) int8_t lds_b0[kBStage], lds_b1[kBStage], lds_b2[kBStage];
-  int8_t *const stage_a[kStages] = {lds_a0, lds_a1, lds_a2};
-  int8_t *const stage_b[kStages] = {lds_b0, lds_b1, lds_b2};
+  // Arrays past the ring depth are never referenced and not allocated.
+  __shared__ __align__(16) int8_t lds_a0[kAStage], lds_a1[kAStage], lds_a2[kAStage],
+      lds_a3[kAStage], lds_a4[kAStage], lds_a5[kAStage];
+  __shared__ __align__(16) int8_t lds_b0[kBStage], lds_b1[kBStage], lds_b2[kBStage],
+      lds_b3[kBStage], lds_b4[kBStage], lds_b5[kBStage];
+  int8_t *const stage_a[kMaxStages] = {lds_a0, lds_a1, lds_a2, lds_a3, lds_a4, lds_a5};
+  int8_t *const stage_b[kMaxStages] = {lds_b0, lds_b1, lds_b2, lds_b3, lds_b4, lds_b5};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -460,13 +478,8 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
 
   // One K step on ring stage `stage` (a compile-time index after unrolling).
   auto step = [&](int it, int stage) {
-    // This step's six direct loads are the oldest outstanding ones (the next
-    // step's six may stay in flight); lgkmcnt(0) retires this wave's reads of
-    // the stage that the issue below overwrites.  A plain __syncthreads()
-    // would drain every outstanding load (vmcnt(0)) and serialise the ring;
-    // the "memory" clobber keeps the compiler from moving LDS accesses across.
-    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(it + 2, (stage + 2) % kStages);  // the stage every wave finished reading
+    RingBarrier<S>();
+    issue(it + S - 1, (stage + S - 1) % S);  // the stage every wave finished reading
     __builtin_amdgcn_sched_barrier(0);     // keep the loads at the top of the step
     const int8_t *sa = stage_a[stage];
     const int8_t *sb = stage_b[stage];
@@ -495,16 +508,16 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
     }
   };
 
-  issue(0, 0);
-  issue(1, 1);
+#pragma unroll
+  for (int s0 = 0; s0 < S - 1; ++s0) issue(s0, s0);
   int it = 0;
-  for (; it + 3 <= nk; it += 3) {
-    step(it, 0);
-    step(it + 1, 1);
-    step(it + 2, 2);
+  for (; it + S <= nk; it += S) {
+#pragma unroll
+    for (int s0 = 0; s0 < S; ++s0) step(it + s0, s0);
   }
-  if (it < nk) step(it, 0);
-  if (it + 1 < nk) step(it + 1, 1);
+#pragma unroll
+  for (int s0 = 0; s0 < S - 1; ++s0)
+    if (it + s0 < nk) step(it + s0, s0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): drain the look-ahead loads
 
   const unsigned Ku = (unsigned)K;
@@ -546,9 +559,16 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
   }
 }
 
+int g_ring_stages = 4;  // ring depth of the fast path (ONNXL_AMD_IGEMM_STAGES overrides)
+
 template <int EPI, bool RA, bool CB>
 void LaunchLds(const IGemmParams &p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((IGemmLdsKernel<EPI, RA, CB>), grid, dim3(kThreads), 0, s, p);
+  switch (g_ring_stages) {
+  case 3: hipLaunchKernelGGL((IGemmLdsKernel<EPI, RA, CB, 3>), grid, dim3(kThreads), 0, s, p); break;
+  case 5: hipLaunchKernelGGL((IGemmLdsKernel<EPI, RA, CB, 5>), grid, dim3(kThreads), 0, s, p); break;
+  case 6: hipLaunchKernelGGL((IGemmLdsKernel<EPI, RA, CB, 6>), grid, dim3(kThreads), 0, s, p); break;
+  default: hipLaunchKernelGGL((IGemmLdsKernel<EPI, RA, CB, 4>), grid, dim3(kThreads), 0, s, p); break;
+  }
 }
 
 template <int EPI, bool RA, bool CB, int MODE>
@@ -578,6 +598,11 @@ void LaunchEpi(const IGemmParams &p, int mode, dim3 grid, hipStream_t s) {
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return;
+  static const int stages_env = [] {
+    const char *e = std::getenv("ONNXL_AMD_IGEMM_STAGES");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (stages_env >= 3 && stages_env <= kMaxStages) g_ring_stages = stages_env;
   const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
   // Buffer paths: 16-byte A rows, 8-byte B rows (every batch base and row
   // start aligned) and per-matrix byte counts, plus the look-ahead of two K
