@@ -1,16 +1,182 @@
-// Dequantize-fused MatMul (placeholder until the GEMV / GEMM kernels land).
+// Dequantize-fused MatMul dispatch and the FLOAT16 / BFLOAT16 MatMul.
+//
+//  - int4 / uint4 weights with FLOAT16 scales, M <= 16 (decode): the
+//    bandwidth-bound GEMV (gemv_q4.hip).
+//  - float8e4m3fn weights, FLOAT scales per column or per tensor, Cast to
+//    BFLOAT16, bf16 activations (prefill): the pipelined MFMA core with the
+//    weight decoded and scaled as it is read from LDS (mfma_gemm.hpp, kBf16F8).
+//  - anything else the C ABI accepts: the weight is dequantised into scratch
+//    with the chain's exact rounding, then multiplied by the 16-bit MatMul.
+#include <algorithm>
+
 #include "common.hpp"
+#include "device_codecs.hpp"
 #include "kernels.hpp"
+#include "mfma_gemm.hpp"
 
 namespace onnxl_amd {
 
-size_t DqMatMulScratchBytes(const DqMatMulParams &) { return 0; }
-size_t DqMatMulCounters(const DqMatMulParams &) { return 0; }
-bool LaunchDqMatMul(const DqMatMulParams &, void *, size_t, unsigned *, size_t, hipStream_t) {
-  return false;
+bool GemvQ4Eligible(const DqMatMulParams &p);
+size_t GemvQ4ScratchBytes(const DqMatMulParams &p);
+size_t GemvQ4Counters(const DqMatMulParams &p);
+void LaunchGemvQ4(const DqMatMulParams &p, void *scratch, unsigned *counters, hipStream_t stream);
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Generic 16-bit MatMul for shapes the MFMA core does not take: one thread per
+// output, fp32 accumulation in k order.
+template <bool BF16>
+__global__ __launch_bounds__(256) void HMatMulSimpleKernel(const HMatMulParams p) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  if (n >= p.N) return;
+  int64_t ao, bo;
+  BatchOffsets(p.bm, b, ao, bo);
+  const uint16_t *a = p.A + ao + m * p.K;
+  const uint16_t *w = p.B + bo + n;
+  float acc = 0.f;
+  for (int64_t k = 0; k < p.K; ++k) {
+    const float x = BF16 ? Bf16ToF32(a[k]) : F16ToF32(a[k]);
+    const float y = BF16 ? Bf16ToF32(w[k * p.N]) : F16ToF32(w[k * p.N]);
+    acc += x * y;
+  }
+  p.Y[(b * p.M + m) * p.N + n] = BF16 ? F32ToBf16(acc) : F32ToF16(acc);
 }
-void LaunchHMatMul(const HMatMulParams &, hipStream_t) {
-  throw Unsupported("MatMul FLOAT16/BFLOAT16: kernel not built yet");
+
+mg::GemmArgs HArgs(const HMatMulParams &p) {
+  mg::GemmArgs g{};
+  g.A = p.A;
+  g.B = p.B;
+  g.Y = p.Y;
+  g.M = p.M;
+  g.N = p.N;
+  g.K = p.K;
+  g.batch = p.batch;
+  g.bm = p.bm;
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// Weight dequantisation into a 16-bit [K, N] scratch matrix with the unfused
+// chain's rounding: DequantizeLinear computes (x - zp) * scale in fp32 and
+// stores the scale's dtype (FLOAT16: round to nearest even); an optional Cast
+// rounds FLOAT to BFLOAT16 / FLOAT16
+// (kq/kernel_dequantizelinear.cc:57-63,259-285; kernel_cast.cc:360-370).
+__device__ __forceinline__ float DecodeWeight(const uint8_t *w, int dt, int64_t i) {
+  switch (dt) {
+  case kInt4: return (float)Int4ToInt((w[i >> 1] >> (4 * (i & 1))) & 0xfu);
+  case kUint4: return (float)((w[i >> 1] >> (4 * (i & 1))) & 0xfu);
+  case kInt8: return (float)(int8_t)w[i];
+  case kUint8: return (float)w[i];
+  default: return Fp8E4M3ToF32(w[i]);
+  }
+}
+
+__global__ __launch_bounds__(256) void DequantWeightKernel(const DqMatMulParams p, uint16_t *out) {
+  const int64_t total = p.K * p.N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t k = i / p.N, n = i % p.N;
+    int64_t si = 0;
+    if (p.mode == 1) si = n;
+    else if (p.mode == 2) si = (k / p.block) * p.N + n;
+    const float s = p.scale_f16 ? F16ToF32(static_cast<const uint16_t *>(p.scale)[si])
+                                : static_cast<const float *>(p.scale)[si];
+    const float z = p.zp ? DecodeWeight(p.zp, p.w_dtype, si) : 0.f;
+    const float v = (DecodeWeight(p.W, p.w_dtype, i) - z) * s;
+    uint16_t bits;
+    if (p.deq_round_f16) {
+      bits = F32ToF16(v);  // DequantizeLinear output FLOAT16 (no Cast follows)
+    } else if (p.cast_round == 16) {
+      bits = F32ToBf16(v);
+    } else {
+      bits = F32ToF16(v);
+    }
+    out[i] = bits;
+  }
+}
+
+bool Fp8Eligible(const DqMatMulParams &p) {
+  return p.w_dtype == kFloat8E4M3FN && p.a_bf16 && p.cast_round == 16 && !p.scale_f16 &&
+         (p.mode == 0 || p.mode == 1) && p.zp == nullptr;
+}
+
+mg::GemmArgs Fp8Args(const DqMatMulParams &p) {
+  mg::GemmArgs g{};
+  g.A = p.A;
+  g.B = p.W;
+  g.Y = p.Y;
+  g.M = p.M;
+  g.N = p.N;
+  g.K = p.K;
+  g.batch = 1;
+  g.scale = p.scale;
+  g.scale_f16 = 0;
+  g.scale_per_col = p.mode == 1;
+  return g;
+}
+
+}  // namespace
+
+void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0 || p.batch == 0) return;
+  const mg::GemmArgs g = HArgs(p);
+  if (mg::Eligible<mg::kH16>(g)) {
+    if (p.bf16) mg::Launch<mg::kH16, mg::kOutBf16, false, false, false>(g, stream);
+    else mg::Launch<mg::kH16, mg::kOutF16, false, false, false>(g, stream);
+    return;
+  }
+  const dim3 grid((unsigned)((p.N + 255) / 256), (unsigned)p.M, (unsigned)p.batch);
+  if (p.bf16) hipLaunchKernelGGL(HMatMulSimpleKernel<true>, grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL(HMatMulSimpleKernel<false>, grid, dim3(256), 0, stream, p);
+}
+
+size_t DqMatMulScratchBytes(const DqMatMulParams &p) {
+  if (GemvQ4Eligible(p)) return GemvQ4ScratchBytes(p);
+  if (Fp8Eligible(p) && mg::Eligible<mg::kBf16F8>(Fp8Args(p))) return 0;
+  return (size_t)(p.K * p.N) * sizeof(uint16_t);
+}
+
+size_t DqMatMulCounters(const DqMatMulParams &p) {
+  return GemvQ4Eligible(p) ? GemvQ4Counters(p) : 0;
+}
+
+bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes, unsigned *counters,
+                    size_t n_counters, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0) return true;
+  if (GemvQ4Eligible(p)) {
+    if (scratch_bytes < GemvQ4ScratchBytes(p) || n_counters < GemvQ4Counters(p)) return false;
+    LaunchGemvQ4(p, scratch, counters, stream);
+    return true;
+  }
+  if (Fp8Eligible(p)) {
+    const mg::GemmArgs g = Fp8Args(p);
+    if (mg::Eligible<mg::kBf16F8>(g)) {
+      mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false>(g, stream);
+      return true;
+    }
+  }
+  // general path: dequantise into scratch, then the 16-bit MatMul (K == 0
+  // leaves nothing to dequantise and the MatMul writes zeros)
+  if (scratch_bytes < (size_t)(p.K * p.N) * sizeof(uint16_t)) return false;
+  uint16_t *w16 = static_cast<uint16_t *>(scratch);
+  const int64_t total = p.K * p.N;
+  if (total > 0) {
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(DequantWeightKernel, dim3(blocks), dim3(256), 0, stream, p, w16);
+  }
+  HMatMulParams h{};
+  h.A = static_cast<const uint16_t *>(p.A);
+  h.B = w16;
+  h.Y = static_cast<uint16_t *>(p.Y);
+  h.M = p.M;
+  h.N = p.N;
+  h.K = p.K;
+  h.batch = 1;
+  h.bf16 = p.a_bf16;
+  LaunchHMatMul(h, stream);
+  return true;
 }
 
 }  // namespace onnxl_amd

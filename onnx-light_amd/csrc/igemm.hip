@@ -29,6 +29,7 @@
 #include <cstdlib>
 
 #include "kernels.hpp"
+#include "igemm_fast.hpp"
 
 namespace onnxl_amd {
 namespace {
@@ -598,6 +599,12 @@ void LaunchEpi(const IGemmParams &p, int mode, dim3 grid, hipStream_t s) {
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return;
+  // K % 128 == 0: the pipelined MFMA core (mfma_gemm.hpp).
+  if (mg::Eligible<mg::kI8>(ToGemmArgs(p))) {
+    if (p.epilogue == kEpiInt32) LaunchIGemmFastI32(p, stream);
+    else LaunchIGemmFastQ8(p, stream);
+    return;
+  }
   static const int stages_env = [] {
     const char *e = std::getenv("ONNXL_AMD_IGEMM_STAGES");
     return e ? std::atoi(e) : 0;

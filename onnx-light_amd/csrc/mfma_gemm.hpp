@@ -1,0 +1,560 @@
+// Pipelined MFMA GEMM core for gfx950, shared by the int8 GEMM
+// (MatMulInteger / QLinearMatMul), the fp8-weight bf16 GEMM (fused
+// DequantizeLinear -> Cast -> MatMul) and the fp16 / bf16 MatMul.
+//
+// Y[b] = A[b] (M x K, row-major) * B[b] (K x N, row-major).
+//
+// Workgroup: 256 threads = 4 waves (2 x 2), one wave per SIMD, output tile
+// 256 x 128; each wave owns 128 x 64 = 4 x 2 blocks of 32 x 32 MFMA outputs.
+// A K step covers 128 bytes of every A row (128 int8 or 64 16-bit values).
+//
+// Memory path.
+//  - Both operands go global -> LDS with direct buffer loads (16 bytes per
+//    lane, 1 KB per wave instruction, no registers held) into a 3-stage ring:
+//    while step t is multiplied, steps t+1 and t+2 are in flight.
+//  - A stage [256 rows][128 B] is stored as 1 KB blocks of 8 rows,
+//    [row/8][16-byte chunk c ^ ((row/8) & 1)][row%8]: one direct load moves 8
+//    whole 128-byte rows (full cache lines), and the 16 lanes of a fragment
+//    read (ds_read_b128, 16 consecutive rows, one chunk) cover 256 bytes
+//    spread over all banks thanks to the chunk XOR.
+//  - B stage [k rows][128 columns] is stored row-major with its 16-byte chunks
+//    XOR-swizzled by the row index.  The MFMA wants consecutive k of one column
+//    per lane; the transposing LDS reads (ds_read_b64_tr_b8 / _b16) deliver
+//    exactly that from the row-major tile.  Within a 16-lane group, result
+//    lane i element t is, for 8-bit elements, byte i%8 of the 8 bytes that
+//    lane 2t + i/8 addressed; for 16-bit elements, element i%4 of the 4 that
+//    lane 4t + i/4 addressed.  So lanes address (row k0 + s/2, columns
+//    c0 + 8(s%2) ..) resp. (row k0 + s/4, columns c0 + 4(s%4) ..) and lane i
+//    receives column c0 + i at k0, k0+1, ...
+//
+// Schedule (per K step of 4 sub-steps): the fragments of sub-step kk+1 are
+// read from LDS while the MFMAs of sub-step kk run (two register sets).  The
+// single barrier per step sits inside the last sub-step, after half of its
+// MFMAs are issued, so the matrix pipe stays busy across it.  The barrier
+// waits only for the oldest ring stage (s_waitcnt vmcnt(L) with L the direct
+// loads per step), never for all loads.
+//
+// Epilogue: each wave converts its accumulators, stages 32 rows at a time in
+// LDS and writes them back with 16-byte row-contiguous stores.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace onnxl_amd {
+namespace mg {
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef __attribute__((address_space(3))) v2i *lds_v2i_t;
+typedef __attribute__((address_space(3))) v4s *lds_v4s_t;
+
+constexpr int kBM = 256, kBN = 128, kStepBytes = 128, kStages = 3, kThreads = 256;
+constexpr int kGroupM = 8, kXcds = 8;
+constexpr int kAStage = kBM * kStepBytes;  // 32 KB
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr unsigned kOob = 0x80000000u;
+constexpr unsigned kFlip = 0x80808080u;
+
+// Operand kinds.
+//  kI8:     int8 / uint8 x int8 / uint8 -> int32 (v_mfma_i32_32x32x32_i8)
+//  kBf16F8: bf16 A x float8e4m3fn B with a per-column (or single) fp32 scale;
+//           B is decoded to bf16 as round_bf16(decode(b) * scale[n]), the
+//           rounding of the DequantizeLinear(FLOAT) -> Cast(BFLOAT16) chain.
+//  kH16:    fp16 x fp16 or bf16 x bf16 -> fp32 accumulate.
+enum Kind : int { kI8 = 0, kBf16F8 = 1, kH16 = 2 };
+
+// Output conversions.
+enum Out : int { kOutI32 = 0, kOutQ8 = 1, kOutF16 = 2, kOutBf16 = 3 };
+
+template <int KIND> struct Traits;
+template <> struct Traits<kI8> {
+  static constexpr int kKStep = 128;     // k values per step
+  static constexpr int kBRows = 128;     // B rows per step
+  static constexpr int kBPitch = 128;    // bytes per B row in LDS
+  using Acc = v16i;
+};
+template <> struct Traits<kBf16F8> {
+  static constexpr int kKStep = 64;
+  static constexpr int kBRows = 64;
+  static constexpr int kBPitch = 128;
+  using Acc = v16f;
+};
+template <> struct Traits<kH16> {
+  static constexpr int kKStep = 64;
+  static constexpr int kBRows = 64;
+  static constexpr int kBPitch = 256;
+  using Acc = v16f;
+};
+template <int KIND> constexpr int BStageBytes() { return Traits<KIND>::kBRows * Traits<KIND>::kBPitch; }
+// direct loads per wave per K step: A 32 KB + B stage, 1 KB per instruction
+template <int KIND> constexpr int LoadsPerWave() { return (kAStage + BStageBytes<KIND>()) / 1024 / 4; }
+template <int KIND> constexpr int BLoadsPerWave() { return BStageBytes<KIND>() / 1024 / 4; }
+
+__device__ __forceinline__ int64_t MinI64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+// float pair -> packed bf16 pair (round to nearest even), lo in bits 0-15.
+__device__ __forceinline__ unsigned PackBf16(float lo, float hi) {
+  unsigned r;
+  asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+  return r;
+}
+
+// Waits for all but the newest `L` direct loads (the oldest in-flight ring
+// stage has then landed), retires this wave's LDS reads and joins the
+// workgroup barrier.  A __syncthreads() would wait for every load.
+template <int L> __device__ __forceinline__ void RingBarrier() {
+  static_assert(L >= 0 && L < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(L) : "memory");
+}
+
+// Common launch-time description of one GEMM (all kinds).
+struct GemmArgs {
+  const void *A;
+  const void *B;
+  void *Y;
+  int64_t M, N, K;
+  int64_t batch;
+  BatchMap bm;
+  // kI8
+  int a_u8, b_u8;
+  const uint8_t *a_zp;
+  const uint8_t *b_zp;
+  int32_t alpha_scalar, beta_scalar;
+  float cs, zy, qmin, qmax;
+  int y_signed;
+  // kBf16F8: dequantization scales (FLOAT or FLOAT16), one per column
+  // (scale_per_col) or a single value
+  const void *scale;
+  int scale_f16;
+  int scale_per_col;
+};
+
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8>
+__global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) {
+  constexpr bool RA = ZP, CB = ZP;
+  using T = Traits<KIND>;
+  using Acc = typename T::Acc;
+  constexpr int kBStage = BStageBytes<KIND>();
+  constexpr int L = LoadsPerWave<KIND>();
+  constexpr int LB = BLoadsPerWave<KIND>();
+  constexpr int kOsz = OUT == kOutI32 ? 4 : (OUT == kOutQ8 ? 1 : 2);
+  static_assert(LB >= 1 && LB <= 4, "B direct loads per wave");
+  // One object per ring stage: the compiler's LDS-DMA wait tracking can then
+  // tell a read of one stage from a direct load into another.
+  __shared__ __align__(16) char sa0[kAStage], sa1[kAStage], sa2[kAStage];
+  __shared__ __align__(16) char sb0[kBStage], sb1[kBStage], sb2[kBStage];
+  __shared__ int32_t zsum[ZP ? 2 * (kBM + kBN) : 1];
+  // stage index -> array (indices are compile-time constants after unrolling)
+  auto SA = [&](int s) -> char * { return s == 0 ? sa0 : (s == 1 ? sa1 : sa2); };
+  auto SB = [&](int s) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lg = lane >> 5;
+  const int64_t M = p.M, N = p.N, K = p.K;
+
+  // ---- tile selection: each XCD owns a contiguous run of tiles, grouped
+  // kGroupM tile-rows high, so tiles sharing A rows / B columns share an L2 ----
+  const int64_t nbm = (M + kBM - 1) / kBM, nbn = (N + kBN - 1) / kBN;
+  const int64_t tiles = nbm * nbn;
+  const int64_t total = tiles * p.batch;
+  const int64_t pid = blockIdx.x;
+  const int64_t xcd = pid % kXcds, per = total / kXcds, extra = total % kXcds;
+  const int64_t t_all = xcd * per + MinI64(xcd, extra) + pid / kXcds;
+  const int64_t bt = t_all / tiles, tt = t_all % tiles;
+  const int64_t group = tt / (kGroupM * nbn);
+  const int64_t first_m = group * kGroupM;
+  const int64_t gsize = MinI64(nbm - first_m, kGroupM);
+  const int64_t tm = first_m + (tt % (kGroupM * nbn)) % gsize;
+  const int64_t tn = (tt % (kGroupM * nbn)) / gsize;
+  const int64_t row0 = tm * kBM, col0 = tn * kBN;
+
+  constexpr int kAsz = KIND == kI8 ? 1 : 2;
+  constexpr int kBsz = KIND == kH16 ? 2 : 1;
+  int64_t a_off, b_off;
+  BatchOffsets(p.bm, bt, a_off, b_off);
+  const char *Ab = static_cast<const char *>(p.A) + a_off * kAsz;
+  const char *Bb = static_cast<const char *>(p.B) + b_off * kBsz;
+  const int64_t KA = K * kAsz;   // A row pitch in bytes
+  const int64_t NB = N * kBsz;   // B row pitch in bytes
+  const __amdgpu_buffer_rsrc_t rsA =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsB =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(K * NB), kRsrcWord3);
+  const int nk = (int)(K / T::kKStep);
+
+  // ---- direct-load offsets (K step 0) ----
+  unsigned a_g[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int64_t row = row0 + 8 * (8 * wave + q) + (lane & 7);  // 8-row block 8 * wave + q
+    a_g[q] = row < M ? (unsigned)(row * KA + 16 * ((lane >> 3) ^ (q & 1))) : kOob;
+  }
+  unsigned b_g[4];  // LB <= 4 (a fixed bound: a template-dependent size here
+                    // makes the host compiler drop the kernel stub)
+#pragma unroll
+  for (int q = 0; q < LB; ++q) {
+    const int i = wave * LB + q;  // 1 KB piece of the B stage
+    if constexpr (KIND == kH16) {
+      const int krow = 4 * i + (lane >> 4);
+      const int64_t cb = 2 * col0 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3)));
+      b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
+    } else {
+      const int krow = 8 * i + (lane >> 3);
+      const int64_t cb = col0 + 16 * ((lane & 7) ^ (lane >> 3));
+      b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
+    }
+  }
+  // ---- LDS fragment offsets (sub-step 0; sub-step kk adds kk * const) ----
+  int a_rd[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm * 128 + i * 32 + lr;
+    a_rd[i] = (r >> 3) * 1024 + 128 * (lg ^ ((r >> 3) & 1)) + (r & 7) * 16;
+  }
+  const int s16 = lane & 15, g16 = lane >> 4;
+  int b_rd[2][2];  // [j][h]
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (KIND == kI8) {
+        const int krow = 16 * (g16 >> 1) + 8 * h + (s16 >> 1);
+        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
+        b_rd[j][h] = krow * 128 + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+      } else if constexpr (KIND == kBf16F8) {
+        const int krow = 8 * (g16 >> 1) + (s16 >> 1);
+        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
+        b_rd[j][h] = krow * 128 + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+      } else {
+        const int krow = 8 * (g16 >> 1) + 4 * h + (s16 >> 2);
+        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+        b_rd[j][h] = krow * 256 + 16 * ((col >> 3) ^ (2 * (krow & 3))) + ((2 * col) & 15);
+      }
+    }
+  // B rows per sub-step: 32 (int8) or 16 (16-bit k values)
+  constexpr int kSubRows = KIND == kI8 ? 32 : 16;
+
+  // per-column dequantization scales (kBf16F8)
+  float bscale[2] = {1.f, 1.f};
+  if constexpr (KIND == kBf16F8) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = col0 + wn * 64 + j * 32 + lr;
+      const int64_t si = p.scale_per_col ? (col < N ? col : 0) : 0;
+      bscale[j] = p.scale_f16 ? (float)static_cast<const _Float16 *>(p.scale)[si]
+                              : static_cast<const float *>(p.scale)[si];
+    }
+  }
+  constexpr int aflip = (KIND == kI8 && AU8) ? (int)kFlip : 0;
+  constexpr int bflip = (KIND == kI8 && BU8) ? (int)kFlip : 0;
+
+  auto issue = [&](int step, int stage) {
+    const bool live = step < nk;
+    const unsigned ka = (unsigned)step * kStepBytes;
+    const unsigned kb = (unsigned)((int64_t)step * T::kBRows * NB);
+    char *sa = SA(stage);
+    char *sb = SB(stage);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsA, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16,
+          live ? a_g[q] + ka : kOob, 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < LB; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16,
+                                               live ? b_g[q] + kb : kOob, 0, 0, 0);
+  };
+
+  // ---- fragments: raw LDS reads (two sets) and MFMA-ready operands ----
+  v4i ra[2][4];
+  v4i rb[2][2];  // kI8: 2 x tr8; kBf16F8: 1 x tr8 (.xy); kH16: 2 x tr16
+  auto read = [&](int buf, const char *sa, const char *sb, int kk) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const char *base = sb + kk * kSubRows * T::kBPitch;
+      if constexpr (KIND == kI8) {
+        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][0]));
+        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][1]));
+        rb[buf][j] = v4i{lo.x, lo.y, hi.x, hi.y};
+      } else if constexpr (KIND == kBf16F8) {
+        const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][0]));
+        rb[buf][j] = v4i{v.x, v.y, 0, 0};
+      } else {
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j][0]));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j][1]));
+        rb[buf][j] = v4i{__builtin_bit_cast(v2i, lo).x, __builtin_bit_cast(v2i, lo).y,
+                         __builtin_bit_cast(v2i, hi).x, __builtin_bit_cast(v2i, hi).y};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ra[buf][i] = *reinterpret_cast<const v4i *>(sa + a_rd[i] + kk * 256);
+  };
+
+  Acc acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = Acc{0};
+  int rsum[4] = {0, 0, 0, 0};  // kI8: partial row sums of a' (this lane's k group)
+  int csum[2] = {0, 0};        // kI8: partial column sums of b'
+
+  v4i bop[2];  // MFMA-ready B operands of the current sub-step
+  auto build_b = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (KIND == kI8) {
+        bop[j] = rb[buf][j] ^ bflip;
+        if (CB) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) csum[j] = __builtin_amdgcn_sdot4(bop[j][e], 0x01010101, csum[j], false);
+        }
+      } else if constexpr (KIND == kBf16F8) {
+        const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].x, false);
+        const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].x, true);
+        const v2f f2 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].y, false);
+        const v2f f3 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].y, true);
+        const float s = bscale[j];
+        bop[j] = v4i{(int)PackBf16(f0.x * s, f0.y * s), (int)PackBf16(f1.x * s, f1.y * s),
+                     (int)PackBf16(f2.x * s, f2.y * s), (int)PackBf16(f3.x * s, f3.y * s)};
+      } else {
+        bop[j] = rb[buf][j];
+      }
+    }
+  };
+  auto mma = [&](int buf, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      if constexpr (KIND == kI8) {
+        const v4i av = ra[buf][i] ^ aflip;
+        if (RA) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rsum[i] = __builtin_amdgcn_sdot4(av[e], 0x01010101, rsum[i], false);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bop[j], av, acc[i][j], 0, 0, 0);
+      } else if constexpr (KIND == kBf16F8) {
+        const v8bf av = __builtin_bit_cast(v8bf, ra[buf][i]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[j]), av,
+                                                              acc[i][j], 0, 0, 0);
+      } else {
+        if constexpr (OUT == kOutBf16) {  // MatMul: operands share the output dtype
+          const v8bf av = __builtin_bit_cast(v8bf, ra[buf][i]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[j]), av,
+                                                                acc[i][j], 0, 0, 0);
+        } else {
+          const v8h av = __builtin_bit_cast(v8h, ra[buf][i]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, bop[j]), av,
+                                                               acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Instruction order (the scheduler would otherwise sink each LDS read next
+  // to its first use and expose its latency): a plain sub-step issues all
+  // LDS reads of the next sub-step first, then its own 8 MFMAs, so the reads
+  // complete under the MFMAs.  The barrier sub-step issues the next stage's
+  // reads right after the barrier and spreads the ring refill over its last
+  // 4 MFMAs.
+  constexpr int kReads = KIND == kBf16F8 ? 6 : 8;
+  auto order_plain = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);       // MFMA
+  };
+  auto order_refill = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, (L + 3) / 4, 0);  // VMEM (ring refill)
+    }
+  };
+
+  // One K step on ring stage `cur` (compile-time after unrolling); the
+  // fragments of its sub-step 0 are in register set 0.
+  auto step = [&](int t, int cur, int nxt) {
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      read((kk + 1) & 1, SA(cur), SB(cur), kk + 1);
+      build_b(kk & 1);
+      mma(kk & 1, 0, 4);
+      order_plain();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    build_b(1);
+    mma(1, 0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    RingBarrier<L>();       // step t+1 landed; every wave is done with `cur`
+    read(0, SA(nxt), SB(nxt), 0);
+    issue(t + 3, cur);
+    mma(1, 2, 4);
+    order_refill();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  RingBarrier<2 * L>();
+  read(0, sa0, sb0, 0);
+  int t = 0;
+  for (; t + 3 <= nk; t += 3) {
+    step(t, 0, 1);
+    step(t + 1, 1, 2);
+    step(t + 2, 2, 0);
+  }
+  if (t < nk) step(t, 0, 1);
+  if (t + 1 < nk) step(t + 1, 1, 2);
+  // drain the look-ahead (out-of-range) loads before the LDS is reused
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // ---- zero-point terms (kI8 with zero points): per-row RA and alpha,
+  // per-column CB and beta, exchanged through LDS ----
+  if constexpr (KIND == kI8 && ZP) {
+    int32_t *z_ra = zsum, *z_al = zsum + kBM, *z_cb = zsum + 2 * kBM, *z_be = zsum + 2 * kBM + kBN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = rsum[i] + __shfl_xor(rsum[i], 32);
+      const int r = wm * 128 + i * 32 + lr;
+      if (lg == 0 && wn == 0) {
+        const int64_t row = row0 + r;
+        z_ra[r] = v;
+        z_al[r] = (p.a_zp && row < M) ? (p.a_u8 ? 128 - (int)p.a_zp[row] : -(int)(int8_t)p.a_zp[row])
+                                      : p.alpha_scalar;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int v = csum[j] + __shfl_xor(csum[j], 32);
+      const int c = wn * 64 + j * 32 + lr;
+      if (lg == 0 && wm == 0) {
+        const int64_t col = col0 + c;
+        z_cb[c] = v;
+        z_be[c] = (p.b_zp && col < N) ? (p.b_u8 ? 128 - (int)p.b_zp[col] : -(int)(int8_t)p.b_zp[col])
+                                      : p.beta_scalar;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  // The MFMAs compute the transposed block (B fragment as the row operand),
+  // so lane (lr, lg) of block (i, j) holds output row 32i + lr and, in
+  // registers 4g .. 4g+3, the four consecutive columns 32j + 8g + 4lg + 0..3.
+  // Per 32-row block the wave packs those four values, stages the block in LDS
+  // (row pitch padded by 16 bytes) and writes whole 16-byte row pieces.
+  constexpr int kPitch = 64 * kOsz + 16;
+  char *stg = SA(wave >> 1) + (wave & 1) * 16384;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wm * 128 + i * 32 + lr;  // row within the workgroup tile
+    int32_t ra_r = 0, al_r = 0;
+    if constexpr (KIND == kI8 && ZP) {
+      ra_r = zsum[r];
+      al_r = zsum[kBM + r];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cl = j * 32 + g * 8 + lg * 4;  // first of the 4 columns (within the wave tile)
+        char *dst = stg + lr * kPitch + cl * kOsz;
+        if constexpr (KIND == kI8) {
+          unsigned v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = (unsigned)acc[i][j][4 * g + e];
+            if constexpr (ZP) {
+              // Y = sum a'b' + beta_j RA_i + alpha_i CB_j + K alpha_i beta_j (mod 2^32)
+              const int c = wn * 64 + cl + e;
+              const unsigned be = (unsigned)zsum[2 * kBM + kBN + c];
+              v[e] += be * (unsigned)ra_r + (unsigned)al_r * (unsigned)zsum[2 * kBM + c] +
+                      (unsigned)K * (unsigned)al_r * be;
+            }
+          }
+          if constexpr (OUT == kOutI32) {
+            *reinterpret_cast<v4i *>(dst) = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+          } else {
+            // ties-to-even rounding before the zero point, then saturation
+            unsigned packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + p.zy;
+              packed |= ((unsigned)(int)__builtin_amdgcn_fmed3f(f, p.qmin, p.qmax) & 0xffu) << (8 * e);
+            }
+            *reinterpret_cast<unsigned *>(dst) = packed;
+          }
+        } else {
+          const Acc &a = acc[i][j];
+          if constexpr (OUT == kOutBf16) {
+            *reinterpret_cast<v2i *>(dst) = v2i{(int)PackBf16(a[4 * g], a[4 * g + 1]),
+                                                (int)PackBf16(a[4 * g + 2], a[4 * g + 3])};
+          } else {
+            typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+            const v4h h = {(_Float16)a[4 * g], (_Float16)a[4 * g + 1], (_Float16)a[4 * g + 2],
+                           (_Float16)a[4 * g + 3]};
+            *reinterpret_cast<v4h *>(dst) = h;
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 32 rows x 64 columns x kOsz bytes = 128 * kOsz 16-byte pieces, 2 * kOsz per lane
+    constexpr int kChunksPerRow = 4 * kOsz;
+    const int64_t brow = row0 + wm * 128 + i * 32;
+    char *ybase = static_cast<char *>(p.Y) + ((bt * M + brow) * N + col0 + wn * 64) * kOsz;
+    const int64_t ncol = N - (col0 + wn * 64);
+#pragma unroll
+    for (int c = 0; c < 2 * kOsz; ++c) {
+      const int id = c * 64 + lane;
+      const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
+      const v4i v = *reinterpret_cast<const v4i *>(stg + rr * kPitch + cc * 16);
+      if (brow + rr < M && cc * (16 / kOsz) < ncol)
+        *reinterpret_cast<v4i *>(ybase + (int64_t)rr * N * kOsz + cc * 16) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Host-side eligibility of the pipelined kernel for a problem: K a multiple
+// of the K step, N a multiple of 16, 16-byte aligned operands and output, and
+// every per-matrix byte offset (plus the look-ahead) below 2^31 - 2^24.
+template <int KIND> inline bool Eligible(const GemmArgs &p) {
+  constexpr int kAsz = KIND == kI8 ? 1 : 2, kBsz = KIND == kH16 ? 2 : 1;
+  const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
+  auto al = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  return p.K > 0 && p.K % Traits<KIND>::kKStep == 0 && p.N % 16 == 0 && al(p.A) && al(p.B) &&
+         al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim &&
+         (p.K + 3 * Traits<KIND>::kKStep) * p.N * kBsz < lim;
+}
+
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8>
+inline void Launch(const GemmArgs &p, hipStream_t s) {
+  const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
+  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8>), dim3((unsigned)tiles), dim3(kThreads), 0,
+                     s, p);
+}
+
+}  // namespace mg
+}  // namespace onnxl_amd
