@@ -9,7 +9,10 @@ ops over the kernel time measured with HIP events on the launch stream.
 kernel, single core as the reference runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
-                  [--extra] [--no-cpu-baseline]
+                  [--no-extra] [--no-cpu-baseline]
+
+The other configurations (3, 4, 5) are timed too and reported under
+`extra` unless --no-extra is given.
 """
 from __future__ import annotations
 
@@ -228,7 +231,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
-    ap.add_argument("--extra", action="store_true", help="also time the other configurations")
+    ap.add_argument("--no-extra", dest="extra", action="store_false",
+                    help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--replicas", type=int, default=0,
                     help="buffer replicas for HBM-bound configs (0 = enough to exceed 512 MB)")

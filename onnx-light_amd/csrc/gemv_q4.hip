@@ -18,11 +18,13 @@
 //    v_mfma_f32_16x16x32_f16 (row = column n of the strip, 8 consecutive k);
 //    the activations are its B operand (column = row m of A).  Accumulation
 //    is fp32.
-//  - The 4 waves of a workgroup take consecutive K ranges of the same strip
+//  - The 8 waves of a workgroup take consecutive K ranges of the same strip
 //    and are reduced through LDS in a fixed order; when K is also split over
 //    workgroups, each writes its fp32 partial and the last one to arrive (an
 //    agent-scope counter per strip, reset by that workgroup) sums the
-//    partials in slice order and stores fp16 (round to nearest even).
+//    partials in slice order and stores fp16 (round to nearest even).  The
+//    partials travel through agent-scope atomic loads and stores, which are
+//    coherent across the XCDs' L2 caches without a cache-wide writeback.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -34,10 +36,12 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kStrip = 128;        // columns per workgroup
 constexpr int kChunk = 32;         // k rows per MFMA
-constexpr int kMaxChunks = 8;      // chunks per wave (all loads in flight at once)
+constexpr int kMaxChunks = 4;      // chunks per wave (all loads in flight at once)
+constexpr int kRedG = 33, kRedRow = 132;  // padded reduction layout
 
 struct GemvArgs {
   const _Float16 *A;      // [M, K]
@@ -54,55 +58,102 @@ struct GemvArgs {
   int cpw;                // chunks per wave
 };
 
-// Zero-point nibble of column c (0..7) of a packed dword.
-template <bool SIGNED> __device__ __forceinline__ int Nibble(uint32_t w, int c) {
-  const int u = (int)((w >> (4 * c)) & 0xfu);
-  return SIGNED ? ((u ^ 8) - 8) : u;
+// Nibbles of byte b of two k rows -> two fp16 pairs 0x6400 | u (= 1024 + u):
+// column 2b at rows (r0, r1) and column 2b + 1 at rows (r0, r1).  `sel`
+// gathers [x0.byte b, 0, x1.byte b, 0]; the AND-OR keeps one nibble per half
+// and inserts the fp16 exponent of 1024.
+__device__ __forceinline__ void DecodeBytePair(uint32_t x0, uint32_t x1, uint32_t sel, uint32_t mask,
+                                               uint32_t magic, uint32_t &even, uint32_t &odd) {
+  const uint32_t pb = __builtin_amdgcn_perm(x1, x0, sel);
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(even) : "v"(pb), "v"(mask), "v"(magic));
+  const uint32_t sh = pb >> 4;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(odd) : "v"(sh), "v"(mask), "v"(magic));
 }
 
-template <bool SIGNED, bool HAS_ZP>
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr unsigned kOob = 0x80000000u;  // past every buffer: loads return zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+template <bool SIGNED, bool HAS_ZP, int MODE>
 __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
-  __shared__ float red[4][16][kStrip];  // per-wave partial sums [wave][m][column]
+  // Per-wave partial sums; row m, strip column 8 * (4g + q) + e sits at
+  // m * kRedRow + g * kRedG + 8q + e (padding makes the 64 lanes' writes hit 64
+  // distinct banks).
+  __shared__ float red[kWaves][16 * kRedRow];
   __shared__ unsigned last_flag;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int li = lane & 15, g = lane >> 4;
-  const int strip = blockIdx.x, slice = blockIdx.y;
+  // Workgroups are dealt to the 8 XCDs round-robin: give each XCD a run of
+  // adjacent strips so the two halves of a 128-byte weight line (read by
+  // neighbouring strips) meet in the same L2.
+  // (XCD x owns the contiguous strips [x*base + min(x, extra), +count_x)).
+  const int nstrips = gridDim.x;
+  const int base = nstrips / 8, extra = nstrips % 8;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const int strip = xcd * base + min(xcd, extra) + slot;
+  const int slice = blockIdx.y;
   const int n0 = strip * kStrip + 8 * li;  // first of this lane's 8 columns
   const bool col_ok = n0 < p.N;
-  const int nq = p.N >> 3;                 // dwords per packed row
+  const int64_t row_bytes = p.N >> 1;     // packed bytes per k row
   const int total = p.K / kChunk;
-  const int c_begin = (slice * 4 + wave) * p.cpw;
-  const int c_end = min(c_begin + p.cpw, total);
-  const int nch = max(c_end - c_begin, 0);
+  const int c_begin = (slice * kWaves + wave) * p.cpw;
+  const int nch = max(min(c_begin + p.cpw, total) - c_begin, 0);
 
-  // ---- issue every load of this wave's K range ----
+  const int64_t s_rows = MODE == 2 ? p.K / p.blk : 1;
+  const __amdgpu_buffer_rsrc_t rsW = Rsrc(p.W, (int64_t)p.K * row_bytes);
+  const __amdgpu_buffer_rsrc_t rsS = Rsrc(p.scale, MODE == 0 ? 2 : s_rows * p.N * 2);
+  const __amdgpu_buffer_rsrc_t rsZ = Rsrc(p.zp, HAS_ZP ? (MODE == 0 ? 1 : (s_rows * p.N) >> 1) : 0);
+  const __amdgpu_buffer_rsrc_t rsA = Rsrc(p.A, (int64_t)p.M * p.K * 2);
+
+  // ---- issue every load of this wave's K range (branch-free: out-of-range
+  // lanes and chunks read from an offset past the buffer, which returns 0) ----
   uint32_t wq[kMaxChunks][8];
   v4i sc_raw[kMaxChunks];
   uint32_t zp_raw[kMaxChunks];
   v8h act[kMaxChunks];
+  v4i sc_fixed = v4i{0, 0, 0, 0};
+  uint32_t zp_fixed = 0;
+  if constexpr (MODE == 0) {
+    const uint32_t h = *static_cast<const uint16_t *>(static_cast<const void *>(p.scale));
+    const int s2 = (int)(h | (h << 16));
+    sc_fixed = v4i{s2, s2, s2, s2};
+    if (HAS_ZP) zp_fixed = (*reinterpret_cast<const uint8_t *>(p.zp) & 0xfu) * 0x11111111u;
+  } else if constexpr (MODE == 1) {
+    sc_fixed = __builtin_amdgcn_raw_buffer_load_b128(rsS, col_ok ? (unsigned)n0 * 2u : kOob, 0, 0);
+    if (HAS_ZP) zp_fixed = __builtin_amdgcn_raw_buffer_load_b32(rsZ, col_ok ? (unsigned)n0 >> 1 : kOob, 0, 0);
+  }
+  // Weight rows: the lane part of the offset is fixed, the row part is
+  // wave-uniform and goes into the scalar offset (no per-load vector math).
+  // Chunks past this wave's range re-read its first chunk (in bounds) and
+  // meet zero activations.
+  const unsigned w_lane = col_ok ? (unsigned)(8 * g * row_bytes + (n0 >> 1)) : kOob;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    if (c < nch) {
-      const int k0 = (c_begin + c) * kChunk + 8 * g;  // first of this lane's 8 k rows
+    const bool live = c < nch;
+    const int cc = live ? c_begin + c : min(c_begin, total - 1);
+    const int k0 = cc * kChunk + 8 * g;  // first of this lane's 8 k rows
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        wq[c][t] = col_ok ? __builtin_nontemporal_load(p.W + (int64_t)(k0 + t) * nq + (n0 >> 3)) : 0u;
-      int64_t si = 0;
-      if (p.mode == 2) si = (int64_t)(k0 / p.blk) * p.N + n0;
-      else if (p.mode == 1) si = n0;
-      if (p.mode == 0) {
-        const uint32_t s = *reinterpret_cast<const uint16_t *>(p.scale);
-        const int s2 = (int)(s | (s << 16));
-        sc_raw[c] = v4i{s2, s2, s2, s2};
-        if (HAS_ZP) {
-          const uint32_t z = *reinterpret_cast<const uint8_t *>(p.zp) & 0xfu;
-          zp_raw[c] = z * 0x11111111u;
-        }
-      } else {
-        sc_raw[c] = col_ok ? *reinterpret_cast<const v4i *>(p.scale + si) : v4i{0, 0, 0, 0};
-        if (HAS_ZP) zp_raw[c] = col_ok ? p.zp[si >> 3] : 0u;
-      }
-      act[c] = li < p.M ? *reinterpret_cast<const v8h *>(p.A + (int64_t)li * p.K + k0) : v8h{};
+    for (int t = 0; t < 8; ++t)
+      wq[c][t] = __builtin_amdgcn_raw_buffer_load_b32(
+          rsW, w_lane, (int)((int64_t)(cc * kChunk + t) * row_bytes), 0);
+    if constexpr (MODE == 2) {
+      const int64_t si = (int64_t)(k0 / p.blk) * p.N + n0;
+      sc_raw[c] = __builtin_amdgcn_raw_buffer_load_b128(rsS, col_ok ? (unsigned)(si * 2) : kOob, 0, 0);
+      if (HAS_ZP) zp_raw[c] = __builtin_amdgcn_raw_buffer_load_b32(rsZ, col_ok ? (unsigned)(si >> 1) : kOob, 0, 0);
+    }
+    act[c] = __builtin_bit_cast(
+        v8h, __builtin_amdgcn_raw_buffer_load_b128(
+                 rsA, (live && li < p.M) ? (unsigned)(((int64_t)li * p.K + k0) * 2) : kOob, 0, 0));
+  }
+  if constexpr (MODE != 2) {
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      sc_raw[c] = sc_fixed;
+      zp_raw[c] = zp_fixed;
     }
   }
 
@@ -110,43 +161,46 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  const uint32_t mask = 0x000f000fu, magic = 0x64006400u;
+  const uint32_t flip = SIGNED ? 0x88888888u : 0u;  // signed nibble s -> s + 8
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    if (c < nch) {
-      // per-column scale pair (s, s) and bias pair (1024 [+ 8] + zp)
-      v2h sc2[8], sub2[8];
+    if (c < nch) {  // wave-uniform
+      // Per column e: scale pair (s_e, s_e) and bias pair (1024 + zb_e) twice,
+      // zb = zero point (+ 8 for INT4, matching the weight's own offset), so
+      // that (0x6400 | u) - bias = x - zp exactly.
+      uint32_t sc2[8], bias2[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t word = (uint32_t)sc_raw[c][e >> 1];
-        const uint32_t h = (e & 1) ? (word >> 16) : (word & 0xffffu);
-        sc2[e] = __builtin_bit_cast(v2h, h | (h << 16));
-        const int bias = (SIGNED ? 1032 : 1024) + (HAS_ZP ? Nibble<SIGNED>(zp_raw[c], e) : 0);
-        const _Float16 b = (_Float16)bias;  // exact: 1016 .. 1047
-        sub2[e] = v2h{b, b};
+        sc2[e] = __builtin_amdgcn_perm(word, word, (e & 1) ? 0x03020302u : 0x01000100u);
+      }
+      if (HAS_ZP) {
+        const uint32_t z = zp_raw[c] ^ flip;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          DecodeBytePair(z, z, 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b, mask, magic,
+                         bias2[2 * b], bias2[2 * b + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bias2[e] = SIGNED ? 0x64086408u : 0x64006400u;  // 1032 / 1024
       }
       uint32_t wk[8][4];  // [column][row pair]: fp16 (1024 + u) at rows 2p, 2p+1
 #pragma unroll
       for (int pr = 0; pr < 4; ++pr) {
-        uint32_t x0 = wq[c][2 * pr], x1 = wq[c][2 * pr + 1];
-        if (SIGNED) {
-          x0 ^= 0x88888888u;  // signed nibble s -> s + 8
-          x1 ^= 0x88888888u;
-        }
+        const uint32_t x0 = wq[c][2 * pr] ^ flip, x1 = wq[c][2 * pr + 1] ^ flip;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          // bytes: [x0.byte b, 0, x1.byte b, 0]  (selector 0x0c = zero byte)
-          const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
-          const uint32_t pb = __builtin_amdgcn_perm(x1, x0, sel);
-          wk[2 * b][pr] = (pb & 0x000f000fu) | 0x64006400u;
-          wk[2 * b + 1][pr] = ((pb >> 4) & 0x000f000fu) | 0x64006400u;
-        }
+        for (int b = 0; b < 4; ++b)
+          DecodeBytePair(x0, x1, 0x0c000c00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b, mask, magic,
+                         wk[2 * b][pr], wk[2 * b + 1][pr]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         v8h wop;
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
-          const v2h q = (__builtin_bit_cast(v2h, wk[e][pr]) - sub2[e]) * sc2[e];
+          const v2h q = (__builtin_bit_cast(v2h, wk[e][pr]) - __builtin_bit_cast(v2h, bias2[e])) *
+                        __builtin_bit_cast(v2h, sc2[e]);
           wop[2 * pr] = q.x;
           wop[2 * pr + 1] = q.y;
         }
@@ -155,13 +209,13 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
     }
   }
 
-  // ---- reduce the 4 waves: lane (li, g), register q holds row m = li of
-  // strip columns 8 * (4g + q) + e ----
+  // ---- reduce the waves: lane (li, g), register q of acc[e] holds row m = li
+  // of strip column 8 * (4g + q) + e ----
   if (li < p.M) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) red[wave][li][8 * (4 * g + q) + e] = acc[e][q];
+      for (int q = 0; q < 4; ++q) red[wave][li * kRedRow + g * kRedG + 8 * q + e] = acc[e][q];
   }
   __syncthreads();
   const int M = p.M;
@@ -169,32 +223,44 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
   for (int idx = threadIdx.x; idx < M * kStrip; idx += kThreads) {
     const int m = idx / kStrip, col = idx % kStrip;
     const int n = strip * kStrip + col;
-    const float v = ((red[0][m][col] + red[1][m][col]) + red[2][m][col]) + red[3][m][col];
+    const int ri = m * kRedRow + (col >> 5) * kRedG + 8 * ((col >> 3) & 3) + (col & 7);
+    float v = red[0][ri];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += red[w][ri];  // fixed order
     if (n < p.N) {
-      if (split) p.partial[((int64_t)slice * M + m) * p.N + n] = v;
-      else p.Y[(int64_t)m * p.N + n] = (_Float16)v;
+      if (split) {
+        // agent-scope atomic store: coherent across XCDs without a cache-wide fence
+        __hip_atomic_store(p.partial + ((int64_t)slice * M + m) * p.N + n, v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        p.Y[(int64_t)m * p.N + n] = (_Float16)v;
+      }
     }
   }
   if (!split) return;
 
-  // ---- K split over workgroups: the last one to arrive sums the partials ----
-  __threadfence();
+  // ---- K split over workgroups: the last one to arrive sums the partials.
+  // The partials are written and read with agent-scope atomic accesses; every
+  // wave waits for its stores to complete before the barrier that precedes the
+  // counter update, so a workgroup that sees the final count reads complete
+  // partials. ----
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(p.counters + strip, 1u, __ATOMIC_ACQ_REL,
+    const unsigned prev = __hip_atomic_fetch_add(p.counters + strip, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == (unsigned)(p.slices - 1);
   }
   __syncthreads();
   if (!last_flag) return;
-  __threadfence();
   for (int idx = threadIdx.x; idx < M * kStrip; idx += kThreads) {
     const int m = idx / kStrip, col = idx % kStrip;
     const int n = strip * kStrip + col;
     if (n < p.N) {
       float v = 0.f;
       for (int s = 0; s < p.slices; ++s)
-        v += __builtin_nontemporal_load(p.partial + ((int64_t)s * M + m) * p.N + n);
+        v += __hip_atomic_load(p.partial + ((int64_t)s * M + m) * p.N + n, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
       p.Y[(int64_t)m * p.N + n] = (_Float16)v;
     }
   }
@@ -204,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
 
 int Slices(const DqMatMulParams &p) {
   const int total = (int)(p.K / kChunk);
-  return (total + 4 * kMaxChunks - 1) / (4 * kMaxChunks);
+  return (total + kWaves * kMaxChunks - 1) / (kWaves * kMaxChunks);
 }
 
 }  // namespace
@@ -212,8 +278,8 @@ int Slices(const DqMatMulParams &p) {
 bool GemvQ4Eligible(const DqMatMulParams &p) {
   const bool four = p.w_dtype == kInt4 || p.w_dtype == kUint4;
   return four && p.M >= 1 && p.M <= 16 && !p.a_bf16 && p.scale_f16 && p.deq_round_f16 &&
-         p.cast_round == 0 && p.K % kChunk == 0 && p.N % 8 == 0 && p.K <= (1 << 30) &&
-         p.N <= (1 << 30) && (p.mode != 2 || (p.block % 8 == 0)) &&
+         p.cast_round == 0 && p.K % kChunk == 0 && p.N % 8 == 0 &&
+         p.K * p.N / 2 < (int64_t(1) << 31) - 64 && p.M * p.K * 2 < (int64_t(1) << 31) - 64 && (p.mode != 2 || (p.block % 8 == 0)) &&
          reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && reinterpret_cast<uintptr_t>(p.W) % 4 == 0 &&
          reinterpret_cast<uintptr_t>(p.scale) % 16 == 0;
 }
@@ -241,15 +307,24 @@ void LaunchGemvQ4(const DqMatMulParams &p, void *scratch, unsigned *counters, hi
   g.mode = p.mode;
   g.slices = Slices(p);
   const int total = (int)(p.K / kChunk);
-  g.cpw = (total + 4 * g.slices - 1) / (4 * g.slices);
+  g.cpw = (total + kWaves * g.slices - 1) / (kWaves * g.slices);
   const dim3 grid((unsigned)((p.N + kStrip - 1) / kStrip), (unsigned)g.slices);
   const bool sgn = p.w_dtype == kInt4, zp = p.zp != nullptr;
-  if (sgn) {
-    if (zp) hipLaunchKernelGGL((GemvQ4Kernel<true, true>), grid, dim3(kThreads), 0, stream, g);
-    else hipLaunchKernelGGL((GemvQ4Kernel<true, false>), grid, dim3(kThreads), 0, stream, g);
-  } else {
-    if (zp) hipLaunchKernelGGL((GemvQ4Kernel<false, true>), grid, dim3(kThreads), 0, stream, g);
-    else hipLaunchKernelGGL((GemvQ4Kernel<false, false>), grid, dim3(kThreads), 0, stream, g);
+  const int sel = (sgn ? 4 : 0) | (zp ? 2 : 0);
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, g); };
+  switch (p.mode * 8 + sel) {
+  case 0: go(GemvQ4Kernel<false, false, 0>); break;
+  case 2: go(GemvQ4Kernel<false, true, 0>); break;
+  case 4: go(GemvQ4Kernel<true, false, 0>); break;
+  case 6: go(GemvQ4Kernel<true, true, 0>); break;
+  case 8: go(GemvQ4Kernel<false, false, 1>); break;
+  case 10: go(GemvQ4Kernel<false, true, 1>); break;
+  case 12: go(GemvQ4Kernel<true, false, 1>); break;
+  case 14: go(GemvQ4Kernel<true, true, 1>); break;
+  case 16: go(GemvQ4Kernel<false, false, 2>); break;
+  case 18: go(GemvQ4Kernel<false, true, 2>); break;
+  case 20: go(GemvQ4Kernel<true, false, 2>); break;
+  default: go(GemvQ4Kernel<true, true, 2>); break;
   }
 }
 
