@@ -153,7 +153,10 @@ bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes
   if (Fp8Eligible(p)) {
     const mg::GemmArgs g = Fp8Args(p);
     if (mg::Eligible<mg::kBf16F8>(g)) {
-      mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false>(g, stream);
+      // 256 x 256 tiles when there are enough of them to fill the GPU
+      const int64_t big_tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+      if (big_tiles >= 512) mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 4>(g, stream);
+      else mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 2>(g, stream);
       return true;
     }
   }

@@ -5,7 +5,9 @@
 // Y[b] = A[b] (M x K, row-major) * B[b] (K x N, row-major).
 //
 // Workgroup: 256 threads = 4 waves (2 x 2), one wave per SIMD, output tile
-// 256 x 128; each wave owns 128 x 64 = 4 x 2 blocks of 32 x 32 MFMA outputs.
+// 256 x (64 * WB); each wave owns 128 x (32 * WB) = 4 x WB blocks of 32 x 32
+// MFMA outputs (WB = 2, or 4 for large GEMMs: the 256 accumulators then fill
+// the AGPRs and each operand byte read from LDS feeds twice the MFMAs).
 // A K step covers 128 bytes of every A row (128 int8 or 64 16-bit values).
 //
 // Memory path.
@@ -27,12 +29,13 @@
 //    c0 + 8(s%2) ..) resp. (row k0 + s/4, columns c0 + 4(s%4) ..) and lane i
 //    receives column c0 + i at k0, k0+1, ...
 //
-// Schedule (per K step of 4 sub-steps): the fragments of sub-step kk+1 are
-// read from LDS while the MFMAs of sub-step kk run (two register sets).  The
-// single barrier per step sits inside the last sub-step, after half of its
-// MFMAs are issued, so the matrix pipe stays busy across it.  The barrier
-// waits only for the oldest ring stage (s_waitcnt vmcnt(L) with L the direct
-// loads per step), never for all loads.
+// Schedule (per K step of 4 sub-steps): the fragments of sub-step s are read
+// from LDS two sub-steps ahead (three register sets) and its B operand is
+// decoded (fp8 -> bf16 with scale, or the int8 sign flip) under the MFMAs of
+// sub-step s - 1, so neither LDS latency nor decode VALU work stalls the
+// matrix pipe.  The single barrier per step sits inside sub-step 2, after
+// half of its MFMAs are issued.  It waits only for the oldest ring stage
+// (s_waitcnt vmcnt(L), L = direct loads per step), never for all loads.
 //
 // Epilogue: each wave converts its accumulators, stages 32 rows at a time in
 // LDS and writes them back with 16-byte row-contiguous stores.
@@ -55,7 +58,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef __attribute__((address_space(3))) v2i *lds_v2i_t;
 typedef __attribute__((address_space(3))) v4s *lds_v4s_t;
 
-constexpr int kBM = 256, kBN = 128, kStepBytes = 128, kStages = 3, kThreads = 256;
+constexpr int kBM = 256, kStepBytes = 128, kStages = 3, kThreads = 256;
 constexpr int kGroupM = 8, kXcds = 8;
 constexpr int kAStage = kBM * kStepBytes;  // 32 KB
 constexpr int kRsrcWord3 = 0x00020000;
@@ -77,25 +80,29 @@ template <int KIND> struct Traits;
 template <> struct Traits<kI8> {
   static constexpr int kKStep = 128;     // k values per step
   static constexpr int kBRows = 128;     // B rows per step
-  static constexpr int kBPitch = 128;    // bytes per B row in LDS
+  static constexpr int kBsz = 1;         // bytes per B element
   using Acc = v16i;
 };
 template <> struct Traits<kBf16F8> {
   static constexpr int kKStep = 64;
   static constexpr int kBRows = 64;
-  static constexpr int kBPitch = 128;
+  static constexpr int kBsz = 1;
   using Acc = v16f;
 };
 template <> struct Traits<kH16> {
   static constexpr int kKStep = 64;
   static constexpr int kBRows = 64;
-  static constexpr int kBPitch = 256;
+  static constexpr int kBsz = 2;
   using Acc = v16f;
 };
-template <int KIND> constexpr int BStageBytes() { return Traits<KIND>::kBRows * Traits<KIND>::kBPitch; }
+// The workgroup tile is 256 x BN with BN = 64 * WB: each wave owns 4 x WB
+// blocks of 32 x 32 (WB = 2: 128 x 64 per wave; WB = 4: 128 x 128, which
+// halves the operand bytes per MFMA and fills the 256 accumulator registers).
+template <int KIND, int WB> constexpr int BPitch() { return 64 * WB * Traits<KIND>::kBsz; }
+template <int KIND, int WB> constexpr int BStageBytes() { return Traits<KIND>::kBRows * BPitch<KIND, WB>(); }
 // direct loads per wave per K step: A 32 KB + B stage, 1 KB per instruction
-template <int KIND> constexpr int LoadsPerWave() { return (kAStage + BStageBytes<KIND>()) / 1024 / 4; }
-template <int KIND> constexpr int BLoadsPerWave() { return BStageBytes<KIND>() / 1024 / 4; }
+template <int KIND, int WB> constexpr int LoadsPerWave() { return (kAStage + BStageBytes<KIND, WB>()) / 1024 / 4; }
+template <int KIND, int WB> constexpr int BLoadsPerWave() { return BStageBytes<KIND, WB>() / 1024 / 4; }
 
 __device__ __forceinline__ int64_t MinI64(int64_t a, int64_t b) { return a < b ? a : b; }
 
@@ -136,14 +143,18 @@ struct GemmArgs {
   int scale_per_col;
 };
 
-template <int KIND, int OUT, bool ZP, bool AU8, bool BU8>
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB>
 __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) {
   constexpr bool RA = ZP, CB = ZP;
   using T = Traits<KIND>;
   using Acc = typename T::Acc;
-  constexpr int kBStage = BStageBytes<KIND>();
-  constexpr int L = LoadsPerWave<KIND>();
-  constexpr int LB = BLoadsPerWave<KIND>();
+  constexpr int kBN = 64 * WB;                 // workgroup tile columns
+  constexpr int kWN = 32 * WB;                 // wave tile columns
+  constexpr int kBP = BPitch<KIND, WB>();      // bytes per B row in LDS
+  constexpr int kBStage = BStageBytes<KIND, WB>();
+  constexpr int L = LoadsPerWave<KIND, WB>();
+  constexpr int LB = BLoadsPerWave<KIND, WB>();
+  static_assert(WB == 2 || (WB == 4 && KIND != kH16), "tile width");
   constexpr int kOsz = OUT == kOutI32 ? 4 : (OUT == kOutQ8 ? 1 : 2);
   static_assert(LB >= 1 && LB <= 4, "B direct loads per wave");
   // One object per ring stage: the compiler's LDS-DMA wait tracking can then
@@ -152,8 +163,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   __shared__ __align__(16) char sb0[kBStage], sb1[kBStage], sb2[kBStage];
   __shared__ int32_t zsum[ZP ? 2 * (kBM + kBN) : 1];
   // stage index -> array (indices are compile-time constants after unrolling)
-  auto SA = [&](int s) -> char * { return s == 0 ? sa0 : (s == 1 ? sa1 : sa2); };
-  auto SB = [&](int s) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
+  auto SA = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sa0 : (s == 1 ? sa1 : sa2); };
+  auto SB = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -189,7 +200,10 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(K * NB), kRsrcWord3);
-  const int nk = (int)(K / T::kKStep);
+  const int nfull = (int)(K / T::kKStep);                  // full K steps
+  const bool half = K % T::kKStep != 0;                     // K % kKStep == kKStep / 2
+  const int nk = nfull + (half ? 1 : 0);                    // K steps to load
+  const int n_sub = 4 * nfull + (half ? 2 : 0);             // sub-steps to multiply
 
   // ---- direct-load offsets (K step 0) ----
   unsigned a_g[8];
@@ -208,47 +222,54 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       const int64_t cb = 2 * col0 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3)));
       b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
     } else {
-      const int krow = 8 * i + (lane >> 3);
-      const int64_t cb = col0 + 16 * ((lane & 7) ^ (lane >> 3));
+      // 1-byte B: a 1 KB piece is 1024 / kBP rows; lane -> (row, 16-byte
+      // position p), holding global chunk p ^ (row % 8)
+      constexpr int kCpr = kBP / 16;
+      const int krow = (1024 / kBP) * i + lane / kCpr;
+      const int64_t cb = col0 + 16 * ((lane % kCpr) ^ (krow & 7));
       b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
     }
   }
   // ---- LDS fragment offsets (sub-step 0; sub-step kk adds kk * const) ----
-  int a_rd[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = wm * 128 + i * 32 + lr;
-    a_rd[i] = (r >> 3) * 1024 + 128 * (lg ^ ((r >> 3) & 1)) + (r & 7) * 16;
+  // Block i of a wave's A fragment sits exactly 4096 bytes after block i-1
+  // (4 row blocks of 8), so one base register per stage serves all four
+  // blocks and the four sub-steps through the 16-bit DS offset field.
+  int a_rd0;
+  {
+    const int r = wm * 128 + lr;
+    a_rd0 = (r >> 3) * 1024 + 128 * (lg ^ ((r >> 3) & 1)) + (r & 7) * 16;
   }
   const int s16 = lane & 15, g16 = lane >> 4;
-  int b_rd[2][2];  // [j][h]
+  // One base per column block j; the second transposing read of a fragment
+  // (h = 1) is 8 rows (int8) or 4 rows (16-bit) further, the same swizzle.
+  int b_rd[WB];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if constexpr (KIND == kI8) {
-        const int krow = 16 * (g16 >> 1) + 8 * h + (s16 >> 1);
-        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
-        b_rd[j][h] = krow * 128 + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
-      } else if constexpr (KIND == kBf16F8) {
-        const int krow = 8 * (g16 >> 1) + (s16 >> 1);
-        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
-        b_rd[j][h] = krow * 128 + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
-      } else {
-        const int krow = 8 * (g16 >> 1) + 4 * h + (s16 >> 2);
-        const int col = wn * 64 + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
-        b_rd[j][h] = krow * 256 + 16 * ((col >> 3) ^ (2 * (krow & 3))) + ((2 * col) & 15);
-      }
+  for (int j = 0; j < WB; ++j) {
+    if constexpr (KIND == kI8) {
+      const int krow = 16 * (g16 >> 1) + (s16 >> 1);
+      const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
+      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+    } else if constexpr (KIND == kBf16F8) {
+      const int krow = 8 * (g16 >> 1) + (s16 >> 1);
+      const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
+      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+    } else {
+      const int krow = 8 * (g16 >> 1) + (s16 >> 2);
+      const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
+      b_rd[j] = krow * kBP + 16 * ((col >> 3) ^ (2 * (krow & 3))) + ((2 * col) & 15);
     }
+  }
   // B rows per sub-step: 32 (int8) or 16 (16-bit k values)
   constexpr int kSubRows = KIND == kI8 ? 32 : 16;
 
   // per-column dequantization scales (kBf16F8)
-  float bscale[2] = {1.f, 1.f};
+  float bscale[WB];
+#pragma unroll
+  for (int j = 0; j < WB; ++j) bscale[j] = 1.f;
   if constexpr (KIND == kBf16F8) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = col0 + wn * 64 + j * 32 + lr;
+    for (int j = 0; j < WB; ++j) {
+      const int64_t col = col0 + wn * kWN + j * 32 + lr;
       const int64_t si = p.scale_per_col ? (col < N ? col : 0) : 0;
       bscale[j] = p.scale_f16 ? (float)static_cast<const _Float16 *>(p.scale)[si]
                               : static_cast<const float *>(p.scale)[si];
@@ -257,7 +278,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int aflip = (KIND == kI8 && AU8) ? (int)kFlip : 0;
   constexpr int bflip = (KIND == kI8 && BU8) ? (int)kFlip : 0;
 
-  auto issue = [&](int step, int stage) {
+  auto issue = [&](int step, int stage) __attribute__((always_inline)) {
     const bool live = step < nk;
     const unsigned ka = (unsigned)step * kStepBytes;
     const unsigned kb = (unsigned)((int64_t)step * T::kBRows * NB);
@@ -274,139 +295,165 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
                                                live ? b_g[q] + kb : kOob, 0, 0, 0);
   };
 
-  // ---- fragments: raw LDS reads (two sets) and MFMA-ready operands ----
-  v4i ra[2][4];
-  v4i rb[2][2];  // kI8: 2 x tr8; kBf16F8: 1 x tr8 (.xy); kH16: 2 x tr16
-  auto read = [&](int buf, const char *sa, const char *sb, int kk) {
+  // ---- fragments ----
+  // Sub-step s (4 per K step) multiplies A fragments ra[s % 3] by the decoded
+  // B operands bop[s % 2].  Its LDS reads were issued two sub-steps earlier
+  // and its B decode ran under the MFMAs of sub-step s - 1, so neither the LDS
+  // latency nor the decode VALU work stalls the matrix pipe.
+  v4i ra[3][4];
+  v4i rb[3][WB];  // raw B: kI8 2 x tr8; kBf16F8 1 x tr8 (.xy); kH16 2 x tr16
+  auto read = [&](int buf, const char *sa, const char *sb, int kk) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const char *base = sb + kk * kSubRows * T::kBPitch;
+    for (int j = 0; j < WB; ++j) {
+      const char *base = sb + kk * kSubRows * kBP;
       if constexpr (KIND == kI8) {
-        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][0]));
-        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][1]));
+        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j]));
+        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j] + 8 * kBP));
         rb[buf][j] = v4i{lo.x, lo.y, hi.x, hi.y};
       } else if constexpr (KIND == kBf16F8) {
-        const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j][0]));
+        const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j]));
         rb[buf][j] = v4i{v.x, v.y, 0, 0};
       } else {
-        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j][0]));
-        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j][1]));
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j]));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(base + b_rd[j] + 4 * kBP));
         rb[buf][j] = v4i{__builtin_bit_cast(v2i, lo).x, __builtin_bit_cast(v2i, lo).y,
                          __builtin_bit_cast(v2i, hi).x, __builtin_bit_cast(v2i, hi).y};
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      ra[buf][i] = *reinterpret_cast<const v4i *>(sa + a_rd[i] + kk * 256);
+      ra[buf][i] = *reinterpret_cast<const v4i *>(sa + a_rd0 + i * 4096 + kk * 256);
   };
 
-  Acc acc[4][2];
+  Acc acc[4][WB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = Acc{0};
+    for (int j = 0; j < WB; ++j) acc[i][j] = Acc{0};
   int rsum[4] = {0, 0, 0, 0};  // kI8: partial row sums of a' (this lane's k group)
-  int csum[2] = {0, 0};        // kI8: partial column sums of b'
+  int csum[WB];                // kI8: partial column sums of b'
+#pragma unroll
+  for (int j = 0; j < WB; ++j) csum[j] = 0;
 
-  v4i bop[2];  // MFMA-ready B operands of the current sub-step
-  auto build_b = [&](int buf) {
+  v4i bop[2][WB];  // MFMA-ready B operands
+  // `live` is false for the look-ahead decode of a sub-step past K, whose
+  // bytes must not enter the column sums.
+  auto decode = [&](int rbuf, int bbuf, bool live) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < WB; ++j) {
       if constexpr (KIND == kI8) {
-        bop[j] = rb[buf][j] ^ bflip;
-        if (CB) {
+        bop[bbuf][j] = rb[rbuf][j] ^ bflip;
+        if (CB && live) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) csum[j] = __builtin_amdgcn_sdot4(bop[j][e], 0x01010101, csum[j], false);
+          for (int e = 0; e < 4; ++e)
+            csum[j] = __builtin_amdgcn_sdot4(bop[bbuf][j][e], 0x01010101, csum[j], false);
         }
       } else if constexpr (KIND == kBf16F8) {
-        const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].x, false);
-        const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].x, true);
-        const v2f f2 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].y, false);
-        const v2f f3 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[buf][j].y, true);
-        const float s = bscale[j];
-        bop[j] = v4i{(int)PackBf16(f0.x * s, f0.y * s), (int)PackBf16(f1.x * s, f1.y * s),
-                     (int)PackBf16(f2.x * s, f2.y * s), (int)PackBf16(f3.x * s, f3.y * s)};
+        const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, false);
+        const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, true);
+        const v2f f2 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, false);
+        const v2f f3 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, true);
+        const float sc = bscale[j];
+        bop[bbuf][j] = v4i{(int)PackBf16(f0.x * sc, f0.y * sc), (int)PackBf16(f1.x * sc, f1.y * sc),
+                           (int)PackBf16(f2.x * sc, f2.y * sc), (int)PackBf16(f3.x * sc, f3.y * sc)};
       } else {
-        bop[j] = rb[buf][j];
+        bop[bbuf][j] = rb[rbuf][j];
       }
     }
   };
-  auto mma = [&](int buf, int i0, int i1) {
+  auto mma = [&](int abuf, int bbuf, int i0, int i1) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
       if constexpr (KIND == kI8) {
-        const v4i av = ra[buf][i] ^ aflip;
+        const v4i av = ra[abuf][i] ^ aflip;
         if (RA) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) rsum[i] = __builtin_amdgcn_sdot4(av[e], 0x01010101, rsum[i], false);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bop[j], av, acc[i][j], 0, 0, 0);
-      } else if constexpr (KIND == kBf16F8) {
-        const v8bf av = __builtin_bit_cast(v8bf, ra[buf][i]);
+        for (int j = 0; j < WB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bop[bbuf][j], av, acc[i][j], 0, 0, 0);
+      } else if constexpr (KIND == kBf16F8 || OUT == kOutBf16) {
+        const v8bf av = __builtin_bit_cast(v8bf, ra[abuf][i]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[j]), av,
+        for (int j = 0; j < WB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[bbuf][j]), av,
                                                               acc[i][j], 0, 0, 0);
-      } else {
-        if constexpr (OUT == kOutBf16) {  // MatMul: operands share the output dtype
-          const v8bf av = __builtin_bit_cast(v8bf, ra[buf][i]);
+      } else {  // kH16 with FLOAT16 operands
+        const v8h av = __builtin_bit_cast(v8h, ra[abuf][i]);
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[j]), av,
-                                                                acc[i][j], 0, 0, 0);
-        } else {
-          const v8h av = __builtin_bit_cast(v8h, ra[buf][i]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, bop[j]), av,
-                                                               acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < WB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, bop[bbuf][j]), av,
+                                                             acc[i][j], 0, 0, 0);
       }
     }
   };
 
-  // Instruction order (the scheduler would otherwise sink each LDS read next
-  // to its first use and expose its latency): a plain sub-step issues all
-  // LDS reads of the next sub-step first, then its own 8 MFMAs, so the reads
-  // complete under the MFMAs.  The barrier sub-step issues the next stage's
-  // reads right after the barrier and spreads the ring refill over its last
-  // 4 MFMAs.
-  constexpr int kReads = KIND == kBf16F8 ? 6 : 8;
-  auto order_plain = [&]() {
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);       // MFMA
-  };
-  auto order_refill = [&]() {
+  // Instruction order inside a sub-step (the scheduler would otherwise sink
+  // each LDS read next to its first use): the LDS reads two sub-steps ahead
+  // go first, then each MFMA is followed by its share of the next sub-step's
+  // decode, so the VALU work issues while the matrix pipe is busy.
+  constexpr int kReads = 4 + WB * (KIND == kBf16F8 ? 1 : 2);
+  constexpr int kDecodeValu = KIND == kBf16F8 ? 16 * WB : (KIND == kI8 ? 12 * WB : 0);
+  auto order = [&]() __attribute__((always_inline)) {
+    constexpr int kNM = 4 * WB;  // MFMAs of a plain sub-step
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, (L + 3) / 4, 0);  // VMEM (ring refill)
+    for (int x = 0; x < kNM; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if constexpr (kDecodeValu > 0)
+        __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + kNM - 1) / kNM, 0);  // VALU
+    }
+  };
+  auto order_refill = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
+#pragma unroll
+    for (int x = 0; x < 2 * WB; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, (L + 2 * WB - 1) / (2 * WB), 0);  // VMEM
+      if constexpr (kDecodeValu > 0)
+        __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + 2 * WB - 1) / (2 * WB), 0);  // VALU
     }
   };
 
-  // One K step on ring stage `cur` (compile-time after unrolling); the
-  // fragments of its sub-step 0 are in register set 0.
-  auto step = [&](int t, int cur, int nxt) {
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      read((kk + 1) & 1, SA(cur), SB(cur), kk + 1);
-      build_b(kk & 1);
-      mma(kk & 1, 0, 4);
-      order_plain();
+  // Sub-step s = 4 t + kk of K step t (ring stage t % 3); all buffer and
+  // stage indices are compile-time after unrolling.  Sub-step kk == 2 holds
+  // the step's barrier: every wave has retired its reads of stage t - 1 ... t
+  // (its last reads of stage t were issued in sub-step kk == 1), and step
+  // t + 1 has landed, so stage t is refilled with step t + 3 and the reads of
+  // step t + 1 begin.
+  auto substep = [&](int t, int kk, int sb3, int sb2, int cur, int nxt) __attribute__((always_inline)) {
+    const int nb3 = (sb3 + 1) % 3, nb2 = (sb2 + 1) % 2, rb3 = (sb3 + 2) % 3;
+    if (kk != 2) {
+      if (kk < 2) read(rb3, SA(cur), SB(cur), kk + 2);
+      else read(rb3, SA(nxt), SB(nxt), kk - 2);
+      decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
+      mma(sb3, sb2, 0, 4);
+      order();
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      mma(sb3, sb2, 0, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      RingBarrier<L>();
+      read(rb3, SA(nxt), SB(nxt), 0);
+      issue(t + 3, cur);
+      decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
+      mma(sb3, sb2, 2, 4);
+      order_refill();
       __builtin_amdgcn_sched_barrier(0);
     }
-    build_b(1);
-    mma(1, 0, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    RingBarrier<L>();       // step t+1 landed; every wave is done with `cur`
-    read(0, SA(nxt), SB(nxt), 0);
-    issue(t + 3, cur);
-    mma(1, 2, 4);
-    order_refill();
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  // one full K step t whose first sub-step index s = 4t has s % 3 == r3
+  auto step = [&](int t, int r3, int cur, int nxt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) substep(t, kk, (r3 + kk) % 3, kk % 2, cur, nxt);
+  };
+  // A final half step (K % kKStep == kKStep / 2) runs 2 of the 4 sub-steps;
+  // its stage was loaded whole (k past K: zero rows of B, unread bytes of A).
+  auto half_step = [&](int r3) __attribute__((always_inline)) {
+    decode((r3 + 1) % 3, 1, true);
+    mma(r3, 0, 0, 4);
+    mma((r3 + 1) % 3, 1, 0, 4);
   };
 
   issue(0, 0);
@@ -414,14 +461,22 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   issue(2, 2);
   RingBarrier<2 * L>();
   read(0, sa0, sb0, 0);
+  read(1, sa0, sb0, 1);
+  decode(0, 0, true);
   int t = 0;
-  for (; t + 3 <= nk; t += 3) {
-    step(t, 0, 1);
-    step(t + 1, 1, 2);
-    step(t + 2, 2, 0);
+  for (; t + 3 <= nfull; t += 3) {  // 12 sub-steps: s % 3 and the stages repeat
+    step(t, 0, 0, 1);
+    step(t + 1, 1, 1, 2);
+    step(t + 2, 2, 2, 0);
   }
-  if (t < nk) step(t, 0, 1);
-  if (t + 1 < nk) step(t + 1, 1, 2);
+  if (t < nfull) step(t, 0, 0, 1);
+  if (t + 1 < nfull) step(t + 1, 1, 1, 2);
+  if (half) {
+    const int r3 = nfull % 3;  // (4 * nfull) % 3
+    if (r3 == 0) half_step(0);
+    else if (r3 == 1) half_step(1);
+    else half_step(2);
+  }
   // drain the look-ahead (out-of-range) loads before the LDS is reused
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -441,9 +496,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < WB; ++j) {
       const int v = csum[j] + __shfl_xor(csum[j], 32);
-      const int c = wn * 64 + j * 32 + lr;
+      const int c = wn * kWN + j * 32 + lr;
       if (lg == 0 && wm == 0) {
         const int64_t col = col0 + c;
         z_cb[c] = v;
@@ -460,7 +515,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // registers 4g .. 4g+3, the four consecutive columns 32j + 8g + 4lg + 0..3.
   // Per 32-row block the wave packs those four values, stages the block in LDS
   // (row pitch padded by 16 bytes) and writes whole 16-byte row pieces.
-  constexpr int kPitch = 64 * kOsz + 16;
+  constexpr int kPitch = kWN * kOsz + 16;
   char *stg = SA(wave >> 1) + (wave & 1) * 16384;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -471,7 +526,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       al_r = zsum[kBM + r];
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < WB; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int cl = j * 32 + g * 8 + lg * 4;  // first of the 4 columns (within the wave tile)
@@ -483,7 +538,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
             v[e] = (unsigned)acc[i][j][4 * g + e];
             if constexpr (ZP) {
               // Y = sum a'b' + beta_j RA_i + alpha_i CB_j + K alpha_i beta_j (mod 2^32)
-              const int c = wn * 64 + cl + e;
+              const int c = wn * kWN + cl + e;
               const unsigned be = (unsigned)zsum[2 * kBM + kBN + c];
               v[e] += be * (unsigned)ra_r + (unsigned)al_r * (unsigned)zsum[2 * kBM + c] +
                       (unsigned)K * (unsigned)al_r * be;
@@ -518,13 +573,13 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 32 rows x 64 columns x kOsz bytes = 128 * kOsz 16-byte pieces, 2 * kOsz per lane
-    constexpr int kChunksPerRow = 4 * kOsz;
+    // 32 rows x kWN columns x kOsz bytes in 16-byte pieces, WB * kOsz per lane
+    constexpr int kChunksPerRow = kWN * kOsz / 16;
     const int64_t brow = row0 + wm * 128 + i * 32;
-    char *ybase = static_cast<char *>(p.Y) + ((bt * M + brow) * N + col0 + wn * 64) * kOsz;
-    const int64_t ncol = N - (col0 + wn * 64);
+    char *ybase = static_cast<char *>(p.Y) + ((bt * M + brow) * N + col0 + wn * kWN) * kOsz;
+    const int64_t ncol = N - (col0 + wn * kWN);
 #pragma unroll
-    for (int c = 0; c < 2 * kOsz; ++c) {
+    for (int c = 0; c < WB * kOsz; ++c) {
       const int id = c * 64 + lane;
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
       const v4i v = *reinterpret_cast<const v4i *>(stg + rr * kPitch + cc * 16);
@@ -538,22 +593,23 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 }
 
 // Host-side eligibility of the pipelined kernel for a problem: K a multiple
-// of the K step, N a multiple of 16, 16-byte aligned operands and output, and
+// of half the K step (a trailing half step is allowed), N a multiple of 16, 16-byte aligned operands and output, and
 // every per-matrix byte offset (plus the look-ahead) below 2^31 - 2^24.
 template <int KIND> inline bool Eligible(const GemmArgs &p) {
   constexpr int kAsz = KIND == kI8 ? 1 : 2, kBsz = KIND == kH16 ? 2 : 1;
   const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
   auto al = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-  return p.K > 0 && p.K % Traits<KIND>::kKStep == 0 && p.N % 16 == 0 && al(p.A) && al(p.B) &&
+  return p.K > 0 && p.K % (Traits<KIND>::kKStep / 2) == 0 && p.N % 16 == 0 && al(p.A) && al(p.B) &&
          al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim &&
          (p.K + 3 * Traits<KIND>::kKStep) * p.N * kBsz < lim;
 }
 
-template <int KIND, int OUT, bool ZP, bool AU8, bool BU8>
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB = 2>
 inline void Launch(const GemmArgs &p, hipStream_t s) {
+  constexpr int kBN = 64 * WB;
   const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
-  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8>), dim3((unsigned)tiles), dim3(kThreads), 0,
-                     s, p);
+  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8, WB>), dim3((unsigned)tiles), dim3(kThreads),
+                     0, s, p);
 }
 
 }  // namespace mg
