@@ -59,7 +59,7 @@ typedef __attribute__((address_space(3))) v2i *lds_v2i_t;
 typedef __attribute__((address_space(3))) v4s *lds_v4s_t;
 
 constexpr int kBM = 256, kStepBytes = 128, kStages = 3, kThreads = 256;
-constexpr int kGroupM = 8, kXcds = 8;
+constexpr int kGroupM = 4, kXcds = 8;
 constexpr int kAStage = kBM * kStepBytes;  // 32 KB
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr unsigned kOob = 0x80000000u;
@@ -278,21 +278,27 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int aflip = (KIND == kI8 && AU8) ? (int)kFlip : 0;
   constexpr int bflip = (KIND == kI8 && BU8) ? (int)kFlip : 0;
 
-  auto issue = [&](int step, int stage) __attribute__((always_inline)) {
+  // Direct loads of K step `step` into ring stage `stage`: the L loads of a
+  // step, numbered A pieces 0..7 then B pieces, in halves (part 0 / 1) or
+  // all at once (part 2).
+  auto issue = [&](int step, int stage, int part) __attribute__((always_inline)) {
     const bool live = step < nk;
     const unsigned ka = (unsigned)step * kStepBytes;
     const unsigned kb = (unsigned)((int64_t)step * T::kBRows * NB);
     char *sa = SA(stage);
     char *sb = SB(stage);
+    const int lo = part == 1 ? L / 2 : 0, hi = part == 0 ? L / 2 : L;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsA, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16,
-          live ? a_g[q] + ka : kOob, 0, 0, 0);
+      if (q >= lo && q < hi)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsA, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16,
+            live ? a_g[q] + ka : kOob, 0, 0, 0);
 #pragma unroll
     for (int q = 0; q < LB; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16,
-                                               live ? b_g[q] + kb : kOob, 0, 0, 0);
+      if (8 + q >= lo && 8 + q < hi)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16,
+                                                 live ? b_g[q] + kb : kOob, 0, 0, 0);
   };
 
   // ---- fragments ----
@@ -405,12 +411,23 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
         __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + kNM - 1) / kNM, 0);  // VALU
     }
   };
+  auto order_vm = [&]() __attribute__((always_inline)) {  // plain sub-step + half a refill
+    constexpr int kNM = 4 * WB;
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
+#pragma unroll
+    for (int x = 0; x < kNM; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (x < L - L / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+      if constexpr (kDecodeValu > 0)
+        __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + kNM - 1) / kNM, 0);  // VALU
+    }
+  };
   auto order_refill = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
     for (int x = 0; x < 2 * WB; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, (L + 2 * WB - 1) / (2 * WB), 0);  // VMEM
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, (L / 2 + 2 * WB - 1) / (2 * WB), 0);  // VMEM
       if constexpr (kDecodeValu > 0)
         __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + 2 * WB - 1) / (2 * WB), 0);  // VALU
     }
@@ -427,16 +444,18 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     if (kk != 2) {
       if (kk < 2) read(rb3, SA(cur), SB(cur), kk + 2);
       else read(rb3, SA(nxt), SB(nxt), kk - 2);
+      if (kk == 3) issue(t + 3, cur, 1);
       decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
       mma(sb3, sb2, 0, 4);
-      order();
+      if (kk == 3) order_vm();
+      else order();
       __builtin_amdgcn_sched_barrier(0);
     } else {
       mma(sb3, sb2, 0, 2);
       __builtin_amdgcn_sched_barrier(0);
       RingBarrier<L>();
       read(rb3, SA(nxt), SB(nxt), 0);
-      issue(t + 3, cur);
+      issue(t + 3, cur, 0);  // first half of the refill; the rest in sub-step 3
       decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
       mma(sb3, sb2, 2, 4);
       order_refill();
@@ -456,9 +475,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     mma((r3 + 1) % 3, 1, 0, 4);
   };
 
-  issue(0, 0);
-  issue(1, 1);
-  issue(2, 2);
+  issue(0, 0, 2);
+  issue(1, 1, 2);
+  issue(2, 2, 2);
   RingBarrier<2 * L>();
   read(0, sa0, sb0, 0);
   read(1, sa0, sb0, 1);
