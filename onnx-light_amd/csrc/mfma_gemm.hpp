@@ -200,6 +200,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(K * NB), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsY = __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<char *>(p.Y) + bt * M * N * kOsz, (short)0, (int)(M * N * kOsz), kRsrcWord3);
   const int nfull = (int)(K / T::kKStep);                  // full K steps
   const bool half = K % T::kKStep != 0;                     // K % kKStep == kKStep / 2
   const int nk = nfull + (half ? 1 : 0);                    // K steps to load
@@ -594,16 +596,25 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // 32 rows x kWN columns x kOsz bytes in 16-byte pieces, WB * kOsz per lane
     constexpr int kChunksPerRow = kWN * kOsz / 16;
+    // Branch-free stores: pieces outside the matrix get an offset past the
+    // buffer, which the buffer store drops; all LDS reads issue first.
     const int64_t brow = row0 + wm * 128 + i * 32;
-    char *ybase = static_cast<char *>(p.Y) + ((bt * M + brow) * N + col0 + wn * kWN) * kOsz;
     const int64_t ncol = N - (col0 + wn * kWN);
+    const unsigned ybase = (unsigned)((brow * N + col0 + wn * kWN) * kOsz);
+    v4i piece[WB * kOsz];
 #pragma unroll
     for (int c = 0; c < WB * kOsz; ++c) {
       const int id = c * 64 + lane;
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
-      const v4i v = *reinterpret_cast<const v4i *>(stg + rr * kPitch + cc * 16);
-      if (brow + rr < M && cc * (16 / kOsz) < ncol)
-        *reinterpret_cast<v4i *>(ybase + (int64_t)rr * N * kOsz + cc * 16) = v;
+      piece[c] = *reinterpret_cast<const v4i *>(stg + rr * kPitch + cc * 16);
+    }
+#pragma unroll
+    for (int c = 0; c < WB * kOsz; ++c) {
+      const int id = c * 64 + lane;
+      const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
+      const bool ok = brow + rr < M && cc * (16 / kOsz) < ncol;
+      __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY,
+                                             ok ? ybase + (unsigned)(rr * N * kOsz + cc * 16) : kOob, 0, 0);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -619,7 +630,7 @@ template <int KIND> inline bool Eligible(const GemmArgs &p) {
   const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
   auto al = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
   return p.K > 0 && p.K % (Traits<KIND>::kKStep / 2) == 0 && p.N % 16 == 0 && al(p.A) && al(p.B) &&
-         al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim &&
+         al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim && p.M * p.N * 4 < lim &&
          (p.K + 3 * Traits<KIND>::kKStep) * p.N * kBsz < lim;
 }
 
