@@ -342,6 +342,7 @@ class Prepared:
     keeps per node): calling it re-runs the kernel on the same buffers."""
 
     def __init__(self, fn_name: str, descs: list, extra: tuple, stream):
+        self._fn_name = fn_name
         self._fn = getattr(lib(), fn_name)
         self._descs = descs
         self._args = [ctypes.byref(d) if isinstance(d, Tensor) else d for d in descs]
@@ -350,6 +351,12 @@ class Prepared:
 
     def __call__(self) -> None:
         _check(self._fn(*self._args, self._stream))
+
+    def on(self, stream) -> "Prepared":
+        """The same call launched on `stream` (a torch stream or a raw
+        hipStream_t handle), e.g. the stream a HIP graph is captured on."""
+        handle = getattr(stream, "cuda_stream", stream)
+        return Prepared(self._fn_name, self._descs, self._extra, ctypes.c_void_p(handle))
 
 
 def prepare(fn_name: str, *tensors, descs=None, **kw):

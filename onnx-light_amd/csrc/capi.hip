@@ -38,13 +38,10 @@ void *Workspace::Get(size_t bytes) {
   if (bytes <= cap_ && ptr_ != nullptr) return ptr_;
   size_t want = std::max<size_t>(bytes, size_t(1) << 20);
   want = std::max(want, cap_ * 2);
-  if (ptr_ != nullptr) {
-    OLA_HIP(hipDeviceSynchronize());
-    OLA_HIP(hipFree(ptr_));
-    ptr_ = nullptr;
-    cap_ = 0;
-  }
-  OLA_HIP(hipMalloc(&ptr_, want));
+  void *fresh = nullptr;
+  OLA_HIP(hipMalloc(&fresh, want));
+  if (ptr_ != nullptr) retired_.push_back(ptr_);
+  ptr_ = fresh;
   cap_ = want;
   return ptr_;
 }
@@ -52,13 +49,16 @@ void *Workspace::Get(size_t bytes) {
 unsigned *Workspace::Counters(size_t count) {
   if (count <= counters_cap_ && counters_ != nullptr) return counters_;
   size_t want = std::max<size_t>(count, 4096);
-  if (counters_ != nullptr) {
-    OLA_HIP(hipDeviceSynchronize());
-    OLA_HIP(hipFree(counters_));
-    counters_ = nullptr;
+  want = std::max(want, counters_cap_ * 2);
+  unsigned *fresh = nullptr;
+  OLA_HIP(hipMalloc(&fresh, want * sizeof(unsigned)));
+  const hipError_t err = hipMemset(fresh, 0, want * sizeof(unsigned));
+  if (err != hipSuccess) {
+    (void)hipFree(fresh);
+    OLA_HIP(err);
   }
-  OLA_HIP(hipMalloc(&counters_, want * sizeof(unsigned)));
-  OLA_HIP(hipMemset(counters_, 0, want * sizeof(unsigned)));
+  if (counters_ != nullptr) retired_.push_back(counters_);
+  counters_ = fresh;
   counters_cap_ = want;
   return counters_;
 }
@@ -66,6 +66,8 @@ unsigned *Workspace::Counters(size_t count) {
 void Workspace::Release() {
   if (ptr_) (void)hipFree(ptr_);
   if (counters_) (void)hipFree(counters_);
+  for (void *q : retired_) (void)hipFree(q);
+  retired_.clear();
   ptr_ = nullptr;
   counters_ = nullptr;
   cap_ = counters_cap_ = 0;

@@ -121,9 +121,12 @@ MatMulPlan MakeMatMulPlan(const Shape &a, const Shape &b, const char *kname, con
 class Workspace {
 public:
   // Returns device memory of at least `bytes`, 256-byte aligned.  Growing it
-  // synchronises the device first (earlier calls may still read it).
+  // allocates a larger buffer and retires the old one without freeing it:
+  // launches already queued, and HIP graphs captured earlier, keep valid
+  // pointers.  Retired buffers are freed by Release().
   void *Get(size_t bytes);
-  // Zero-initialised counters that kernels leave at zero when they finish.
+  // Zero-initialised counters that kernels leave at zero when they finish
+  // (grown the same way).
   unsigned *Counters(size_t count);
   void Release();
 
@@ -132,6 +135,7 @@ private:
   size_t cap_ = 0;
   unsigned *counters_ = nullptr;
   size_t counters_cap_ = 0;
+  std::vector<void *> retired_;
 };
 
 struct DeviceContext {

@@ -6,6 +6,7 @@ per-column)."""
 import hashlib
 import json
 import os
+import zlib
 
 import numpy as np
 import pytest
@@ -70,7 +71,7 @@ def _zps(kind, dt, n, rng):
                                  (np.int8, np.uint8)], ids=["u8s8", "s8s8", "u8u8", "s8u8"])
 def test_matmul_integer_vs_oracle(olamd, oracle, dev, shapes, dts):
     a_shape, b_shape = shapes
-    rng = np.random.default_rng(abs(hash((a_shape, b_shape, str(dts)))) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(repr((a_shape, b_shape, str(dts))).encode()))
     ia, ib = np.iinfo(dts[0]), np.iinfo(dts[1])
     a = rng.integers(ia.min, ia.max + 1, a_shape).astype(dts[0])
     b = rng.integers(ib.min, ib.max + 1, b_shape).astype(dts[1])
@@ -164,7 +165,7 @@ def test_qlinear_known_answers(olamd, golden, dev):
                          ids=["u8s8-u8", "s8s8-s8", "u8u8-s8", "s8u8-u8"])
 def test_qlinear_vs_oracle(olamd, oracle, dev, shapes, dts):
     a_shape, b_shape = shapes
-    rng = np.random.default_rng(abs(hash((a_shape, b_shape, str(dts)))) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(repr((a_shape, b_shape, str(dts))).encode()))
     ia, ib, iy = np.iinfo(dts[0]), np.iinfo(dts[1]), np.iinfo(dts[2])
     a = rng.integers(ia.min, ia.max + 1, a_shape).astype(dts[0])
     b = rng.integers(ib.min, ib.max + 1, b_shape).astype(dts[1])
