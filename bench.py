@@ -88,15 +88,21 @@ def make_c2(olamd, dev):
     return w
 
 
-def make_c3(olamd, dev, replicas):
+def make_c3(olamd, dev, replicas, prepared=True):
+    """Configuration 3.  `prepared`: the weight is given in the tiled layout
+    written once by onnxl_amd_prepare_weight (the session-time preparation of
+    a constant weight; the dequantisation itself still runs in every call),
+    else in the ONNX packing."""
     import importlib
     import torch
     syn = importlib.import_module("onnx_light_amd.synth")
     x = syn.config_inputs(3)
     w = Workload()
     w.name = ("C3 decode GEMV fp16[8,4096] x DequantizeLinear(int4[4096,11008], block 32 on K, fp16 "
-              "scales) -> fp16[8,11008]")
+              "scales) -> fp16[8,11008], weight " + ("prepared (tiled layout)" if prepared else "in the ONNX packing"))
     w.key, w.unit, w.dtype, w.bound = "c3", "GB/s", "fp16 x int4 (fp32 accumulate)", "hbm"
+    if not prepared:
+        w.key = "c3_onnx_layout"
     K, N = x["w_shape"]
     w.nbytes = K * N // 2 + (K // 32) * N * 2 + 8 * K * 2 + 8 * N * 2
     w.work = float(w.nbytes)
@@ -106,8 +112,13 @@ def make_c3(olamd, dev, replicas):
         wq = _t(x["w"], dev)
         sc = _t(x["scale"], dev)
         y = torch.empty((8, N), dtype=torch.float16, device=dev)
-        w.calls.append(olamd.prepare("dequantize_linear_matmul", a, wq, sc, None, 0, 0, y,
-                                     descs={1: olamd.describe(wq, olamd.INT4, (K, N))}))
+        if prepared:
+            pw = olamd.prepare_weight(wq, olamd.INT4, (K, N))
+            del wq
+            w.calls.append(olamd.prepare("dequantize_linear_matmul", a, pw, sc, None, 0, 0, y))
+        else:
+            w.calls.append(olamd.prepare("dequantize_linear_matmul", a, wq, sc, None, 0, 0, y,
+                                         descs={1: olamd.describe(wq, olamd.INT4, (K, N))}))
     w.inputs = x
     return w
 
@@ -270,7 +281,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c3_onnx_layout", "c4", "c5"])
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -293,6 +304,8 @@ def main():
             return make_c2(olamd, dev)
         if key == "c3":
             return make_c3(olamd, dev, args.replicas or 24)
+        if key == "c3_onnx_layout":
+            return make_c3(olamd, dev, args.replicas or 24, prepared=False)
         if key == "c4":
             return make_c4(olamd, dev)
         return make_c5(olamd, dev, args.replicas or 16)
@@ -309,7 +322,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c4", "c5"):
+        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5"):
             if key == args.workload:
                 continue
             try:

@@ -50,6 +50,14 @@ typedef enum onnxl_amd_status {
 
 typedef enum onnxl_amd_location { ONNXL_AMD_DEVICE = 0, ONNXL_AMD_HOST = 1 } onnxl_amd_location;
 
+/* Element order of a payload.  Every tensor uses ONNXL_AMD_LAYOUT_ONNX except
+ * a weight prepared by onnxl_amd_prepare_weight, which only the x input of
+ * onnxl_amd_dequantize_linear_matmul accepts. */
+typedef enum onnxl_amd_layout {
+  ONNXL_AMD_LAYOUT_ONNX = 0,       /* row-major; 4-bit values two per byte, low nibble first */
+  ONNXL_AMD_LAYOUT_TILED_INT4 = 1  /* the tiled INT4 / UINT4 form of onnxl_amd_prepare_weight */
+} onnxl_amd_layout;
+
 /* Mirrors the fields of the reference core::runtime::Tensor that kernels read
  * (core/runtime/memory/simple_tensor.h:526): data_type, shape, bytes. */
 typedef struct onnxl_amd_tensor {
@@ -59,7 +67,7 @@ typedef struct onnxl_amd_tensor {
   void *data;                       /* payload (see location) */
   int64_t size_bytes;               /* payload bytes */
   int32_t location;                 /* onnxl_amd_location */
-  int32_t reserved;                 /* must be 0 */
+  int32_t layout;                   /* onnxl_amd_layout (0 = ONNX) */
 } onnxl_amd_tensor;
 
 /* Library lifetime.  init selects the device for all later calls on this
@@ -132,11 +140,26 @@ int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, v
  * (axis 0) scales.  No single reference kernel: it computes the chain
  * kq/kernel_dequantizelinear.cc:522-693 -> kernel_cast.cc:360-370 ->
  * km/kernel_matmul.cc:181-223 that a DequantizeLinear->[Cast]->MatMul
- * subgraph runs node by node. */
+ * subgraph runs node by node.  x may be a weight prepared by
+ * onnxl_amd_prepare_weight (layout ONNXL_AMD_LAYOUT_TILED_INT4). */
 int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
                                        const onnxl_amd_tensor *x_scale,
                                        const onnxl_amd_tensor *x_zero_point, int64_t axis,
                                        int32_t cast_to, onnxl_amd_tensor *y, void *stream);
+
+/* Session-time preparation of a constant INT4 / UINT4 weight x [K, N] (ONNX
+ * layout) for onnxl_amd_dequantize_linear_matmul: writes it into `prepared`
+ * (device memory of onnxl_amd_prepare_weight_size bytes, 16-byte aligned,
+ * allocated by the caller) in a tiled order in which each 16-column tile's
+ * full K range is contiguous, and sets prepared's data_type, dims and layout
+ * (ONNXL_AMD_LAYOUT_TILED_INT4).  The prepared descriptor then replaces x in
+ * every later call; the values, scales, zero points and results are those of
+ * the original x.  This is the counterpart of the reference's kernel
+ * preparations (core/runtime/kernels/kernel_context.h:45-76), through which
+ * its Gemm kernel packs a constant B once per session
+ * (km/kernel_gemm.cc:378-405, representation "Gemm:B:column-major-k-v1"). */
+int onnxl_amd_prepare_weight_size(const onnxl_amd_tensor *x, int64_t *bytes);
+int onnxl_amd_prepare_weight(const onnxl_amd_tensor *x, onnxl_amd_tensor *prepared, void *stream);
 
 /* Waits for all work queued by this library on `stream`. */
 int onnxl_amd_synchronize(void *stream);

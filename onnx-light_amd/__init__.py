@@ -32,6 +32,7 @@ FLOAT16, DOUBLE, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 10, 11, 16, 17, 21, 22
 
 OK, INVALID_ARGUMENT, UNSUPPORTED, DEVICE_ERROR, NOT_INITIALIZED = 0, 1, 2, 3, 4
 DEVICE, HOST = 0, 1
+LAYOUT_ONNX, LAYOUT_TILED_INT4 = 0, 1
 
 
 class InvalidArgument(ValueError):
@@ -51,7 +52,7 @@ class Tensor(ctypes.Structure):
     _fields_ = [("data_type", ctypes.c_int32), ("rank", ctypes.c_int32),
                 ("dims", ctypes.c_int64 * MAX_RANK), ("data", ctypes.c_void_p),
                 ("size_bytes", ctypes.c_int64), ("location", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("layout", ctypes.c_int32)]
 
 
 TP = ctypes.POINTER(Tensor)
@@ -86,6 +87,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_prepare_weight_size.argtypes = [TP, ctypes.POINTER(ctypes.c_int64)]
+        L.onnxl_amd_prepare_weight.argtypes = [TP, TP, ctypes.c_void_p]
         L.onnxl_amd_synchronize.argtypes = [ctypes.c_void_p]
         _lib = L
     return _lib
@@ -145,6 +148,8 @@ def describe(t, dtype: int | None = None, shape=None) -> Tensor:
 
     ``dtype`` overrides the element type (4-bit types, FLOAT16 bits held in
     uint16 arrays, ...); ``shape`` overrides the logical shape."""
+    if isinstance(t, PreparedWeight):
+        return t.desc
     d = Tensor()
     if t is None:
         d.rank = -1
@@ -176,8 +181,39 @@ def describe(t, dtype: int | None = None, shape=None) -> Tensor:
     return d
 
 
+class PreparedWeight:
+    """A constant INT4 / UINT4 weight in the tiled device layout written by
+    onnxl_amd_prepare_weight: `storage` holds the bytes, `desc` the descriptor
+    (layout LAYOUT_TILED_INT4) that stands for the weight in later calls."""
+
+    def __init__(self, storage, desc: Tensor):
+        self.storage = storage
+        self.desc = desc
+        self.shape = tuple(desc.dims[i] for i in range(desc.rank))
+        self.is_cuda = True
+        self.device = storage.device
+
+
+def prepare_weight(x, x_dtype: int, x_shape=None) -> PreparedWeight:
+    """Session-time preparation of a constant 4-bit weight x [K, N] (packed
+    uint8 storage in the ONNX layout) for dequantize_linear_matmul."""
+    torch = _torch()
+    d = describe(x, x_dtype, _shape_of(x, x_shape))
+    n = ctypes.c_int64(0)
+    _check(lib().onnxl_amd_prepare_weight_size(ctypes.byref(d), ctypes.byref(n)))
+    dev = x.device if (not isinstance(x, np.ndarray) and x.is_cuda) else torch.device("cuda", torch.cuda.current_device())
+    storage = torch.empty(max(n.value, 1), dtype=torch.uint8, device=dev)
+    out = describe(storage)
+    _check(lib().onnxl_amd_prepare_weight(ctypes.byref(d), ctypes.byref(out),
+                                          ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    out._keep = storage
+    return PreparedWeight(storage, out)
+
+
 def _stream_of(*ts):
     for t in ts:
+        if isinstance(t, PreparedWeight):
+            continue
         if t is not None and not isinstance(t, np.ndarray) and t.is_cuda:
             return ctypes.c_void_p(_torch().cuda.current_stream(t.device).cuda_stream)
     return None
@@ -185,6 +221,8 @@ def _stream_of(*ts):
 
 def _device_of(*ts):
     for t in ts:
+        if isinstance(t, PreparedWeight):
+            return t.device
         if t is not None and not isinstance(t, np.ndarray) and t.is_cuda:
             return t.device
     return "cpu"

@@ -138,14 +138,21 @@ BatchMap ToBatchMap(const MatMulPlan &p) {
 // ---------------------------------------------------------------------------
 // Descriptor helpers.
 
-void CheckDescriptor(const onnxl_amd_tensor *t, const char *what) {
+void CheckDescriptor(const onnxl_amd_tensor *t, const char *what, bool allow_tiled = false) {
   if (t == nullptr) return;
   OLA_ENFORCE(t->rank <= ONNXL_AMD_MAX_RANK, what, ": rank above ", ONNXL_AMD_MAX_RANK);
   if (t->rank < 0) return;
   for (int i = 0; i < t->rank; ++i) OLA_ENFORCE(t->dims[i] >= 0, what, ": negative dimension");
   OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE || t->location == ONNXL_AMD_HOST, what,
               ": unknown location");
-  const int64_t need = PackedBytes(t->data_type, NumElements(*t));
+  const bool tiled = t->layout == ONNXL_AMD_LAYOUT_TILED_INT4;
+  OLA_ENFORCE(t->layout == ONNXL_AMD_LAYOUT_ONNX || (allow_tiled && tiled), what, ": layout ", t->layout,
+              " is not accepted here");
+  if (tiled)
+    OLA_ENFORCE(IsFourBit(t->data_type) && t->rank == 2, what,
+                ": the tiled layout holds 2-D INT4 / UINT4 weights only");
+  const int64_t need = tiled ? TiledInt4Bytes(t->dims[0], t->dims[1])
+                             : PackedBytes(t->data_type, NumElements(*t));
   OLA_ENFORCE(t->size_bytes >= need, what, ": payload of ", t->size_bytes,
               " bytes is smaller than its shape needs (", need, ")");
   OLA_ENFORCE(need == 0 || t->data != nullptr, what, ": null payload");
@@ -598,7 +605,7 @@ int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_a
   OLA_ENFORCE(!Absent(a) && !Absent(x) && !Absent(x_scale) && y, kDqmName,
               ": A, x, x_scale and the output are required.");
   CheckDescriptor(a, "A");
-  CheckDescriptor(x, "x");
+  CheckDescriptor(x, "x", /*allow_tiled=*/true);
   CheckDescriptor(x_scale, "x_scale");
   CheckDescriptor(x_zp, "x_zero_point");
   CheckDescriptor(y, "Y");
@@ -672,6 +679,7 @@ int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_a
   p.a_bf16 = a->data_type == kBfloat16;
   p.deq_round_f16 = dq_out == kFloat16;
   p.cast_round = cast_to == kBfloat16 ? 16 : (cast_to == kFloat16 ? 10 : 0);
+  p.w_tiled = x->layout == ONNXL_AMD_LAYOUT_TILED_INT4;
   const size_t scratch = DqMatMulScratchBytes(p);
   Staging st(stream, scratch, {a, x, x_scale, has_zp ? x_zp : nullptr}, {y});
   p.A = st.In(a);
@@ -827,6 +835,44 @@ int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_am
                                        int32_t cast_to, onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DqMatMul(a, x, x_scale, x_zero_point, axis, cast_to, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_weight_size(const onnxl_amd_tensor *x, int64_t *bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(!Absent(x) && bytes, "prepare_weight: x and bytes are required.");
+    CheckDescriptor(x, "x");
+    OLA_ENFORCE(IsFourBit(x->data_type) && x->rank == 2,
+                "prepare_weight: only 2-D INT4 / UINT4 weights have a prepared layout.");
+    *bytes = TiledInt4Bytes(x->dims[0], x->dims[1]);
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_weight(const onnxl_amd_tensor *x, onnxl_amd_tensor *prepared, void *stream) {
+  return Guard([&] {
+    OLA_ENFORCE(!Absent(x) && prepared, "prepare_weight: x and prepared are required.");
+    CheckDescriptor(x, "x");
+    OLA_ENFORCE(IsFourBit(x->data_type) && x->rank == 2,
+                "prepare_weight: only 2-D INT4 / UINT4 weights have a prepared layout.");
+    const int64_t K = x->dims[0], N = x->dims[1];
+    const int64_t need = TiledInt4Bytes(K, N);
+    OLA_ENFORCE(prepared->location == ONNXL_AMD_DEVICE, "prepare_weight: prepared must be device memory.");
+    OLA_ENFORCE(prepared->size_bytes >= need, "prepare_weight: prepared holds ", prepared->size_bytes,
+                " bytes, the tiled weight needs ", need);
+    OLA_ENFORCE(need == 0 || (prepared->data != nullptr && reinterpret_cast<uintptr_t>(prepared->data) % 16 == 0),
+                "prepare_weight: prepared must be a 16-byte aligned device buffer.");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Ctx();
+    Staging st(s, 0, {x}, {});
+    LaunchTileInt4(static_cast<const uint8_t *>(st.In(x)), K, N, x->data_type == kInt4,
+                   static_cast<uint32_t *>(prepared->data), s);
+    prepared->data_type = x->data_type;
+    prepared->rank = 2;
+    for (int i = 0; i < ONNXL_AMD_MAX_RANK; ++i) prepared->dims[i] = i < 2 ? x->dims[i] : 0;
+    prepared->layout = ONNXL_AMD_LAYOUT_TILED_INT4;
+    st.Finish();
+    return ONNXL_AMD_OK;
   });
 }
 

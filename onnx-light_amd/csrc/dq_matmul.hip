@@ -1,7 +1,8 @@
 // Dequantize-fused MatMul dispatch and the FLOAT16 / BFLOAT16 MatMul.
 //
 //  - int4 / uint4 weights with FLOAT16 scales, M <= 16 (decode): the
-//    bandwidth-bound GEMV (gemv_q4.hip).
+//    bandwidth-bound GEMV, on the ONNX packing (gemv_q4.hip) or on the tiled
+//    layout of a prepared weight (gemv_q4_tiled.hip).
 //  - float8e4m3fn weights, FLOAT scales per column or per tensor, Cast to
 //    BFLOAT16, bf16 activations (prefill): the pipelined MFMA core with the
 //    weight decoded and scaled as it is read from LDS (mfma_gemm.hpp, kBf16F8).
@@ -17,6 +18,8 @@
 namespace onnxl_amd {
 
 bool GemvQ4Eligible(const DqMatMulParams &p);
+bool GemvQ4TiledEligible(const DqMatMulParams &p);
+void LaunchGemvQ4Tiled(const DqMatMulParams &p, hipStream_t stream);
 size_t GemvQ4ScratchBytes(const DqMatMulParams &p);
 size_t GemvQ4Counters(const DqMatMulParams &p);
 void LaunchGemvQ4(const DqMatMulParams &p, void *scratch, unsigned *counters, hipStream_t stream);
@@ -74,8 +77,17 @@ __device__ __forceinline__ float DecodeWeight(const uint8_t *w, int dt, int64_t 
   }
 }
 
+// Element (k, n) of a 4-bit weight in the tiled layout (kernels.hpp).
+__device__ __forceinline__ float DecodeTiled(const uint8_t *w, int dt, int64_t ngroups, int64_t k, int64_t n) {
+  const int64_t t = n >> 4, i = n & 15, q = k >> 7, c = (k >> 5) & 3, g = (k >> 3) & 3, j = k & 7;
+  const uint32_t word = reinterpret_cast<const uint32_t *>(w)[((t * ngroups + q) * 64 + g * 16 + i) * 4 + c];
+  const uint32_t u = (word >> ((j & 1) ? 16 + 4 * (j >> 1) : 4 * (j >> 1))) & 15u;
+  return dt == kInt4 ? (float)((int)u - 8) : (float)u;
+}
+
 __global__ __launch_bounds__(256) void DequantWeightKernel(const DqMatMulParams p, uint16_t *out) {
   const int64_t total = p.K * p.N;
+  const int64_t ngroups = (p.K + 127) / 128;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t k = i / p.N, n = i % p.N;
     int64_t si = 0;
@@ -84,7 +96,8 @@ __global__ __launch_bounds__(256) void DequantWeightKernel(const DqMatMulParams 
     const float s = p.scale_f16 ? F16ToF32(static_cast<const uint16_t *>(p.scale)[si])
                                 : static_cast<const float *>(p.scale)[si];
     const float z = p.zp ? DecodeWeight(p.zp, p.w_dtype, si) : 0.f;
-    const float v = (DecodeWeight(p.W, p.w_dtype, i) - z) * s;
+    const float x = p.w_tiled ? DecodeTiled(p.W, p.w_dtype, ngroups, k, n) : DecodeWeight(p.W, p.w_dtype, i);
+    const float v = (x - z) * s;
     uint16_t bits;
     if (p.deq_round_f16) {
       bits = F32ToF16(v);  // DequantizeLinear output FLOAT16 (no Cast follows)
@@ -133,6 +146,7 @@ void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream) {
 }
 
 size_t DqMatMulScratchBytes(const DqMatMulParams &p) {
+  if (GemvQ4TiledEligible(p)) return 0;
   if (GemvQ4Eligible(p)) return GemvQ4ScratchBytes(p);
   if (Fp8Eligible(p) && mg::Eligible<mg::kBf16F8>(Fp8Args(p))) return 0;
   return (size_t)(p.K * p.N) * sizeof(uint16_t);
@@ -145,6 +159,10 @@ size_t DqMatMulCounters(const DqMatMulParams &p) {
 bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes, unsigned *counters,
                     size_t n_counters, hipStream_t stream) {
   if (p.M == 0 || p.N == 0) return true;
+  if (GemvQ4TiledEligible(p)) {
+    LaunchGemvQ4Tiled(p, stream);
+    return true;
+  }
   if (GemvQ4Eligible(p)) {
     if (scratch_bytes < GemvQ4ScratchBytes(p) || n_counters < GemvQ4Counters(p)) return false;
     LaunchGemvQ4(p, scratch, counters, stream);

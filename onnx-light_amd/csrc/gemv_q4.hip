@@ -44,7 +44,8 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;          // k rows per MFMA
-constexpr int kMaxChunks = 4;       // chunks per wave (all loads in flight at once)
+constexpr int kMaxChunks = 4;       // chunks per wave
+constexpr int kDepth = 4;           // chunks whose loads are in flight ahead of use
 constexpr int kTargetGroups = 256;  // workgroups wanted: about one per CU
 
 // Strip geometry for CPL columns per lane.
@@ -150,8 +151,8 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
   const __amdgpu_buffer_rsrc_t rsZ = Rsrc(p.zp, HAS_ZP ? (MODE == 0 ? 1 : (s_rows * p.N) >> 1) : 0);
   const __amdgpu_buffer_rsrc_t rsA = Rsrc(p.A, (int64_t)p.M * p.K * 2);
 
-  // ---- issue every load of this wave's K range (branch-free: out-of-range
-  // lanes and chunks read from an offset past the buffer, which returns 0) ----
+  // ---- loads of this wave's K range (branch-free: out-of-range lanes and
+  // chunks read from an offset past the buffer, which returns 0) ----
   uint32_t wq[kMaxChunks][8][kH];
   v4i sc_raw[kMaxChunks][kH];
   uint32_t zp_raw[kMaxChunks][kH];
@@ -187,11 +188,11 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
   // Chunks past this wave's range (c >= nch) read zero weights, scales and
   // activations, so they add exactly 0 and need no branch: a branch would let
   // the compiler sink chunk 0's loads behind the others, and the first MFMA
-  // would then wait for every load of the wave.  Each chunk's loads are
-  // issued before the next chunk's, in the order the chunks are consumed.
+  // would then wait for every load of the wave.  The loads of chunk c are
+  // issued kDepth chunks ahead of its use, in the order the chunks are
+  // consumed.
   const unsigned w_lane = col_ok ? (unsigned)(8 * g * row_bytes + (n0 >> 1)) : kOob;
-#pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
+  auto issue = [&](int c) __attribute__((always_inline)) {
     const bool live = c < nch;  // wave-uniform
     const int cc = live ? c_begin + c : 0;
     const int k0 = cc * kChunk + 8 * g;  // first of this lane's 8 k rows
@@ -219,8 +220,7 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
     act[c] = __builtin_bit_cast(
         v8h, __builtin_amdgcn_raw_buffer_load_b128(
                  rsA, (live && li < p.M) ? (unsigned)(((int64_t)li * p.K + k0) * 2) : kOob, 0, 0));
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  };
 
   v4f acc[CPL];
 #pragma unroll
@@ -228,51 +228,59 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
 
   const uint32_t mask = 0x000f000fu, magic = 0x64006400u;
   const uint32_t flip = SIGNED ? 0x88888888u : 0u;  // signed nibble s -> s + 8
+  auto compute = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    {
+    for (int h = 0; h < kH; ++h) {
+      // Columns 8h + e of the lane: scale pair (s_e, s_e) and bias pair
+      // (1024 + zb_e) twice, zb = zero point (+ 8 for INT4, matching the
+      // weight's own offset), so that (0x6400 | u) - bias = x - zp exactly.
+      uint32_t sc2[8], bias2[8];
 #pragma unroll
-      for (int h = 0; h < kH; ++h) {
-        // Columns 8h + e of the lane: scale pair (s_e, s_e) and bias pair
-        // (1024 + zb_e) twice, zb = zero point (+ 8 for INT4, matching the
-        // weight's own offset), so that (0x6400 | u) - bias = x - zp exactly.
-        uint32_t sc2[8], bias2[8];
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t word = (uint32_t)sc_raw[c][h][e >> 1];
+        sc2[e] = __builtin_amdgcn_perm(word, word, (e & 1) ? 0x03020302u : 0x01000100u);
+      }
+      if (HAS_ZP) {
+        const uint32_t z = zp_raw[c][h] ^ flip;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t word = (uint32_t)sc_raw[c][h][e >> 1];
-          sc2[e] = __builtin_amdgcn_perm(word, word, (e & 1) ? 0x03020302u : 0x01000100u);
-        }
-        if (HAS_ZP) {
-          const uint32_t z = zp_raw[c][h] ^ flip;
+        for (int b = 0; b < 4; ++b)
+          DecodeBytePair(z, z, ByteSel(b), mask, magic, bias2[2 * b], bias2[2 * b + 1]);
+      } else {
 #pragma unroll
-          for (int b = 0; b < 4; ++b)
-            DecodeBytePair(z, z, ByteSel(b), mask, magic, bias2[2 * b], bias2[2 * b + 1]);
-        } else {
+        for (int e = 0; e < 8; ++e) bias2[e] = SIGNED ? 0x64086408u : 0x64006400u;  // 1032 / 1024
+      }
+      uint32_t wk[8][4];  // [column][row pair]: fp16 (1024 + u) at rows 2p, 2p+1
 #pragma unroll
-          for (int e = 0; e < 8; ++e) bias2[e] = SIGNED ? 0x64086408u : 0x64006400u;  // 1032 / 1024
-        }
-        uint32_t wk[8][4];  // [column][row pair]: fp16 (1024 + u) at rows 2p, 2p+1
+      for (int pr = 0; pr < 4; ++pr) {
+        const uint32_t x0 = wq[c][2 * pr][h] ^ flip, x1 = wq[c][2 * pr + 1][h] ^ flip;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          DecodeBytePair(x0, x1, ByteSel(b), mask, magic, wk[2 * b][pr], wk[2 * b + 1][pr]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v8h wop;
 #pragma unroll
         for (int pr = 0; pr < 4; ++pr) {
-          const uint32_t x0 = wq[c][2 * pr][h] ^ flip, x1 = wq[c][2 * pr + 1][h] ^ flip;
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            DecodeBytePair(x0, x1, ByteSel(b), mask, magic, wk[2 * b][pr], wk[2 * b + 1][pr]);
+          const v2h q = (__builtin_bit_cast(v2h, wk[e][pr]) - __builtin_bit_cast(v2h, bias2[e])) *
+                        __builtin_bit_cast(v2h, sc2[e]);
+          wop[2 * pr] = q.x;
+          wop[2 * pr + 1] = q.y;
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          v8h wop;
-#pragma unroll
-          for (int pr = 0; pr < 4; ++pr) {
-            const v2h q = (__builtin_bit_cast(v2h, wk[e][pr]) - __builtin_bit_cast(v2h, bias2[e])) *
-                          __builtin_bit_cast(v2h, sc2[e]);
-            wop[2 * pr] = q.x;
-            wop[2 * pr + 1] = q.y;
-          }
-          acc[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, act[c], acc[8 * h + e], 0, 0, 0);
-        }
+        acc[8 * h + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, act[c], acc[8 * h + e], 0, 0, 0);
       }
     }
+  };
+
+#pragma unroll
+  for (int c = 0; c < kDepth; ++c) {
+    issue(c);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    compute(c);
+    if (c + kDepth < kMaxChunks) issue(c + kDepth);
     // chunk by chunk: decode work of a later chunk must not pull its data
     // waits into this one
     __builtin_amdgcn_sched_barrier(0);
@@ -389,7 +397,7 @@ int Slices(const DqMatMulParams &p) {
 
 bool GemvQ4Eligible(const DqMatMulParams &p) {
   const bool four = p.w_dtype == kInt4 || p.w_dtype == kUint4;
-  return four && p.M >= 1 && p.M <= 16 && !p.a_bf16 && p.scale_f16 && p.deq_round_f16 &&
+  return four && !p.w_tiled && p.M >= 1 && p.M <= 16 && !p.a_bf16 && p.scale_f16 && p.deq_round_f16 &&
          p.cast_round == 0 && p.K % kChunk == 0 && p.N % 8 == 0 &&
          p.K * p.N / 2 < (int64_t(1) << 31) - 64 && p.M * p.K * 2 < (int64_t(1) << 31) - 64 &&
          (p.mode != 2 || (p.block % 8 == 0)) && reinterpret_cast<uintptr_t>(p.A) % 16 == 0 &&

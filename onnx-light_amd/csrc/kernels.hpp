@@ -111,7 +111,24 @@ struct DqMatMulParams {
   //   cast_round: 16 = to BFLOAT16, 10 = to FLOAT16, 0 = none
   int deq_round_f16;
   int cast_round;
+  // W is in the tiled 4-bit layout written by LaunchTileInt4 (INT4 / UINT4
+  // only) instead of the ONNX row-major packing.
+  int w_tiled;
 };
+
+// ---------------------------------------------------------------------------
+// Tiled 4-bit weight layout (a session-time preparation of a constant
+// INT4 / UINT4 weight x [K, N]):
+//   16-column tiles t (N padded to a multiple of 16), each holding K padded to
+//   a multiple of 128 rows as 128-row groups of 1 KiB; in a group, 16-byte
+//   lane l = 16 * g + i holds four dwords c = 0..3, dword c = column 16t + i,
+//   rows 128q + 32c + 8g + (0..7).  Row r0 + j sits at bits 4 * (j / 2)
+//   (j even) or 16 + 4 * (j / 2) (j odd); values are offset binary
+//   (INT4 q -> q + 8, UINT4 unchanged); padding rows and columns hold the
+//   offset-binary zero.
+int64_t TiledInt4Bytes(int64_t K, int64_t N);
+void LaunchTileInt4(const uint8_t *x, int64_t K, int64_t N, int is_signed, uint32_t *out,
+                    hipStream_t stream);
 
 // Returns false when the shape/dtype combination has no GPU kernel.
 bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes,
