@@ -11,9 +11,11 @@
 //  - a workgroup owns T adjacent tiles over all of K (no split over
 //    workgroups, no partial sums in memory); T is chosen so that the strips
 //    spread over about 256 workgroups, one per CU;
-//  - its 8 waves take consecutive 128-row groups and each load instruction
-//    reads 1 KiB of contiguous weight bytes (a 16-byte lane = 4 chunks of 8 k
-//    rows of one column);
+//  - its 4 waves (one per SIMD) take consecutive 128-row groups, keeping two
+//    groups' loads in flight, and each load instruction reads 1 KiB of
+//    contiguous weight bytes (a 16-byte lane = 4 chunks of 8 k rows of one
+//    column).  The decode is VALU-bound, and two waves sharing a SIMD left it
+//    idle while both waited for data;
 //  - a lane's dword already holds 8 consecutive k rows of one column with the
 //    nibbles of rows 2j and 2j+1 at bits 4j and 16+4j, so one AND-OR (plus a
 //    shift) yields the fp16 pair 0x6400 | u of two rows: the A operand of
@@ -22,7 +24,7 @@
 //    (0x6400 | u) - (1024 + offset + zp) is the exact integer x - zp, and one
 //    packed fp16 multiply by the scale rounds fp16(float(x - zp) * scale)
 //    (the fp32 product of a 5-bit integer and an fp16 scale is exact);
-//  - the 8 waves' fp32 partial sums are reduced through LDS in a fixed order
+//  - the waves' fp32 partial sums are reduced through LDS in a fixed order
 //    and stored as fp16 (round to nearest even).
 #include <algorithm>
 #include <type_traits>
@@ -39,7 +41,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;             // one wave per SIMD: no two waves of a CU compete for its VALU
 constexpr int kThreads = 64 * kWaves;
 constexpr int kGroupRows = 128;      // k rows per 1 KiB group of a tile
 constexpr int kGroupBytes = 1024;
