@@ -41,6 +41,8 @@
 // LDS and writes them back with 16-byte row-contiguous stores.
 #pragma once
 
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace onnxl_amd {
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // tell a read of one stage from a direct load into another.
   __shared__ __align__(16) char sa0[kAStage], sa1[kAStage], sa2[kAStage];
   __shared__ __align__(16) char sb0[kBStage], sb1[kBStage], sb2[kBStage];
-  __shared__ int32_t zsum[ZP ? 2 * (kBM + kBN) : 1];
+  __shared__ int32_t zsum[ZP ? (kThreads / 64) * 2 * kWN : 1];  // per wave: CB and beta of its columns
   // stage index -> array (indices are compile-time constants after unrolling)
   auto SA = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sa0 : (s == 1 ? sa1 : sa2); };
   auto SB = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
@@ -477,57 +479,96 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     mma((r3 + 1) % 3, 1, 0, 4);
   };
 
-  issue(0, 0, 2);
-  issue(1, 1, 2);
-  issue(2, 2, 2);
-  RingBarrier<2 * L>();
-  read(0, sa0, sb0, 0);
-  read(1, sa0, sb0, 1);
-  decode(0, 0, true);
-  int t = 0;
-  for (; t + 3 <= nfull; t += 3) {  // 12 sub-steps: s % 3 and the stages repeat
-    step(t, 0, 0, 1);
-    step(t + 1, 1, 1, 2);
-    step(t + 2, 2, 2, 0);
-  }
-  if (t < nfull) step(t, 0, 0, 1);
-  if (t + 1 < nfull) step(t + 1, 1, 1, 2);
-  if (half) {
-    const int r3 = nfull % 3;  // (4 * nfull) % 3
-    if (r3 == 0) half_step(0);
-    else if (r3 == 1) half_step(1);
-    else half_step(2);
-  }
-  // drain the look-ahead (out-of-range) loads before the LDS is reused
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-
-  // ---- zero-point terms (kI8 with zero points): per-row RA and alpha,
-  // per-column CB and beta, exchanged through LDS ----
-  if constexpr (KIND == kI8 && ZP) {
-    int32_t *z_ra = zsum, *z_al = zsum + kBM, *z_cb = zsum + 2 * kBM, *z_be = zsum + 2 * kBM + kBN;
+  // Zero points of this lane's rows (32i + lr) and columns (32j + lr).
+  uint32_t za[4] = {0, 0, 0, 0}, zb[4] = {0, 0, 0, 0};  // raw zero-point bytes
+  auto load_zp = [&]() __attribute__((always_inline)) {
+    if constexpr (KIND == kI8 && ZP) {
+      const __amdgpu_buffer_rsrc_t rsZa =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.a_zp), (short)0, (int)(p.a_zp ? M : 0), kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rsZb =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.b_zp), (short)0, (int)(p.b_zp ? N : 0), kRsrcWord3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int v = rsum[i] + __shfl_xor(rsum[i], 32);
-      const int r = wm * 128 + i * 32 + lr;
-      if (lg == 0 && wn == 0) {
-        const int64_t row = row0 + r;
-        z_ra[r] = v;
-        z_al[r] = (p.a_zp && row < M) ? (p.a_u8 ? 128 - (int)p.a_zp[row] : -(int)(int8_t)p.a_zp[row])
-                                      : p.alpha_scalar;
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = row0 + wm * 128 + i * 32 + lr;
+        za[i] = __builtin_amdgcn_raw_buffer_load_b8(rsZa, row < M ? (unsigned)row : kOob, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < WB; ++j) {
+        const int64_t col = col0 + wn * kWN + j * 32 + lr;
+        zb[j] = __builtin_amdgcn_raw_buffer_load_b8(rsZb, col < N ? (unsigned)col : kOob, 0, 0);
       }
     }
+  };
+
+  // A single half step (K <= kKStep / 2, e.g. attention scores over a 64-wide
+  // head) needs one stage and no look-ahead: it and the zero points are
+  // loaded together, and each 32-row block's MFMAs come right before its
+  // epilogue, so the output stores start after the first block.
+  const bool block_major = nfull == 0;  // then half is set (K > 0)
+  if (block_major) {
+    issue(0, 0, 2);
+    load_zp();
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read(0, sa0, sb0, 0);
+    read(1, sa0, sb0, 1);
+    decode(0, 0, true);
+    decode(1, 1, true);
+  } else {
+    issue(0, 0, 2);
+    issue(1, 1, 2);
+    issue(2, 2, 2);
+    RingBarrier<2 * L>();
+    read(0, sa0, sb0, 0);
+    read(1, sa0, sb0, 1);
+    decode(0, 0, true);
+    int t = 0;
+    for (; t + 3 <= nfull; t += 3) {  // 12 sub-steps: s % 3 and the stages repeat
+      step(t, 0, 0, 1);
+      step(t + 1, 1, 1, 2);
+      step(t + 2, 2, 2, 0);
+    }
+    if (t < nfull) step(t, 0, 0, 1);
+    if (t + 1 < nfull) step(t + 1, 1, 1, 2);
+    if (half) {
+      const int r3 = nfull % 3;  // (4 * nfull) % 3
+      if (r3 == 0) half_step(0);
+      else if (r3 == 1) half_step(1);
+      else half_step(2);
+    }
+    // the zero points load after the last hand-counted wait (the K loop
+    // keeps every register busy); then drain the look-ahead (out-of-range)
+    // loads before the LDS is reused
+    load_zp();
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  // ---- zero-point terms (kI8 with zero points) ----
+  // A wave holds the full K range of its 128 rows and kWN columns, so the
+  // terms never cross waves: RA of row 32i + lr is rsum[i] plus its other lane
+  // half, alpha is in zrow; CB and beta of the wave's columns go through the
+  // wave's own LDS area to the lanes that store those columns.  Per element
+  // Y = sum a'b' + beta_j RA_i + alpha_i Q_j with Q_j = CB_j + K beta_j
+  // (mod 2^32); below K = 21845 every factor fits 24 signed bits, and the
+  // full-rate 24-bit multiplies give the same low 32 bits.
+  const bool mul24 = K < 21845;
+  int32_t *zc = zsum + (KIND == kI8 && ZP ? wave * 2 * kWN : 0);
+  int zrow[4] = {0, 0, 0, 0};
+  if constexpr (KIND == kI8 && ZP) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      zrow[i] = p.a_zp ? (p.a_u8 ? 128 - (int)za[i] : -(int)(int8_t)za[i]) : p.alpha_scalar;
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
       const int v = csum[j] + __shfl_xor(csum[j], 32);
-      const int c = wn * kWN + j * 32 + lr;
-      if (lg == 0 && wm == 0) {
-        const int64_t col = col0 + c;
-        z_cb[c] = v;
-        z_be[c] = (p.b_zp && col < N) ? (p.b_u8 ? 128 - (int)p.b_zp[col] : -(int)(int8_t)p.b_zp[col])
-                                      : p.beta_scalar;
+      if (lg == 0) {
+        const int be = p.b_zp ? (p.b_u8 ? 128 - (int)zb[j] : -(int)(int8_t)zb[j]) : p.beta_scalar;
+        zc[j * 32 + lr] = (int)((unsigned)v + (unsigned)K * (unsigned)be);  // CB + K beta (mod 2^32)
+        zc[kWN + j * 32 + lr] = be;
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---- epilogue ----
@@ -538,13 +579,12 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // (row pitch padded by 16 bytes) and writes whole 16-byte row pieces.
   constexpr int kPitch = kWN * kOsz + 16;
   char *stg = SA(wave >> 1) + (wave & 1) * 16384;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = wm * 128 + i * 32 + lr;  // row within the workgroup tile
+  // Epilogue of 32-row block i (use24: the 24-bit zero-point products).
+  auto epi = [&](int i, auto use24) __attribute__((always_inline)) {
     int32_t ra_r = 0, al_r = 0;
     if constexpr (KIND == kI8 && ZP) {
-      ra_r = zsum[r];
-      al_r = zsum[kBM + r];
+      ra_r = rsum[i] + __shfl_xor(rsum[i], 32);
+      al_r = zrow[i];
     }
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
@@ -559,10 +599,11 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
             v[e] = (unsigned)acc[i][j][4 * g + e];
             if constexpr (ZP) {
               // Y = sum a'b' + beta_j RA_i + alpha_i CB_j + K alpha_i beta_j (mod 2^32)
-              const int c = wn * kWN + cl + e;
-              const unsigned be = (unsigned)zsum[2 * kBM + kBN + c];
-              v[e] += be * (unsigned)ra_r + (unsigned)al_r * (unsigned)zsum[2 * kBM + c] +
-                      (unsigned)K * (unsigned)al_r * be;
+              const int be = zc[kWN + cl + e], q = zc[cl + e];
+              if constexpr (decltype(use24)::value)
+                v[e] += (unsigned)(__mul24(be, ra_r) + __mul24(al_r, q));
+              else
+                v[e] += (unsigned)be * (unsigned)ra_r + (unsigned)al_r * (unsigned)q;
             }
           }
           if constexpr (OUT == kOutI32) {
@@ -619,6 +660,15 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (block_major) {
+      mma(0, 0, i, i + 1);
+      mma(1, 1, i, i + 1);
+    }
+    if (!(KIND == kI8 && ZP) || mul24) epi(i, std::true_type{});
+    else epi(i, std::false_type{});
   }
 }
 
