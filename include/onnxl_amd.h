@@ -134,7 +134,12 @@ int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, v
  * BFLOAT16 [..., M, K]; the dequantized weight is rounded exactly as the
  * unfused reference chain rounds it (to x_scale's dtype, then to cast_to), so
  * only the fp32 summation order differs from the chain of the three kernels
- * above.  cast_to = 0 means no Cast node (the DequantizeLinear output dtype
+ * above.  One exception: FLOAT8E4M3FN weights with FLOAT scales and
+ * cast_to = BFLOAT16 on the matrix-core path (per-tensor or per-column scale,
+ * no zero point, K % 32 == 0, N % 16 == 0) multiply the fp32
+ * sums by the scale instead of rounding each scaled weight to bfloat16 (at
+ * most 2^-9 relative per weight; with an infinite scale a column the chain
+ * turns to NaN through 0 * inf is +-inf here).  cast_to = 0 means no Cast node (the DequantizeLinear output dtype
  * must then equal A's dtype).  Y dtype = A dtype.  x: INT4, UINT4, INT8,
  * UINT8, FLOAT8E4M3FN; per-tensor, per-axis (axis 1) or blocked along K
  * (axis 0) scales.  No single reference kernel: it computes the chain

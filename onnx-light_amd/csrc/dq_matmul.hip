@@ -5,7 +5,8 @@
 //    layout of a prepared weight (gemv_q4_tiled.hip).
 //  - float8e4m3fn weights, FLOAT scales per column or per tensor, Cast to
 //    BFLOAT16, bf16 activations (prefill): the pipelined MFMA core with the
-//    weight decoded and scaled as it is read from LDS (mfma_gemm.hpp, kBf16F8).
+//    weight decoded exactly to bf16 as it is read from LDS and the scale
+//    applied to the fp32 sums (mfma_gemm.hpp, kBf16F8).
 //  - anything else the C ABI accepts: the weight is dequantised into scratch
 //    with the chain's exact rounding, then multiplied by the 16-bit MatMul.
 #include <algorithm>

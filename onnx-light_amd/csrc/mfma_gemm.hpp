@@ -52,6 +52,7 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -70,8 +71,12 @@ constexpr unsigned kFlip = 0x80808080u;
 // Operand kinds.
 //  kI8:     int8 / uint8 x int8 / uint8 -> int32 (v_mfma_i32_32x32x32_i8)
 //  kBf16F8: bf16 A x float8e4m3fn B with a per-column (or single) fp32 scale;
-//           B is decoded to bf16 as round_bf16(decode(b) * scale[n]), the
-//           rounding of the DequantizeLinear(FLOAT) -> Cast(BFLOAT16) chain.
+//           B values enter the MFMA exactly (every e4m3fn value is a bf16
+//           value: the high half of its fp32 decode) and the column's scale
+//           multiplies the fp32 sum in the epilogue, Y = s_n * sum_k a q.
+//           The DequantizeLinear(FLOAT) -> Cast(BFLOAT16) chain instead rounds
+//           each s_n * q to bf16 first; the two differ by at most half a bf16
+//           ulp of each product.
 //  kH16:    fp16 x fp16 or bf16 x bf16 -> fp32 accumulate.
 enum Kind : int { kI8 = 0, kBf16F8 = 1, kH16 = 2 };
 
@@ -112,6 +117,16 @@ __device__ __forceinline__ int64_t MinI64(int64_t a, int64_t b) { return a < b ?
 __device__ __forceinline__ unsigned PackBf16(float lo, float hi) {
   unsigned r;
   asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+  return r;
+}
+
+// Two floats that are bf16 values (fp8 decodes) -> packed bf16 pair, lo in
+// bits 0-15: their high halves, exact for such values.  Inline asm: the
+// compiler folds __builtin_amdgcn_perm of the two halves of one register pair
+// into a perm of the low half with itself.
+__device__ __forceinline__ unsigned HighHalves(v2f f) {
+  unsigned r;
+  asm("v_perm_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f.y), "v"(f.x), "s"(0x07060302u));
   return r;
 }
 
@@ -164,6 +179,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   __shared__ __align__(16) char sa0[kAStage], sa1[kAStage], sa2[kAStage];
   __shared__ __align__(16) char sb0[kBStage], sb1[kBStage], sb2[kBStage];
   __shared__ int32_t zsum[ZP ? (kThreads / 64) * 2 * kWN : 1];  // per wave: CB and beta of its columns
+  __shared__ __align__(16) float cscale[KIND == kBf16F8 ? (kThreads / 64) * kWN : 4];  // per wave: column scales
   // stage index -> array (indices are compile-time constants after unrolling)
   auto SA = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sa0 : (s == 1 ? sa1 : sa2); };
   auto SB = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
@@ -359,13 +375,12 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
             csum[j] = __builtin_amdgcn_sdot4(bop[bbuf][j][e], 0x01010101, csum[j], false);
         }
       } else if constexpr (KIND == kBf16F8) {
+        // exact fp8 -> bf16: the high halves of the fp32 decode
         const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, false);
         const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, true);
         const v2f f2 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, false);
         const v2f f3 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, true);
-        const float sc = bscale[j];
-        bop[bbuf][j] = v4i{(int)PackBf16(f0.x * sc, f0.y * sc), (int)PackBf16(f1.x * sc, f1.y * sc),
-                           (int)PackBf16(f2.x * sc, f2.y * sc), (int)PackBf16(f3.x * sc, f3.y * sc)};
+        bop[bbuf][j] = v4i{(int)HighHalves(f0), (int)HighHalves(f1), (int)HighHalves(f2), (int)HighHalves(f3)};
       } else {
         bop[bbuf][j] = rb[rbuf][j];
       }
@@ -404,7 +419,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // go first, then each MFMA is followed by its share of the next sub-step's
   // decode, so the VALU work issues while the matrix pipe is busy.
   constexpr int kReads = 4 + WB * (KIND == kBf16F8 ? 1 : 2);
-  constexpr int kDecodeValu = KIND == kBf16F8 ? 16 * WB : (KIND == kI8 ? 12 * WB : 0);
+  constexpr int kDecodeValu = KIND == kBf16F8 ? 8 * WB : (KIND == kI8 ? 12 * WB : 0);
   auto order = [&]() __attribute__((always_inline)) {
     constexpr int kNM = 4 * WB;  // MFMAs of a plain sub-step
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
@@ -571,6 +586,17 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
+  // kBf16F8: the scales of the wave's columns, to the lanes that store them
+  float *csc = cscale + (KIND == kBf16F8 ? wave * kWN : 0);
+  if constexpr (KIND == kBf16F8) {
+#pragma unroll
+    for (int j = 0; j < WB; ++j)
+      if (lg == 0) csc[j * 32 + lr] = bscale[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
   // ---- epilogue ----
   // The MFMAs compute the transposed block (B fragment as the row operand),
   // so lane (lr, lg) of block (i, j) holds output row 32i + lr and, in
@@ -619,7 +645,12 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
             *reinterpret_cast<unsigned *>(dst) = packed;
           }
         } else {
-          const Acc &a = acc[i][j];
+          Acc a = acc[i][j];
+          if constexpr (KIND == kBf16F8) {  // the columns' dequantization scales
+            const v4f sc4 = *reinterpret_cast<const v4f *>(csc + cl);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[4 * g + e] *= sc4[e];
+          }
           if constexpr (OUT == kOutBf16) {
             *reinterpret_cast<v2i *>(dst) = v2i{(int)PackBf16(a[4 * g], a[4 * g + 1]),
                                                 (int)PackBf16(a[4 * g + 2], a[4 * g + 3])};

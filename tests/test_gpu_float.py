@@ -4,8 +4,10 @@ known answers:
 - DequantizeLinear and the FLOAT -> FLOAT16 / BFLOAT16 Cast: bit-exact.
 - FLOAT16 / BFLOAT16 MatMul and the fused DequantizeLinear -> [Cast] ->
   MatMul: the dequantised weights are rounded exactly as the unfused chain
-  rounds them, so only the fp32 summation order differs from the oracle.  The
-  stated tolerance is
+  rounds them, so only the fp32 summation order differs from the oracle;
+  the fp8 matrix-core path instead scales the fp32 sums, skipping each
+  weight's bf16 rounding (<= 2^-9 relative), which the magnitude term below
+  covers.  The stated tolerance is
       |got - ref| <= 1e-2 * |ref| + u * sum_k |a_mk * w_kn|
   with u the unit roundoff of the output type (2^-11 FLOAT16, 2^-8 BFLOAT16):
   relative 1e-2 as the north star states, plus the magnitude term that a
