@@ -14,11 +14,18 @@
 //  - Both operands go global -> LDS with direct buffer loads (16 bytes per
 //    lane, 1 KB per wave instruction, no registers held) into a 3-stage ring:
 //    while step t is multiplied, steps t+1 and t+2 are in flight.
-//  - A stage [256 rows][128 B] is stored as 1 KB blocks of 8 rows,
-//    [row/8][16-byte chunk c ^ ((row/8) & 1)][row%8]: one direct load moves 8
-//    whole 128-byte rows (full cache lines), and the 16 lanes of a fragment
-//    read (ds_read_b128, 16 consecutive rows, one chunk) cover 256 bytes
-//    spread over all banks thanks to the chunk XOR.
+//  - A stage [256 rows][128 B] is row-major with the 16-byte chunks of row r
+//    permuted, chunk c at position c ^ h(r), h(r) = (r % 8) ^ ((r / 8) % 2).
+//    A direct load puts lane i's
+//    16 bytes at position i of its 1 KB, so lanes 8j .. 8j+7 fetch the eight
+//    chunks of one row: every group of eight lanes reads one whole 128-byte
+//    line (8 rows per load).  A layout with consecutive lanes on consecutive
+//    rows (one load = the same 8 rows, column-wise) runs the address unit
+//    about four times slower per byte and made the loads, not the MFMAs, the
+//    bound.  A fragment read (ds_read_b128) has lanes on consecutive rows, one
+//    chunk: any 8 consecutive rows hold it at 8 different positions, and any
+//    16 at 16 different (row parity, position) pairs, so neither 8 lanes over
+//    32 banks nor 16 lanes over 64 banks conflict.
 //  - B stage [k rows][128 columns] is stored row-major with its 16-byte chunks
 //    XOR-swizzled by the row index.  The MFMA wants consecutive k of one column
 //    per lane; the transposing LDS reads (ds_read_b64_tr_b8 / _b16) deliver
@@ -30,10 +37,9 @@
 //    receives column c0 + i at k0, k0+1, ...
 //
 // Schedule (per K step of 4 sub-steps): the fragments of sub-step s are read
-// from LDS two sub-steps ahead (three register sets) and its B operand is
-// decoded (fp8 -> bf16 with scale, or the int8 sign flip) under the MFMAs of
-// sub-step s - 1, so neither LDS latency nor decode VALU work stalls the
-// matrix pipe.  The single barrier per step sits inside sub-step 2, after
+// from LDS two sub-steps ahead (three register sets); the fp8 B operand is
+// decoded to bf16 under the MFMAs of sub-step s - 1, so neither LDS latency
+// nor decode VALU work stalls the matrix pipe.  The single barrier per step sits inside sub-step 2, after
 // half of its MFMAs are issued.  It waits only for the oldest ring stage
 // (s_waitcnt vmcnt(L), L = direct loads per step), never for all loads.
 //
@@ -185,7 +191,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   auto SB = [&](int s) __attribute__((always_inline)) -> char * { return s == 0 ? sb0 : (s == 1 ? sb1 : sb2); };
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // the wave index as a scalar: the LDS destinations of the direct loads (M0)
+  // then need no per-load readfirstlane
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lg = lane >> 5;
   const int64_t M = p.M, N = p.N, K = p.K;
@@ -218,19 +226,22 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(K * NB), kRsrcWord3);
+  // look-ahead loads past the last K step go through empty descriptors (every
+  // access out of range): a scalar select instead of a per-lane one
+  const __amdgpu_buffer_rsrc_t rsA0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, 0, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsB0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsY = __builtin_amdgcn_make_buffer_rsrc(
       static_cast<char *>(p.Y) + bt * M * N * kOsz, (short)0, (int)(M * N * kOsz), kRsrcWord3);
   const int nfull = (int)(K / T::kKStep);                  // full K steps
   const bool half = K % T::kKStep != 0;                     // K % kKStep == kKStep / 2
   const int nk = nfull + (half ? 1 : 0);                    // K steps to load
-  const int n_sub = 4 * nfull + (half ? 2 : 0);             // sub-steps to multiply
 
   // ---- direct-load offsets (K step 0) ----
   unsigned a_g[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const int64_t row = row0 + 8 * (8 * wave + q) + (lane & 7);  // 8-row block 8 * wave + q
-    a_g[q] = row < M ? (unsigned)(row * KA + 16 * ((lane >> 3) ^ (q & 1))) : kOob;
+    const int64_t row = row0 + 8 * (8 * wave + q) + (lane >> 3);  // 8-row block 8 * wave + q
+    a_g[q] = row < M ? (unsigned)(row * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (q & 1))) : kOob;
   }
   unsigned b_g[4];  // LB <= 4 (a fixed bound: a template-dependent size here
                     // makes the host compiler drop the kernel stub)
@@ -251,14 +262,13 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     }
   }
   // ---- LDS fragment offsets (sub-step 0; sub-step kk adds kk * const) ----
-  // Block i of a wave's A fragment sits exactly 4096 bytes after block i-1
-  // (4 row blocks of 8), so one base register per stage serves all four
-  // blocks and the four sub-steps through the 16-bit DS offset field.
-  int a_rd0;
-  {
-    const int r = wm * 128 + lr;
-    a_rd0 = (r >> 3) * 1024 + 128 * (lg ^ ((r >> 3) & 1)) + (r & 7) * 16;
-  }
+  // Sub-step kk reads chunk 2 kk + lg of row wm * 128 + 32 i + lr; block i
+  // sits exactly 4096 bytes after block i-1, so one base per sub-step serves
+  // all four blocks through the DS offset field.
+  int a_rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    a_rd[kk] = (wm * 128 + lr) * 128 + 16 * ((2 * kk + lg) ^ (lr & 7) ^ ((lr >> 3) & 1));
   const int s16 = lane & 15, g16 = lane >> 4;
   // One base per column block j; the second transposing read of a fragment
   // (h = 1) is 8 rows (int8) or 4 rows (16-bit) further, the same swizzle.
@@ -299,33 +309,32 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int bflip = (KIND == kI8 && BU8) ? (int)kFlip : 0;
 
   // Direct loads of K step `step` into ring stage `stage`: the L loads of a
-  // step, numbered A pieces 0..7 then B pieces, in halves (part 0 / 1) or
-  // all at once (part 2).
+  // step, numbered A pieces 0..7 then B pieces, in quarters (parts 0..3) or
+  // all at once (part 4).
   auto issue = [&](int step, int stage, int part) __attribute__((always_inline)) {
     const bool live = step < nk;
     const unsigned ka = (unsigned)step * kStepBytes;
     const unsigned kb = (unsigned)((int64_t)step * T::kBRows * NB);
     char *sa = SA(stage);
     char *sb = SB(stage);
-    const int lo = part == 1 ? L / 2 : 0, hi = part == 0 ? L / 2 : L;
+    const __amdgpu_buffer_rsrc_t rsa = live ? rsA : rsA0, rsb = live ? rsB : rsB0;
+    const int lo = part == 4 ? 0 : part * L / 4, hi = part == 4 ? L : (part + 1) * L / 4;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       if (q >= lo && q < hi)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rsA, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16,
-            live ? a_g[q] + ka : kOob, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16, a_g[q] + ka, 0, 0, 0);
 #pragma unroll
     for (int q = 0; q < LB; ++q)
       if (8 + q >= lo && 8 + q < hi)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16,
-                                                 live ? b_g[q] + kb : kOob, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16, b_g[q] + kb, 0, 0, 0);
   };
 
   // ---- fragments ----
-  // Sub-step s (4 per K step) multiplies A fragments ra[s % 3] by the decoded
-  // B operands bop[s % 2].  Its LDS reads were issued two sub-steps earlier
-  // and its B decode ran under the MFMAs of sub-step s - 1, so neither the LDS
-  // latency nor the decode VALU work stalls the matrix pipe.
+  // Sub-step s (4 per K step) multiplies A fragments ra[s % 3] by the B
+  // fragments rb[s % 3] (kBf16F8: by the decoded operands bop[s % 2]).  Its
+  // LDS reads were issued two sub-steps earlier and the fp8 decode ran under
+  // the MFMAs of sub-step s - 1, so neither the LDS latency nor the decode
+  // VALU work stalls the matrix pipe.
   v4i ra[3][4];
   v4i rb[3][WB];  // raw B: kI8 2 x tr8; kBf16F8 1 x tr8 (.xy); kH16 2 x tr16
   auto read = [&](int buf, const char *sa, const char *sb, int kk) __attribute__((always_inline)) {
@@ -348,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      ra[buf][i] = *reinterpret_cast<const v4i *>(sa + a_rd0 + i * 4096 + kk * 256);
+      ra[buf][i] = *reinterpret_cast<const v4i *>(sa + a_rd[kk] + i * 4096);
   };
 
   Acc acc[4][WB];
@@ -361,28 +370,32 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
   for (int j = 0; j < WB; ++j) csum[j] = 0;
 
-  v4i bop[2][WB];  // MFMA-ready B operands
-  // `live` is false for the look-ahead decode of a sub-step past K, whose
-  // bytes must not enter the column sums.
-  auto decode = [&](int rbuf, int bbuf, bool live) __attribute__((always_inline)) {
+  // kBf16F8: the decoded B operands, two sets.  The other kinds multiply the
+  // raw fragments of the sub-step's own register set (int8: sign flip
+  // inline), so their B reads keep the full two-sub-step look-ahead.
+  v4i bop[KIND == kBf16F8 ? 2 : 1][WB];
+  auto decode = [&](int rbuf, int bbuf) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
-      if constexpr (KIND == kI8) {
-        bop[bbuf][j] = rb[rbuf][j] ^ bflip;
-        if (CB && live) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            csum[j] = __builtin_amdgcn_sdot4(bop[bbuf][j][e], 0x01010101, csum[j], false);
-        }
-      } else if constexpr (KIND == kBf16F8) {
+      if constexpr (KIND == kBf16F8) {
         // exact fp8 -> bf16: the high halves of the fp32 decode
         const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, false);
         const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, true);
         const v2f f2 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, false);
         const v2f f3 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].y, true);
         bop[bbuf][j] = v4i{(int)HighHalves(f0), (int)HighHalves(f1), (int)HighHalves(f2), (int)HighHalves(f3)};
-      } else {
-        bop[bbuf][j] = rb[rbuf][j];
+      }
+    }
+  };
+  // kI8 with zero points: this lane's partial column sums of b' over the
+  // fragments in register set `buf` (one sub-step)
+  auto colsum = [&](int buf) __attribute__((always_inline)) {
+    if constexpr (KIND == kI8 && CB) {
+#pragma unroll
+      for (int j = 0; j < WB; ++j) {
+        const v4i bv = rb[buf][j] ^ bflip;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) csum[j] = __builtin_amdgcn_sdot4(bv[e], 0x01010101, csum[j], false);
       }
     }
   };
@@ -397,18 +410,21 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
         }
 #pragma unroll
         for (int j = 0; j < WB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bop[bbuf][j], av, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(rb[abuf][j] ^ bflip, av, acc[i][j], 0, 0, 0);
       } else if constexpr (KIND == kBf16F8 || OUT == kOutBf16) {
         const v8bf av = __builtin_bit_cast(v8bf, ra[abuf][i]);
 #pragma unroll
-        for (int j = 0; j < WB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bop[bbuf][j]), av,
-                                                              acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WB; ++j) {
+          v4i bv;
+          if constexpr (KIND == kBf16F8) bv = bop[bbuf][j];
+          else bv = rb[abuf][j];
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, bv), av, acc[i][j], 0, 0, 0);
+        }
       } else {  // kH16 with FLOAT16 operands
         const v8h av = __builtin_bit_cast(v8h, ra[abuf][i]);
 #pragma unroll
         for (int j = 0; j < WB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, bop[bbuf][j]), av,
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, rb[abuf][j]), av,
                                                              acc[i][j], 0, 0, 0);
       }
     }
@@ -420,64 +436,65 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // decode, so the VALU work issues while the matrix pipe is busy.
   constexpr int kReads = 4 + WB * (KIND == kBf16F8 ? 1 : 2);
   constexpr int kDecodeValu = KIND == kBf16F8 ? 8 * WB : (KIND == kI8 ? 12 * WB : 0);
-  auto order = [&]() __attribute__((always_inline)) {
-    constexpr int kNM = 4 * WB;  // MFMAs of a plain sub-step
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
-#pragma unroll
-    for (int x = 0; x < kNM; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if constexpr (kDecodeValu > 0)
-        __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + kNM - 1) / kNM, 0);  // VALU
-    }
-  };
-  auto order_vm = [&]() __attribute__((always_inline)) {  // plain sub-step + half a refill
+  // plain sub-step with `nvm` direct loads, one after each of the first MFMAs
+  auto order_vm = [&](int nvm) __attribute__((always_inline)) {
     constexpr int kNM = 4 * WB;
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
     for (int x = 0; x < kNM; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if (x < L - L / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+      if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
       if constexpr (kDecodeValu > 0)
         __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + kNM - 1) / kNM, 0);  // VALU
     }
   };
-  auto order_refill = [&]() __attribute__((always_inline)) {
+  // second half of the barrier sub-step with `nvm` direct loads
+  auto order_refill = [&](int nvm) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
     for (int x = 0; x < 2 * WB; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, (L / 2 + 2 * WB - 1) / (2 * WB), 0);  // VMEM
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+      if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+      if (x + 2 * WB < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if constexpr (kDecodeValu > 0)
         __builtin_amdgcn_sched_group_barrier(0x002, (kDecodeValu + 2 * WB - 1) / (2 * WB), 0);  // VALU
     }
   };
+  // direct loads in refill quarter `part`
+  auto quarter = [](int part) constexpr { return (part + 1) * L / 4 - part * L / 4; };
 
   // Sub-step s = 4 t + kk of K step t (ring stage t % 3); all buffer and
   // stage indices are compile-time after unrolling.  Sub-step kk == 2 holds
   // the step's barrier: every wave has retired its reads of stage t - 1 ... t
   // (its last reads of stage t were issued in sub-step kk == 1), and step
   // t + 1 has landed, so stage t is refilled with step t + 3 and the reads of
-  // step t + 1 begin.
+  // step t + 1 begin.  The refill is spread over four sub-steps (quarters in
+  // sub-steps 2 and 3 of step t and 0 and 1 of step t + 1): issued in bursts,
+  // the direct loads back up in the address unit and stall the MFMAs behind
+  // them in each wave's instruction stream.
   auto substep = [&](int t, int kk, int sb3, int sb2, int cur, int nxt) __attribute__((always_inline)) {
     const int nb3 = (sb3 + 1) % 3, nb2 = (sb2 + 1) % 2, rb3 = (sb3 + 2) % 3;
+    const int prv = (cur + 2) % 3;  // stage of step t - 1, being refilled with step t + 2
     if (kk != 2) {
       if (kk < 2) read(rb3, SA(cur), SB(cur), kk + 2);
       else read(rb3, SA(nxt), SB(nxt), kk - 2);
       if (kk == 3) issue(t + 3, cur, 1);
-      decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
+      else issue(t + 2, prv, 2 + kk);
+      decode(nb3, nb2);
+      colsum(sb3);
       mma(sb3, sb2, 0, 4);
-      if (kk == 3) order_vm();
-      else order();
+      order_vm(kk == 3 ? quarter(1) : quarter(2 + kk));
       __builtin_amdgcn_sched_barrier(0);
     } else {
       mma(sb3, sb2, 0, 2);
       __builtin_amdgcn_sched_barrier(0);
       RingBarrier<L>();
       read(rb3, SA(nxt), SB(nxt), 0);
-      issue(t + 3, cur, 0);  // first half of the refill; the rest in sub-step 3
-      decode(nb3, nb2, 4 * t + kk + 1 < n_sub);
+      issue(t + 3, cur, 0);  // first quarter of the refill
+      decode(nb3, nb2);
+      colsum(sb3);
       mma(sb3, sb2, 2, 4);
-      order_refill();
+      order_refill(quarter(0));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -489,7 +506,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // A final half step (K % kKStep == kKStep / 2) runs 2 of the 4 sub-steps;
   // its stage was loaded whole (k past K: zero rows of B, unread bytes of A).
   auto half_step = [&](int r3) __attribute__((always_inline)) {
-    decode((r3 + 1) % 3, 1, true);
+    decode((r3 + 1) % 3, 1);
+    colsum(r3);
+    colsum((r3 + 1) % 3);
     mma(r3, 0, 0, 4);
     mma((r3 + 1) % 3, 1, 0, 4);
   };
@@ -521,21 +540,26 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // epilogue, so the output stores start after the first block.
   const bool block_major = nfull == 0;  // then half is set (K > 0)
   if (block_major) {
-    issue(0, 0, 2);
+    issue(0, 0, 4);
     load_zp();
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read(0, sa0, sb0, 0);
     read(1, sa0, sb0, 1);
-    decode(0, 0, true);
-    decode(1, 1, true);
+    decode(0, 0);
+    decode(1, 1);
+    colsum(0);  // before the zero-point exchange; the MFMAs run block by block in the epilogue
+    colsum(1);
   } else {
-    issue(0, 0, 2);
-    issue(1, 1, 2);
-    issue(2, 2, 2);
-    RingBarrier<2 * L>();
+    // steps 0 and 1 whole, the first half of step 2 (sub-steps 0 and 1 of
+    // step 0 issue the rest)
+    issue(0, 0, 4);
+    issue(1, 1, 4);
+    issue(2, 2, 0);
+    issue(2, 2, 1);
+    RingBarrier<L + 2 * L / 4>();
     read(0, sa0, sb0, 0);
     read(1, sa0, sb0, 1);
-    decode(0, 0, true);
+    decode(0, 0);
     int t = 0;
     for (; t + 3 <= nfull; t += 3) {  // 12 sub-steps: s % 3 and the stages repeat
       step(t, 0, 0, 1);
@@ -604,7 +628,12 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // Per 32-row block the wave packs those four values, stages the block in LDS
   // (row pitch padded by 16 bytes) and writes whole 16-byte row pieces.
   constexpr int kPitch = kWN * kOsz + 16;
-  char *stg = SA(wave >> 1) + (wave & 1) * 16384;
+  static_assert(32 * kPitch <= 16384 && 2 * 16384 <= kAStage, "epilogue staging: 32 rows per wave, two waves per stage");
+  // Staging areas in ring stages 1 and 2: the block-major path (one half
+  // step) loads only stage 0 and writes a block's outputs while the partner
+  // wave (same wm) may still read its fragments from stage 0; the full path
+  // has drained every stage behind a barrier.
+  char *stg = (wave >> 1 ? sa2 : sa1) + (wave & 1) * 16384;
   // Epilogue of 32-row block i (use24: the 24-bit zero-point products).
   auto epi = [&](int i, auto use24) __attribute__((always_inline)) {
     int32_t ra_r = 0, al_r = 0;
