@@ -371,13 +371,22 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   for (int j = 0; j < WB; ++j) csum[j] = 0;
 
   // kBf16F8: the decoded B operands, two sets.  The other kinds multiply the
-  // raw fragments of the sub-step's own register set (int8: sign flip
-  // inline), so their B reads keep the full two-sub-step look-ahead.
+  // fragments of the sub-step's own register set, so their B reads keep the
+  // full two-sub-step look-ahead; uint8 fragments are turned into int8
+  // (x ^ 0x80 = x - 128) in place one sub-step ahead, under the MFMAs of the
+  // sub-step before (right before their own MFMAs the flips cost 4% more
+  // cycles).
   v4i bop[KIND == kBf16F8 ? 2 : 1][WB];
   auto decode = [&](int rbuf, int bbuf) __attribute__((always_inline)) {
+    if constexpr (KIND == kI8 && AU8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ra[rbuf][i] ^= aflip;
+    }
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
-      if constexpr (KIND == kBf16F8) {
+      if constexpr (KIND == kI8 && BU8) {
+        rb[rbuf][j] ^= bflip;
+      } else if constexpr (KIND == kBf16F8) {
         // exact fp8 -> bf16: the high halves of the fp32 decode
         const v2f f0 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, false);
         const v2f f1 = __builtin_amdgcn_cvt_pk_f32_fp8(rb[rbuf][j].x, true);
@@ -393,7 +402,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     if constexpr (KIND == kI8 && CB) {
 #pragma unroll
       for (int j = 0; j < WB; ++j) {
-        const v4i bv = rb[buf][j] ^ bflip;
+        const v4i bv = rb[buf][j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) csum[j] = __builtin_amdgcn_sdot4(bv[e], 0x01010101, csum[j], false);
       }
@@ -403,14 +412,14 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
       if constexpr (KIND == kI8) {
-        const v4i av = ra[abuf][i] ^ aflip;
+        const v4i av = ra[abuf][i];
         if (RA) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) rsum[i] = __builtin_amdgcn_sdot4(av[e], 0x01010101, rsum[i], false);
         }
 #pragma unroll
         for (int j = 0; j < WB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(rb[abuf][j] ^ bflip, av, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(rb[abuf][j], av, acc[i][j], 0, 0, 0);
       } else if constexpr (KIND == kBf16F8 || OUT == kOutBf16) {
         const v8bf av = __builtin_bit_cast(v8bf, ra[abuf][i]);
 #pragma unroll
@@ -435,7 +444,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // go first, then each MFMA is followed by its share of the next sub-step's
   // decode, so the VALU work issues while the matrix pipe is busy.
   constexpr int kReads = 4 + WB * (KIND == kBf16F8 ? 1 : 2);
-  constexpr int kDecodeValu = KIND == kBf16F8 ? 8 * WB : (KIND == kI8 ? 12 * WB : 0);
+  constexpr int kDecodeValu = KIND == kBf16F8 ? 8 * WB : (KIND == kI8 ? (AU8 ? 16 : 0) + (BU8 ? 4 * WB : 0) + (CB ? 4 * WB : 0) : 0);
   // plain sub-step with `nvm` direct loads, one after each of the first MFMAs
   auto order_vm = [&](int nvm) __attribute__((always_inline)) {
     constexpr int kNM = 4 * WB;
