@@ -73,6 +73,11 @@ constexpr int kAStage = kBM * kStepBytes;  // 32 KB
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr unsigned kOob = 0x80000000u;
 constexpr unsigned kFlip = 0x80808080u;
+// Cache policy of the output stores: sc1 (device scope) writes through the
+// XCD's L2.  Plain write-back stores leave up to the whole L2 dirty at the end
+// of the kernel, and the kernel then completes only after that writeback: on
+// C5 (33.5 MB of int32 output) 12.2 us per launch against 9.7 us with sc1.
+constexpr int kStoreThrough = 16;
 
 // Operand kinds.
 //  kI8:     int8 / uint8 x int8 / uint8 -> int32 (v_mfma_i32_32x32x32_i8)
@@ -724,7 +729,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
       const bool ok = brow + rr < M && cc * (16 / kOsz) < ncol;
       __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY,
-                                             ok ? ybase + (unsigned)(rr * N * kOsz + cc * 16) : kOob, 0, 0);
+                                             ok ? ybase + (unsigned)(rr * N * kOsz + cc * 16) : kOob, 0, kStoreThrough);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
