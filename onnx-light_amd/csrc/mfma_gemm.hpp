@@ -648,6 +648,10 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // wave (same wm) may still read its fragments from stage 0; the full path
   // has drained every stage behind a barrier.
   char *stg = (wave >> 1 ? sa2 : sa1) + (wave & 1) * 16384;
+  // QLinearMatMul requantization constants (signed outputs biased by 128)
+  const float q_bias = p.y_signed ? 128.f : 0.f;
+  const float q_zy = p.zy + q_bias, q_lo = p.qmin + q_bias, q_hi = p.qmax + q_bias;
+  const unsigned q_flip = p.y_signed ? 0x80808080u : 0u;
   // Epilogue of 32-row block i (use24: the 24-bit zero-point products).
   auto epi = [&](int i, auto use24) __attribute__((always_inline)) {
     int32_t ra_r = 0, al_r = 0;
@@ -678,14 +682,17 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
           if constexpr (OUT == kOutI32) {
             *reinterpret_cast<v4i *>(dst) = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
           } else {
-            // ties-to-even rounding before the zero point, then saturation
+            // ties-to-even rounding before the zero point, then saturation.
+            // Signed outputs are biased by 128 (exact on these integer
+            // values) so one byte conversion packs both kinds; the XOR
+            // removes the bias.
             unsigned packed = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + p.zy;
-              packed |= ((unsigned)(int)__builtin_amdgcn_fmed3f(f, p.qmin, p.qmax) & 0xffu) << (8 * e);
+              const float f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + q_zy;
+              packed = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(f, q_lo, q_hi), e, packed);
             }
-            *reinterpret_cast<unsigned *>(dst) = packed;
+            *reinterpret_cast<unsigned *>(dst) = packed ^ q_flip;
           }
         } else {
           Acc a = acc[i][j];
