@@ -116,6 +116,56 @@ bool Fp8Eligible(const DqMatMulParams &p) {
          (p.mode == 0 || p.mode == 1) && p.zp == nullptr;
 }
 
+// Compute units of the current device, queried once per device.
+int64_t DeviceCUs() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The fp8 GEMM in 256 x 256 tiles, except that when those tiles leave a last,
+// partly filled round of workgroups, the trailing columns go to a second
+// launch in 256 x 128 tiles.  C4 (4096 x 14336): 896 tiles are 3.5 rounds on
+// 256 CUs; 768 tiles (12288 columns) make 3 whole rounds and the last 2048
+// columns are 256 half-size tiles, one round of half the time.
+void LaunchFp8Gemm(const mg::GemmArgs &g, hipStream_t stream) {
+  const int64_t cus = DeviceCUs();
+  const int64_t nbm = (g.M + 255) / 256, nbn = (g.N + 255) / 256;
+  if (nbm * nbn < 512) {
+    mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 2>(g, stream);
+    return;
+  }
+  int64_t nb = nbn;  // tile-columns in 256 x 256 tiles
+  if ((nbm * nbn) % cus != 0 && g.N % 256 == 0) {
+    int64_t c = nbn - 1;
+    while (c > 0 && (nbm * c) % cus != 0) --c;
+    if (c > 0 && nbm * (nbn - c) * 2 <= cus) nb = c;
+  }
+  if (nb == nbn) {
+    mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 4>(g, stream);
+    return;
+  }
+  const int64_t n0 = nb * 256;
+  mg::GemmArgs g1 = g, g2 = g;
+  g1.N = n0;
+  g1.ldb = g.N;
+  g1.ldy = g.N;
+  g2.N = g.N - n0;
+  g2.ldb = g.N;
+  g2.ldy = g.N;
+  g2.B = static_cast<const uint8_t *>(g.B) + n0;
+  g2.Y = static_cast<uint16_t *>(g.Y) + n0;
+  if (g.scale_per_col) g2.scale = static_cast<const float *>(g.scale) + n0;
+  mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 4>(g1, stream);
+  mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 2>(g2, stream);
+}
+
 mg::GemmArgs Fp8Args(const DqMatMulParams &p) {
   mg::GemmArgs g{};
   g.A = p.A;
@@ -172,10 +222,7 @@ bool LaunchDqMatMul(const DqMatMulParams &p, void *scratch, size_t scratch_bytes
   if (Fp8Eligible(p)) {
     const mg::GemmArgs g = Fp8Args(p);
     if (mg::Eligible<mg::kBf16F8>(g)) {
-      // 256 x 256 tiles when there are enough of them to fill the GPU
-      const int64_t big_tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256);
-      if (big_tiles >= 512) mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 4>(g, stream);
-      else mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 2>(g, stream);
+      LaunchFp8Gemm(g, stream);
       return true;
     }
   }

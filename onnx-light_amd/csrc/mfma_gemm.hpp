@@ -169,6 +169,9 @@ struct GemmArgs {
   const void *scale;
   int scale_f16;
   int scale_per_col;
+  // Row pitches of B and Y in elements (0: N), so a launch can cover a
+  // column range of larger matrices; N stays the width computed.
+  int64_t ldb, ldy;
 };
 
 template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB>
@@ -202,6 +205,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lg = lane >> 5;
   const int64_t M = p.M, N = p.N, K = p.K;
+  const int64_t LDB = p.ldb ? p.ldb : N, LDY = p.ldy ? p.ldy : N;
 
   // ---- tile selection: each XCD owns a contiguous run of tiles, grouped
   // kGroupM tile-rows high, so tiles sharing A rows / B columns share an L2 ----
@@ -226,7 +230,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const char *Ab = static_cast<const char *>(p.A) + a_off * kAsz;
   const char *Bb = static_cast<const char *>(p.B) + b_off * kBsz;
   const int64_t KA = K * kAsz;   // A row pitch in bytes
-  const int64_t NB = N * kBsz;   // B row pitch in bytes
+  const int64_t NB = LDB * kBsz;  // B row pitch in bytes
+  const int64_t NW = N * kBsz;    // bytes of a B row inside the computed columns
   const __amdgpu_buffer_rsrc_t rsA =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB =
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const __amdgpu_buffer_rsrc_t rsA0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsY = __builtin_amdgcn_make_buffer_rsrc(
-      static_cast<char *>(p.Y) + bt * M * N * kOsz, (short)0, (int)(M * N * kOsz), kRsrcWord3);
+      static_cast<char *>(p.Y) + bt * M * LDY * kOsz, (short)0, (int)(M * LDY * kOsz), kRsrcWord3);
   const int nfull = (int)(K / T::kKStep);                  // full K steps
   const bool half = K % T::kKStep != 0;                     // K % kKStep == kKStep / 2
   const int nk = nfull + (half ? 1 : 0);                    // K steps to load
@@ -256,14 +261,14 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     if constexpr (KIND == kH16) {
       const int krow = 4 * i + (lane >> 4);
       const int64_t cb = 2 * col0 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3)));
-      b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
+      b_g[q] = cb < NW ? (unsigned)(krow * NB + cb) : kOob;
     } else {
       // 1-byte B: a 1 KB piece is 1024 / kBP rows; lane -> (row, 16-byte
       // position p), holding global chunk p ^ (row % 8)
       constexpr int kCpr = kBP / 16;
       const int krow = (1024 / kBP) * i + lane / kCpr;
       const int64_t cb = col0 + 16 * ((lane % kCpr) ^ (krow & 7));
-      b_g[q] = cb < NB ? (unsigned)(krow * NB + cb) : kOob;
+      b_g[q] = cb < NW ? (unsigned)(krow * NB + cb) : kOob;
     }
   }
   // ---- LDS fragment offsets (sub-step 0; sub-step kk adds kk * const) ----
@@ -722,7 +727,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     // buffer, which the buffer store drops; all LDS reads issue first.
     const int64_t brow = row0 + wm * 128 + i * 32;
     const int64_t ncol = N - (col0 + wn * kWN);
-    const unsigned ybase = (unsigned)((brow * N + col0 + wn * kWN) * kOsz);
+    const unsigned ybase = (unsigned)((brow * LDY + col0 + wn * kWN) * kOsz);
     v4i piece[WB * kOsz];
 #pragma unroll
     for (int c = 0; c < WB * kOsz; ++c) {
@@ -736,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
       const bool ok = brow + rr < M && cc * (16 / kOsz) < ncol;
       __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY,
-                                             ok ? ybase + (unsigned)(rr * N * kOsz + cc * 16) : kOob, 0, kStoreThrough);
+                                             ok ? ybase + (unsigned)(rr * LDY * kOsz + cc * 16) : kOob, 0, kStoreThrough);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -759,10 +764,11 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 template <int KIND> inline bool Eligible(const GemmArgs &p) {
   constexpr int kAsz = KIND == kI8 ? 1 : 2, kBsz = KIND == kH16 ? 2 : 1;
   const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
+  const int64_t ldb = p.ldb ? p.ldb : p.N, ldy = p.ldy ? p.ldy : p.N;
   auto al = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-  return p.K > 0 && p.K % (Traits<KIND>::kKStep / 2) == 0 && p.N % 16 == 0 && al(p.A) && al(p.B) &&
-         al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim && p.M * p.N * 4 < lim &&
-         (p.K + 3 * Traits<KIND>::kKStep) * p.N * kBsz < lim;
+  return p.K > 0 && p.K % (Traits<KIND>::kKStep / 2) == 0 && p.N % 16 == 0 && ldb % 16 == 0 && ldy % 16 == 0 &&
+         ldb >= p.N && ldy >= p.N && al(p.A) && al(p.B) && al(p.Y) && p.M * p.K * kAsz + 4 * kStepBytes < lim &&
+         p.M * ldy * 4 < lim && (p.K + 3 * Traits<KIND>::kKStep) * ldb * kBsz < lim;
 }
 
 template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB = 2>

@@ -358,3 +358,20 @@ def test_config4_full_size(olamd, oracle, dev):
                                                          oracle.FLOAT, None, 1))
     mag = np.abs(decode(x["a_bits"][rows], "bf16", oracle)) @ np.abs(decode(w, "bf16", oracle))
     assert_close(got, fx["c4_y_bits"], mag, "bf16", oracle, "config 4")
+
+
+def test_fp8_gemm_column_split(olamd, oracle, dev):
+    """A 4096 x 8448 fp8 GEMM has 528 tiles of 256 x 256: the first 8192
+    columns run as whole rounds of such tiles and the last 256 columns as a
+    second launch in 256 x 128 tiles, with the full matrices' row pitches and
+    the offset scales.  Rows checked against the oracle chain, every column."""
+    rng = np.random.default_rng(20261202)
+    M, K, N = 4096, 64, 8448
+    a = oracle.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x = oracle.f32_to_f8e4m3fn_bits(rng.standard_normal(K * N).astype(np.float32)).reshape(K, N)
+    sc = rng.uniform(0.005, 0.05, N).astype(np.float32)
+    y = olamd.dequantize_linear_matmul(bits_tensor(a, "bf16", dev), T(x, dev), T(sc, dev), None, axis=1,
+                                       cast_to=olamd.BFLOAT16, x_dtype=oracle.FLOAT8E4M3FN, x_shape=(K, N))
+    rows = np.array([0, 1, 255, 256, 2047, 3840, 4095])
+    ref, mag = _chain_ref(oracle, a, x, oracle.FLOAT8E4M3FN, K, N, sc, False, None, 1, "bf16", "bf16", rows=rows)
+    assert_close(tensor_bits(y)[rows], ref, mag, "bf16", oracle, "fp8 column split")
