@@ -224,7 +224,7 @@ def cpu_baseline_c2(w, budget_s=20.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     x = w.inputs
-    rows = 16
+    rows = 40  # about 2.5 s per run on one core, 5 runs: 10-15 s of CPU work
     orc.qlinear_matmul(x["a"], x["a_scale"], 128, x["b"], x["b_scale"], 0, x["y_scale"], 128,
                        rows=(0, 2))  # warm-up
     times = []
