@@ -449,18 +449,20 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     }
   };
 
-  // Instruction order inside a sub-step (the scheduler would otherwise sink
-  // each LDS read next to its first use): the LDS reads two sub-steps ahead
-  // go first, then each MFMA is followed by its share of the next sub-step's
-  // decode, so the VALU work issues while the matrix pipe is busy.
+  // Instruction order inside a sub-step, pinned because the scheduler would
+  // otherwise sink each LDS read next to its first use.
   constexpr int kReads = 4 + WB * (KIND == kBf16F8 ? 1 : 2);
   constexpr int kDecodeValu = KIND == kBf16F8 ? 8 * WB : (KIND == kI8 ? (AU8 ? 16 : 0) + (BU8 ? 4 * WB : 0) + (CB ? 4 * WB : 0) : 0);
-  // plain sub-step with `nvm` direct loads, one after each of the first MFMAs
+  // A plain sub-step with `nvm` direct loads: each MFMA is preceded by its
+  // share of the LDS reads two sub-steps ahead and followed by a direct load
+  // and its share of the decode.  Reads issued all at once at the top of a
+  // sub-step (4 waves x 8 reads) queue up in the LDS; one read per MFMA cost
+  // 9% fewer cycles on C2.
   auto order_vm = [&](int nvm) __attribute__((always_inline)) {
     constexpr int kNM = 4 * WB;
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
     for (int x = 0; x < kNM; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x100, (kReads + kNM - 1) / kNM, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
       if constexpr (kDecodeValu > 0)
@@ -469,9 +471,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   };
   // second half of the barrier sub-step with `nvm` direct loads
   auto order_refill = [&](int nvm) __attribute__((always_inline)) {
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS read
 #pragma unroll
     for (int x = 0; x < 2 * WB; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x100, (kReads + 2 * WB - 1) / (2 * WB), 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
       if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
       if (x + 2 * WB < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
