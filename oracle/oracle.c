@@ -463,6 +463,141 @@ int orc_dequantize_linear(const void *x, int x_dtype, const int64_t *x_shape, in
 }
 
 /* ------------------------------------------------------------------------ */
+/* QuantizeLinear, kq/kernel_quantizelinear.cc.                              */
+
+/* fp32 value of x (FLOAT or FLOAT16), FloatValues :33-55. */
+static float ql_load(const void *x, int dtype, int64_t i) {
+  return dtype == ORC_FLOAT16 ? orc_f16_to_f32(((const uint16_t *)x)[i]) : ((const float *)x)[i];
+}
+
+/* Zero point of scale index si as fp32: the integer value (4-bit nibbles
+ * sign- or zero-extended, :186-188) or the fp8 decode (:93-107). */
+static float ql_zero_point(const void *zp, int dtype, int64_t si) {
+  if (!zp) return 0.0f;
+  switch (dtype) {
+  case ORC_UINT8: return (float)((const uint8_t *)zp)[si];
+  case ORC_INT8: return (float)((const int8_t *)zp)[si];
+  case ORC_UINT16: return (float)((const uint16_t *)zp)[si];
+  case ORC_INT16: return (float)((const int16_t *)zp)[si];
+  case ORC_UINT4: return (float)orc_read_4bit((const uint8_t *)zp, si);
+  case ORC_INT4: return (float)orc_int4_to_i8(orc_read_4bit((const uint8_t *)zp, si));
+  case ORC_FLOAT8E4M3FN: return orc_f8e4m3fn_to_f32(((const uint8_t *)zp)[si]);
+  default: return 0.0f;
+  }
+}
+
+/* Integer result of nearbyint(v) + zp clamped to [lo, hi] by the
+ * reference's two comparisons (:75-80); NaN passes both comparisons and the
+ * x86-64 float-to-int conversion of the reference build turns it into
+ * 0x80000000, whose low bits the narrowing keeps: 0 for every output type. */
+static int32_t ql_saturate(float v, float lo, float hi) {
+  if (v < lo) v = lo;
+  else if (v > hi) v = hi;
+  if (isnan(v)) return 0;
+  return (int32_t)v;
+}
+
+int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int x_rank,
+                        const void *scale, int scale_dtype, const int64_t *s_shape, int s_rank,
+                        const void *zp, int y_dtype, int64_t axis, void *y) {
+  if (x_dtype != ORC_FLOAT && x_dtype != ORC_FLOAT16) return 1;
+  if (scale_dtype != ORC_FLOAT && scale_dtype != ORC_FLOAT16) return 1;
+  float lo, hi;
+  switch (y_dtype) {
+  case ORC_UINT8: lo = 0.0f; hi = 255.0f; break;
+  case ORC_INT8: lo = -128.0f; hi = 127.0f; break;
+  case ORC_UINT16: lo = 0.0f; hi = 65535.0f; break;
+  case ORC_INT16: lo = -32768.0f; hi = 32767.0f; break;
+  case ORC_UINT4: lo = 0.0f; hi = 15.0f; break;
+  case ORC_INT4: lo = -8.0f; hi = 7.0f; break;
+  case ORC_FLOAT8E4M3FN: lo = hi = 0.0f; break;
+  default: return 1;
+  }
+  const int64_t n = numel(x_shape, x_rank);
+  const int64_t ns = numel(s_shape, s_rank);
+  int64_t repeats[ORC_MAX_RANK], sstr[ORC_MAX_RANK], coord[ORC_MAX_RANK];
+  const int blocked = ns != 1 && s_rank == x_rank;
+  int64_t inner = 1, axis_size = 1;
+  if (ns != 1) {
+    if (axis < 0 || axis >= x_rank || x_rank > ORC_MAX_RANK) return 1;
+    if (blocked) {
+      int64_t st = 1;
+      for (int d = x_rank - 1; d >= 0; --d) {
+        sstr[d] = st;
+        st *= s_shape[d];
+        repeats[d] = s_shape[d] ? x_shape[d] / s_shape[d] : 1;
+        coord[d] = 0;
+      }
+    } else {
+      for (int d = (int)axis + 1; d < x_rank; ++d) inner *= x_shape[d];
+      axis_size = x_shape[axis];
+    }
+  }
+  if (y_dtype == ORC_UINT4 || y_dtype == ORC_INT4) memset(y, 0, (size_t)((n + 1) / 2));
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t si = 0;
+    if (ns != 1) {
+      if (blocked) {
+        for (int d = 0; d < x_rank; ++d) si += (coord[d] / repeats[d]) * sstr[d];
+        for (int d = x_rank - 1; d >= 0; --d) {
+          if (++coord[d] < x_shape[d]) break;
+          coord[d] = 0;
+        }
+      } else {
+        si = (i / inner) % axis_size;
+      }
+    }
+    const float q = ql_load(x, x_dtype, i) / ql_load(scale, scale_dtype, si);
+    const float z = ql_zero_point(zp, y_dtype, si);
+    if (y_dtype == ORC_FLOAT8E4M3FN) {
+      ((uint8_t *)y)[i] = orc_f32_to_f8e4m3fn(q + z);
+      continue;
+    }
+    const int32_t v = ql_saturate(nearbyintf(q) + z, lo, hi);
+    switch (y_dtype) {
+    case ORC_UINT8: ((uint8_t *)y)[i] = (uint8_t)v; break;
+    case ORC_INT8: ((int8_t *)y)[i] = (int8_t)v; break;
+    case ORC_UINT16: ((uint16_t *)y)[i] = (uint16_t)v; break;
+    case ORC_INT16: ((int16_t *)y)[i] = (int16_t)v; break;
+    default: /* 4-bit, low nibble first on the flat index (rk/cast_sub_byte.h:50-60) */
+      ((uint8_t *)y)[i >> 1] |= (uint8_t)(((uint32_t)v & 0x0fu) << ((i & 1) ? 4 : 0));
+    }
+  }
+  return 0;
+}
+
+/* kq/kernel_dynamicquantizelinear.cc:57-121: range widened to include 0,
+ * scale = range / 255 (1 when the range is 0), zero point
+ * saturate(nearbyint(-min / scale)), y = saturate(nearbyint(x / scale) + zp). */
+int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_scale,
+                                uint8_t *y_zero_point) {
+  if (n <= 0) return 1;
+  float x_min = 0.0f, x_max = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    if (!isfinite(v)) return 1;
+    if (v < x_min) x_min = v;
+    if (v > x_max) x_max = v;
+  }
+  const float range = x_max - x_min;
+  const float scale = range == 0.0f ? 1.0f : range / 255.0f;
+  float zpf = nearbyintf(-x_min / scale);
+  if (zpf < 0.0f) zpf = 0.0f;
+  if (zpf > 255.0f) zpf = 255.0f;
+  const uint8_t zp = (uint8_t)zpf;
+  *y_scale = scale;
+  *y_zero_point = zp;
+  const float zf = (float)zp;
+  for (int64_t i = 0; i < n; ++i) {
+    float v = nearbyintf(x[i] / scale) + zf;
+    if (v < 0.0f) v = 0.0f;
+    if (v > 255.0f) v = 255.0f;
+    y[i] = (uint8_t)v;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* MatMul, km/kernel_matmul.cc:61-147 and :206-218.                          */
 
 typedef struct {

@@ -22,6 +22,13 @@
  *   DequantizeLinear - reference known-answer tests (per-tensor, per-axis,
  *                   blocked, fp16, fp8, int4/uint4) + numpy closed form.
  *   MatMul fp16/bf16 - reference known-answer test + float64 bound.
+ *   QuantizeLinear - the reference's known answers (u8/i8/u16/i16 per-tensor,
+ *                   per-axis u8 and u16, fp16 rounding, fp8 e4m3fn, int4/uint4
+ *                   per-axis) + numpy float32 closed form (true division,
+ *                   np.rint, clip) over random inputs.
+ *   DynamicQuantizeLinear - the reference's known answers (scale, zero point
+ *                   and the ONNX export cases' outputs, all-zero input,
+ *                   non-finite rejection) + numpy float32 closed form.
  * No function is "parity unpinned".
  */
 #ifndef ONNXL_AMD_ORACLE_H_
@@ -109,6 +116,25 @@ int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank, const flo
 int orc_matmul_half(const uint16_t *a, const int64_t *a_shape, int a_rank, const uint16_t *b,
                     const int64_t *b_shape, int b_rank, int dtype, uint16_t *y,
                     int64_t row_begin, int64_t row_end, int nthreads);
+
+/* ---- QuantizeLinear (kq/kernel_quantizelinear.cc) ----
+ * y = saturate(nearbyint(x / scale) + zero_point) for integer outputs
+ * (:67-84 per-tensor, :133-174 per-axis, :339-380 blocked, :176-200 and
+ * :435-457 4-bit), y = fp8(x / scale + zero_point) for FLOAT8E4M3FN
+ * (:257-270, :459-473).  x and scale are FLOAT or FLOAT16 (decoded to fp32,
+ * :33-55); fp32 division; the scale index rules are DequantizeLinear's.
+ * zp (same dtype as y) may be NULL (zero).  y_dtype: UINT8, INT8, UINT16,
+ * INT16, UINT4, INT4 or FLOAT8E4M3FN.  A NaN before the integer cast gives 0
+ * (the x86-64 conversion of the reference build).  Returns 0, or 1 for an
+ * unsupported combination. */
+int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int x_rank,
+                        const void *scale, int scale_dtype, const int64_t *s_shape, int s_rank,
+                        const void *zp, int y_dtype, int64_t axis, void *y);
+
+/* ---- DynamicQuantizeLinear (kq/kernel_dynamicquantizelinear.cc:57-121) ----
+ * Returns 0, or 1 for an empty or non-finite x (the reference throws). */
+int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_scale,
+                                uint8_t *y_zero_point);
 
 #ifdef __cplusplus
 }

@@ -82,6 +82,11 @@ def _declare(L):
     L.orc_dequantize_linear.restype = ctypes.c_int
     L.orc_dequantize_linear.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
                                         ctypes.c_int, P, ctypes.c_int64, P]
+    L.orc_quantize_linear.restype = ctypes.c_int
+    L.orc_quantize_linear.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P,
+                                      ctypes.c_int, P, ctypes.c_int, ctypes.c_int64, P]
+    L.orc_dynamic_quantize_linear.restype = ctypes.c_int
+    L.orc_dynamic_quantize_linear.argtypes = [P, ctypes.c_int64, P, P, P]
     L.orc_matmul_f32.restype = ctypes.c_int
     L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int]
@@ -247,6 +252,42 @@ def dequantize_linear(x: np.ndarray, x_dtype: int, x_shape, scale: np.ndarray, s
         raise ValueError(f"dequantize_linear error {rc}")
     assert y.size == n
     return y
+
+
+def quantize_linear(x: np.ndarray, x_dtype: int, scale: np.ndarray, scale_dtype: int, y_dtype: int,
+                    zp=None, axis: int = 1) -> np.ndarray:
+    """QuantizeLinear.  x holds FLOAT values or FLOAT16 bit patterns (its shape
+    is x's shape); scale likewise; zp holds the raw storage of the y dtype
+    (bytes for 4-bit types).  Returns the raw y storage: a uint8 / int8 /
+    uint16 / int16 array of x's shape, or packed bytes for 4-bit types."""
+    x = np.ascontiguousarray(x)
+    scale = np.ascontiguousarray(scale)
+    zp_arr = None if zp is None else np.ascontiguousarray(zp)
+    n = x.size
+    if y_dtype in (UINT4, INT4):
+        y = np.zeros((n + 1) // 2, np.uint8)
+    else:
+        y = np.empty(x.shape, {UINT8: np.uint8, INT8: np.int8, UINT16: np.uint16, INT16: np.int16,
+                               FLOAT8E4M3FN: np.uint8}[y_dtype])
+    rc = lib().orc_quantize_linear(_ptr(x), x_dtype, _ptr(_shape(x.shape)), x.ndim, _ptr(scale),
+                                   scale_dtype, _ptr(_shape(scale.shape)), scale.ndim,
+                                   None if zp_arr is None else _ptr(zp_arr), y_dtype, axis, _ptr(y))
+    if rc:
+        raise ValueError(f"quantize_linear error {rc}")
+    return y
+
+
+def dynamic_quantize_linear(x: np.ndarray):
+    """DynamicQuantizeLinear of a FLOAT array: (y uint8, scale, zero point).
+    Raises ValueError for an empty or non-finite x, as the reference does."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint8)
+    sc = np.zeros(1, np.float32)
+    zp = np.zeros(1, np.uint8)
+    rc = lib().orc_dynamic_quantize_linear(_ptr(x), x.size, _ptr(y), _ptr(sc), _ptr(zp))
+    if rc:
+        raise ValueError("kernel::DynamicQuantizeLinear: x must be non-empty and finite")
+    return y, sc[0], zp[0]
 
 
 def matmul_f32(a: np.ndarray, b: np.ndarray, rows=None, nthreads=1) -> np.ndarray:
