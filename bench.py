@@ -16,11 +16,13 @@ reported as `host_path_ms_per_step`.  `cpu_baseline` times the serial CPU
 oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql]
                   [--no-extra] [--no-cpu-baseline]
 
-The other configurations (3, 4, 5) are timed too and reported under
-`extra` unless --no-extra is given.
+The other configurations (3, 4, 5) and the quantizers in front of the
+integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
+configuration 2's fp32 activation) are timed too and reported under `extra`
+unless --no-extra is given.
 """
 from __future__ import annotations
 
@@ -166,6 +168,50 @@ def make_c5(olamd, dev, replicas):
     return w
 
 
+def make_q8(olamd, dev, replicas):
+    """QuantizeLinear of configuration 2's activation: fp32[2048,4096] -> u8
+    with a scalar scale and zero point (the producer of QLinearMatMul's A)."""
+    import torch
+    w = Workload()
+    w.name = "QuantizeLinear fp32[2048,4096] -> u8, scalar scale and zero point"
+    w.key, w.unit, w.dtype, w.bound = "q8", "GB/s", "f32 -> u8", "hbm"
+    n = 2048 * 4096
+    w.nbytes = n * 4 + n + 4 + 1
+    w.work = float(w.nbytes)
+    g = torch.Generator(device=dev).manual_seed(11)
+    sc = torch.tensor(0.031, device=dev)
+    zp = torch.tensor(128, dtype=torch.uint8, device=dev)
+    w.calls = []
+    for _ in range(replicas):
+        x = torch.randn((2048, 4096), generator=g, device=dev) * 4
+        y = torch.empty((2048, 4096), dtype=torch.uint8, device=dev)
+        w.calls.append(olamd.prepare("quantize_linear", x, sc, zp, 1, 0, y))
+    return w
+
+
+def make_dql(olamd, dev, replicas):
+    """DynamicQuantizeLinear of configuration 2's activation: fp32[2048,4096]
+    -> u8 plus scale and zero point.  The scale depends on all of x before any
+    element is quantized, so x is read twice (min/max pass, quantize pass):
+    algorithmic bytes 2 * 4n + n."""
+    import torch
+    w = Workload()
+    w.name = "DynamicQuantizeLinear fp32[2048,4096] -> u8, scale, zero point"
+    w.key, w.unit, w.dtype, w.bound = "dql", "GB/s", "f32 -> u8", "hbm"
+    n = 2048 * 4096
+    w.nbytes = 2 * n * 4 + n + 5
+    w.work = float(w.nbytes)
+    g = torch.Generator(device=dev).manual_seed(12)
+    w.calls = []
+    for _ in range(replicas):
+        x = torch.randn((2048, 4096), generator=g, device=dev) * 3 + 0.5
+        y = torch.empty((2048, 4096), dtype=torch.uint8, device=dev)
+        s = torch.empty((), device=dev)
+        z = torch.empty((), dtype=torch.uint8, device=dev)
+        w.calls.append(olamd.prepare("dynamic_quantize_linear", x, y, s, z))
+    return w
+
+
 def time_direct(w, steps, warmup):
     """Host path: one C-ABI call from Python per step (validation + launch),
     `steps` calls bracketed by synchronisations; ms per step by wall clock."""
@@ -281,7 +327,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c3_onnx_layout", "c4", "c5"])
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql"])
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -308,6 +355,10 @@ def main():
             return make_c3(olamd, dev, args.replicas or 24, prepared=False)
         if key == "c4":
             return make_c4(olamd, dev)
+        if key == "q8":
+            return make_q8(olamd, dev, args.replicas or 14)
+        if key == "dql":
+            return make_dql(olamd, dev, args.replicas or 14)
         return make_c5(olamd, dev, args.replicas or 16)
 
     w = build(args.workload)
@@ -322,7 +373,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5"):
+        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql"):
             if key == args.workload:
                 continue
             try:

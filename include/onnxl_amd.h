@@ -117,6 +117,35 @@ int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tenso
                                 const onnxl_amd_tensor *x_zero_point, int64_t axis,
                                 onnxl_amd_tensor *y, void *stream);
 
+/* QuantizeLinear: y = saturate(nearbyint(x / y_scale) + y_zero_point), the
+ * division in IEEE fp32; FLOAT8E4M3FN outputs take the saturating fp8 cast of
+ * x / y_scale + y_zero_point.  x and y_scale: FLOAT or FLOAT16.  The output
+ * dtype follows the reference's node dispatch (kq/kernel_quantizelinear.cc:
+ * 917-941): y_zero_point's dtype when it is given (per-tensor, per-axis or
+ * blocked; UINT8, INT8, UINT16, INT16, UINT4, INT4, FLOAT8E4M3FN), else
+ * output_dtype when non-zero (UINT8, INT8, UINT16, INT16), else UINT8 with a
+ * scalar y_scale.  y must already carry that dtype.  Output types the
+ * reference quantizes but this library does not (the other fp8 formats, 2-bit,
+ * FLOAT4E2M1, FLOAT6) return ONNXL_AMD_UNSUPPORTED.  axis may be negative.
+ * Replaces kernel::QuantizeLinear::operator(), kq/kernel_quantizelinear.cc:
+ * 485-532 (per tensor), :543-648 (per tensor with zero point), :664-822 (per
+ * axis and blocked with zero point), :833-916 (output_dtype). */
+int onnxl_amd_quantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *y_scale,
+                              const onnxl_amd_tensor *y_zero_point, int64_t axis, int32_t output_dtype,
+                              onnxl_amd_tensor *y, void *stream);
+
+/* DynamicQuantizeLinear: x FLOAT (non-empty) -> y UINT8 of x's shape, y_scale a
+ * 0-D FLOAT, y_zero_point a 0-D UINT8.  The range [min(x, 0), max(x, 0)] is
+ * reduced on the device; scale = range / 255 (1 for an empty range).  The
+ * reference rejects non-finite input; here the outputs cannot be inspected
+ * without a synchronisation, so such input is reported by y_scale = NaN (the
+ * caller checks it when it reads y_scale back).
+ * Replaces kernel::DynamicQuantizeLinear::operator(),
+ * kq/kernel_dynamicquantizelinear.cc:57-121. */
+int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tensor *y,
+                                      onnxl_amd_tensor *y_scale, onnxl_amd_tensor *y_zero_point,
+                                      void *stream);
+
 /* MatMul for FLOAT16 / BFLOAT16 operands (fp32 accumulation, output rounded
  * to the input dtype).  Replaces kernel::MatMul::operator()(a, b, Tensor &)
  * for those dtypes, km/kernel_matmul.cc:242-253 (compute :61-147, :206-218). */

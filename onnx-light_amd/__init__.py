@@ -87,6 +87,9 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_quantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, ctypes.c_int32, TP,
+                                                ctypes.c_void_p]
+        L.onnxl_amd_dynamic_quantize_linear.argtypes = [TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_prepare_weight_size.argtypes = [TP, ctypes.POINTER(ctypes.c_int64)]
         L.onnxl_amd_prepare_weight.argtypes = [TP, TP, ctypes.c_void_p]
         L.onnxl_amd_synchronize.argtypes = [ctypes.c_void_p]
@@ -334,6 +337,59 @@ def dequantize_linear_matmul(a, x, x_scale, x_zero_point=None, axis: int = 1, ca
     return out
 
 
+def _code_of(t):
+    if isinstance(t, np.ndarray):
+        return _NP_CODES[t.dtype]
+    return _torch_code(t.dtype)
+
+
+def quantize_linear(x, y_scale, y_zero_point=None, axis: int = 1, output_dtype: int = 0,
+                    y_dtype=None, out=None):
+    """kernel::QuantizeLinear with the node dispatch of QuantizeLinear::Run
+    (kq/kernel_quantizelinear.cc:917-941): the output dtype is y_zero_point's
+    (``y_dtype`` names it for packed 4-bit zero points), else output_dtype,
+    else UINT8.  4-bit outputs are returned as packed uint8 storage
+    (element 2k in the low nibble of byte k), FLOAT8E4M3FN as
+    torch.float8_e4m3fn."""
+    torch = _torch()
+    shape = _shape_of(x)
+    if y_dtype is None:
+        y_dtype = (_code_of(y_zero_point) if y_zero_point is not None
+                   else output_dtype if output_dtype else UINT8)
+    n = int(np.prod(shape, dtype=np.int64))
+    if out is None:
+        if y_dtype in (INT4, UINT4):
+            out = _empty(((n + 1) // 2,), torch.uint8, _device_of(x))
+        else:
+            tdt = {UINT8: torch.uint8, INT8: torch.int8, UINT16: torch.uint16, INT16: torch.int16,
+                   FLOAT8E4M3FN: torch.float8_e4m3fn}.get(y_dtype, torch.uint8)
+            out = _empty(shape, tdt, _device_of(x))
+    dy = describe(out, y_dtype, shape)
+    dz = _describe_zp(y_zero_point, y_dtype, y_scale)
+    _check(lib().onnxl_amd_quantize_linear(describe(x), describe(y_scale), dz, axis, output_dtype,
+                                           dy, _stream_of(x, out)))
+    return out
+
+
+def dynamic_quantize_linear(x, out=None, check: bool = True):
+    """kernel::DynamicQuantizeLinear (kq/kernel_dynamicquantizelinear.cc:
+    57-121): returns (y, y_scale, y_zero_point).  The library reports
+    non-finite input through y_scale = NaN (finite input never gives a NaN
+    scale: the range is >= 0, an infinite range gives an infinite scale);
+    with ``check`` the scale is read back (a synchronisation) and such input
+    raises InvalidArgument with the reference's message."""
+    torch = _torch()
+    dev = _device_of(x)
+    y, y_scale, y_zp = out if out is not None else (
+        _empty(_shape_of(x), torch.uint8, dev), _empty((), torch.float32, dev),
+        _empty((), torch.uint8, dev))
+    _check(lib().onnxl_amd_dynamic_quantize_linear(describe(x), describe(y), describe(y_scale),
+                                                   describe(y_zp), _stream_of(x, y)))
+    if check and bool(torch.isnan(y_scale).item()):
+        raise InvalidArgument("kernel::DynamicQuantizeLinear: x elements must be finite.")
+    return y, y_scale, y_zp
+
+
 class MatMulInteger:
     """Kernel-class mirror of kernel::MatMulInteger."""
     name = "onnxl_amd:GPU:ai.onnx:MatMulInteger"
@@ -369,10 +425,30 @@ class MatMul:
         return matmul(a, b, out)
 
 
+class QuantizeLinear:
+    """Kernel-class mirror of kernel::QuantizeLinear (axis defaults to 1 as in
+    QuantizeLinear::Run, kq/kernel_quantizelinear.cc:927)."""
+    name = "onnxl_amd:GPU:ai.onnx:QuantizeLinear"
+
+    def __call__(self, x, y_scale, y_zero_point=None, axis=1, output_dtype=0, y_dtype=None,
+                 out=None):
+        return quantize_linear(x, y_scale, y_zero_point, axis, output_dtype, y_dtype, out)
+
+
+class DynamicQuantizeLinear:
+    """Kernel-class mirror of kernel::DynamicQuantizeLinear."""
+    name = "onnxl_amd:GPU:ai.onnx:DynamicQuantizeLinear"
+
+    def __call__(self, x, out=None, check=True):
+        return dynamic_quantize_linear(x, out, check)
+
+
 # Dispatch keys "<domain>:<op_type>" as the reference table uses them
 # (core/runtime/kernels/kernel_dispatch_table.h:148-164).
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
-           "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul}
+           "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul,
+           "ai.onnx:QuantizeLinear": QuantizeLinear,
+           "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear}
 
 
 class Prepared:

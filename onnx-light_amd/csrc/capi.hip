@@ -537,6 +537,136 @@ int DequantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
 }
 
 // ---------------------------------------------------------------------------
+// QuantizeLinear, kq/kernel_quantizelinear.cc.  Dispatch as Run (:917-941):
+// a zero point fixes the output dtype; otherwise output_dtype does; otherwise
+// the output is UINT8 and the scale must be a scalar.
+
+bool QlGpuOutput(int32_t dt) {
+  return dt == kUint8 || dt == kInt8 || dt == kUint16 || dt == kInt16 || dt == kInt4 || dt == kUint4 ||
+         dt == kFloat8E4M3FN;
+}
+
+int QuantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zp,
+                   int64_t axis, int32_t output_dtype, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && !Absent(y_scale) && y,
+              "kernel::QuantizeLinear: x, y_scale and the output are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y_scale, "y_scale");
+  CheckDescriptor(y_zp, "y_zero_point");
+  CheckDescriptor(y, "y");
+  // FloatValues (:33-55)
+  OLA_ENFORCE(x->data_type == kFloat || x->data_type == kFloat16,
+              "kernel::QuantizeLinear: x must be FLOAT or FLOAT16.");
+  OLA_ENFORCE(y_scale->data_type == kFloat || y_scale->data_type == kFloat16,
+              "kernel::QuantizeLinear: y_scale must be FLOAT or FLOAT16.");
+  const bool has_zp = !Absent(y_zp);
+  if (axis < 0) axis += x->rank;  // :928-930
+  const bool scalar = NumElements(*y_scale) == 1;
+  int32_t yt = kUint8;
+  if (has_zp) {
+    OLA_ENFORCE(y->data_type == y_zp->data_type,
+                "kernel::QuantizeLinear: output data_type must match y_zero_point.");
+    yt = y_zp->data_type;
+    if (scalar)
+      OLA_ENFORCE(NumElements(*y_zp) == 1,
+                  "kernel::QuantizeLinear: y_zero_point must be a scalar (per-tensor quantization).");
+  } else if (output_dtype != 0) {
+    OLA_ENFORCE(y->data_type == output_dtype, "kernel::QuantizeLinear: output data_type must match output_dtype.");
+    yt = output_dtype;
+  } else {
+    OLA_ENFORCE(scalar, "kernel::QuantizeLinear: y_scale must be a scalar (per-tensor quantization).");
+    OLA_ENFORCE(y->data_type == kUint8,
+                "kernel::QuantizeLinear: without y_zero_point and output_dtype the output is UINT8.");
+  }
+  const int64_t n = NumElements(*x);
+  OLA_ENFORCE(ShapeOf(*y) == ShapeOf(*x), "kernel::QuantizeLinear preallocated output shape must match x shape.");
+  QuantParams p{};
+  p.n = n;
+  p.mode = 0;
+  if (!scalar) {
+    OLA_ENFORCE(axis >= 0 && axis < x->rank, "kernel::QuantizeLinear: axis out of range.");
+    if (has_zp)
+      OLA_ENFORCE(ShapeOf(*y_scale) == ShapeOf(*y_zp),
+                  "kernel::QuantizeLinear: y_scale and y_zero_point must have the same shape.");
+    const Shape xs = ShapeOf(*x), ss = ShapeOf(*y_scale);
+    p.inner = 1;
+    for (int d = (int)axis + 1; d < x->rank; ++d) p.inner *= xs[d];
+    p.axis_len = xs[axis];
+    if (ss.size() == xs.size()) {  // blocked (:684-693)
+      for (size_t d = 0; d < xs.size(); ++d) {
+        const int64_t s_dim = ss[d];
+        OLA_ENFORCE(s_dim > 0 && xs[d] % s_dim == 0,
+                    "kernel::QuantizeLinear: blocked y_scale dimension must divide the matching x dimension.");
+        OLA_ENFORCE((int64_t)d == axis || s_dim == xs[d],
+                    "kernel::QuantizeLinear: blocked y_scale may only differ from x along the quantization axis.");
+      }
+      p.mode = 2;
+      p.s_axis = ss[axis];
+      p.block = xs[axis] / ss[axis];
+    } else {  // per-axis (:694-698)
+      OLA_ENFORCE(NumElements(*y_scale) == xs[axis],
+                  "kernel::QuantizeLinear: y_scale element count must equal axis dimension.");
+      p.mode = 1;
+    }
+  }
+  // Output types: the no-zero-point overloads take 8- and 16-bit integers
+  // (:485-532 adds FLOAT4E2M1 and FLOAT6 per tensor; :891-915 per axis and
+  // blocked); with a zero point every type of :543-648 and :700-822.  Types
+  // the reference quantizes but this path has no kernel for are reported as
+  // unsupported, so an adapter can hand them back to the reference.
+  const bool eight_sixteen = yt == kUint8 || yt == kInt8 || yt == kUint16 || yt == kInt16;
+  const bool ref_only = has_zp ? (yt == 18 || yt == 19 || yt == 20 || yt == 23 || yt == 25 || yt == 26 ||
+                                  yt == 27 || yt == 28)
+                               : (scalar && (yt == 23 || yt == 27 || yt == 28));
+  if (ref_only) throw Unsupported(Cat("QuantizeLinear: output dtype ", yt, " has no GPU kernel"));
+  if (has_zp ? !QlGpuOutput(yt) : !eight_sixteen)
+    throw InvalidArgument(Cat("unsupported data type ", yt, ", kernel::QuantizeLinear: unsupported output dtype."));
+  OLA_ENFORCE(y->size_bytes == PackedBytes(yt, n),
+              "kernel::QuantizeLinear preallocated output buffer has unexpected size in bytes.");
+  p.x_f16 = x->data_type == kFloat16;
+  p.scale_f16 = y_scale->data_type == kFloat16;
+  p.y_dtype = yt;
+  Staging st(stream, 0, {x, y_scale, has_zp ? y_zp : nullptr}, {y});
+  p.x = st.In(x);
+  p.scale = st.In(y_scale);
+  p.zp = has_zp ? st.In(y_zp) : nullptr;
+  p.y = st.Out(y);
+  p.vec = reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
+  LaunchQuantize(p, stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// DynamicQuantizeLinear, kq/kernel_dynamicquantizelinear.cc:57-121.
+int DynamicQuantizeLinear(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, onnxl_amd_tensor *y_scale,
+                          onnxl_amd_tensor *y_zp, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && y && y_scale && y_zp,
+              "kernel::DynamicQuantizeLinear: x, y, y_scale and y_zero_point are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y, "y");
+  CheckDescriptor(y_scale, "y_scale");
+  CheckDescriptor(y_zp, "y_zero_point");
+  OLA_ENFORCE(x->data_type == kFloat, "kernel::DynamicQuantizeLinear: x must be FLOAT.");
+  OLA_ENFORCE(y->data_type == kUint8, "kernel::DynamicQuantizeLinear: y must be UINT8.");
+  OLA_ENFORCE(ShapeOf(*y) == ShapeOf(*x), "kernel::DynamicQuantizeLinear: y shape must match x shape.");
+  const int64_t n = NumElements(*x);
+  OLA_ENFORCE(y->size_bytes == n, "kernel::DynamicQuantizeLinear: y buffer has unexpected size.");
+  OLA_ENFORCE(y_scale->data_type == kFloat, "kernel::DynamicQuantizeLinear: y_scale must be FLOAT.");
+  OLA_ENFORCE(y_scale->rank == 0 && y_scale->size_bytes == 4,
+              "kernel::DynamicQuantizeLinear: y_scale must be a scalar FLOAT.");
+  OLA_ENFORCE(y_zp->data_type == kUint8, "kernel::DynamicQuantizeLinear: y_zero_point must be UINT8.");
+  OLA_ENFORCE(y_zp->rank == 0 && y_zp->size_bytes == 1,
+              "kernel::DynamicQuantizeLinear: y_zero_point must be a scalar UINT8.");
+  OLA_ENFORCE(n > 0, "kernel::DynamicQuantizeLinear: x must be non-empty.");
+  Staging st(stream, DynQuantScratchBytes(n), {x}, {y, y_scale, y_zp});
+  LaunchDynamicQuantize(static_cast<const float *>(st.In(x)), n, static_cast<uint8_t *>(st.Out(y)),
+                        static_cast<float *>(st.Out(y_scale)), static_cast<uint8_t *>(st.Out(y_zp)), st.Extra(),
+                        stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Cast FLOAT -> FLOAT16 / BFLOAT16.
 
 int Cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, hipStream_t stream) {
@@ -817,6 +947,21 @@ int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tenso
                                 onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DequantizeLinear(x, x_scale, x_zero_point, axis, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_quantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *y_scale,
+                              const onnxl_amd_tensor *y_zero_point, int64_t axis, int32_t output_dtype,
+                              onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return QuantizeLinear(x, y_scale, y_zero_point, axis, output_dtype, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, onnxl_amd_tensor *y_scale,
+                                      onnxl_amd_tensor *y_zero_point, void *stream) {
+  return Guard([&] {
+    return DynamicQuantizeLinear(x, y, y_scale, y_zero_point, static_cast<hipStream_t>(stream));
   });
 }
 

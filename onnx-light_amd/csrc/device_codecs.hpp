@@ -45,6 +45,29 @@ __device__ __forceinline__ float Fp8E4M3ToF32(uint8_t c) {
   return __builtin_bit_cast(float, s | ((e + 120u) << 23) | (m << 20));
 }
 
+// Round half to even of x / 2^sh for 1 <= sh <= 31.
+__device__ __forceinline__ uint32_t ShrRne(uint32_t x, uint32_t sh) {
+  const uint32_t q = x >> sh, rem = x & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+  return q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+}
+
+// float -> FLOAT8E4M3FN bits, saturating round to nearest even: NaN ->
+// sign|0x7f, +-inf and magnitudes past 448 -> sign|0x7e, fp32 subnormals and
+// magnitudes below 2^-10 -> signed zero (cast_float8.cc:27-81).
+__device__ __forceinline__ uint8_t F32ToFp8E4M3Sat(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+  if (a == 0x7f800000u) return (uint8_t)(sign | 0x7eu);
+  const int e = (int)(a >> 23);
+  if (e < 117) return (uint8_t)sign;
+  const int E = e - 120;  // fp8 biased exponent of a normal result
+  uint32_t mag = E >= 1 ? ShrRne(((uint32_t)E << 23) | (a & 0x7fffffu), 20)
+                        : ShrRne((a & 0x7fffffu) | 0x800000u, (uint32_t)(21 - E));
+  if (mag > 0x7eu) mag = 0x7eu;
+  return (uint8_t)(sign | mag);
+}
+
 __device__ __forceinline__ int Int4ToInt(uint32_t nibble) {
   return (int)((nibble & 0xfu) ^ 8u) - 8;
 }

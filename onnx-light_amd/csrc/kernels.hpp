@@ -88,6 +88,28 @@ struct DequantParams {
 
 void LaunchDequantize(const DequantParams &p, hipStream_t stream);
 
+// QuantizeLinear (kq/kernel_quantizelinear.cc): y = saturate(nearbyint(x /
+// scale) + zp) for integer outputs, fp8(x / scale + zp) for FLOAT8E4M3FN;
+// same scale-index modes as DequantParams.
+struct QuantParams {
+  const void *x;      // FLOAT or FLOAT16
+  const void *scale;  // FLOAT or FLOAT16
+  const void *zp;     // y's storage type (packed nibbles for 4-bit), or nullptr
+  void *y;
+  int64_t n;
+  int x_f16, scale_f16, y_dtype;
+  int vec;            // x and y allow whole 8-element vector accesses
+  int mode;           // 0 per-tensor, 1 per-axis, 2 blocked
+  int64_t inner, axis_len, block, s_axis;
+};
+void LaunchQuantize(const QuantParams &p, hipStream_t stream);
+
+// DynamicQuantizeLinear (kq/kernel_dynamicquantizelinear.cc:57-121) of n > 0
+// FLOAT values.  A non-finite x leaves y_scale = NaN, y_zero_point = 0, y = 0.
+size_t DynQuantScratchBytes(int64_t n);
+void LaunchDynamicQuantize(const float *x, int64_t n, uint8_t *y, float *y_scale, uint8_t *y_zero_point,
+                           void *scratch, hipStream_t stream);
+
 // Cast FLOAT -> FLOAT16 / BFLOAT16 (round to nearest even).
 void LaunchCastF32(const float *x, void *y, int64_t n, int to_bf16, hipStream_t stream);
 

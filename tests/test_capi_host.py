@@ -184,3 +184,83 @@ def test_not_initialized_before_device_work(olamd):
     with pytest.raises(olamd.DeviceError):
         olamd.matmul_integer(np.zeros((2, 2), np.uint8), np.zeros((2, 2), np.uint8),
                              out=np.zeros((2, 2), np.int32))
+
+
+def test_quantize_validation(olamd):
+    """kq/kernel_quantizelinear.cc:485-941: dispatch on zero point /
+    output_dtype / UINT8 default, and the same messages."""
+    d = olamd.describe
+    x = np.zeros((2, 3), np.float32)
+    sc = np.array([1.0, 2.0, 3.0], np.float32)
+    L = olamd.lib()
+
+    def run(x=x, s=sc, z=None, axis=1, odt=0, y=np.zeros((2, 3), np.uint8), ydt=None, zdt=None):
+        rc = L.onnxl_amd_quantize_linear(d(x), d(s), d(z, zdt), axis, odt,
+                                         d(y, ydt, None if ydt is None else (2, 3)), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    rc, err = run(s=sc)  # per-axis scale with neither zero point nor output_dtype
+    assert rc == olamd.INVALID_ARGUMENT and "y_scale must be a scalar (per-tensor quantization)." in err
+    rc, err = run(x=np.zeros((2, 3), np.int32), s=np.array(1.0, np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "x must be FLOAT or FLOAT16." in err
+    rc, err = run(z=np.zeros(3, np.int32), y=np.zeros((2, 3), np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "unsupported data type 6" in err
+    rc, err = run(z=np.zeros(3, np.int8))
+    assert rc == olamd.INVALID_ARGUMENT and "output data_type must match y_zero_point." in err
+    rc, err = run(z=np.zeros(3, np.uint8), axis=2)
+    assert rc == olamd.INVALID_ARGUMENT and "axis out of range." in err
+    rc, _ = run(z=np.zeros(3, np.uint8), axis=-1)  # Run normalises negative axes (:928-930)
+    assert rc == olamd.NOT_INITIALIZED
+    rc, err = run(z=np.zeros(2, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "y_scale and y_zero_point must have the same shape." in err
+    rc, err = run(s=np.ones(2, np.float32), z=np.zeros(2, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "y_scale element count must equal axis dimension." in err
+    rc, err = run(s=np.ones((2, 2), np.float32), odt=olamd.UINT8)
+    assert rc == olamd.INVALID_ARGUMENT and "blocked y_scale dimension must divide" in err
+    rc, err = run(s=np.ones((1, 3), np.float32), odt=olamd.UINT8)
+    assert rc == olamd.INVALID_ARGUMENT and "may only differ from x along the quantization axis" in err
+    rc, err = run(odt=olamd.INT8)
+    assert rc == olamd.INVALID_ARGUMENT and "output data_type must match output_dtype." in err
+    rc, err = run(odt=olamd.INT4, y=np.zeros(3, np.uint8), ydt=olamd.INT4)  # symmetric per-axis: 8/16-bit only
+    assert rc == olamd.INVALID_ARGUMENT and "unsupported output dtype." in err
+    rc, err = run(z=np.zeros(3, np.uint8), y=np.zeros((3, 2), np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "preallocated output shape must match x shape." in err
+    rc, err = run(s=np.array(1.0, np.float32), z=np.zeros(2, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "y_zero_point must be a scalar" in err
+    rc, err = run(s=np.array(1.0, np.float32), y=np.zeros((2, 3), np.int8))
+    assert rc == olamd.INVALID_ARGUMENT
+    rc, _ = run(z=np.zeros(3, np.uint8))
+    assert rc == olamd.NOT_INITIALIZED
+    rc, _ = run(s=np.array(1.0, np.float32))
+    assert rc == olamd.NOT_INITIALIZED
+    # output types the reference quantizes and this library has no kernel for
+    for dt in (18, 19, 20, 25, 26):
+        rc, _ = run(s=np.array(1.0, np.float32), z=np.zeros(1, np.uint8), zdt=dt,
+                    y=np.zeros(6 if dt < 25 else 2, np.uint8), ydt=dt)
+        assert rc == olamd.UNSUPPORTED, dt
+    rc, _ = run(s=np.array(1.0, np.float32), odt=23, y=np.zeros(3, np.uint8), ydt=23)
+    assert rc == olamd.UNSUPPORTED
+
+
+def test_dynamic_quantize_validation(olamd):
+    """kq/kernel_dynamicquantizelinear.cc:57-77."""
+    d = olamd.describe
+    L = olamd.lib()
+    x = np.zeros((2, 3), np.float32)
+
+    def run(x=x, y=np.zeros((2, 3), np.uint8), s=np.zeros((), np.float32), z=np.zeros((), np.uint8)):
+        rc = L.onnxl_amd_dynamic_quantize_linear(d(x), d(y), d(s), d(z), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(x=x.astype(np.float16)), "x must be FLOAT."),
+                    (dict(y=np.zeros((2, 3), np.int8)), "y must be UINT8."),
+                    (dict(y=np.zeros((3, 2), np.uint8)), "y shape must match x shape."),
+                    (dict(s=np.zeros((), np.float16)), "y_scale must be FLOAT."),
+                    (dict(s=np.zeros(1, np.float32)), "y_scale must be a scalar FLOAT."),
+                    (dict(z=np.zeros((), np.int8)), "y_zero_point must be UINT8."),
+                    (dict(z=np.zeros(1, np.uint8)), "y_zero_point must be a scalar UINT8."),
+                    (dict(x=np.zeros(0, np.float32), y=np.zeros(0, np.uint8)), "x must be non-empty.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    rc, _ = run()
+    assert rc == olamd.NOT_INITIALIZED

@@ -90,3 +90,37 @@ def test_qlinear_graph_replays_match_eager(olamd, dev):
         call()
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"eager after replay {rep}"
+
+
+def test_quantize_graph_replays_match_eager(olamd, dev):
+    """QuantizeLinear and the two-pass DynamicQuantizeLinear (its min / max
+    partials live in the shared workspace) captured together."""
+    g0 = torch.Generator(device=dev).manual_seed(5)
+    x1 = torch.randn((1000, 777), generator=g0, device=dev) * 7
+    x2 = torch.randn((3001, 1024), generator=g0, device=dev) - 2
+    sc = torch.tensor(0.05, device=dev)
+    zp = torch.tensor(-3, dtype=torch.int8, device=dev)
+    y1 = torch.empty((1000, 777), dtype=torch.int8, device=dev)
+    y2 = torch.empty((3001, 1024), dtype=torch.uint8, device=dev)
+    s2 = torch.empty((), device=dev)
+    z2 = torch.empty((), dtype=torch.uint8, device=dev)
+    c1 = olamd.prepare("quantize_linear", x1, sc, zp, 1, 0, y1)
+    c2 = olamd.prepare("dynamic_quantize_linear", x2, y2, s2, z2)
+    c1()
+    c2()
+    torch.cuda.synchronize()
+    refs = [t.clone() for t in (y1, y2, s2, z2)]
+    g = _capture([c2, c1])
+    for rep in range(4):
+        for t in (y1, y2, s2, z2):
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for t, r in zip((y1, y2, s2, z2), refs):
+            assert torch.equal(t, r), f"replay {rep}"
+        c1()
+        c2()
+        torch.cuda.synchronize()
+        for t, r in zip((y1, y2, s2, z2), refs):
+            assert torch.equal(t, r), f"eager after replay {rep}"

@@ -137,3 +137,22 @@ def test_dynamic_quantize_closed_form_random(oracle, spread):
     assert np.float32(sc) == want_sc and int(zp) == want_zp
     want = np.clip(np.rint(x / want_sc) + np.float32(want_zp), 0, 255).astype(np.uint8)
     assert np.array_equal(y, want)
+
+
+def test_fp8_nan_sign_follows_x86(oracle):
+    """FLOAT8E4M3FN keeps the fp32 NaN's sign (0x7f / 0xff).  On x86-64, where
+    the reference is built, an invalid operation (0/0, inf/inf) returns the
+    negative "real indefinite" QNaN 0xffc00000, and a NaN operand is returned
+    as it is (the destination operand when both are NaN: x for x / scale; for
+    the commutative quotient + zero point gcc -O2 puts the zero point there).
+    The oracle runs on the same instruction set, and the GPU kernel restates
+    the rule."""
+    x = np.array([0.0, np.inf, np.nan, -np.nan, 1.0], np.float32)
+    zp = np.zeros(1, np.uint8).reshape(())
+    for sv, want in ((0.0, [0xff, 0x7e, 0x7f, 0xff, 0x7e]), (np.inf, [0x00, 0xff, 0x7f, 0xff, 0x00])):
+        y = oracle.quantize_linear(x, 1, np.array(sv, np.float32), 1, DT["float8e4m3fn"], zp, 1)
+        assert y.tolist() == want, sv
+    nan_zp = np.array(0x7f, np.uint8).reshape(())
+    y = oracle.quantize_linear(np.array([1.0, -np.nan], np.float32), 1, np.array(1.0, np.float32), 1,
+                               DT["float8e4m3fn"], nan_zp, 1)
+    assert y.tolist() == [0x7f, 0x7f]
