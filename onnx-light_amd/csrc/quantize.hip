@@ -22,6 +22,23 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
+// x is read once: non-temporal loads keep it from displacing cache lines that
+// are reused.  y is not read again either: its stores write through the L2
+// (sc1), because dirty write-back lines left in the L2 at the end of a kernel
+// hold its completion until they are flushed.
+constexpr int kWriteThrough = 16;
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ v4f LoadNt(const float *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p));
+}
+
+// Buffer descriptor over `bytes` bytes of y starting at byte `at` (a
+// workgroup's share; the stores then carry the cache policy above).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ShareRsrc(void *y, int64_t at, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(y) + at, (short)0, bytes, kRsrcWord3);
+}
+
 template <bool F16> __device__ __forceinline__ float LoadF(const void *p, int64_t i) {
   if constexpr (F16) return F16ToF32(static_cast<const uint16_t *>(p)[i]);
   return static_cast<const float *>(p)[i];
@@ -86,12 +103,12 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
   float xv[kQPer];
   if (full && p.vec) {
     if constexpr (XF16) {
-      const v8h h = *reinterpret_cast<const v8h *>(static_cast<const uint16_t *>(p.x) + i0);
+      const v8h h = __builtin_nontemporal_load(reinterpret_cast<const v8h *>(static_cast<const uint16_t *>(p.x) + i0));
 #pragma unroll
       for (int e = 0; e < kQPer; ++e) xv[e] = (float)h[e];
     } else {
-      const v4f a = *reinterpret_cast<const v4f *>(static_cast<const float *>(p.x) + i0);
-      const v4f b = *reinterpret_cast<const v4f *>(static_cast<const float *>(p.x) + i0 + 4);
+      const v4f a = LoadNt(static_cast<const float *>(p.x) + i0);
+      const v4f b = LoadNt(static_cast<const float *>(p.x) + i0 + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         xv[e] = a[e];
@@ -146,6 +163,10 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
     }
   }
 
+  // full vector stores go through the workgroup's buffer descriptor
+  constexpr int kYBits = YT == kUint4 || YT == kInt4 ? 4 : YT == kUint16 || YT == kInt16 ? 16 : 8;
+  constexpr int kShare = kQBlock * kQPer * kYBits / 8;
+  const unsigned off = threadIdx.x * (kQPer * kYBits / 8);
   if constexpr (YT == kUint4 || YT == kInt4) {
     // element 2k in the low nibble of byte k (rk/cast_sub_byte.h:50-60)
     uint32_t word = 0;
@@ -153,7 +174,8 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
     for (int e = 0; e < kQPer; ++e) word |= (i0 + e < p.n ? (code[e] & 0xfu) : 0u) << (4 * e);
     uint8_t *y = static_cast<uint8_t *>(p.y) + (i0 >> 1);
     if (full && p.vec) {
-      *reinterpret_cast<uint32_t *>(y) = word;
+      __builtin_amdgcn_raw_buffer_store_b32((int)word, ShareRsrc(p.y, (int64_t)blockIdx.x * kShare, kShare), off, 0,
+                                            kWriteThrough);
     } else {
       const int64_t bytes = (p.n - i0 + 1) >> 1;
 #pragma unroll
@@ -166,7 +188,8 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
       v4i w;
 #pragma unroll
       for (int k = 0; k < 4; ++k) w[k] = (int)((code[2 * k] & 0xffffu) | (code[2 * k + 1] << 16));
-      *reinterpret_cast<v4i *>(y) = w;
+      __builtin_amdgcn_raw_buffer_store_b128(w, ShareRsrc(p.y, (int64_t)blockIdx.x * kShare, kShare), off, 0,
+                                             kWriteThrough);
     } else {
 #pragma unroll
       for (int e = 0; e < kQPer; ++e)
@@ -180,7 +203,8 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
       for (int k = 0; k < 2; ++k)
         w[k] = (int)((code[4 * k] & 0xffu) | (code[4 * k + 1] & 0xffu) << 8 | (code[4 * k + 2] & 0xffu) << 16 |
                      (code[4 * k + 3] << 24));
-      *reinterpret_cast<v2i *>(y) = w;
+      __builtin_amdgcn_raw_buffer_store_b64(w, ShareRsrc(p.y, (int64_t)blockIdx.x * kShare, kShare), off, 0,
+                                            kWriteThrough);
     } else {
 #pragma unroll
       for (int e = 0; e < kQPer; ++e)
@@ -212,15 +236,19 @@ template <bool XF16> void LaunchQX(const QuantParams &p, dim3 g, hipStream_t s) 
 }
 
 // ---------------------------------------------------------------------------
-// DynamicQuantizeLinear: a min/max pass writes one (min, max, non-finite)
-// triple per workgroup; every workgroup of the quantize pass reduces those
-// triples itself (min and max are order-independent, so all agree), derives
-// scale and zero point with the reference's fp32 operations, and quantizes its
-// share.  No atomics and no counters, so the pair can be captured in a graph.
+// DynamicQuantizeLinear, two launches.  The min / max pass has kDqParts
+// workgroups (fewer for small x), each writing one (min, max, non-finite)
+// triple into structure-of-arrays partials [mn[P], mx[P], bad[P]].  The
+// quantize pass covers x with one 8-element chunk per thread like
+// QuantizeLinear; every workgroup issues its x loads, reduces the P partials
+// itself while they land (min and max are order-independent, so all
+// workgroups agree), derives scale and zero point with the reference's fp32
+// operations and quantizes.  No atomics and no counters, so the pair can be
+// captured in a graph.
 
 constexpr int kDqBlock = 256;
-constexpr int kDqMaxParts = 512;
-constexpr int kDqPerThread = 16;
+constexpr int kDqParts = 512;
+constexpr int kDqUnroll = 4;  // float4 loads in flight per thread in the min / max pass
 
 __device__ __forceinline__ void BlockMinMax(float &mn, float &mx, float &bad) {
   __shared__ float red[3][kDqBlock / 64];
@@ -256,38 +284,66 @@ __global__ __launch_bounds__(kDqBlock) void MinMaxKernel(const float *x, int64_t
     mn = fminf(mn, v);
     mx = fmaxf(mx, v);
   };
-  const int64_t stride = (int64_t)gridDim.x * kDqBlock;
   const int64_t t = (int64_t)blockIdx.x * kDqBlock + threadIdx.x;
   int64_t done = 0;
   if (vec) {
     const int64_t n4 = n >> 2;
-    for (int64_t i = t; i < n4; i += stride) {
-      const v4f v = reinterpret_cast<const v4f *>(x)[i];
-      take(v[0]);
-      take(v[1]);
-      take(v[2]);
-      take(v[3]);
+    const int64_t stride = (int64_t)gridDim.x * kDqBlock * kDqUnroll;
+    for (int64_t i = (int64_t)blockIdx.x * kDqBlock * kDqUnroll + threadIdx.x; i < n4; i += stride) {
+      v4f v[kDqUnroll];
+#pragma unroll
+      for (int u = 0; u < kDqUnroll; ++u)
+        v[u] = i + u * kDqBlock < n4 ? reinterpret_cast<const v4f *>(x)[i + u * kDqBlock] : v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < kDqUnroll; ++u) {
+        take(v[u][0]);
+        take(v[u][1]);
+        take(v[u][2]);
+        take(v[u][3]);
+      }
     }
     done = n4 << 2;
   }
-  for (int64_t i = done + t; i < n; i += stride) take(x[i]);
+  for (int64_t i = done + t; i < n; i += (int64_t)gridDim.x * kDqBlock) take(x[i]);
   BlockMinMax(mn, mx, bad);
   if (threadIdx.x == 0) {
-    part[3 * blockIdx.x] = mn;
-    part[3 * blockIdx.x + 1] = mx;
-    part[3 * blockIdx.x + 2] = bad;
+    part[blockIdx.x] = mn;
+    part[gridDim.x + blockIdx.x] = mx;
+    part[2 * gridDim.x + blockIdx.x] = bad;
   }
 }
 
 __global__ __launch_bounds__(kDqBlock) void DynQuantKernel(const float *x, int64_t n, int vec, const float *part,
                                                            int nparts, uint8_t *y, float *y_scale,
                                                            uint8_t *y_zp) {
-  float mn = 0.f, mx = 0.f, bad = 0.f;
-  for (int i = threadIdx.x; i < nparts; i += kDqBlock) {
-    mn = fminf(mn, part[3 * i]);
-    mx = fmaxf(mx, part[3 * i + 1]);
-    bad = fmaxf(bad, part[3 * i + 2]);
+  const int64_t i0 = ((int64_t)blockIdx.x * kDqBlock + threadIdx.x) * kQPer;
+  // workgroup-uniform, so the two load paths are a scalar branch
+  const bool full = vec && ((int64_t)blockIdx.x + 1) * kDqBlock * kQPer <= n;
+  float xv[kQPer];
+  if (full) {
+    const v4f a = LoadNt(x + i0), b = LoadNt(x + i0 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[e] = a[e];
+      xv[4 + e] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kQPer; ++e) xv[e] = x[std::min<int64_t>(i0 + e, n - 1)];  // clamped ones are not stored
   }
+  // The partials are loaded after x, all at once: the load counter retires
+  // loads in issue order, so one wait covers x and the partials, which are
+  // in flight together (a partial read twice changes no minimum or maximum).
+  static_assert(kDqParts <= 2 * kDqBlock, "two partials per thread");
+  float pmn[2], pmx[2], pbad[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = min((int)threadIdx.x + k * kDqBlock, nparts - 1);
+    pmn[k] = part[i];
+    pmx[k] = part[nparts + i];
+    pbad[k] = part[2 * nparts + i];
+  }
+  float mn = fminf(pmn[0], pmn[1]), mx = fmaxf(pmx[0], pmx[1]), bad = fmaxf(pbad[0], pbad[1]);
   BlockMinMax(mn, mx, bad);
   // :96-106: scale = range / 255 (1 for an empty range), zero point
   // saturate(nearbyint(-min / scale))
@@ -302,30 +358,32 @@ __global__ __launch_bounds__(kDqBlock) void DynQuantKernel(const float *x, int64
     *y_scale = scale;
     *y_zp = (uint8_t)zpf;
   }
-  // :113-120: y = saturate(nearbyint(x / scale) + zero point), 16 per thread
-  auto q = [&](float v) -> uint32_t {
-    const float r = __builtin_rintf(v / scale) + zpf;
-    return r != r ? 0u : (uint32_t)__builtin_amdgcn_fmed3f(r, 0.f, 255.f);
-  };
-  const int64_t stride = (int64_t)gridDim.x * kDqBlock * kDqPerThread;
-  for (int64_t i0 = ((int64_t)blockIdx.x * kDqBlock + threadIdx.x) * kDqPerThread; i0 < n; i0 += stride) {
-    if (vec && i0 + kDqPerThread <= n) {
-      v4i w;
+  if (i0 >= n) return;
+  // :113-120: y = saturate(nearbyint(x / scale) + zero point)
+  uint32_t code[kQPer];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const v4f v = reinterpret_cast<const v4f *>(x + i0)[k];
-        w[k] = (int)(q(v[0]) | q(v[1]) << 8 | q(v[2]) << 16 | q(v[3]) << 24);
-      }
-      *reinterpret_cast<v4i *>(y + i0) = w;
-    } else {
-      for (int e = 0; e < kDqPerThread && i0 + e < n; ++e) y[i0 + e] = (uint8_t)q(x[i0 + e]);
-    }
+  for (int e = 0; e < kQPer; ++e) {
+    const float r = __builtin_rintf(xv[e] / scale) + zpf;
+    code[e] = r != r ? 0u : (uint32_t)__builtin_amdgcn_fmed3f(r, 0.f, 255.f);
+  }
+  if (full) {
+    v2i w;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      w[k] = (int)(code[4 * k] | code[4 * k + 1] << 8 | code[4 * k + 2] << 16 | code[4 * k + 3] << 24);
+    constexpr int kShare = kDqBlock * kQPer;
+    __builtin_amdgcn_raw_buffer_store_b64(w, ShareRsrc(y, (int64_t)blockIdx.x * kShare, kShare),
+                                          threadIdx.x * kQPer, 0, kWriteThrough);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kQPer; ++e)
+      if (i0 + e < n) y[i0 + e] = (uint8_t)code[e];
   }
 }
 
 int DynQuantParts(int64_t n) {
-  const int64_t per_block = (int64_t)kDqBlock * kDqPerThread;
-  return (int)std::min<int64_t>(kDqMaxParts, std::max<int64_t>(1, (n + per_block - 1) / per_block));
+  const int64_t per_block = (int64_t)kDqBlock * kDqUnroll * 4;
+  return (int)std::min<int64_t>(kDqParts, std::max<int64_t>(1, (n + per_block - 1) / per_block));
 }
 
 }  // namespace
@@ -344,9 +402,10 @@ void LaunchDynamicQuantize(const float *x, int64_t n, uint8_t *y, float *y_scale
   const int parts = DynQuantParts(n);
   const int vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
   float *part = static_cast<float *>(scratch);
+  const int64_t chunk = (int64_t)kDqBlock * kQPer;
   hipLaunchKernelGGL(MinMaxKernel, dim3(parts), dim3(kDqBlock), 0, s, x, n, vec, part);
-  hipLaunchKernelGGL(DynQuantKernel, dim3(parts), dim3(kDqBlock), 0, s, x, n, vec, part, parts, y, y_scale,
-                     y_zero_point);
+  hipLaunchKernelGGL(DynQuantKernel, dim3((unsigned)((n + chunk - 1) / chunk)), dim3(kDqBlock), 0, s, x, n, vec,
+                     part, parts, y, y_scale, y_zero_point);
 }
 
 }  // namespace onnxl_amd
