@@ -226,10 +226,13 @@ def test_dynamic_known_answers(olamd, oracle, golden, dev):
         assert y.reshape(-1).tolist() == c["y"], c["name"]
 
 
-@pytest.mark.parametrize("n", [1, 7, 16, 4095, 4096, 65539, 1 << 20, 2_097_152, 5_000_011])
+@pytest.mark.parametrize("n", [1, 7, 16, 4095, 4096, 65539, 1 << 20, 2_097_152, 5_000_011, 8_388_608,
+                               12_582_912])
 def test_dynamic_random_vs_oracle(olamd, oracle, dev, n):
-    """Sizes below, at and above the 512 x 4096 elements where every
-    workgroup of the reduction covers more than one chunk."""
+    """Sizes below, at and above 512 x 4096 elements, where every workgroup
+    of the min / max pass covers more than one chunk, up to the BASELINE
+    activation (2^23) and beyond; ragged sizes and misaligned offsets take
+    the per-element paths."""
     rng = np.random.default_rng(n)
     for shift, spread, offset in ((0.0, 1.0, 0), (3.0, 0.5, 1), (-5.0, 0.01, 0), (0.0, 1e-30, 2)):
         xv = (shift + spread * rng.standard_normal(n)).astype(np.float32)
