@@ -598,6 +598,176 @@ int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_
 }
 
 /* ------------------------------------------------------------------------ */
+/* ConvInteger (nn/kernel_conv_integer.cc) and QLinearConv
+ * (kq/kernel_qlinearconv.cc): the same attribute resolution and the same
+ * direct loops over (n, m, output position) x (input channel of the group,
+ * kernel tap); taps that fall into the padding are skipped.               */
+
+/* ResolveAttributes + ComputeOutputSpatial (kernel_conv_integer.cc:24-54,
+ * :107-141; kernel_qlinearconv.cc:53-119 are the same).  kernel_shape,
+ * strides, dilations and pads may be NULL (defaults); pads_out receives the
+ * resolved pads (2 * spatial rank), out_spatial the output sizes.  Returns
+ * 0, or 1 for an attribute the reference rejects. */
+int orc_conv_geometry(const int64_t *x_shape, int x_rank, const int64_t *w_shape,
+                      const int64_t *kernel_shape, const int64_t *strides, const int64_t *pads,
+                      const int64_t *dilations, int auto_pad, int64_t *k_out, int64_t *s_out,
+                      int64_t *d_out, int64_t *pads_out, int64_t *out_spatial) {
+  const int sr = x_rank - 2;
+  if (sr < 1 || sr > ORC_MAX_RANK) return 1;
+  for (int i = 0; i < sr; ++i) {
+    k_out[i] = kernel_shape ? kernel_shape[i] : w_shape[i + 2];
+    s_out[i] = strides ? strides[i] : 1;
+    d_out[i] = dilations ? dilations[i] : 1;
+    pads_out[i] = pads_out[i + sr] = 0;
+    if (auto_pad == ORC_AUTO_PAD_NOTSET && pads) {
+      pads_out[i] = pads[i];
+      pads_out[i + sr] = pads[i + sr];
+    }
+  }
+  if (auto_pad < ORC_AUTO_PAD_NOTSET || auto_pad > ORC_AUTO_PAD_VALID) return 1;
+  for (int i = 0; i < sr; ++i) {
+    const int64_t in = x_shape[i + 2], s = s_out[i];
+    const int64_t eff_k = (k_out[i] - 1) * d_out[i] + 1;
+    if (auto_pad == ORC_AUTO_PAD_VALID) {
+      out_spatial[i] = (in - eff_k) / s + 1;
+    } else if (auto_pad == ORC_AUTO_PAD_NOTSET) {
+      out_spatial[i] = (in + pads_out[i] + pads_out[i + sr] - eff_k) / s + 1;
+    } else {
+      const int64_t out = (in + s - 1) / s;
+      int64_t need = (out - 1) * s + eff_k - in;
+      if (need < 0) need = 0;
+      if (auto_pad == ORC_AUTO_PAD_SAME_UPPER) {
+        pads_out[i] = need / 2;
+        pads_out[i + sr] = need - need / 2;
+      } else {
+        pads_out[i + sr] = need / 2;
+        pads_out[i] = need - need / 2;
+      }
+      out_spatial[i] = out;
+    }
+  }
+  return 0;
+}
+
+/* Accumulates sum over the group's input channels and the kernel taps of
+ * (x - x_zp) * (w - w_zp) for output (n, m, op) in int64 (QLinearConv,
+ * kernel_qlinearconv.cc:306-330); ConvInteger truncates it to int32
+ * (kernel_conv_integer.cc:269-299 accumulates in int32, which wraps). */
+static int64_t conv_point(const void *x, int x_dtype, const int64_t *x_shape, int sr, const void *w,
+                          int w_dtype, int64_t cpg, int64_t mpg, int64_t n, int64_t m, const int64_t *oidx,
+                          const int64_t *k, const int64_t *s, const int64_t *d, const int64_t *pads,
+                          int32_t x_zp, int32_t w_zp) {
+  int64_t in_strides[ORC_MAX_RANK], in_size = 1, ks = 1;
+  for (int a = sr - 1; a >= 0; --a) {
+    in_strides[a] = in_size;
+    in_size *= x_shape[a + 2];
+    ks *= k[a];
+  }
+  const int64_t C = x_shape[1], g = m / mpg;
+  int64_t acc = 0;
+  for (int64_t ic = 0; ic < cpg; ++ic) {
+    const int64_t x_base = (n * C + g * cpg + ic) * in_size;
+    const int64_t w_base = (m * cpg + ic) * ks;
+    int64_t kidx[ORC_MAX_RANK] = {0};
+    for (int64_t kp = 0; kp < ks; ++kp) {
+      int in_bounds = 1;
+      int64_t off = 0;
+      for (int a = 0; a < sr; ++a) {
+        const int64_t ia = oidx[a] * s[a] + kidx[a] * d[a] - pads[a];
+        if (ia < 0 || ia >= x_shape[a + 2]) {
+          in_bounds = 0;
+          break;
+        }
+        off += ia * in_strides[a];
+      }
+      if (in_bounds)
+        acc += (int64_t)(read_byte_elem(x, x_dtype, x_base + off) - x_zp) *
+               (int64_t)(read_byte_elem(w, w_dtype, w_base + kp) - w_zp);
+      for (int a = sr - 1; a >= 0; --a) {
+        if (++kidx[a] < k[a]) break;
+        kidx[a] = 0;
+      }
+    }
+  }
+  return acc;
+}
+
+/* Shared driver: y_i32 (ConvInteger) or y_q8 (QLinearConv) for every output.
+ * w_zp / w_scale have w_zp_count / w_scale_count values (1 or M). */
+static int conv_run(const void *x, int x_dtype, const int64_t *x_shape, int x_rank, const void *w,
+                    int w_dtype, const int64_t *w_shape, int32_t x_zp, const void *w_zp,
+                    int64_t w_zp_count, int64_t group, const int64_t *kernel_shape,
+                    const int64_t *strides, const int64_t *pads, const int64_t *dilations, int auto_pad,
+                    int32_t *y_i32, const float *combined, int64_t cs_count, const int32_t *bias,
+                    float y_zp, int y_signed, void *y_q8) {
+  const int sr = x_rank - 2;
+  int64_t k[ORC_MAX_RANK], s[ORC_MAX_RANK], d[ORC_MAX_RANK], pd[2 * ORC_MAX_RANK], od[ORC_MAX_RANK];
+  if (orc_conv_geometry(x_shape, x_rank, w_shape, kernel_shape, strides, pads, dilations, auto_pad, k, s,
+                        d, pd, od))
+    return 1;
+  const int64_t N = x_shape[0], M = w_shape[0], cpg = w_shape[1];
+  if (group < 1 || x_shape[1] != cpg * group || M % group != 0) return 1;
+  const int64_t mpg = M / group;
+  int64_t osize = 1;
+  for (int a = 0; a < sr; ++a) osize *= od[a];
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t m = 0; m < M; ++m) {
+      const int32_t wz = w_zp ? read_byte_elem(w_zp, w_dtype, w_zp_count == M ? m : 0) : 0;
+      for (int64_t op = 0; op < osize; ++op) {
+        int64_t oidx[ORC_MAX_RANK], rem = op;
+        for (int a = sr - 1; a >= 0; --a) {
+          oidx[a] = rem % od[a];
+          rem /= od[a];
+        }
+        int64_t acc = conv_point(x, x_dtype, x_shape, sr, w, w_dtype, cpg, mpg, n, m, oidx, k, s, d, pd, x_zp,
+                                 wz);
+        const int64_t o = (n * M + m) * osize + op;
+        if (y_i32) {
+          y_i32[o] = (int32_t)(uint32_t)(uint64_t)acc;
+          continue;
+        }
+        if (bias) acc += bias[m];
+        const float scaled = (float)acc * combined[cs_count == M ? m : 0];
+        float v = nearbyintf(scaled) + y_zp;
+        const float lo = y_signed ? -128.0f : 0.0f, hi = y_signed ? 127.0f : 255.0f;
+        if (v < lo) v = lo;
+        else if (v > hi) v = hi;
+        const int32_t q = isnan(v) ? 0 : (int32_t)v; /* x86-64 NaN conversion, then the narrowing */
+        if (y_signed) ((int8_t *)y_q8)[o] = (int8_t)q;
+        else ((uint8_t *)y_q8)[o] = (uint8_t)q;
+      }
+    }
+  return 0;
+}
+
+int orc_conv_integer(const void *x, int x_dtype, const int64_t *x_shape, int x_rank, const void *w,
+                     int w_dtype, const int64_t *w_shape, const void *x_zp, const void *w_zp,
+                     int64_t w_zp_count, int64_t group, const int64_t *kernel_shape,
+                     const int64_t *strides, const int64_t *pads, const int64_t *dilations, int auto_pad,
+                     int32_t *y) {
+  const int32_t xz = x_zp ? read_byte_elem(x_zp, x_dtype, 0) : 0;
+  return conv_run(x, x_dtype, x_shape, x_rank, w, w_dtype, w_shape, xz, w_zp, w_zp_count, group, kernel_shape,
+                  strides, pads, dilations, auto_pad, y, NULL, 0, NULL, 0.0f, 0, NULL);
+}
+
+int orc_qlinear_conv(const void *x, int x_dtype, const int64_t *x_shape, int x_rank, float x_scale,
+                     int32_t x_zp, const void *w, int w_dtype, const int64_t *w_shape, const float *w_scale,
+                     int64_t w_scale_count, const void *w_zp, int64_t w_zp_count, float y_scale,
+                     int32_t y_zp, int y_signed, const int32_t *bias, int64_t group,
+                     const int64_t *kernel_shape, const int64_t *strides, const int64_t *pads,
+                     const int64_t *dilations, int auto_pad, void *y) {
+  const int64_t M = w_shape[0];
+  float *cs = (float *)malloc(sizeof(float) * (size_t)(w_scale_count > 0 ? w_scale_count : 1));
+  if (!cs) return 1;
+  for (int64_t i = 0; i < w_scale_count; ++i) cs[i] = x_scale * w_scale[i] / y_scale; /* :289 */
+  const int rc = conv_run(x, x_dtype, x_shape, x_rank, w, w_dtype, w_shape, x_zp, w_zp, w_zp_count, group,
+                          kernel_shape, strides, pads, dilations, auto_pad, NULL, cs,
+                          w_scale_count == M ? M : 1, bias, (float)y_zp, y_signed, y);
+  free(cs);
+  return rc;
+}
+
+/* ------------------------------------------------------------------------ */
 /* MatMul, km/kernel_matmul.cc:61-147 and :206-218.                          */
 
 typedef struct {

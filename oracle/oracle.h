@@ -136,6 +136,37 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
 int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_scale,
                                 uint8_t *y_zero_point);
 
+/* ---- ConvInteger (nn/kernel_conv_integer.cc:178-304) and QLinearConv
+ * (kq/kernel_qlinearconv.cc:178-340) ----
+ * x [N, C, spatial...] and w [M, C/group, kernel...] of INT8 or UINT8;
+ * spatial rank 1..ORC_MAX_RANK-2.  kernel_shape / strides / pads /
+ * dilations may be NULL (the reference's defaults); auto_pad is one of the
+ * ORC_AUTO_PAD_* values.  Output [N, M, out spatial...] (sizes from
+ * orc_conv_geometry).  ConvInteger: int32 accumulation that wraps; absent
+ * zero points are 0; w_zp has w_zp_count values (1 or M).  QLinearConv:
+ * int64 accumulation plus bias (may be NULL), then
+ * saturate(nearbyint((float)acc * (x_scale * w_scale[m] / y_scale)) + y_zp).
+ * Returns 0, or 1 for attributes or shapes the reference rejects. */
+#define ORC_AUTO_PAD_NOTSET 0
+#define ORC_AUTO_PAD_SAME_UPPER 1
+#define ORC_AUTO_PAD_SAME_LOWER 2
+#define ORC_AUTO_PAD_VALID 3
+int orc_conv_geometry(const int64_t *x_shape, int x_rank, const int64_t *w_shape,
+                      const int64_t *kernel_shape, const int64_t *strides, const int64_t *pads,
+                      const int64_t *dilations, int auto_pad, int64_t *k_out, int64_t *s_out,
+                      int64_t *d_out, int64_t *pads_out, int64_t *out_spatial);
+int orc_conv_integer(const void *x, int x_dtype, const int64_t *x_shape, int x_rank, const void *w,
+                     int w_dtype, const int64_t *w_shape, const void *x_zp, const void *w_zp,
+                     int64_t w_zp_count, int64_t group, const int64_t *kernel_shape,
+                     const int64_t *strides, const int64_t *pads, const int64_t *dilations, int auto_pad,
+                     int32_t *y);
+int orc_qlinear_conv(const void *x, int x_dtype, const int64_t *x_shape, int x_rank, float x_scale,
+                     int32_t x_zp, const void *w, int w_dtype, const int64_t *w_shape, const float *w_scale,
+                     int64_t w_scale_count, const void *w_zp, int64_t w_zp_count, float y_scale,
+                     int32_t y_zp, int y_signed, const int32_t *bias, int64_t group,
+                     const int64_t *kernel_shape, const int64_t *strides, const int64_t *pads,
+                     const int64_t *dilations, int auto_pad, void *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,16 @@ def _declare(L):
                                       ctypes.c_int, P, ctypes.c_int, ctypes.c_int64, P]
     L.orc_dynamic_quantize_linear.restype = ctypes.c_int
     L.orc_dynamic_quantize_linear.argtypes = [P, ctypes.c_int64, P, P, P]
+    L.orc_conv_geometry.restype = ctypes.c_int
+    L.orc_conv_geometry.argtypes = [P, ctypes.c_int, P, P, P, P, P, ctypes.c_int, P, P, P, P, P]
+    L.orc_conv_integer.restype = ctypes.c_int
+    L.orc_conv_integer.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int, P, P, P,
+                                   ctypes.c_int64, ctypes.c_int64, P, P, P, P, ctypes.c_int, P]
+    L.orc_qlinear_conv.restype = ctypes.c_int
+    L.orc_qlinear_conv.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_float, ctypes.c_int32,
+                                   P, ctypes.c_int, P, P, ctypes.c_int64, P, ctypes.c_int64,
+                                   ctypes.c_float, ctypes.c_int32, ctypes.c_int, P, ctypes.c_int64,
+                                   P, P, P, P, ctypes.c_int, P]
     L.orc_matmul_f32.restype = ctypes.c_int
     L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int]
@@ -313,4 +323,74 @@ def matmul_half(a_bits: np.ndarray, b_bits: np.ndarray, dtype: int, rows=None,
                                _ptr(_shape(b.shape)), b.ndim, dtype, _ptr(y), r0, r1, nthreads)
     if rc:
         raise ValueError(f"matmul_half error {rc}")
+    return y
+
+
+# ---- ConvInteger / QLinearConv ----------------------------------------------
+
+AUTO_PAD = {"NOTSET": 0, "SAME_UPPER": 1, "SAME_LOWER": 2, "VALID": 3}
+
+
+def _opt(v):
+    return None if v is None else _shape(v)
+
+
+def conv_geometry(x_shape, w_shape, kernel_shape=None, strides=None, pads=None, dilations=None,
+                  auto_pad="NOTSET"):
+    """(kernel, strides, dilations, resolved pads, output spatial sizes) as the
+    reference resolves them; raises ValueError where it rejects."""
+    sr = len(x_shape) - 2
+    outs = [np.zeros(max(sr, 1) * (2 if i == 3 else 1), np.int64) for i in range(5)]
+    args = [_opt(v) for v in (kernel_shape, strides, pads, dilations)]
+    rc = lib().orc_conv_geometry(_ptr(_shape(x_shape)), len(x_shape), _ptr(_shape(w_shape)),
+                                 *[None if a is None else _ptr(a) for a in args], AUTO_PAD[auto_pad],
+                                 *[_ptr(o) for o in outs])
+    if rc:
+        raise ValueError("conv attributes rejected")
+    return tuple(tuple(int(v) for v in o) for o in outs)
+
+
+def _conv_args(x, w, group, kernel_shape, strides, pads, dilations, auto_pad):
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w)
+    geo = conv_geometry(x.shape, w.shape, kernel_shape, strides, pads, dilations, auto_pad)
+    out_shape = (x.shape[0], w.shape[0]) + geo[4]
+    attrs = [_opt(v) for v in (kernel_shape, strides, pads, dilations)]
+    return x, w, out_shape, attrs
+
+
+def conv_integer(x, x_dtype, w, w_dtype, x_zp=None, w_zp=None, group=1, kernel_shape=None, strides=None,
+                 pads=None, dilations=None, auto_pad="NOTSET"):
+    """ConvInteger on raw int8 / uint8 storage: int32 output (wrapping)."""
+    x, w, out_shape, attrs = _conv_args(x, w, group, kernel_shape, strides, pads, dilations, auto_pad)
+    xz = None if x_zp is None else np.ascontiguousarray(x_zp).reshape(-1)
+    wz = None if w_zp is None else np.ascontiguousarray(w_zp).reshape(-1)
+    y = np.zeros(out_shape, np.int32)
+    rc = lib().orc_conv_integer(_ptr(x), x_dtype, _ptr(_shape(x.shape)), x.ndim, _ptr(w), w_dtype,
+                                _ptr(_shape(w.shape)), None if xz is None else _ptr(xz),
+                                None if wz is None else _ptr(wz), 0 if wz is None else wz.size, group,
+                                *[None if a is None else _ptr(a) for a in attrs], AUTO_PAD[auto_pad],
+                                _ptr(y))
+    if rc:
+        raise ValueError(f"conv_integer error {rc}")
+    return y
+
+
+def qlinear_conv(x, x_dtype, x_scale, x_zp, w, w_dtype, w_scale, w_zp, y_scale, y_zp, y_dtype, bias=None,
+                 group=1, kernel_shape=None, strides=None, pads=None, dilations=None, auto_pad="NOTSET"):
+    """QLinearConv on raw storage; scales are float32 values (w_scale and w_zp
+    scalar or length M), bias int32 length M or None."""
+    x, w, out_shape, attrs = _conv_args(x, w, group, kernel_shape, strides, pads, dilations, auto_pad)
+    ws = np.ascontiguousarray(np.asarray(w_scale, np.float32).reshape(-1))
+    wz = np.ascontiguousarray(np.asarray(w_zp).reshape(-1).astype(_NP_OF[w_dtype]))
+    b = None if bias is None else np.ascontiguousarray(np.asarray(bias, np.int32).reshape(-1))
+    y = np.zeros(out_shape, np.int8 if y_dtype == INT8 else np.uint8)
+    rc = lib().orc_qlinear_conv(_ptr(x), x_dtype, _ptr(_shape(x.shape)), x.ndim, float(np.float32(x_scale)),
+                                int(x_zp), _ptr(w), w_dtype, _ptr(_shape(w.shape)), _ptr(ws), ws.size,
+                                _ptr(wz), wz.size, float(np.float32(y_scale)), int(y_zp),
+                                int(y_dtype == INT8), None if b is None else _ptr(b), group,
+                                *[None if a is None else _ptr(a) for a in attrs], AUTO_PAD[auto_pad],
+                                _ptr(y))
+    if rc:
+        raise ValueError(f"qlinear_conv error {rc}")
     return y
