@@ -146,6 +146,55 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
                                       onnxl_amd_tensor *y_scale, onnxl_amd_tensor *y_zero_point,
                                       void *stream);
 
+/* Convolution attributes, as the reference's ConvInteger / QLinearConv
+ * Attributes: n_* entries of each array are used, 0 means the attribute is
+ * absent (kernel_shape from w, strides and dilations 1, pads 0).  pads holds
+ * the begin values of every spatial dim, then the end values. */
+#define ONNXL_AMD_MAX_CONV_SPATIAL 3
+enum {
+  ONNXL_AMD_AUTO_PAD_NOTSET = 0,
+  ONNXL_AMD_AUTO_PAD_SAME_UPPER = 1,
+  ONNXL_AMD_AUTO_PAD_SAME_LOWER = 2,
+  ONNXL_AMD_AUTO_PAD_VALID = 3
+};
+typedef struct onnxl_amd_conv_attrs {
+  int32_t n_kernel_shape, n_strides, n_pads, n_dilations;
+  int64_t kernel_shape[ONNXL_AMD_MAX_CONV_SPATIAL];
+  int64_t strides[ONNXL_AMD_MAX_CONV_SPATIAL];
+  int64_t pads[2 * ONNXL_AMD_MAX_CONV_SPATIAL];
+  int64_t dilations[ONNXL_AMD_MAX_CONV_SPATIAL];
+  int64_t group;
+  int32_t auto_pad; /* ONNXL_AMD_AUTO_PAD_* */
+} onnxl_amd_conv_attrs;
+
+/* Output dims [N, M, out spatial...] of a convolution, with the reference's
+ * attribute resolution (nn/kernel_conv_integer.cc:24-54, :107-141;
+ * kq/kernel_qlinearconv.cc:53-119), for callers that allocate the output. */
+int onnxl_amd_conv_shape(const int64_t *x_dims, int32_t x_rank, const int64_t *w_dims, int32_t w_rank,
+                         const onnxl_amd_conv_attrs *attrs, int64_t *y_dims, int32_t *y_rank);
+
+/* ConvInteger: x [N, C, spatial...] and w [M, C/group, kernel...] of INT8 or
+ * UINT8, optional scalar x_zero_point and scalar or per-output-channel
+ * w_zero_point; y INT32 [N, M, out...], the int32 sums of
+ * (x - x_zp)(w - w_zp) over the taps inside x (wrapping like the
+ * reference's int32 accumulator).  1 to 3 spatial dims.
+ * Replaces kernel::ConvInteger::operator(), nn/kernel_conv_integer.cc:178-304. */
+int onnxl_amd_conv_integer(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w,
+                           const onnxl_amd_tensor *x_zero_point, const onnxl_amd_tensor *w_zero_point,
+                           const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y, void *stream);
+
+/* QLinearConv: as ConvInteger with int64 sums, plus the optional INT32 bias B
+ * [M], then y = saturate(nearbyint((float)sum * (x_scale * w_scale[m] /
+ * y_scale)) + y_zero_point); FLOAT scalar x_scale / y_scale, scalar or
+ * per-output-channel w_scale and w_zero_point; y dtype = y_zero_point's.
+ * Replaces kernel::QLinearConv::operator(), kq/kernel_qlinearconv.cc:178-340. */
+int onnxl_amd_qlinear_conv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                           const onnxl_amd_tensor *x_zero_point, const onnxl_amd_tensor *w,
+                           const onnxl_amd_tensor *w_scale, const onnxl_amd_tensor *w_zero_point,
+                           const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zero_point,
+                           const onnxl_amd_tensor *B, const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y,
+                           void *stream);
+
 /* MatMul for FLOAT16 / BFLOAT16 operands (fp32 accumulation, output rounded
  * to the input dtype).  Replaces kernel::MatMul::operator()(a, b, Tensor &)
  * for those dtypes, km/kernel_matmul.cc:242-253 (compute :61-147, :206-218). */

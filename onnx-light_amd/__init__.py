@@ -90,6 +90,12 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_quantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, ctypes.c_int32, TP,
                                                 ctypes.c_void_p]
         L.onnxl_amd_dynamic_quantize_linear.argtypes = [TP, TP, TP, TP, ctypes.c_void_p]
+        CA = ctypes.POINTER(ConvAttrs)
+        L.onnxl_amd_conv_shape.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
+                                           ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, CA,
+                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)]
+        L.onnxl_amd_conv_integer.argtypes = [TP, TP, TP, TP, CA, TP, ctypes.c_void_p]
+        L.onnxl_amd_qlinear_conv.argtypes = [TP] * 9 + [CA, TP, ctypes.c_void_p]
         L.onnxl_amd_prepare_weight_size.argtypes = [TP, ctypes.POINTER(ctypes.c_int64)]
         L.onnxl_amd_prepare_weight.argtypes = [TP, TP, ctypes.c_void_p]
         L.onnxl_amd_synchronize.argtypes = [ctypes.c_void_p]
@@ -211,6 +217,36 @@ def prepare_weight(x, x_dtype: int, x_shape=None) -> PreparedWeight:
                                           ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
     out._keep = storage
     return PreparedWeight(storage, out)
+
+
+class ConvAttrs(ctypes.Structure):
+    """onnxl_amd_conv_attrs: the reference's Attributes of ConvInteger /
+    QLinearConv (empty lists are the absent attributes)."""
+    _fields_ = [("n_kernel_shape", ctypes.c_int32), ("n_strides", ctypes.c_int32),
+                ("n_pads", ctypes.c_int32), ("n_dilations", ctypes.c_int32),
+                ("kernel_shape", ctypes.c_int64 * 3), ("strides", ctypes.c_int64 * 3),
+                ("pads", ctypes.c_int64 * 6), ("dilations", ctypes.c_int64 * 3),
+                ("group", ctypes.c_int64), ("auto_pad", ctypes.c_int32)]
+
+
+AUTO_PAD = {"NOTSET": 0, "SAME_UPPER": 1, "SAME_LOWER": 2, "VALID": 3}
+
+
+def conv_attrs(kernel_shape=None, strides=None, pads=None, dilations=None, group=1,
+               auto_pad="NOTSET") -> ConvAttrs:
+    a = ConvAttrs()
+    for name, vals, cap in (("kernel_shape", kernel_shape, 3), ("strides", strides, 3),
+                            ("pads", pads, 6), ("dilations", dilations, 3)):
+        vals = list(vals or [])
+        if len(vals) > cap:
+            raise Unsupported(f"'{name}' with {len(vals)} entries: at most 3 spatial dimensions")
+        setattr(a, "n_" + name, len(vals))
+        arr = getattr(a, name)
+        for i, v in enumerate(vals):
+            arr[i] = int(v)
+    a.group = int(group)
+    a.auto_pad = AUTO_PAD[auto_pad] if isinstance(auto_pad, str) else int(auto_pad)
+    return a
 
 
 def _stream_of(*ts):
@@ -390,6 +426,46 @@ def dynamic_quantize_linear(x, out=None, check: bool = True):
     return y, y_scale, y_zp
 
 
+def conv_shape(x_shape, w_shape, attrs: ConvAttrs) -> tuple:
+    xs = (ctypes.c_int64 * MAX_RANK)(*x_shape)
+    ws = (ctypes.c_int64 * MAX_RANK)(*w_shape)
+    out = (ctypes.c_int64 * MAX_RANK)()
+    r = ctypes.c_int32(0)
+    _check(lib().onnxl_amd_conv_shape(xs, len(x_shape), ws, len(w_shape), ctypes.byref(attrs), out,
+                                      ctypes.byref(r)))
+    return tuple(out[i] for i in range(r.value))
+
+
+def conv_integer(x, w, x_zero_point=None, w_zero_point=None, out=None, **attrs):
+    """kernel::ConvInteger (nn/kernel_conv_integer.cc:152-304); attrs are
+    kernel_shape, strides, pads, dilations, group, auto_pad."""
+    torch = _torch()
+    a = conv_attrs(**attrs)
+    if out is None:
+        out = _empty(conv_shape(_shape_of(x), _shape_of(w), a), torch.int32, _device_of(x, w))
+    _check(lib().onnxl_amd_conv_integer(describe(x), describe(w), describe(x_zero_point),
+                                        describe(w_zero_point), ctypes.byref(a), describe(out),
+                                        _stream_of(x, w, out)))
+    return out
+
+
+def qlinear_conv(x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point, B=None,
+                 out=None, **attrs):
+    """kernel::QLinearConv (kq/kernel_qlinearconv.cc:146-340); the output
+    dtype follows y_zero_point."""
+    torch = _torch()
+    a = conv_attrs(**attrs)
+    if out is None:
+        ydt = y_zero_point.dtype
+        if isinstance(y_zero_point, np.ndarray):
+            ydt = torch.int8 if ydt == np.int8 else torch.uint8
+        out = _empty(conv_shape(_shape_of(x), _shape_of(w), a), ydt, _device_of(x, w))
+    ds = [describe(t) for t in (x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale,
+                                y_zero_point, B)]
+    _check(lib().onnxl_amd_qlinear_conv(*ds, ctypes.byref(a), describe(out), _stream_of(x, w, out)))
+    return out
+
+
 class MatMulInteger:
     """Kernel-class mirror of kernel::MatMulInteger."""
     name = "onnxl_amd:GPU:ai.onnx:MatMulInteger"
@@ -425,6 +501,24 @@ class MatMul:
         return matmul(a, b, out)
 
 
+class ConvInteger:
+    """Kernel-class mirror of kernel::ConvInteger."""
+    name = "onnxl_amd:GPU:ai.onnx:ConvInteger"
+
+    def __call__(self, x, w, x_zero_point=None, w_zero_point=None, out=None, **attrs):
+        return conv_integer(x, w, x_zero_point, w_zero_point, out, **attrs)
+
+
+class QLinearConv:
+    """Kernel-class mirror of kernel::QLinearConv."""
+    name = "onnxl_amd:GPU:ai.onnx:QLinearConv"
+
+    def __call__(self, x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point, B=None,
+                 out=None, **attrs):
+        return qlinear_conv(x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point, B, out,
+                            **attrs)
+
+
 class QuantizeLinear:
     """Kernel-class mirror of kernel::QuantizeLinear (axis defaults to 1 as in
     QuantizeLinear::Run, kq/kernel_quantizelinear.cc:927)."""
@@ -448,7 +542,8 @@ class DynamicQuantizeLinear:
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
            "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul,
            "ai.onnx:QuantizeLinear": QuantizeLinear,
-           "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear}
+           "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear,
+           "ai.onnx:ConvInteger": ConvInteger, "ai.onnx:QLinearConv": QLinearConv}
 
 
 class Prepared:

@@ -667,6 +667,312 @@ int DynamicQuantizeLinear(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, onnxl_
 }
 
 // ---------------------------------------------------------------------------
+// ConvInteger (nn/kernel_conv_integer.cc) and QLinearConv
+// (kq/kernel_qlinearconv.cc).
+
+constexpr const char *kCiName = "kernel::ConvInteger";
+constexpr const char *kQcName = "kernel::QLinearConv";
+
+struct ConvResolved {
+  Shape k, s, d, pads, out;
+};
+
+// ResolveAttributes + ComputeOutputSpatial (kernel_conv_integer.cc:24-54,
+// :107-141; kernel_qlinearconv.cc:53-119).  The rank checks run first so a
+// malformed x cannot index past its shape.
+ConvResolved ResolveConv(const Shape &xs, const Shape &ws, const onnxl_amd_conv_attrs *a, const char *name) {
+  OLA_ENFORCE(a != nullptr, name, ": attributes are required.");
+  OLA_ENFORCE(xs.size() >= 3, name, ": x must have rank >= 3.");
+  OLA_ENFORCE(ws.size() == xs.size(), name, ": w rank must match x rank.");
+  OLA_ENFORCE(a->n_kernel_shape >= 0 && a->n_kernel_shape <= ONNXL_AMD_MAX_CONV_SPATIAL && a->n_strides >= 0 &&
+                  a->n_strides <= ONNXL_AMD_MAX_CONV_SPATIAL && a->n_dilations >= 0 &&
+                  a->n_dilations <= ONNXL_AMD_MAX_CONV_SPATIAL && a->n_pads >= 0 &&
+                  a->n_pads <= 2 * ONNXL_AMD_MAX_CONV_SPATIAL,
+              name, ": attribute counts out of range.");
+  const size_t sr = xs.size() - 2;
+  ConvResolved r;
+  r.k = a->n_kernel_shape ? Shape(a->kernel_shape, a->kernel_shape + a->n_kernel_shape)
+                          : Shape(ws.begin() + 2, ws.end());
+  OLA_ENFORCE(r.k.size() == sr, name, ": 'kernel_shape' size must match input spatial rank.");
+  r.s = a->n_strides ? Shape(a->strides, a->strides + a->n_strides) : Shape(sr, 1);
+  OLA_ENFORCE(r.s.size() == sr, name, ": 'strides' size must match input spatial rank.");
+  r.d = a->n_dilations ? Shape(a->dilations, a->dilations + a->n_dilations) : Shape(sr, 1);
+  OLA_ENFORCE(r.d.size() == sr, name, ": 'dilations' size must match input spatial rank.");
+  if (a->auto_pad == ONNXL_AMD_AUTO_PAD_NOTSET) {
+    r.pads = a->n_pads ? Shape(a->pads, a->pads + a->n_pads) : Shape(2 * sr, 0);
+    OLA_ENFORCE(r.pads.size() == 2 * sr, name, ": 'pads' size must be 2 * spatial rank.");
+  } else {
+    OLA_ENFORCE(a->auto_pad == ONNXL_AMD_AUTO_PAD_SAME_UPPER || a->auto_pad == ONNXL_AMD_AUTO_PAD_SAME_LOWER ||
+                    a->auto_pad == ONNXL_AMD_AUTO_PAD_VALID,
+                name, ": 'auto_pad' must be NOTSET/SAME_UPPER/SAME_LOWER/VALID.");
+    r.pads.assign(2 * sr, 0);
+  }
+  r.out.assign(sr, 0);
+  for (size_t i = 0; i < sr; ++i) {
+    const int64_t in = xs[i + 2], st = r.s[i];
+    OLA_ENFORCE(st > 0 && r.d[i] > 0 && r.k[i] > 0, name, ": strides, dilations and kernel_shape must be positive.");
+    const int64_t eff_k = (r.k[i] - 1) * r.d[i] + 1;
+    if (a->auto_pad == ONNXL_AMD_AUTO_PAD_VALID) {
+      r.out[i] = (in - eff_k) / st + 1;
+    } else if (a->auto_pad == ONNXL_AMD_AUTO_PAD_NOTSET) {
+      r.out[i] = (in + r.pads[i] + r.pads[i + sr] - eff_k) / st + 1;
+    } else {
+      const int64_t out = (in + st - 1) / st;
+      const int64_t need = std::max<int64_t>(0, (out - 1) * st + eff_k - in);
+      if (a->auto_pad == ONNXL_AMD_AUTO_PAD_SAME_UPPER) {
+        r.pads[i] = need / 2;
+        r.pads[i + sr] = need - need / 2;
+      } else {
+        r.pads[i + sr] = need / 2;
+        r.pads[i] = need - need / 2;
+      }
+      r.out[i] = out;
+    }
+  }
+  return r;
+}
+
+// x / w validation shared by both kernels (kernel_conv_integer.cc:74-88,
+// kernel_qlinearconv.cc:178-192).
+void CheckConvOperands(const onnxl_amd_tensor &x, const onnxl_amd_tensor &w, int64_t group, const char *name) {
+  OLA_ENFORCE(IsInt8OrUint8(x.data_type), name, ": x must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(w.data_type), name, ": w must be INT8 or UINT8.");
+  OLA_ENFORCE(group >= 1, name, ": 'group' must be >= 1.");
+  OLA_ENFORCE(x.dims[1] == w.dims[1] * group, name, ": x.shape[1] must equal w.shape[1] * group.");
+  OLA_ENFORCE(w.dims[0] % group == 0, name, ": w.shape[0] must be divisible by group.");
+}
+
+Shape ConvOutShape(const onnxl_amd_tensor &x, const onnxl_amd_tensor &w, const ConvResolved &r) {
+  Shape out = {x.dims[0], w.dims[0]};
+  out.insert(out.end(), r.out.begin(), r.out.end());
+  return out;
+}
+
+// Geometry for the kernels; the GPU kernels take up to 3 spatial dims and
+// the kernel_shape the weights actually have (the reference indexes w with
+// the kernel_shape attribute).
+ConvGeom MakeConvGeom(const onnxl_amd_tensor &x, const onnxl_amd_tensor &w, const ConvResolved &r, int64_t group,
+                      const char *name) {
+  const size_t sr = r.k.size();
+  if (sr > 3) throw Unsupported(Cat(name, ": more than 3 spatial dimensions has no GPU kernel"));
+  for (size_t i = 0; i < sr; ++i)
+    if (r.k[i] != w.dims[i + 2]) throw Unsupported(Cat(name, ": kernel_shape differs from w's shape"));
+  ConvGeom g{};
+  g.N = x.dims[0];
+  g.C = x.dims[1];
+  g.G = group;
+  g.cpg = w.dims[1];
+  g.M = w.dims[0];
+  g.Mg = g.M / group;
+  for (int i = 0; i < 3; ++i) {
+    g.in[i] = g.out[i] = 1;
+    g.k[i] = 1;
+    g.s[i] = g.d[i] = 1;
+    g.pb[i] = 0;
+  }
+  for (size_t i = 0; i < sr; ++i) {
+    const size_t j = 3 - sr + i;
+    g.in[j] = x.dims[2 + i];
+    g.out[j] = r.out[i];
+    g.k[j] = (int)r.k[i];
+    g.s[j] = r.s[i];
+    g.d[j] = r.d[i];
+    g.pb[j] = r.pads[i];
+  }
+  g.in_size = g.in[0] * g.in[1] * g.in[2];
+  g.P = g.out[0] * g.out[1] * g.out[2];
+  g.ks = (int64_t)g.k[0] * g.k[1] * g.k[2];
+  g.Kc = g.cpg * g.ks;
+  return g;
+}
+
+bool PresentOptional(const onnxl_amd_tensor *t) { return !(Absent(t) || (t->rank == 0 && t->size_bytes == 0)); }
+
+// The GEMM over im2col columns: A = W as [G, Mg, Kc] (broadcast over the
+// batch), B = Col [N, G, Kc, P], Y = [N, G, Mg, P] int32 sums.  a_zp: Mg
+// per-row weight zero points on device (group 1 only), or nullptr with the
+// scalar w_zp.
+void LaunchConvGemm(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t *a_zp, int32_t w_zp,
+                    const uint8_t *col, int x_u8, int32_t x_zp, int32_t *y, hipStream_t stream) {
+  IGemmParams p{};
+  p.A = reinterpret_cast<const int8_t *>(w);
+  p.B = reinterpret_cast<const int8_t *>(col);
+  p.Y = y;
+  p.M = g.Mg;
+  p.N = g.P;
+  p.K = g.Kc;
+  p.batch = g.N * g.G;
+  p.bm.rank = 2;
+  p.bm.dims[0] = g.N;
+  p.bm.dims[1] = g.G;
+  p.bm.a_stride[0] = 0;
+  p.bm.a_stride[1] = g.Mg * g.Kc;
+  p.bm.b_stride[0] = g.G * g.Kc * g.P;
+  p.bm.b_stride[1] = g.Kc * g.P;
+  p.a_u8 = w_u8;
+  p.b_u8 = x_u8;
+  p.a_zp = a_zp;
+  p.b_zp = nullptr;
+  p.alpha_scalar = (w_u8 ? 128 : 0) - (a_zp ? 0 : w_zp);
+  p.beta_scalar = (x_u8 ? 128 : 0) - x_zp;
+  p.need_cb = a_zp != nullptr || p.alpha_scalar != 0;
+  p.need_ra = p.beta_scalar != 0;
+  p.epilogue = kEpiInt32;
+  LaunchIGemm(p, stream);
+}
+
+int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnxl_amd_tensor *x_zp,
+                const onnxl_amd_tensor *w_zp, const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y,
+                hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && !Absent(w) && y, kCiName, ": x, w and the output are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(w, "w");
+  CheckDescriptor(x_zp, "x_zero_point");
+  CheckDescriptor(w_zp, "w_zero_point");
+  CheckDescriptor(y, "y");
+  const ConvResolved r = ResolveConv(ShapeOf(*x), ShapeOf(*w), attrs, kCiName);
+  CheckConvOperands(*x, *w, attrs->group, kCiName);  // ValidateInputs, :74-88
+  const int64_t M = w->dims[0];
+  const bool xz_present = PresentOptional(x_zp), wz_present = PresentOptional(w_zp);
+  if (xz_present) {  // :88-96
+    OLA_ENFORCE(x_zp->data_type == x->data_type, kCiName, ": x_zero_point dtype must match x.");
+    OLA_ENFORCE(NumElements(*x_zp) == 1, kCiName, ": x_zero_point must be a scalar.");
+  }
+  if (wz_present) {  // :97-106
+    OLA_ENFORCE(w_zp->data_type == w->data_type, kCiName, ": w_zero_point dtype must match w.");
+    const int64_t numel = NumElements(*w_zp);
+    OLA_ENFORCE(numel == 1 || numel == M, kCiName, ": w_zero_point must be a scalar or 1-D of length M.");
+  }
+  const Shape out_shape = ConvOutShape(*x, *w, r);  // :184-201
+  OLA_ENFORCE(y->data_type == kInt32, kCiName, " preallocated output must be INT32.");
+  OLA_ENFORCE(ShapeOf(*y) == out_shape, kCiName, " preallocated output shape mismatch.");
+  OLA_ENFORCE(y->size_bytes == NumElements(out_shape) * 4, kCiName,
+              " preallocated output buffer has unexpected size.");
+  const ConvGeom g = MakeConvGeom(*x, *w, r, attrs->group, kCiName);
+  // :240-246: per-channel only for a 1-D zero point of length M
+  const bool w_per_channel = wz_present && w_zp->rank == 1 && w_zp->dims[0] == M;
+  const int32_t xz = xz_present ? ReadIntElem(*x_zp, 0) : 0;
+  const int32_t wz = wz_present && !w_per_channel ? ReadIntElem(*w_zp, 0) : 0;
+  const bool gemm = (g.G == 1 || !w_per_channel) && g.Kc > 0;
+  const size_t col_bytes = gemm ? ConvColBytes(g) : 0;
+  Staging st(stream, col_bytes, {x, w, w_per_channel ? w_zp : nullptr}, {y});
+  const uint8_t *xd = static_cast<const uint8_t *>(st.In(x));
+  const uint8_t *wd = static_cast<const uint8_t *>(st.In(w));
+  const uint8_t *wzd = w_per_channel ? static_cast<const uint8_t *>(st.In(w_zp)) : nullptr;
+  int32_t *yd = static_cast<int32_t *>(st.Out(y));
+  if (g.N * g.M * g.P > 0) {
+    if (gemm) {
+      uint8_t *col = static_cast<uint8_t *>(st.Extra());
+      LaunchImToCol(g, xd, (uint8_t)xz, col, stream);
+      LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, yd, stream);
+    } else {
+      LaunchDirectConv(g, xd, x->data_type == kUint8, (uint8_t)xz, wd, w->data_type == kUint8, wzd, wz, nullptr,
+                       yd, stream);
+    }
+  }
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+float QcReadFloat(const onnxl_amd_tensor &t, int64_t idx) {  // ReadFloatElem, :47-51
+  OLA_ENFORCE(t.data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
+  float v;
+  ReadBytes(t, idx * 4, &v, 4);
+  return v;
+}
+
+int32_t QcReadScalarInt(const onnxl_amd_tensor &t, const char *name) {  // ReadScalarInt, :38-45
+  OLA_ENFORCE(NumElements(t) == 1, kQcName, ": '", name, "' must be a scalar.");
+  return ReadIntElem(t, 0);
+}
+
+int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, const onnxl_amd_tensor *x_zp,
+                const onnxl_amd_tensor *w, const onnxl_amd_tensor *w_scale, const onnxl_amd_tensor *w_zp,
+                const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zp, const onnxl_amd_tensor *bias,
+                const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y, hipStream_t stream) {
+  const onnxl_amd_tensor *req[] = {x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, y};
+  for (auto *t : req) OLA_ENFORCE(!Absent(t), kQcName, ": the 8 inputs and the output are required.");
+  const char *names[] = {"x", "x_scale", "x_zero_point", "w", "w_scale", "w_zero_point", "y_scale",
+                         "y_zero_point", "y"};
+  for (int i = 0; i < 9; ++i) CheckDescriptor(req[i], names[i]);
+  CheckDescriptor(bias, "B");
+  const ConvResolved r = ResolveConv(ShapeOf(*x), ShapeOf(*w), attrs, kQcName);  // :178-180
+  OLA_ENFORCE(IsInt8OrUint8(x->data_type), kQcName, ": x must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(w->data_type), kQcName, ": w must be INT8 or UINT8.");
+  OLA_ENFORCE(IsInt8OrUint8(y_zp->data_type), kQcName, ": y_zero_point must be INT8 or UINT8.");
+  CheckConvOperands(*x, *w, attrs->group, kQcName);
+  const Shape out_shape = ConvOutShape(*x, *w, r);  // :194-199
+  OLA_ENFORCE(y->data_type == y_zp->data_type, kQcName, ": output dtype must match y_zero_point.");
+  OLA_ENFORCE(ShapeOf(*y) == out_shape, kQcName, ": preallocated output shape mismatch.");
+  OLA_ENFORCE(y->size_bytes == NumElements(out_shape), kQcName, ": preallocated output buffer has unexpected size.");
+  const int32_t xz = QcReadScalarInt(*x_zp, "x_zero_point");  // :200-205
+  const int32_t yz = QcReadScalarInt(*y_zp, "y_zero_point");
+  OLA_ENFORCE(x_zp->data_type == x->data_type, kQcName, ": x_zero_point dtype must match x.");
+  OLA_ENFORCE(w_zp->data_type == w->data_type, kQcName, ": w_zero_point dtype must match w.");
+  const float xs = QcReadFloat(*x_scale, 0), ys = QcReadFloat(*y_scale, 0);  // :207-211
+  OLA_ENFORCE(ys != 0.0f, kQcName, ": y_scale must be non-zero.");
+  OLA_ENFORCE(NumElements(*x_scale) == 1 && NumElements(*y_scale) == 1, kQcName,
+              ": 'x_scale' and 'y_scale' must be scalar.");
+  const int64_t M = w->dims[0];
+  const int64_t ws_n = NumElements(*w_scale), wz_n = NumElements(*w_zp);  // :213-227
+  OLA_ENFORCE(ws_n == 1 || ws_n == M, kQcName, ": 'w_scale' must be scalar or length-M.");
+  OLA_ENFORCE(wz_n == 1 || wz_n == M, kQcName, ": 'w_zero_point' must be scalar or length-M.");
+  OLA_ENFORCE(w_scale->data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
+  const bool has_bias = PresentOptional(bias);  // :229-238
+  if (has_bias) {
+    OLA_ENFORCE(bias->data_type == kInt32, kQcName, ": B must be INT32.");
+    OLA_ENFORCE(NumElements(*bias) == M, kQcName, ": B must be 1-D with length M.");
+  }
+  const ConvGeom g = MakeConvGeom(*x, *w, r, attrs->group, kQcName);
+  const bool w_per_channel = wz_n == M && M > 1;
+  const int32_t wz = w_per_channel ? 0 : ReadIntElem(*w_zp, 0);
+  // The reference accumulates in int64 (:306-330).  The GEMM's int32 sums are
+  // exact while Kc * max|x - x_zp| * max|w - w_zp| < 2^31; the bias is added
+  // in int64 afterwards.  Otherwise, and for grouped convolutions with
+  // per-channel weight zero points, the direct kernel sums in int64.
+  auto span = [](int32_t dt, int32_t z) -> int64_t {
+    const int64_t lo = dt == kInt8 ? -128 : 0, hi = dt == kInt8 ? 127 : 255;
+    return std::max<int64_t>(std::llabs(lo - z), std::llabs(hi - z));
+  };
+  const int64_t w_span = w_per_channel ? 255 : span(w->data_type, wz);
+  const bool exact32 = (double)g.Kc * (double)span(x->data_type, xz) * (double)w_span < 2147483648.0;
+  const bool gemm = exact32 && (g.G == 1 || !w_per_channel) && g.Kc > 0;
+  const size_t col_bytes = gemm ? ConvColBytes(g) : 0;
+  const size_t acc_off = Scratch::Round(col_bytes);
+  const size_t acc_bytes = gemm ? (size_t)(g.N * g.M * g.P) * 4 : 0;
+  Staging st(stream, acc_off + acc_bytes, {x, w, w_scale, w_per_channel ? w_zp : nullptr, has_bias ? bias : nullptr},
+             {y});
+  const uint8_t *xd = static_cast<const uint8_t *>(st.In(x));
+  const uint8_t *wd = static_cast<const uint8_t *>(st.In(w));
+  const uint8_t *wzd = w_per_channel ? static_cast<const uint8_t *>(st.In(w_zp)) : nullptr;
+  ConvQuant q{};
+  q.x_scale = xs;
+  q.y_scale = ys;
+  q.w_scale = static_cast<const float *>(st.In(w_scale));
+  q.w_scale_per_channel = ws_n == M && M > 1;
+  q.bias = has_bias ? static_cast<const int32_t *>(st.In(bias)) : nullptr;
+  const bool y_signed = y->data_type == kInt8;
+  q.zy = (float)yz;
+  q.qmin = y_signed ? -128.f : 0.f;
+  q.qmax = y_signed ? 127.f : 255.f;
+  uint8_t *yd = static_cast<uint8_t *>(st.Out(y));
+  if (g.N * g.M * g.P > 0) {
+    if (gemm) {
+      uint8_t *col = static_cast<uint8_t *>(st.Extra());
+      int32_t *acc = reinterpret_cast<int32_t *>(static_cast<char *>(st.Extra()) + acc_off);
+      LaunchImToCol(g, xd, (uint8_t)xz, col, stream);
+      LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, acc, stream);
+      LaunchConvRequant(g, acc, q, yd, stream);
+    } else {
+      LaunchDirectConv(g, xd, x->data_type == kUint8, (uint8_t)xz, wd, w->data_type == kUint8, wzd, wz, &q, yd,
+                       stream);
+    }
+  }
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Cast FLOAT -> FLOAT16 / BFLOAT16.
 
 int Cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, hipStream_t stream) {
@@ -947,6 +1253,44 @@ int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tenso
                                 onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DequantizeLinear(x, x_scale, x_zero_point, axis, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_conv_shape(const int64_t *x_dims, int32_t x_rank, const int64_t *w_dims, int32_t w_rank,
+                         const onnxl_amd_conv_attrs *attrs, int64_t *y_dims, int32_t *y_rank) {
+  return Guard([&] {
+    OLA_ENFORCE(x_dims && w_dims && y_dims && y_rank && x_rank >= 0 && x_rank <= ONNXL_AMD_MAX_RANK &&
+                    w_rank >= 0 && w_rank <= ONNXL_AMD_MAX_RANK,
+                "conv_shape: invalid arguments.");
+    const Shape xs(x_dims, x_dims + x_rank), ws(w_dims, w_dims + w_rank);
+    const ConvResolved r = ResolveConv(xs, ws, attrs, "kernel::Conv");
+    OLA_ENFORCE(attrs->group >= 1 && ws[0] % attrs->group == 0 && xs[1] == ws[1] * attrs->group,
+                "kernel::Conv: x.shape[1] must equal w.shape[1] * group.");
+    y_dims[0] = xs[0];
+    y_dims[1] = ws[0];
+    for (size_t i = 0; i < r.out.size(); ++i) y_dims[2 + i] = r.out[i];
+    *y_rank = (int32_t)(2 + r.out.size());
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_conv_integer(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w,
+                           const onnxl_amd_tensor *x_zero_point, const onnxl_amd_tensor *w_zero_point,
+                           const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return ConvInteger(x, w, x_zero_point, w_zero_point, attrs, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_qlinear_conv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                           const onnxl_amd_tensor *x_zero_point, const onnxl_amd_tensor *w,
+                           const onnxl_amd_tensor *w_scale, const onnxl_amd_tensor *w_zero_point,
+                           const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zero_point,
+                           const onnxl_amd_tensor *B, const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y,
+                           void *stream) {
+  return Guard([&] {
+    return QLinearConv(x, x_scale, x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point, B, attrs, y,
+                       static_cast<hipStream_t>(stream));
   });
 }
 

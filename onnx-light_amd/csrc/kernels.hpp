@@ -68,6 +68,36 @@ struct IGemmParams {
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// ConvInteger / QLinearConv.  Spatial dims are right-aligned into 3 slots
+// (missing leading dims have size 1, kernel 1, stride 1, dilation 1, pad 0).
+struct ConvGeom {
+  int64_t N, C, G, cpg, M, Mg;
+  int64_t in[3], out[3];
+  int k[3];
+  int64_t s[3], d[3], pb[3];  // stride, dilation, leading pad
+  int64_t in_size, P, ks, Kc;  // input plane size, output positions, kernel taps, cpg * ks
+};
+
+// QLinearConv requantization: y = saturate(rint((float)(acc + bias[m]) *
+// (x_scale * w_scale[m] / y_scale)) + zy).
+struct ConvQuant {
+  float x_scale, y_scale;
+  const float *w_scale;  // device, 1 or M values
+  int w_scale_per_channel;
+  const int32_t *bias;  // device, M values, or nullptr
+  float zy, qmin, qmax;
+};
+
+size_t ConvColBytes(const ConvGeom &g);
+void LaunchImToCol(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, uint8_t *col, hipStream_t stream);
+// q == nullptr: ConvInteger (int32 output); else QLinearConv (8-bit output).
+// w_zp_per_channel: M device bytes, or nullptr for the value w_zp_scalar.
+void LaunchDirectConv(const ConvGeom &g, const uint8_t *x, int x_u8, uint8_t x_zp, const uint8_t *w, int w_u8,
+                      const uint8_t *w_zp_per_channel, int32_t w_zp_scalar, const ConvQuant *q, void *y,
+                      hipStream_t stream);
+void LaunchConvRequant(const ConvGeom &g, const int32_t *acc, const ConvQuant &q, uint8_t *y, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // DequantizeLinear (standalone, element-wise).
 
 struct DequantParams {

@@ -2,6 +2,7 @@
 header declares, and reproduces the reference kernels' validation (same
 checks and message text) before touching the device.  Calls whose arguments
 are valid stop at NOT_INITIALIZED (no GPU here): no kernel runs on the CPU."""
+import ctypes
 import os
 import re
 
@@ -264,3 +265,64 @@ def test_dynamic_quantize_validation(olamd):
         assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
     rc, _ = run()
     assert rc == olamd.NOT_INITIALIZED
+
+
+def test_conv_validation(olamd):
+    """nn/kernel_conv_integer.cc:24-201 and kq/kernel_qlinearconv.cc:53-238."""
+    d = olamd.describe
+    L = olamd.lib()
+    x = np.zeros((1, 4, 5, 5), np.uint8)
+    w = np.zeros((6, 2, 3, 3), np.uint8)
+    ok_attrs = dict(group=2, pads=[1, 1, 1, 1])
+
+    def ci(x=x, w=w, xz=None, wz=None, y=None, **kw):
+        a = olamd.conv_attrs(**(kw or ok_attrs))
+        y = np.zeros((1, 6, 5, 5), np.int32) if y is None else y
+        rc = L.onnxl_amd_conv_integer(d(x), d(w), d(xz), d(wz), ctypes.byref(a), d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(kernel_shape=[3]), "'kernel_shape' size must match input spatial rank."),
+                    (dict(strides=[1, 1, 1]), "'strides' size must match input spatial rank."),
+                    (dict(pads=[1, 1]), "'pads' size must be 2 * spatial rank."),
+                    (dict(auto_pad=7), "'auto_pad' must be NOTSET/SAME_UPPER/SAME_LOWER/VALID."),
+                    (dict(group=3, pads=[1, 1, 1, 1]), "x.shape[1] must equal w.shape[1] * group.")):
+        rc, err = ci(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    rc, err = ci(x=np.zeros((1, 4, 5, 5), np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "x must be INT8 or UINT8." in err
+    rc, err = ci(xz=np.zeros(1, np.int8))
+    assert rc == olamd.INVALID_ARGUMENT and "x_zero_point dtype must match x." in err
+    rc, err = ci(wz=np.zeros(4, np.uint8))
+    assert rc == olamd.INVALID_ARGUMENT and "w_zero_point must be a scalar or 1-D of length M." in err
+    rc, err = ci(y=np.zeros((1, 6, 5, 5), np.float32))
+    assert rc == olamd.INVALID_ARGUMENT and "preallocated output must be INT32." in err
+    rc, err = ci(y=np.zeros((1, 6, 3, 3), np.int32))
+    assert rc == olamd.INVALID_ARGUMENT and "preallocated output shape mismatch." in err
+    rc, _ = ci(xz=np.zeros((), np.uint8), wz=np.zeros(6, np.uint8))
+    assert rc == olamd.NOT_INITIALIZED
+
+    f = lambda v: np.array(v, np.float32)
+
+    def qc(ws=f(1.0), wz=np.zeros((), np.uint8), xs=f(0.5), ys=f(2.0), yz=np.zeros((), np.uint8), B=None,
+           y=None, xz=np.zeros((), np.uint8)):
+        a = olamd.conv_attrs(**ok_attrs)
+        y = np.zeros((1, 6, 5, 5), yz.dtype) if y is None else y
+        rc = L.onnxl_amd_qlinear_conv(d(x), d(xs), d(xz), d(w), d(ws), d(wz), d(ys), d(yz), d(B),
+                                      ctypes.byref(a), d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(ys=f(0.0)), "y_scale must be non-zero."),
+                    (dict(xs=f([1.0, 2.0])), "'x_scale' and 'y_scale' must be scalar."),
+                    (dict(ws=f([1.0, 2.0])), "'w_scale' must be scalar or length-M."),
+                    (dict(wz=np.zeros(2, np.uint8)), "'w_zero_point' must be scalar or length-M."),
+                    (dict(B=np.zeros(6, np.int64)), "B must be INT32."),
+                    (dict(B=np.zeros(5, np.int32)), "B must be 1-D with length M."),
+                    (dict(xz=np.zeros(2, np.uint8)), "'x_zero_point' must be a scalar."),
+                    (dict(yz=np.zeros((), np.int8), y=np.zeros((1, 6, 5, 5), np.uint8)),
+                     "output dtype must match y_zero_point."),
+                    (dict(xs=np.array(0.5, np.float16)), "scale must be FLOAT for the reference kernel.")):
+        rc, err = qc(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    rc, _ = qc(ws=f(np.ones(6)), wz=np.zeros(6, np.uint8), B=np.zeros(6, np.int32))
+    assert rc == olamd.NOT_INITIALIZED
+    assert olamd.conv_shape((2, 3, 9, 8), (4, 3, 3, 3), olamd.conv_attrs(strides=[2, 2])) == (2, 4, 4, 3)
