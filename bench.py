@@ -16,17 +16,18 @@ reported as `host_path_ms_per_step`.  `cpu_baseline` times the serial CPU
 oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
-configuration 2's fp32 activation) are timed too and reported under `extra`
-unless --no-extra is given.
+configuration 2's fp32 activation) and a QLinearConv layer (`qconv`) are
+timed too and reported under `extra` unless --no-extra is given.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import importlib.util
 import json
 import os
@@ -168,6 +169,34 @@ def make_c5(olamd, dev, replicas):
     return w
 
 
+def make_qconv(olamd, dev):
+    """QLinearConv u8[32,256,28,28] x s8[256,256,3,3], pads 1, per-channel
+    w_scale and bias -> u8[32,256,28,28]: im2col + int8 MFMA GEMM +
+    requantization.  Work 2*N*M*P*K with K = 256*9, P = 28*28."""
+    import torch
+    w = Workload()
+    w.name = ("QLinearConv u8[32,256,28,28] x s8[256,256,3,3] pads 1, per-channel w_scale, bias "
+              "-> u8[32,256,28,28]")
+    w.key, w.unit, w.dtype, w.bound = "qconv", "TOPS", "int8 (int32 accumulate)", "mfma"
+    N, C, H, W, M = 32, 256, 28, 28, 256
+    K, P = C * 9, H * W
+    w.work = 2.0 * N * M * P * K
+    w.nbytes = N * C * H * W + M * K + N * M * P
+    rng = np.random.default_rng(21)
+    x = _t(rng.integers(0, 256, (N, C, H, W)).astype(np.uint8), dev)
+    wt = _t(rng.integers(-128, 128, (M, C, 3, 3)).astype(np.int8), dev)
+    ws = _t(rng.uniform(0.0005, 0.002, M).astype(np.float32), dev)
+    bias = _t(rng.integers(-30000, 30000, M).astype(np.int32), dev)
+    y = torch.empty((N, M, H, W), dtype=torch.uint8, device=dev)
+    a = olamd.conv_attrs(pads=[1, 1, 1, 1])
+    descs = [olamd.describe(t) for t in (x, np.array(0.02, np.float32), np.array(128, np.uint8), wt, ws,
+                                         np.array(0, np.int8), np.array(0.8, np.float32),
+                                         np.array(120, np.uint8), bias)]
+    w.calls = [olamd.Prepared("onnxl_amd_qlinear_conv", descs + [ctypes.byref(a), olamd.describe(y)],
+                              (a, x, wt, ws, bias, y), olamd._stream_of(x))]
+    return w
+
+
 def make_q8(olamd, dev, replicas):
     """QuantizeLinear of configuration 2's activation: fp32[2048,4096] -> u8
     with a scalar scale and zero point (the producer of QLinearMatMul's A)."""
@@ -294,9 +323,10 @@ def cpu_baseline_c2(w, budget_s=20.0):
 
 def roofline(w, kernel_ms, traffic):
     if w.bound == "mfma":
-        peak = PEAK["int8_TOPs"] if w.key == "c2" else PEAK["bf16_TFLOPs"]
+        int8 = w.key in ("c2", "qconv")
+        peak = PEAK["int8_TOPs"] if int8 else PEAK["bf16_TFLOPs"]
         achieved = w.work / (kernel_ms * 1e-3) / 1e12
-        unit = "TOP/s" if w.key == "c2" else "TFLOP/s"
+        unit = "TOP/s" if int8 else "TFLOP/s"
     else:
         peak = PEAK["hbm_GBps"]
         achieved = w.nbytes / (kernel_ms * 1e-3) / 1e9
@@ -328,7 +358,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql"])
+                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv"])
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -359,6 +389,8 @@ def main():
             return make_q8(olamd, dev, args.replicas or 14)
         if key == "dql":
             return make_dql(olamd, dev, args.replicas or 14)
+        if key == "qconv":
+            return make_qconv(olamd, dev)
         return make_c5(olamd, dev, args.replicas or 16)
 
     w = build(args.workload)
@@ -373,7 +405,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql"):
+        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv"):
             if key == args.workload:
                 continue
             try:

@@ -862,8 +862,11 @@ int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnx
   int32_t *yd = static_cast<int32_t *>(st.Out(y));
   if (g.N * g.M * g.P > 0) {
     if (gemm) {
-      uint8_t *col = static_cast<uint8_t *>(st.Extra());
-      LaunchImToCol(g, xd, (uint8_t)xz, col, stream);
+      const uint8_t *col = xd;
+      if (!ConvColIsInput(g)) {
+        col = static_cast<uint8_t *>(st.Extra());
+        LaunchImToCol(g, xd, (uint8_t)xz, static_cast<uint8_t *>(st.Extra()), stream);
+      }
       LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, yd, stream);
     } else {
       LaunchDirectConv(g, xd, x->data_type == kUint8, (uint8_t)xz, wd, w->data_type == kUint8, wzd, wz, nullptr,
@@ -958,9 +961,12 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   uint8_t *yd = static_cast<uint8_t *>(st.Out(y));
   if (g.N * g.M * g.P > 0) {
     if (gemm) {
-      uint8_t *col = static_cast<uint8_t *>(st.Extra());
+      const uint8_t *col = xd;
       int32_t *acc = reinterpret_cast<int32_t *>(static_cast<char *>(st.Extra()) + acc_off);
-      LaunchImToCol(g, xd, (uint8_t)xz, col, stream);
+      if (!ConvColIsInput(g)) {
+        col = static_cast<uint8_t *>(st.Extra());
+        LaunchImToCol(g, xd, (uint8_t)xz, static_cast<uint8_t *>(st.Extra()), stream);
+      }
       LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, acc, stream);
       LaunchConvRequant(g, acc, q, yd, stream);
     } else {

@@ -76,6 +76,82 @@ __global__ __launch_bounds__(kCBlock) void ImToColKernel(const ConvGeom g, const
   }
 }
 
+// Col rows of kPlanesPerBlock consecutive input planes (n, channel c of
+// group grp) for every kernel tap: the planes are staged in LDS once, each
+// thread decodes its 4 output positions once (32-bit arithmetic) and writes
+// the ks rows Col[n, grp, c_in_group * ks + tap, p0 .. p0 + 3] of each plane.
+// Several planes per workgroup keep enough loads in flight: one plane per
+// workgroup left the pass waiting on plane loads.  For planes up to
+// kPlaneMax bytes, 2-D or 1-D (the leading slot of the geometry is 1).
+constexpr int kPlaneMax = 12 * 1024;  // per plane; kPlanesPerBlock of them share the LDS
+constexpr int kPlanesPerBlock = 4;
+
+template <int KH, int KW>  // 0: the kernel extent from the geometry
+__global__ __launch_bounds__(kCBlock) void ImToColPlaneKernel(const ConvGeom g, const uint8_t *x, uint8_t x_zp,
+                                                               uint8_t *col) {
+  // kPlanesPerBlock planes of in_size bytes each (dynamic: occupancy follows
+  // the plane size); their loads are all in flight before the first wait
+  extern __shared__ __align__(16) uint8_t planes[];
+  const uint32_t in_size = (uint32_t)g.in_size, P = (uint32_t)g.P;
+  const int64_t nplanes = g.N * g.C;
+  const int64_t first = (int64_t)blockIdx.x * kPlanesPerBlock;
+  const int count = (int)std::min<int64_t>(kPlanesPerBlock, nplanes - first);
+  const uint32_t lds_pitch = (in_size + 15) & ~15u;
+  for (int pl = 0; pl < count; ++pl) {
+    const uint8_t *src = x + (first + pl) * in_size;
+    for (uint32_t i = threadIdx.x; i < in_size; i += kCBlock) planes[pl * lds_pitch + i] = src[i];
+  }
+  __syncthreads();
+  const uint32_t C = (uint32_t)g.C, cpg = (uint32_t)g.cpg;
+  const int H = (int)g.in[1], W = (int)g.in[2], OW = (int)g.out[2];
+  const int sy = (int)g.s[1], sx = (int)g.s[2], dy = (int)g.d[1], dx = (int)g.d[2];
+  const int py = (int)g.pb[1], px = (int)g.pb[2];
+  const int kh = KH ? KH : g.k[1], kw = KW ? KW : g.k[2];
+  for (uint32_t p0 = threadIdx.x * 4; p0 < P; p0 += kCBlock * 4) {
+    int oy[4], ox[4];
+    const uint32_t q = p0 / (uint32_t)OW;
+    oy[0] = (int)q;
+    ox[0] = (int)(p0 - q * (uint32_t)OW);
+#pragma unroll
+    for (int e = 1; e < 4; ++e) {
+      ox[e] = ox[e - 1] + 1;
+      oy[e] = oy[e - 1];
+      if (ox[e] == OW) {
+        ox[e] = 0;
+        ++oy[e];
+      }
+    }
+    const int nvalid = (int)min(4u, P - p0);
+    for (int pl = 0; pl < count; ++pl) {
+      const int64_t nc = first + pl;  // n * C + channel
+      const uint32_t n = (uint32_t)(nc / C), ch = (uint32_t)(nc - (int64_t)n * C);
+      const uint32_t grp = ch / cpg, ci = ch - grp * cpg;
+      // first Col row of this plane: (n * G + grp) * Kc + ci * ks
+      uint8_t *rows = col + (((int64_t)n * g.G + grp) * g.Kc + (int64_t)ci * kh * kw) * P;
+      const uint8_t *plane = planes + pl * lds_pitch;
+#pragma unroll
+      for (int ky = 0; ky < kh; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < kw; ++kx) {
+          const int tap = ky * kw + kx;
+          uint32_t word = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int iy = oy[e] * sy - py + ky * dy, ix = ox[e] * sx - px + kx * dx;
+            const bool in = e < nvalid && iy >= 0 && iy < H && ix >= 0 && ix < W;
+            word |= (uint32_t)(in ? plane[iy * W + ix] : x_zp) << (8 * e);
+          }
+          uint8_t *dst = rows + (int64_t)tap * P + p0;
+          if (nvalid == 4 && (reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+            *reinterpret_cast<uint32_t *>(dst) = word;
+          } else {
+            for (int e = 0; e < nvalid; ++e) dst[e] = (uint8_t)(word >> (8 * e));
+          }
+        }
+    }
+  }
+}
+
 __device__ __forceinline__ int32_t ByteValue(const uint8_t *p, int64_t i, int is_u8) {
   return is_u8 ? (int32_t)p[i] : (int32_t)(int8_t)p[i];
 }
@@ -136,31 +212,57 @@ __global__ __launch_bounds__(kCBlock) void DirectConvKernel(const ConvGeom g, co
 }
 
 // QLinearConv's bias and requantization of the GEMM's int32 sums [N, M, P]:
-// 4 positions per thread, one channel per thread.
+// workgroup y = (n, m) plane, 4 positions per thread (16-byte loads when P %
+// 4 == 0).
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
 __global__ __launch_bounds__(kCBlock) void ConvRequantKernel(const ConvGeom g, const int32_t *acc, const ConvQuant q,
                                                              uint8_t *y) {
-  const int64_t quads = (g.P + 3) / 4;
-  const int64_t t = (int64_t)blockIdx.x * kCBlock + threadIdx.x;
-  if (t >= g.N * g.M * quads) return;
-  const int64_t nm = t / quads;
-  const int64_t p0 = (t - nm * quads) * 4;
+  const uint32_t P = (uint32_t)g.P;
+  const int64_t nm = (int64_t)blockIdx.y + (int64_t)blockIdx.z * 65535;
+  const uint32_t p0 = (blockIdx.x * kCBlock + threadIdx.x) * 4;
+  if (nm >= g.N * g.M || p0 >= P) return;
   const int64_t m = nm % g.M;
   const float cs = CombinedScale(q, m);
   const int64_t bias = q.bias ? q.bias[m] : 0;
-  const int64_t base = nm * g.P + p0;
-  for (int e = 0; e < 4 && p0 + e < g.P; ++e) y[base + e] = Requant((int64_t)acc[base + e] + bias, cs, q);
+  const int32_t *a = acc + nm * g.P + p0;
+  uint8_t *dst = y + nm * g.P + p0;
+  if ((P & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 3) == 0) {  // acc is 16-byte aligned scratch
+    const v4i_t v = *reinterpret_cast<const v4i_t *>(a);
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) word |= (uint32_t)Requant((int64_t)v[e] + bias, cs, q) << (8 * e);
+    *reinterpret_cast<uint32_t *>(dst) = word;
+  } else {
+    for (uint32_t e = 0; e < 4 && p0 + e < P; ++e) dst[e] = Requant((int64_t)a[e] + bias, cs, q);
+  }
 }
 
 unsigned Blocks(int64_t threads) { return (unsigned)((threads + kCBlock - 1) / kCBlock); }
 
 }  // namespace
 
-size_t ConvColBytes(const ConvGeom &g) { return (size_t)(g.N * g.G * g.Kc * g.P); }
+bool ConvColIsInput(const ConvGeom &g) {
+  for (int i = 0; i < 3; ++i)
+    if (g.k[i] != 1 || g.s[i] != 1 || g.pb[i] != 0 || g.in[i] != g.out[i]) return false;
+  return true;
+}
+
+size_t ConvColBytes(const ConvGeom &g) { return ConvColIsInput(g) ? 0 : (size_t)(g.N * g.G * g.Kc * g.P); }
 
 void LaunchImToCol(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, uint8_t *col, hipStream_t s) {
   const int64_t threads = g.N * g.G * g.Kc * ((g.P + 3) / 4);
   if (threads == 0) return;
-  hipLaunchKernelGGL(ImToColKernel, dim3(Blocks(threads)), dim3(kCBlock), 0, s, g, x, x_zp, col);
+  const bool plane = g.in[0] == 1 && g.k[0] == 1 && g.in_size <= kPlaneMax && g.P < (1ll << 31) &&
+                     g.N * g.C < (1ll << 31) * kPlanesPerBlock;
+  const dim3 grid((unsigned)((g.N * g.C + kPlanesPerBlock - 1) / kPlanesPerBlock));
+  const unsigned lds = (unsigned)(kPlanesPerBlock * ((g.in_size + 15) & ~15ll));
+  if (plane && g.k[1] == 3 && g.k[2] == 3)
+    hipLaunchKernelGGL((ImToColPlaneKernel<3, 3>), grid, dim3(kCBlock), lds, s, g, x, x_zp, col);
+  else if (plane)
+    hipLaunchKernelGGL((ImToColPlaneKernel<0, 0>), grid, dim3(kCBlock), lds, s, g, x, x_zp, col);
+  else
+    hipLaunchKernelGGL(ImToColKernel, dim3(Blocks(threads)), dim3(kCBlock), 0, s, g, x, x_zp, col);
 }
 
 void LaunchDirectConv(const ConvGeom &g, const uint8_t *x, int x_u8, uint8_t x_zp, const uint8_t *w, int w_u8,
@@ -177,9 +279,13 @@ void LaunchDirectConv(const ConvGeom &g, const uint8_t *x, int x_u8, uint8_t x_z
 }
 
 void LaunchConvRequant(const ConvGeom &g, const int32_t *acc, const ConvQuant &q, uint8_t *y, hipStream_t s) {
-  const int64_t threads = g.N * g.M * ((g.P + 3) / 4);
-  if (threads == 0) return;
-  hipLaunchKernelGGL(ConvRequantKernel, dim3(Blocks(threads)), dim3(kCBlock), 0, s, g, acc, q, y);
+  const int64_t planes = g.N * g.M;
+  if (planes == 0 || g.P == 0) return;
+  if (g.P >= (1ll << 31) || planes > 65535ll * 65535ll)
+    throw Unsupported("QLinearConv: output planes beyond the requantization grid");
+  const unsigned gx = Blocks((g.P + 3) / 4);
+  const unsigned gy = (unsigned)std::min<int64_t>(planes, 65535), gz = (unsigned)((planes + 65534) / 65535);
+  hipLaunchKernelGGL(ConvRequantKernel, dim3(gx, gy, gz), dim3(kCBlock), 0, s, g, acc, q, y);
 }
 
 }  // namespace onnxl_amd

@@ -88,6 +88,9 @@ struct ConvQuant {
   float zy, qmin, qmax;
 };
 
+// A 1x1 kernel with stride 1 and no padding reads x itself as the columns
+// ([N, C, P] is [N, G, Kc, P]); no im2col pass, ConvColBytes 0.
+bool ConvColIsInput(const ConvGeom &g);
 size_t ConvColBytes(const ConvGeom &g);
 void LaunchImToCol(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, uint8_t *col, hipStream_t stream);
 // q == nullptr: ConvInteger (int32 output); else QLinearConv (8-bit output).
