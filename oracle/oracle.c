@@ -598,6 +598,68 @@ int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_
 }
 
 /* ------------------------------------------------------------------------ */
+/* DequantizePacked for the 32-value GGUF block formats
+ * (onnx_core/runtime/dequantize_packed.cc:173-235, the ggml layouts at ggml
+ * da8e2a54b919557b816b1c2beb432ccb766f7ce0): an fp16 scale d, and for the
+ * affine formats an fp16 minimum m, then the codes.  Every fp32 product and
+ * sum is rounded on its own (the reference forces it through volatile). */
+
+static int pk_unpack4(const uint8_t *p, int i) { /* Unpack(p, i, 4, 16) */
+  return (p[i % 16] >> (4 * (i / 16))) & 15;
+}
+
+static const int pk_iq4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+int orc_packed_block_bytes(int ggml_type) {
+  switch (ggml_type) {
+  case 2: return 18;  /* q4_0 */
+  case 3: return 20;  /* q4_1 */
+  case 6: return 22;  /* q5_0 */
+  case 7: return 24;  /* q5_1 */
+  case 8: return 34;  /* q8_0 */
+  case 9: return 36;  /* q8_1 */
+  case 20: return 18; /* iq4_nl */
+  default: return 0;
+  }
+}
+
+int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out) {
+  const int bytes = orc_packed_block_bytes(ggml_type);
+  if (!bytes) return 1;
+  for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += 32) {
+    const float d = orc_f16_to_f32((uint16_t)(x[0] | (x[1] << 8)));
+    for (int i = 0; i < 32; ++i) {
+      volatile float v;
+      if (ggml_type == 8 || ggml_type == 9) {
+        const int q = (int8_t)x[(ggml_type == 8 ? 2 : 4) + i];
+        v = d * (float)q;
+      } else {
+        const int affine = ggml_type == 3 || ggml_type == 7, five = ggml_type == 6 || ggml_type == 7;
+        const int off = affine ? 4 : 2;
+        int q = pk_unpack4(x + off + (five ? 4 : 0), i);
+        if (five) {
+          const uint32_t qh = (uint32_t)x[off] | ((uint32_t)x[off + 1] << 8) | ((uint32_t)x[off + 2] << 16) |
+                              ((uint32_t)x[off + 3] << 24);
+          q |= (int)((qh >> i) & 1u) << 4;
+        }
+        if (ggml_type == 20) {
+          v = d * (float)pk_iq4[q];
+        } else {
+          if (!affine) q -= five ? 16 : 8;
+          v = d * (float)q;
+          if (affine) {
+            const float m = orc_f16_to_f32((uint16_t)(x[2] | (x[3] << 8)));
+            v = v + m;
+          }
+        }
+      }
+      out[i] = v;
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* ConvInteger (nn/kernel_conv_integer.cc) and QLinearConv
  * (kq/kernel_qlinearconv.cc): the same attribute resolution and the same
  * direct loops over (n, m, output position) x (input channel of the group,

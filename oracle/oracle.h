@@ -136,6 +136,16 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
 int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_scale,
                                 uint8_t *y_zero_point);
 
+/* ---- DequantizePacked, 32-value GGUF formats
+ * (onnx_core/runtime/dequantize_packed.cc:173-235) ----
+ * ggml_type 2 q4_0, 3 q4_1, 6 q5_0, 7 q5_1, 8 q8_0, 9 q8_1, 20 iq4_nl:
+ * nblocks blocks of orc_packed_block_bytes(type) bytes -> 32 * nblocks FLOAT
+ * values (each fp32 step rounded on its own).  Returns 0, or 1 for another
+ * type.  The FLOAT16 / BFLOAT16 / DOUBLE outputs are the FLOAT values
+ * converted (:358-370). */
+int orc_packed_block_bytes(int ggml_type);
+int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out);
+
 /* ---- ConvInteger (nn/kernel_conv_integer.cc:178-304) and QLinearConv
  * (kq/kernel_qlinearconv.cc:178-340) ----
  * x [N, C, spatial...] and w [M, C/group, kernel...] of INT8 or UINT8;

@@ -97,6 +97,10 @@ def _declare(L):
                                    P, ctypes.c_int, P, P, ctypes.c_int64, P, ctypes.c_int64,
                                    ctypes.c_float, ctypes.c_int32, ctypes.c_int, P, ctypes.c_int64,
                                    P, P, P, P, ctypes.c_int, P]
+    L.orc_packed_block_bytes.restype = ctypes.c_int
+    L.orc_packed_block_bytes.argtypes = [ctypes.c_int]
+    L.orc_dequantize_packed.restype = ctypes.c_int
+    L.orc_dequantize_packed.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
     L.orc_matmul_f32.restype = ctypes.c_int
     L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int]
@@ -394,3 +398,32 @@ def qlinear_conv(x, x_dtype, x_scale, x_zp, w, w_dtype, w_scale, w_zp, y_scale, 
     if rc:
         raise ValueError(f"qlinear_conv error {rc}")
     return y
+
+
+# ---- DequantizePacked (32-value GGUF formats) -------------------------------
+
+GGUF_TYPES = {"gguf:q4_0": 2, "gguf:q4_1": 3, "gguf:q5_0": 6, "gguf:q5_1": 7, "gguf:q8_0": 8,
+              "gguf:q8_1": 9, "gguf:iq4_nl": 20}
+
+
+def packed_block_bytes(fmt: str) -> int:
+    return lib().orc_packed_block_bytes(GGUF_TYPES[fmt])
+
+
+def dequantize_packed(x: np.ndarray, fmt: str, shape, output_dtype: int = FLOAT) -> np.ndarray:
+    """FLOAT values (float32 array of `shape`), or FLOAT16 / BFLOAT16 bit
+    patterns (uint16) / DOUBLE values converted from them."""
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    n = int(np.prod(shape)) if len(shape) else 1
+    out = np.empty(n, np.float32)
+    rc = lib().orc_dequantize_packed(GGUF_TYPES[fmt], _ptr(x), n // 32, _ptr(out))
+    if rc:
+        raise ValueError(f"dequantize_packed error {rc}")
+    out = out.reshape(shape)
+    if output_dtype == FLOAT16:
+        return f32_to_f16_bits(out)
+    if output_dtype == BFLOAT16:
+        return f32_to_bf16_bits(out)
+    if output_dtype == 11:  # DOUBLE
+        return out.astype(np.float64)
+    return out
