@@ -16,13 +16,14 @@ reported as `host_path_ms_per_step`.  `cpu_baseline` times the serial CPU
 oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv|pk]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
-configuration 2's fp32 activation) and a QLinearConv layer (`qconv`) are
-timed too and reported under `extra` unless --no-extra is given.
+configuration 2's fp32 activation), a QLinearConv layer (`qconv`) and a
+GGUF q4_0 weight decode (`pk`) are timed too and reported under `extra`
+unless --no-extra is given.
 """
 from __future__ import annotations
 
@@ -197,6 +198,30 @@ def make_qconv(olamd, dev):
     return w
 
 
+def make_pk(olamd, dev, replicas):
+    """DequantizePacked gguf:q4_0 [14336, 4096] -> FLOAT16: 18 bytes in and
+    64 bytes out per 32 values."""
+    import torch
+    w = Workload()
+    w.name = "DequantizePacked gguf:q4_0 [14336,4096] -> float16"
+    w.key, w.unit, w.dtype, w.bound = "pk", "GB/s", "q4_0 -> f16 (fp32 decode)", "hbm"
+    n = 14336 * 4096
+    w.nbytes = n // 32 * 18 + n * 2
+    w.work = float(w.nbytes)
+    rng = np.random.default_rng(31)
+    blocks = rng.integers(0, 256, (n // 32, 18)).astype(np.uint8)
+    blocks[:, 1] = rng.integers(0x20, 0x30, n // 32)  # fp16 scales of moderate size
+    w.calls = []
+    for _ in range(replicas):
+        x = _t(blocks.reshape(-1), dev)
+        y = torch.empty((14336, 4096), dtype=torch.float16, device=dev)
+        dims = (ctypes.c_int64 * olamd.MAX_RANK)(14336, 4096)
+        w.calls.append(olamd.Prepared("onnxl_amd_dequantize_packed",
+                                      [olamd.describe(x), b"gguf:q4_0", dims, 2, olamd.FLOAT16, olamd.describe(y)],
+                                      (x, y, dims), olamd._stream_of(x)))
+    return w
+
+
 def make_q8(olamd, dev, replicas):
     """QuantizeLinear of configuration 2's activation: fp32[2048,4096] -> u8
     with a scalar scale and zero point (the producer of QLinearMatMul's A)."""
@@ -358,7 +383,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv"])
+                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk"])
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -391,6 +416,8 @@ def main():
             return make_dql(olamd, dev, args.replicas or 14)
         if key == "qconv":
             return make_qconv(olamd, dev)
+        if key == "pk":
+            return make_pk(olamd, dev, args.replicas or 4)
         return make_c5(olamd, dev, args.replicas or 16)
 
     w = build(args.workload)
@@ -405,7 +432,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv"):
+        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk"):
             if key == args.workload:
                 continue
             try:

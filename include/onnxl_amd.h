@@ -146,6 +146,18 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
                                       onnxl_amd_tensor *y_scale, onnxl_amd_tensor *y_zero_point,
                                       void *stream);
 
+/* DequantizePacked: decodes a 1-D UINT8 vector in one of the reference's
+ * fixed GGUF wire formats (`format`, e.g. "gguf:q4_0") into y of the given
+ * shape and output_dtype (FLOAT, FLOAT16, BFLOAT16 or DOUBLE); the last
+ * dimension holds whole blocks.  The GPU decodes gguf:q4_0, q4_1, q5_0, q5_1,
+ * q8_0, q8_1 and iq4_nl; the reference's other 20 formats return
+ * ONNXL_AMD_UNSUPPORTED, an unknown format INVALID_ARGUMENT.
+ * Replaces DequantizePackedTensor (onnx_core/runtime/dequantize_packed.cc:
+ * 334-372) behind kernel::DequantizePacked::operator()
+ * (kq/kernel_dequantize_packed.cc:11-15). */
+int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, const int64_t *shape,
+                                int32_t rank, int64_t output_dtype, onnxl_amd_tensor *y, void *stream);
+
 /* Convolution attributes, as the reference's ConvInteger / QLinearConv
  * Attributes: n_* entries of each array are used, 0 means the attribute is
  * absent (kernel_shape from w, strides and dilations 1, pads 0).  pads holds

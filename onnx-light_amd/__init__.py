@@ -90,6 +90,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_quantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, ctypes.c_int32, TP,
                                                 ctypes.c_void_p]
         L.onnxl_amd_dynamic_quantize_linear.argtypes = [TP, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_packed.argtypes = [TP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
+                                                  ctypes.c_int32, ctypes.c_int64, TP, ctypes.c_void_p]
         CA = ctypes.POINTER(ConvAttrs)
         L.onnxl_amd_conv_shape.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
                                            ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, CA,
@@ -426,6 +428,21 @@ def dynamic_quantize_linear(x, out=None, check: bool = True):
     return y, y_scale, y_zp
 
 
+def dequantize_packed(x, format: str, shape, output_dtype: int = FLOAT, out=None):
+    """kernel::DequantizePacked (kq/kernel_dequantize_packed.cc:11-28): decodes
+    the packed UINT8 vector x into `shape` values of output_dtype."""
+    torch = _torch()
+    shape = tuple(int(d) for d in shape)
+    if out is None:
+        tdt = {FLOAT: torch.float32, FLOAT16: torch.float16, BFLOAT16: torch.bfloat16,
+               DOUBLE: torch.float64}.get(output_dtype, torch.float32)
+        out = _empty(shape, tdt, _device_of(x))
+    dims = (ctypes.c_int64 * MAX_RANK)(*shape)
+    _check(lib().onnxl_amd_dequantize_packed(describe(x), format.encode(), dims, len(shape), output_dtype,
+                                             describe(out), _stream_of(x, out)))
+    return out
+
+
 def conv_shape(x_shape, w_shape, attrs: ConvAttrs) -> tuple:
     xs = (ctypes.c_int64 * MAX_RANK)(*x_shape)
     ws = (ctypes.c_int64 * MAX_RANK)(*w_shape)
@@ -501,6 +518,14 @@ class MatMul:
         return matmul(a, b, out)
 
 
+class DequantizePacked:
+    """Kernel-class mirror of kernel::DequantizePacked (ai.rt domain)."""
+    name = "onnxl_amd:GPU:ai.rt:DequantizePacked"
+
+    def __call__(self, x, format, shape, output_dtype=FLOAT, out=None):
+        return dequantize_packed(x, format, shape, output_dtype, out)
+
+
 class ConvInteger:
     """Kernel-class mirror of kernel::ConvInteger."""
     name = "onnxl_amd:GPU:ai.onnx:ConvInteger"
@@ -543,7 +568,8 @@ KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLin
            "ai.onnx:DequantizeLinear": DequantizeLinear, "ai.onnx:MatMul": MatMul,
            "ai.onnx:QuantizeLinear": QuantizeLinear,
            "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear,
-           "ai.onnx:ConvInteger": ConvInteger, "ai.onnx:QLinearConv": QLinearConv}
+           "ai.onnx:ConvInteger": ConvInteger, "ai.onnx:QLinearConv": QLinearConv,
+           "ai.rt:DequantizePacked": DequantizePacked}
 
 
 class Prepared:

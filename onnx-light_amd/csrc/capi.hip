@@ -979,6 +979,74 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
 }
 
 // ---------------------------------------------------------------------------
+// DequantizePacked, onnx_core/runtime/dequantize_packed.cc:296-372.
+
+struct PackedProfile {
+  const char *format;
+  int64_t block_size, block_bytes;
+  int ggml_type;
+};
+
+// The reference's 27 fixed wire profiles (ggml block sizes and bytes,
+// dequantize_packed.cc:27-36); the GPU decodes the 32-value formats.
+constexpr PackedProfile kPackedProfiles[] = {
+    {"gguf:q4_0", 32, 18, 2},      {"gguf:q4_1", 32, 20, 3},      {"gguf:q5_0", 32, 22, 6},
+    {"gguf:q5_1", 32, 24, 7},      {"gguf:q8_0", 32, 34, 8},      {"gguf:q8_1", 32, 36, 9},
+    {"gguf:q2_k", 256, 84, 10},    {"gguf:q3_k", 256, 110, 11},   {"gguf:q4_k", 256, 144, 12},
+    {"gguf:q5_k", 256, 176, 13},   {"gguf:q6_k", 256, 210, 14},   {"gguf:q8_k", 256, 292, 15},
+    {"gguf:iq2_xxs", 256, 66, 16}, {"gguf:iq2_xs", 256, 74, 17},  {"gguf:iq3_xxs", 256, 98, 18},
+    {"gguf:iq1_s", 256, 50, 19},   {"gguf:iq4_nl", 32, 18, 20},   {"gguf:iq3_s", 256, 110, 21},
+    {"gguf:iq2_s", 256, 82, 22},   {"gguf:iq4_xs", 256, 136, 23}, {"gguf:iq1_m", 256, 56, 29},
+    {"gguf:tq1_0", 256, 54, 34},   {"gguf:tq2_0", 256, 66, 35},   {"gguf:mxfp4", 32, 17, 39},
+    {"gguf:nvfp4", 64, 36, 40},    {"gguf:q1_0", 128, 18, 41},    {"gguf:q2_0", 64, 18, 42}};
+
+int DequantizePacked(const onnxl_amd_tensor *x, const char *format, const int64_t *shape, int32_t rank,
+                     int64_t output_dtype, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(format != nullptr && x && y && (rank == 0 || shape) && rank >= 0 && rank <= ONNXL_AMD_MAX_RANK,
+              "DequantizePacked: invalid arguments.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y, "y");
+  const PackedProfile *prof = nullptr;  // PackedQuantizationLayout, :296-302
+  for (const auto &pp : kPackedProfiles)
+    if (std::strcmp(pp.format, format) == 0) prof = &pp;
+  if (!prof) throw InvalidArgument(Cat("DequantizePacked: unsupported format '", format, "'."));
+  // ValidatePackedQuantizationShape, :304-332
+  OLA_ENFORCE(output_dtype == kFloat || output_dtype == kFloat16 || output_dtype == kBfloat16 ||
+                  output_dtype == kDouble,
+              "DequantizePacked: output_dtype must be FLOAT, FLOAT16, BFLOAT16 or DOUBLE.");
+  OLA_ENFORCE(rank >= 1, "DequantizePacked: shape must have rank at least one.");
+  bool empty = false;
+  for (int i = 0; i < rank; ++i) {
+    OLA_ENFORCE(shape[i] >= 0, "DequantizePacked: dimensions must be nonnegative.");
+    empty |= shape[i] == 0;
+  }
+  OLA_ENFORCE(shape[rank - 1] % prof->block_size == 0,
+              "DequantizePacked: last dimension must contain complete blocks.");
+  int64_t count = 1;
+  for (int i = 0; i < rank && !empty; ++i) {
+    OLA_ENFORCE(shape[i] == 0 || count <= INT64_MAX / shape[i], "DequantizePacked: dimension exceeds size_t.");
+    count *= shape[i];
+  }
+  if (empty) count = 0;
+  const int64_t expected = count / prof->block_size * prof->block_bytes;
+  // DequantizePackedTensor, :337-343
+  OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
+  OLA_ENFORCE(x->dims[0] == expected && x->size_bytes == expected,
+              "DequantizePacked: packed input length must match exactly.");
+  OLA_ENFORCE(y->data_type == output_dtype, "DequantizePacked: preallocated output dtype must be output_dtype.");
+  OLA_ENFORCE(ShapeOf(*y) == Shape(shape, shape + rank), "DequantizePacked: preallocated output shape mismatch.");
+  OLA_ENFORCE(y->size_bytes == count * ElementSize((int32_t)output_dtype),
+              "DequantizePacked: preallocated output buffer has unexpected size.");
+  if (!PackedFormatOnGpu(prof->ggml_type))
+    throw Unsupported(Cat("DequantizePacked: format ", format, " has no GPU kernel"));
+  Staging st(stream, 0, {x}, {y});
+  LaunchDequantizePacked(prof->ggml_type, static_cast<const uint8_t *>(st.In(x)), count / prof->block_size,
+                         (int)output_dtype, st.Out(y), stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Cast FLOAT -> FLOAT16 / BFLOAT16.
 
 int Cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, hipStream_t stream) {
@@ -1259,6 +1327,13 @@ int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tenso
                                 onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DequantizeLinear(x, x_scale, x_zero_point, axis, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, const int64_t *shape, int32_t rank,
+                                int64_t output_dtype, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizePacked(x, format, shape, rank, output_dtype, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -68,6 +68,14 @@ struct IGemmParams {
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// DequantizePacked, 32-value GGUF formats (ggml type codes 2, 3, 6, 7, 8, 9,
+// 20): nblocks blocks -> 32 * nblocks values of out_dtype (FLOAT, FLOAT16,
+// BFLOAT16 or DOUBLE).
+bool PackedFormatOnGpu(int ggml_type);
+void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, int out_dtype, void *y,
+                            hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // ConvInteger / QLinearConv.  Spatial dims are right-aligned into 3 slots
 // (missing leading dims have size 1, kernel 1, stride 1, dilation 1, pad 0).
 struct ConvGeom {

@@ -326,3 +326,28 @@ def test_conv_validation(olamd):
     rc, _ = qc(ws=f(np.ones(6)), wz=np.zeros(6, np.uint8), B=np.zeros(6, np.int32))
     assert rc == olamd.NOT_INITIALIZED
     assert olamd.conv_shape((2, 3, 9, 8), (4, 3, 3, 3), olamd.conv_attrs(strides=[2, 2])) == (2, 4, 4, 3)
+
+
+def test_dequantize_packed_validation(olamd):
+    """onnx_core/runtime/dequantize_packed.cc:296-343."""
+    d = olamd.describe
+    L = olamd.lib()
+
+    def run(x=np.zeros(36, np.uint8), fmt=b"gguf:q4_0", shape=(2, 32), odt=olamd.FLOAT, y=None):
+        y = np.zeros(shape, np.float32) if y is None else y
+        dims = (ctypes.c_int64 * olamd.MAX_RANK)(*shape)
+        rc = L.onnxl_amd_dequantize_packed(d(x), fmt, dims, len(shape), odt, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(fmt=b"gguf:Q4_0"), "unsupported format 'gguf:Q4_0'."),
+                    (dict(odt=6), "output_dtype must be FLOAT, FLOAT16, BFLOAT16 or DOUBLE."),
+                    (dict(shape=(2, 31), y=np.zeros((2, 31), np.float32)), "last dimension must contain complete blocks."),
+                    (dict(x=np.zeros(36, np.int8)), "x must be a one-dimensional UINT8 tensor."),
+                    (dict(x=np.zeros(35, np.uint8)), "packed input length must match exactly.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    rc, _ = run()
+    assert rc == olamd.NOT_INITIALIZED
+    # a format of the reference with no GPU kernel here
+    rc, _ = run(x=np.zeros(144, np.uint8), fmt=b"gguf:q4_k", shape=(256,), y=np.zeros(256, np.float32))
+    assert rc == olamd.UNSUPPORTED
