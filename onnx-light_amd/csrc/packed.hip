@@ -36,13 +36,32 @@ __constant__ int kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 
 
 __device__ __forceinline__ float Half2(const uint8_t *p) { return F16ToF32((uint16_t)(p[0] | (p[1] << 8))); }
 
+// The output is not read again: vector stores go through a buffer descriptor
+// over the workgroup's share with the write-through policy (sc1), so no dirty
+// lines are left in the L2 to flush at the end of the kernel.
+constexpr int kWriteThrough = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ShareRsrc(void *y, int64_t at, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(y) + at, (short)0, bytes, 0x00020000);
+}
+
 template <int OUT> __device__ __forceinline__ void StoreEight(void *y, int64_t i0, const float *v, bool vec) {
+  constexpr int kBytes = OUT == kFloat ? 32 : 16;  // per thread on the vector paths
   if constexpr (OUT == kFloat) {
     float *dst = static_cast<float *>(y) + i0;
     if (vec) {
-      typedef float v4f __attribute__((ext_vector_type(4)));
-      reinterpret_cast<v4f *>(dst)[0] = v4f{v[0], v[1], v[2], v[3]};
-      reinterpret_cast<v4f *>(dst)[1] = v4f{v[4], v[5], v[6], v[7]};
+      typedef int v4i __attribute__((ext_vector_type(4)));
+      const __amdgpu_buffer_rsrc_t rs =
+          ShareRsrc(y, ((int64_t)blockIdx.x * kPkThreads) * kBytes, kPkThreads * kBytes);
+      const unsigned off = threadIdx.x * kBytes;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          v4i{__builtin_bit_cast(int, v[0]), __builtin_bit_cast(int, v[1]), __builtin_bit_cast(int, v[2]),
+              __builtin_bit_cast(int, v[3])},
+          rs, off, 0, kWriteThrough);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          v4i{__builtin_bit_cast(int, v[4]), __builtin_bit_cast(int, v[5]), __builtin_bit_cast(int, v[6]),
+              __builtin_bit_cast(int, v[7])},
+          rs, off + 16, 0, kWriteThrough);
     } else {
       for (int e = 0; e < 8; ++e) dst[e] = v[e];
     }
@@ -59,7 +78,9 @@ template <int OUT> __device__ __forceinline__ void StoreEight(void *y, int64_t i
       v4i w;
 #pragma unroll
       for (int k = 0; k < 4; ++k) w[k] = (int)((uint32_t)h[2 * k] | (uint32_t)h[2 * k + 1] << 16);
-      *reinterpret_cast<v4i *>(dst) = w;
+      __builtin_amdgcn_raw_buffer_store_b128(w, ShareRsrc(y, ((int64_t)blockIdx.x * kPkThreads) * kBytes,
+                                                          kPkThreads * kBytes),
+                                             threadIdx.x * kBytes, 0, kWriteThrough);
     } else {
       for (int e = 0; e < 8; ++e) dst[e] = h[e];
     }
