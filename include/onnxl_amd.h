@@ -158,6 +158,18 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
 int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, const int64_t *shape,
                                 int32_t rank, int64_t output_dtype, onnxl_amd_tensor *y, void *stream);
 
+/* Fused y = a @ W^T with W = DequantizePacked(x, format, shape = [N, K],
+ * FLOAT16): a FLOAT16 [M, K], y FLOAT16 [M, N] (fp32 accumulation).  The
+ * weight is in the ggml layout, each output's blocks contiguous along K; the
+ * dequantized weights are rounded to FLOAT16 exactly as the unfused chain
+ * rounds them, so only the fp32 summation order differs.  gguf:q4_0 with
+ * M <= 8 and K % 64 == 0; other inputs return ONNXL_AMD_UNSUPPORTED.  No
+ * single reference kernel: it computes the DequantizePacked -> Transpose ->
+ * MatMul chain, onnx_core/runtime/dequantize_packed.cc:334-372 ->
+ * km/kernel_matmul.cc:181-223. */
+int onnxl_amd_dequantize_packed_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const char *format,
+                                       const int64_t *shape, int32_t rank, onnxl_amd_tensor *y, void *stream);
+
 /* Convolution attributes, as the reference's ConvInteger / QLinearConv
  * Attributes: n_* entries of each array are used, 0 means the attribute is
  * absent (kernel_shape from w, strides and dilations 1, pads 0).  pads holds

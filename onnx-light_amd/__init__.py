@@ -92,6 +92,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dynamic_quantize_linear.argtypes = [TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_packed.argtypes = [TP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                                   ctypes.c_int32, ctypes.c_int64, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_packed_matmul.argtypes = [TP, TP, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
+                                                         ctypes.c_int32, TP, ctypes.c_void_p]
         CA = ctypes.POINTER(ConvAttrs)
         L.onnxl_amd_conv_shape.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32,
                                            ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, CA,
@@ -440,6 +442,18 @@ def dequantize_packed(x, format: str, shape, output_dtype: int = FLOAT, out=None
     dims = (ctypes.c_int64 * MAX_RANK)(*shape)
     _check(lib().onnxl_amd_dequantize_packed(describe(x), format.encode(), dims, len(shape), output_dtype,
                                              describe(out), _stream_of(x, out)))
+    return out
+
+
+def dequantize_packed_matmul(a, x, format: str, shape, out=None):
+    """Fused a @ DequantizePacked(x, format, shape=[N, K], FLOAT16)^T."""
+    torch = _torch()
+    N, K = (int(d) for d in shape)
+    if out is None:
+        out = _empty((a.shape[0], N), torch.float16, _device_of(a, x))
+    dims = (ctypes.c_int64 * MAX_RANK)(N, K)
+    _check(lib().onnxl_amd_dequantize_packed_matmul(describe(a), describe(x), format.encode(), dims, 2,
+                                                    describe(out), _stream_of(a, x, out)))
     return out
 
 

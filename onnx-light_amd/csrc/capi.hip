@@ -1046,6 +1046,38 @@ int DequantizePacked(const onnxl_amd_tensor *x, const char *format, const int64_
   return ONNXL_AMD_OK;
 }
 
+// Fused DequantizePacked(gguf:q4_0, shape [N, K], FLOAT16) -> MatMul with the
+// weight transposed: y = a @ W^T.  No single reference kernel: it computes
+// the chain dequantize_packed.cc:334-372 -> km/kernel_matmul.cc:181-223 that a
+// DequantizePacked -> Transpose -> MatMul subgraph runs node by node.
+int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const char *format,
+                           const int64_t *shape, int32_t rank, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(a && x && y && format && shape && rank == 2, "DequantizePackedMatMul: invalid arguments.");
+  CheckDescriptor(a, "a");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y, "y");
+  const int64_t N = shape[0], K = shape[1];
+  OLA_ENFORCE(N >= 0 && K >= 0, "DequantizePacked: dimensions must be nonnegative.");
+  OLA_ENFORCE(a->data_type == kFloat16 && a->rank == 2 && a->dims[1] == K,
+              "DequantizePackedMatMul: a must be FLOAT16 [M, K].");
+  const int64_t M = a->dims[0];
+  OLA_ENFORCE(y->data_type == kFloat16 && ShapeOf(*y) == Shape({M, N}) && y->size_bytes == M * N * 2,
+              "DequantizePackedMatMul: y must be FLOAT16 [M, N].");
+  if (std::strcmp(format, "gguf:q4_0") != 0)
+    throw Unsupported(Cat("DequantizePackedMatMul: format ", format, " has no fused GPU kernel"));
+  OLA_ENFORCE(K % 32 == 0, "DequantizePacked: last dimension must contain complete blocks.");
+  OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
+  OLA_ENFORCE(x->dims[0] == N * (K / 32) * 18 && x->size_bytes == x->dims[0],
+              "DequantizePacked: packed input length must match exactly.");
+  Staging st(stream, 0, {a, x}, {y});
+  const void *ad = st.In(a), *xd = st.In(x);
+  if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");
+  LaunchGemvQ40(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
+                static_cast<uint16_t *>(st.Out(y)), stream);
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Cast FLOAT -> FLOAT16 / BFLOAT16.
 
@@ -1334,6 +1366,13 @@ int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, c
                                 int64_t output_dtype, onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DequantizePacked(x, format, shape, rank, output_dtype, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_packed_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const char *format,
+                                       const int64_t *shape, int32_t rank, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizePackedMatMul(a, x, format, shape, rank, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -74,6 +74,11 @@ void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
 bool PackedFormatOnGpu(int ggml_type);
 void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, int out_dtype, void *y,
                             hipStream_t stream);
+// y[M, N] (FLOAT16) = a[M, K] (FLOAT16) x W^T, W the FLOAT16 decode of a
+// gguf:q4_0 [N, K] weight; M <= 8, K % 64 == 0, a and w dword aligned.
+bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w);
+void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                   hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // ConvInteger / QLinearConv.  Spatial dims are right-aligned into 3 slots

@@ -139,7 +139,154 @@ template <int TYPE> void LaunchPkOut(const uint8_t *x, int64_t nblocks, int out,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused q4_0 GEMV: y[m, n] = sum_k a[m, k] * W[n, k] with W = the FLOAT16
+// DequantizePacked values of a gguf:q4_0 [N, K] weight (ggml layout: the
+// blocks of output n run along k, contiguous).  One wave per output n; each
+// lane takes pairs of blocks (36 bytes, dword aligned when K % 64 == 0).
+// Code byte j holds elements j (low nibble) and j + 16 (high nibble) of its
+// block, so the two form one fp16 pair: (0x6400 | nibble) is 1024 + q exactly,
+// adding -1032 gives q - 8 exactly, and the packed fp16 multiply by d rounds
+// d * (q - 8) to FLOAT16 exactly as the DequantizePacked -> FLOAT16 chain
+// does.  v_dot2_f32_f16 then accumulates with the activation pair
+// (a[k + j], a[k + 16 + j]) in fp32.
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t AsH2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+
+// The workgroup's 4 weight rows are contiguous; they are staged through LDS in
+// chunks of kGvChunkK values per row with 16-byte loads of consecutive
+// addresses (a direct per-lane load of its 36-byte block pair touches every
+// cache line of the wave for 4 bytes at a time).  Each lane then reads its
+// block pair from LDS (a 36-byte stride: no bank conflicts).
+constexpr int kGvChunkK = 4096;                 // values per row per chunk
+constexpr int kGvRowBytes = kGvChunkK / 32 * 18;  // 2304
+
+template <int M>
+__global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
+                                                     int64_t N, int64_t K, uint16_t *__restrict__ y) {
+  __shared__ __align__(16) uint32_t stage[4 * kGvRowBytes / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * 4;
+  const int64_t n = n0 + wave;
+  const int rows = (int)std::min<int64_t>(4, N - n0);
+  const int64_t row_bytes = K / 32 * 18;
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+  const h2_t kMinus1032 = AsH2(0xE408E408u);
+  for (int64_t kc = 0; kc < K; kc += kGvChunkK) {
+    const int64_t chunk_k = std::min<int64_t>(kGvChunkK, K - kc);
+    const int chunk_bytes = (int)(chunk_k / 32 * 18);  // a multiple of 36
+    // stage rows [n0, n0 + rows) of this chunk: row r at stage byte r * chunk_bytes
+    const uint8_t *src = w + n0 * row_bytes + kc / 32 * 18;
+    if ((chunk_bytes & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (row_bytes & 15) == 0) {
+      const int per_row = chunk_bytes / 16;
+      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
+        const int r = i / per_row, c = i - r * per_row;
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + r * row_bytes) + c);
+        reinterpret_cast<v4i *>(stage)[(r * chunk_bytes) / 16 + c] = v;
+      }
+    } else {
+      const int per_row = chunk_bytes / 4;
+      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
+        const int r = i / per_row, c = i - r * per_row;
+        stage[(r * chunk_bytes) / 4 + c] =
+            __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src + r * row_bytes) + c);
+      }
+    }
+    __syncthreads();
+    if (wave < rows) {
+      for (int64_t jj = lane; jj < chunk_k / 64; jj += 64) {
+        const uint32_t *sp = stage + (wave * chunk_bytes + jj * 36) / 4;
+        uint32_t q[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) q[i] = sp[i];
+        const int64_t j = kc / 64 + jj;  // block pair index within the row
+      #pragma unroll
+          for (int blk = 0; blk < 2; ++blk) {
+            // block blk: d in bytes 18*blk + 0..1, codes in bytes 18*blk + 2..17
+            const int base = 18 * blk;
+            const uint32_t dbits = blk == 0 ? (q[0] & 0xffffu) : (q[4] >> 16);
+            const h2_t dd = AsH2(dbits | dbits << 16);
+            uint32_t c[4];  // code dwords, realigned from the 2-byte offset
+      #pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int byte = base + 2 + 4 * t;  // first code byte of this dword
+              const uint32_t lo = q[byte >> 2], hi = q[(byte >> 2) + 1 < 9 ? (byte >> 2) + 1 : 8];  // hi unused when aligned
+              c[t] = (byte & 3) ? __builtin_amdgcn_alignbyte(hi, lo, byte & 3) : lo;
+            }
+            h2_t wp[16];  // weight pairs (element j, element j + 16), j = 0..15
+      #pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const uint32_t lo = c[t] & 0x0F0F0F0Fu, hi = (c[t] >> 4) & 0x0F0F0F0Fu;
+      #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                // bytes: [lo_e, 0, hi_e, 0] | 0x64006400
+                const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + e) << 16) | (uint32_t)e;
+                const uint32_t bits = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+                wp[4 * t + e] = (AsH2(bits) + kMinus1032) * dd;
+              }
+            }
+            const int64_t k0 = (2 * j + blk) * 32;
+      #pragma unroll
+            for (int m = 0; m < M; ++m) {
+              const uint32_t *ar = reinterpret_cast<const uint32_t *>(a + m * K + k0);
+              uint32_t al[8], ah[8];  // a[k0 + 0..15] and a[k0 + 16..31] as half pairs
+      #pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                al[i] = ar[i];
+                ah[i] = ar[8 + i];
+              }
+              float s = acc[m];
+      #pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const h2_t p0 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x05040100u));  // (a[2i], a[16 + 2i])
+                const h2_t p1 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x07060302u));  // (a[2i+1], a[17 + 2i])
+                s = __builtin_amdgcn_fdot2(p0, wp[2 * i], s, false);
+                s = __builtin_amdgcn_fdot2(p1, wp[2 * i + 1], s, false);
+              }
+              acc[m] = s;
+            }
+          }
+      }
+    }
+    __syncthreads();  // the stage is rewritten by the next chunk
+  }
+  if (wave >= rows) return;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float s = acc[m];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) y[m * N + n] = F32ToF16(s);
+  }
+}
+
 }  // namespace
+
+bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w) {
+  return M >= 1 && M <= 8 && K % 64 == 0 && K > 0 && reinterpret_cast<uintptr_t>(w) % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(a) % 4 == 0;
+}
+
+void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                   hipStream_t s) {
+  if (N == 0) return;
+  const dim3 g((unsigned)((N + 3) / 4));
+  switch (M) {
+  case 1: hipLaunchKernelGGL(GemvQ40Kernel<1>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 2: hipLaunchKernelGGL(GemvQ40Kernel<2>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 3: hipLaunchKernelGGL(GemvQ40Kernel<3>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 4: hipLaunchKernelGGL(GemvQ40Kernel<4>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 5: hipLaunchKernelGGL(GemvQ40Kernel<5>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 6: hipLaunchKernelGGL(GemvQ40Kernel<6>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 7: hipLaunchKernelGGL(GemvQ40Kernel<7>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 8: hipLaunchKernelGGL(GemvQ40Kernel<8>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  default: throw Unsupported("q4_0 GEMV: M above 8");
+  }
+}
 
 bool PackedFormatOnGpu(int ggml_type) {
   return ggml_type == 2 || ggml_type == 3 || ggml_type == 6 || ggml_type == 7 || ggml_type == 8 ||
