@@ -154,26 +154,31 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ h2_t AsH2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 
-// The workgroup's 4 weight rows are contiguous; they are staged through LDS in
-// chunks of kGvChunkK values per row with 16-byte loads of consecutive
-// addresses (a direct per-lane load of its 36-byte block pair touches every
-// cache line of the wave for 4 bytes at a time).  Each lane then reads its
-// block pair from LDS (a 36-byte stride: no bank conflicts).
-constexpr int kGvChunkK = 4096;                 // values per row per chunk
+// Each wave computes kGvCols consecutive outputs at once, so the activation
+// pairs it loads for a block serve all of them (loading and pairing the
+// activation per output cost as much as the weight stream).  The
+// workgroup's 4 * kGvCols weight rows are contiguous; they are staged through
+// LDS in chunks of kGvChunkK values per row with 16-byte loads of
+// consecutive addresses, and each lane reads its block pairs from there (a
+// 36-byte stride: no bank conflicts).
+constexpr int kGvCols = 4;
+constexpr int kGvRows = 4 * kGvCols;              // outputs per workgroup
+constexpr int kGvChunkK = 4096;                   // values per row per chunk: 64 block pairs, one per lane
 constexpr int kGvRowBytes = kGvChunkK / 32 * 18;  // 2304
 
 template <int M>
 __global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
                                                      int64_t N, int64_t K, uint16_t *__restrict__ y) {
-  __shared__ __align__(16) uint32_t stage[4 * kGvRowBytes / 4];
+  __shared__ __align__(16) uint32_t stage[kGvRows * kGvRowBytes / 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * 4;
-  const int64_t n = n0 + wave;
-  const int rows = (int)std::min<int64_t>(4, N - n0);
+  const int64_t n0 = (int64_t)blockIdx.x * kGvRows;
+  const int rows = (int)std::min<int64_t>(kGvRows, N - n0);
   const int64_t row_bytes = K / 32 * 18;
-  float acc[M];
+  float acc[kGvCols][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+  for (int c = 0; c < kGvCols; ++c)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[c][m] = 0.f;
   const h2_t kMinus1032 = AsH2(0xE408E408u);
   for (int64_t kc = 0; kc < K; kc += kGvChunkK) {
     const int64_t chunk_k = std::min<int64_t>(kGvChunkK, K - kc);
@@ -197,70 +202,78 @@ __global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict_
       }
     }
     __syncthreads();
-    if (wave < rows) {
-      for (int64_t jj = lane; jj < chunk_k / 64; jj += 64) {
-        const uint32_t *sp = stage + (wave * chunk_bytes + jj * 36) / 4;
-        uint32_t q[9];
+    for (int64_t jj = lane; jj < chunk_k / 64; jj += 64) {
 #pragma unroll
-        for (int i = 0; i < 9; ++i) q[i] = sp[i];
-        const int64_t j = kc / 64 + jj;  // block pair index within the row
-      #pragma unroll
-          for (int blk = 0; blk < 2; ++blk) {
-            // block blk: d in bytes 18*blk + 0..1, codes in bytes 18*blk + 2..17
-            const int base = 18 * blk;
-            const uint32_t dbits = blk == 0 ? (q[0] & 0xffffu) : (q[4] >> 16);
-            const h2_t dd = AsH2(dbits | dbits << 16);
-            uint32_t c[4];  // code dwords, realigned from the 2-byte offset
-      #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int byte = base + 2 + 4 * t;  // first code byte of this dword
-              const uint32_t lo = q[byte >> 2], hi = q[(byte >> 2) + 1 < 9 ? (byte >> 2) + 1 : 8];  // hi unused when aligned
-              c[t] = (byte & 3) ? __builtin_amdgcn_alignbyte(hi, lo, byte & 3) : lo;
-            }
-            h2_t wp[16];  // weight pairs (element j, element j + 16), j = 0..15
-      #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const uint32_t lo = c[t] & 0x0F0F0F0Fu, hi = (c[t] >> 4) & 0x0F0F0F0Fu;
-      #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                // bytes: [lo_e, 0, hi_e, 0] | 0x64006400
-                const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + e) << 16) | (uint32_t)e;
-                const uint32_t bits = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
-                wp[4 * t + e] = (AsH2(bits) + kMinus1032) * dd;
-              }
-            }
-            const int64_t k0 = (2 * j + blk) * 32;
-      #pragma unroll
-            for (int m = 0; m < M; ++m) {
-              const uint32_t *ar = reinterpret_cast<const uint32_t *>(a + m * K + k0);
-              uint32_t al[8], ah[8];  // a[k0 + 0..15] and a[k0 + 16..31] as half pairs
-      #pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                al[i] = ar[i];
-                ah[i] = ar[8 + i];
-              }
-              float s = acc[m];
-      #pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                const h2_t p0 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x05040100u));  // (a[2i], a[16 + 2i])
-                const h2_t p1 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x07060302u));  // (a[2i+1], a[17 + 2i])
-                s = __builtin_amdgcn_fdot2(p0, wp[2 * i], s, false);
-                s = __builtin_amdgcn_fdot2(p1, wp[2 * i + 1], s, false);
-              }
-              acc[m] = s;
+      for (int blk = 0; blk < 2; ++blk) {
+        // weight pairs (element j, element j + 16) of this block for each column
+        h2_t wp[kGvCols][16];
+#pragma unroll
+        for (int c = 0; c < kGvCols; ++c) {
+          const int r = wave * kGvCols + c;
+          const int rr = r < rows ? r : 0;  // rows past N decode row 0 and are not stored
+          const uint32_t *sp = stage + (rr * chunk_bytes + jj * 36 + 18 * blk - 2 * blk) / 4;
+          // the block starts 18 * blk bytes into the pair (2 bytes into a dword
+          // for blk 1): the 5 dwords from the one at or before its start cover
+          // it, and stay inside the 36-byte pair; q[5] only feeds an unused
+          // high word
+          uint32_t q[6];
+#pragma unroll
+          for (int i = 0; i < 5; ++i) q[i] = sp[i];
+          q[5] = q[4];
+          const int sh = blk ? 2 : 0;  // byte offset of the block in q[0]
+          const uint32_t q0 = sh ? __builtin_amdgcn_alignbyte(q[1], q[0], 2) : q[0];
+          const uint32_t dbits = q0 & 0xffffu;
+          const h2_t dd = AsH2(dbits | dbits << 16);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int byte = sh + 2 + 4 * t;  // first code byte of this dword within q
+            const uint32_t lo = q[byte >> 2], hi = q[(byte >> 2) + 1];
+            const uint32_t cw = (byte & 3) ? __builtin_amdgcn_alignbyte(hi, lo, byte & 3) : lo;
+            const uint32_t nl = cw & 0x0F0F0F0Fu, nh = (cw >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              // bytes: [lo_e, 0, hi_e, 0] | 0x64006400
+              const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + e) << 16) | (uint32_t)e;
+              const uint32_t bits = __builtin_amdgcn_perm(nh, nl, sel) | 0x64006400u;
+              wp[c][4 * t + e] = (AsH2(bits) + kMinus1032) * dd;
             }
           }
+        }
+        const int64_t k0 = (2 * (kc / 64 + jj) + blk) * 32;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint32_t *ar = reinterpret_cast<const uint32_t *>(a + m * K + k0);
+          uint32_t al[8], ah[8];  // a[k0 + 0..15] and a[k0 + 16..31] as half pairs
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            al[i] = ar[i];
+            ah[i] = ar[8 + i];
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const h2_t p0 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x05040100u));  // (a[2i], a[16 + 2i])
+            const h2_t p1 = AsH2(__builtin_amdgcn_perm(ah[i], al[i], 0x07060302u));  // (a[2i+1], a[17 + 2i])
+#pragma unroll
+            for (int c = 0; c < kGvCols; ++c) {
+              acc[c][m] = __builtin_amdgcn_fdot2(p0, wp[c][2 * i], acc[c][m], false);
+              acc[c][m] = __builtin_amdgcn_fdot2(p1, wp[c][2 * i + 1], acc[c][m], false);
+            }
+          }
+        }
       }
     }
     __syncthreads();  // the stage is rewritten by the next chunk
   }
-  if (wave >= rows) return;
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float s = acc[m];
+  for (int c = 0; c < kGvCols; ++c) {
+    const int64_t n = n0 + wave * kGvCols + c;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) y[m * N + n] = F32ToF16(s);
+    for (int m = 0; m < M; ++m) {
+      float s = acc[c][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0 && n < N) y[m * N + n] = F32ToF16(s);
+    }
   }
 }
 
@@ -274,7 +287,7 @@ bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w) {
 void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t s) {
   if (N == 0) return;
-  const dim3 g((unsigned)((N + 3) / 4));
+  const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
   switch (M) {
   case 1: hipLaunchKernelGGL(GemvQ40Kernel<1>, g, dim3(256), 0, s, a, w, N, K, y); break;
   case 2: hipLaunchKernelGGL(GemvQ40Kernel<2>, g, dim3(256), 0, s, a, w, N, K, y); break;
