@@ -123,8 +123,6 @@ DQ_CASES = [
 @pytest.mark.parametrize("with_zp", [False, True], ids=["nozp", "zp"])
 def test_dequantize_vs_oracle(olamd, oracle, dev, case, s16, with_zp):
     kind, shape, skind, axis, block = case
-    if kind == "fp8" and with_zp:
-        pytest.skip("float8 zero points are zero in practice; covered by the fallback path")
     rng = np.random.default_rng(zlib.crc32(repr((case, s16, with_zp)).encode()))
     n = int(np.prod(shape))
     if kind in ("int4", "uint4"):
@@ -155,6 +153,9 @@ def test_dequantize_vs_oracle(olamd, oracle, dev, case, s16, with_zp):
         if kind in ("int4", "uint4"):
             lo, hi = (-8, 8) if kind == "int4" else (0, 16)
             zp = oracle.pack_int4(rng.integers(lo, hi, m))
+        elif kind == "fp8":  # finite fp8 zero points, signed and fractional
+            zp = oracle.f32_to_f8e4m3fn_bits(rng.choice([0.0, 0.5, -1.0, 2.0, -3.5, 448.0], m).astype(np.float32))
+            zp = zp.reshape(s_shape)
         else:
             zp = rng.integers(-20 if kind not in ("uint8", "uint16") else 0, 30, m).astype(x.dtype).reshape(s_shape)
     got = olamd.dequantize_linear(T(x, dev), T(sc, dev), None if zp is None else T(zp, dev), axis=axis,
