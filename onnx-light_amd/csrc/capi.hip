@@ -792,8 +792,8 @@ bool PresentOptional(const onnxl_amd_tensor *t) { return !(Absent(t) || (t->rank
 // batch), B = Col [N, G, Kc, P], Y = [N, G, Mg, P] int32 sums.  a_zp: Mg
 // per-row weight zero points on device (group 1 only), or nullptr with the
 // scalar w_zp.
-void LaunchConvGemm(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t *a_zp, int32_t w_zp,
-                    const uint8_t *col, int x_u8, int32_t x_zp, int32_t *y, hipStream_t stream) {
+IGemmParams ConvGemmParams(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t *a_zp, int32_t w_zp,
+                           const uint8_t *col, int x_u8, int32_t x_zp, void *y) {
   IGemmParams p{};
   p.A = reinterpret_cast<const int8_t *>(w);
   p.B = reinterpret_cast<const int8_t *>(col);
@@ -818,7 +818,12 @@ void LaunchConvGemm(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t
   p.need_cb = a_zp != nullptr || p.alpha_scalar != 0;
   p.need_ra = p.beta_scalar != 0;
   p.epilogue = kEpiInt32;
-  LaunchIGemm(p, stream);
+  return p;
+}
+
+void LaunchConvGemm(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t *a_zp, int32_t w_zp,
+                    const uint8_t *col, int x_u8, int32_t x_zp, int32_t *y, hipStream_t stream) {
+  LaunchIGemm(ConvGemmParams(g, w, w_u8, a_zp, w_zp, col, x_u8, x_zp, y), stream);
 }
 
 int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnxl_amd_tensor *x_zp,
@@ -967,8 +972,25 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
         col = static_cast<uint8_t *>(st.Extra());
         LaunchImToCol(g, xd, (uint8_t)xz, static_cast<uint8_t *>(st.Extra()), stream);
       }
-      LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, acc, stream);
-      LaunchConvRequant(g, acc, q, yd, stream);
+      // group 1 on the pipelined kernel: the GEMM epilogue requantizes each
+      // output channel's row itself; otherwise int32 sums, then the pass
+      IGemmParams p = ConvGemmParams(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, yd);
+      p.epilogue = kEpiQuant8Row;
+      p.zy = q.zy;
+      p.qmin = q.qmin;
+      p.qmax = q.qmax;
+      p.y_signed = y_signed;
+      p.row_wscale = q.w_scale;
+      p.row_wscale_per = q.w_scale_per_channel;
+      p.row_xs = q.x_scale;
+      p.row_ys = q.y_scale;
+      p.row_bias = q.bias;
+      if (g.G == 1 && IGemmFastEligible(p)) {
+        LaunchIGemm(p, stream);
+      } else {
+        LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, acc, stream);
+        LaunchConvRequant(g, acc, q, yd, stream);
+      }
     } else {
       LaunchDirectConv(g, xd, x->data_type == kUint8, (uint8_t)xz, wd, w->data_type == kUint8, wzd, wz, &q, yd,
                        stream);

@@ -28,6 +28,7 @@
 //    so tiles sharing A rows / B columns share that XCD's L2.
 #include <cstdlib>
 
+#include "common.hpp"
 #include "kernels.hpp"
 #include "igemm_fast.hpp"
 
@@ -597,14 +598,18 @@ void LaunchEpi(const IGemmParams &p, int mode, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
+bool IGemmFastEligible(const IGemmParams &p) { return mg::Eligible<mg::kI8>(ToGemmArgs(p)); }
+
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return;
   // K % 128 == 0: the pipelined MFMA core (mfma_gemm.hpp).
   if (mg::Eligible<mg::kI8>(ToGemmArgs(p))) {
     if (p.epilogue == kEpiInt32) LaunchIGemmFastI32(p, stream);
+    else if (p.epilogue == kEpiQuant8Row) LaunchIGemmFastQ8Row(p, stream);
     else LaunchIGemmFastQ8(p, stream);
     return;
   }
+  if (p.epilogue == kEpiQuant8Row) throw DeviceError("internal: per-row requantization needs the pipelined GEMM");
   static const int stages_env = [] {
     const char *e = std::getenv("ONNXL_AMD_IGEMM_STAGES");
     return e ? std::atoi(e) : 0;

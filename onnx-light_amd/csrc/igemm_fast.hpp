@@ -29,6 +29,11 @@ inline mg::GemmArgs ToGemmArgs(const IGemmParams &p) {
   g.qmin = p.qmin;
   g.qmax = p.qmax;
   g.y_signed = p.y_signed;
+  g.row_wscale = p.row_wscale;
+  g.row_wscale_per = p.row_wscale_per;
+  g.row_xs = p.row_xs;
+  g.row_ys = p.row_ys;
+  g.row_bias = p.row_bias;
   return g;
 }
 
@@ -51,5 +56,6 @@ template <int OUT> void LaunchIGemmFastOut(const IGemmParams &p, hipStream_t s) 
 
 void LaunchIGemmFastI32(const IGemmParams &p, hipStream_t s);
 void LaunchIGemmFastQ8(const IGemmParams &p, hipStream_t s);
+void LaunchIGemmFastQ8Row(const IGemmParams &p, hipStream_t s);
 
 }  // namespace onnxl_amd

@@ -42,7 +42,7 @@ __host__ __device__ inline void BatchOffsets(const BatchMap &m, int64_t batch, i
 // RA_i = sum_k a'_ik, CB_j = sum_k b'_kj, evaluated modulo 2^32 (which is the
 // int32 wrap of the reference's accumulator).
 
-enum IGemmEpilogue : int { kEpiInt32 = 0, kEpiQuant8 = 1 };
+enum IGemmEpilogue : int { kEpiInt32 = 0, kEpiQuant8 = 1, kEpiQuant8Row = 2 };
 
 struct IGemmParams {
   const int8_t *A;  // [.., M, K] row-major
@@ -63,9 +63,19 @@ struct IGemmParams {
   float cs, zy, qmin, qmax;
   int y_signed;
   int epilogue;
+  // kEpiQuant8Row (pipelined kernel only): row r uses the scale
+  // row_xs * row_wscale[r or 0] / row_ys and adds row_bias[r] (if not null)
+  // to the int32 sum exactly before the conversion.
+  const float *row_wscale;
+  int row_wscale_per;
+  float row_xs, row_ys;
+  const int32_t *row_bias;
 };
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
+// Whether LaunchIGemm takes the pipelined MFMA kernel for p (kEpiQuant8Row
+// requires it).
+bool IGemmFastEligible(const IGemmParams &p);
 
 // ---------------------------------------------------------------------------
 // DequantizePacked, 32-value GGUF formats (ggml type codes 2, 3, 6, 7, 8, 9,

@@ -92,7 +92,9 @@ constexpr int kStoreThrough = 16;
 enum Kind : int { kI8 = 0, kBf16F8 = 1, kH16 = 2 };
 
 // Output conversions.
-enum Out : int { kOutI32 = 0, kOutQ8 = 1, kOutF16 = 2, kOutBf16 = 3 };
+// kOutQ8Row: the 8-bit requantization of kOutQ8 with a scale and an int32
+// bias per output row (QLinearConv's per-output-channel w_scale and B).
+enum Out : int { kOutI32 = 0, kOutQ8 = 1, kOutF16 = 2, kOutBf16 = 3, kOutQ8Row = 4 };
 
 template <int KIND> struct Traits;
 template <> struct Traits<kI8> {
@@ -172,6 +174,13 @@ struct GemmArgs {
   // Row pitches of B and Y in elements (0: N), so a launch can cover a
   // column range of larger matrices; N stays the width computed.
   int64_t ldb, ldy;
+  // kOutQ8Row: row r is requantized with (row_xs * row_wscale[r] / row_ys)
+  // (index 0 when !row_wscale_per) after adding row_bias[r] (none when null)
+  // in exact integer arithmetic.
+  const float *row_wscale;
+  int row_wscale_per;
+  float row_xs, row_ys;
+  const int32_t *row_bias;
 };
 
 template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB>
@@ -186,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int L = LoadsPerWave<KIND, WB>();
   constexpr int LB = BLoadsPerWave<KIND, WB>();
   static_assert(WB == 2 || (WB == 4 && KIND != kH16), "tile width");
-  constexpr int kOsz = OUT == kOutI32 ? 4 : (OUT == kOutQ8 ? 1 : 2);
+  constexpr int kOsz = OUT == kOutI32 ? 4 : (OUT == kOutQ8 || OUT == kOutQ8Row ? 1 : 2);
   static_assert(LB >= 1 && LB <= 4, "B direct loads per wave");
   // One object per ring stage: the compiler's LDS-DMA wait tracking can then
   // tell a read of one stage from a direct load into another.
@@ -666,6 +675,16 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       ra_r = rsum[i] + __shfl_xor(rsum[i], 32);
       al_r = zrow[i];
     }
+    // kOutQ8Row: this lane's output row (row0 + wm * 128 + 32 i + lr) scale
+    // and bias, computed with the fp32 operations of the reference
+    float cs_r = p.cs;
+    double bias_r = 0.0;
+    if constexpr (OUT == kOutQ8Row) {
+      const int64_t row = row0 + wm * 128 + i * 32 + lr;
+      const int64_t rc = row < M ? row : 0;
+      cs_r = p.row_xs * p.row_wscale[p.row_wscale_per ? rc : 0] / p.row_ys;
+      bias_r = p.row_bias ? (double)p.row_bias[rc] : 0.0;
+    }
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
 #pragma unroll
@@ -696,7 +715,15 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
             unsigned packed = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + q_zy;
+              float f;
+              if constexpr (OUT == kOutQ8Row) {
+                // (float) of the exact int64 sum acc + bias (the double sum is
+                // exact below 2^53); NaN lands as 0 as through the x86-64 cast
+                f = __builtin_rintf((float)((double)(int32_t)v[e] + bias_r) * cs_r) + q_zy;
+                if (f != f) f = q_bias;
+              } else {
+                f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + q_zy;
+              }
               packed = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(f, q_lo, q_hi), e, packed);
             }
             *reinterpret_cast<unsigned *>(dst) = packed ^ q_flip;
