@@ -16,14 +16,15 @@ reported as `host_path_ms_per_step`.  `cpu_baseline` times the serial CPU
 oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv|pk|pkgemv]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
-GGUF q4_0 weight decode (`pk`) and the fused q4_0 GEMV (`pkgemv`) are timed too and reported under `extra`
-unless --no-extra is given.
+GGUF q4_0 weight decode (`pk`) and the fused q4_0 / q8_0 GEMVs (`pkgemv`,
+`pkgemv8`) are timed too and reported under `extra` unless --no-extra is
+given.
 """
 from __future__ import annotations
 
@@ -222,18 +223,21 @@ def make_pk(olamd, dev, replicas):
     return w
 
 
-def make_pkgemv(olamd, dev, replicas):
-    """Fused GEMV y[1, 14336] = a[1, 4096] @ DequantizePacked(gguf:q4_0,
-    [14336, 4096], FLOAT16)^T: 18 bytes of weight per 32 values dominate."""
+def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
+    """Fused GEMV y[1, 14336] = a[1, 4096] @ DequantizePacked(gguf:q4_0 or
+    gguf:q8_0, [14336, 4096], FLOAT16)^T: the weight's 18 (q4_0) or 34 (q8_0)
+    bytes per 32 values dominate."""
     import torch
     w = Workload()
-    w.name = "GEMV fp16[1,4096] x DequantizePacked(gguf:q4_0 [14336,4096])^T -> fp16[1,14336]"
-    w.key, w.unit, w.dtype, w.bound = "pkgemv", "GB/s", "f16 (fp32 accumulate)", "hbm"
+    block_bytes = {"q4_0": 18, "q8_0": 34}[fmt]
+    w.name = f"GEMV fp16[1,4096] x DequantizePacked(gguf:{fmt} [14336,4096])^T -> fp16[1,14336]"
+    w.key = "pkgemv" if fmt == "q4_0" else "pkgemv8"
+    w.unit, w.dtype, w.bound = "GB/s", "f16 (fp32 accumulate)", "hbm"
     N, K = 14336, 4096
-    w.nbytes = N * K // 32 * 18 + K * 2 + N * 2
+    w.nbytes = N * K // 32 * block_bytes + K * 2 + N * 2
     w.work = float(w.nbytes)
     rng = np.random.default_rng(41)
-    blocks = rng.integers(0, 256, (N * K // 32, 18)).astype(np.uint8)
+    blocks = rng.integers(0, 256, (N * K // 32, block_bytes)).astype(np.uint8)
     d = np.float16(rng.uniform(0.001, 0.05, N * K // 32)).view(np.uint16)
     blocks[:, 0], blocks[:, 1] = d & 255, d >> 8
     a = _t(np.float16(rng.standard_normal((1, K))), dev)
@@ -243,7 +247,8 @@ def make_pkgemv(olamd, dev, replicas):
         y = torch.empty((1, N), dtype=torch.float16, device=dev)
         dims = (ctypes.c_int64 * olamd.MAX_RANK)(N, K)
         w.calls.append(olamd.Prepared("onnxl_amd_dequantize_packed_matmul",
-                                      [olamd.describe(a), olamd.describe(x), b"gguf:q4_0", dims, 2, olamd.describe(y)],
+                                      [olamd.describe(a), olamd.describe(x), f"gguf:{fmt}".encode(), dims, 2,
+                                       olamd.describe(y)],
                                       (a, x, y, dims), olamd._stream_of(x)))
     return w
 
@@ -409,7 +414,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv"])
+                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv", "pkgemv8"])
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -446,6 +451,8 @@ def main():
             return make_pk(olamd, dev, args.replicas or 4)
         if key == "pkgemv":
             return make_pkgemv(olamd, dev, args.replicas or 10)
+        if key == "pkgemv8":
+            return make_pkgemv(olamd, dev, args.replicas or 10, "q8_0")
         return make_c5(olamd, dev, args.replicas or 16)
 
     w = build(args.workload)
@@ -460,7 +467,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv"):
+        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv", "pkgemv8"):
             if key == args.workload:
                 continue
             try:

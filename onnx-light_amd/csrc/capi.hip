@@ -1085,17 +1085,18 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
   const int64_t M = a->dims[0];
   OLA_ENFORCE(y->data_type == kFloat16 && ShapeOf(*y) == Shape({M, N}) && y->size_bytes == M * N * 2,
               "DequantizePackedMatMul: y must be FLOAT16 [M, N].");
-  if (std::strcmp(format, "gguf:q4_0") != 0)
+  const bool q8 = std::strcmp(format, "gguf:q8_0") == 0;
+  if (!q8 && std::strcmp(format, "gguf:q4_0") != 0)
     throw Unsupported(Cat("DequantizePackedMatMul: format ", format, " has no fused GPU kernel"));
   OLA_ENFORCE(K % 32 == 0, "DequantizePacked: last dimension must contain complete blocks.");
   OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
-  OLA_ENFORCE(x->dims[0] == N * (K / 32) * 18 && x->size_bytes == x->dims[0],
+  OLA_ENFORCE(x->dims[0] == N * (K / 32) * (q8 ? 34 : 18) && x->size_bytes == x->dims[0],
               "DequantizePacked: packed input length must match exactly.");
   Staging st(stream, 0, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
-  if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");
-  LaunchGemvQ40(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
-                static_cast<uint16_t *>(st.Out(y)), stream);
+  if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");  // q8_0 alike
+  (q8 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
+                                       static_cast<uint16_t *>(st.Out(y)), stream);
   st.Finish();
   return ONNXL_AMD_OK;
 }

@@ -89,6 +89,9 @@ void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, in
 bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w);
 void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t stream);
+// The same for gguf:q8_0 (same eligibility).
+void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                   hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // ConvInteger / QLinearConv.  Spatial dims are right-aligned into 3 slots

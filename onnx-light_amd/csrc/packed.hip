@@ -277,7 +277,123 @@ __global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict_
   }
 }
 
+// Fused q8_0 GEMV, as the q4_0 one: y[m, n] = sum_k a[m, k] * W[n, k] with W
+// the FLOAT16 decode of a gguf:q8_0 [N, K] weight (34-byte blocks: fp16 d and
+// 32 int8 codes).  Chunks of 2048 values give one block per lane (64 blocks
+// per row); a lane reads its block as the 9 dwords from the one at or before
+// its start (34-byte stride, 0 or 2 bytes into the dword).  Codes pair as
+// consecutive elements: (b ^ 0x80) | 0x6400 is 1152 + q exactly, one XOR
+// with 0x64806480 for two codes placed in bytes 0 and 2; adding -1152 gives q
+// and the packed multiply by d rounds d * q to FLOAT16 as the chain does.
+constexpr int kGv8ChunkK = 2048;
+constexpr int kGv8RowBytes = kGv8ChunkK / 32 * 34;  // 2176
+
+template <int M>
+__global__ __launch_bounds__(256) void GemvQ80Kernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
+                                                     int64_t N, int64_t K, uint16_t *__restrict__ y) {
+  __shared__ __align__(16) uint32_t stage[kGvRows * kGv8RowBytes / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * kGvRows;
+  const int rows = (int)std::min<int64_t>(kGvRows, N - n0);
+  const int64_t row_bytes = K / 32 * 34;
+  float acc[kGvCols][M];
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[c][m] = 0.f;
+  const h2_t kMinus1152 = AsH2(0xE480E480u);
+  for (int64_t kc = 0; kc < K; kc += kGv8ChunkK) {
+    const int64_t chunk_k = std::min<int64_t>(kGv8ChunkK, K - kc);
+    const int cb = (int)(chunk_k / 32 * 34);  // a multiple of 68
+    const uint8_t *src = w + n0 * row_bytes + kc / 32 * 34;
+    if ((cb & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (row_bytes & 15) == 0) {
+      const int per_row = cb / 16;
+      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
+        const int r = i / per_row, c = i - r * per_row;
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + r * row_bytes) + c);
+        reinterpret_cast<v4i *>(stage)[(r * cb) / 16 + c] = v;
+      }
+    } else {
+      const int per_row = cb / 4;
+      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
+        const int r = i / per_row, c = i - r * per_row;
+        stage[(r * cb) / 4 + c] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src + r * row_bytes) + c);
+      }
+    }
+    __syncthreads();
+    const int64_t jb = lane;  // block of this lane within the chunk
+    if (jb < chunk_k / 32) {
+      h2_t wp[kGvCols][16];  // weight pairs (element 2i, element 2i + 1) per column
+#pragma unroll
+      for (int c = 0; c < kGvCols; ++c) {
+        const int r = wave * kGvCols + c;
+        const int rr = r < rows ? r : 0;  // rows past N decode row 0 and are not stored
+        const int byte0 = rr * cb + (int)jb * 34;  // 2-byte aligned
+        const uint32_t *sp = stage + (byte0 >> 2);
+        const int sh = byte0 & 3;  // 0 or 2
+        uint32_t q[10];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) q[i] = sp[i];  // 36 bytes; the block ends at or before the last
+        q[9] = q[8];
+        const uint32_t dbits = __builtin_amdgcn_alignbyte(q[1], q[0], sh) & 0xffffu;
+        const h2_t dd = AsH2(dbits | dbits << 16);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int at = sh + 2 + 4 * t;  // code bytes 4t .. 4t + 3, at bytes into q
+          const uint32_t cw = __builtin_amdgcn_alignbyte(q[(at >> 2) + 1], q[at >> 2], at & 3);
+          // [b0, 0, b1, 0] and [b2, 0, b3, 0], then the offset into 1152 + q
+          const uint32_t lo = __builtin_amdgcn_perm(0u, cw, 0x0c010c00u) ^ 0x64806480u;
+          const uint32_t hi = __builtin_amdgcn_perm(0u, cw, 0x0c030c02u) ^ 0x64806480u;
+          wp[c][2 * t] = (AsH2(lo) + kMinus1152) * dd;
+          wp[c][2 * t + 1] = (AsH2(hi) + kMinus1152) * dd;
+        }
+      }
+      const int64_t k0 = kc + jb * 32;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint32_t *ar = reinterpret_cast<const uint32_t *>(a + m * K + k0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const h2_t ap = AsH2(ar[i]);  // (a[2i], a[2i + 1])
+#pragma unroll
+          for (int c = 0; c < kGvCols; ++c) acc[c][m] = __builtin_amdgcn_fdot2(ap, wp[c][i], acc[c][m], false);
+        }
+      }
+    }
+    __syncthreads();  // the stage is rewritten by the next chunk
+  }
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c) {
+    const int64_t n = n0 + wave * kGvCols + c;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float s = acc[c][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0 && n < N) y[m * N + n] = F32ToF16(s);
+    }
+  }
+}
+
 }  // namespace
+
+void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                   hipStream_t s) {
+  if (N == 0) return;
+  const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
+  switch (M) {
+  case 1: hipLaunchKernelGGL(GemvQ80Kernel<1>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 2: hipLaunchKernelGGL(GemvQ80Kernel<2>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 3: hipLaunchKernelGGL(GemvQ80Kernel<3>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 4: hipLaunchKernelGGL(GemvQ80Kernel<4>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 5: hipLaunchKernelGGL(GemvQ80Kernel<5>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 6: hipLaunchKernelGGL(GemvQ80Kernel<6>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 7: hipLaunchKernelGGL(GemvQ80Kernel<7>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 8: hipLaunchKernelGGL(GemvQ80Kernel<8>, g, dim3(256), 0, s, a, w, N, K, y); break;
+  default: throw Unsupported("q8_0 GEMV: M above 8");
+  }
+}
 
 bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w) {
   return M >= 1 && M <= 8 && K % 64 == 0 && K > 0 && reinterpret_cast<uintptr_t>(w) % 4 == 0 &&

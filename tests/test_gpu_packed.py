@@ -72,40 +72,51 @@ def test_empty_shape(olamd, dev):
     assert tuple(y.shape) == (0, 32)
 
 
-# ---- fused q4_0 GEMV: y = a @ DequantizePacked(W)^T --------------------------
+# ---- fused q4_0 / q8_0 GEMV: y = a @ DequantizePacked(W)^T -------------------
 
-def _q4_0_weight(rng, N, K):
-    blocks = rng.integers(0, 256, (N * K // 32, 18)).astype(np.uint8)
+def _block_weight(rng, N, K, block_bytes):
+    blocks = rng.integers(0, 256, (N * K // 32, block_bytes)).astype(np.uint8)
     d = np.float16(rng.uniform(0.001, 0.05, N * K // 32)).view(np.uint16)
     blocks[:, 0], blocks[:, 1] = d & 255, d >> 8
     return blocks.reshape(-1)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 96, 64), (3, 200, 256), (8, 64, 4096), (2, 1000, 1024), (1, 14336, 4096)])
-def test_q4_0_gemv_vs_chain(olamd, oracle, dev, M, N, K):
-    """The chain: DequantizePacked(gguf:q4_0, [N, K], FLOAT16), then the fp16
+def _q4_0_weight(rng, N, K):
+    return _block_weight(rng, N, K, 18)
+
+
+_GEMV_SHAPES = [(1, 96, 64), (3, 200, 256), (8, 64, 4096), (2, 1000, 1024), (1, 14336, 4096), (5, 37, 2112),
+                (4, 129, 6144)]
+
+
+@pytest.mark.parametrize("fmt,block_bytes", [("gguf:q4_0", 18), ("gguf:q8_0", 34)])
+@pytest.mark.parametrize("M,N,K", _GEMV_SHAPES)
+def test_packed_gemv_vs_chain(olamd, oracle, dev, fmt, block_bytes, M, N, K):
+    """The chain: DequantizePacked(fmt, [N, K], FLOAT16), then the fp16
     MatMul of a with its transpose (fp32 accumulation).  The fused kernel
     rounds the weights exactly as the chain does; only the summation order
     differs, so the float path's tolerance applies:
         |got - ref| <= 1e-2 * |ref| + 2^-11 * sum_k |a_mk * w_nk|."""
     from test_gpu_float import assert_close
-    rng = np.random.default_rng(M * 7919 + N * 31 + K)
-    x = _q4_0_weight(rng, N, K)
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + block_bytes)
+    x = _block_weight(rng, N, K, block_bytes)
     a = np.float16(rng.standard_normal((M, K)))
-    w_bits = oracle.dequantize_packed(x, "gguf:q4_0", (N, K), 10)
+    w_bits = oracle.dequantize_packed(x, fmt, (N, K), 10)
     ref = oracle.matmul_half(a.view(np.uint16), np.ascontiguousarray(w_bits.T), 10)
-    got = olamd.dequantize_packed_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(x).to(dev), "gguf:q4_0",
-                                         (N, K))
+    got = olamd.dequantize_packed_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(x).to(dev), fmt, (N, K))
     got_bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
     mag = np.abs(a.astype(np.float64)) @ np.abs(oracle.f16_bits_to_f32(w_bits).astype(np.float64)).T
-    assert_close(got_bits, ref, mag, "f16", oracle, f"q4_0 gemv {M}x{N}x{K}")
+    assert_close(got_bits, ref, mag, "f16", oracle, f"{fmt} gemv {M}x{N}x{K}")
 
 
-def test_q4_0_gemv_unsupported(olamd, dev):
+def test_packed_gemv_unsupported(olamd, dev):
     a = torch.zeros((9, 64), dtype=torch.float16, device=dev)
     x = torch.zeros(4 * 2 * 18, dtype=torch.uint8, device=dev)
     with pytest.raises(olamd.Unsupported):
         olamd.dequantize_packed_matmul(a, x, "gguf:q4_0", (4, 64))
     with pytest.raises(olamd.Unsupported):
-        olamd.dequantize_packed_matmul(a[:1], torch.zeros(4 * 2 * 34, dtype=torch.uint8, device=dev),
-                                       "gguf:q8_0", (4, 64))
+        olamd.dequantize_packed_matmul(a[:1], torch.zeros(4 * 2 * 22, dtype=torch.uint8, device=dev),
+                                       "gguf:q5_0", (4, 64))
+    with pytest.raises(olamd.Unsupported):  # K % 64 != 0
+        olamd.dequantize_packed_matmul(a[:1, :32], torch.zeros(4 * 34, dtype=torch.uint8, device=dev),
+                                       "gguf:q8_0", (4, 32))
