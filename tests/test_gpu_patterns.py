@@ -1,0 +1,36 @@
+"""The rewritten DequantizeLinear -> [Cast] -> MatMul node on the GPU
+against the unfused chain (oracle), with the float path's tolerance."""
+import importlib
+
+import numpy as np
+import pytest
+
+from test_gpu_float import T, _chain_ref, assert_close, bits_tensor, dev, tensor_bits  # noqa: F401 (dev: fixture)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_rewritten_graph_runs_fused_kernel(olamd, oracle, dev, dt):
+    pt = importlib.import_module("onnx_light_amd.patterns")
+    M, K, N = 4, 512, 384
+    rng = np.random.default_rng(17 if dt == "f16" else 18)
+    a = oracle.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32)) if dt == "f16" else \
+        oracle.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    s16 = dt == "f16"
+    sc = rng.uniform(0.002, 0.02, (N,)).astype(np.float16 if s16 else np.float32)
+    zp = rng.integers(0, 20, (N,)).astype(np.int8)
+    Nd = pt.Node
+    nodes = [Nd("DequantizeLinear", ["W", "s", "z"], ["Wd"], attrs={"axis": 1})]
+    if not s16:
+        nodes.append(Nd("Cast", ["Wd"], ["Wc"], attrs={"to": 16}))
+    nodes.append(Nd("MatMul", ["A", nodes[-1].outputs[0]], ["Y"]))
+    g = pt.Graph(nodes, {"W", "s", "z"}, ["A"], ["Y"])
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizeLinearMatMulGpu")]) == 1
+    (node,) = g.nodes
+    feeds = {"A": bits_tensor(a, dt, dev), "W": T(x, dev), "s": T(sc, dev), "z": T(zp, dev)}
+    kernel = olamd.KERNELS[f"{node.domain}:{node.op_type}"]()
+    y = kernel(*[feeds[i] for i in node.inputs], **node.attrs)
+    ref, mag = _chain_ref(oracle, a, x, oracle.INT8, K, N, sc, s16, zp, 1, "bf16", dt)
+    assert_close(tensor_bits(y), ref, mag, dt, oracle, f"pattern {dt}")
