@@ -255,6 +255,28 @@ int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_am
                                        const onnxl_amd_tensor *x_zero_point, int64_t axis,
                                        int32_t cast_to, onnxl_amd_tensor *y, void *stream);
 
+/* onnxl_amd_dequantize_linear_matmul with no allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, validation and results as
+ * onnxl_amd_dequantize_linear_matmul (same kernels), but:
+ * - every payload (A, x, x_scale, x_zero_point, y) must be device memory
+ *   (no host staging; a host payload is an INVALID_ARGUMENT);
+ * - its scratch is a fixed array of 8 MiB per device, held until the process
+ *   ends: 64 KiB of counters (16384, one per 256-column strip of the ONNX-
+ *   layout int4 GEMV) and 8128 KiB for split-K partial sums or a dequantised
+ *   weight.  A call that needs more returns ONNXL_AMD_UNSUPPORTED, naming the
+ *   sizes (the allocating entry point then serves it);
+ * - it calls no hipMalloc / hipFree.
+ * All calls on one device share that array: calls that overlap on one device
+ * (different streams, or different threads without ordering) race.  The
+ * counters are cleared once per device by onnxl_amd_init and every completed
+ * call leaves them at zero. */
+int onnxl_amd_dequantize_linear_matmul_noalloc(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
+                                               const onnxl_amd_tensor *x_scale,
+                                               const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                               int32_t cast_to, onnxl_amd_tensor *y, void *stream);
+
 /* Session-time preparation of a constant INT4 / UINT4 weight x [K, N] (ONNX
  * layout) for onnxl_amd_dequantize_linear_matmul: writes it into `prepared`
  * (device memory of onnxl_amd_prepare_weight_size bytes, 16-byte aligned,

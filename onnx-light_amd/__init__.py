@@ -87,6 +87,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
+                                                                 ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_quantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, ctypes.c_int32, TP,
                                                 ctypes.c_void_p]
         L.onnxl_amd_dynamic_quantize_linear.argtypes = [TP, TP, TP, TP, ctypes.c_void_p]
@@ -374,6 +376,20 @@ def dequantize_linear_matmul(a, x, x_scale, x_zero_point=None, axis: int = 1, ca
     _check(lib().onnxl_amd_dequantize_linear_matmul(describe(a), describe(x, x_dtype, shape),
                                                     describe(x_scale), dz, axis, cast_to,
                                                     describe(out), _stream_of(a, x, out)))
+    return out
+
+
+def dequantize_linear_matmul_noalloc(a, x, x_scale, x_zero_point=None, axis: int = 1, cast_to: int = 0,
+                                     x_dtype=None, x_shape=None, out=None):
+    """dequantize_linear_matmul through the no-allocation entry point: device
+    tensors only, scratch from the library's fixed per-device array."""
+    shape = _shape_of(x, x_shape)
+    if out is None:
+        out = _empty(matmul_shape(_shape_of(a), shape), a.dtype, _device_of(a, x))
+    dz = _describe_zp(x_zero_point, x_dtype, x_scale)
+    _check(lib().onnxl_amd_dequantize_linear_matmul_noalloc(describe(a), describe(x, x_dtype, shape),
+                                                            describe(x_scale), dz, axis, cast_to,
+                                                            describe(out), _stream_of(a, x, out)))
     return out
 
 

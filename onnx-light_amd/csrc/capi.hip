@@ -15,6 +15,16 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Scratch of onnxl_amd_dequantize_linear_matmul_noalloc: a fixed array that
+// every GPU the library runs on holds for the life of the process (each GPU
+// its own copy, at its own address).  The first 64 KiB hold the split-K
+// counters of the int4 GEMV (zeroed once per device at set-up; every GEMV
+// launch returns the counters it used to zero), the rest holds partial sums
+// or a dequantised weight.  Host code never passes `scratch` itself to a
+// kernel: it is a host-side stand-in; the device address comes from
+// hipGetSymbolAddress (onnxl_amd::NoAllocScratch).
+static __device__ __align__(256) unsigned char scratch[8u << 20];
+
 namespace onnxl_amd {
 
 // ---------------------------------------------------------------------------
@@ -25,6 +35,33 @@ DeviceContext g_ctx;
 std::atomic<bool> g_init{false};
 std::mutex g_mu;  // serialises entry points: one workspace per device
 thread_local std::string g_last_error;
+
+constexpr size_t kNoAllocBytes = sizeof(scratch);
+constexpr size_t kNoAllocCounterBytes = size_t(64) << 10;
+constexpr size_t kNoAllocDataBytes = kNoAllocBytes - kNoAllocCounterBytes;
+constexpr int kMaxDevices = 64;
+void *g_noalloc_ptr[kMaxDevices] = {};  // device address of `scratch` per device (under g_mu)
+
+__global__ __launch_bounds__(256) void ZeroWordsKernel(unsigned *p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Once per device, with that device current: looks up the device address of
+// `scratch` and clears its counters (with a fill kernel, then waits).
+void SetUpNoAllocScratch(int device) {
+  OLA_ENFORCE(device >= 0 && device < kMaxDevices, "onnxl_amd_init: device ", device, " above ", kMaxDevices - 1);
+  if (g_noalloc_ptr[device] != nullptr) return;
+  void *ptr = nullptr;
+  OLA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  OLA_ENFORCE(ptr != nullptr, "onnxl_amd_init: no device address for the no-allocation scratch");
+  const size_t words = kNoAllocCounterBytes / sizeof(unsigned);
+  hipLaunchKernelGGL(ZeroWordsKernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, nullptr,
+                     static_cast<unsigned *>(ptr), words);
+  OLA_HIP(hipGetLastError());
+  OLA_HIP(hipDeviceSynchronize());
+  g_noalloc_ptr[device] = ptr;
+}
 }  // namespace
 
 bool Initialized() { return g_init.load(); }
@@ -33,6 +70,16 @@ DeviceContext &Ctx() {
   if (!g_init.load()) throw NotInitialized();
   return g_ctx;
 }
+
+namespace {
+// The current device's address of `scratch` (set up by onnxl_amd_init).
+void *NoAllocScratch() {
+  const int dev = Ctx().device;
+  void *ptr = dev >= 0 && dev < kMaxDevices ? g_noalloc_ptr[dev] : nullptr;
+  if (ptr == nullptr) throw DeviceError("internal: the no-allocation scratch was not set up for this device");
+  return ptr;
+}
+}  // namespace
 
 void *Workspace::Get(size_t bytes) {
   if (bytes <= cap_ && ptr_ != nullptr) return ptr_;
@@ -1164,9 +1211,11 @@ int MatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tenso
 
 constexpr const char *kDqmName = "DequantizeLinearMatMul";
 
-int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
-             const onnxl_amd_tensor *x_zp, int64_t axis, int32_t cast_to, onnxl_amd_tensor *y,
-             hipStream_t stream) {
+// Validation of the fused node (the DequantizeLinear, Cast and MatMul nodes'
+// own checks) and its launch parameters; payload pointers are left unset.
+DqMatMulParams PlanDqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
+                            const onnxl_amd_tensor *x_scale, const onnxl_amd_tensor *x_zp, int64_t axis,
+                            int32_t cast_to, onnxl_amd_tensor *y) {
   OLA_ENFORCE(!Absent(a) && !Absent(x) && !Absent(x_scale) && y, kDqmName,
               ": A, x, x_scale and the output are required.");
   CheckDescriptor(a, "A");
@@ -1245,8 +1294,16 @@ int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_a
   p.deq_round_f16 = dq_out == kFloat16;
   p.cast_round = cast_to == kBfloat16 ? 16 : (cast_to == kFloat16 ? 10 : 0);
   p.w_tiled = x->layout == ONNXL_AMD_LAYOUT_TILED_INT4;
-  const size_t scratch = DqMatMulScratchBytes(p);
-  Staging st(stream, scratch, {a, x, x_scale, has_zp ? x_zp : nullptr}, {y});
+  return p;
+}
+
+int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+             const onnxl_amd_tensor *x_zp, int64_t axis, int32_t cast_to, onnxl_amd_tensor *y,
+             hipStream_t stream) {
+  DqMatMulParams p = PlanDqMatMul(a, x, x_scale, x_zp, axis, cast_to, y);
+  const bool has_zp = !Absent(x_zp);
+  const size_t scratch_bytes = DqMatMulScratchBytes(p);
+  Staging st(stream, scratch_bytes, {a, x, x_scale, has_zp ? x_zp : nullptr}, {y});
   p.A = st.In(a);
   p.W = static_cast<const uint8_t *>(st.In(x));
   p.scale = st.In(x_scale);
@@ -1254,9 +1311,37 @@ int DqMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_a
   p.Y = st.Out(y);
   const size_t nc = DqMatMulCounters(p);
   unsigned *counters = nc ? Ctx().ws.Counters(nc) : nullptr;
-  if (!LaunchDqMatMul(p, st.Extra(), scratch, counters, nc, stream))
+  if (!LaunchDqMatMul(p, st.Extra(), scratch_bytes, counters, nc, stream))
     throw Unsupported(Cat(kDqmName, ": no GPU kernel for this shape / dtype combination"));
   st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// The same node with no allocation: every payload on the device, scratch and
+// counters taken from the device's fixed array (NoAllocScratch).
+int DqMatMulNoAlloc(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                    const onnxl_amd_tensor *x_zp, int64_t axis, int32_t cast_to, onnxl_amd_tensor *y,
+                    hipStream_t stream) {
+  DqMatMulParams p = PlanDqMatMul(a, x, x_scale, x_zp, axis, cast_to, y);
+  const bool has_zp = !Absent(x_zp);
+  for (const onnxl_amd_tensor *t : {a, x, x_scale, has_zp ? x_zp : nullptr, (const onnxl_amd_tensor *)y})
+    OLA_ENFORCE(t == nullptr || t->location == ONNXL_AMD_DEVICE, kDqmName,
+                ": the no-allocation entry point takes device payloads only (no host staging).");
+  char *base = static_cast<char *>(NoAllocScratch());
+  p.A = a->data;
+  p.W = static_cast<const uint8_t *>(x->data);
+  p.scale = x_scale->data;
+  p.zp = has_zp ? static_cast<const uint8_t *>(x_zp->data) : nullptr;
+  p.Y = y->data;
+  const size_t need = DqMatMulScratchBytes(p), nc = DqMatMulCounters(p);
+  if (need > kNoAllocDataBytes || nc * sizeof(unsigned) > kNoAllocCounterBytes)
+    throw Unsupported(Cat(kDqmName, ": this call needs ", need, " bytes of scratch and ", nc,
+                          " counters; the no-allocation entry point holds ", kNoAllocDataBytes, " bytes and ",
+                          kNoAllocCounterBytes / sizeof(unsigned), " counters (use the allocating entry point)"));
+  if (!LaunchDqMatMul(p, base + kNoAllocCounterBytes, kNoAllocDataBytes, reinterpret_cast<unsigned *>(base),
+                      kNoAllocCounterBytes / sizeof(unsigned), stream))
+    throw Unsupported(Cat(kDqmName, ": no GPU kernel for this shape / dtype combination"));
+  OLA_HIP(hipGetLastError());
   return ONNXL_AMD_OK;
 }
 
@@ -1305,6 +1390,7 @@ int onnxl_amd_init(int device_ordinal) {
       throw Unsupported(Cat("onnxl_amd_init: device is ", arch, ", kernels are built for gfx950"));
     if (g_init.load() && g_ctx.device != device_ordinal) g_ctx.ws.Release();
     g_ctx.device = device_ordinal;
+    SetUpNoAllocScratch(device_ordinal);
     g_ctx.num_cus = prop.multiProcessorCount;
     g_init.store(true);
     return ONNXL_AMD_OK;
@@ -1467,6 +1553,15 @@ int onnxl_amd_dequantize_linear_matmul(const onnxl_amd_tensor *a, const onnxl_am
                                        int32_t cast_to, onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return DqMatMul(a, x, x_scale, x_zero_point, axis, cast_to, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_linear_matmul_noalloc(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
+                                               const onnxl_amd_tensor *x_scale,
+                                               const onnxl_amd_tensor *x_zero_point, int64_t axis,
+                                               int32_t cast_to, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DqMatMulNoAlloc(a, x, x_scale, x_zero_point, axis, cast_to, y, static_cast<hipStream_t>(stream));
   });
 }
 
