@@ -1139,6 +1139,7 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
   OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
   OLA_ENFORCE(x->dims[0] == N * (K / 32) * (q8 ? 34 : 18) && x->size_bytes == x->dims[0],
               "DequantizePacked: packed input length must match exactly.");
+  if (M == 0 || N == 0) return ONNXL_AMD_OK;  // empty [M, N] result, nothing to launch
   Staging st(stream, 0, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
   if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");  // q8_0 alike

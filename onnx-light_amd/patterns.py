@@ -21,6 +21,21 @@ becomes one node ``ai.rt.amd:DequantizeLinearMatMul(A, W, s[, zp])`` with
 attributes ``axis`` and ``cast_to`` (0 when there is no Cast), computed by
 ``dequantize_linear_matmul``.  The intermediate tensors must have no other
 consumer and must not be graph outputs.
+
+The rewrite only fires where the fused kernel accepts the node, so a graph
+that runs unfused never becomes one that raises.  That needs the element type
+and shape of W, s and zp (``Graph.value_info``, as an ONNX model's
+initializers carry them); a chain without them is left alone.  The checks are
+those of the fused entry point (DequantizeLinear's own, kq/kernel_
+dequantizelinear.cc:522-565, then the fused kernel's limits): W is a 2-D
+INT4 / UINT4 / INT8 / UINT8 / FLOAT8E4M3FN tensor; s is FLOAT or FLOAT16 and
+either a scalar, 1-D along axis 1 (per output column) or 2-D blocked along
+axis 0 (K); zp matches W's type and s's shape; the MatMul runs in FLOAT16 or
+BFLOAT16 (a FLOAT DequantizeLinear needs the Cast, a FLOAT16 one must not
+have one).  FLOAT8E4M3FN weights with a FLOAT per-tensor / per-column scale,
+no zero point and a Cast to BFLOAT16 take the matrix-core path that scales
+the fp32 sums instead of rounding each scaled weight to bfloat16; the pattern
+rewrites such chains only when built with ``fp8_scaled_sums=True``.
 """
 from __future__ import annotations
 
@@ -31,6 +46,9 @@ FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
 _ONNX_DOMAINS = ("", "ai.onnx")
 _CAST_TARGETS = (10, 16)  # FLOAT16, BFLOAT16: the types the fused kernel rounds to
+FLOAT, UINT8, INT8, FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 1, 2, 3, 10, 16, 17, 21, 22
+_WEIGHT_TYPES = (INT4, UINT4, INT8, UINT8, FLOAT8E4M3FN)
+_SCALE_TYPES = (FLOAT, FLOAT16)
 
 
 @dataclasses.dataclass
@@ -49,6 +67,8 @@ class Graph:
     initializers: set = dataclasses.field(default_factory=set)
     inputs: List[str] = dataclasses.field(default_factory=list)
     outputs: List[str] = dataclasses.field(default_factory=list)
+    # name -> (ONNX element type, shape) for the tensors whose types are known
+    value_info: Dict[str, tuple] = dataclasses.field(default_factory=dict)
 
     def producer(self, name: str) -> Optional[Node]:
         for n in self.nodes:
@@ -101,9 +121,62 @@ class DequantizeLinearMatMulPattern(PatternOptimization):
     def fast_op_type(self) -> set:
         return {"MatMul"}
 
-    def _single_use(self, graph: Graph, name: str, user: Node) -> bool:
-        users = graph.consumers(name)
-        return len(users) == 1 and users[0] is user and name not in graph.outputs
+    def __init__(self, fp8_scaled_sums: bool = False):
+        self.fp8_scaled_sums = fp8_scaled_sums
+
+    @staticmethod
+    def _single_use(graph: Graph, name: str, user: Node) -> bool:
+        """name feeds exactly one input slot in the graph, an input of `user`,
+        and is not a graph output (MatMul(Wd, Wd) uses Wd twice)."""
+        slots = [n for n in graph.nodes for i in n.inputs if i == name]
+        return len(slots) == 1 and slots[0] is user and name not in graph.outputs
+
+    def _check_types(self, graph: Graph, dq: Node, cast_to: int) -> str:
+        """Why the fused kernel would refuse this chain ("" if it accepts it)."""
+        info = graph.value_info
+        names = [i for i in dq.inputs if i]
+        if any(i not in info for i in names):
+            return "type or shape of a DequantizeLinear input unknown"
+        (w_t, w_shape), (s_t, s_shape) = info[names[0]], info[names[1]]
+        zp = info[names[2]] if len(names) > 2 else None
+        w_shape, s_shape = tuple(w_shape), tuple(s_shape)
+        if w_t not in _WEIGHT_TYPES:
+            return f"weight type {w_t} has no fused kernel"
+        if len(w_shape) != 2:
+            return "weight is not 2-D"
+        if s_t not in _SCALE_TYPES:
+            return "scale is not FLOAT or FLOAT16"
+        if zp is not None and (zp[0] != w_t or tuple(zp[1]) != s_shape):
+            return "zero point type or shape does not match"
+        axis = int(dq.attrs.get("axis", 1))
+        count = 1
+        for d in s_shape:
+            count *= d
+        per_tensor = count == 1
+        if not per_tensor:
+            if not 0 <= axis < 2:
+                return "axis out of range"
+            if len(s_shape) == 2:
+                if any(s_shape[d] <= 0 or w_shape[d] % s_shape[d] or (d != axis and s_shape[d] != w_shape[d])
+                       for d in range(2)):
+                    return "blocked scale does not fit the weight"
+                if axis != 0:
+                    return "scales blocked along N"
+            elif len(s_shape) == 1:
+                if count != w_shape[axis]:
+                    return "scale size differs from the axis dimension"
+                if axis != 1:
+                    return "per-row (axis 0) scales"
+            else:
+                return "scale rank above 2"
+        if cast_to and s_t != FLOAT:
+            return "Cast of a FLOAT16 DequantizeLinear output"
+        if (cast_to or s_t) not in (FLOAT16, BFLOAT16):
+            return "MatMul would run in FLOAT"
+        if (w_t == FLOAT8E4M3FN and cast_to == BFLOAT16 and s_t == FLOAT and zp is None
+                and (per_tensor or len(s_shape) == 1) and not self.fp8_scaled_sums):
+            return "FLOAT8E4M3FN -> BFLOAT16 chain would scale the sums (fp8_scaled_sums=True allows it)"
+        return ""
 
     def match(self, graph: Graph, candidate: Node) -> MatchResult:
         if not _is_onnx(candidate, "MatMul") or len(candidate.inputs) != 2:
@@ -125,6 +198,9 @@ class DequantizeLinearMatMulPattern(PatternOptimization):
             return self.no_match("DequantizeLinear inputs are not all initializers")
         if not self._single_use(graph, prod.outputs[0], cast if cast is not None else candidate):
             return self.no_match("DequantizeLinear output has another consumer")
+        why = self._check_types(graph, prod, int(cast.attrs["to"]) if cast is not None else 0)
+        if why:
+            return self.no_match(why)
         return MatchResult([prod] + ([cast] if cast is not None else []) + [candidate])
 
     def apply(self, graph: Graph, nodes: Sequence[Node]) -> List[Node]:

@@ -359,6 +359,28 @@ def test_config4_full_size(olamd, oracle, dev):
                                                          oracle.FLOAT, None, 1))
     mag = np.abs(decode(x["a_bits"][rows], "bf16", oracle)) @ np.abs(decode(w, "bf16", oracle))
     assert_close(got, fx["c4_y_bits"], mag, "bf16", oracle, "config 4")
+    _fp8_chain_closed_form(y, x["a_bits"], x["w"], x["scale"], dev, "config 4")
+
+
+def _fp8_chain_closed_form(y, a_bits, w_bits, scale, dev, what):
+    """Every output element against a float64 closed form of the chain,
+    computed on the device: W = bf16(fp32(decode(x)) * scale[n]), the rounding
+    of DequantizeLinear(FLOAT) -> Cast(BFLOAT16), then sum_k a_mk * W_kn in
+    float64, under the stated tolerance 1e-2 * |ref| + 2^-8 * sum_k |a_mk W_kn|.
+    It covers every tile of the launch; the oracle rows above pin the weight
+    decode and the chain's rounding bit for bit."""
+    w = T(w_bits, dev).view(torch.float8_e4m3fn).to(torch.float32) * T(scale, dev)
+    w64 = w.to(torch.bfloat16).to(torch.float64)
+    del w
+    a64 = bits_tensor(a_bits, "bf16", dev).to(torch.float64)
+    ref = a64 @ w64
+    mag = a64.abs() @ w64.abs()
+    del a64, w64
+    err = (y.to(torch.float64) - ref).abs()
+    bad = ~(err <= 1e-2 * ref.abs() + 2.0 ** -8 * mag)
+    n_bad = int(bad.sum())
+    assert n_bad == 0, f"{what}: {n_bad} of {bad.numel()} outside tolerance (max err {float(err.max()):.3g})"
+    assert bool(torch.isfinite(y.float()).all())
 
 
 def test_fp8_gemm_column_split(olamd, oracle, dev):
@@ -376,3 +398,4 @@ def test_fp8_gemm_column_split(olamd, oracle, dev):
     rows = np.array([0, 1, 255, 256, 2047, 3840, 4095])
     ref, mag = _chain_ref(oracle, a, x, oracle.FLOAT8E4M3FN, K, N, sc, False, None, 1, "bf16", "bf16", rows=rows)
     assert_close(tensor_bits(y)[rows], ref, mag, "bf16", oracle, "fp8 column split")
+    _fp8_chain_closed_form(y, a, x, sc, dev, "fp8 column split")

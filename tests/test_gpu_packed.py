@@ -120,3 +120,16 @@ def test_packed_gemv_unsupported(olamd, dev):
     with pytest.raises(olamd.Unsupported):  # K % 64 != 0
         olamd.dequantize_packed_matmul(a[:1, :32], torch.zeros(4 * 34, dtype=torch.uint8, device=dev),
                                        "gguf:q8_0", (4, 32))
+
+
+@pytest.mark.parametrize("fmt,bpb", [("gguf:q4_0", 18), ("gguf:q8_0", 34)])
+def test_packed_gemv_empty(olamd, dev, fmt, bpb):
+    """MatMul semantics: a [0, K] activation gives an empty [0, N] result, and
+    N = 0 an empty [M, 0] one (no launch)."""
+    y = olamd.dequantize_packed_matmul(torch.zeros((0, 64), dtype=torch.float16, device=dev),
+                                       torch.zeros(4 * 2 * bpb, dtype=torch.uint8, device=dev), fmt, (4, 64))
+    assert tuple(y.shape) == (0, 4)
+    y = olamd.dequantize_packed_matmul(torch.zeros((3, 64), dtype=torch.float16, device=dev),
+                                       torch.zeros(0, dtype=torch.uint8, device=dev), fmt, (0, 64))
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (3, 0)

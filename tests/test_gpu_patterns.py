@@ -26,7 +26,8 @@ def test_rewritten_graph_runs_fused_kernel(olamd, oracle, dev, dt):
     if not s16:
         nodes.append(Nd("Cast", ["Wd"], ["Wc"], attrs={"to": 16}))
     nodes.append(Nd("MatMul", ["A", nodes[-1].outputs[0]], ["Y"]))
-    g = pt.Graph(nodes, {"W", "s", "z"}, ["A"], ["Y"])
+    g = pt.Graph(nodes, {"W", "s", "z"}, ["A"], ["Y"],
+                 {"W": (pt.INT8, (K, N)), "s": (pt.FLOAT16 if s16 else pt.FLOAT, (N,)), "z": (pt.INT8, (N,))})
     assert pt.optimize(g, [pt.create_registered_pattern("DequantizeLinearMatMulGpu")]) == 1
     (node,) = g.nodes
     feeds = {"A": bits_tensor(a, dt, dev), "W": T(x, dev), "s": T(sc, dev), "z": T(zp, dev)}

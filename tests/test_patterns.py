@@ -9,7 +9,8 @@ def pt(olamd):
     return importlib.import_module("onnx_light_amd.patterns")
 
 
-def _graph(pt, cast_to=None, zp=True, extra_use=False, dq_is_output=False, w_const=True, axis=1):
+def _graph(pt, cast_to=None, zp=True, extra_use=False, dq_is_output=False, w_const=True, axis=1,
+           w_type=None, s_type=None, w_shape=(64, 32), s_shape=None):
     N = pt.Node
     nodes = [N("DequantizeLinear", ["W", "s", "z" if zp else ""], ["Wd"], attrs={"axis": axis}, name="dq")]
     b = "Wd"
@@ -21,7 +22,13 @@ def _graph(pt, cast_to=None, zp=True, extra_use=False, dq_is_output=False, w_con
         nodes.append(N("Relu", ["Wd"], ["R"], name="relu"))
     init = {"s", "z"} | ({"W"} if w_const else set())
     outs = ["Y"] + (["Wd"] if dq_is_output else []) + (["R"] if extra_use else [])
-    return pt.Graph(nodes, init, ["A"] + ([] if w_const else ["W"]), outs)
+    w_type = pt.INT8 if w_type is None else w_type
+    # a FLOAT16 scale makes a FLOAT16 MatMul; a FLOAT one needs the Cast
+    s_type = (pt.FLOAT16 if cast_to is None else pt.FLOAT) if s_type is None else s_type
+    if s_shape is None:
+        s_shape = (w_shape[0] // 32, w_shape[1]) if axis == 0 else (w_shape[1],)
+    info = {"W": (w_type, w_shape), "s": (s_type, s_shape), "z": (w_type, s_shape)}
+    return pt.Graph(nodes, init, ["A"] + ([] if w_const else ["W"]), outs, info)
 
 
 def _pattern(pt):
@@ -57,6 +64,61 @@ def test_no_match(pt, kw, reason):
     assert [n.op_type for n in g.nodes] == before
 
 
+@pytest.mark.parametrize("kw,reason", [
+    # a FLOAT DequantizeLinear into a FLOAT MatMul: the fused kernel needs 16-bit A
+    (dict(s_type=1), "MatMul would run in FLOAT"),
+    # an FLOAT16 DequantizeLinear output followed by a Cast
+    (dict(cast_to=16, s_type=10), "Cast of a FLOAT16"),
+    (dict(w_type=5), "no fused kernel"),                      # INT16 weight
+    (dict(w_type=4), "no fused kernel"),                      # UINT16 weight
+    (dict(w_type=6), "no fused kernel"),                      # INT32 weight
+    (dict(axis=0, s_shape=(64,)), "per-row (axis 0)"),        # 1-D scale along K
+    (dict(axis=1, s_shape=(64, 2)), "blocked along N"),
+    (dict(axis=0, s_shape=(3, 32)), "does not fit"),          # 64 rows in blocks of 3 scales
+    (dict(axis=1, s_shape=(31,)), "differs from the axis"),
+    (dict(axis=2, s_shape=(32,)), "axis out of range"),
+    (dict(w_shape=(2, 64, 32), s_shape=(32,)), "not 2-D"),
+    (dict(s_type=11), "not FLOAT or FLOAT16"),                # DOUBLE scale
+    (dict(w_type=17, cast_to=16, zp=False), "scale the sums"),  # fp8 scaled-sum path, not opted in
+])
+def test_no_match_types(pt, kw, reason):
+    g = _graph(pt, **kw)
+    mm = next(n for n in g.nodes if n.op_type == "MatMul")
+    m = _pattern(pt).match(g, mm)
+    assert not m and reason in m.reason, m.reason
+    assert pt.optimize(g, [_pattern(pt)]) == 0
+
+
+def test_zero_point_mismatch_and_unknown_types(pt):
+    g = _graph(pt, zp=True)
+    g.value_info["z"] = (pt.UINT8, g.value_info["s"][1])
+    assert "zero point" in _pattern(pt).match(g, g.nodes[-1]).reason
+    g = _graph(pt, zp=True)
+    del g.value_info["s"]
+    assert "unknown" in _pattern(pt).match(g, g.nodes[-1]).reason
+
+
+def test_fp8_scaled_sums_opt_in(pt):
+    g = _graph(pt, w_type=17, cast_to=16, zp=False)
+    assert pt.optimize(g, [pt.DequantizeLinearMatMulPattern(fp8_scaled_sums=True)]) == 1
+    # with a zero point or a FLOAT16 target the chain keeps the exact rounding and is fused by default
+    g = _graph(pt, w_type=17, cast_to=16, zp=True)
+    assert pt.optimize(g, [_pattern(pt)]) == 1
+    g = _graph(pt, w_type=17, cast_to=10, zp=False)
+    assert pt.optimize(g, [_pattern(pt)]) == 1
+
+
+def test_same_tensor_twice_is_two_uses(pt):
+    """MatMul(Wd, Wd): the DequantizeLinear output feeds two input slots, so
+    removing the DequantizeLinear would leave A dangling."""
+    N = pt.Node
+    g = pt.Graph([N("DequantizeLinear", ["W", "s"], ["Wd"], attrs={"axis": 1}), N("MatMul", ["Wd", "Wd"], ["Y"])],
+                 {"W", "s"}, [], ["Y"], {"W": (pt.INT8, (32, 32)), "s": (pt.FLOAT16, (32,))})
+    m = _pattern(pt).match(g, g.nodes[1])
+    assert not m and "another consumer" in m.reason
+    assert pt.optimize(g, [_pattern(pt)]) == 0
+
+
 def test_first_input_and_other_attrs_do_not_match(pt):
     N = pt.Node
     g = pt.Graph([N("DequantizeLinear", ["W", "s"], ["Wd"]), N("MatMul", ["Wd", "B"], ["Y"])], {"W", "s"},
@@ -76,7 +138,9 @@ def test_two_chains_and_order(pt):
                   N("DequantizeLinear", ["W1", "s1"], ["D1"]), N("MatMul", ["A", "D1"], ["H"]),
                   N("DequantizeLinear", ["W2", "s2"], ["D2"]), N("Cast", ["D2"], ["C2"], attrs={"to": 16}),
                   N("MatMul", ["H", "C2"], ["Y"])],
-                 {"W1", "s1", "W2", "s2"}, ["X"], ["Y"])
+                 {"W1", "s1", "W2", "s2"}, ["X"], ["Y"],
+                 {"W1": (pt.INT4, (64, 32)), "s1": (pt.FLOAT16, (32,)), "W2": (pt.UINT8, (32, 16)),
+                  "s2": (pt.FLOAT, ())})
     assert pt.optimize(g, [_pattern(pt)]) == 2
     assert [n.op_type for n in g.nodes] == ["Relu", pt.FUSED_OP, pt.FUSED_OP]
     assert g.nodes[1].outputs == ["H"] and g.nodes[2].inputs[0] == "H" and g.nodes[2].attrs["cast_to"] == 16
