@@ -16,7 +16,8 @@ reported as `host_path_ms_per_step`.  `cpu_baseline` times the serial CPU
 oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
+                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
@@ -24,7 +25,17 @@ integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
 GGUF q4_0 weight decode (`pk`) and the fused q4_0 / q8_0 GEMVs (`pkgemv`,
 `pkgemv8`) are timed too and reported under `extra` unless --no-extra is
-given.
+given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
+25,604,096 bytes with the same replica rotation (libonnxl_amd_bench.so): the
+rate a kernel that only reads those bytes reaches, beside which the GEMV's
+own rate is read.
+
+HBM-bound lines rotate buffer replicas totalling more than 512 MB, so each
+launch misses the 256 MB Infinity Cache.  `cpu_baseline` (configurations 2,
+3, 4 and 5) times the CPU oracle as the reference runs: MatMulInteger,
+QLinearMatMul and DequantizeLinear on one core, MatMul and Cast on the
+physical cores of the process's CPU set; it reports `nproc` and the physical
+core count.
 """
 from __future__ import annotations
 
@@ -132,7 +143,9 @@ def make_c4(olamd, dev):
     import importlib
     import torch
     syn = importlib.import_module("onnx_light_amd.synth")
-    x = syn.config_inputs(4)
+    xt = syn.config4_torch(dev)  # drawn on the GPU, equal to config_inputs(4)
+    x = {"a_bits": xt["a"].view(torch.int16).cpu().numpy().view(np.uint16), "w": xt["w"].cpu().numpy(),
+         "scale": xt["scale"].cpu().numpy(), "axis": 1}
     w = Workload()
     w.name = ("C4 fp8 per-axis prefill bf16[4096,4096] x Cast(bf16, DequantizeLinear(fp8e4m3fn"
               "[4096,14336], fp32 per-column scale)) -> bf16[4096,14336]")
@@ -140,9 +153,7 @@ def make_c4(olamd, dev):
     M, K, N = 4096, 4096, 14336
     w.work = 2.0 * M * N * K
     w.nbytes = M * K * 2 + K * N + N * 4 + M * N * 2
-    a = _t(x["a_bits"], dev).view(torch.bfloat16)
-    wq = _t(x["w"], dev)
-    sc = _t(x["scale"], dev)
+    a, wq, sc = xt["a"], xt["w"], xt["scale"]
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     w.calls = [olamd.prepare("dequantize_linear_matmul", a, wq, sc, None, 1, olamd.BFLOAT16, y,
                              descs={1: olamd.describe(wq, olamd.FLOAT8E4M3FN)})]
@@ -297,6 +308,157 @@ def make_dql(olamd, dev, replicas):
     return w
 
 
+class _StreamCall:
+    """One streaming read of `nbytes` at `ptr` (libonnxl_amd_bench.so), with
+    the `on(stream)` interface of a prepared call."""
+
+    def __init__(self, lib, ptr, nbytes, sink, stream=None):
+        self.lib, self.ptr, self.nbytes, self.sink, self.stream = lib, ptr, nbytes, sink, stream
+
+    def __call__(self):
+        rc = self.lib.onnxl_amd_bench_stream_read(ctypes.c_void_p(self.ptr), ctypes.c_int64(self.nbytes),
+                                                  ctypes.c_void_p(self.sink), self.stream)
+        if rc:
+            raise RuntimeError(f"stream read failed ({rc})")
+
+    def on(self, stream):
+        handle = getattr(stream, "cuda_stream", stream)
+        return _StreamCall(self.lib, self.ptr, self.nbytes, self.sink, ctypes.c_void_p(handle))
+
+
+def make_stream(olamd, dev, replicas, nbytes, key, name):
+    """A plain read of `nbytes` per launch over `replicas` buffers: the
+    streaming ceiling for a bandwidth-bound kernel of that byte count."""
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "onnx-light_amd", "libonnxl_amd_bench.so"))
+    lib.onnxl_amd_bench_stream_blocks.argtypes = [ctypes.c_int64]
+    lib.onnxl_amd_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    w = Workload()
+    w.name = name
+    w.key, w.unit, w.dtype, w.bound = key, "GB/s", "u8 (read only)", "hbm"
+    w.nbytes = nbytes
+    w.work = float(nbytes)
+    sink = torch.empty(lib.onnxl_amd_bench_stream_blocks(nbytes) * 256, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    w.bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev, generator=g) for _ in range(replicas)]
+    w.sink = sink
+    w.calls = [_StreamCall(lib, b.data_ptr(), nbytes, sink.data_ptr(), olamd._stream_of(b)) for b in w.bufs]
+    return w
+
+
+def replicas_for(nbytes, floor=512 << 20):
+    """Buffer replicas whose total exceeds `floor` (the MALL is 256 MB)."""
+    return max(2, floor // nbytes + 1)
+
+
+def cpu_topology():
+    """(logical CPUs in this process's CPU set, physical cores among them)."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f1, open(base + "core_id") as f2:
+                cores.add((f1.read().strip(), f2.read().strip()))
+        except OSError:
+            cores.add(("cpu", str(c)))
+    return len(cpus), len(cores)
+
+
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    orc.lib()
+    return orc
+
+
+def _median_time(fn, runs=3, budget_s=20.0):
+    fn()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < runs and (not times or time.perf_counter() - t_start < budget_s):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), len(times)
+
+
+def _threaded(fn, n, nthreads):
+    """fn(lo, hi) over [0, n) split into nthreads slices (the oracle's C code
+    releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    step = (n + nthreads - 1) // nthreads
+    with ThreadPoolExecutor(nthreads) as ex:
+        list(ex.map(lambda lo: fn(lo, min(n, lo + step)), range(0, n, step)))
+
+
+def cpu_baseline_c3(x):
+    """The reference chain on the host: DequantizeLinear (serial, INT4 ->
+    FLOAT16) then the fp16 MatMul (promote/demote serial, the product on the
+    physical cores), the whole job, median of 3."""
+    orc = _oracle()
+    nproc, phys = cpu_topology()
+    K, N = x["w_shape"]
+    sbits = x["scale"].view(np.uint16)
+    a = x["a"].view(np.uint16)
+
+    def job():
+        w = orc.dequantize_linear(x["w"], orc.INT4, (K, N), sbits, orc.FLOAT16, None, 0)
+        orc.matmul_half(a, w, orc.FLOAT16, nthreads=phys)
+
+    t, runs = _median_time(job)
+    nbytes = K * N // 2 + (K // 32) * N * 2 + 8 * K * 2 + 8 * N * 2
+    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": phys, "kind": "port",
+            "sample": f"the whole job, median of {runs}: serial oracle DequantizeLinear (int4 -> fp16) then "
+                      f"oracle fp16 MatMul on {phys} threads ({t:.3f} s per job)",
+            "nproc": nproc, "physical_cores": phys}
+
+
+def cpu_baseline_c4(x):
+    """The reference chain on the host: DequantizeLinear (serial, fp8 ->
+    FLOAT), Cast FLOAT -> BFLOAT16 (parallel), bf16 MatMul (promote serial,
+    product on the physical cores).  The MatMul is timed on two row samples
+    and fitted as fixed + per-row cost, then extrapolated to the 4096 rows."""
+    orc = _oracle()
+    nproc, phys = cpu_topology()
+    K, N = x["w"].shape
+    a = x["a_bits"]
+    t_dq, _ = _median_time(lambda: orc.dequantize_linear(x["w"], orc.FLOAT8E4M3FN, (K, N), x["scale"], orc.FLOAT,
+                                                         None, 1), runs=1)
+    wf = orc.dequantize_linear(x["w"], orc.FLOAT8E4M3FN, (K, N), x["scale"], orc.FLOAT, None, 1).reshape(-1)
+    wb = np.empty(wf.size, np.uint16)
+
+    def cast(lo, hi):
+        wb[lo:hi] = orc.f32_to_bf16_bits(wf[lo:hi])
+
+    t_cast, _ = _median_time(lambda: _threaded(cast, wf.size, phys), runs=1)
+    wb = wb.reshape(K, N)
+    r1, r2 = 8, 40
+    t1, _ = _median_time(lambda: orc.matmul_half(a, wb, orc.BFLOAT16, rows=(0, r1), nthreads=phys), runs=2)
+    t2, _ = _median_time(lambda: orc.matmul_half(a, wb, orc.BFLOAT16, rows=(0, r2), nthreads=phys), runs=2)
+    per_row = max(0.0, (t2 - t1) / (r2 - r1))
+    fixed = max(0.0, t1 - per_row * r1)
+    job = t_dq + t_cast + fixed + per_row * a.shape[0]
+    return {"value": round(2.0 * a.shape[0] * K * N / job / 1e12, 6), "unit": "TFLOPS", "cores": phys,
+            "kind": "port",
+            "sample": f"serial oracle DequantizeLinear ({t_dq:.2f} s) + Cast on {phys} threads ({t_cast:.2f} s) + "
+                      f"oracle bf16 MatMul on {phys} threads timed at {r1} and {r2} rows and extrapolated as "
+                      f"{fixed:.2f} s + {per_row * 1e3:.1f} ms/row to {a.shape[0]} rows ({job:.1f} s per job)",
+            "nproc": nproc, "physical_cores": phys}
+
+
+def cpu_baseline_c5(x):
+    """Serial oracle MatMulInteger (int32 accumulate, one core as the
+    reference), the whole job, median of 3."""
+    orc = _oracle()
+    nproc, phys = cpu_topology()
+    t, runs = _median_time(lambda: orc.matmul_integer(x["a"], x["b"], x["a_zp"], x["b_zp"]))
+    nbytes = 32 * 512 * 64 * 2 + 1024 + 32 * 512 * 512 * 4
+    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the whole job, median of {runs}: serial oracle MatMulInteger ({t:.3f} s per job)",
+            "nproc": nproc, "physical_cores": phys}
+
+
 def time_direct(w, steps, warmup):
     """Host path: one C-ABI call from Python per step (validation + launch),
     `steps` calls bracketed by synchronisations; ms per step by wall clock."""
@@ -352,8 +514,7 @@ def time_workload(w, steps, warmup):
 def cpu_baseline_c2(w, budget_s=20.0):
     """Serial oracle QLinearMatMul (the reference kernel restated, 1 core) on a
     row sample of configuration 2; median of repeated timed runs."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as orc
+    orc = _oracle()
     x = w.inputs
     rows = 40  # about 2.5 s per run on one core, 5 runs: 10-15 s of CPU work
     orc.qlinear_matmul(x["a"], x["a_scale"], 128, x["b"], x["b_scale"], 0, x["y_scale"], 128,
@@ -374,7 +535,7 @@ def cpu_baseline_c2(w, budget_s=20.0):
             "sample": f"{len(times)} timed runs of {rows} rows (of 2048) through the serial oracle "
                       f"QLinearMatMul (oracle/oracle.c, int64 accumulate, column-strided B), median, "
                       f"extrapolated linearly to the full 2048 rows ({full_s:.1f} s per job)",
-            "nproc": os.cpu_count()}
+            "nproc": cpu_topology()[0], "physical_cores": cpu_topology()[1]}
 
 
 def roofline(w, kernel_ms, traffic):
@@ -408,13 +569,19 @@ def value_of(w, ms):
     return w.nbytes / (ms * 1e-3) / 1e9
 
 
+WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
+             "pkgemv8")
+CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
+                 "c5": cpu_baseline_c5}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv", "pkgemv8"])
+                    choices=list(WORKLOADS))
     ap.add_argument("--no-extra", dest="extra", action="store_false",
                     help="time only --workload (default: the other configurations too, under `extra`)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -450,9 +617,13 @@ def main():
         if key == "pk":
             return make_pk(olamd, dev, args.replicas or 4)
         if key == "pkgemv":
-            return make_pkgemv(olamd, dev, args.replicas or 10)
+            return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 18))
         if key == "pkgemv8":
-            return make_pkgemv(olamd, dev, args.replicas or 10, "q8_0")
+            return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 34), "q8_0")
+        if key == "c3_stream_ceiling":
+            return make_stream(olamd, dev, args.replicas or 24, 25604096, key,
+                               "streaming read of 25,604,096 bytes per launch (configuration 3's algorithmic "
+                               "bytes), 24 replicas: the ceiling for the C3 GEMV")
         return make_c5(olamd, dev, args.replicas or 16)
 
     w = build(args.workload)
@@ -467,7 +638,7 @@ def main():
             "roofline": roofline(w, kern_mean, load_traffic(w.key))}
     if args.extra:
         extra = {}
-        for key in ("c2", "c3", "c3_onnx_layout", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv", "pkgemv8"):
+        for key in WORKLOADS:
             if key == args.workload:
                 continue
             try:
@@ -477,6 +648,8 @@ def main():
                               "ms_per_step": round(e_ms, 5), "kernel_ms_mean": round(e_mean, 5),
                               "host_path_ms_per_step": round(e_host, 5),
                               "roofline": roofline(ew, e_mean, load_traffic(key))}
+                if not args.no_cpu_baseline and key in CPU_BASELINES:
+                    extra[key]["cpu_baseline"] = CPU_BASELINES[key](ew.inputs)
                 del ew
                 torch.cuda.empty_cache()
             except olamd.Unsupported as e:
@@ -484,6 +657,8 @@ def main():
         line["extra"] = extra
     if not args.no_cpu_baseline and args.workload == "c2":
         line["cpu_baseline"] = cpu_baseline_c2(w)
+    elif not args.no_cpu_baseline and args.workload in CPU_BASELINES:
+        line["cpu_baseline"] = CPU_BASELINES[args.workload](w.inputs)
     print(json.dumps(line), flush=True)
     return 0
 

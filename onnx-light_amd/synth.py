@@ -62,6 +62,59 @@ def randn(seed: int, n: int, chunk: int = 1 << 20) -> np.ndarray:
     return out
 
 
+# ---- the same draws with torch (any device; bit-identical to the numpy path) --
+
+def _torch_u64(v: int):
+    """A 64-bit pattern as a torch int64 value (two's complement)."""
+    return v - (1 << 64) if v >= 1 << 63 else v
+
+
+def _lsr(z, k: int):
+    """Logical right shift of int64 patterns (torch shifts arithmetically)."""
+    return (z >> k) & ((1 << (64 - k)) - 1)
+
+
+def splitmix64_draws_torch(seed: int, n: int, start: int = 0, device="cpu"):
+    """splitmix64_draws as torch int64 bit patterns.  int64 products wrap
+    modulo 2^64 like the uint64 ones, and XOR / masked shifts act on the bit
+    patterns, so the draws are the same 64-bit values."""
+    import torch
+    idx = torch.arange(start + 1, start + n + 1, dtype=torch.int64, device=device)
+    z = _torch_u64(seed) + idx * _torch_u64(int(GAMMA))
+    z = (z ^ _lsr(z, 30)) * _torch_u64(int(_M1))
+    z = (z ^ _lsr(z, 27)) * _torch_u64(int(_M2))
+    return z ^ _lsr(z, 31)
+
+
+def randn_torch(seed: int, n: int, device="cpu", chunk: int = 1 << 22):
+    """randn (float64) computed with torch on `device`: the same uniforms
+    ((x >> 11) * 2^-53) summed in the same order."""
+    import torch
+    out = torch.empty(n, dtype=torch.float64, device=device)
+    for c0 in range(0, n, chunk):
+        c = min(chunk, n - c0)
+        u = (_lsr(splitmix64_draws_torch(seed, 12 * c, 12 * c0, device), 11).to(torch.float64)
+             * (1.0 / 2.0**53)).view(c, 12)
+        acc = torch.zeros(c, dtype=torch.float64, device=device)
+        for j in range(12):
+            acc = acc + u[:, j]
+        out[c0:c0 + c] = acc - 6.0
+    return out
+
+
+def config4_torch(device, scale: float = 1.0) -> dict:
+    """Configuration 4's inputs as torch tensors on `device` (the bench draws
+    them on the GPU: 700 M uniforms take half a minute in numpy): w uint8
+    fp8e4m3fn codes [4096, 14336], scale float32 [14336], a bfloat16
+    [M, 4096].  Equal to config_inputs(4) bit for bit."""
+    import torch
+    K, N, M = 4096, 14336, max(1, int(4096 * scale))
+    w = randn_torch(4000, K * N, device).to(torch.float32).to(torch.float8_e4m3fn).view(torch.uint8).view(K, N)
+    s = torch.from_numpy((0.005 + 0.045 * uniform(4001, N)).astype(np.float32)).to(device)
+    a = randn_torch(4002, M * K, device).to(torch.float32).to(torch.bfloat16).view(M, K)
+    return {"w": w, "scale": s, "a": a}
+
+
 def pack_int4(values: np.ndarray) -> np.ndarray:
     """Two 4-bit values per byte, low nibble = even flat index."""
     v = np.asarray(values, np.int64).reshape(-1) & 0xF

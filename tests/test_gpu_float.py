@@ -360,6 +360,11 @@ def test_config4_full_size(olamd, oracle, dev):
     mag = np.abs(decode(x["a_bits"][rows], "bf16", oracle)) @ np.abs(decode(w, "bf16", oracle))
     assert_close(got, fx["c4_y_bits"], mag, "bf16", oracle, "config 4")
     _fp8_chain_closed_form(y, x["a_bits"], x["w"], x["scale"], dev, "config 4")
+    # the bench draws the same inputs on the GPU (torch SplitMix64): bit for bit these
+    xt = _synth().config4_torch(dev)
+    assert torch.equal(xt["w"].cpu(), torch.from_numpy(x["w"]))
+    assert torch.equal(xt["a"].view(torch.int16).cpu(), torch.from_numpy(x["a_bits"].view(np.int16)))
+    assert torch.equal(xt["scale"].cpu(), torch.from_numpy(x["scale"]))
 
 
 def _fp8_chain_closed_form(y, a_bits, w_bits, scale, dev, what):
