@@ -137,7 +137,7 @@ int64_t DeviceCUs() {
 void LaunchFp8Gemm(const mg::GemmArgs &g, hipStream_t stream) {
   const int64_t cus = DeviceCUs();
   const int64_t nbm = (g.M + 255) / 256, nbn = (g.N + 255) / 256;
-  if (nbm * nbn < 512) {
+  if (nbm * nbn < 512 || g.K % 64 != 0) {  // 256 x 256 tiles take whole K steps only
     mg::Launch<mg::kBf16F8, mg::kOutBf16, false, false, false, 2>(g, stream);
     return;
   }

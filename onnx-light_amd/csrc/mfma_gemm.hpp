@@ -568,7 +568,11 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // head) needs one stage and no look-ahead: it and the zero points are
   // loaded together, and each 32-row block's MFMAs come right before its
   // epilogue, so the output stores start after the first block.
-  const bool block_major = nfull == 0;  // then half is set (K > 0)
+  // WB = 4 serves only whole K steps (the launcher checks K % kKStep == 0):
+  // without the half-step and single-step paths the register allocator keeps
+  // all 256 accumulators in registers through the loop.
+  constexpr bool kWhole = WB == 4;
+  const bool block_major = !kWhole && nfull == 0;  // then half is set (K > 0)
   if (block_major) {
     issue(0, 0, 4);
     load_zp();
@@ -591,14 +595,17 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     read(1, sa0, sb0, 1);
     decode(0, 0);
     int t = 0;
-    for (; t + 3 <= nfull; t += 3) {  // 12 sub-steps: s % 3 and the stages repeat
+    // 12 sub-steps per iteration: s % 3 and the stages repeat.  The last
+    // iteration's missing steps are skipped by uniform branches inside the
+    // loop: steps after the loop (another path with every accumulator live)
+    // made the register allocator spill the 256 accumulators of WB = 4 inside
+    // the loop.
+    for (; t < nfull; t += 3) {
       step(t, 0, 0, 1);
-      step(t + 1, 1, 1, 2);
-      step(t + 2, 2, 2, 0);
+      if (t + 1 < nfull) step(t + 1, 1, 1, 2);
+      if (t + 2 < nfull) step(t + 2, 2, 2, 0);
     }
-    if (t < nfull) step(t, 0, 0, 1);
-    if (t + 1 < nfull) step(t + 1, 1, 1, 2);
-    if (half) {
+    if (!kWhole && half) {
       const int r3 = nfull % 3;  // (4 * nfull) % 3
       if (r3 == 0) half_step(0);
       else if (r3 == 1) half_step(1);

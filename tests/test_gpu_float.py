@@ -404,3 +404,21 @@ def test_fp8_gemm_column_split(olamd, oracle, dev):
     ref, mag = _chain_ref(oracle, a, x, oracle.FLOAT8E4M3FN, K, N, sc, False, None, 1, "bf16", "bf16", rows=rows)
     assert_close(tensor_bits(y)[rows], ref, mag, "bf16", oracle, "fp8 column split")
     _fp8_chain_closed_form(y, a, x, sc, dev, "fp8 column split")
+
+
+def test_fp8_gemm_large_odd_k_step(olamd, oracle, dev):
+    """512 tiles of 256 x 256 would take the whole-K-step 256 x 256 kernel,
+    but K = 96 leaves half a K step: the launcher falls back to 256 x 128
+    tiles (every element against the float64 closed form of the chain, rows
+    against the oracle)."""
+    rng = np.random.default_rng(20261203)
+    M, K, N = 4096, 96, 8192
+    a = oracle.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    x = oracle.f32_to_f8e4m3fn_bits(rng.standard_normal(K * N).astype(np.float32)).reshape(K, N)
+    sc = rng.uniform(0.005, 0.05, N).astype(np.float32)
+    y = olamd.dequantize_linear_matmul(bits_tensor(a, "bf16", dev), T(x, dev), T(sc, dev), None, axis=1,
+                                       cast_to=olamd.BFLOAT16, x_dtype=oracle.FLOAT8E4M3FN, x_shape=(K, N))
+    rows = np.array([0, 255, 2048, 4095])
+    ref, mag = _chain_ref(oracle, a, x, oracle.FLOAT8E4M3FN, K, N, sc, False, None, 1, "bf16", "bf16", rows=rows)
+    assert_close(tensor_bits(y)[rows], ref, mag, "bf16", oracle, "fp8 K=96")
+    _fp8_chain_closed_form(y, a, x, sc, dev, "fp8 K=96")
