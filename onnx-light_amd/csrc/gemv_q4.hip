@@ -12,9 +12,11 @@
 //    segments of 64 bytes (CPL = 8) read HBM at about two thirds of the rate.
 //  - Dequantisation happens in registers.  Two k rows are merged byte-wise
 //    with v_perm_b32 so that each 32-bit register holds the nibbles of one
-//    column at rows k and k+1; OR-ing 0x6400 (fp16 1024) makes them exact fp16
-//    values 1024 + u, a packed fp16 subtract of (1024 + bias + zero point)
-//    recovers the integer, and a packed fp16 multiply by the column's scale
+//    column at rows k and k+1; OR-ing 0x6400 (fp16 1024) into the low nibbles
+//    makes them exact fp16 values 1024 + u, OR-ing 0x5400 (fp16 64, step
+//    1/16) into the high nibbles where they lie makes them 64 + u (no shift),
+//    a packed fp16 subtract of (1024 or 64 + bias + zero point) recovers the
+//    integer, and a packed fp16 multiply by the column's scale
 //    rounds exactly as fp16(float(q) * float(scale)) does (the fp32 product of
 //    a 4-bit integer and an fp16 scale is exact, so one rounding remains).
 //  - The decoded registers are already the A operand of
@@ -70,16 +72,16 @@ struct GemvArgs {
   int cpw;                // chunks per wave
 };
 
-// Nibbles of byte b of two k rows -> two fp16 pairs 0x6400 | u (= 1024 + u):
-// column 2b at rows (r0, r1) and column 2b + 1 at rows (r0, r1).  `sel`
-// gathers [x0.byte b, 0, x1.byte b, 0]; the AND-OR keeps one nibble per half
-// and inserts the fp16 exponent of 1024.
-__device__ __forceinline__ void DecodeBytePair(uint32_t x0, uint32_t x1, uint32_t sel, uint32_t mask,
-                                               uint32_t magic, uint32_t &even, uint32_t &odd) {
+// Nibbles of byte b of two k rows -> two fp16 pairs: column 2b at rows
+// (r0, r1) as 0x6400 | u (= 1024 + u, unit step 1) and column 2b + 1 at rows
+// (r0, r1) as 0x5400 | u << 4 (= 64 + u, step 1/16: the nibble stays at bits
+// 4-7, no shift).  `sel` gathers [x0.byte b, 0, x1.byte b, 0]; each AND-OR
+// keeps one nibble per half and inserts the fp16 exponent.
+__device__ __forceinline__ void DecodeBytePair(uint32_t x0, uint32_t x1, uint32_t sel, uint32_t &even,
+                                               uint32_t &odd) {
   const uint32_t pb = __builtin_amdgcn_perm(x1, x0, sel);
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(even) : "v"(pb), "v"(mask), "v"(magic));
-  const uint32_t sh = pb >> 4;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(odd) : "v"(sh), "v"(mask), "v"(magic));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(even) : "v"(pb), "v"(0x000f000fu), "v"(0x64006400u));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(odd) : "v"(pb), "v"(0x00f000f0u), "v"(0x54005400u));
 }
 
 __device__ __forceinline__ constexpr uint32_t ByteSel(int b) {
@@ -226,14 +228,14 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
 #pragma unroll
   for (int e = 0; e < CPL; ++e) acc[e] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t mask = 0x000f000fu, magic = 0x64006400u;
   const uint32_t flip = SIGNED ? 0x88888888u : 0u;  // signed nibble s -> s + 8
   auto compute = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < kH; ++h) {
       // Columns 8h + e of the lane: scale pair (s_e, s_e) and bias pair
-      // (1024 + zb_e) twice, zb = zero point (+ 8 for INT4, matching the
-      // weight's own offset), so that (0x6400 | u) - bias = x - zp exactly.
+      // (1024 + zb_e) (even e) or (64 + zb_e) (odd e) twice, zb = zero point
+      // (+ 8 for INT4, matching the weight's own offset), decoded like the
+      // weights, so that decoded weight - bias = x - zp exactly.
       uint32_t sc2[8], bias2[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -244,18 +246,19 @@ __global__ __launch_bounds__(kThreads) void GemvQ4Kernel(const GemvArgs p) {
         const uint32_t z = zp_raw[c][h] ^ flip;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          DecodeBytePair(z, z, ByteSel(b), mask, magic, bias2[2 * b], bias2[2 * b + 1]);
+          DecodeBytePair(z, z, ByteSel(b), bias2[2 * b], bias2[2 * b + 1]);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bias2[e] = SIGNED ? 0x64086408u : 0x64006400u;  // 1032 / 1024
+        for (int e = 0; e < 8; ++e)  // 1032 / 1024 (even), 72 / 64 (odd)
+          bias2[e] = (e & 1) ? (SIGNED ? 0x54805480u : 0x54005400u) : (SIGNED ? 0x64086408u : 0x64006400u);
       }
-      uint32_t wk[8][4];  // [column][row pair]: fp16 (1024 + u) at rows 2p, 2p+1
+      uint32_t wk[8][4];  // [column][row pair]: fp16 1024 + u (even) / 64 + u (odd) at rows 2p, 2p+1
 #pragma unroll
       for (int pr = 0; pr < 4; ++pr) {
         const uint32_t x0 = wq[c][2 * pr][h] ^ flip, x1 = wq[c][2 * pr + 1][h] ^ flip;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          DecodeBytePair(x0, x1, ByteSel(b), mask, magic, wk[2 * b][pr], wk[2 * b + 1][pr]);
+          DecodeBytePair(x0, x1, ByteSel(b), wk[2 * b][pr], wk[2 * b + 1][pr]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {

@@ -17,13 +17,18 @@
 //    column).  The decode is VALU-bound, and two waves sharing a SIMD left it
 //    idle while both waited for data;
 //  - a lane's dword already holds 8 consecutive k rows of one column with the
-//    nibbles of rows 2j and 2j+1 at bits 4j and 16+4j, so one AND-OR (plus a
-//    shift) yields the fp16 pair 0x6400 | u of two rows: the A operand of
-//    v_mfma_f32_16x16x32_f16 needs no byte permutation;
+//    nibbles of rows 2j and 2j+1 at bits 4j and 16+4j, so one AND-OR yields
+//    an fp16 pair of two rows: the A operand of v_mfma_f32_16x16x32_f16 needs
+//    no byte permutation.  Pairs 0 and 2 (nibbles at bits 0-3 of each half)
+//    OR into 0x6400 (1024, unit step 1) to give 1024 + u; pairs 1 and 3
+//    (bits 4-7) OR into 0x5400 (64, step 1/16) to give 64 + u without a
+//    shift; pairs 2 and 3 take the dword shifted right by 8.  One shift and
+//    four AND-ORs per dword;
 //  - the dequantised value is rounded exactly as the unfused chain rounds it:
-//    (0x6400 | u) - (1024 + offset + zp) is the exact integer x - zp, and one
-//    packed fp16 multiply by the scale rounds fp16(float(x - zp) * scale)
-//    (the fp32 product of a 5-bit integer and an fp16 scale is exact);
+//    (1024 + u) - (1024 + offset + zp) and (64 + u) - (64 + offset + zp) are
+//    the exact integer x - zp, and one packed fp16 multiply by the scale
+//    rounds fp16(float(x - zp) * scale) (the fp32 product of a 5-bit integer
+//    and an fp16 scale is exact);
 //  - the waves' fp32 partial sums are reduced through LDS in a fixed order
 //    and stored as fp16 (round to nearest even).
 #include <algorithm>
@@ -69,13 +74,20 @@ struct TiledArgs {
   uint32_t bias2;         // fp16 pair 1024 + offset (8 for INT4, 0 for UINT4), no zero point
 };
 
-// fp16 pair (1024 + u) of rows 2j, 2j+1 from a tiled dword.
-template <int J> __device__ __forceinline__ uint32_t RowPair(uint32_t w) {
-  const uint32_t x = J == 0 ? w : w >> (4 * J);
+// fp16 pair of rows 2j, 2j+1 from a tiled dword w (w8 = w >> 8): 1024 + u
+// for even j, 64 + u for odd j.
+template <int J> __device__ __forceinline__ uint32_t RowPair(uint32_t w, uint32_t w8) {
+  const uint32_t x = J < 2 ? w : w8;
+  const uint32_t mask = J & 1 ? 0x00f000f0u : 0x000f000fu;
+  const uint32_t magic = J & 1 ? 0x54005400u : 0x64006400u;
   uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(0x000f000fu), "v"(0x64006400u));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(magic));
   return r;
 }
+
+// The bias of the odd pairs (64 + offset + zp) from that of the even pairs
+// (0x6400 + offset + zp as fp16 bits): the integer moves to bits 4-7.
+__device__ __forceinline__ uint32_t OddBias(uint32_t b) { return 0x5400u + ((b - 0x6400u) << 4); }
 
 template <int T, bool HAS_ZP, bool SIGNED, int MODE>
 __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p) {
@@ -198,14 +210,15 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
           }
         }
         const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)s1);
-        const _Float16 bv = __builtin_bit_cast(_Float16, (uint16_t)b1);
-        const v2h s2 = v2h{sv, sv}, b2 = v2h{bv, bv};
-        const uint32_t w = (uint32_t)wq[s][t][c];
-        const uint32_t pr[4] = {RowPair<0>(w), RowPair<1>(w), RowPair<2>(w), RowPair<3>(w)};
+        const _Float16 bv = __builtin_bit_cast(_Float16, (uint16_t)(b1 & 0xffffu));
+        const _Float16 bo = __builtin_bit_cast(_Float16, (uint16_t)OddBias(b1 & 0xffffu));
+        const v2h s2 = v2h{sv, sv}, b2 = v2h{bv, bv}, b2o = v2h{bo, bo};
+        const uint32_t w = (uint32_t)wq[s][t][c], w8 = w >> 8;
+        const uint32_t pr[4] = {RowPair<0>(w, w8), RowPair<1>(w, w8), RowPair<2>(w, w8), RowPair<3>(w, w8)};
         v8h wop;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const v2h v = (__builtin_bit_cast(v2h, pr[j]) - b2) * s2;
+          const v2h v = (__builtin_bit_cast(v2h, pr[j]) - (j & 1 ? b2o : b2)) * s2;
           wop[2 * j] = v.x;
           wop[2 * j + 1] = v.y;
         }

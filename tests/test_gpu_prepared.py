@@ -51,6 +51,12 @@ PREP_CASES = [
     ("tensor-n77", "int4", 6, 136, 77, "tensor", None, False),
     ("m1-longk", "int4", 1, 8192, 256, "blocked", 128, False),
     ("wide-n", "int4", 8, 512, 9000, "blocked", 32, False),
+    # 2 and 4 tiles per workgroup, a partial last tile, a partial last 128-row
+    # group, scale blocks longer than a group
+    ("b256-t2", "uint4", 2, 768, 4808, "blocked", 256, False),
+    ("b8-k96-t4", "int4", 5, 96, 12808, "blocked", 8, False),
+    ("b32-k224", "int4", 4, 224, 1040, "blocked", 32, False),
+    ("b16-m16", "int4", 16, 384, 272, "blocked", 16, False),
     # M > 16: the general path dequantises the tiled weight, then the 16-bit MatMul
     ("general-m40", "int4", 40, 256, 80, "blocked", 32, True),
     ("general-m300", "uint4", 300, 128, 96, "col", None, False),
