@@ -1,0 +1,764 @@
+// onnx-light kernels backed by the MI355X library (include/onnxl_amd.h).
+//
+// This translation unit is compiled inside the onnx-light tree (it includes
+// the runtime's headers) and linked with onnx-light-amd/libonnxl_amd.so and
+// the HIP runtime (amdhip64).  Call RegisterMi355xKernelFunctions() once,
+// after the built-in kernels are registered (onnx_kernels::
+// RegisterKernelFunctions) and before any session resolves its kernels: the
+// registries are not synchronised (core/runtime/kernels/
+// kernel_dispatch_table.h:134-137).  Unchanged models and RuntimeSessions then
+// run the operators below on the GPU.
+//
+// What it does:
+//  - one KernelBase subclass per operator of the quantized-matmul path
+//    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
+//    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked)
+//    and for the two fused nodes the GPU patterns produce
+//    (ai.rt.amd:DequantizeLinearMatMul, ai.rt.amd:DequantizePackedMatMul),
+//    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
+//    the plain key the built-ins use (examples/register_custom_kernel/
+//    main.cc:105-114): a kGPU key would need RuntimeContextOptions.device =
+//    kGPU0, and then every other operator of the graph would fail to resolve;
+//  - the reference's contract for outputs: host tensors, complete when Run
+//    returns.  Host-descriptor calls stage their inputs to HBM, compute and
+//    copy the output back before returning;
+//  - constant inputs (weights, scales, zero points) are moved to HBM once per
+//    session through the kernel-preparation hooks (HasPreparations /
+//    DeclarePreparations, core/runtime/kernels/kernel_context.h:238-249), the
+//    way the built-in Gemm packs its constant B (km/kernel_gemm.cc:378-405).
+//    A constant INT4 / UINT4 weight of the fused node is also tiled there by
+//    onnxl_amd_prepare_weight;
+//  - inputs the library does not take (dtypes, ranks, formats it reports as
+//    ONNXL_AMD_UNSUPPORTED) run on the built-in kernel that was registered
+//    for the operator before this one; library errors become the reference's
+//    exception types (std::invalid_argument / std::runtime_error).
+#include "onnx_core/runtime/kernels/kernel_context.h"
+#include "onnx_core/runtime/kernels/kernel_dispatch_table.h"
+#include "onnx_core/runtime/kernels/node_helpers.h"
+#include "onnx_core/runtime/memory/simple_tensor.h"
+#include "onnx_core/runtime/runtime_context.h"
+#include "onnx_core/symbolic/sym_tensor.h"
+#include "onnx_proto/onnx.h"
+
+#include <hip/hip_runtime.h>
+
+#include "onnxl_amd.h"
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_set>
+#include <utility>
+#include <vector>
+
+namespace rt = ONNX_LIGHT_NAMESPACE::core::runtime;
+namespace sym = ONNX_LIGHT_NAMESPACE::core::symbolic;
+using ONNX_LIGHT_NAMESPACE::NodeProto;
+
+namespace mi355x {
+
+// ONNX TensorProto data types used below.
+constexpr int32_t kFloat = 1, kUint8 = 2, kInt8 = 3, kInt32 = 6, kFloat16 = 10, kBfloat16 = 16,
+                  kUint4 = 21, kInt4 = 22;
+constexpr const char *kFusedDomain = "ai.rt.amd";
+
+// Library status -> the reference's exception types.
+void Check(int rc) {
+  if (rc == ONNXL_AMD_OK) return;
+  if (rc == ONNXL_AMD_INVALID_ARGUMENT) throw std::invalid_argument(onnxl_amd_last_error());
+  throw std::runtime_error(onnxl_amd_last_error());
+}
+
+void CheckHip(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string("mi355x: ") + what + ": " + hipGetErrorString(e));
+}
+
+onnxl_amd_tensor Absent() {
+  onnxl_amd_tensor d{};
+  d.rank = -1;
+  return d;
+}
+
+// Host tensor -> C-ABI descriptor.  The library never writes an input.
+onnxl_amd_tensor Describe(const rt::Tensor *t) {
+  if (t == nullptr || t->data_type == 0) return Absent();  // absent optional input
+  if (t->shape.size() > ONNXL_AMD_MAX_RANK)
+    throw std::invalid_argument("mi355x: tensor rank above " + std::to_string(ONNXL_AMD_MAX_RANK));
+  onnxl_amd_tensor d{};
+  d.data_type = t->data_type;
+  d.rank = static_cast<int32_t>(t->shape.size());
+  for (int i = 0; i < d.rank; ++i) d.dims[i] = t->shape[i];
+  d.data = const_cast<uint8_t *>(t->bytes());
+  d.size_bytes = static_cast<int64_t>(t->size_bytes());
+  d.location = ONNXL_AMD_HOST;
+  d.layout = ONNXL_AMD_LAYOUT_ONNX;
+  return d;
+}
+
+onnxl_amd_tensor DescribeOutput(rt::Tensor &t) {
+  onnxl_amd_tensor d = Describe(&t);
+  d.data = t.mutable_bytes();
+  return d;
+}
+
+rt::Shape ShapeOf(const int64_t *dims, int32_t rank) {
+  return rt::Shape(std::vector<int64_t>(dims, dims + rank));
+}
+
+int64_t Count(const rt::Shape &s) {
+  int64_t n = 1;
+  for (size_t i = 0; i < s.size(); ++i) n *= s[i];
+  return n;
+}
+
+// HBM copy of a session constant, owned by the kernel that prepared it.
+struct DeviceTensor {
+  onnxl_amd_tensor desc{};
+  void *ptr = nullptr;
+  DeviceTensor() = default;
+  DeviceTensor(const DeviceTensor &) = delete;
+  DeviceTensor &operator=(const DeviceTensor &) = delete;
+  ~DeviceTensor() {
+    if (ptr != nullptr) (void)hipFree(ptr);
+  }
+  void Allocate(int64_t bytes) {
+    CheckHip(hipMalloc(&ptr, static_cast<size_t>(bytes > 0 ? bytes : 16)), "hipMalloc");
+  }
+};
+
+std::shared_ptr<DeviceTensor> UploadToHbm(const rt::Tensor &t) {
+  auto d = std::make_shared<DeviceTensor>();
+  d->desc = Describe(&t);
+  d->Allocate(d->desc.size_bytes);
+  if (d->desc.size_bytes > 0)
+    CheckHip(hipMemcpy(d->ptr, t.bytes(), t.size_bytes(), hipMemcpyHostToDevice), "hipMemcpy");
+  d->desc.data = d->ptr;
+  d->desc.location = ONNXL_AMD_DEVICE;
+  return d;
+}
+
+// A device buffer reused across runs (the fused node's activations and
+// output); grows only when a larger shape arrives.
+struct Staging {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  ~Staging() {
+    if (ptr != nullptr) (void)hipFree(ptr);
+  }
+  void *Reserve(size_t n) {
+    if (n > bytes) {
+      if (ptr != nullptr) CheckHip(hipFree(ptr), "hipFree");
+      ptr = nullptr;
+      CheckHip(hipMalloc(&ptr, n > 0 ? n : 16), "hipMalloc");
+      bytes = n;
+    }
+    return ptr;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Common base: constant inputs moved to HBM at preparation time, and the
+// built-in kernel of the same operator for the inputs the library does not
+// take.
+class Mi355xKernel : public rt::KernelBase {
+public:
+  Mi355xKernel(const rt::KernelContext &kc, std::unique_ptr<rt::KernelBase> builtin)
+      : rt::KernelBase(kc), builtin_(std::move(builtin)) {}
+
+  bool HasPreparations(const std::unordered_set<std::string> &immutable_inputs) const override {
+    for (int i : ConstantInputs())
+      if (i < node_->input_size() && !node_->input(i).empty() &&
+          immutable_inputs.count(node_->input(i)) != 0)
+        return true;
+    return builtin_ != nullptr && builtin_->HasPreparations(immutable_inputs);
+  }
+
+  void DeclarePreparations(const std::unordered_set<std::string> &immutable_inputs,
+                           std::vector<rt::KernelPreparation> &preparations) override {
+    for (int i : ConstantInputs()) {
+      if (i >= node_->input_size() || node_->input(i).empty() || immutable_inputs.count(node_->input(i)) == 0)
+        continue;
+      const std::string source = node_->input(i);
+      rt::KernelPreparation p;
+      p.info.source_inputs = {source};
+      p.info.representation = Representation(i);
+      p.info.output_slots = {source + ":" + p.info.representation};
+      // The prepared copy lives in HBM: no host memory beyond the source.
+      p.estimate_memory = [source](const rt::RuntimeContext &ctx) {
+        return rt::KernelPreparationMemory{ctx.Get(source).size_bytes(), 0, 0};
+      };
+      p.execute = [this, i, source](rt::RuntimeContext &ctx) {
+        auto d = Prepare(i, ctx.Get(source));
+        std::lock_guard<std::mutex> lock(mu_);
+        prepared_[i] = std::move(d);  // published only once complete
+      };
+      preparations.push_back(std::move(p));
+    }
+    // The built-in kernel keeps its own preparations for the inputs it runs.
+    if (builtin_ != nullptr) builtin_->DeclarePreparations(immutable_inputs, preparations);
+  }
+
+protected:
+  // Node inputs that are worth keeping in HBM when they are constants.
+  virtual std::vector<int> ConstantInputs() const { return {}; }
+  virtual std::string Representation(int /*index*/) const { return "mi355x:hbm-copy-v1"; }
+  virtual std::shared_ptr<DeviceTensor> Prepare(int /*index*/, const rt::Tensor &t) { return UploadToHbm(t); }
+
+  // Descriptor of input `i` for this run: its HBM copy when prepared, else the
+  // host tensor, else absent.
+  onnxl_amd_tensor In(int i, rt::RuntimeContext &ctx) const {
+    auto it = prepared_.find(i);
+    if (it != prepared_.end()) return it->second->desc;
+    if (i >= node_->input_size() || node_->input(i).empty()) return Absent();
+    return Describe(rt::GetOptionalInput(*node_, i, ctx));
+  }
+  bool Prepared(int i) const { return prepared_.count(i) != 0; }
+
+  // Runs the built-in kernel (after the library reported UNSUPPORTED).
+  void RunBuiltin(rt::RuntimeContext &ctx, const char *why) {
+    if (builtin_ == nullptr)
+      throw std::runtime_error(std::string("mi355x: ") + node_->op_type() + ": " + why +
+                               " and no built-in kernel is registered");
+    builtin_->Run(ctx);
+  }
+
+  // Library call with the built-in kernel as the fallback for UNSUPPORTED.
+  // Returns true when the library computed the output.
+  bool Call(int rc, rt::RuntimeContext &ctx) {
+    if (rc == ONNXL_AMD_UNSUPPORTED) {
+      RunBuiltin(ctx, onnxl_amd_last_error());
+      return false;
+    }
+    Check(rc);
+    return true;
+  }
+
+  std::unique_ptr<rt::KernelBase> builtin_;
+  std::map<int, std::shared_ptr<DeviceTensor>> prepared_;
+  std::mutex mu_;
+};
+
+// MatMul output shape as the reference computes it (km/matmul_shape_utils.h).
+rt::Shape MatMulShape(const onnxl_amd_tensor &a, const onnxl_amd_tensor &b) {
+  int64_t dims[ONNXL_AMD_MAX_RANK];
+  int32_t rank = 0;
+  Check(onnxl_amd_matmul_shape(a.dims, a.rank, b.dims, b.rank, dims, &rank));
+  return ShapeOf(dims, rank);
+}
+
+// ---------------------------------------------------------------------------
+// MatMulInteger (km/kernel_matmul_integer.cc): A, B, optional zero points.
+class Mi355xMatMulInteger : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:MatMulInteger";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor a = In(0, ctx), b = In(1, ctx), za = In(2, ctx), zb = In(3, ctx);
+    const rt::Shape shape = MatMulShape(a, b);
+    rt::Tensor y = ctx.MakeOutputTensor(0, kInt32, shape, static_cast<size_t>(Count(shape)) * 4);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_matmul_integer(&a, &b, &za, &zb, &dy, nullptr), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2, 3}; }
+};
+
+// QLinearMatMul (kq/kernel_qlinearmatmul.cc:269-296): 8 inputs.
+class Mi355xQLinearMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:QLinearMatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 8);
+    rt::RequireOutputCount(node, 1);
+    onnxl_amd_tensor in[8];
+    for (int i = 0; i < 8; ++i) in[i] = In(i, ctx);
+    const rt::Shape shape = MatMulShape(in[0], in[3]);
+    rt::Tensor y = ctx.MakeOutputTensor(0, in[7].data_type, shape, static_cast<size_t>(Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_qlinear_matmul(&in[0], &in[1], &in[2], &in[3], &in[4], &in[5], &in[6], &in[7], &dy, nullptr),
+             ctx))
+      rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2, 3, 4, 5, 6, 7}; }
+};
+
+// Bytes of `count` elements of `dtype`, 4-bit types packed two per byte.
+size_t ByteSize(int32_t dtype, int64_t count) { return rt::PackedByteSize(dtype, count); }
+
+// DequantizeLinear (kq/kernel_dequantizelinear.cc:695-712): axis defaults to
+// 1; y takes x_scale's dtype.
+class Mi355xDequantizeLinear : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:DequantizeLinear";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor x = In(0, ctx), s = In(1, ctx), z = In(2, ctx);
+    const int64_t axis = rt::GetAttributeIntOrDefault(node, "axis", 1);
+    const rt::Shape shape = ShapeOf(x.dims, x.rank);
+    rt::Tensor y = ctx.MakeOutputTensor(0, s.data_type, shape, ByteSize(s.data_type, Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_dequantize_linear(&x, &s, &z, axis, &dy, nullptr), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {0, 1, 2}; }
+};
+
+// QuantizeLinear (kq/kernel_quantizelinear.cc:917-941): y's dtype is the zero
+// point's, else output_dtype, else UINT8.
+class Mi355xQuantizeLinear : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:QuantizeLinear";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor x = In(0, ctx), s = In(1, ctx), z = In(2, ctx);
+    const int64_t axis = rt::GetAttributeIntOrDefault(node, "axis", 1);  // may be negative
+    const int64_t odt = rt::GetAttributeIntOrDefault(node, "output_dtype", 0);
+    const int32_t yt = z.rank >= 0 ? z.data_type : (odt != 0 ? static_cast<int32_t>(odt) : kUint8);
+    const rt::Shape shape = ShapeOf(x.dims, x.rank);
+    rt::Tensor y = ctx.MakeOutputTensor(0, yt, shape, ByteSize(yt, Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_quantize_linear(&x, &s, &z, axis, static_cast<int32_t>(odt), &dy, nullptr), ctx))
+      rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2}; }
+};
+
+// DynamicQuantizeLinear (kq/kernel_dynamicquantizelinear.cc): three outputs.
+// The library reports non-finite x as y_scale = NaN; the outputs are host
+// tensors, complete on return, so the adapter raises the reference's error.
+class Mi355xDynamicQuantizeLinear : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:DynamicQuantizeLinear";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 1);
+    rt::RequireOutputCount(node, 3);
+    const onnxl_amd_tensor x = In(0, ctx);
+    const rt::Shape shape = ShapeOf(x.dims, x.rank);
+    rt::Tensor y = ctx.MakeOutputTensor(0, kUint8, shape, static_cast<size_t>(Count(shape)));
+    rt::Tensor s = ctx.MakeOutputTensor(1, kFloat, rt::Shape{}, sizeof(float));
+    rt::Tensor z = ctx.MakeOutputTensor(2, kUint8, rt::Shape{}, 1);
+    onnxl_amd_tensor dy = DescribeOutput(y), ds = DescribeOutput(s), dz = DescribeOutput(z);
+    if (!Call(onnxl_amd_dynamic_quantize_linear(&x, &dy, &ds, &dz, nullptr), ctx)) return;
+    float scale;
+    std::memcpy(&scale, s.bytes(), sizeof(float));
+    if (std::isnan(scale)) throw std::invalid_argument("kernel::DynamicQuantizeLinear: x elements must be finite.");
+    rt::SetOutput(node, 0, std::move(y), ctx);
+    rt::SetOutput(node, 1, std::move(s), ctx);
+    rt::SetOutput(node, 2, std::move(z), ctx);
+  }
+};
+
+// MatMul (km/kernel_matmul.cc): FLOAT16 / BFLOAT16 on the GPU, every other
+// dtype on the built-in kernel.
+class Mi355xMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:MatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor a = In(0, ctx), b = In(1, ctx);
+    if ((a.data_type != kFloat16 && a.data_type != kBfloat16) || b.data_type != a.data_type) {
+      RunBuiltin(ctx, "dtype other than FLOAT16 / BFLOAT16");
+      return;
+    }
+    const rt::Shape shape = MatMulShape(a, b);
+    rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_matmul(&a, &b, &dy, nullptr), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1}; }
+};
+
+// Cast (ext/kernels/kernels/tensor/kernel_cast.cc:360-370): FLOAT ->
+// FLOAT16 / BFLOAT16 on the GPU (the Cast between DequantizeLinear and a
+// 16-bit MatMul), every other pair on the built-in kernel.
+class Mi355xCast : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:Cast";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 1);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor x = In(0, ctx);
+    const int32_t to = static_cast<int32_t>(rt::GetAttributeIntOrDefault(node, "to", 0));
+    if (x.data_type != kFloat || (to != kFloat16 && to != kBfloat16) ||
+        rt::GetAttributeIntOrDefault(node, "saturate", 1) != 1) {
+      RunBuiltin(ctx, "cast other than FLOAT -> FLOAT16 / BFLOAT16");
+      return;
+    }
+    const rt::Shape shape = ShapeOf(x.dims, x.rank);
+    rt::Tensor y = ctx.MakeOutputTensor(0, to, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_cast(&x, to, &dy, nullptr), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+};
+
+// Convolution attributes as ConvInteger::Run / QLinearConv::Run read them
+// (nn/kernel_conv_integer.cc:306-330, kq/kernel_qlinearconv.cc:352-375).
+// Returns false when the node has more spatial dims than the library takes.
+bool ConvAttrs(const NodeProto &node, onnxl_amd_conv_attrs &a) {
+  a = onnxl_amd_conv_attrs{};
+  const std::vector<int64_t> ks = rt::GetAttributeIntsOrDefault(node, "kernel_shape", {});
+  const std::vector<int64_t> st = rt::GetAttributeIntsOrDefault(node, "strides", {});
+  const std::vector<int64_t> pd = rt::GetAttributeIntsOrDefault(node, "pads", {});
+  const std::vector<int64_t> dl = rt::GetAttributeIntsOrDefault(node, "dilations", {});
+  if (ks.size() > ONNXL_AMD_MAX_CONV_SPATIAL || st.size() > ONNXL_AMD_MAX_CONV_SPATIAL ||
+      pd.size() > 2 * ONNXL_AMD_MAX_CONV_SPATIAL || dl.size() > ONNXL_AMD_MAX_CONV_SPATIAL)
+    return false;
+  a.n_kernel_shape = static_cast<int32_t>(ks.size());
+  a.n_strides = static_cast<int32_t>(st.size());
+  a.n_pads = static_cast<int32_t>(pd.size());
+  a.n_dilations = static_cast<int32_t>(dl.size());
+  for (size_t i = 0; i < ks.size(); ++i) a.kernel_shape[i] = ks[i];
+  for (size_t i = 0; i < st.size(); ++i) a.strides[i] = st[i];
+  for (size_t i = 0; i < pd.size(); ++i) a.pads[i] = pd[i];
+  for (size_t i = 0; i < dl.size(); ++i) a.dilations[i] = dl[i];
+  a.group = rt::GetAttributeIntOrDefault(node, "group", 1);
+  const std::string ap = rt::GetAttributeStringOrDefault(node, "auto_pad", "NOTSET");
+  a.auto_pad = ap == "SAME_UPPER"   ? ONNXL_AMD_AUTO_PAD_SAME_UPPER
+               : ap == "SAME_LOWER" ? ONNXL_AMD_AUTO_PAD_SAME_LOWER
+               : ap == "VALID"      ? ONNXL_AMD_AUTO_PAD_VALID
+                                    : ONNXL_AMD_AUTO_PAD_NOTSET;  // as AutoPadFromString
+  return true;
+}
+
+rt::Shape ConvShape(const onnxl_amd_tensor &x, const onnxl_amd_tensor &w, const onnxl_amd_conv_attrs &a) {
+  int64_t dims[ONNXL_AMD_MAX_RANK];
+  int32_t rank = 0;
+  Check(onnxl_amd_conv_shape(x.dims, x.rank, w.dims, w.rank, &a, dims, &rank));
+  return ShapeOf(dims, rank);
+}
+
+// ConvInteger (nn/kernel_conv_integer.cc:306-330).
+class Mi355xConvInteger : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:ConvInteger";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    onnxl_amd_conv_attrs attrs;
+    if (!ConvAttrs(node, attrs)) {
+      RunBuiltin(ctx, "more than 3 spatial dims");
+      return;
+    }
+    const onnxl_amd_tensor x = In(0, ctx), w = In(1, ctx), zx = In(2, ctx), zw = In(3, ctx);
+    if (x.rank < 3 || x.rank > 2 + ONNXL_AMD_MAX_CONV_SPATIAL) {
+      RunBuiltin(ctx, "input rank outside 3..5");
+      return;
+    }
+    const rt::Shape shape = ConvShape(x, w, attrs);
+    rt::Tensor y = ctx.MakeOutputTensor(0, kInt32, shape, static_cast<size_t>(Count(shape)) * 4);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_conv_integer(&x, &w, &zx, &zw, &attrs, &dy, nullptr), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 3}; }
+};
+
+// QLinearConv (kq/kernel_qlinearconv.cc:352-375): 8 inputs and an optional
+// INT32 bias; y takes y_zero_point's dtype.
+class Mi355xQLinearConv : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:QLinearConv";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 8);
+    rt::RequireOutputCount(node, 1);
+    onnxl_amd_conv_attrs attrs;
+    if (!ConvAttrs(node, attrs)) {
+      RunBuiltin(ctx, "more than 3 spatial dims");
+      return;
+    }
+    onnxl_amd_tensor in[9];
+    for (int i = 0; i < 9; ++i) in[i] = In(i, ctx);
+    if (in[0].rank < 3 || in[0].rank > 2 + ONNXL_AMD_MAX_CONV_SPATIAL) {
+      RunBuiltin(ctx, "input rank outside 3..5");
+      return;
+    }
+    const rt::Shape shape = ConvShape(in[0], in[3], attrs);
+    rt::Tensor y = ctx.MakeOutputTensor(0, in[7].data_type, shape, static_cast<size_t>(Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_qlinear_conv(&in[0], &in[1], &in[2], &in[3], &in[4], &in[5], &in[6], &in[7], &in[8], &attrs,
+                                    &dy, nullptr),
+             ctx))
+      rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2, 3, 4, 5, 6, 7, 8}; }
+};
+
+// DequantizePacked (kq/kernel_dequantize_packed.cc:13-26): format, shape and
+// output_dtype attributes; the GGUF formats the GPU decodes, the others on
+// the built-in kernel.
+class Mi355xDequantizePacked : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:DequantizePacked";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 1);
+    rt::RequireOutputCount(node, 1);
+    const std::string format = rt::GetRequiredAttributeString(node, "format");
+    const std::vector<int64_t> dims = rt::GetAttributeIntsOrDefault(node, "shape", {});
+    const int64_t odt = rt::GetAttributeIntOrDefault(node, "output_dtype", kFloat);
+    const onnxl_amd_tensor x = In(0, ctx);
+    if (dims.empty() || dims.size() > ONNXL_AMD_MAX_RANK) {
+      RunBuiltin(ctx, "shape attribute the library does not take");
+      return;
+    }
+    const rt::Shape shape(dims);
+    rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(odt), shape,
+                                        ByteSize(static_cast<int32_t>(odt), Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_dequantize_packed(&x, format.c_str(), dims.data(), static_cast<int32_t>(dims.size()), odt, &dy,
+                                         nullptr),
+             ctx))
+      rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {0}; }
+};
+
+// ---------------------------------------------------------------------------
+// Fused nodes.  They exist only in graphs rewritten by the GPU patterns, so
+// there is no built-in kernel: the adapter computes their chain itself when
+// the fused kernel does not take an input.
+
+// ai.rt.amd:DequantizeLinearMatMul(A, x, x_scale[, x_zero_point]; axis,
+// cast_to) = MatMul(A, [Cast(to=cast_to)](DequantizeLinear(x, x_scale,
+// x_zero_point, axis))).  A constant INT4 / UINT4 weight is tiled once at
+// preparation.  When x, x_scale and x_zero_point are all prepared, each run
+// stages A into a reused device buffer and calls the no-allocation entry
+// point, so a steady serving loop performs no device allocation at all; when
+// that entry point's fixed scratch is too small it calls the allocating one.
+class Mi355xDequantizeLinearMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizeLinearMatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 3);
+    rt::RequireOutputCount(node, 1);
+    const int64_t axis = rt::GetAttributeIntOrDefault(node, "axis", 1);
+    const int32_t cast_to = static_cast<int32_t>(rt::GetAttributeIntOrDefault(node, "cast_to", 0));
+    onnxl_amd_tensor a = In(0, ctx), x = In(1, ctx), s = In(2, ctx), z = In(3, ctx);
+    // logical weight shape [K, N] (a prepared weight's dims are the logical ones)
+    const rt::Shape shape = MatMulShape(a, x);
+    const size_t y_bytes = static_cast<size_t>(Count(shape)) * 2;
+    rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, y_bytes);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const bool constants_on_device = Prepared(1) && Prepared(2) && (z.rank < 0 || Prepared(3));
+    if (constants_on_device) {
+      // device-resident call: stage A, compute, copy Y back
+      const size_t a_bytes = static_cast<size_t>(a.size_bytes);
+      void *da = a_stage_.Reserve(a_bytes);
+      void *dyp = y_stage_.Reserve(y_bytes);
+      if (a_bytes > 0) CheckHip(hipMemcpy(da, a.data, a_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+      onnxl_amd_tensor ad = a, yd = dy;
+      ad.data = da;
+      ad.location = ONNXL_AMD_DEVICE;
+      yd.data = dyp;
+      yd.location = ONNXL_AMD_DEVICE;
+      int rc = onnxl_amd_dequantize_linear_matmul_noalloc(&ad, &x, &s, &z, axis, cast_to, &yd, nullptr);
+      if (rc == ONNXL_AMD_UNSUPPORTED)  // beyond the fixed scratch: the allocating entry point
+        rc = onnxl_amd_dequantize_linear_matmul(&ad, &x, &s, &z, axis, cast_to, &yd, nullptr);
+      if (rc == ONNXL_AMD_UNSUPPORTED) {
+        RunChain(ctx, a, x, s, z, axis, cast_to, y);
+      } else {
+        Check(rc);
+        Check(onnxl_amd_synchronize(nullptr));
+        if (y_bytes > 0) CheckHip(hipMemcpy(y.mutable_bytes(), dyp, y_bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+      }
+    } else {
+      const int rc = onnxl_amd_dequantize_linear_matmul(&a, &x, &s, &z, axis, cast_to, &dy, nullptr);
+      if (rc == ONNXL_AMD_UNSUPPORTED) RunChain(ctx, a, x, s, z, axis, cast_to, y);
+      else Check(rc);
+    }
+    rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2, 3}; }
+  std::string Representation(int index) const override {
+    return index == 1 ? "mi355x:tiled-int4-or-hbm-copy-v1" : "mi355x:hbm-copy-v1";
+  }
+  std::shared_ptr<DeviceTensor> Prepare(int index, const rt::Tensor &t) override {
+    if (index != 1 || (t.data_type != kInt4 && t.data_type != kUint4) || t.shape.size() != 2) return UploadToHbm(t);
+    // Tiled 4-bit weight: each 16-column tile's K range contiguous.
+    auto host = Describe(&t);
+    int64_t bytes = 0;
+    Check(onnxl_amd_prepare_weight_size(&host, &bytes));
+    auto d = std::make_shared<DeviceTensor>();
+    d->Allocate(bytes);
+    d->desc = onnxl_amd_tensor{};
+    d->desc.data = d->ptr;
+    d->desc.size_bytes = bytes;
+    d->desc.location = ONNXL_AMD_DEVICE;
+    Check(onnxl_amd_prepare_weight(&host, &d->desc, nullptr));
+    Check(onnxl_amd_synchronize(nullptr));
+    return d;
+  }
+
+private:
+  // The unfused chain on the GPU for inputs the fused kernel does not take:
+  // DequantizeLinear into x_scale's dtype, the optional Cast, then MatMul.
+  void RunChain(rt::RuntimeContext &ctx, const onnxl_amd_tensor &a, const onnxl_amd_tensor &x,
+                const onnxl_amd_tensor &s, const onnxl_amd_tensor &z, int64_t axis, int32_t cast_to, rt::Tensor &y) {
+    if (x.layout != ONNXL_AMD_LAYOUT_ONNX)
+      throw std::runtime_error("mi355x: DequantizeLinearMatMul: prepared weight outside the fused kernel's range");
+    const rt::Shape wshape = ShapeOf(x.dims, x.rank);
+    const int64_t n = Count(wshape);
+    rt::Tensor w = ctx.MakeTemporaryTensor(s.data_type, wshape, ByteSize(s.data_type, n));
+    onnxl_amd_tensor dw = DescribeOutput(w);
+    Check(onnxl_amd_dequantize_linear(&x, &s, &z, axis, &dw, nullptr));
+    onnxl_amd_tensor b = dw;
+    rt::Tensor wc;
+    if (cast_to != 0) {
+      wc = ctx.MakeTemporaryTensor(cast_to, wshape, static_cast<size_t>(n) * 2);
+      onnxl_amd_tensor dwc = DescribeOutput(wc);
+      Check(onnxl_amd_cast(&dw, cast_to, &dwc, nullptr));
+      b = dwc;
+    }
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    Check(onnxl_amd_matmul(&a, &b, &dy, nullptr));
+  }
+
+  Staging a_stage_, y_stage_;
+};
+
+// ai.rt.amd:DequantizePackedMatMul(A, x; format, shape = [N, K]) =
+// MatMul(A, Transpose(DequantizePacked(x, format, shape, FLOAT16))), the
+// chain onnx_core/runtime/dequantize_packed.cc:334-372 -> km/kernel_matmul.cc.
+// The fused GEMV takes q4_0 / q8_0 with M <= 8 and K % 64 == 0; other inputs
+// run the chain (GPU decode, host transpose, GPU MatMul).
+class Mi355xDequantizePackedMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizePackedMatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const std::string format = rt::GetRequiredAttributeString(node, "format");
+    const std::vector<int64_t> nk = rt::GetAttributeIntsOrDefault(node, "shape", {});
+    if (nk.size() != 2) throw std::invalid_argument("DequantizePackedMatMul: shape must be [N, K].");
+    const onnxl_amd_tensor a = In(0, ctx), x = In(1, ctx);
+    onnxl_amd_tensor wt{};  // logical [K, N] operand for the output shape
+    wt.rank = 2;
+    wt.dims[0] = nk[1];
+    wt.dims[1] = nk[0];
+    const rt::Shape shape = MatMulShape(a, wt);
+    rt::Tensor y = ctx.MakeOutputTensor(0, kFloat16, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const int rc = onnxl_amd_dequantize_packed_matmul(&a, &x, format.c_str(), nk.data(), 2, &dy, nullptr);
+    if (rc == ONNXL_AMD_UNSUPPORTED) {
+      // W [N, K] decoded to FLOAT16 on the GPU, transposed on the host, MatMul
+      const int64_t N = nk[0], K = nk[1];
+      rt::Tensor w = ctx.MakeTemporaryTensor(kFloat16, rt::Shape{N, K}, static_cast<size_t>(N * K) * 2);
+      onnxl_amd_tensor dw = DescribeOutput(w);
+      Check(onnxl_amd_dequantize_packed(&x, format.c_str(), nk.data(), 2, kFloat16, &dw, nullptr));
+      rt::Tensor wtt = ctx.MakeTemporaryTensor(kFloat16, rt::Shape{K, N}, static_cast<size_t>(N * K) * 2);
+      const uint16_t *src = reinterpret_cast<const uint16_t *>(w.bytes());
+      uint16_t *dst = reinterpret_cast<uint16_t *>(wtt.mutable_bytes());
+      for (int64_t r = 0; r < N; ++r)
+        for (int64_t c = 0; c < K; ++c) dst[c * N + r] = src[r * K + c];
+      const onnxl_amd_tensor b = Describe(&wtt);
+      Check(onnxl_amd_matmul(&a, &b, &dy, nullptr));
+    } else {
+      Check(rc);
+    }
+    rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1}; }
+};
+
+// ---------------------------------------------------------------------------
+// Registration.
+
+rt::NodeKernelFn BuiltinFactory(const std::string &key) {
+  const auto &table = rt::KernelDispatchTable();
+  const auto it = table.find(key);
+  return it == table.end() ? rt::NodeKernelFn{} : it->second;
+}
+
+template <typename K> void Register(const char *domain, const char *op_type) {
+  const std::string key = std::string(*domain ? domain : "ai.onnx") + ":" + op_type;
+  rt::NodeKernelFn builtin = BuiltinFactory(key);  // captured before the override
+  rt::RegisterKernelFn(
+      domain, op_type, sym::Device::kCPU,
+      [builtin](const NodeProto &node, rt::RuntimeContext &ctx,
+                const rt::KernelContext &kc) -> std::unique_ptr<rt::KernelBase> {
+        std::unique_ptr<rt::KernelBase> fallback = builtin ? builtin(node, ctx, kc) : nullptr;
+        auto k = std::make_unique<K>(kc, std::move(fallback));
+        k->set_node(node);
+        return k;
+      },
+      /*overwrite=*/true);
+}
+
+std::once_flag g_registered;
+
+}  // namespace mi355x
+
+// Registers the MI355X kernels over the built-in CPU kernels of the same
+// operators (and the two fused nodes).  Call once, after the built-ins are
+// registered; later calls do nothing.  Returns the library version string.
+const char *RegisterMi355xKernelFunctions(int device_ordinal = 0) {
+  using namespace mi355x;
+  std::call_once(g_registered, [device_ordinal] {
+    Check(onnxl_amd_init(device_ordinal));
+    Register<Mi355xMatMulInteger>("", "MatMulInteger");
+    Register<Mi355xQLinearMatMul>("", "QLinearMatMul");
+    Register<Mi355xDequantizeLinear>("", "DequantizeLinear");
+    Register<Mi355xQuantizeLinear>("", "QuantizeLinear");
+    Register<Mi355xDynamicQuantizeLinear>("", "DynamicQuantizeLinear");
+    Register<Mi355xMatMul>("", "MatMul");
+    Register<Mi355xCast>("", "Cast");
+    Register<Mi355xConvInteger>("", "ConvInteger");
+    Register<Mi355xQLinearConv>("", "QLinearConv");
+    Register<Mi355xDequantizePacked>("", "DequantizePacked");
+    Register<Mi355xDequantizeLinearMatMul>(kFusedDomain, "DequantizeLinearMatMul");
+    Register<Mi355xDequantizePackedMatMul>(kFusedDomain, "DequantizePackedMatMul");
+  });
+  return onnxl_amd_version();
+}
+
+// Releases the library's device buffers; call after every session has ended.
+void ShutdownMi355xKernelFunctions() { mi355x::Check(onnxl_amd_shutdown()); }

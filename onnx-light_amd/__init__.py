@@ -549,8 +549,9 @@ class MatMul:
 
 
 class DequantizePacked:
-    """Kernel-class mirror of kernel::DequantizePacked (ai.rt domain)."""
-    name = "onnxl_amd:GPU:ai.rt:DequantizePacked"
+    """Kernel-class mirror of kernel::DequantizePacked (default ONNX domain,
+    onnx-light opset 29; kernel_dispatch_table.cc:147)."""
+    name = "onnxl_amd:GPU:ai.onnx:DequantizePacked"
 
     def __call__(self, x, format, shape, output_dtype=FLOAT, out=None):
         return dequantize_packed(x, format, shape, output_dtype, out)
@@ -605,6 +606,18 @@ class DequantizeLinearMatMul:
         return dequantize_linear_matmul(a, x, x_scale, x_zero_point, axis, cast_to, x_dtype, x_shape, out)
 
 
+class DequantizePackedMatMul:
+    """Kernel of the fused node that the DequantizePacked -> Transpose ->
+    MatMul rewrite (``patterns.DequantizePackedMatMulPattern``) produces:
+    inputs (A, x), attributes format and shape = [N, K].  No reference
+    kernel: it computes kernel::DequantizePacked (FLOAT16), the transpose and
+    kernel::MatMul in one pass."""
+    name = "onnxl_amd:GPU:ai.rt.amd:DequantizePackedMatMul"
+
+    def __call__(self, a, x, format, shape, out=None):
+        return dequantize_packed_matmul(a, x, format, shape, out)
+
+
 # Dispatch keys "<domain>:<op_type>" as the reference table uses them
 # (core/runtime/kernels/kernel_dispatch_table.h:148-164).
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
@@ -612,8 +625,9 @@ KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLin
            "ai.onnx:QuantizeLinear": QuantizeLinear,
            "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear,
            "ai.onnx:ConvInteger": ConvInteger, "ai.onnx:QLinearConv": QLinearConv,
-           "ai.rt:DequantizePacked": DequantizePacked,
-           "ai.rt.amd:DequantizeLinearMatMul": DequantizeLinearMatMul}
+           "ai.onnx:DequantizePacked": DequantizePacked,
+           "ai.rt.amd:DequantizeLinearMatMul": DequantizeLinearMatMul,
+           "ai.rt.amd:DequantizePackedMatMul": DequantizePackedMatMul}
 
 
 class Prepared:

@@ -1,5 +1,5 @@
-"""Graph rewrite that hands DequantizeLinear -> [Cast] -> MatMul to the fused
-GPU kernel.
+"""Graph rewrites that hand DequantizeLinear -> [Cast] -> MatMul and
+DequantizePacked -> Transpose -> MatMul to the fused GPU kernels.
 
 Mirrors the reference's pattern interface: a pattern's ``match`` returns the
 nodes of a rewrite in the order ``apply`` expects, or a no-match carrying the
@@ -44,6 +44,8 @@ from typing import Callable, Dict, List, Optional, Sequence
 
 FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
+PACKED_FUSED_OP = "DequantizePackedMatMul"
+_PACKED_FORMATS = ("gguf:q4_0", "gguf:q8_0")  # the fused packed GEMV's formats
 _ONNX_DOMAINS = ("", "ai.onnx")
 _CAST_TARGETS = (10, 16)  # FLOAT16, BFLOAT16: the types the fused kernel rounds to
 FLOAT, UINT8, INT8, FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 1, 2, 3, 10, 16, 17, 21, 22
@@ -141,7 +143,7 @@ class DequantizeLinearMatMulPattern(PatternOptimization):
         zp = info[names[2]] if len(names) > 2 else None
         w_shape, s_shape = tuple(w_shape), tuple(s_shape)
         if w_t not in _WEIGHT_TYPES:
-            return f"weight type {w_t} has no fused kernel"
+            return "weight type has no fused kernel"
         if len(w_shape) != 2:
             return "weight is not 2-D"
         if s_t not in _SCALE_TYPES:
@@ -214,6 +216,61 @@ class DequantizeLinearMatMulPattern(PatternOptimization):
                      matmul.name or dq.name)]
 
 
+class DequantizePackedMatMulPattern(PatternOptimization):
+    """DequantizePacked(x; format, shape = [N, K], output_dtype = FLOAT16) over
+    a constant x -> Transpose(perm = [1, 0]) -> MatMul's second input, with a
+    FLOAT16 A -> one fused node ``ai.rt.amd:DequantizePackedMatMul(A, x)``
+    with attributes format and shape, computed by
+    ``dequantize_packed_matmul``.  Only the formats the fused GEMV decodes
+    (q4_0, q8_0) and K % 64 == 0 are rewritten; the GEMV takes up to 8 rows
+    of A, and a session adapter runs the chain for taller A (the row count is
+    only known at run time)."""
+    device = "gpu"
+
+    def fast_op_type(self) -> set:
+        return {"MatMul"}
+
+    def match(self, graph: Graph, candidate: Node) -> MatchResult:
+        if not _is_onnx(candidate, "MatMul") or len(candidate.inputs) != 2:
+            return self.no_match("not a MatMul")
+        tr = graph.producer(candidate.inputs[1])
+        if tr is None or not _is_onnx(tr, "Transpose"):
+            return self.no_match("MatMul's second input is not a Transpose output")
+        if [int(p) for p in tr.attrs.get("perm", [1, 0])] != [1, 0]:
+            return self.no_match("Transpose is not a 2-D transpose")
+        if not DequantizeLinearMatMulPattern._single_use(graph, tr.outputs[0], candidate):
+            return self.no_match("Transpose output has another consumer")
+        dp = graph.producer(tr.inputs[0])
+        if dp is None or not _is_onnx(dp, "DequantizePacked"):
+            return self.no_match("Transpose input is not a DequantizePacked output")
+        if not DequantizeLinearMatMulPattern._single_use(graph, dp.outputs[0], tr):
+            return self.no_match("DequantizePacked output has another consumer")
+        if dp.inputs[0] not in graph.initializers:
+            return self.no_match("packed weight is not an initializer")
+        fmt = dp.attrs.get("format")
+        if fmt not in _PACKED_FORMATS:
+            return self.no_match("format has no fused kernel")
+        shape = [int(d) for d in dp.attrs.get("shape", [])]
+        if len(shape) != 2:
+            return self.no_match("DequantizePacked shape is not [N, K]")
+        if int(dp.attrs.get("output_dtype", FLOAT)) != FLOAT16:
+            return self.no_match("DequantizePacked output is not FLOAT16")
+        if shape[1] % 64:
+            return self.no_match("K is not a multiple of 64")
+        a_info = graph.value_info.get(candidate.inputs[0])
+        if a_info is None:
+            return self.no_match("type of A unknown")
+        if a_info[0] != FLOAT16:
+            return self.no_match("A is not FLOAT16")
+        return MatchResult([dp, tr, candidate])
+
+    def apply(self, graph: Graph, nodes: Sequence[Node]) -> List[Node]:
+        dp, _, matmul = nodes
+        return [Node(PACKED_FUSED_OP, [matmul.inputs[0], dp.inputs[0]], list(matmul.outputs), FUSED_DOMAIN,
+                     {"format": dp.attrs["format"], "shape": [int(d) for d in dp.attrs["shape"]]},
+                     matmul.name or dp.name)]
+
+
 # ---- registry --------------------------------------------------------------
 
 _REGISTRY: Dict[str, tuple] = {}
@@ -249,6 +306,7 @@ def create_registered_patterns(device: Optional[str] = None) -> List[PatternOpti
 
 
 register_pattern("DequantizeLinearMatMulGpu", DequantizeLinearMatMulPattern, enabled_by_default=False)
+register_pattern("DequantizePackedMatMulGpu", DequantizePackedMatMulPattern, enabled_by_default=False)
 
 
 def optimize(graph: Graph, patterns: Sequence[PatternOptimization]) -> int:

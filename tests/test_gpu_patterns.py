@@ -35,3 +35,28 @@ def test_rewritten_graph_runs_fused_kernel(olamd, oracle, dev, dt):
     y = kernel(*[feeds[i] for i in node.inputs], **node.attrs)
     ref, mag = _chain_ref(oracle, a, x, oracle.INT8, K, N, sc, s16, zp, 1, "bf16", dt)
     assert_close(tensor_bits(y), ref, mag, dt, oracle, f"pattern {dt}")
+
+
+@pytest.mark.parametrize("fmt,bpb", [("gguf:q4_0", 18), ("gguf:q8_0", 34)])
+def test_rewritten_packed_graph_runs_fused_kernel(olamd, oracle, dev, fmt, bpb):
+    """DequantizePacked -> Transpose -> MatMul rewritten into the fused node,
+    run through the kernel table, against the oracle chain."""
+    from test_gpu_packed import _block_weight
+    pt = importlib.import_module("onnx_light_amd.patterns")
+    M, N, K = 3, 200, 256
+    rng = np.random.default_rng(len(fmt) + bpb)
+    x = _block_weight(rng, N, K, bpb)
+    a = np.float16(rng.standard_normal((M, K)))
+    Nd = pt.Node
+    g = pt.Graph([Nd("DequantizePacked", ["X"], ["Wd"], attrs={"format": fmt, "shape": [N, K], "output_dtype": 10}),
+                  Nd("Transpose", ["Wd"], ["Wt"], attrs={"perm": [1, 0]}), Nd("MatMul", ["A", "Wt"], ["Y"])],
+                 {"X"}, ["A"], ["Y"], {"A": (pt.FLOAT16, (M, K))})
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizePackedMatMulGpu")]) == 1
+    (node,) = g.nodes
+    feeds = {"A": T(a, dev), "X": T(x, dev)}
+    kernel = olamd.KERNELS[f"{node.domain}:{node.op_type}"]()
+    y = kernel(*[feeds[i] for i in node.inputs], **node.attrs)
+    w_bits = oracle.dequantize_packed(x, fmt, (N, K), 10)
+    ref = oracle.matmul_half(a.view(np.uint16), np.ascontiguousarray(w_bits.T), 10)
+    mag = np.abs(a.astype(np.float64)) @ np.abs(oracle.f16_bits_to_f32(w_bits).astype(np.float64)).T
+    assert_close(tensor_bits(y), ref, mag, "f16", oracle, f"packed pattern {fmt}")

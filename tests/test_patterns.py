@@ -155,3 +155,57 @@ def test_registry(pt):
         pt.register_pattern("DequantizeLinearMatMulGpu", pt.DequantizeLinearMatMulPattern)
     with pytest.raises(ValueError):
         pt.register_pattern("", pt.DequantizeLinearMatMulPattern)
+
+
+# ---- DequantizePacked -> Transpose -> MatMul --------------------------------
+
+def _packed_graph(pt, fmt="gguf:q4_0", shape=(96, 128), odt=None, perm=None, a_type=None, extra=None,
+                  const=True):
+    N = pt.Node
+    dattrs = {"format": fmt, "shape": list(shape), "output_dtype": pt.FLOAT16 if odt is None else odt}
+    tattrs = {} if perm is None else {"perm": perm}
+    nodes = [N("DequantizePacked", ["X"], ["Wd"], attrs=dattrs), N("Transpose", ["Wd"], ["Wt"], attrs=tattrs),
+             N("MatMul", ["A", "Wt"], ["Y"])] + (extra or [])
+    info = {"A": (pt.FLOAT16 if a_type is None else a_type, (4, shape[1]))}
+    return pt.Graph(nodes, {"X"} if const else set(), ["A"] + ([] if const else ["X"]), ["Y"], info)
+
+
+def test_packed_rewrite(pt):
+    g = _packed_graph(pt)
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizePackedMatMulGpu")]) == 1
+    (node,) = g.nodes
+    assert (node.domain, node.op_type) == (pt.FUSED_DOMAIN, pt.PACKED_FUSED_OP)
+    assert node.inputs == ["A", "X"] and node.outputs == ["Y"]
+    assert node.attrs == {"format": "gguf:q4_0", "shape": [96, 128]}
+
+
+@pytest.mark.parametrize("kw,reason", [
+    ({"fmt": "gguf:q4_k"}, "format has no fused kernel"),
+    ({"shape": (96, 96)}, "K is not a multiple of 64"),
+    ({"shape": (2, 96, 128)}, "DequantizePacked shape is not [N, K]"),
+    ({"odt": 1}, "DequantizePacked output is not FLOAT16"),
+    ({"perm": [0, 1]}, "Transpose is not a 2-D transpose"),
+    ({"a_type": 16}, "A is not FLOAT16"),
+    ({"const": False}, "packed weight is not an initializer"),
+])
+def test_packed_no_match(pt, kw, reason):
+    g = _packed_graph(pt, **kw)
+    pat = pt.create_registered_pattern("DequantizePackedMatMulGpu")
+    m = pat.match(g, g.nodes[2])
+    assert not m and m.reason == reason
+    assert pt.optimize(g, [pat]) == 0
+
+
+def test_packed_shared_intermediate_is_left_alone(pt):
+    N = pt.Node
+    g = _packed_graph(pt, extra=[N("Relu", ["Wt"], ["R"])])
+    m = pt.create_registered_pattern("DequantizePackedMatMulGpu").match(g, g.nodes[2])
+    assert not m and m.reason == "Transpose output has another consumer"
+    g = _packed_graph(pt, extra=[N("Relu", ["Wd"], ["R"])])
+    m = pt.create_registered_pattern("DequantizePackedMatMulGpu").match(g, g.nodes[2])
+    assert not m and m.reason == "DequantizePacked output has another consumer"
+
+
+def test_packed_registry(pt):
+    assert "DequantizePackedMatMulGpu" in pt.registered_pattern_names()
+    assert "DequantizePackedMatMulGpu" not in pt.registered_pattern_names(include_opt_in=False)
