@@ -12,7 +12,8 @@
 // What it does:
 //  - one KernelBase subclass per operator of the quantized-matmul path
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
-//    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked)
+//    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
+//    GroupedMatMul)
 //    and for the two fused nodes the GPU patterns produce
 //    (ai.rt.amd:DequantizeLinearMatMul, ai.rt.amd:DequantizePackedMatMul),
 //    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
@@ -554,6 +555,40 @@ protected:
   std::vector<int> ConstantInputs() const override { return {0}; }
 };
 
+// GroupedMatMul (math/kernel_grouped_matmul.cc:105-114): input [M, K],
+// weights [G, K, N] (or [G, N, K] with transB), group_indices [M, S],
+// optional bias [G, N] -> [M, S, N].  FLOAT16 / BFLOAT16 on the GPU, FLOAT and
+// DOUBLE on the built-in kernel.  Host indices are range-checked by the
+// library before any work, with the reference's message.
+class Mi355xGroupedMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.onnx:GroupedMatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 3);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor x = In(0, ctx), w = In(1, ctx), idx = In(2, ctx), b = In(3, ctx);
+    const int64_t transB = rt::GetAttributeIntOrDefault(node, "transB", 0);
+    if (x.data_type != kFloat16 && x.data_type != kBfloat16) {
+      RunBuiltin(ctx, "dtype other than FLOAT16 / BFLOAT16");
+      return;
+    }
+    if (x.rank != 2 || w.rank != 3 || idx.rank != 2) {  // the library raises the reference's error
+      onnxl_amd_tensor none{};
+      Check(onnxl_amd_grouped_matmul(&x, &w, &idx, &b, transB, &none, nullptr));
+    }
+    const rt::Shape shape{x.dims[0], idx.dims[1], w.dims[transB != 0 ? 1 : 2]};
+    rt::Tensor y = ctx.MakeOutputTensor(0, x.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    if (Call(onnxl_amd_grouped_matmul(&x, &w, &idx, &b, transB, &dy, nullptr), ctx))
+      rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 3}; }
+};
+
 // ---------------------------------------------------------------------------
 // Fused nodes.  They exist only in graphs rewritten by the GPU patterns, so
 // there is no built-in kernel: the adapter computes their chain itself when
@@ -754,6 +789,7 @@ const char *RegisterMi355xKernelFunctions(int device_ordinal = 0) {
     Register<Mi355xConvInteger>("", "ConvInteger");
     Register<Mi355xQLinearConv>("", "QLinearConv");
     Register<Mi355xDequantizePacked>("", "DequantizePacked");
+    Register<Mi355xGroupedMatMul>("", "GroupedMatMul");
     Register<Mi355xDequantizeLinearMatMul>(kFusedDomain, "DequantizeLinearMatMul");
     Register<Mi355xDequantizePackedMatMul>(kFusedDomain, "DequantizePackedMatMul");
   });

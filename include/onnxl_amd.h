@@ -226,6 +226,23 @@ int onnxl_amd_qlinear_conv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_
 int onnxl_amd_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tensor *y,
                      void *stream);
 
+/* GroupedMatMul (onnx-light opset 29, the MoE expert contraction):
+ * y[m, s, :] = input[m, :] @ W[g] (+ bias[g, :]), g = group_indices[m, s],
+ * W[g] = weights[g] ([G, K, N]) or its transpose when transB != 0 (weights
+ * [G, N, K]).  input, weights, bias and y FLOAT16 or BFLOAT16 (fp32 sums over
+ * exact products; with a bias the sum is rounded to the dtype, the bias
+ * added, the result rounded again, as MatMul followed by Add); group_indices
+ * INT32 or INT64 [M, S]; y [M, S, N].  FLOAT and DOUBLE inputs, which the
+ * reference also takes, return ONNXL_AMD_UNSUPPORTED, as do more than 4096
+ * groups.  A group index outside [0, G) is an INVALID_ARGUMENT when the
+ * indices are host memory; with device-resident indices the call cannot see
+ * them before the work runs, and such a pair's row of y is NaN instead.
+ * Replaces kernel::GroupedMatMul::operator(),
+ * math/kernel_grouped_matmul.cc:48-103. */
+int onnxl_amd_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights,
+                             const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
+                             onnxl_amd_tensor *y, void *stream);
+
 /* Cast FLOAT -> FLOAT16 / BFLOAT16 (round-to-nearest-even), the Cast step
  * between DequantizeLinear and a bf16 MatMul.
  * Replaces the FLOAT->BFLOAT16 / FLOAT16 branch of the reference Cast kernel,

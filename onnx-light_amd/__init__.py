@@ -85,6 +85,7 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dequantize_linear.argtypes = [TP, TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
         L.onnxl_amd_matmul.argtypes = [TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
+        L.onnxl_amd_grouped_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -155,7 +156,7 @@ def _torch_code(dt):
 
 _NP_CODES = {np.dtype(np.float32): FLOAT, np.dtype(np.uint8): UINT8, np.dtype(np.int8): INT8,
              np.dtype(np.uint16): UINT16, np.dtype(np.int16): INT16, np.dtype(np.int32): INT32,
-             np.dtype(np.int64): INT64, np.dtype(np.float16): FLOAT16}
+             np.dtype(np.int64): INT64, np.dtype(np.float16): FLOAT16, np.dtype(np.float64): DOUBLE}
 
 
 def describe(t, dtype: int | None = None, shape=None) -> Tensor:
@@ -353,6 +354,27 @@ def matmul(a, b, out=None):
     if out is None:
         out = _empty(matmul_shape(_shape_of(a), _shape_of(b)), a.dtype, _device_of(a, b))
     _check(lib().onnxl_amd_matmul(describe(a), describe(b), describe(out), _stream_of(a, b, out)))
+    return out
+
+
+def grouped_matmul(input, weights, group_indices, bias=None, transB: int = 0, out=None, check: bool = True):
+    """kernel::GroupedMatMul (math/kernel_grouped_matmul.cc:48-103) for FLOAT16
+    / BFLOAT16: out[m, s] = input[m] @ W[group_indices[m, s]] (+ bias).  With
+    device-resident indices and ``check``, an index outside [0, G) raises
+    InvalidArgument before the launch, as the reference does (one
+    synchronisation); without ``check`` such a pair's row comes out NaN."""
+    torch = _torch()
+    M, S = (int(d) for d in _shape_of(group_indices))
+    G = int(_shape_of(weights)[0])
+    N = int(_shape_of(weights)[1 if transB else 2])
+    if check and isinstance(group_indices, torch.Tensor) and group_indices.is_cuda and group_indices.numel():
+        if bool(((group_indices < 0) | (group_indices >= G)).any()):
+            raise InvalidArgument("kernel::GroupedMatMul group index must be in [0,G).")
+    if out is None:
+        out = _empty((M, S, N), input.dtype, _device_of(input, weights))
+    _check(lib().onnxl_amd_grouped_matmul(describe(input), describe(weights), describe(group_indices),
+                                          describe(bias), int(transB), describe(out),
+                                          _stream_of(input, weights, group_indices, out)))
     return out
 
 
@@ -618,6 +640,15 @@ class DequantizePackedMatMul:
         return dequantize_packed_matmul(a, x, format, shape, out)
 
 
+class GroupedMatMul:
+    """Kernel-class mirror of kernel::GroupedMatMul (transB defaults to 0 as
+    in GroupedMatMul::Run, math/kernel_grouped_matmul.cc:105-114)."""
+    name = "onnxl_amd:GPU:ai.onnx:GroupedMatMul"
+
+    def __call__(self, input, weights, group_indices, bias=None, transB=0, out=None):
+        return grouped_matmul(input, weights, group_indices, bias, transB, out)
+
+
 # Dispatch keys "<domain>:<op_type>" as the reference table uses them
 # (core/runtime/kernels/kernel_dispatch_table.h:148-164).
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
@@ -626,6 +657,7 @@ KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLin
            "ai.onnx:DynamicQuantizeLinear": DynamicQuantizeLinear,
            "ai.onnx:ConvInteger": ConvInteger, "ai.onnx:QLinearConv": QLinearConv,
            "ai.onnx:DequantizePacked": DequantizePacked,
+           "ai.onnx:GroupedMatMul": GroupedMatMul,
            "ai.rt.amd:DequantizeLinearMatMul": DequantizeLinearMatMul,
            "ai.rt.amd:DequantizePackedMatMul": DequantizePackedMatMul}
 

@@ -1346,6 +1346,90 @@ int DqMatMulNoAlloc(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const 
   return ONNXL_AMD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// GroupedMatMul.  Validation and messages of GroupedMatMul::operator()
+// (math/kernel_grouped_matmul.cc:50-90).
+
+constexpr const char *kGmmName = "kernel::GroupedMatMul";
+constexpr int64_t kGmmMaxGroups = 4096;  // routing counters in LDS
+
+int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights,
+                  const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
+                  onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(input) && !Absent(weights) && !Absent(group_indices) && y, kGmmName,
+              ": input, weights, group_indices and the output are required.");
+  CheckDescriptor(input, "input");
+  CheckDescriptor(weights, "weights");
+  CheckDescriptor(group_indices, "group_indices");
+  CheckDescriptor(bias, "bias");
+  CheckDescriptor(y, "output");
+  const bool tb = transB != 0;
+  OLA_ENFORCE(input->rank == 2 && weights->rank == 3 && group_indices->rank == 2, kGmmName,
+              " expects input rank 2, weights rank 3, and indices rank 2.");
+  const int64_t M = input->dims[0], K = input->dims[1], G = weights->dims[0];
+  const int64_t N = weights->dims[tb ? 1 : 2], S = group_indices->dims[1];
+  OLA_ENFORCE(K == weights->dims[tb ? 2 : 1] && M == group_indices->dims[0], kGmmName,
+              " incompatible input dimensions.");
+  const int32_t dt = input->data_type;
+  OLA_ENFORCE(dt == kFloat || dt == kDouble || dt == kFloat16 || dt == kBfloat16, kGmmName,
+              " expects floating-point inputs.");
+  OLA_ENFORCE(weights->data_type == dt, kGmmName, " weights must match the input dtype.");
+  OLA_ENFORCE(group_indices->data_type == kInt32 || group_indices->data_type == kInt64, kGmmName,
+              " indices must be INT32 or INT64.");
+  for (const onnxl_amd_tensor *t : {input, weights, group_indices})
+    OLA_ENFORCE(t->size_bytes == PackedBytes(t->data_type, NumElements(*t)), kGmmName,
+                " tensor payload does not match its shape.");
+  const bool has_bias = !Absent(bias);
+  if (has_bias) {
+    OLA_ENFORCE(bias->data_type == dt && bias->rank == 2 && bias->dims[0] == G && bias->dims[1] == N, kGmmName,
+                " bias must have shape [G,N] and match the input dtype.");
+    OLA_ENFORCE(bias->size_bytes == PackedBytes(dt, G * N), kGmmName, " tensor payload does not match its shape.");
+  }
+  const int64_t P = M * S;
+  if (group_indices->location == ONNXL_AMD_HOST) {
+    // host indices: the reference's range check before any work
+    const bool i64 = group_indices->data_type == kInt64;
+    for (int64_t i = 0; i < P; ++i) {
+      const int64_t g = i64 ? static_cast<const int64_t *>(group_indices->data)[i]
+                            : static_cast<const int32_t *>(group_indices->data)[i];
+      OLA_ENFORCE(g >= 0 && g < G, kGmmName, " group index must be in [0,G).");
+    }
+  }
+  OLA_ENFORCE(y->data_type == dt && y->rank == 3 && y->dims[0] == M && y->dims[1] == S && y->dims[2] == N, kGmmName,
+              ": the output must be [M, S, N] of the input dtype.");
+  OLA_ENFORCE(y->size_bytes == PackedBytes(dt, P * N), kGmmName, ": output buffer size does not match its shape.");
+  if (dt != kFloat16 && dt != kBfloat16) throw Unsupported("GroupedMatMul: only FLOAT16 / BFLOAT16 run on the GPU path");
+  if (G > kGmmMaxGroups) throw Unsupported(Cat("GroupedMatMul: more than ", kGmmMaxGroups, " groups"));
+  OLA_ENFORCE(P < (int64_t(1) << 31) - 1, kGmmName, ": more than 2^31 (token, selection) pairs");
+  if (P == 0 || N == 0) return ONNXL_AMD_OK;
+  Ctx();
+  const size_t ws = (size_t)(2 * (G + 1) + P) * sizeof(int32_t);
+  Staging st(stream, ws, {input, weights, group_indices, has_bias ? bias : nullptr}, {y});
+  GroupedParams p{};
+  p.A = st.In(input);
+  p.W = st.In(weights);
+  p.idx = st.In(group_indices);
+  p.bias = has_bias ? st.In(bias) : nullptr;
+  p.Y = st.Out(y);
+  p.M = M;
+  p.K = K;
+  p.N = N;
+  p.G = G;
+  p.S = S;
+  p.idx64 = group_indices->data_type == kInt64;
+  p.transB = tb;
+  p.bf16 = dt == kBfloat16;
+  p.nbn = (N + 127) / 128;
+  int32_t *w32 = static_cast<int32_t *>(st.Extra());
+  p.row_off = w32;
+  p.tile_off = w32 + (G + 1);
+  p.rows = w32 + 2 * (G + 1);
+  LaunchGroupedMatMul(p, stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
 // Validation runs before any device work, so argument errors are reported
 // even before onnxl_amd_init (the first device access then raises
 // NotInitialized).
@@ -1542,6 +1626,14 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
 int onnxl_amd_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b, onnxl_amd_tensor *y,
                      void *stream) {
   return Guard([&] { return MatMul(a, b, y, static_cast<hipStream_t>(stream)); });
+}
+
+int onnxl_amd_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights,
+                             const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
+                             onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return GroupedMatMul(input, weights, group_indices, bias, transB, y, static_cast<hipStream_t>(stream));
+  });
 }
 
 int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, void *stream) {

@@ -229,4 +229,21 @@ struct HMatMulParams {
 };
 void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// GroupedMatMul (grouped.hip): Y[m, s, :] = A[m, :] @ W[idx[m, s]] (+ bias).
+struct GroupedParams {
+  const void *A;     // [M, K] FLOAT16 / BFLOAT16
+  const void *W;     // [G, K, N], or [G, N, K] with transB
+  const void *idx;   // [M, S] INT32 / INT64
+  const void *bias;  // [G, N] or nullptr
+  void *Y;           // [M, S, N]
+  int64_t M, K, N, G, S;
+  int idx64, transB, bf16;
+  int64_t nbn;       // column tiles of the GEMM core: ceil(N / 128)
+  // device workspace: G + 1, G + 1 and M * S int32
+  int32_t *row_off, *tile_off, *rows;
+};
+int64_t GroupedMaxTiles(const GroupedParams &p);
+void LaunchGroupedMatMul(const GroupedParams &p, hipStream_t stream);
+
 }  // namespace onnxl_amd

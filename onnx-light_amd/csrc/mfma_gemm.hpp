@@ -181,11 +181,28 @@ struct GemmArgs {
   int row_wscale_per;
   float row_xs, row_ys;
   const int32_t *row_bias;
+  // Grouped mode (GroupedMatMul; kernels with GM != 0): the rows of A are
+  // gathered and the rows of Y scattered through a routing table written on
+  // the device, and each group of rows multiplies its own B.  M is then the
+  // number of rows of A and Y has M * grp_sel rows.
+  const int32_t *grp_tile_off;  // [grp_count + 1] first workgroup tile of each group
+  const int32_t *grp_row_off;   // [grp_count + 1] first routed row of each group
+  const int32_t *grp_rows;      // routed row -> row of Y (token * grp_sel + selection)
+  int grp_count;
+  int grp_sel;                  // row of A of Y row r: r / grp_sel
+  int64_t grp_b_stride;         // elements from one group's B to the next
+  const void *grp_bias;         // [grp_count, N] in the output dtype, or null
 };
 
-template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB>
+// GM: 0 one GEMM per batch entry; 1 grouped with each group's B [K, N]
+// row-major; 2 grouped with each group's B given transposed, [N, K]
+// row-major (kH16 only): its stage is then loaded and read like A's, rows of
+// N with consecutive k, which is exactly the B operand of the MFMA.
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB, int GM = 0>
 __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) {
   constexpr bool RA = ZP, CB = ZP;
+  constexpr bool BT = GM == 2;
+  static_assert(GM == 0 || (KIND == kH16 && WB == 2 && !ZP), "grouped mode: 16-bit operands, 128-column tiles");
   using T = Traits<KIND>;
   using Acc = typename T::Acc;
   constexpr int kBN = 64 * WB;                 // workgroup tile columns
@@ -218,24 +235,52 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 
   // ---- tile selection: each XCD owns a contiguous run of tiles, grouped
   // kGroupM tile-rows high, so tiles sharing A rows / B columns share an L2 ----
-  const int64_t nbm = (M + kBM - 1) / kBM, nbn = (N + kBN - 1) / kBN;
-  const int64_t tiles = nbm * nbn;
-  const int64_t total = tiles * p.batch;
-  const int64_t pid = blockIdx.x;
-  const int64_t xcd = pid % kXcds, per = total / kXcds, extra = total % kXcds;
-  const int64_t t_all = xcd * per + MinI64(xcd, extra) + pid / kXcds;
-  const int64_t bt = t_all / tiles, tt = t_all % tiles;
-  const int64_t group = tt / (kGroupM * nbn);
-  const int64_t first_m = group * kGroupM;
-  const int64_t gsize = MinI64(nbm - first_m, kGroupM);
-  const int64_t tm = first_m + (tt % (kGroupM * nbn)) % gsize;
-  const int64_t tn = (tt % (kGroupM * nbn)) / gsize;
-  const int64_t row0 = tm * kBM, col0 = tn * kBN;
+  const int64_t nbn = (N + kBN - 1) / kBN;
+  int64_t bt = 0, row0, col0;
+  // grouped mode: this tile's group, its routed rows [rbase, rbase + rcount)
+  int grp = 0;
+  int64_t rbase = 0, rcount = M;
+  if constexpr (GM != 0) {
+    // tile t of group g, g with grp_tile_off[g] <= t < grp_tile_off[g + 1]
+    // (a non-empty group); tiles past the last one leave at once, before any
+    // load or barrier (the whole workgroup takes the same branch)
+    const int t = (int)blockIdx.x;
+    if (t >= p.grp_tile_off[p.grp_count]) return;
+    int lo = 0, hi = p.grp_count;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.grp_tile_off[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    grp = lo;
+    const int local = t - p.grp_tile_off[grp];
+    rbase = p.grp_row_off[grp];
+    rcount = p.grp_row_off[grp + 1] - rbase;
+    row0 = (int64_t)(local / nbn) * kBM;
+    col0 = (int64_t)(local % nbn) * kBN;
+  } else {
+    const int64_t nbm = (M + kBM - 1) / kBM;
+    const int64_t tiles = nbm * nbn;
+    const int64_t total = tiles * p.batch;
+    const int64_t pid = blockIdx.x;
+    const int64_t xcd = pid % kXcds, per = total / kXcds, extra = total % kXcds;
+    const int64_t t_all = xcd * per + MinI64(xcd, extra) + pid / kXcds;
+    bt = t_all / tiles;
+    const int64_t tt = t_all % tiles;
+    const int64_t group = tt / (kGroupM * nbn);
+    const int64_t first_m = group * kGroupM;
+    const int64_t gsize = MinI64(nbm - first_m, kGroupM);
+    const int64_t tm = first_m + (tt % (kGroupM * nbn)) % gsize;
+    const int64_t tn = (tt % (kGroupM * nbn)) / gsize;
+    row0 = tm * kBM;
+    col0 = tn * kBN;
+  }
 
   constexpr int kAsz = KIND == kI8 ? 1 : 2;
   constexpr int kBsz = KIND == kH16 ? 2 : 1;
-  int64_t a_off, b_off;
-  BatchOffsets(p.bm, bt, a_off, b_off);
+  int64_t a_off = 0, b_off = 0;
+  if constexpr (GM != 0) b_off = grp * p.grp_b_stride;
+  else BatchOffsets(p.bm, bt, a_off, b_off);
   const char *Ab = static_cast<const char *>(p.A) + a_off * kAsz;
   const char *Bb = static_cast<const char *>(p.B) + b_off * kBsz;
   const int64_t KA = K * kAsz;   // A row pitch in bytes
@@ -244,13 +289,14 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const __amdgpu_buffer_rsrc_t rsA =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(K * NB), kRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(BT ? N * KA : K * NB), kRsrcWord3);
   // look-ahead loads past the last K step go through empty descriptors (every
   // access out of range): a scalar select instead of a per-lane one
   const __amdgpu_buffer_rsrc_t rsA0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, 0, kRsrcWord3);
+  const int64_t YR = GM != 0 ? M * p.grp_sel : M;  // rows of Y
   const __amdgpu_buffer_rsrc_t rsY = __builtin_amdgcn_make_buffer_rsrc(
-      static_cast<char *>(p.Y) + bt * M * LDY * kOsz, (short)0, (int)(M * LDY * kOsz), kRsrcWord3);
+      static_cast<char *>(p.Y) + bt * M * LDY * kOsz, (short)0, (int)(YR * LDY * kOsz), kRsrcWord3);
   const int nfull = (int)(K / T::kKStep);                  // full K steps
   const bool half = K % T::kKStep != 0;                     // K % kKStep == kKStep / 2
   const int nk = nfull + (half ? 1 : 0);                    // K steps to load
@@ -260,14 +306,20 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int64_t row = row0 + 8 * (8 * wave + q) + (lane >> 3);  // 8-row block 8 * wave + q
-    a_g[q] = row < M ? (unsigned)(row * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (q & 1))) : kOob;
+    int64_t src = row;  // row of A
+    if constexpr (GM != 0) src = row < rcount ? p.grp_rows[rbase + row] / p.grp_sel : 0;
+    a_g[q] = row < rcount ? (unsigned)(src * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (q & 1))) : kOob;
   }
   unsigned b_g[4];  // LB <= 4 (a fixed bound: a template-dependent size here
                     // makes the host compiler drop the kernel stub)
 #pragma unroll
   for (int q = 0; q < LB; ++q) {
     const int i = wave * LB + q;  // 1 KB piece of the B stage
-    if constexpr (KIND == kH16) {
+    if constexpr (BT) {
+      // rows of N like A's rows of M: 8 rows of 128 bytes per piece
+      const int64_t n = col0 + 8 * i + (lane >> 3);
+      b_g[q] = n < N ? (unsigned)(n * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (i & 1))) : kOob;
+    } else if constexpr (KIND == kH16) {
       const int krow = 4 * i + (lane >> 4);
       const int64_t cb = 2 * col0 + 16 * ((lane & 15) ^ (2 * ((lane >> 4) & 3)));
       b_g[q] = cb < NW ? (unsigned)(krow * NB + cb) : kOob;
@@ -294,7 +346,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   int b_rd[WB];
 #pragma unroll
   for (int j = 0; j < WB; ++j) {
-    if constexpr (KIND == kI8) {
+    if constexpr (BT) {
+      b_rd[j] = 0;  // bt_rd below
+    } else if constexpr (KIND == kI8) {
       const int krow = 16 * (g16 >> 1) + (s16 >> 1);
       const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
       b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
@@ -308,6 +362,12 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       b_rd[j] = krow * kBP + 16 * ((col >> 3) ^ (2 * (krow & 3))) + ((2 * col) & 15);
     }
   }
+  // BT: sub-step kk reads chunk 2 kk + lg of B row (column of Y)
+  // wn * kWN + 32 j + lr, block j 4096 bytes after block j - 1 (as for A)
+  int bt_rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    bt_rd[kk] = BT ? (wn * kWN + lr) * 128 + 16 * ((2 * kk + lg) ^ (lr & 7) ^ ((lr >> 3) & 1)) : 0;
   // B rows per sub-step: 32 (int8) or 16 (16-bit k values)
   constexpr int kSubRows = KIND == kI8 ? 32 : 16;
 
@@ -333,7 +393,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   auto issue = [&](int step, int stage, int part) __attribute__((always_inline)) {
     const bool live = step < nk;
     const unsigned ka = (unsigned)step * kStepBytes;
-    const unsigned kb = (unsigned)((int64_t)step * T::kBRows * NB);
+    const unsigned kb = BT ? (unsigned)step * kStepBytes : (unsigned)((int64_t)step * T::kBRows * NB);
     char *sa = SA(stage);
     char *sb = SB(stage);
     const __amdgpu_buffer_rsrc_t rsa = live ? rsA : rsA0, rsb = live ? rsB : rsB0;
@@ -360,7 +420,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
       const char *base = sb + kk * kSubRows * kBP;
-      if constexpr (KIND == kI8) {
+      if constexpr (BT) {
+        rb[buf][j] = *reinterpret_cast<const v4i *>(sb + bt_rd[kk] + j * 4096);
+      } else if constexpr (KIND == kI8) {
         const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j]));
         const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)(base + b_rd[j] + 8 * kBP));
         rb[buf][j] = v4i{lo.x, lo.y, hi.x, hi.y};
@@ -675,6 +737,24 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const float q_bias = p.y_signed ? 128.f : 0.f;
   const float q_zy = p.zy + q_bias, q_lo = p.qmin + q_bias, q_hi = p.qmax + q_bias;
   const unsigned q_flip = p.y_signed ? 0x80808080u : 0u;
+  // Grouped mode with a bias: the bias of this lane's columns (4 per
+  // (j, g) register group, the output dtype's bits).  GroupedMatMul adds it
+  // as MatMul followed by Add does: the sum rounded to the output dtype, the
+  // bias added in fp32, rounded again.
+  v2i gbias[GM != 0 ? WB : 1][4];
+  const bool has_gbias = GM != 0 && p.grp_bias != nullptr;
+  if constexpr (GM != 0) {
+    const __amdgpu_buffer_rsrc_t rsBias = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(p.grp_bias), (short)0, has_gbias ? (int)(p.grp_count * N * kOsz) : 0, kRsrcWord3);
+#pragma unroll
+    for (int j = 0; j < WB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = col0 + wn * kWN + j * 32 + g * 8 + lg * 4;
+        gbias[j][g] = __builtin_amdgcn_raw_buffer_load_b64(
+            rsBias, col < N ? (unsigned)((grp * N + col) * kOsz) : kOob, 0, 0);
+      }
+  }
   // Epilogue of 32-row block i (use24: the 24-bit zero-point products).
   auto epi = [&](int i, auto use24) __attribute__((always_inline)) {
     int32_t ra_r = 0, al_r = 0;
@@ -742,6 +822,23 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
             for (int e = 0; e < 4; ++e) a[4 * g + e] *= sc4[e];
           }
+          if constexpr (GM != 0) {
+            if (has_gbias) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const unsigned bb = ((unsigned)gbias[j][g][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                float r, bv;
+                if constexpr (OUT == kOutBf16) {
+                  r = __builtin_bit_cast(float, (PackBf16(a[4 * g + e], 0.f) & 0xffffu) << 16);
+                  bv = __builtin_bit_cast(float, bb << 16);
+                } else {
+                  r = (float)(_Float16)a[4 * g + e];
+                  bv = (float)__builtin_bit_cast(_Float16, (unsigned short)bb);
+                }
+                a[4 * g + e] = r + bv;
+              }
+            }
+          }
           if constexpr (OUT == kOutBf16) {
             *reinterpret_cast<v2i *>(dst) = v2i{(int)PackBf16(a[4 * g], a[4 * g + 1]),
                                                 (int)PackBf16(a[4 * g + 2], a[4 * g + 3])};
@@ -764,6 +861,17 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     const int64_t brow = row0 + wm * 128 + i * 32;
     const int64_t ncol = N - (col0 + wn * kWN);
     const unsigned ybase = (unsigned)((brow * LDY + col0 + wn * kWN) * kOsz);
+    // grouped mode: each staged row goes to its own row of Y
+    unsigned grow[WB * kOsz];
+#pragma unroll
+    for (int c = 0; c < WB * kOsz; ++c) {
+      grow[c] = 0;
+      if constexpr (GM != 0) {
+        const int rr = (c * 64 + lane) / kChunksPerRow;
+        if (brow + rr < rcount)
+          grow[c] = (unsigned)(((int64_t)p.grp_rows[rbase + brow + rr] * LDY + col0 + wn * kWN) * kOsz);
+      }
+    }
     v4i piece[WB * kOsz];
 #pragma unroll
     for (int c = 0; c < WB * kOsz; ++c) {
@@ -775,9 +883,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     for (int c = 0; c < WB * kOsz; ++c) {
       const int id = c * 64 + lane;
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
-      const bool ok = brow + rr < M && cc * (16 / kOsz) < ncol;
-      __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY,
-                                             ok ? ybase + (unsigned)(rr * LDY * kOsz + cc * 16) : kOob, 0, kStoreThrough);
+      const bool ok = brow + rr < rcount && cc * (16 / kOsz) < ncol;
+      const unsigned at = GM != 0 ? grow[c] + (unsigned)(cc * 16) : ybase + (unsigned)(rr * LDY * kOsz + cc * 16);
+      __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY, ok ? at : kOob, 0, kStoreThrough);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -813,6 +921,13 @@ inline void Launch(const GemmArgs &p, hipStream_t s) {
   const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
   hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8, WB>), dim3((unsigned)tiles), dim3(kThreads),
                      0, s, p);
+}
+
+// Grouped launch: `max_tiles` workgroups, an upper bound of the tiles the
+// routing table holds (the rest leave at once).
+template <int OUT, int GM> inline void LaunchGrouped(const GemmArgs &p, int64_t max_tiles, hipStream_t s) {
+  hipLaunchKernelGGL((MfmaGemmKernel<kH16, OUT, false, false, false, 2, GM>), dim3((unsigned)max_tiles),
+                     dim3(kThreads), 0, s, p);
 }
 
 }  // namespace mg

@@ -931,3 +931,61 @@ int orc_matmul_half(const uint16_t *a, const int64_t *a_shape, int a_rank, const
   free(yf);
   return 0;
 }
+
+/* GroupedMatMul (math/kernel_grouped_matmul.cc:22-46, validation :50-90):
+ * y[i, :] for pair i = m * S + s is x[m, :] @ W[g], g = idx[i], W[g] the
+ * [K, N] slice of w (transB == 0) or the transpose of its [N, K] slice.  The
+ * sum over k runs in order from 0 in the compute type: float for FLOAT,
+ * FLOAT16 and BFLOAT16 (16-bit values decoded exactly), double for DOUBLE.
+ * With a bias the sum is first rounded to the element type, then
+ * bias[g, n] added in the compute type and the result rounded (MatMul
+ * followed by Add).  dtype: 1 FLOAT, 11 DOUBLE, 10 FLOAT16, 16 BFLOAT16; idx
+ * already widened to int64.  Returns 0, 5 for an index outside [0, G), 4
+ * for another dtype. */
+int orc_grouped_matmul(int dtype, const void *x, int64_t M, int64_t K, const void *w, int64_t G, int64_t N,
+                       int transB, const int64_t *idx, int64_t S, const void *bias, void *y) {
+  if (dtype != ORC_FLOAT && dtype != 11 && dtype != ORC_FLOAT16 && dtype != ORC_BFLOAT16) return 4;
+  for (int64_t i = 0; i < M * S; ++i)
+    if (idx[i] < 0 || idx[i] >= G) return 5;
+  for (int64_t i = 0; i < M * S; ++i) {
+    const int64_t g = idx[i], m = i / S;
+    for (int64_t n = 0; n < N; ++n) {
+      if (dtype == 11) {
+        const double *xd = (const double *)x, *wd = (const double *)w, *bd = (const double *)bias;
+        double v = 0.0;
+        for (int64_t l = 0; l < K; ++l)
+          v += xd[m * K + l] * wd[transB ? (g * N + n) * K + l : (g * K + l) * N + n];
+        if (bd) v = v + bd[g * N + n];
+        ((double *)y)[i * N + n] = v;
+        continue;
+      }
+      float v = 0.f;
+      for (int64_t l = 0; l < K; ++l) {
+        const int64_t wo = transB ? (g * N + n) * K + l : (g * K + l) * N + n;
+        float a, b;
+        if (dtype == ORC_FLOAT) {
+          a = ((const float *)x)[m * K + l];
+          b = ((const float *)w)[wo];
+        } else if (dtype == ORC_FLOAT16) {
+          a = orc_f16_to_f32(((const uint16_t *)x)[m * K + l]);
+          b = orc_f16_to_f32(((const uint16_t *)w)[wo]);
+        } else {
+          a = orc_bf16_to_f32(((const uint16_t *)x)[m * K + l]);
+          b = orc_bf16_to_f32(((const uint16_t *)w)[wo]);
+        }
+        v += a * b;
+      }
+      if (dtype == ORC_FLOAT) {
+        if (bias) v = v + ((const float *)bias)[g * N + n];
+        ((float *)y)[i * N + n] = v;
+      } else if (dtype == ORC_FLOAT16) {
+        if (bias) v = orc_f16_to_f32(orc_f32_to_f16(v)) + orc_f16_to_f32(((const uint16_t *)bias)[g * N + n]);
+        ((uint16_t *)y)[i * N + n] = orc_f32_to_f16(v);
+      } else {
+        if (bias) v = orc_bf16_to_f32(orc_f32_to_bf16(v)) + orc_bf16_to_f32(((const uint16_t *)bias)[g * N + n]);
+        ((uint16_t *)y)[i * N + n] = orc_f32_to_bf16(v);
+      }
+    }
+  }
+  return 0;
+}

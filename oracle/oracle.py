@@ -104,6 +104,9 @@ def _declare(L):
     L.orc_matmul_f32.restype = ctypes.c_int
     L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int]
+    L.orc_grouped_matmul.restype = ctypes.c_int
+    L.orc_grouped_matmul.argtypes = [ctypes.c_int, P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int64,
+                                     ctypes.c_int64, ctypes.c_int, P, ctypes.c_int64, P, P]
     L.orc_matmul_half.restype = ctypes.c_int
     L.orc_matmul_half.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, P,
                                   ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
@@ -327,6 +330,32 @@ def matmul_half(a_bits: np.ndarray, b_bits: np.ndarray, dtype: int, rows=None,
                                _ptr(_shape(b.shape)), b.ndim, dtype, _ptr(y), r0, r1, nthreads)
     if rc:
         raise ValueError(f"matmul_half error {rc}")
+    return y
+
+
+DOUBLE = 11
+
+
+def grouped_matmul(x: np.ndarray, w: np.ndarray, indices: np.ndarray, bias=None, transB: int = 0,
+                   dtype: int = FLOAT) -> np.ndarray:
+    """GroupedMatMul: x [M, K], w [G, K, N] (or [G, N, K] with transB), indices
+    [M, S] -> y [M, S, N].  FLOAT16 / BFLOAT16 tensors are uint16 bit arrays."""
+    np_t = {FLOAT: np.float32, DOUBLE: np.float64, FLOAT16: np.uint16, BFLOAT16: np.uint16}[dtype]
+    x = np.ascontiguousarray(x, dtype=np_t)
+    w = np.ascontiguousarray(w, dtype=np_t)
+    idx = np.ascontiguousarray(indices, dtype=np.int64)
+    M, K = x.shape
+    G = w.shape[0]
+    N = w.shape[1] if transB else w.shape[2]
+    S = idx.shape[1]
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np_t)
+    y = np.zeros((M, S, N), np_t)
+    rc = lib().orc_grouped_matmul(dtype, _ptr(x), M, K, _ptr(w), G, N, 1 if transB else 0, _ptr(idx), S,
+                                  None if b is None else _ptr(b), _ptr(y))
+    if rc == 5:
+        raise ValueError("group index must be in [0,G)")
+    if rc:
+        raise ValueError(f"grouped_matmul error {rc}")
     return y
 
 

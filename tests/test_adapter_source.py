@@ -19,7 +19,7 @@ REFERENCE = "/root/reference/onnx_light"
 
 OPERATORS = ["MatMulInteger", "QLinearMatMul", "DequantizeLinear", "MatMul", "QuantizeLinear",
              "DynamicQuantizeLinear", "ConvInteger", "QLinearConv", "Cast", "DequantizePacked",
-             "DequantizeLinearMatMul", "DequantizePackedMatMul"]
+             "GroupedMatMul", "DequantizeLinearMatMul", "DequantizePackedMatMul"]
 
 
 def _strip_comments(text):
