@@ -17,22 +17,22 @@ oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
-                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8]
+                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|moe]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
-GGUF q4_0 weight decode (`pk`) and the fused q4_0 / q8_0 GEMVs (`pkgemv`,
-`pkgemv8`) are timed too and reported under `extra` unless --no-extra is
-given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
+GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 GEMVs (`pkgemv`,
+`pkgemv8`) and a Mixtral-shaped MoE GroupedMatMul (`moe`) are timed too and
+reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
 25,604,096 bytes with the same replica rotation (libonnxl_amd_bench.so): the
 rate a kernel that only reads those bytes reaches, beside which the GEMV's
 own rate is read.
 
 HBM-bound lines rotate buffer replicas totalling more than 512 MB, so each
 launch misses the 256 MB Infinity Cache.  `cpu_baseline` (configurations 2,
-3, 4 and 5) times the CPU oracle as the reference runs: MatMulInteger,
+3, 4 and 5, and `moe`) times the CPU oracle as the reference runs: MatMulInteger,
 QLinearMatMul and DequantizeLinear on one core, MatMul and Cast on the
 physical cores of the process's CPU set; it reports `nproc` and the physical
 core count.
@@ -326,6 +326,29 @@ class _StreamCall:
         return _StreamCall(self.lib, self.ptr, self.nbytes, self.sink, ctypes.c_void_p(handle))
 
 
+def make_moe(olamd, dev):
+    """GroupedMatMul, the MoE expert contraction of a Mixtral-8x7B-shaped
+    layer: 4096 tokens x top-2 of 8 experts, hidden 4096 -> 14336, bf16,
+    weights in the [G, N, K] layout (transB = 1).  Routing: two distinct
+    experts per token drawn uniformly (device generator, fixed seed)."""
+    import torch
+    M, S, G, K, N = 4096, 2, 8, 4096, 14336
+    w = Workload()
+    w.name = ("MoE GroupedMatMul bf16[4096,4096] x experts bf16[8,14336,4096] (transB=1), top-2 routing "
+              "-> bf16[4096,2,14336]")
+    w.key, w.unit, w.dtype, w.bound = "moe", "TFLOPS", "bf16 (fp32 accumulate)", "mfma"
+    w.work = 2.0 * M * S * K * N
+    w.nbytes = M * K * 2 + G * N * K * 2 + M * S * 8 + M * S * N * 2
+    g = torch.Generator(device=dev).manual_seed(29)
+    x = (torch.randn((M, K), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    wt = (torch.randn((G, N, K), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    idx = torch.rand((M, G), device=dev, generator=g).argsort(dim=1)[:, :S].contiguous()  # distinct experts
+    y = torch.empty((M, S, N), dtype=torch.bfloat16, device=dev)
+    w.calls = [olamd.prepare("grouped_matmul", x, wt, idx, None, 1, y)]
+    w.inputs = {"x": x, "w": wt, "idx": idx}
+    return w
+
+
 def make_stream(olamd, dev, replicas, nbytes, key, name):
     """A plain read of `nbytes` per launch over `replicas` buffers: the
     streaming ceiling for a bandwidth-bound kernel of that byte count."""
@@ -459,6 +482,26 @@ def cpu_baseline_c5(x):
             "nproc": nproc, "physical_cores": phys}
 
 
+def cpu_baseline_moe(x):
+    """Oracle GroupedMatMul (bf16, in-order fp32 sums, one core as the
+    reference) on the first 4 tokens of the job (8 expert rows), extrapolated
+    per routed row to the 8192 of the job."""
+    orc = _oracle()
+    nproc, phys = cpu_topology()
+    rows = 4
+    xs = x["x"][:rows].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    ws = x["w"].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    idx = x["idx"][:rows].cpu().numpy()
+    t, runs = _median_time(lambda: orc.grouped_matmul(xs, ws, idx, None, 1, orc.BFLOAT16), runs=2)
+    M, S = x["idx"].shape
+    G, N, K = x["w"].shape
+    job = t * (M * S) / (rows * S)
+    return {"value": round(2.0 * M * S * K * N / job / 1e12, 6), "unit": "TFLOPS", "cores": 1, "kind": "port",
+            "sample": f"serial oracle GroupedMatMul on {rows} tokens ({rows * S} routed rows, {t:.2f} s, median "
+                      f"of {runs}), extrapolated per row to {M * S} rows ({job:.0f} s per job)",
+            "nproc": nproc, "physical_cores": phys}
+
+
 def time_direct(w, steps, warmup):
     """Host path: one C-ABI call from Python per step (validation + launch),
     `steps` calls bracketed by synchronisations; ms per step by wall clock."""
@@ -570,9 +613,9 @@ def value_of(w, ms):
 
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
-             "pkgemv8")
+             "pkgemv8", "moe")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
-                 "c5": cpu_baseline_c5}
+                 "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
 
 
 def main():
@@ -620,6 +663,8 @@ def main():
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 18))
         if key == "pkgemv8":
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 34), "q8_0")
+        if key == "moe":
+            return make_moe(olamd, dev)
         if key == "c3_stream_ceiling":
             return make_stream(olamd, dev, args.replicas or 24, 25604096, key,
                                "streaming read of 25,604,096 bytes per launch (configuration 3's algorithmic "

@@ -241,11 +241,18 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   int grp = 0;
   int64_t rbase = 0, rcount = M;
   if constexpr (GM != 0) {
-    // tile t of group g, g with grp_tile_off[g] <= t < grp_tile_off[g + 1]
-    // (a non-empty group); tiles past the last one leave at once, before any
-    // load or barrier (the whole workgroup takes the same branch)
-    const int t = (int)blockIdx.x;
-    if (t >= p.grp_tile_off[p.grp_count]) return;
+    // Workgroups past the routed tiles leave at once, before any load or
+    // barrier (the whole workgroup takes the same branch).  The others are
+    // spread as in the plain mode: each XCD a contiguous run of tiles (about
+    // one group's worth when the groups are even), within a group kGroupM
+    // tile-rows high and column by column, so each column tile of the group's
+    // B is read once per run while its A rows stay in the caches.
+    const int total = p.grp_tile_off[p.grp_count];
+    const int pid = (int)blockIdx.x;
+    if (pid >= total) return;
+    const int xcd = pid % kXcds, per = total / kXcds, extra = total % kXcds;
+    const int t = xcd * per + (xcd < extra ? xcd : extra) + pid / kXcds;
+    // group g with grp_tile_off[g] <= t < grp_tile_off[g + 1] (non-empty)
     int lo = 0, hi = p.grp_count;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -253,11 +260,14 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       else hi = mid;
     }
     grp = lo;
-    const int local = t - p.grp_tile_off[grp];
+    const int64_t local = t - p.grp_tile_off[grp];
     rbase = p.grp_row_off[grp];
     rcount = p.grp_row_off[grp + 1] - rbase;
-    row0 = (int64_t)(local / nbn) * kBM;
-    col0 = (int64_t)(local % nbn) * kBN;
+    const int64_t nbm = (rcount + kBM - 1) / kBM;
+    const int64_t first_m = local / (kGroupM * nbn) * kGroupM;
+    const int64_t gsize = MinI64(nbm - first_m, kGroupM);
+    row0 = (first_m + (local % (kGroupM * nbn)) % gsize) * kBM;
+    col0 = (local % (kGroupM * nbn)) / gsize * kBN;
   } else {
     const int64_t nbm = (M + kBM - 1) / kBM;
     const int64_t tiles = nbm * nbn;
