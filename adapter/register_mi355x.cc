@@ -13,7 +13,7 @@
 //  - one KernelBase subclass per operator of the quantized-matmul path
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
-//    GroupedMatMul)
+//    GroupedMatMul, and com.microsoft:MatMulNBits on ORT-packed weights)
 //    and for the two fused nodes the GPU patterns produce
 //    (ai.rt.amd:DequantizeLinearMatMul, ai.rt.amd:DequantizePackedMatMul),
 //    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
@@ -589,6 +589,102 @@ protected:
   std::vector<int> ConstantInputs() const override { return {1, 3}; }
 };
 
+// com.microsoft:MatMulNBits (the ORT operator whose inputs
+// ExportMatMulNBitsInputs writes, onnx_core/runtime/quantization.h:492-532):
+// A [..., K] FLOAT16, B UINT8 [N, groups, blob], scales FLOAT16 [N, groups],
+// optional packed zero points; attributes K, N, bits, block_size.  The
+// weight is prepared once (onnxl_amd_prepare_matmul_nbits) into the fused
+// kernels' operands when B, scales and zero points are session constants,
+// else before each run; then one fused DequantizeLinear -> MatMul call.
+class Mi355xMatMulNBits : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:com.microsoft:MatMulNBits";
+  using Mi355xKernel::Mi355xKernel;
+
+  bool HasPreparations(const std::unordered_set<std::string> &immutable_inputs) const override {
+    return Constants(immutable_inputs);
+  }
+  void DeclarePreparations(const std::unordered_set<std::string> &immutable_inputs,
+                           std::vector<rt::KernelPreparation> &preparations) override {
+    if (!Constants(immutable_inputs)) return;
+    rt::KernelPreparation p;
+    for (int i = 1; i < 4 && i < node_->input_size(); ++i)
+      if (!node_->input(i).empty()) p.info.source_inputs.push_back(node_->input(i));
+    p.info.representation = "mi355x:matmul-nbits-prepared-v1";
+    p.info.output_slots = {node_->input(1) + ":" + p.info.representation};
+    const std::vector<std::string> sources = p.info.source_inputs;
+    p.estimate_memory = [sources](const rt::RuntimeContext &ctx) {
+      size_t bytes = 0;
+      for (const auto &s : sources) bytes += ctx.Get(s).size_bytes();
+      return rt::KernelPreparationMemory{bytes, 0, 0};  // the prepared operands live in HBM
+    };
+    p.execute = [this](rt::RuntimeContext &ctx) {
+      auto w = PrepareWeight(ctx);
+      std::lock_guard<std::mutex> lock(mu_);
+      weight_ = std::move(w);
+    };
+    preparations.push_back(std::move(p));
+  }
+
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 3);
+    rt::RequireOutputCount(node, 1);
+    for (int i = 4; i < node.input_size(); ++i)
+      if (!node.input(i).empty()) throw std::invalid_argument("mi355x: MatMulNBits g_idx and bias inputs are not supported.");
+    const onnxl_amd_tensor a = In(0, ctx);
+    std::shared_ptr<Prepared> w = weight_ ? weight_ : PrepareWeight(ctx);  // non-constant weights: every run
+    const rt::Shape shape = MatMulShape(a, w->weight.desc);
+    rt::Tensor y = ctx.MakeOutputTensor(0, kFloat16, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const onnxl_amd_tensor z = w->has_zp ? w->zero_point.desc : Absent();
+    Check(onnxl_amd_dequantize_linear_matmul(&a, &w->weight.desc, &w->scale.desc, &z, /*axis=*/0, /*cast_to=*/0, &dy,
+                                             nullptr));
+    rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+private:
+  struct Prepared {
+    DeviceTensor weight, scale, zero_point;
+    bool has_zp = false;
+  };
+
+  bool Constants(const std::unordered_set<std::string> &immutable_inputs) const {
+    for (int i = 1; i < 4 && i < node_->input_size(); ++i)
+      if (!node_->input(i).empty() && immutable_inputs.count(node_->input(i)) == 0) return false;
+    return node_->input_size() >= 3;
+  }
+
+  std::shared_ptr<Prepared> PrepareWeight(rt::RuntimeContext &ctx) const {
+    const NodeProto &node = *node_;
+    const int64_t K = rt::GetRequiredAttributeInt(node, "K"), N = rt::GetRequiredAttributeInt(node, "N");
+    const int64_t bits = rt::GetRequiredAttributeInt(node, "bits");
+    const int64_t block = rt::GetRequiredAttributeInt(node, "block_size");
+    const onnxl_amd_tensor B = In(1, ctx), s = In(2, ctx), zp = In(3, ctx);
+    auto w = std::make_shared<Prepared>();
+    w->has_zp = zp.rank >= 0;
+    int64_t wb = 0, sb = 0, zb = 0;
+    Check(onnxl_amd_prepare_matmul_nbits_size(K, N, bits, block, w->has_zp ? 1 : 0, &wb, &sb, &zb));
+    w->weight.Allocate(wb);
+    w->scale.Allocate(sb);
+    w->zero_point.Allocate(zb);
+    for (auto *d : {&w->weight, &w->scale, &w->zero_point}) {
+      d->desc = onnxl_amd_tensor{};
+      d->desc.data = d->ptr;
+      d->desc.location = ONNXL_AMD_DEVICE;
+    }
+    w->weight.desc.size_bytes = wb;
+    w->scale.desc.size_bytes = sb;
+    w->zero_point.desc.size_bytes = zb;
+    Check(onnxl_amd_prepare_matmul_nbits(&B, &s, &zp, K, N, bits, block, &w->weight.desc, &w->scale.desc,
+                                         &w->zero_point.desc, nullptr));
+    Check(onnxl_amd_synchronize(nullptr));
+    return w;
+  }
+
+  std::shared_ptr<Prepared> weight_;
+};
+
 // ---------------------------------------------------------------------------
 // Fused nodes.  They exist only in graphs rewritten by the GPU patterns, so
 // there is no built-in kernel: the adapter computes their chain itself when
@@ -790,6 +886,7 @@ const char *RegisterMi355xKernelFunctions(int device_ordinal = 0) {
     Register<Mi355xQLinearConv>("", "QLinearConv");
     Register<Mi355xDequantizePacked>("", "DequantizePacked");
     Register<Mi355xGroupedMatMul>("", "GroupedMatMul");
+    Register<Mi355xMatMulNBits>("com.microsoft", "MatMulNBits");
     Register<Mi355xDequantizeLinearMatMul>(kFusedDomain, "DequantizeLinearMatMul");
     Register<Mi355xDequantizePackedMatMul>(kFusedDomain, "DequantizePackedMatMul");
   });

@@ -308,6 +308,34 @@ int onnxl_amd_dequantize_linear_matmul_noalloc(const onnxl_amd_tensor *a, const 
 int onnxl_amd_prepare_weight_size(const onnxl_amd_tensor *x, int64_t *bytes);
 int onnxl_amd_prepare_weight(const onnxl_amd_tensor *x, onnxl_amd_tensor *prepared, void *stream);
 
+/* Session-time preparation of an ORT MatMulNBits weight (the format of
+ * onnx_core/runtime/quantization.cc:916-930, decoded at :1806-1880) for
+ * onnxl_amd_dequantize_linear_matmul, so that MatMul(A, W) with W [K, N] =
+ * (code - zero point) * scale runs on the fused kernels without a dense W.
+ * B: UINT8 [N, groups, block_size * bits / 8] (column n, row g * block + j at
+ * bit (j % (8 / bits)) * bits of byte j / (8 / bits)); scales: FLOAT16
+ * [N, groups]; zero_points: absent (2^(bits-1)) or packed UINT8 codes
+ * [N, ceil(groups * bits / 8)].  Writes into caller-allocated device buffers
+ * of the sizes onnxl_amd_prepare_matmul_nbits_size returns (16-byte aligned):
+ *   weight: bits 4 -> the tiled layout of onnxl_amd_prepare_weight, INT4 (no
+ *           zero points: code - 8) or UINT4; bits 8 -> [K, N] INT8 (code -
+ *           128) or UINT8;
+ *   scale: FLOAT16 [groups, N]; zero_point: UINT4 / UINT8 [groups, N] (set
+ *           absent, rank -1, without zero points),
+ * and sets their dtypes, dims and layouts; then pass (A, weight, scale,
+ * zero_point, axis = 0, cast_to = 0) to onnxl_amd_dequantize_linear_matmul.
+ * The format's checks raise INVALID_ARGUMENT with the reference's messages
+ * (dimensions, block size, nonfinite scales, nonzero zero-point padding).
+ * 2-bit weights, K not a multiple of block_size, FLOAT / BFLOAT16 scales and
+ * floating-point zero points return ONNXL_AMD_UNSUPPORTED.  No single
+ * reference kernel: the reference materialises the dense weight. */
+int onnxl_amd_prepare_matmul_nbits_size(int64_t K, int64_t N, int64_t bits, int64_t block_size, int has_zero_points,
+                                        int64_t *weight_bytes, int64_t *scale_bytes, int64_t *zero_point_bytes);
+int onnxl_amd_prepare_matmul_nbits(const onnxl_amd_tensor *B, const onnxl_amd_tensor *scales,
+                                   const onnxl_amd_tensor *zero_points, int64_t K, int64_t N, int64_t bits,
+                                   int64_t block_size, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                                   onnxl_amd_tensor *zero_point, void *stream);
+
 /* Waits for all work queued by this library on `stream`. */
 int onnxl_amd_synchronize(void *stream);
 

@@ -86,6 +86,11 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_matmul.argtypes = [TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_grouped_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
+        I64 = ctypes.c_int64
+        L.onnxl_amd_prepare_matmul_nbits_size.argtypes = [I64, I64, I64, I64, ctypes.c_int, ctypes.POINTER(I64),
+                                                          ctypes.POINTER(I64), ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_matmul_nbits.argtypes = [TP, TP, TP, I64, I64, I64, I64, ctypes.POINTER(Tensor),
+                                                     ctypes.POINTER(Tensor), ctypes.POINTER(Tensor), ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -224,6 +229,45 @@ def prepare_weight(x, x_dtype: int, x_shape=None) -> PreparedWeight:
                                           ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
     out._keep = storage
     return PreparedWeight(storage, out)
+
+
+class PreparedNbits:
+    """An ORT MatMulNBits weight prepared by onnxl_amd_prepare_matmul_nbits:
+    the fused kernels' weight, scale and zero point (None without zero
+    points), each a PreparedWeight (device storage + descriptor)."""
+
+    def __init__(self, weight, scale, zero_point, K, N):
+        self.weight, self.scale, self.zero_point = weight, scale, zero_point
+        self.shape = (K, N)
+
+
+def prepare_matmul_nbits(B, scales, zero_points, K: int, N: int, bits: int, block_size: int) -> PreparedNbits:
+    """Session-time preparation of an ORT MatMulNBits weight: B uint8 [N,
+    groups, block_size * bits / 8], scales FLOAT16 [N, groups], zero_points
+    None or packed uint8 codes [N, ceil(groups * bits / 8)]."""
+    torch = _torch()
+    has_zp = zero_points is not None
+    wb, sb, zb = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    _check(lib().onnxl_amd_prepare_matmul_nbits_size(K, N, bits, block_size, int(has_zp), ctypes.byref(wb),
+                                                      ctypes.byref(sb), ctypes.byref(zb)))
+    dev = torch.device("cuda", torch.cuda.current_device())
+    bufs = [torch.empty(max(n.value, 16), dtype=torch.uint8, device=dev) for n in (wb, sb, zb)]
+    descs = [describe(b) for b in bufs]
+    _check(lib().onnxl_amd_prepare_matmul_nbits(describe(B), describe(scales, FLOAT16), describe(zero_points), K, N,
+                                                bits, block_size, ctypes.byref(descs[0]), ctypes.byref(descs[1]),
+                                                ctypes.byref(descs[2]),
+                                                ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    for d, b in zip(descs, bufs):
+        d._keep = b
+    zp = PreparedWeight(bufs[2], descs[2]) if has_zp else None
+    return PreparedNbits(PreparedWeight(bufs[0], descs[0]), PreparedWeight(bufs[1], descs[1]), zp, K, N)
+
+
+def matmul_nbits(a, prepared: PreparedNbits, out=None):
+    """MatMul(a, W) for a prepared ORT MatMulNBits weight W [K, N] through the
+    fused DequantizeLinear -> MatMul entry point (blocked scales, axis 0)."""
+    return dequantize_linear_matmul(a, prepared.weight, prepared.scale, prepared.zero_point, 0, 0,
+                                    x_shape=prepared.shape, out=out)
 
 
 class ConvAttrs(ctypes.Structure):

@@ -1430,6 +1430,117 @@ int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights
   return ONNXL_AMD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// ORT MatMulNBits preparation.  The format's own checks
+// (onnx_core/runtime/quantization.cc:117-124 dimensions, :940-970 storage
+// sizes, :1826-1860 padding bits and finite scales), then the limits of the
+// fused kernels this prepares for.
+
+struct NbitsLayout {
+  int64_t groups, blob, zcol;
+  int64_t weight_bytes, scale_bytes, zp_bytes;  // prepared sizes
+};
+
+NbitsLayout PlanNbits(int64_t K, int64_t N, int64_t bits, int64_t block, bool has_zp) {
+  OLA_ENFORCE(K > 0 && N > 0, "ORT MatMulNBits requires positive K and N dimensions.");
+  OLA_ENFORCE(block >= 16 && block <= 0xffffffffLL && (block & (block - 1)) == 0,
+              "ORT MatMulNBits block_size must be a power of two in [16, UINT32_MAX].");
+  OLA_ENFORCE(bits == 2 || bits == 4 || bits == 8, "Expected an ORT MatMulNBits quantization format.");
+  if (bits == 2) throw Unsupported("MatMulNBits: 2-bit weights have no GPU kernel");
+  if (K % block != 0)
+    throw Unsupported(Cat("MatMulNBits: K = ", K, " is not a multiple of block_size ", block,
+                          " (a partial last block has no fused kernel)"));
+  NbitsLayout l{};
+  l.groups = K / block;
+  l.blob = block * bits / 8;
+  l.zcol = (l.groups * bits + 7) / 8;
+  l.weight_bytes = bits == 4 ? TiledInt4Bytes(K, N) : K * N;
+  l.scale_bytes = l.groups * N * 2;
+  l.zp_bytes = !has_zp ? 0 : (bits == 8 ? l.groups * N : (l.groups * N + 1) / 2);
+  return l;
+}
+
+int PrepareMatMulNbits(const onnxl_amd_tensor *B, const onnxl_amd_tensor *scales, const onnxl_amd_tensor *zero_points,
+                       int64_t K, int64_t N, int64_t bits, int64_t block, onnxl_amd_tensor *weight,
+                       onnxl_amd_tensor *scale, onnxl_amd_tensor *zero_point, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(B) && !Absent(scales) && weight && scale, "prepare_matmul_nbits: B, scales, weight and scale are required.");
+  CheckDescriptor(B, "B");
+  CheckDescriptor(scales, "scales");
+  CheckDescriptor(zero_points, "zero_points");
+  const bool has_zp = !Absent(zero_points);
+  const NbitsLayout l = PlanNbits(K, N, bits, block, has_zp);
+  OLA_ENFORCE(B->data_type == kUint8 && B->rank == 3 && B->dims[0] == N && B->dims[1] == l.groups &&
+                  B->dims[2] == l.blob,
+              "prepare_matmul_nbits: B must be UINT8 [N, groups, block_size * bits / 8].");
+  if (scales->data_type != kFloat16)
+    throw Unsupported("MatMulNBits: only FLOAT16 scales (FLOAT16 weights) have a fused kernel");
+  OLA_ENFORCE(scales->rank == 2 && scales->dims[0] == N && scales->dims[1] == l.groups,
+              "prepare_matmul_nbits: scales must be [N, groups].");
+  if (has_zp) {
+    if (zero_points->data_type != kUint8)
+      throw Unsupported("MatMulNBits: floating-point zero points have no fused kernel");
+    OLA_ENFORCE(zero_points->rank == 2 && zero_points->dims[0] == N && zero_points->dims[1] == l.zcol,
+                "Invalid ORT MatMulNBits zero-point dtype.");
+  }
+  // the format's value checks, on a host copy (one-time preparation)
+  {
+    std::vector<uint16_t> sc((size_t)(N * l.groups));
+    ReadBytes(*scales, 0, sc.data(), sc.size() * 2);
+    for (uint16_t h : sc) OLA_ENFORCE((h & 0x7c00u) != 0x7c00u, "Nonfinite ORT MatMulNBits scale.");
+    if (has_zp) {
+      const int64_t per = 8 / bits;
+      if (l.groups % per != 0) {
+        std::vector<uint8_t> zb((size_t)(N * l.zcol));
+        ReadBytes(*zero_points, 0, zb.data(), zb.size());
+        for (int64_t n = 0; n < N; ++n)
+          OLA_ENFORCE((zb[(size_t)((n + 1) * l.zcol - 1)] >> ((l.groups % per) * bits)) == 0,
+                      "Nonzero ORT MatMulNBits zero-point padding.");
+      }
+    }
+  }
+  const bool four = bits == 4;
+  auto out_ok = [](onnxl_amd_tensor *t, int64_t need, const char *what) {
+    OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE, "prepare_matmul_nbits: ", what, " must be device memory.");
+    OLA_ENFORCE(t->size_bytes >= need, "prepare_matmul_nbits: ", what, " holds ", t->size_bytes, " bytes, needs ", need);
+    OLA_ENFORCE(need == 0 || (t->data != nullptr && reinterpret_cast<uintptr_t>(t->data) % 16 == 0),
+                "prepare_matmul_nbits: ", what, " must be a 16-byte aligned device buffer.");
+  };
+  out_ok(weight, l.weight_bytes, "weight");
+  out_ok(scale, l.scale_bytes, "scale");
+  if (has_zp) {
+    OLA_ENFORCE(zero_point, "prepare_matmul_nbits: zero_point is required with zero_points.");
+    out_ok(zero_point, l.zp_bytes, "zero_point");
+  }
+  Ctx();
+  Staging st(stream, 0, {B, scales, has_zp ? zero_points : nullptr}, {});
+  NbitsPrepParams p{};
+  p.B = static_cast<const uint8_t *>(st.In(B));
+  p.scales = static_cast<const uint16_t *>(st.In(scales));
+  p.zp = has_zp ? static_cast<const uint8_t *>(st.In(zero_points)) : nullptr;
+  p.K = K;
+  p.N = N;
+  p.block = block;
+  p.bits = bits;
+  p.weight = weight->data;
+  p.scale_out = scale->data;
+  p.zp_out = has_zp ? zero_point->data : nullptr;
+  LaunchPrepareNbits(p, stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  auto set = [](onnxl_amd_tensor *t, int32_t dt, int64_t d0, int64_t d1, int32_t layout) {
+    t->data_type = dt;
+    t->rank = 2;
+    for (int i = 0; i < ONNXL_AMD_MAX_RANK; ++i) t->dims[i] = i == 0 ? d0 : (i == 1 ? d1 : 0);
+    t->layout = layout;
+  };
+  set(weight, four ? (has_zp ? kUint4 : kInt4) : (has_zp ? kUint8 : kInt8), K, N,
+      four ? ONNXL_AMD_LAYOUT_TILED_INT4 : ONNXL_AMD_LAYOUT_ONNX);
+  set(scale, kFloat16, l.groups, N, ONNXL_AMD_LAYOUT_ONNX);
+  if (has_zp) set(zero_point, four ? kUint4 : kUint8, l.groups, N, ONNXL_AMD_LAYOUT_ONNX);
+  else if (zero_point) zero_point->rank = -1;
+  return ONNXL_AMD_OK;
+}
+
 // Validation runs before any device work, so argument errors are reported
 // even before onnxl_amd_init (the first device access then raises
 // NotInitialized).
@@ -1633,6 +1744,28 @@ int onnxl_amd_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tens
                              onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return GroupedMatMul(input, weights, group_indices, bias, transB, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_matmul_nbits_size(int64_t K, int64_t N, int64_t bits, int64_t block_size, int has_zero_points,
+                                        int64_t *weight_bytes, int64_t *scale_bytes, int64_t *zero_point_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(weight_bytes && scale_bytes && zero_point_bytes, "prepare_matmul_nbits_size: null output");
+    const NbitsLayout l = PlanNbits(K, N, bits, block_size, has_zero_points != 0);
+    *weight_bytes = l.weight_bytes;
+    *scale_bytes = l.scale_bytes;
+    *zero_point_bytes = l.zp_bytes;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_matmul_nbits(const onnxl_amd_tensor *B, const onnxl_amd_tensor *scales,
+                                   const onnxl_amd_tensor *zero_points, int64_t K, int64_t N, int64_t bits,
+                                   int64_t block_size, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                                   onnxl_amd_tensor *zero_point, void *stream) {
+  return Guard([&] {
+    return PrepareMatMulNbits(B, scales, zero_points, K, N, bits, block_size, weight, scale, zero_point,
+                              static_cast<hipStream_t>(stream));
   });
 }
 

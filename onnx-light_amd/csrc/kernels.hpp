@@ -246,4 +246,17 @@ struct GroupedParams {
 int64_t GroupedMaxTiles(const GroupedParams &p);
 void LaunchGroupedMatMul(const GroupedParams &p, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// ORT MatMulNBits weight preparation (nbits.hip).
+struct NbitsPrepParams {
+  const uint8_t *B;         // [N, groups, block * bits / 8]
+  const uint16_t *scales;   // FLOAT16 [N, groups]
+  const uint8_t *zp;        // packed codes [N, ceil(groups * bits / 8)] or nullptr
+  int64_t K, N, block, bits;
+  void *weight;             // bits 4: tiled INT4 / UINT4; bits 8: [K, N] INT8 / UINT8
+  void *scale_out;          // FLOAT16 [groups, N]
+  void *zp_out;             // UINT4 / UINT8 [groups, N] (with zp)
+};
+void LaunchPrepareNbits(const NbitsPrepParams &p, hipStream_t stream);
+
 }  // namespace onnxl_amd

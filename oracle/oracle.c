@@ -989,3 +989,31 @@ int orc_grouped_matmul(int dtype, const void *x, int64_t M, int64_t K, const voi
   }
   return 0;
 }
+
+/* ORT MatMulNBits value -> dense [K, N] (onnx_core/runtime/quantization.cc:
+ * 1806-1880, DecodeValues): B [N, groups, blob] holds the `bits`-bit codes of
+ * column n, row r = g * block + j at bit ((j % (8 / bits)) * bits) of byte
+ * j / (8 / bits) of blob (n, g); scales [N, groups] (already decoded to
+ * double); zero points per (n, g): zp_kind 0 absent (2^(bits-1)), 1 packed
+ * UINT8 codes [N, ceil(groups / (8 / bits))] (same bit order), 2 float values
+ * [N, groups] (decoded to double).  value = (code - zp) * scale in double,
+ * written as double (the caller rounds to the reconstruction dtype).
+ * Returns 0, 4 for bits outside {2, 4, 8}. */
+int orc_ort_nbits_decode(const uint8_t *B, const double *scales, int zp_kind, const uint8_t *zp_codes,
+                         const double *zp_values, int64_t K, int64_t N, int bits, int64_t block, double *out) {
+  if (bits != 2 && bits != 4 && bits != 8) return 4;
+  const int64_t groups = (K + block - 1) / block, per = 8 / bits, blob = block * bits / 8;
+  const int64_t zcol = (groups + per - 1) / per;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t r = 0; r < K; ++r) {
+      const int64_t g = r / block, j = r % block, idx = n * groups + g;
+      const uint32_t code = (B[idx * blob + j / per] >> ((j % per) * bits)) & mask;
+      double zp;
+      if (zp_kind == 0) zp = (double)(1u << (bits - 1));
+      else if (zp_kind == 1) zp = (double)((zp_codes[n * zcol + g / per] >> ((g % per) * bits)) & mask);
+      else zp = zp_values[idx];
+      out[r * N + n] = ((double)code - zp) * scales[idx];
+    }
+  return 0;
+}

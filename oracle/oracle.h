@@ -113,6 +113,8 @@ int orc_matmul_f32(const float *a, const int64_t *a_shape, int a_rank, const flo
 
 /* ---- MatMul FLOAT16/BFLOAT16 (km/kernel_matmul.cc:206-218):
  * PromoteToFloat32 -> MatMulCompute<float> -> DemoteFromFloat32 ---- */
+int orc_ort_nbits_decode(const uint8_t *B, const double *scales, int zp_kind, const uint8_t *zp_codes,
+                         const double *zp_values, int64_t K, int64_t N, int bits, int64_t block, double *out);
 int orc_grouped_matmul(int dtype, const void *x, int64_t M, int64_t K, const void *w, int64_t G, int64_t N,
                        int transB, const int64_t *idx, int64_t S, const void *bias, void *y);
 int orc_matmul_half(const uint16_t *a, const int64_t *a_shape, int a_rank, const uint16_t *b,

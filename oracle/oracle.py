@@ -104,6 +104,9 @@ def _declare(L):
     L.orc_matmul_f32.restype = ctypes.c_int
     L.orc_matmul_f32.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int]
+    L.orc_ort_nbits_decode.restype = ctypes.c_int
+    L.orc_ort_nbits_decode.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                       ctypes.c_int64, P]
     L.orc_grouped_matmul.restype = ctypes.c_int
     L.orc_grouped_matmul.argtypes = [ctypes.c_int, P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int, P, ctypes.c_int64, P, P]
@@ -334,6 +337,28 @@ def matmul_half(a_bits: np.ndarray, b_bits: np.ndarray, dtype: int, rows=None,
 
 
 DOUBLE = 11
+
+
+def ort_nbits_decode(B: np.ndarray, scales: np.ndarray, zero_points, K: int, N: int, bits: int,
+                     block: int) -> np.ndarray:
+    """ORT MatMulNBits value -> float64 [K, N] = (code - zp) * scale.  B uint8
+    [N, groups, blob]; scales float [N, groups] (values); zero_points None,
+    uint8 packed codes [N, ceil(groups * bits / 8)], or float [N, groups]."""
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    sc = np.ascontiguousarray(scales, dtype=np.float64)
+    out = np.zeros((K, N), np.float64)
+    kind, zc, zv = 0, None, None
+    if zero_points is not None:
+        zp = np.asarray(zero_points)
+        if zp.dtype == np.uint8:
+            kind, zc = 1, np.ascontiguousarray(zp)
+        else:
+            kind, zv = 2, np.ascontiguousarray(zp, dtype=np.float64)
+    rc = lib().orc_ort_nbits_decode(_ptr(B), _ptr(sc), kind, None if zc is None else _ptr(zc),
+                                    None if zv is None else _ptr(zv), K, N, bits, block, _ptr(out))
+    if rc:
+        raise ValueError(f"ort_nbits_decode error {rc}")
+    return out
 
 
 def grouped_matmul(x: np.ndarray, w: np.ndarray, indices: np.ndarray, bias=None, transB: int = 0,

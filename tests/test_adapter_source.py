@@ -19,7 +19,7 @@ REFERENCE = "/root/reference/onnx_light"
 
 OPERATORS = ["MatMulInteger", "QLinearMatMul", "DequantizeLinear", "MatMul", "QuantizeLinear",
              "DynamicQuantizeLinear", "ConvInteger", "QLinearConv", "Cast", "DequantizePacked",
-             "GroupedMatMul", "DequantizeLinearMatMul", "DequantizePackedMatMul"]
+             "GroupedMatMul", "MatMulNBits", "DequantizeLinearMatMul", "DequantizePackedMatMul"]
 
 
 def _strip_comments(text):
@@ -88,7 +88,8 @@ def test_operator_has_registered_kernel_class(op):
     assert re.search(rf"class {cls} : public Mi355xKernel\b", text), cls
     assert re.search(rf'static constexpr const char \*name = "onnxl_amd:CPU:[\w.]+:{op}";', text), cls
     assert re.search(rf"void Run\(rt::RuntimeContext &ctx\) override", text)
-    domain = "kFusedDomain" if op.endswith("MatMul") and op.startswith("Dequantize") else '""'
+    domain = ("kFusedDomain" if op.endswith("MatMul") and op.startswith("Dequantize")
+              else '"com.microsoft"' if op == "MatMulNBits" else '""')
     assert re.search(rf'Register<{cls}>\({re.escape(domain)}, "{op}"\);', text), cls
 
 
