@@ -218,13 +218,16 @@ public:
     if (!SingleUse(graph, Out(*dp, 0), *tr)) return NoMatch(candidate, "DequantizePacked output has another consumer");
     if (!graph.IsConstant(In(*dp, 0))) return NoMatch(candidate, "packed weight is not an initializer");
     const std::string format = ol::GetAttributeOr<std::string>(*dp, "format", "");
-    if (format != "gguf:q4_0" && format != "gguf:q8_0") return NoMatch(candidate, "format has no fused kernel");
+    const int64_t k_multiple = format == "gguf:q4_0" || format == "gguf:q8_0"   ? 64
+                               : format == "gguf:q4_k" || format == "gguf:q6_k" ? 256
+                                                                                : 0;
+    if (k_multiple == 0) return NoMatch(candidate, "format has no fused kernel");
     std::vector<int64_t> shape;
     ol::GetAttributeInts(*dp, "shape", shape);
     if (shape.size() != 2) return NoMatch(candidate, "DequantizePacked shape is not [N, K]");
     if (ol::GetAttributeOr<int64_t>(*dp, "output_dtype", kFloat) != kFloat16)
       return NoMatch(candidate, "DequantizePacked output is not FLOAT16");
-    if (shape[1] % 64 != 0) return NoMatch(candidate, "K is not a multiple of 64");
+    if (shape[1] % k_multiple != 0) return NoMatch(candidate, "K does not fit the fused GEMV");
     if (!graph.HasType(In(candidate, 0))) return NoMatch(candidate, "type of A unknown");
     if (graph.GetType(In(candidate, 0)) != TensorType::kFloat16) return NoMatch(candidate, "A is not FLOAT16");
     return builder::MatchResult{this, {dp, tr, &candidate}, &candidate};

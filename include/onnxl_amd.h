@@ -150,7 +150,7 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
  * fixed GGUF wire formats (`format`, e.g. "gguf:q4_0") into y of the given
  * shape and output_dtype (FLOAT, FLOAT16, BFLOAT16 or DOUBLE); the last
  * dimension holds whole blocks.  The GPU decodes gguf:q4_0, q4_1, q5_0, q5_1,
- * q8_0, q8_1 and iq4_nl; the reference's other 20 formats return
+ * q8_0, q8_1, iq4_nl, q4_k and q6_k; the reference's other 18 formats return
  * ONNXL_AMD_UNSUPPORTED, an unknown format INVALID_ARGUMENT.
  * Replaces DequantizePackedTensor (onnx_core/runtime/dequantize_packed.cc:
  * 334-372) behind kernel::DequantizePacked::operator()
@@ -163,7 +163,8 @@ int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, c
  * weight is in the ggml layout, each output's blocks contiguous along K; the
  * dequantized weights are rounded to FLOAT16 exactly as the unfused chain
  * rounds them, so only the fp32 summation order differs.  gguf:q4_0 and
- * gguf:q8_0 with M <= 8 and K % 64 == 0; other inputs return
+ * gguf:q8_0 with M <= 8 and K % 64 == 0, gguf:q4_k and gguf:q6_k with
+ * M <= 8 (K a multiple of their 256-value blocks); other inputs return
  * ONNXL_AMD_UNSUPPORTED.  No
  * single reference kernel: it computes the DequantizePacked -> Transpose ->
  * MatMul chain, onnx_core/runtime/dequantize_packed.cc:334-372 ->

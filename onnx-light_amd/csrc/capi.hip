@@ -1057,7 +1057,8 @@ struct PackedProfile {
 };
 
 // The reference's 27 fixed wire profiles (ggml block sizes and bytes,
-// dequantize_packed.cc:27-36); the GPU decodes the 32-value formats.
+// dequantize_packed.cc:27-36); the GPU decodes the 32-value formats, q4_k and
+// q6_k.
 constexpr PackedProfile kPackedProfiles[] = {
     {"gguf:q4_0", 32, 18, 2},      {"gguf:q4_1", 32, 20, 3},      {"gguf:q5_0", 32, 22, 6},
     {"gguf:q5_1", 32, 24, 7},      {"gguf:q8_0", 32, 34, 8},      {"gguf:q8_1", 32, 36, 9},
@@ -1133,18 +1134,27 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
   OLA_ENFORCE(y->data_type == kFloat16 && ShapeOf(*y) == Shape({M, N}) && y->size_bytes == M * N * 2,
               "DequantizePackedMatMul: y must be FLOAT16 [M, N].");
   const bool q8 = std::strcmp(format, "gguf:q8_0") == 0;
-  if (!q8 && std::strcmp(format, "gguf:q4_0") != 0)
+  const bool q4k = std::strcmp(format, "gguf:q4_k") == 0, q6k = std::strcmp(format, "gguf:q6_k") == 0;
+  if (!q8 && !q4k && !q6k && std::strcmp(format, "gguf:q4_0") != 0)
     throw Unsupported(Cat("DequantizePackedMatMul: format ", format, " has no fused GPU kernel"));
-  OLA_ENFORCE(K % 32 == 0, "DequantizePacked: last dimension must contain complete blocks.");
+  const int64_t bv = q4k || q6k ? 256 : 32, bb = q8 ? 34 : (q4k ? 144 : (q6k ? 210 : 18));
+  OLA_ENFORCE(K % bv == 0, "DequantizePacked: last dimension must contain complete blocks.");
   OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
-  OLA_ENFORCE(x->dims[0] == N * (K / 32) * (q8 ? 34 : 18) && x->size_bytes == x->dims[0],
+  OLA_ENFORCE(x->dims[0] == N * (K / bv) * bb && x->size_bytes == x->dims[0],
               "DequantizePacked: packed input length must match exactly.");
   if (M == 0 || N == 0) return ONNXL_AMD_OK;  // empty [M, N] result, nothing to launch
   Staging st(stream, 0, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
-  if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");  // q8_0 alike
-  (q8 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
-                                       static_cast<uint16_t *>(st.Out(y)), stream);
+  if (q4k || q6k) {
+    if (M > 8 || K == 0 || reinterpret_cast<uintptr_t>(ad) % 16 != 0)
+      throw Unsupported("DequantizePackedMatMul: k-quant GEMV needs 1 <= M <= 8, K > 0 and 16-byte aligned a");
+    LaunchGemvK(q4k ? 12 : 14, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
+                static_cast<uint16_t *>(st.Out(y)), stream);
+  } else {
+    if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");  // q8_0 alike
+    (q8 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
+                                         static_cast<uint16_t *>(st.Out(y)), stream);
+  }
   st.Finish();
   return ONNXL_AMD_OK;
 }

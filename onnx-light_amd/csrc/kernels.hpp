@@ -90,6 +90,9 @@ bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w);
 void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t stream);
 // The same for gguf:q8_0 (same eligibility).
+// Fused q4_k (ggml type 12) / q6_k (14) GEMV, K % 256 == 0, M <= 8, a 16-byte aligned.
+void LaunchGemvK(int ggml_type, const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                 hipStream_t s);
 void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t stream);
 

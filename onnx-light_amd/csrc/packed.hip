@@ -1,5 +1,6 @@
 // DequantizePacked (onnx_core/runtime/dequantize_packed.cc) for the 32-value
-// GGUF block formats: q4_0, q4_1, q5_0, q5_1, q8_0, q8_1 and iq4_nl.  A block
+// GGUF block formats q4_0, q4_1, q5_0, q5_1, q8_0, q8_1 and iq4_nl, and the
+// 256-value k-quants q4_k and q6_k (below).  A 32-value block
 // is an fp16 scale d (plus an fp16 minimum m for q4_1 / q5_1, a 4-byte high
 // bit plane for q5_*, an fp16 sum for q8_1) and 32 codes; the value is
 // d * q (+ m), every fp32 step rounded on its own (no contraction), then
@@ -127,6 +128,91 @@ __global__ __launch_bounds__(kPkThreads) void DequantPackedKernel(const uint8_t 
     }
   }
   StoreEight<OUT>(y, b * 32 + i0, v, vec != 0);
+}
+
+// ---------------------------------------------------------------------------
+// q4_k and q6_k, 256-value blocks (dequantize_packed.cc:240-252): 8
+// consecutive values i0 .. i0 + 7 (i0 % 8 == 0) of block p, with the
+// reference's fp32 steps.
+//  q4_k (144 bytes): fp16 d, fp16 dmin, 12 bytes of 6-bit scales / minima of
+//   the eight 32-value sub-blocks, 128 code bytes: value i is nibble
+//   (i / 32) % 2 of byte (i / 64) * 32 + i % 32; value = (d * scale) * q -
+//   dmin * minimum.
+//  q6_k (210 bytes): low nibbles, byte (i / 128) * 64 + i % 64, nibble
+//   (i / 64) % 2; high 2 bits from byte 128 + (i / 128) * 32 + i % 32, field
+//   (i / 32) % 4; int8 scale per 16 values at byte 192 + i / 16; fp16 d at
+//   byte 208; value = (d * scale) * (q - 32).
+//
+// The NaN a step produces follows the reference's x86-64 build, whose SSE
+// arithmetic returns the first operand (quieted) when both are NaN, else the
+// NaN one, and the negative default NaN 0xffc00000 for inf * 0 and inf - inf;
+// the GPU's own choice of operand and default NaN is replaced by that.
+__device__ __forceinline__ float SseNaN(float r, float a, float b) {
+  if (r == r) return r;
+  const uint32_t bits = a != a   ? __builtin_bit_cast(uint32_t, a) | 0x00400000u
+                        : b != b ? __builtin_bit_cast(uint32_t, b) | 0x00400000u
+                                 : 0xffc00000u;
+  return __builtin_bit_cast(float, bits);
+}
+__device__ __forceinline__ float SseMul(float a, float b) { return SseNaN(a * b, a, b); }
+__device__ __forceinline__ float SseSub(float a, float b) { return SseNaN(a - b, a, b); }
+
+__device__ __forceinline__ void DecodeQ4K8(const uint8_t *p, int i0, float v[8]) {
+  const float d = Half2(p), dmin = Half2(p + 2);
+  const uint8_t *sc = p + 4;
+  const int g = i0 >> 5;
+  const int scale = g < 4 ? sc[g] & 63 : (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+  const int minimum = g < 4 ? sc[g + 4] & 63 : (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+  const float ds = SseMul(d, (float)scale);
+  const float dm = SseMul(dmin, (float)minimum);
+  const uint8_t *q = p + 16 + (i0 >> 6) * 32 + (i0 & 31);
+  const int sh = 4 * (g & 1);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = SseSub(SseMul(ds, (float)((q[e] >> sh) & 15)), dm);
+}
+
+__device__ __forceinline__ void DecodeQ6K8(const uint8_t *p, int i0, float v[8]) {
+  const float d = Half2(p + 208);
+  const float ds = SseMul(d, (float)(int8_t)p[192 + (i0 >> 4)]);
+  const uint8_t *ql = p + (i0 >> 7) * 64 + (i0 & 63);
+  const uint8_t *qh = p + 128 + (i0 >> 7) * 32 + (i0 & 31);
+  const int shl = 4 * ((i0 >> 6) & 1), shh = 2 * ((i0 >> 5) & 3);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    v[e] = SseMul(ds, (float)((((ql[e] >> shl) & 15) | (((qh[e] >> shh) & 3) << 4)) - 32));
+}
+
+template <int TYPE> struct KLayout;
+template <> struct KLayout<12> { static constexpr int bytes = 144; };
+template <> struct KLayout<14> { static constexpr int bytes = 210; };
+
+template <int TYPE> __device__ __forceinline__ void DecodeK8(const uint8_t *p, int i0, float v[8]) {
+  if constexpr (TYPE == 12) DecodeQ4K8(p, i0, v);
+  else DecodeQ6K8(p, i0, v);
+}
+
+// 32 threads per block, 8 consecutive values each: thread t writes values
+// 8t .. 8t + 7 of the output, as the 32-value kernel does.
+template <int TYPE, int OUT>
+__global__ __launch_bounds__(kPkThreads) void DequantPackedKKernel(const uint8_t *__restrict__ x, int64_t nblocks,
+                                                                   void *__restrict__ y, int vec) {
+  const int64_t t = (int64_t)blockIdx.x * kPkThreads + threadIdx.x;
+  if (t >= nblocks * 32) return;
+  const int64_t b = t >> 5;
+  const int i0 = (int)(t & 31) * 8;
+  float v[8];
+  DecodeK8<TYPE>(x + b * KLayout<TYPE>::bytes, i0, v);
+  StoreEight<OUT>(y, b * 256 + i0, v, vec != 0);
+}
+
+template <int TYPE> void LaunchPkKOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
+  const dim3 g((unsigned)((nblocks * 32 + kPkThreads - 1) / kPkThreads));
+  switch (out) {
+  case kFloat: hipLaunchKernelGGL((DequantPackedKKernel<TYPE, kFloat>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kFloat16: hipLaunchKernelGGL((DequantPackedKKernel<TYPE, kFloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kBfloat16: hipLaunchKernelGGL((DequantPackedKKernel<TYPE, kBfloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  default: hipLaunchKernelGGL((DequantPackedKKernel<TYPE, kDouble>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  }
 }
 
 template <int TYPE> void LaunchPkOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
@@ -376,7 +462,88 @@ __global__ __launch_bounds__(256) void GemvQ80Kernel(const uint16_t *__restrict_
   }
 }
 
+// Fused q4_k / q6_k GEMV: y[m, n] = sum_k a[m, k] * W[n, k] with W the
+// FLOAT16 DequantizePacked values of the [N, K] weight (ggml layout: the
+// 256-value blocks of output n contiguous along k).  A workgroup computes 16
+// outputs, 4 per wave; within a wave, lanes 0-31 and 32-63 take alternate
+// blocks, each lane 8 consecutive values of its block.  A lane decodes its 8
+// values per output with the reference's fp32 steps, rounds them to FLOAT16
+// (the chain's DequantizePacked output) and accumulates with the activations
+// through v_dot2_f32_f16 in fp32.
+template <int TYPE, int M>
+__global__ __launch_bounds__(256) void GemvKKernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
+                                                   int64_t N, int64_t K, uint16_t *__restrict__ y) {
+  constexpr int kBytes = KLayout<TYPE>::bytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, i0 = (lane & 31) * 8;
+  const int64_t nb = K / 256;
+  const int64_t n0 = (int64_t)blockIdx.x * kGvRows + wave * kGvCols;
+  float acc[kGvCols][M];
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[c][m] = 0.f;
+  for (int64_t kb = half; kb < nb; kb += 2) {
+    h2_t wp[kGvCols][4];
+#pragma unroll
+    for (int c = 0; c < kGvCols; ++c) {
+      const int64_t n = n0 + c < N ? n0 + c : N - 1;  // columns past N decode the last and are not stored
+      float v[8];
+      DecodeK8<TYPE>(w + (n * nb + kb) * kBytes, i0, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wp[c][e] = AsH2((uint32_t)F32ToF16(v[2 * e]) | (uint32_t)F32ToF16(v[2 * e + 1]) << 16);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      typedef unsigned v4u __attribute__((ext_vector_type(4)));
+      const v4u av = *reinterpret_cast<const v4u *>(a + m * K + kb * 256 + i0);  // 16-byte aligned (K % 256 == 0)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const h2_t ap = AsH2(av[e]);
+#pragma unroll
+        for (int c = 0; c < kGvCols; ++c) acc[c][m] = __builtin_amdgcn_fdot2(ap, wp[c][e], acc[c][m], false);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c) {
+    const int64_t n = n0 + c;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float s = acc[c][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0 && n < N) y[m * N + n] = F32ToF16(s);
+    }
+  }
+}
+
+template <int TYPE>
+void LaunchGemvKType(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                     hipStream_t s) {
+  const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
+  switch (M) {
+  case 1: hipLaunchKernelGGL((GemvKKernel<TYPE, 1>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 2: hipLaunchKernelGGL((GemvKKernel<TYPE, 2>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 3: hipLaunchKernelGGL((GemvKKernel<TYPE, 3>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 4: hipLaunchKernelGGL((GemvKKernel<TYPE, 4>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 5: hipLaunchKernelGGL((GemvKKernel<TYPE, 5>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 6: hipLaunchKernelGGL((GemvKKernel<TYPE, 6>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 7: hipLaunchKernelGGL((GemvKKernel<TYPE, 7>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  case 8: hipLaunchKernelGGL((GemvKKernel<TYPE, 8>), g, dim3(256), 0, s, a, w, N, K, y); break;
+  default: throw Unsupported("k-quant GEMV: M above 8");
+  }
+}
+
 }  // namespace
+
+void LaunchGemvK(int ggml_type, const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                 hipStream_t s) {
+  if (N == 0) return;
+  if (ggml_type == 12) LaunchGemvKType<12>(a, w, M, N, K, y, s);
+  else LaunchGemvKType<14>(a, w, M, N, K, y, s);
+}
 
 void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t s) {
@@ -419,7 +586,7 @@ void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, in
 
 bool PackedFormatOnGpu(int ggml_type) {
   return ggml_type == 2 || ggml_type == 3 || ggml_type == 6 || ggml_type == 7 || ggml_type == 8 ||
-         ggml_type == 9 || ggml_type == 20;
+         ggml_type == 9 || ggml_type == 20 || ggml_type == 12 || ggml_type == 14;
 }
 
 void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, int out_dtype, void *y,
@@ -434,6 +601,8 @@ void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, in
   case 8: LaunchPkOut<8>(x, nblocks, out_dtype, y, vec, s); break;
   case 9: LaunchPkOut<9>(x, nblocks, out_dtype, y, vec, s); break;
   case 20: LaunchPkOut<20>(x, nblocks, out_dtype, y, vec, s); break;
+  case 12: LaunchPkKOut<12>(x, nblocks, out_dtype, y, vec, s); break;
+  case 14: LaunchPkKOut<14>(x, nblocks, out_dtype, y, vec, s); break;
   default: throw Unsupported("DequantizePacked: no GPU kernel for this format");
   }
 }

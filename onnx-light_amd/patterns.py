@@ -45,7 +45,7 @@ from typing import Callable, Dict, List, Optional, Sequence
 FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
 PACKED_FUSED_OP = "DequantizePackedMatMul"
-_PACKED_FORMATS = ("gguf:q4_0", "gguf:q8_0")  # the fused packed GEMV's formats
+_PACKED_FORMATS = {"gguf:q4_0": 64, "gguf:q8_0": 64, "gguf:q4_k": 256, "gguf:q6_k": 256}  # format: K multiple
 _ONNX_DOMAINS = ("", "ai.onnx")
 _CAST_TARGETS = (10, 16)  # FLOAT16, BFLOAT16: the types the fused kernel rounds to
 FLOAT, UINT8, INT8, FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 1, 2, 3, 10, 16, 17, 21, 22
@@ -221,8 +221,9 @@ class DequantizePackedMatMulPattern(PatternOptimization):
     a constant x -> Transpose(perm = [1, 0]) -> MatMul's second input, with a
     FLOAT16 A -> one fused node ``ai.rt.amd:DequantizePackedMatMul(A, x)``
     with attributes format and shape, computed by
-    ``dequantize_packed_matmul``.  Only the formats the fused GEMV decodes
-    (q4_0, q8_0) and K % 64 == 0 are rewritten; the GEMV takes up to 8 rows
+    ``dequantize_packed_matmul``.  Only the formats the fused GEMVs decode
+    (q4_0 and q8_0 with K % 64 == 0, q4_k and q6_k with K % 256 == 0) are
+    rewritten; the GEMV takes up to 8 rows
     of A, and a session adapter runs the chain for taller A (the row count is
     only known at run time)."""
     device = "gpu"
@@ -255,8 +256,8 @@ class DequantizePackedMatMulPattern(PatternOptimization):
             return self.no_match("DequantizePacked shape is not [N, K]")
         if int(dp.attrs.get("output_dtype", FLOAT)) != FLOAT16:
             return self.no_match("DequantizePacked output is not FLOAT16")
-        if shape[1] % 64:
-            return self.no_match("K is not a multiple of 64")
+        if shape[1] % _PACKED_FORMATS[fmt]:
+            return self.no_match("K does not fit the fused GEMV")
         a_info = graph.value_info.get(candidate.inputs[0])
         if a_info is None:
             return self.no_match("type of A unknown")

@@ -598,8 +598,8 @@ int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_
 }
 
 /* ------------------------------------------------------------------------ */
-/* DequantizePacked for the 32-value GGUF block formats
- * (onnx_core/runtime/dequantize_packed.cc:173-235, the ggml layouts at ggml
+/* DequantizePacked for the 32-value GGUF block formats and q4_k / q6_k
+ * (onnx_core/runtime/dequantize_packed.cc:173-252, the ggml layouts at ggml
  * da8e2a54b919557b816b1c2beb432ccb766f7ce0): an fp16 scale d, and for the
  * affine formats an fp16 minimum m, then the codes.  Every fp32 product and
  * sum is rounded on its own (the reference forces it through volatile). */
@@ -619,13 +619,57 @@ int orc_packed_block_bytes(int ggml_type) {
   case 8: return 34;  /* q8_0 */
   case 9: return 36;  /* q8_1 */
   case 20: return 18; /* iq4_nl */
+  case 12: return 144; /* q4_k */
+  case 14: return 210; /* q6_k */
   default: return 0;
+  }
+}
+
+/* Unpack(p, i, bits, group) of dequantize_packed.cc:64-68: value i of
+ * grouped bit planes (8 / bits planes of `group` bytes). */
+static int pk_unpack(const uint8_t *p, int i, int bits, int group) {
+  const int planes = 8 / bits;
+  return (p[(i / (planes * group)) * group + i % group] >> (bits * ((i / group) % planes))) & ((1 << bits) - 1);
+}
+
+/* q4_k and q6_k, the 256-value blocks of dequantize_packed.cc:193-208 and
+ * :240-252.  q4_k: fp16 d and dmin, 12 bytes of 6-bit sub-block scales and
+ * minima, 128 code bytes; value = (d * scale) * q - dmin * minimum.  q6_k:
+ * 128 low-nibble bytes, 64 bytes of 2-bit high parts, 16 int8 sub-block
+ * scales, fp16 d; value = (d * scale) * (q - 32).  Every fp32 step rounded
+ * on its own. */
+static void pk_decode_k(int ggml_type, const uint8_t *p, float *out) {
+  for (int i = 0; i < 256; ++i) {
+    volatile float v;
+    if (ggml_type == 12) {
+      const float d = orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+      const float dmin = orc_f16_to_f32((uint16_t)(p[2] | (p[3] << 8)));
+      const uint8_t *sc = p + 4;
+      const int g = i / 32;
+      const int scale = g < 4 ? sc[g] & 63 : (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+      const int minimum = g < 4 ? sc[g + 4] & 63 : (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+      const int q = pk_unpack(p + 16, i, 4, 32);
+      volatile float ds = d * (float)scale;
+      volatile float dq = ds * (float)q;
+      volatile float dm = dmin * (float)minimum;
+      v = dq - dm;
+    } else {
+      const float d = orc_f16_to_f32((uint16_t)(p[208] | (p[209] << 8)));
+      const int q = (pk_unpack(p, i, 4, 64) | (pk_unpack(p + 128, i, 2, 32) << 4)) - 32;
+      volatile float ds = d * (float)(int8_t)p[192 + i / 16];
+      v = ds * (float)q;
+    }
+    out[i] = v;
   }
 }
 
 int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out) {
   const int bytes = orc_packed_block_bytes(ggml_type);
   if (!bytes) return 1;
+  if (ggml_type == 12 || ggml_type == 14) {
+    for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += 256) pk_decode_k(ggml_type, x, out);
+    return 0;
+  }
   for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += 32) {
     const float d = orc_f16_to_f32((uint16_t)(x[0] | (x[1] << 8)));
     for (int i = 0; i < 32; ++i) {

@@ -457,7 +457,8 @@ def qlinear_conv(x, x_dtype, x_scale, x_zp, w, w_dtype, w_scale, w_zp, y_scale, 
 # ---- DequantizePacked (32-value GGUF formats) -------------------------------
 
 GGUF_TYPES = {"gguf:q4_0": 2, "gguf:q4_1": 3, "gguf:q5_0": 6, "gguf:q5_1": 7, "gguf:q8_0": 8,
-              "gguf:q8_1": 9, "gguf:iq4_nl": 20}
+              "gguf:q8_1": 9, "gguf:iq4_nl": 20, "gguf:q4_k": 12, "gguf:q6_k": 14}
+BLOCK_VALUES = {"gguf:q4_k": 256, "gguf:q6_k": 256}  # the others: 32
 
 
 def packed_block_bytes(fmt: str) -> int:
@@ -470,7 +471,7 @@ def dequantize_packed(x: np.ndarray, fmt: str, shape, output_dtype: int = FLOAT)
     x = np.ascontiguousarray(x, dtype=np.uint8)
     n = int(np.prod(shape)) if len(shape) else 1
     out = np.empty(n, np.float32)
-    rc = lib().orc_dequantize_packed(GGUF_TYPES[fmt], _ptr(x), n // 32, _ptr(out))
+    rc = lib().orc_dequantize_packed(GGUF_TYPES[fmt], _ptr(x), n // BLOCK_VALUES.get(fmt, 32), _ptr(out))
     if rc:
         raise ValueError(f"dequantize_packed error {rc}")
     out = out.reshape(shape)

@@ -349,5 +349,5 @@ def test_dequantize_packed_validation(olamd):
     rc, _ = run()
     assert rc == olamd.NOT_INITIALIZED
     # a format of the reference with no GPU kernel here
-    rc, _ = run(x=np.zeros(144, np.uint8), fmt=b"gguf:q4_k", shape=(256,), y=np.zeros(256, np.float32))
+    rc, _ = run(x=np.zeros(176, np.uint8), fmt=b"gguf:q5_k", shape=(256,), y=np.zeros(256, np.float32))
     assert rc == olamd.UNSUPPORTED

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from test_oracle_packed import FORMATS, corpus, fnv1a64
+from test_oracle_packed import FORMATS, block_values, corpus, fnv1a64
 
 pytestmark = pytest.mark.gpu
 OUT = {"float": (1, torch.float32), "float16": (10, torch.float16), "bfloat16": (16, torch.bfloat16),
@@ -32,7 +32,7 @@ def _bits(t, out):
 def test_corpus_hashes_on_gpu(olamd, oracle, golden, dev, fmt):
     g = golden["dequantize_packed_gguf"]
     x = corpus(oracle, fmt, g["corpus_scales"])
-    y = olamd.dequantize_packed(torch.from_numpy(x).to(dev), fmt, (2, 1024))
+    y = olamd.dequantize_packed(torch.from_numpy(x).to(dev), fmt, (2, 32 * block_values(fmt)))
     assert fnv1a64(y.cpu().numpy()) == g["fnv1a64"][fmt]
 
 
@@ -41,14 +41,17 @@ def test_corpus_hashes_on_gpu(olamd, oracle, golden, dev, fmt):
 def test_random_blocks_vs_oracle(olamd, oracle, dev, fmt, out):
     rng = np.random.default_rng(len(fmt) * 7 + len(out) + FORMATS.index(fmt) * 101)
     size = oracle.packed_block_bytes(fmt)
-    for shape in [(32,), (3, 5, 64), (7, 4096), (1, 96)]:
-        nb = int(np.prod(shape)) // 32
+    bv = block_values(fmt)
+    shapes = [(32,), (3, 5, 64), (7, 4096), (1, 96)] if bv == 32 else [(256,), (3, 2, 512), (7, 4096), (1, 768)]
+    at = 208 if fmt == "gguf:q6_k" else 0  # the fp16 d
+    for shape in shapes:
+        nb = int(np.prod(shape)) // bv
         x = rng.integers(0, 256, (nb, size)).astype(np.uint8)
         # scales: random fp16 bit patterns, with NaN, inf, subnormal and 65504 among them
         special = np.array([0x7E00, 0xFC00, 0x0001, 0x7BFF, 0x8000, 0x3C00], np.uint16)
         d = rng.integers(0, 65536, nb).astype(np.uint16)
         d[: min(nb, len(special))] = special[: min(nb, len(special))]
-        x[:, 0], x[:, 1] = d & 255, d >> 8
+        x[:, at], x[:, at + 1] = d & 255, d >> 8
         x = x.reshape(-1)
         want = oracle.dequantize_packed(x, fmt, shape, OUT[out][0])
         for offset in (0, 1):
@@ -83,6 +86,39 @@ def _block_weight(rng, N, K, block_bytes):
 
 def _q4_0_weight(rng, N, K):
     return _block_weight(rng, N, K, 18)
+
+
+def _k_weight(rng, N, K, fmt):
+    """Random q4_k / q6_k blocks with small finite fp16 d (and dmin)."""
+    size = 144 if fmt == "gguf:q4_k" else 210
+    blocks = rng.integers(0, 256, (N * K // 256, size)).astype(np.uint8)
+    d = np.float16(rng.uniform(0.0005, 0.004, N * K // 256)).view(np.uint16)
+    at = 208 if fmt == "gguf:q6_k" else 0
+    blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
+    if fmt == "gguf:q4_k":
+        m = np.float16(rng.uniform(0.0005, 0.004, N * K // 256)).view(np.uint16)
+        blocks[:, 2], blocks[:, 3] = m & 255, m >> 8
+    return blocks.reshape(-1)
+
+
+_K_SHAPES = [(1, 96, 256), (3, 200, 512), (8, 64, 4096), (2, 1000, 1024), (1, 4096, 11008 // 256 * 256), (5, 37, 2304)]
+
+
+@pytest.mark.parametrize("fmt", ["gguf:q4_k", "gguf:q6_k"])
+@pytest.mark.parametrize("M,N,K", _K_SHAPES)
+def test_k_quant_gemv_vs_chain(olamd, oracle, dev, fmt, M, N, K):
+    """The fused q4_k / q6_k GEMV against the chain DequantizePacked(FLOAT16)
+    -> MatMul(a, W^T): same weight rounding, fp32 sums in another order."""
+    from test_gpu_float import assert_close
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + len(fmt))
+    x = _k_weight(rng, N, K, fmt)
+    a = np.float16(rng.standard_normal((M, K)))
+    w_bits = oracle.dequantize_packed(x, fmt, (N, K), 10)
+    ref = oracle.matmul_half(a.view(np.uint16), np.ascontiguousarray(w_bits.T), 10)
+    got = olamd.dequantize_packed_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(x).to(dev), fmt, (N, K))
+    got_bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    mag = np.abs(a.astype(np.float64)) @ np.abs(oracle.f16_bits_to_f32(w_bits).astype(np.float64)).T
+    assert_close(got_bits, ref, mag, "f16", oracle, f"{fmt} gemv {M}x{N}x{K}")
 
 
 _GEMV_SHAPES = [(1, 96, 64), (3, 200, 256), (8, 64, 4096), (2, 1000, 1024), (1, 14336, 4096), (5, 37, 2112),

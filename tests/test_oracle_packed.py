@@ -5,23 +5,29 @@ independent GGML-C oracles, and hand-checked values of each layout."""
 import numpy as np
 import pytest
 
-FORMATS = ["gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1", "gguf:iq4_nl"]
-AFFINE = {"gguf:q4_1", "gguf:q5_1"}
+FORMATS = ["gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1", "gguf:iq4_nl",
+           "gguf:q4_k", "gguf:q6_k"]
+AFFINE = {"gguf:q4_1", "gguf:q5_1", "gguf:q4_k"}  # a second fp16 (minimum) after d
+
+
+def block_values(fmt):
+    return 256 if fmt in ("gguf:q4_k", "gguf:q6_k") else 32
 
 
 def corpus(oracle, fmt, scales):
     """64 blocks: byte j of block i is (73j + 29i + 17(j // 7) + 11(i // 3)) mod 256,
-    then the fp16 scale (and, for the affine formats, the fp16 minimum of the
-    next scale) over the first bytes."""
+    then the fp16 scale d (at byte 208 for q6_k, else 0) and, for the formats
+    with a minimum, the fp16 of the next scale right after it."""
     size = oracle.packed_block_bytes(fmt)
     i = np.arange(64)[:, None]
     j = np.arange(size)[None, :]
     blocks = ((j * 73 + i * 29 + (j // 7) * 17 + (i // 3) * 11) & 255).astype(np.uint8)
+    at = 208 if fmt == "gguf:q6_k" else 0
     d = oracle.f32_to_f16_bits(np.array([scales[k % 8] for k in range(64)], np.float32))
-    blocks[:, 0], blocks[:, 1] = d & 255, d >> 8
+    blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
     if fmt in AFFINE:
         m = oracle.f32_to_f16_bits(np.array([scales[(k + 1) % 8] for k in range(64)], np.float32))
-        blocks[:, 2], blocks[:, 3] = m & 255, m >> 8
+        blocks[:, at + 2], blocks[:, at + 3] = m & 255, m >> 8
     return blocks.reshape(-1)
 
 
@@ -36,7 +42,7 @@ def fnv1a64(values: np.ndarray) -> str:
 def test_ggml_oracle_hashes(oracle, golden, fmt):
     g = golden["dequantize_packed_gguf"]
     x = corpus(oracle, fmt, g["corpus_scales"])
-    y = oracle.dequantize_packed(x, fmt, (2, 32 * 32))
+    y = oracle.dequantize_packed(x, fmt, (2, 32 * block_values(fmt)))
     assert fnv1a64(y) == g["fnv1a64"][fmt]
 
 
@@ -66,3 +72,34 @@ def test_layouts_by_hand(oracle):
     blk[2] = 0x0F
     y = oracle.dequantize_packed(blk, "gguf:iq4_nl", (32,))
     assert y[0] == 113.0 and y[16] == -127.0
+
+
+def test_k_quant_layouts_by_hand(oracle):
+    # q4_k: d = 1, dmin = 0.5; sub-block 0 scale 3 / minimum 2 (bytes 4, 8);
+    # sub-block 5 scale (byte 13 & 15) | ((byte 5 >> 6) << 4) = 4 | 16,
+    # minimum (byte 13 >> 4) | ((byte 9 >> 6) << 4) = 0; byte 5 is also
+    # sub-block 1's scale (& 63 = 0)
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[2:4] = [0x00, 0x38]
+    blk[4] = 3
+    blk[8] = 2
+    blk[16] = 0xA7          # element 0 -> 7 (low nibble), element 32 -> 10 (high nibble)
+    blk[5] = 0x40
+    blk[13] = 0x04
+    y = oracle.dequantize_packed(blk, "gguf:q4_k", (256,))
+    assert y[0] == 3 * 7 - 0.5 * 2
+    assert y[32] == 0.0  # sub-block 1: scale 0, minimum 0
+    # element 168 = sub-block 5, byte (168 // 64) * 32 + 168 % 32 = 72, high nibble
+    blk[16 + 72] = 0x90
+    y = oracle.dequantize_packed(blk, "gguf:q4_k", (256,))
+    assert y[168] == (4 | 16) * 9
+    # q6_k: d = 2 at byte 208, scale -3 for values 0..15; value 0 = (0x5 | (2 << 4)) - 32 = 5
+    blk = np.zeros(210, np.uint8)
+    blk[208:210] = [0x00, 0x40]
+    blk[192] = 0xFD
+    blk[0] = 0x05
+    blk[128] = 0x02
+    y = oracle.dequantize_packed(blk, "gguf:q6_k", (256,))
+    assert y[0] == 2 * -3 * (0x25 - 32)
+    assert y[1] == 2 * -3 * -32

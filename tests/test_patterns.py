@@ -180,8 +180,9 @@ def test_packed_rewrite(pt):
 
 
 @pytest.mark.parametrize("kw,reason", [
-    ({"fmt": "gguf:q4_k"}, "format has no fused kernel"),
-    ({"shape": (96, 96)}, "K is not a multiple of 64"),
+    ({"fmt": "gguf:q5_k"}, "format has no fused kernel"),
+    ({"shape": (96, 96)}, "K does not fit the fused GEMV"),
+    ({"fmt": "gguf:q6_k", "shape": (96, 128)}, "K does not fit the fused GEMV"),
     ({"shape": (2, 96, 128)}, "DequantizePacked shape is not [N, K]"),
     ({"odt": 1}, "DequantizePacked output is not FLOAT16"),
     ({"perm": [0, 1]}, "Transpose is not a 2-D transpose"),
