@@ -143,6 +143,18 @@ __device__ __forceinline__ unsigned HighHalves(v2f f) {
   return r;
 }
 
+// One direct load: lane i's 16 bytes at `voffset` land at LDS address
+// lds + 16 i (M0 holds the wave's LDS base).  Written as inline assembly so
+// the compiler does not track the LDS write: it cannot tell which ring stage
+// a load fills, and before LDS reads of another stage it waited for loads
+// still in flight (s_waitcnt vmcnt(3..12) inside the K loop).  The ring's
+// own waits (RingBarrier) order every read after the loads of its stage; the
+// statements are volatile, so they keep their order against the barriers.
+__device__ __forceinline__ void DirectLoad16(__amdgpu_buffer_rsrc_t rs, const char *lds, unsigned voffset) {
+  const unsigned m0 = (unsigned)(size_t)(lds_ptr_t)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rs), "{m0}"(m0));
+}
+
 // Waits for all but the newest `L` direct loads (the oldest in-flight ring
 // stage has then landed), retires this wave's LDS reads and joins the
 // workgroup barrier.  A __syncthreads() would wait for every load.
@@ -411,11 +423,11 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       if (q >= lo && q < hi)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(sa + (8 * wave + q) * 1024), 16, a_g[q] + ka, 0, 0, 0);
+        DirectLoad16(rsa, sa + (8 * wave + q) * 1024, a_g[q] + ka);
 #pragma unroll
     for (int q = 0; q < LB; ++q)
       if (8 + q >= lo && 8 + q < hi)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(sb + (wave * LB + q) * 1024), 16, b_g[q] + kb, 0, 0, 0);
+        DirectLoad16(rsb, sb + (wave * LB + q) * 1024, b_g[q] + kb);
   };
 
   // ---- fragments ----

@@ -159,7 +159,11 @@ def test_qlinear_known_answers(olamd, golden, dev):
 
 @pytest.mark.parametrize("shapes", [((64, 256), (256, 128)), ((300, 200), (200, 136)),
                                     ((2, 96, 64), (64, 80)), ((3, 17, 40), (3, 40, 24)),
-                                    ((1024, 512), (512, 384))])
+                                    ((1024, 512), (512, 384)),
+                                    # whole K steps without zero-point sums (the K-split
+                                    # waves): one, three and five steps, tails, batches
+                                    ((300, 384), (384, 136)), ((3, 50, 128), (3, 128, 48)),
+                                    ((257, 640), (640, 272))])
 @pytest.mark.parametrize("dts", [(np.uint8, np.int8, np.uint8), (np.int8, np.int8, np.int8),
                                  (np.uint8, np.uint8, np.int8), (np.int8, np.uint8, np.uint8)],
                          ids=["u8s8-u8", "s8s8-s8", "u8u8-s8", "s8u8-u8"])
