@@ -873,6 +873,34 @@ void LaunchConvGemm(const ConvGeom &g, const uint8_t *w, int w_u8, const uint8_t
   LaunchIGemm(ConvGemmParams(g, w, w_u8, a_zp, w_zp, col, x_u8, x_zp, y), stream);
 }
 
+// The implicit GEMM (no im2col matrix in HBM) for group-1 2-D convolutions
+// with C % 128 == 0 (ConvImplicitEligible) and a 16-byte aligned output.  Its
+// scratch holds the zero-point-padded NHWC input, then the tap-major weight.
+bool ConvImplicit(const ConvGeom &g, const onnxl_amd_tensor &y) {
+  return ConvImplicitEligible(g) &&
+         (y.location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(y.data) % 16 == 0);
+}
+
+size_t ConvImplicitScratch(const ConvGeom &g) {
+  return Scratch::Round(ConvImplicitInputBytes(g)) + (size_t)(g.M * g.Kc);
+}
+
+// Launches the two operand passes into `scratch` and returns the GEMM over
+// them: A = the tap-major weight [M, Kc], B = one padded image per batch entry.
+IGemmParams ConvImplicitGemm(const ConvGeom &g, const uint8_t *x, int x_u8, int32_t x_zp, const uint8_t *w,
+                             int w_u8, const uint8_t *a_zp, int32_t w_zp, void *y, void *scratch,
+                             hipStream_t stream) {
+  uint8_t *xh = static_cast<uint8_t *>(scratch);
+  uint8_t *wr = xh + Scratch::Round(ConvImplicitInputBytes(g));
+  LaunchConvImplicitOperands(g, x, (uint8_t)x_zp, w, xh, wr, stream);
+  IGemmParams p = ConvGemmParams(g, wr, w_u8, a_zp, w_zp, xh, x_u8, x_zp, y);
+  p.implicit_conv = 1;
+  p.cv = ConvImplicitDesc(g);
+  p.bm.b_stride[0] = p.cv.image_bytes;  // group 1: one padded image per batch entry
+  p.bm.b_stride[1] = 0;
+  return p;
+}
+
 int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnxl_amd_tensor *x_zp,
                 const onnxl_amd_tensor *w_zp, const onnxl_amd_conv_attrs *attrs, onnxl_amd_tensor *y,
                 hipStream_t stream) {
@@ -906,14 +934,19 @@ int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnx
   const int32_t xz = xz_present ? ReadIntElem(*x_zp, 0) : 0;
   const int32_t wz = wz_present && !w_per_channel ? ReadIntElem(*w_zp, 0) : 0;
   const bool gemm = (g.G == 1 || !w_per_channel) && g.Kc > 0;
-  const size_t col_bytes = gemm ? ConvColBytes(g) : 0;
+  const bool implicit = gemm && ConvImplicit(g, *y);
+  const size_t col_bytes = implicit ? ConvImplicitScratch(g) : (gemm ? ConvColBytes(g) : 0);
   Staging st(stream, col_bytes, {x, w, w_per_channel ? w_zp : nullptr}, {y});
   const uint8_t *xd = static_cast<const uint8_t *>(st.In(x));
   const uint8_t *wd = static_cast<const uint8_t *>(st.In(w));
   const uint8_t *wzd = w_per_channel ? static_cast<const uint8_t *>(st.In(w_zp)) : nullptr;
   int32_t *yd = static_cast<int32_t *>(st.Out(y));
   if (g.N * g.M * g.P > 0) {
-    if (gemm) {
+    if (implicit) {
+      LaunchIGemm(ConvImplicitGemm(g, xd, x->data_type == kUint8, xz, wd, w->data_type == kUint8, wzd, wz, yd,
+                                   st.Extra(), stream),
+                  stream);
+    } else if (gemm) {
       const uint8_t *col = xd;
       if (!ConvColIsInput(g)) {
         col = static_cast<uint8_t *>(st.Extra());
@@ -992,9 +1025,10 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   const int64_t w_span = w_per_channel ? 255 : span(w->data_type, wz);
   const bool exact32 = (double)g.Kc * (double)span(x->data_type, xz) * (double)w_span < 2147483648.0;
   const bool gemm = exact32 && (g.G == 1 || !w_per_channel) && g.Kc > 0;
-  const size_t col_bytes = gemm ? ConvColBytes(g) : 0;
+  const bool implicit = gemm && ConvImplicit(g, *y);  // the GEMM epilogue requantizes
+  const size_t col_bytes = implicit ? ConvImplicitScratch(g) : (gemm ? ConvColBytes(g) : 0);
   const size_t acc_off = Scratch::Round(col_bytes);
-  const size_t acc_bytes = gemm ? (size_t)(g.N * g.M * g.P) * 4 : 0;
+  const size_t acc_bytes = gemm && !implicit ? (size_t)(g.N * g.M * g.P) * 4 : 0;
   Staging st(stream, acc_off + acc_bytes, {x, w, w_scale, w_per_channel ? w_zp : nullptr, has_bias ? bias : nullptr},
              {y});
   const uint8_t *xd = static_cast<const uint8_t *>(st.In(x));
@@ -1015,13 +1049,16 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
     if (gemm) {
       const uint8_t *col = xd;
       int32_t *acc = reinterpret_cast<int32_t *>(static_cast<char *>(st.Extra()) + acc_off);
-      if (!ConvColIsInput(g)) {
+      if (!implicit && !ConvColIsInput(g)) {
         col = static_cast<uint8_t *>(st.Extra());
         LaunchImToCol(g, xd, (uint8_t)xz, static_cast<uint8_t *>(st.Extra()), stream);
       }
       // group 1 on the pipelined kernel: the GEMM epilogue requantizes each
       // output channel's row itself; otherwise int32 sums, then the pass
-      IGemmParams p = ConvGemmParams(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, yd);
+      IGemmParams p = implicit ? ConvImplicitGemm(g, xd, x->data_type == kUint8, xz, wd, w->data_type == kUint8, wzd,
+                                                  wz, yd, st.Extra(), stream)
+                               : ConvGemmParams(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8,
+                                                xz, yd);
       p.epilogue = kEpiQuant8Row;
       p.zy = q.zy;
       p.qmin = q.qmin;
@@ -1032,7 +1069,7 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
       p.row_xs = q.x_scale;
       p.row_ys = q.y_scale;
       p.row_bias = q.bias;
-      if (g.G == 1 && IGemmFastEligible(p)) {
+      if (implicit || (g.G == 1 && IGemmFastEligible(p))) {
         LaunchIGemm(p, stream);
       } else {
         LaunchConvGemm(g, wd, w->data_type == kUint8, wzd, wz, col, x->data_type == kUint8, xz, acc, stream);

@@ -240,7 +240,131 @@ __global__ __launch_bounds__(kCBlock) void ConvRequantKernel(const ConvGeom g, c
 
 unsigned Blocks(int64_t threads) { return (unsigned)((threads + kCBlock - 1) / kCBlock); }
 
+// ---- implicit GEMM operands ----
+// The padded input rows and columns a convolution reads: Hp = (Ho - 1) sh +
+// (kh - 1) dh + 1 rows from input row -pt on (likewise Wp), so every tap of
+// every output position lands inside the padded image.
+constexpr int kCvChannels = 128;  // channels per K step
+constexpr int64_t kCvMaxLds = 65536;  // staged input row (C * W) or weight row (Kc) bytes
+
+int64_t PaddedRows(const ConvGeom &g) { return (g.out[1] - 1) * g.s[1] + (g.k[1] - 1) * g.d[1] + 1; }
+int64_t PaddedCols(const ConvGeom &g) { return (g.out[2] - 1) * g.s[2] + (g.k[2] - 1) * g.d[2] + 1; }
+
+// One launch builds both operands.  Blocks 0 .. N * Hp - 1 write padded row
+// hp of image n: xh[n, hp, wp, c] = x[n, c, hp - pt, wp - pl], or x's zero
+// point outside the input; the C input rows of W bytes are staged in LDS
+// (dword loads when W % 4 == 0 and x is dword aligned), then written as Wp
+// pixels of C bytes, one
+// dword of four channels per thread.  The remaining M blocks write one row of
+// the tap-major weight each, wr[m, tap, c] = w[m, c, tap], from the row
+// staged in LDS.
+__global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom g, int64_t Hp, int64_t Wp,
+                                                                  const uint8_t *x, uint8_t x_zp, const uint8_t *w,
+                                                                  uint8_t *xh, uint8_t *wr) {
+  extern __shared__ uint8_t tile[];  // C * W (input row) or Kc (weight row) bytes, below 2^16
+  // 32-bit index arithmetic inside the loops (64-bit division is a long
+  // software sequence): every per-block count is below 2^16
+  const uint32_t H = (uint32_t)g.in[1], W = (uint32_t)g.in[2], C = (uint32_t)g.C;
+  const int64_t b = blockIdx.x;
+  if (b < g.N * Hp) {
+    const int64_t n = b / Hp, hp = b - n * Hp, h = hp - g.pb[1];
+    const bool row_in = h >= 0 && h < (int64_t)H;
+    if (row_in) {
+      const uint8_t *src = x + (n * C * H + h) * W;  // channel c at + c * H * W
+      if (W % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 4 == 0) {
+        // consecutive threads on consecutive dwords of the channel rows
+        const uint32_t wd = W / 4;
+        for (uint32_t e = threadIdx.x; e < C * wd; e += kCBlock) {
+          const uint32_t c = e / wd, q = e - c * wd;
+          reinterpret_cast<uint32_t *>(tile)[e] = reinterpret_cast<const uint32_t *>(src + (size_t)c * H * W)[q];
+        }
+      } else {
+        for (uint32_t e = threadIdx.x; e < C * W; e += kCBlock) {
+          const uint32_t c = e / W;
+          tile[e] = src[(size_t)c * H * W + (e - c * W)];
+        }
+      }
+    }
+    __syncthreads();
+    uint32_t *dst = reinterpret_cast<uint32_t *>(xh + (n * Hp + hp) * Wp * C);
+    const uint32_t cq = C / 4, pl = (uint32_t)g.pb[2];
+    auto quad = [&](uint32_t wp, uint32_t qd) __attribute__((always_inline)) {
+      const uint32_t wi = wp - pl;  // wraps above W when wp < pl
+      uint32_t v = x_zp * 0x01010101u;
+      if (row_in && wp >= pl && wi < W) {
+        const uint8_t *t = tile + (4 * qd) * W + wi;
+        v = (uint32_t)t[0] | (uint32_t)t[W] << 8 | (uint32_t)t[2 * W] << 16 | (uint32_t)t[3 * W] << 24;
+      }
+      return v;
+    };
+    if (kCBlock % cq == 0) {
+      // fixed channel dword per thread, kCBlock / cq pixels per pass
+      const uint32_t qd = threadIdx.x % cq, step = kCBlock / cq;
+      for (uint32_t wp = threadIdx.x / cq; wp < (uint32_t)Wp; wp += step) dst[wp * cq + qd] = quad(wp, qd);
+    } else {
+      for (uint32_t e = threadIdx.x; e < (uint32_t)Wp * cq; e += kCBlock) {
+        const uint32_t wp = e / cq;
+        dst[e] = quad(wp, e - wp * cq);
+      }
+    }
+  } else {
+    const int64_t m = b - g.N * Hp;
+    const uint32_t T = (uint32_t)g.ks, Kc = (uint32_t)g.Kc, kq = Kc / 4;
+    if (reinterpret_cast<uintptr_t>(w) % 4 == 0) {
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(w + m * Kc);
+      for (uint32_t e = threadIdx.x; e < kq; e += kCBlock) reinterpret_cast<uint32_t *>(tile)[e] = src[e];
+    } else {
+      for (uint32_t e = threadIdx.x; e < Kc; e += kCBlock) tile[e] = w[m * Kc + e];
+    }
+    __syncthreads();
+    uint32_t *dst = reinterpret_cast<uint32_t *>(wr + m * Kc);
+    for (uint32_t e = threadIdx.x; e < kq; e += kCBlock) {
+      const uint32_t tap = (4 * e) / C, c = 4 * e - tap * C;
+      const uint8_t *t = tile + c * T + tap;
+      dst[e] = (uint32_t)t[0] | (uint32_t)t[T] << 8 | (uint32_t)t[2 * T] << 16 | (uint32_t)t[3 * T] << 24;
+    }
+  }
+}
+
+uint32_t Magic(int64_t d) { return d == 1 ? 0u : (uint32_t)(((uint64_t(1) << 32) + (uint64_t)d - 1) / (uint64_t)d); }
+
 }  // namespace
+
+bool ConvImplicitEligible(const ConvGeom &g) {
+  const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
+  if (g.G != 1 || g.in[0] != 1 || g.k[0] != 1 || g.C % kCvChannels != 0 || g.P % 16 != 0 || g.P == 0) return false;
+  const int64_t Hp = PaddedRows(g), Wp = PaddedCols(g);
+  return g.C * g.in[2] <= kCvMaxLds && g.Kc <= kCvMaxLds && g.N * Hp + g.M < (int64_t(1) << 31) &&
+         Hp * Wp * g.C < lim && g.M * g.Kc < lim && g.M * g.P * 4 < lim;
+}
+
+size_t ConvImplicitInputBytes(const ConvGeom &g) { return (size_t)(g.N * PaddedRows(g) * PaddedCols(g) * g.C); }
+
+ImplicitConv ConvImplicitDesc(const ConvGeom &g) {
+  const int64_t Wp = PaddedCols(g), C = g.C;
+  ImplicitConv cv{};
+  cv.pix_row = g.s[1] * Wp * C;
+  cv.pix_col = g.s[2] * C;
+  cv.tap_row = g.d[1] * Wp * C;
+  cv.tap_col = g.d[2] * C;
+  cv.image_bytes = PaddedRows(g) * Wp * C;
+  cv.wo = (int)g.out[2];
+  cv.spt = (int)(C / kCvChannels);
+  cv.kw = g.k[2];
+  cv.spt_magic = Magic(cv.spt);
+  cv.kw_magic = Magic(cv.kw);
+  return cv;
+}
+
+void LaunchConvImplicitOperands(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, const uint8_t *w, uint8_t *xh,
+                                uint8_t *wr, hipStream_t s) {
+  const int64_t Hp = PaddedRows(g), Wp = PaddedCols(g);
+  const int64_t blocks = g.N * Hp + g.M;
+  const unsigned lds = (unsigned)std::max<int64_t>(g.C * g.in[2], g.Kc);
+  if (blocks > 0)
+    hipLaunchKernelGGL(ImplicitOperandsKernel, dim3((unsigned)blocks), dim3(kCBlock), lds, s, g, Hp, Wp, x, x_zp, w,
+                       xh, wr);
+}
 
 bool ConvColIsInput(const ConvGeom &g) {
   for (int i = 0; i < 3; ++i)

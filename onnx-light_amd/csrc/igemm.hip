@@ -602,6 +602,12 @@ bool IGemmFastEligible(const IGemmParams &p) { return mg::Eligible<mg::kI8>(ToGe
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0 || p.batch == 0) return;
+  if (p.implicit_conv) {  // the caller checked the implicit operand's shape
+    if (p.epilogue == kEpiInt32) LaunchIGemmConvI32(p, stream);
+    else if (p.epilogue == kEpiQuant8Row) LaunchIGemmConvQ8Row(p, stream);
+    else throw DeviceError("internal: implicit convolution with a per-tensor requantization");
+    return;
+  }
   // K % 128 == 0: the pipelined MFMA core (mfma_gemm.hpp).
   if (mg::Eligible<mg::kI8>(ToGemmArgs(p))) {
     if (p.epilogue == kEpiInt32) LaunchIGemmFastI32(p, stream);

@@ -34,28 +34,32 @@ inline mg::GemmArgs ToGemmArgs(const IGemmParams &p) {
   g.row_xs = p.row_xs;
   g.row_ys = p.row_ys;
   g.row_bias = p.row_bias;
+  g.cv = p.cv;
   return g;
 }
 
 // Row / column sums are accumulated only when a zero point makes them count.
-template <int OUT> void LaunchIGemmFastOut(const IGemmParams &p, hipStream_t s) {
+// CV: B is an implicit convolution operand (p.implicit_conv).
+template <int OUT, bool CV = false> void LaunchIGemmFastOut(const IGemmParams &p, hipStream_t s) {
   const mg::GemmArgs g = ToGemmArgs(p);
   const bool zp = p.need_ra || p.need_cb;
   const int sel = (zp ? 4 : 0) | (p.a_u8 ? 2 : 0) | (p.b_u8 ? 1 : 0);
   switch (sel) {
-  case 0: mg::Launch<mg::kI8, OUT, false, false, false>(g, s); break;
-  case 1: mg::Launch<mg::kI8, OUT, false, false, true>(g, s); break;
-  case 2: mg::Launch<mg::kI8, OUT, false, true, false>(g, s); break;
-  case 3: mg::Launch<mg::kI8, OUT, false, true, true>(g, s); break;
-  case 4: mg::Launch<mg::kI8, OUT, true, false, false>(g, s); break;
-  case 5: mg::Launch<mg::kI8, OUT, true, false, true>(g, s); break;
-  case 6: mg::Launch<mg::kI8, OUT, true, true, false>(g, s); break;
-  default: mg::Launch<mg::kI8, OUT, true, true, true>(g, s); break;
+  case 0: mg::Launch<mg::kI8, OUT, false, false, false, 2, CV>(g, s); break;
+  case 1: mg::Launch<mg::kI8, OUT, false, false, true, 2, CV>(g, s); break;
+  case 2: mg::Launch<mg::kI8, OUT, false, true, false, 2, CV>(g, s); break;
+  case 3: mg::Launch<mg::kI8, OUT, false, true, true, 2, CV>(g, s); break;
+  case 4: mg::Launch<mg::kI8, OUT, true, false, false, 2, CV>(g, s); break;
+  case 5: mg::Launch<mg::kI8, OUT, true, false, true, 2, CV>(g, s); break;
+  case 6: mg::Launch<mg::kI8, OUT, true, true, false, 2, CV>(g, s); break;
+  default: mg::Launch<mg::kI8, OUT, true, true, true, 2, CV>(g, s); break;
   }
 }
 
 void LaunchIGemmFastI32(const IGemmParams &p, hipStream_t s);
 void LaunchIGemmFastQ8(const IGemmParams &p, hipStream_t s);
 void LaunchIGemmFastQ8Row(const IGemmParams &p, hipStream_t s);
+void LaunchIGemmConvI32(const IGemmParams &p, hipStream_t s);
+void LaunchIGemmConvQ8Row(const IGemmParams &p, hipStream_t s);
 
 }  // namespace onnxl_amd

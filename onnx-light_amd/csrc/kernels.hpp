@@ -44,6 +44,24 @@ __host__ __device__ inline void BatchOffsets(const BatchMap &m, int64_t batch, i
 
 enum IGemmEpilogue : int { kEpiInt32 = 0, kEpiQuant8 = 1, kEpiQuant8Row = 2 };
 
+// Implicit convolution operand: B is not a [K, N] matrix but one image of the
+// zero-point-padded input in NHWC order, [Hp, Wp, C] bytes, and K runs over
+// (kernel tap, channel) with C % 128 == 0, so a K step of 128 bytes is 128
+// channels of one tap.  Output position n = (oh, ow) = (n / wo, n % wo) reads
+// B row pixel (oh * stride_h + i * dilation_h, ow * stride_w + j * dilation_w)
+// for tap (i, j): byte n_off(n) + t_off(t) + 16 * chunk with
+//   n_off = oh * pix_row + ow * pix_col,
+//   t_off = i * tap_row + j * tap_col + 128 * (t % spt),  tap = t / spt.
+struct ImplicitConv {
+  int64_t pix_row, pix_col;  // stride_h * Wp * C, stride_w * C
+  int64_t tap_row, tap_col;  // dilation_h * Wp * C, dilation_w * C
+  int64_t image_bytes;       // Hp * Wp * C
+  int wo;                    // output width
+  int spt;                   // K steps per tap: C / 128
+  int kw;                    // kernel width
+  uint32_t spt_magic, kw_magic;  // ceil(2^32 / d) (0 for d = 1): q = mulhi(x, magic)
+};
+
 struct IGemmParams {
   const int8_t *A;  // [.., M, K] row-major
   const int8_t *B;  // [.., K, N] row-major
@@ -70,6 +88,9 @@ struct IGemmParams {
   int row_wscale_per;
   float row_xs, row_ys;
   const int32_t *row_bias;
+  // B is an implicit convolution operand (pipelined kernel only)
+  int implicit_conv;
+  ImplicitConv cv;
 };
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
@@ -121,6 +142,15 @@ struct ConvQuant {
 // ([N, C, P] is [N, G, Kc, P]); no im2col pass, ConvColBytes 0.
 bool ConvColIsInput(const ConvGeom &g);
 size_t ConvColBytes(const ConvGeom &g);
+// Implicit GEMM (group 1, 2-D, C % 128 == 0, P % 16 == 0, C * W and Kc <= 64 KB):
+// the padded NHWC input (ConvImplicitInputBytes) and the tap-major weight
+// (M * Kc bytes) replace the im2col matrix; ConvImplicitDesc describes the B
+// operand for IGemmParams::cv (one image per batch entry).
+bool ConvImplicitEligible(const ConvGeom &g);
+size_t ConvImplicitInputBytes(const ConvGeom &g);
+ImplicitConv ConvImplicitDesc(const ConvGeom &g);
+void LaunchConvImplicitOperands(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, const uint8_t *w, uint8_t *xh,
+                                uint8_t *wr, hipStream_t stream);
 void LaunchImToCol(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, uint8_t *col, hipStream_t stream);
 // q == nullptr: ConvInteger (int32 output); else QLinearConv (8-bit output).
 // w_zp_per_channel: M device bytes, or nullptr for the value w_zp_scalar.

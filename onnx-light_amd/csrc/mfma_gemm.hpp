@@ -204,17 +204,30 @@ struct GemmArgs {
   int grp_sel;                  // row of A of Y row r: r / grp_sel
   int64_t grp_b_stride;         // elements from one group's B to the next
   const void *grp_bias;         // [grp_count, N] in the output dtype, or null
+  // Implicit convolution (kernels with CV): B per batch entry is one image of
+  // the padded NHWC input, read like A (rows = output positions).
+  ImplicitConv cv;
 };
+
+// x / d for x, d < 2^16 from magic = ceil(2^32 / d) (0 for d = 1).
+__device__ __forceinline__ uint32_t DivMagic(uint32_t x, uint32_t magic) {
+  return magic ? __umulhi(x, magic) : x;
+}
 
 // GM: 0 one GEMM per batch entry; 1 grouped with each group's B [K, N]
 // row-major; 2 grouped with each group's B given transposed, [N, K]
 // row-major (kH16 only): its stage is then loaded and read like A's, rows of
 // N with consecutive k, which is exactly the B operand of the MFMA.
-template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB, int GM = 0>
+//
+// CV: implicit convolution (int8): B is read like A, its row for output
+// position n and K step t at the byte offset of GemmArgs::cv, so the im2col
+// matrix is never written.
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB, int GM = 0, bool CV = false>
 __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) {
   constexpr bool RA = ZP, CB = ZP;
-  constexpr bool BT = GM == 2;
+  constexpr bool BT = GM == 2 || CV;
   static_assert(GM == 0 || (KIND == kH16 && WB == 2 && !ZP), "grouped mode: 16-bit operands, 128-column tiles");
+  static_assert(!CV || (KIND == kI8 && WB == 2 && GM == 0), "implicit convolution: int8, 128-column tiles");
   using T = Traits<KIND>;
   using Acc = typename T::Acc;
   constexpr int kBN = 64 * WB;                 // workgroup tile columns
@@ -310,8 +323,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   const int64_t NW = N * kBsz;    // bytes of a B row inside the computed columns
   const __amdgpu_buffer_rsrc_t rsA =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, (int)(M * KA), kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rsB =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, (int)(BT ? N * KA : K * NB), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(Bb), (short)0, (int)(CV ? p.cv.image_bytes : (BT ? N * KA : K * NB)), kRsrcWord3);
   // look-ahead loads past the last K step go through empty descriptors (every
   // access out of range): a scalar select instead of a per-lane one
   const __amdgpu_buffer_rsrc_t rsA0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, 0, kRsrcWord3);
@@ -337,7 +350,13 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
   for (int q = 0; q < LB; ++q) {
     const int i = wave * LB + q;  // 1 KB piece of the B stage
-    if constexpr (BT) {
+    if constexpr (CV) {
+      // output position n: its input pixel for tap (0, 0) and channel chunk
+      const int64_t n = col0 + 8 * i + (lane >> 3);
+      const int64_t oh = n / p.cv.wo, ow = n - oh * p.cv.wo;
+      b_g[q] = n < N ? (unsigned)(oh * p.cv.pix_row + ow * p.cv.pix_col + 16 * ((lane & 7) ^ (lane >> 3) ^ (i & 1)))
+                     : kOob;
+    } else if constexpr (BT) {
       // rows of N like A's rows of M: 8 rows of 128 bytes per piece
       const int64_t n = col0 + 8 * i + (lane >> 3);
       b_g[q] = n < N ? (unsigned)(n * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (i & 1))) : kOob;
@@ -415,7 +434,14 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   auto issue = [&](int step, int stage, int part) __attribute__((always_inline)) {
     const bool live = step < nk;
     const unsigned ka = (unsigned)step * kStepBytes;
-    const unsigned kb = BT ? (unsigned)step * kStepBytes : (unsigned)((int64_t)step * T::kBRows * NB);
+    unsigned kb = BT ? (unsigned)step * kStepBytes : (unsigned)((int64_t)step * T::kBRows * NB);
+    if constexpr (CV) {
+      // tap (i, j) and channel block of this step (scalar arithmetic)
+      const uint32_t tap = DivMagic((uint32_t)step, p.cv.spt_magic);
+      const uint32_t ti = DivMagic(tap, p.cv.kw_magic);
+      kb = (unsigned)(ti * p.cv.tap_row + (tap - ti * (uint32_t)p.cv.kw) * p.cv.tap_col +
+                      kStepBytes * ((uint32_t)step - tap * (uint32_t)p.cv.spt));
+    }
     char *sa = SA(stage);
     char *sb = SB(stage);
     const __amdgpu_buffer_rsrc_t rsa = live ? rsA : rsA0, rsb = live ? rsB : rsB0;
@@ -937,11 +963,11 @@ template <int KIND> inline bool Eligible(const GemmArgs &p) {
          p.M * ldy * 4 < lim && (p.K + 3 * Traits<KIND>::kKStep) * ldb * kBsz < lim;
 }
 
-template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB = 2>
+template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB = 2, bool CV = false>
 inline void Launch(const GemmArgs &p, hipStream_t s) {
   constexpr int kBN = 64 * WB;
   const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
-  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8, WB>), dim3((unsigned)tiles), dim3(kThreads),
+  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8, WB, 0, CV>), dim3((unsigned)tiles), dim3(kThreads),
                      0, s, p);
 }
 

@@ -2,11 +2,12 @@
 reference's known answers: bit-exact (int32 sums; 8-bit requantized
 outputs).
 
-Cases cover both GPU paths: im2col + the int8 MFMA GEMM (group 1, or any
-group with a scalar weight zero point; the fast GEMM kernel when K is a
-multiple of 64 and the output plane of 16) and the direct kernel (grouped
-convolutions with per-channel weight zero points, and QLinearConv sums past
-exact int32).  Attributes: strides, dilations, explicit and automatic
+Cases cover the three GPU paths: the implicit GEMM (group 1, C % 128 == 0,
+P % 16 == 0: the padded NHWC input read by the int8 MFMA GEMM, no im2col
+matrix), im2col + the int8 MFMA GEMM (group 1, or any group with a scalar
+weight zero point; the fast GEMM kernel when K is a multiple of 64 and the
+output plane of 16) and the direct kernel (grouped convolutions with
+per-channel weight zero points, and QLinearConv sums past exact int32).  Attributes: strides, dilations, explicit and automatic
 padding, 1-D to 3-D.  At the bench shape [32, 256, 28, 28] the output is
 checked against the oracle on exact slices (each output depends only on its
 image and channel)."""
@@ -62,6 +63,14 @@ CASES = [
     ((2, 64, 16, 16), (96, 64, 3, 3), dict(pads=[1, 1, 1, 1])),          # fast GEMM: K = 576, P = 256
     ((1, 128, 14, 14), (64, 128, 1, 1), dict()),                          # 1x1, P = 196
     ((2, 32, 12, 12), (32, 1, 3, 3), dict(group=32, pads=[1, 1, 1, 1])),  # depthwise
+    # implicit GEMM (group 1, C % 128 == 0, P % 16 == 0): padded NHWC input
+    ((2, 128, 8, 8), (40, 128, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ((1, 128, 16, 16), (24, 128, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ((2, 128, 12, 12), (16, 128, 3, 3), dict(dilations=[2, 2], pads=[2, 2, 2, 2])),
+    ((1, 128, 8, 20), (8, 128, 1, 5), dict(pads=[0, 2, 0, 2])),
+    ((1, 256, 4, 8), (300, 256, 1, 1), dict()),
+    ((1, 128, 8, 8), (16, 128, 3, 3), dict(strides=[2, 2], auto_pad="SAME_UPPER")),
+    ((2, 128, 48), (16, 128, 3), dict(pads=[1, 1])),
 ]
 
 
@@ -118,8 +127,8 @@ def test_qlinear_conv_past_exact_int32(olamd, oracle, dev):
 
 def test_bench_shape_slices(olamd, oracle, dev):
     """The bench layer: x u8 [32, 256, 28, 28], w s8 [256, 256, 3, 3], pads 1,
-    per-channel w_scale and bias, on the im2col + MFMA GEMM path; images 0 and
-    31 and channels 0-15 and 240-255 against the oracle."""
+    per-channel w_scale and bias, on the implicit-GEMM path; images 0 and 31
+    and channels 0-15 and 240-255 against the oracle."""
     rng = np.random.default_rng(11)
     x = rng.integers(0, 256, (32, 256, 28, 28)).astype(np.uint8)
     w = rng.integers(-128, 128, (256, 256, 3, 3)).astype(np.int8)
