@@ -17,14 +17,15 @@ oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
-                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|moe]
+                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q4k|pkgemv_q6k|moe]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
-GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 GEMVs (`pkgemv`,
-`pkgemv8`) and a Mixtral-shaped MoE GroupedMatMul (`moe`) are timed too and
+GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q4_k / q6_k GEMVs
+(`pkgemv`, `pkgemv8`, `pkgemv_q4k`, `pkgemv_q6k`) and a Mixtral-shaped MoE
+GroupedMatMul (`moe`) are timed too and
 reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
 25,604,096 bytes with the same replica rotation (libonnxl_amd_bench.so): the
 rate a kernel that only reads those bytes reaches, beside which the GEMV's
@@ -234,23 +235,31 @@ def make_pk(olamd, dev, replicas):
     return w
 
 
+PKGEMV_KEYS = {"q4_0": "pkgemv", "q8_0": "pkgemv8", "q4_k": "pkgemv_q4k", "q6_k": "pkgemv_q6k"}
+PK_BLOCK = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210)}  # values, bytes
+
+
 def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
-    """Fused GEMV y[1, 14336] = a[1, 4096] @ DequantizePacked(gguf:q4_0 or
-    gguf:q8_0, [14336, 4096], FLOAT16)^T: the weight's 18 (q4_0) or 34 (q8_0)
-    bytes per 32 values dominate."""
+    """Fused GEMV y[1, 14336] = a[1, 4096] @ DequantizePacked(gguf:<fmt>,
+    [14336, 4096], FLOAT16)^T: the weight's 18 (q4_0) or 34 (q8_0) bytes per
+    32 values, or 144 (q4_k) or 210 (q6_k) per 256, dominate."""
     import torch
     w = Workload()
-    block_bytes = {"q4_0": 18, "q8_0": 34}[fmt]
+    per, block_bytes = PK_BLOCK[fmt]
     w.name = f"GEMV fp16[1,4096] x DequantizePacked(gguf:{fmt} [14336,4096])^T -> fp16[1,14336]"
-    w.key = "pkgemv" if fmt == "q4_0" else "pkgemv8"
+    w.key = PKGEMV_KEYS[fmt]
     w.unit, w.dtype, w.bound = "GB/s", "f16 (fp32 accumulate)", "hbm"
     N, K = 14336, 4096
-    w.nbytes = N * K // 32 * block_bytes + K * 2 + N * 2
+    w.nbytes = N * K // per * block_bytes + K * 2 + N * 2
     w.work = float(w.nbytes)
     rng = np.random.default_rng(41)
-    blocks = rng.integers(0, 256, (N * K // 32, block_bytes)).astype(np.uint8)
-    d = np.float16(rng.uniform(0.001, 0.05, N * K // 32)).view(np.uint16)
-    blocks[:, 0], blocks[:, 1] = d & 255, d >> 8
+    blocks = rng.integers(0, 256, (N * K // per, block_bytes)).astype(np.uint8)
+    at = 208 if fmt == "q6_k" else 0  # the fp16 d
+    d = np.float16(rng.uniform(0.001, 0.05, N * K // per)).view(np.uint16)
+    blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
+    if fmt == "q4_k":  # dmin
+        m = np.float16(rng.uniform(0.001, 0.05, N * K // per)).view(np.uint16)
+        blocks[:, 2], blocks[:, 3] = m & 255, m >> 8
     a = _t(np.float16(rng.standard_normal((1, K))), dev)
     w.calls = []
     for _ in range(replicas):
@@ -613,7 +622,7 @@ def value_of(w, ms):
 
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
-             "pkgemv8", "moe")
+             "pkgemv8", "pkgemv_q4k", "pkgemv_q6k", "moe")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
                  "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
 
@@ -663,6 +672,9 @@ def main():
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 18))
         if key == "pkgemv8":
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 34), "q8_0")
+        if key in ("pkgemv_q4k", "pkgemv_q6k"):
+            fmt = "q4_k" if key == "pkgemv_q4k" else "q6_k"
+            return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 256 * PK_BLOCK[fmt][1]), fmt)
         if key == "moe":
             return make_moe(olamd, dev)
         if key == "c3_stream_ceiling":

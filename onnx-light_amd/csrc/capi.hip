@@ -1183,8 +1183,10 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
   Staging st(stream, 0, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
   if (q4k || q6k) {
-    if (M > 8 || K == 0 || reinterpret_cast<uintptr_t>(ad) % 16 != 0)
-      throw Unsupported("DequantizePackedMatMul: k-quant GEMV needs 1 <= M <= 8, K > 0 and 16-byte aligned a");
+    if (M > 8 || K == 0 || reinterpret_cast<uintptr_t>(ad) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(xd) % (q4k ? 16 : 2) != 0)
+      throw Unsupported("DequantizePackedMatMul: k-quant GEMV needs 1 <= M <= 8, K > 0, 16-byte aligned a and "
+                        "x aligned to 16 (q4_k) or 2 (q6_k) bytes");
     LaunchGemvK(q4k ? 12 : 14, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
                 static_cast<uint16_t *>(st.Out(y)), stream);
   } else {

@@ -467,44 +467,143 @@ __global__ __launch_bounds__(256) void GemvQ80Kernel(const uint16_t *__restrict_
 // 256-value blocks of output n contiguous along k).  A workgroup computes 16
 // outputs, 4 per wave; within a wave, lanes 0-31 and 32-63 take alternate
 // blocks, each lane 8 consecutive values of its block.  A lane decodes its 8
-// values per output with the reference's fp32 steps, rounds them to FLOAT16
-// (the chain's DequantizePacked output) and accumulates with the activations
-// through v_dot2_f32_f16 in fp32.
+// values per output with the reference's fp32 steps (two roundings, no
+// contraction), rounds them to FLOAT16 (the chain's DequantizePacked output)
+// and accumulates with the activations through v_dot2_f32_f16 in fp32.  A
+// NaN weight makes the sum NaN whatever its sign, so the decode here skips
+// the x86-64 NaN selection of the DequantizePacked kernel.
+//
+// Loads per lane and output: q4_k one 16-byte header (d, dmin, the 12 scale
+// bytes; every block starts 16-byte aligned as 144 = 9 x 16) and one 8-byte
+// run of codes; q6_k (210-byte blocks, 2-byte aligned) four 16-bit loads of
+// low nibbles, four of high bits, the sub-block's scale byte and d.
+__device__ __forceinline__ void NibbleFloats(uint32_t dw, int sh, float *f) {
+  const uint32_t t = (dw >> sh) & 0x0f0f0f0fu;
+  f[0] = (float)(t & 0xffu);
+  f[1] = (float)((t >> 8) & 0xffu);
+  f[2] = (float)((t >> 16) & 0xffu);
+  f[3] = (float)((t >> 24) & 0xffu);
+}
+
+// The raw bytes one lane needs from one block, loaded a block ahead of use.
+template <int TYPE> struct KRaw;
+template <> struct KRaw<12> {
+  uint32_t h[4];  // d, dmin, the 12 scale bytes
+  uint32_t q[2];  // 8 code bytes
+};
+template <> struct KRaw<14> {
+  uint32_t l[2], hb[2];  // 8 low-nibble bytes, 8 high-bit bytes
+  uint32_t d, sc;        // fp16 d, the sub-block's int8 scale
+};
+
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<12> &r) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  const v4u hdr = *reinterpret_cast<const v4u *>(p);
+  const v2u q = *reinterpret_cast<const v2u *>(p + 16 + (i0 >> 6) * 32 + (i0 & 31));
+  r.h[0] = hdr.x, r.h[1] = hdr.y, r.h[2] = hdr.z, r.h[3] = hdr.w;
+  r.q[0] = q.x, r.q[1] = q.y;
+}
+
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<14> &r) {
+  const uint16_t *ql = reinterpret_cast<const uint16_t *>(p + (i0 >> 7) * 64 + (i0 & 63));
+  const uint16_t *qh = reinterpret_cast<const uint16_t *>(p + 128 + (i0 >> 7) * 32 + (i0 & 31));
+  r.l[0] = ql[0] | (uint32_t)ql[1] << 16, r.l[1] = ql[2] | (uint32_t)ql[3] << 16;
+  r.hb[0] = qh[0] | (uint32_t)qh[1] << 16, r.hb[1] = qh[2] | (uint32_t)qh[3] << 16;
+  r.d = *reinterpret_cast<const uint16_t *>(p + 208);
+  r.sc = p[192 + (i0 >> 4)];
+}
+
+__device__ __forceinline__ void DecodeK(const KRaw<12> &r, int i0, h2_t wp[4]) {
+  const float d = F16ToF32((uint16_t)(r.h[0] & 0xffffu)), dmin = F16ToF32((uint16_t)(r.h[0] >> 16));
+  const int g = i0 >> 5;
+  // scale bytes 0..11 are h[1], h[2], h[3]; sub-block g uses byte g % 4 of
+  // each (field extracts, no indexed access into r)
+  const int sh = 8 * (g & 3);
+  const uint32_t b1 = (r.h[1] >> sh) & 0xffu, b2 = (r.h[2] >> sh) & 0xffu, b3 = (r.h[3] >> sh) & 0xffu;
+  const uint32_t scale = g < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
+  const uint32_t minimum = g < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+  const float ds = d * (float)scale, dm = dmin * (float)minimum;
+  float f[8];
+  NibbleFloats(r.q[0], 4 * (g & 1), f);
+  NibbleFloats(r.q[1], 4 * (g & 1), f + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float v0 = ds * f[2 * e] - dm, v1 = ds * f[2 * e + 1] - dm;
+    wp[e] = h2_t{(_Float16)v0, (_Float16)v1};
+  }
+}
+
+__device__ __forceinline__ void DecodeK(const KRaw<14> &r, int i0, h2_t wp[4]) {
+  const float ds = F16ToF32((uint16_t)r.d) * (float)(int8_t)r.sc;
+  const int shl = 4 * ((i0 >> 6) & 1), shh = 2 * ((i0 >> 5) & 3);
+  float f[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // q = low nibble | (2 high bits << 4), as the bytes of a dword
+    const uint32_t q = ((r.l[h] >> shl) & 0x0f0f0f0fu) | (((r.hb[h] >> shh) & 0x03030303u) << 4);
+    f[4 * h] = (float)(q & 0xffu);
+    f[4 * h + 1] = (float)((q >> 8) & 0xffu);
+    f[4 * h + 2] = (float)((q >> 16) & 0xffu);
+    f[4 * h + 3] = (float)((q >> 24) & 0xffu);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // (q - 32) is exact in fp32, then one rounded multiply, as the reference
+    const float v0 = ds * (f[2 * e] - 32.f), v1 = ds * (f[2 * e + 1] - 32.f);
+    wp[e] = h2_t{(_Float16)v0, (_Float16)v1};
+  }
+}
+
 template <int TYPE, int M>
 __global__ __launch_bounds__(256) void GemvKKernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
                                                    int64_t N, int64_t K, uint16_t *__restrict__ y) {
   constexpr int kBytes = KLayout<TYPE>::bytes;
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, i0 = (lane & 31) * 8;
   const int64_t nb = K / 256;
   const int64_t n0 = (int64_t)blockIdx.x * kGvRows + wave * kGvCols;
+  const uint8_t *row[kGvCols];  // columns past N decode the last and are not stored
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c) row[c] = w + (n0 + c < N ? n0 + c : N - 1) * nb * kBytes;
   float acc[kGvCols][M];
 #pragma unroll
   for (int c = 0; c < kGvCols; ++c)
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[c][m] = 0.f;
-  for (int64_t kb = half; kb < nb; kb += 2) {
+  // the raw bytes and activations of the lane's next block load while the
+  // current one is decoded (a lane with no block of its own, nb odd, reloads
+  // its last one and adds nothing)
+  KRaw<TYPE> cur[kGvCols], nxt[kGvCols];
+  v4u av[M], avn[M];
+  int64_t kb = half < nb ? half : nb - 1;
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c) LoadK(row[c] + kb * kBytes, i0, cur[c]);
+#pragma unroll
+  for (int m = 0; m < M; ++m) av[m] = *reinterpret_cast<const v4u *>(a + m * K + kb * 256 + i0);
+  for (kb = half; kb < nb; kb += 2) {
+    const int64_t kn = kb + 2 < nb ? kb + 2 : kb;
+#pragma unroll
+    for (int c = 0; c < kGvCols; ++c) LoadK(row[c] + kn * kBytes, i0, nxt[c]);
+#pragma unroll
+    for (int m = 0; m < M; ++m) avn[m] = *reinterpret_cast<const v4u *>(a + m * K + kn * 256 + i0);  // 16-byte aligned
     h2_t wp[kGvCols][4];
 #pragma unroll
-    for (int c = 0; c < kGvCols; ++c) {
-      const int64_t n = n0 + c < N ? n0 + c : N - 1;  // columns past N decode the last and are not stored
-      float v[8];
-      DecodeK8<TYPE>(w + (n * nb + kb) * kBytes, i0, v);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        wp[c][e] = AsH2((uint32_t)F32ToF16(v[2 * e]) | (uint32_t)F32ToF16(v[2 * e + 1]) << 16);
-    }
+    for (int c = 0; c < kGvCols; ++c) DecodeK(cur[c], i0, wp[c]);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      typedef unsigned v4u __attribute__((ext_vector_type(4)));
-      const v4u av = *reinterpret_cast<const v4u *>(a + m * K + kb * 256 + i0);  // 16-byte aligned (K % 256 == 0)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const h2_t ap = AsH2(av[e]);
+        const h2_t ap = AsH2(av[m][e]);
 #pragma unroll
         for (int c = 0; c < kGvCols; ++c) acc[c][m] = __builtin_amdgcn_fdot2(ap, wp[c][e], acc[c][m], false);
       }
     }
+#pragma unroll
+    for (int c = 0; c < kGvCols; ++c) cur[c] = nxt[c];
+#pragma unroll
+    for (int m = 0; m < M; ++m) av[m] = avn[m];
   }
 #pragma unroll
   for (int c = 0; c < kGvCols; ++c) {
