@@ -233,6 +233,13 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int kBN = 64 * WB;                 // workgroup tile columns
   constexpr int kWN = 32 * WB;                 // wave tile columns
   constexpr int kBP = BPitch<KIND, WB>();      // bytes per B row in LDS
+  // 1-byte B rows hold 8 (128-byte rows) or 16 (256-byte rows) chunks of 16
+  // bytes; chunk c of row r sits at position c ^ (kBSwz * (r % 8)).  A
+  // transposing read takes one chunk from each of 8 rows for 16 lanes, and the
+  // next 16 lanes the neighbouring chunk of the same rows: with 256-byte rows
+  // (all rows on the same banks) the doubled XOR puts the 16 chunks at 16
+  // different positions, where the plain one put them on 8 twice.
+  constexpr int kBSwz = kBP >= 256 ? 2 : 1;
   constexpr int kBStage = BStageBytes<KIND, WB>();
   constexpr int L = LoadsPerWave<KIND, WB>();
   constexpr int LB = BLoadsPerWave<KIND, WB>();
@@ -366,10 +373,10 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       b_g[q] = cb < NW ? (unsigned)(krow * NB + cb) : kOob;
     } else {
       // 1-byte B: a 1 KB piece is 1024 / kBP rows; lane -> (row, 16-byte
-      // position p), holding global chunk p ^ (row % 8)
+      // position p), holding global chunk p ^ BSwz(row)
       constexpr int kCpr = kBP / 16;
       const int krow = (1024 / kBP) * i + lane / kCpr;
-      const int64_t cb = col0 + 16 * ((lane % kCpr) ^ (krow & 7));
+      const int64_t cb = col0 + 16 * ((lane % kCpr) ^ (kBSwz * (krow & 7)));
       b_g[q] = cb < NW ? (unsigned)(krow * NB + cb) : kOob;
     }
   }
@@ -392,11 +399,11 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     } else if constexpr (KIND == kI8) {
       const int krow = 16 * (g16 >> 1) + (s16 >> 1);
       const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
-      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (kBSwz * (krow & 7))) + (col & 15);
     } else if constexpr (KIND == kBf16F8) {
       const int krow = 8 * (g16 >> 1) + (s16 >> 1);
       const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 8 * (s16 & 1);
-      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (krow & 7)) + (col & 15);
+      b_rd[j] = krow * kBP + 16 * ((col >> 4) ^ (kBSwz * (krow & 7))) + (col & 15);
     } else {
       const int krow = 8 * (g16 >> 1) + (s16 >> 2);
       const int col = wn * kWN + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3);
