@@ -149,9 +149,12 @@ int onnxl_amd_dynamic_quantize_linear(const onnxl_amd_tensor *x, onnxl_amd_tenso
 /* DequantizePacked: decodes a 1-D UINT8 vector in one of the reference's
  * fixed GGUF wire formats (`format`, e.g. "gguf:q4_0") into y of the given
  * shape and output_dtype (FLOAT, FLOAT16, BFLOAT16 or DOUBLE); the last
- * dimension holds whole blocks.  The GPU decodes gguf:q4_0, q4_1, q5_0, q5_1,
- * q8_0, q8_1, iq4_nl, q4_k and q6_k; the reference's other 18 formats return
- * ONNXL_AMD_UNSUPPORTED, an unknown format INVALID_ARGUMENT.
+ * dimension holds whole blocks.  The GPU decodes the 20 formats without
+ * codebooks (gguf:q4_0, q4_1, q5_0, q5_1, q8_0, q8_1, iq4_nl, q2_k, q3_k,
+ * q4_k, q5_k, q6_k, q8_k, iq4_xs, tq1_0, tq2_0, mxfp4, nvfp4, q1_0, q2_0); the
+ * reference's 7 codebook formats (iq1_s, iq1_m, iq2_xxs, iq2_xs, iq2_s,
+ * iq3_xxs, iq3_s) return ONNXL_AMD_UNSUPPORTED, an unknown format
+ * INVALID_ARGUMENT.
  * Replaces DequantizePackedTensor (onnx_core/runtime/dequantize_packed.cc:
  * 334-372) behind kernel::DequantizePacked::operator()
  * (kq/kernel_dequantize_packed.cc:11-15). */

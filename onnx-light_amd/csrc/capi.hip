@@ -1094,8 +1094,8 @@ struct PackedProfile {
 };
 
 // The reference's 27 fixed wire profiles (ggml block sizes and bytes,
-// dequantize_packed.cc:27-36); the GPU decodes the 32-value formats, q4_k and
-// q6_k.
+// dequantize_packed.cc:27-36); the GPU decodes all but the 7 codebook formats
+// (iq1, iq2, iq3).
 constexpr PackedProfile kPackedProfiles[] = {
     {"gguf:q4_0", 32, 18, 2},      {"gguf:q4_1", 32, 20, 3},      {"gguf:q5_0", 32, 22, 6},
     {"gguf:q5_1", 32, 24, 7},      {"gguf:q8_0", 32, 34, 8},      {"gguf:q8_1", 32, 36, 9},

@@ -205,6 +205,120 @@ __global__ __launch_bounds__(kPkThreads) void DequantPackedKKernel(const uint8_t
   StoreEight<OUT>(y, b * 256 + i0, v, vec != 0);
 }
 
+// ---------------------------------------------------------------------------
+// The other profiles without codebooks (dequantize_packed.cc:199-279):
+// q2_k, q3_k, q5_k, q8_k, iq4_xs, tq1_0, tq2_0 (256 values), mxfp4 (32),
+// nvfp4 and q2_0 (64), q1_0 (128).  A thread computes 8 consecutive values
+// of one block, value by value with byte reads (the block stays in L1 for
+// the threads that share it), each fp32 step rounded on its own with the
+// x86-64 NaN results.  Layouts and formulas are those of the oracle's
+// pk_decode_ext.
+template <int TYPE> struct XLayout;
+template <> struct XLayout<10> { static constexpr int bytes = 84, values = 256; };   // q2_k
+template <> struct XLayout<11> { static constexpr int bytes = 110, values = 256; };  // q3_k
+template <> struct XLayout<13> { static constexpr int bytes = 176, values = 256; };  // q5_k
+template <> struct XLayout<15> { static constexpr int bytes = 292, values = 256; };  // q8_k
+template <> struct XLayout<23> { static constexpr int bytes = 136, values = 256; };  // iq4_xs
+template <> struct XLayout<34> { static constexpr int bytes = 54, values = 256; };   // tq1_0
+template <> struct XLayout<35> { static constexpr int bytes = 66, values = 256; };   // tq2_0
+template <> struct XLayout<39> { static constexpr int bytes = 17, values = 32; };    // mxfp4
+template <> struct XLayout<40> { static constexpr int bytes = 36, values = 64; };    // nvfp4
+template <> struct XLayout<41> { static constexpr int bytes = 18, values = 128; };   // q1_0
+template <> struct XLayout<42> { static constexpr int bytes = 18, values = 64; };    // q2_0
+
+__constant__ int kFp4Twice[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+// value i of grouped bit planes: 8 / BITS planes of GROUP bytes
+template <int BITS, int GROUP> __device__ __forceinline__ int Planes(const uint8_t *p, int i) {
+  constexpr int kPlanes = 8 / BITS;
+  return (p[(i / (kPlanes * GROUP)) * GROUP + i % GROUP] >> (BITS * ((i / GROUP) % kPlanes))) & ((1 << BITS) - 1);
+}
+
+template <int TYPE> __device__ __forceinline__ float DecodeX(const uint8_t *p, int i) {
+  if constexpr (TYPE == 10) {  // q2_k
+    const int g = i / 16;
+    const float dq = SseMul(SseMul(Half2(p + 80), (float)(p[g] & 15)), (float)Planes<2, 32>(p + 16, i));
+    return SseSub(dq, SseMul(Half2(p + 82), (float)(p[g] >> 4)));
+  } else if constexpr (TYPE == 11) {  // q3_k
+    const int g = i / 16;
+    const int scale = (Planes<4, 8>(p + 96, g) | (Planes<2, 4>(p + 104, g) << 4)) - 32;
+    const int q = Planes<2, 32>(p + 32, i) - (1 - Planes<1, 32>(p, i)) * 4;
+    return SseMul(SseMul(Half2(p + 108), (float)scale), (float)q);
+  } else if constexpr (TYPE == 13) {  // q5_k
+    const uint8_t *sc = p + 4;
+    const int g = i / 32;
+    const int scale = g < 4 ? sc[g] & 63 : (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+    const int minimum = g < 4 ? sc[g + 4] & 63 : (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+    const int q = Planes<4, 32>(p + 48, i) | (Planes<1, 32>(p + 16, i) << 4);
+    return SseSub(SseMul(SseMul(Half2(p), (float)scale), (float)q), SseMul(Half2(p + 2), (float)minimum));
+  } else if constexpr (TYPE == 15) {  // q8_k: fp32 d
+    const uint32_t bits = (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+    return SseMul(__builtin_bit_cast(float, bits), (float)(int8_t)p[4 + i]);
+  } else if constexpr (TYPE == 23) {  // iq4_xs
+    const int g = i / 32;
+    const uint32_t high = (uint32_t)p[2] | (uint32_t)p[3] << 8;
+    const int scale = (((p[4 + g / 2] >> (4 * (g % 2))) & 15) | (int)(((high >> (2 * g)) & 3u) << 4)) - 32;
+    return SseMul(SseMul(Half2(p), (float)scale), (float)kIq4Values[Planes<4, 16>(p + 8, i)]);
+  } else if constexpr (TYPE == 34) {  // tq1_0: base-3 digits
+    const int start = i < 160 ? 0 : (i < 240 ? 32 : 48);
+    const int width = i < 160 ? 32 : (i < 240 ? 16 : 4);
+    const int offset = i < 160 ? i : (i < 240 ? i - 160 : i - 240);
+    const int digit = offset / width;
+    const int power = digit == 0 ? 1 : digit == 1 ? 3 : digit == 2 ? 9 : digit == 3 ? 27 : 81;
+    const int q = ((p[start + offset % width] * power) & 255) * 3 / 256 - 1;
+    return SseMul(Half2(p + 52), (float)q);
+  } else if constexpr (TYPE == 35) {  // tq2_0
+    return SseMul(Half2(p + 64), (float)(Planes<2, 32>(p, i) - 1));
+  } else if constexpr (TYPE == 39) {  // mxfp4: e8m0 scale byte
+    const uint32_t e = p[0];
+    const uint32_t bits = e <= 1 ? 0x00200000u << e : (e - 1) << 23;
+    return SseMul(__builtin_bit_cast(float, bits), (float)kFp4Twice[Planes<4, 16>(p + 1, i)]);
+  } else if constexpr (TYPE == 40) {  // nvfp4: ue4m3 scale per 16 values
+    const int g = i / 16, e = p[g], exponent = (e >> 3) & 15, mantissa = e & 7;
+    const float scale = e == 0 || e == 127 ? 0.f
+                        : exponent == 0    ? ldexpf((float)mantissa, -10)
+                                           : ldexpf(1.f + (float)mantissa / 8.f, exponent - 8);
+    return SseMul(scale, (float)kFp4Twice[Planes<4, 8>(p + 4 + 8 * g, i % 16)]);
+  } else if constexpr (TYPE == 41) {  // q1_0: a sign bit per value
+    // no arithmetic touches d, so its fp32 bits are the reference's software
+    // conversion bit for bit: a signaling NaN stays signaling (the hardware
+    // conversion would quiet it), and -d flips the sign bit only
+    const uint32_t h = (uint32_t)p[0] | (uint32_t)p[1] << 8;
+    const uint32_t bits = (h & 0x7c00u) == 0x7c00u && (h & 0x3ffu)
+                              ? ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13)
+                              : __builtin_bit_cast(uint32_t, Half2(p));
+    return __builtin_bit_cast(float, (p[2 + i / 8] >> (i % 8)) & 1 ? bits : bits ^ 0x80000000u);
+  } else {  // q2_0
+    return SseMul(Half2(p), (float)(Planes<2, 1>(p + 2, i) - 1));
+  }
+}
+
+template <int TYPE, int OUT>
+__global__ __launch_bounds__(kPkThreads) void DequantPackedXKernel(const uint8_t *__restrict__ x, int64_t nblocks,
+                                                                   void *__restrict__ y, int vec) {
+  constexpr int kV = XLayout<TYPE>::values, kTpb = kV / 8;  // threads per block
+  const int64_t t = (int64_t)blockIdx.x * kPkThreads + threadIdx.x;
+  if (t >= nblocks * kTpb) return;
+  const int64_t b = t / kTpb;
+  const int i0 = (int)(t % kTpb) * 8;
+  const uint8_t *p = x + b * XLayout<TYPE>::bytes;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = DecodeX<TYPE>(p, i0 + e);
+  StoreEight<OUT>(y, b * kV + i0, v, vec != 0);  // thread t writes values 8t .. 8t + 7
+}
+
+template <int TYPE> void LaunchPkXOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
+  const int64_t threads = nblocks * (XLayout<TYPE>::values / 8);
+  const dim3 g((unsigned)((threads + kPkThreads - 1) / kPkThreads));
+  switch (out) {
+  case kFloat: hipLaunchKernelGGL((DequantPackedXKernel<TYPE, kFloat>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kFloat16: hipLaunchKernelGGL((DequantPackedXKernel<TYPE, kFloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kBfloat16: hipLaunchKernelGGL((DequantPackedXKernel<TYPE, kBfloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  default: hipLaunchKernelGGL((DequantPackedXKernel<TYPE, kDouble>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  }
+}
+
 template <int TYPE> void LaunchPkKOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
   const dim3 g((unsigned)((nblocks * 32 + kPkThreads - 1) / kPkThreads));
   switch (out) {
@@ -684,8 +798,13 @@ void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, in
 }
 
 bool PackedFormatOnGpu(int ggml_type) {
-  return ggml_type == 2 || ggml_type == 3 || ggml_type == 6 || ggml_type == 7 || ggml_type == 8 ||
-         ggml_type == 9 || ggml_type == 20 || ggml_type == 12 || ggml_type == 14;
+  switch (ggml_type) {
+  case 2: case 3: case 6: case 7: case 8: case 9: case 20: case 12: case 14:
+  case 10: case 11: case 13: case 15: case 23: case 34: case 35: case 39: case 40: case 41: case 42:
+    return true;
+  default:
+    return false;  // the codebook formats (iq1, iq2, iq3)
+  }
 }
 
 void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, int out_dtype, void *y,
@@ -702,6 +821,17 @@ void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, in
   case 20: LaunchPkOut<20>(x, nblocks, out_dtype, y, vec, s); break;
   case 12: LaunchPkKOut<12>(x, nblocks, out_dtype, y, vec, s); break;
   case 14: LaunchPkKOut<14>(x, nblocks, out_dtype, y, vec, s); break;
+  case 10: LaunchPkXOut<10>(x, nblocks, out_dtype, y, vec, s); break;
+  case 11: LaunchPkXOut<11>(x, nblocks, out_dtype, y, vec, s); break;
+  case 13: LaunchPkXOut<13>(x, nblocks, out_dtype, y, vec, s); break;
+  case 15: LaunchPkXOut<15>(x, nblocks, out_dtype, y, vec, s); break;
+  case 23: LaunchPkXOut<23>(x, nblocks, out_dtype, y, vec, s); break;
+  case 34: LaunchPkXOut<34>(x, nblocks, out_dtype, y, vec, s); break;
+  case 35: LaunchPkXOut<35>(x, nblocks, out_dtype, y, vec, s); break;
+  case 39: LaunchPkXOut<39>(x, nblocks, out_dtype, y, vec, s); break;
+  case 40: LaunchPkXOut<40>(x, nblocks, out_dtype, y, vec, s); break;
+  case 41: LaunchPkXOut<41>(x, nblocks, out_dtype, y, vec, s); break;
+  case 42: LaunchPkXOut<42>(x, nblocks, out_dtype, y, vec, s); break;
   default: throw Unsupported("DequantizePacked: no GPU kernel for this format");
   }
 }

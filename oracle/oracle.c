@@ -621,7 +621,28 @@ int orc_packed_block_bytes(int ggml_type) {
   case 20: return 18; /* iq4_nl */
   case 12: return 144; /* q4_k */
   case 14: return 210; /* q6_k */
+  case 10: return 84;  /* q2_k */
+  case 11: return 110; /* q3_k */
+  case 13: return 176; /* q5_k */
+  case 15: return 292; /* q8_k */
+  case 23: return 136; /* iq4_xs */
+  case 34: return 54;  /* tq1_0 */
+  case 35: return 66;  /* tq2_0 */
+  case 39: return 17;  /* mxfp4 */
+  case 40: return 36;  /* nvfp4 */
+  case 41: return 18;  /* q1_0 */
+  case 42: return 18;  /* q2_0 */
   default: return 0;
+  }
+}
+
+/* values per block (dequantize_packed.cc:27-36) */
+int orc_packed_block_values(int ggml_type) {
+  switch (ggml_type) {
+  case 2: case 3: case 6: case 7: case 8: case 9: case 20: case 39: return 32;
+  case 40: case 42: return 64;
+  case 41: return 128;
+  default: return orc_packed_block_bytes(ggml_type) ? 256 : 0;
   }
 }
 
@@ -663,9 +684,107 @@ static void pk_decode_k(int ggml_type, const uint8_t *p, float *out) {
   }
 }
 
+/* The other non-codebook profiles, value by value (dequantize_packed.cc:
+ * 199-279 for the decode, :27-36 for the layouts).  Every fp32 product,
+ * sum and difference rounded on its own:
+ *  q2_k (84 B): 16 scale bytes (low nibble scale, high nibble minimum per 16
+ *    values), 64 bytes of 2-bit codes, fp16 d at 80 and dmin at 82;
+ *    (d * scale) * q - dmin * minimum;
+ *  q3_k (110 B): 32 bytes of high-bit masks, 64 bytes of 2-bit codes, 6-bit
+ *    signed scales (low nibbles at 96, high 2 bits at 104), fp16 d at 108;
+ *    q loses 4 where its mask bit is clear; (d * (scale - 32)) * q;
+ *  q5_k (176 B): q4_k's header, 32 bytes of fifth bits at 16, 128 nibble
+ *    bytes at 48;
+ *  q8_k (292 B): fp32 d, 256 int8 codes (and 32 bytes of sums, unused);
+ *  iq4_xs (136 B): fp16 d, 2 bytes of high scale bits, 4 bytes of low scale
+ *    nibbles, 128 nibble bytes into the iq4 table; (d * (scale - 32)) * v;
+ *  tq1_0 (54 B): base-3 digits packed five (then four) per byte by
+ *    multiplication, fp16 d at 52; d * (digit - 1);
+ *  tq2_0 (66 B): 2-bit codes, fp16 d at 64; d * (q - 1);
+ *  mxfp4 (17 B, 32 values): an e8m0 scale byte (2^(e - 127), with e = 0, 1
+ *    the fp32 subnormals 2^-128, 2^-127 written as 0x00200000 << e), 16 bytes
+ *    of e2m1 codes taken as twice their value; scale * 2v;
+ *  nvfp4 (36 B, 64 values): 4 ue4m3 scale bytes (0 and 127 give 0) per 16
+ *    values, 32 bytes of e2m1 codes; scale * 2v;
+ *  q1_0 (18 B, 128 values): fp16 d, a sign bit per value: +d or -d;
+ *  q2_0 (18 B, 64 values): fp16 d, 2-bit codes four per byte; d * (q - 1). */
+static const int pk_fp4[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+static float pk_half(const uint8_t *p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+static float pk_mul(float a, float b) { volatile float r = a * b; return r; }
+static float pk_sub(float a, float b) { volatile float r = a - b; return r; }
+
+static void pk_decode_ext(int t, const uint8_t *p, float *out) {
+  const int n = orc_packed_block_values(t);
+  for (int i = 0; i < n; ++i) {
+    float v = 0.0f;
+    if (t == 10) {
+      const int g = i / 16, q = pk_unpack(p + 16, i, 2, 32);
+      v = pk_sub(pk_mul(pk_mul(pk_half(p + 80), (float)(p[g] & 15)), (float)q),
+                 pk_mul(pk_half(p + 82), (float)(p[g] >> 4)));
+    } else if (t == 11) {
+      const int g = i / 16;
+      const int scale = (pk_unpack(p + 96, g, 4, 8) | (pk_unpack(p + 104, g, 2, 4) << 4)) - 32;
+      const int q = pk_unpack(p + 32, i, 2, 32) - (1 - pk_unpack(p, i, 1, 32)) * 4;
+      v = pk_mul(pk_mul(pk_half(p + 108), (float)scale), (float)q);
+    } else if (t == 13) {
+      const uint8_t *sc = p + 4;
+      const int g = i / 32;
+      const int scale = g < 4 ? sc[g] & 63 : (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+      const int minimum = g < 4 ? sc[g + 4] & 63 : (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+      const int q = pk_unpack(p + 48, i, 4, 32) | (pk_unpack(p + 16, i, 1, 32) << 4);
+      v = pk_sub(pk_mul(pk_mul(pk_half(p), (float)scale), (float)q), pk_mul(pk_half(p + 2), (float)minimum));
+    } else if (t == 15) {
+      uint32_t bits = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+      float d;
+      memcpy(&d, &bits, 4);
+      v = pk_mul(d, (float)(int8_t)p[4 + i]);
+    } else if (t == 23) {
+      const int g = i / 32;
+      const uint32_t high = (uint32_t)p[2] | ((uint32_t)p[3] << 8);
+      const int scale = (((p[4 + g / 2] >> (4 * (g % 2))) & 15) | (((high >> (2 * g)) & 3) << 4)) - 32;
+      v = pk_mul(pk_mul(pk_half(p), (float)scale), (float)pk_iq4[pk_unpack(p + 8, i, 4, 16)]);
+    } else if (t == 34) {
+      static const int powers[5] = {1, 3, 9, 27, 81};
+      const int start = i < 160 ? 0 : i < 240 ? 32 : 48;
+      const int width = i < 160 ? 32 : i < 240 ? 16 : 4;
+      const int offset = i < 160 ? i : i < 240 ? i - 160 : i - 240;
+      const int q = ((p[start + offset % width] * powers[offset / width]) & 255) * 3 / 256 - 1;
+      v = pk_mul(pk_half(p + 52), (float)q);
+    } else if (t == 35) {
+      v = pk_mul(pk_half(p + 64), (float)(pk_unpack(p, i, 2, 32) - 1));
+    } else if (t == 39) {
+      const uint32_t e = p[0];
+      const uint32_t bits = e <= 1 ? 0x00200000u << e : (e - 1) << 23;
+      float scale;
+      memcpy(&scale, &bits, 4);
+      v = pk_mul(scale, (float)pk_fp4[pk_unpack(p + 1, i, 4, 16)]);
+    } else if (t == 40) {
+      const int g = i / 16, e = p[g], exponent = (e >> 3) & 15, mantissa = e & 7;
+      const float scale = e == 0 || e == 127 ? 0.0f
+                          : exponent == 0    ? ldexpf((float)mantissa, -10)
+                                             : ldexpf(1.0f + (float)mantissa / 8.0f, exponent - 8);
+      v = pk_mul(scale, (float)pk_fp4[pk_unpack(p + 4 + 8 * g, i % 16, 4, 8)]);
+    } else if (t == 41) {
+      const float d = pk_half(p);
+      v = (p[2 + i / 8] >> (i % 8)) & 1 ? d : -d;
+    } else if (t == 42) {
+      v = pk_mul(pk_half(p), (float)(pk_unpack(p + 2, i, 2, 1) - 1));
+    }
+    out[i] = v;
+  }
+}
+
 int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out) {
   const int bytes = orc_packed_block_bytes(ggml_type);
   if (!bytes) return 1;
+  const int ext = ggml_type == 10 || ggml_type == 11 || ggml_type == 13 || ggml_type == 15 || ggml_type == 23 ||
+                  (ggml_type >= 34 && ggml_type <= 42);
+  if (ext) {
+    const int n = orc_packed_block_values(ggml_type);
+    for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += n) pk_decode_ext(ggml_type, x, out);
+    return 0;
+  }
   if (ggml_type == 12 || ggml_type == 14) {
     for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += 256) pk_decode_k(ggml_type, x, out);
     return 0;

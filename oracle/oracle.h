@@ -140,14 +140,17 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
 int orc_dynamic_quantize_linear(const float *x, int64_t n, uint8_t *y, float *y_scale,
                                 uint8_t *y_zero_point);
 
-/* ---- DequantizePacked, 32-value GGUF formats
- * (onnx_core/runtime/dequantize_packed.cc:173-235) ----
- * ggml_type 2 q4_0, 3 q4_1, 6 q5_0, 7 q5_1, 8 q8_0, 9 q8_1, 20 iq4_nl:
- * nblocks blocks of orc_packed_block_bytes(type) bytes -> 32 * nblocks FLOAT
- * values (each fp32 step rounded on its own).  Returns 0, or 1 for another
- * type.  The FLOAT16 / BFLOAT16 / DOUBLE outputs are the FLOAT values
- * converted (:358-370). */
+/* ---- DequantizePacked, the GGUF profiles without codebooks
+ * (onnx_core/runtime/dequantize_packed.cc:173-279) ----
+ * ggml_type 2 q4_0, 3 q4_1, 6 q5_0, 7 q5_1, 8 q8_0, 9 q8_1, 20 iq4_nl,
+ * 10 q2_k, 11 q3_k, 12 q4_k, 13 q5_k, 14 q6_k, 15 q8_k, 23 iq4_xs,
+ * 34 tq1_0, 35 tq2_0, 39 mxfp4, 40 nvfp4, 41 q1_0, 42 q2_0: nblocks blocks of
+ * orc_packed_block_bytes(type) bytes -> orc_packed_block_values(type) *
+ * nblocks FLOAT values (each fp32 step rounded on its own).  Returns 0, or 1
+ * for another type.  The FLOAT16 / BFLOAT16 / DOUBLE outputs are the FLOAT
+ * values converted (:358-370). */
 int orc_packed_block_bytes(int ggml_type);
+int orc_packed_block_values(int ggml_type);
 int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out);
 
 /* ---- ConvInteger (nn/kernel_conv_integer.cc:178-304) and QLinearConv

@@ -99,6 +99,8 @@ def _declare(L):
                                    P, P, P, P, ctypes.c_int, P]
     L.orc_packed_block_bytes.restype = ctypes.c_int
     L.orc_packed_block_bytes.argtypes = [ctypes.c_int]
+    L.orc_packed_block_values.restype = ctypes.c_int
+    L.orc_packed_block_values.argtypes = [ctypes.c_int]
     L.orc_dequantize_packed.restype = ctypes.c_int
     L.orc_dequantize_packed.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
     L.orc_matmul_f32.restype = ctypes.c_int
@@ -454,15 +456,21 @@ def qlinear_conv(x, x_dtype, x_scale, x_zp, w, w_dtype, w_scale, w_zp, y_scale, 
     return y
 
 
-# ---- DequantizePacked (32-value GGUF formats) -------------------------------
+# ---- DequantizePacked (the GGUF profiles without codebooks) ------------------
 
 GGUF_TYPES = {"gguf:q4_0": 2, "gguf:q4_1": 3, "gguf:q5_0": 6, "gguf:q5_1": 7, "gguf:q8_0": 8,
-              "gguf:q8_1": 9, "gguf:iq4_nl": 20, "gguf:q4_k": 12, "gguf:q6_k": 14}
-BLOCK_VALUES = {"gguf:q4_k": 256, "gguf:q6_k": 256}  # the others: 32
+              "gguf:q8_1": 9, "gguf:iq4_nl": 20, "gguf:q4_k": 12, "gguf:q6_k": 14,
+              "gguf:q2_k": 10, "gguf:q3_k": 11, "gguf:q5_k": 13, "gguf:q8_k": 15, "gguf:iq4_xs": 23,
+              "gguf:tq1_0": 34, "gguf:tq2_0": 35, "gguf:mxfp4": 39, "gguf:nvfp4": 40, "gguf:q1_0": 41,
+              "gguf:q2_0": 42}
 
 
 def packed_block_bytes(fmt: str) -> int:
     return lib().orc_packed_block_bytes(GGUF_TYPES[fmt])
+
+
+def packed_block_values(fmt: str) -> int:
+    return lib().orc_packed_block_values(GGUF_TYPES[fmt])
 
 
 def dequantize_packed(x: np.ndarray, fmt: str, shape, output_dtype: int = FLOAT) -> np.ndarray:
@@ -471,7 +479,7 @@ def dequantize_packed(x: np.ndarray, fmt: str, shape, output_dtype: int = FLOAT)
     x = np.ascontiguousarray(x, dtype=np.uint8)
     n = int(np.prod(shape)) if len(shape) else 1
     out = np.empty(n, np.float32)
-    rc = lib().orc_dequantize_packed(GGUF_TYPES[fmt], _ptr(x), n // BLOCK_VALUES.get(fmt, 32), _ptr(out))
+    rc = lib().orc_dequantize_packed(GGUF_TYPES[fmt], _ptr(x), n // packed_block_values(fmt), _ptr(out))
     if rc:
         raise ValueError(f"dequantize_packed error {rc}")
     out = out.reshape(shape)

@@ -348,6 +348,6 @@ def test_dequantize_packed_validation(olamd):
         assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
     rc, _ = run()
     assert rc == olamd.NOT_INITIALIZED
-    # a format of the reference with no GPU kernel here
-    rc, _ = run(x=np.zeros(176, np.uint8), fmt=b"gguf:q5_k", shape=(256,), y=np.zeros(256, np.float32))
+    # a format of the reference with no GPU kernel here (a codebook format)
+    rc, _ = run(x=np.zeros(66, np.uint8), fmt=b"gguf:iq2_xxs", shape=(256,), y=np.zeros(256, np.float32))
     assert rc == olamd.UNSUPPORTED

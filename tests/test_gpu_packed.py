@@ -1,5 +1,5 @@
-"""GPU parity of DequantizePacked for the 32-value GGUF formats against the
-oracle: bit-exact in all four output dtypes (FLOAT, FLOAT16, BFLOAT16,
+"""GPU parity of DequantizePacked for the GGUF profiles without codebooks against
+the oracle: bit-exact in all four output dtypes (FLOAT, FLOAT16, BFLOAT16,
 DOUBLE).  The reference test's corpus is checked against its GGML-C hashes
 through the GPU too; random blocks include NaN, infinite, subnormal and
 maximal fp16 scales; outputs at unaligned addresses take the per-element
@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from test_oracle_packed import FORMATS, block_values, corpus, fnv1a64
+from test_oracle_packed import FORMATS, block_values, corpus, d_offset, fnv1a64
 
 pytestmark = pytest.mark.gpu
 OUT = {"float": (1, torch.float32), "float16": (10, torch.float16), "bfloat16": (16, torch.bfloat16),
@@ -42,16 +42,26 @@ def test_random_blocks_vs_oracle(olamd, oracle, dev, fmt, out):
     rng = np.random.default_rng(len(fmt) * 7 + len(out) + FORMATS.index(fmt) * 101)
     size = oracle.packed_block_bytes(fmt)
     bv = block_values(fmt)
-    shapes = [(32,), (3, 5, 64), (7, 4096), (1, 96)] if bv == 32 else [(256,), (3, 2, 512), (7, 4096), (1, 768)]
-    at = 208 if fmt == "gguf:q6_k" else 0  # the fp16 d
+    shapes = [(bv,), (3, 5, 2 * bv), (7, 4096), (1, 3 * bv)]
+    at = d_offset(fmt)  # the fp16 d (None: q8_k's fp32 d, the fp4 scale bytes)
     for shape in shapes:
         nb = int(np.prod(shape)) // bv
         x = rng.integers(0, 256, (nb, size)).astype(np.uint8)
-        # scales: random fp16 bit patterns, with NaN, inf, subnormal and 65504 among them
-        special = np.array([0x7E00, 0xFC00, 0x0001, 0x7BFF, 0x8000, 0x3C00], np.uint16)
-        d = rng.integers(0, 65536, nb).astype(np.uint16)
-        d[: min(nb, len(special))] = special[: min(nb, len(special))]
-        x[:, at], x[:, at + 1] = d & 255, d >> 8
+        if at is not None:
+            # scales: random fp16 bit patterns, with NaN, inf, subnormal and 65504 among them
+            special = np.array([0x7E00, 0xFC00, 0x0001, 0x7BFF, 0x8000, 0x3C00], np.uint16)
+            d = rng.integers(0, 65536, nb).astype(np.uint16)
+            d[: min(nb, len(special))] = special[: min(nb, len(special))]
+            x[:, at], x[:, at + 1] = d & 255, d >> 8
+        elif fmt == "gguf:q8_k":
+            # fp32 d: NaN, -inf, the smallest subnormal, the largest finite, -0, 1
+            special = np.array([0x7FC00000, 0xFF800000, 0x00000001, 0x7F7FFFFF, 0x80000000, 0x3F800000], np.uint32)
+            d = rng.integers(0, 2 ** 32, nb, dtype=np.uint64).astype(np.uint32)
+            d[: min(nb, len(special))] = special[: min(nb, len(special))]
+            for b in range(4):
+                x[:, b] = (d >> (8 * b)) & 255
+        elif fmt == "gguf:mxfp4":
+            x[: min(nb, 4), 0] = [0, 1, 2, 255][: min(nb, 4)]  # the two subnormal scales, the largest
         x = x.reshape(-1)
         want = oracle.dequantize_packed(x, fmt, shape, OUT[out][0])
         for offset in (0, 1):

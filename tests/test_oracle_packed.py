@@ -6,28 +6,51 @@ import numpy as np
 import pytest
 
 FORMATS = ["gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1", "gguf:iq4_nl",
-           "gguf:q4_k", "gguf:q6_k"]
-AFFINE = {"gguf:q4_1", "gguf:q5_1", "gguf:q4_k"}  # a second fp16 (minimum) after d
+           "gguf:q4_k", "gguf:q6_k", "gguf:q2_k", "gguf:q3_k", "gguf:q5_k", "gguf:q8_k", "gguf:iq4_xs",
+           "gguf:tq1_0", "gguf:tq2_0", "gguf:mxfp4", "gguf:nvfp4", "gguf:q1_0", "gguf:q2_0"]
+AFFINE = {"gguf:q4_1", "gguf:q5_1", "gguf:q2_k", "gguf:q4_k", "gguf:q5_k"}  # a second fp16 (minimum) after d
+# byte offset of the fp16 scale d; None: no fp16 d (q8_k's is fp32, the fp4
+# formats carry scale bytes)
+D_OFFSET = {"gguf:q2_k": 80, "gguf:q3_k": 108, "gguf:q6_k": 208, "gguf:tq1_0": 52, "gguf:tq2_0": 64,
+            "gguf:q8_k": None, "gguf:mxfp4": None, "gguf:nvfp4": None}
+VALUES = {"gguf:nvfp4": 64, "gguf:q2_0": 64, "gguf:q1_0": 128}
 
 
 def block_values(fmt):
-    return 256 if fmt in ("gguf:q4_k", "gguf:q6_k") else 32
+    if fmt in VALUES:
+        return VALUES[fmt]
+    small = ("gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1", "gguf:iq4_nl",
+             "gguf:mxfp4")
+    return 32 if fmt in small else 256
+
+
+def d_offset(fmt):
+    return D_OFFSET.get(fmt, 0)
 
 
 def corpus(oracle, fmt, scales):
-    """64 blocks: byte j of block i is (73j + 29i + 17(j // 7) + 11(i // 3)) mod 256,
-    then the fp16 scale d (at byte 208 for q6_k, else 0) and, for the formats
-    with a minimum, the fp16 of the next scale right after it."""
+    """The reference test's 64-block corpus (test_dequantize_packed.cc:41-73):
+    byte j of block i is (73j + 29i + 17(j // 7) + 11(i // 3)) mod 256, then
+    the fp16 scale d at its offset and, for the formats with a minimum, the
+    fp16 of the next scale right after it; q8_k takes the fp32 scale / 3 in
+    its first 4 bytes, mxfp4 the scale byte (17 i) mod 256."""
     size = oracle.packed_block_bytes(fmt)
     i = np.arange(64)[:, None]
     j = np.arange(size)[None, :]
     blocks = ((j * 73 + i * 29 + (j // 7) * 17 + (i // 3) * 11) & 255).astype(np.uint8)
-    at = 208 if fmt == "gguf:q6_k" else 0
-    d = oracle.f32_to_f16_bits(np.array([scales[k % 8] for k in range(64)], np.float32))
-    blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
-    if fmt in AFFINE:
-        m = oracle.f32_to_f16_bits(np.array([scales[(k + 1) % 8] for k in range(64)], np.float32))
-        blocks[:, at + 2], blocks[:, at + 3] = m & 255, m >> 8
+    at = d_offset(fmt)
+    if at is not None:
+        d = oracle.f32_to_f16_bits(np.array([scales[k % 8] for k in range(64)], np.float32))
+        blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
+        if fmt in AFFINE:
+            m = oracle.f32_to_f16_bits(np.array([scales[(k + 1) % 8] for k in range(64)], np.float32))
+            blocks[:, at + 2], blocks[:, at + 3] = m & 255, m >> 8
+    elif fmt == "gguf:q8_k":
+        bits = np.array([np.float32(scales[k % 8] / 3) for k in range(64)], np.float32).view(np.uint32)
+        for b in range(4):
+            blocks[:, b] = (bits >> (8 * b)) & 255
+    elif fmt == "gguf:mxfp4":
+        blocks[:, 0] = (np.arange(64) * 17) & 255
     return blocks.reshape(-1)
 
 
