@@ -432,6 +432,20 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
                               : static_cast<const float *>(p.scale)[si];
     }
   }
+  // kOutQ8Row: the weight scale and bias of this lane's rows in the four
+  // 32-row blocks, loaded here so that their latency hides under the K loop
+  // instead of opening each block's epilogue
+  float row_ws[OUT == kOutQ8Row ? 4 : 1] = {};
+  int32_t row_b[OUT == kOutQ8Row ? 4 : 1] = {};
+  if constexpr (OUT == kOutQ8Row) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + wm * 128 + i * 32 + lr;
+      const int64_t rc = row < M ? row : 0;
+      row_ws[i] = p.row_wscale[p.row_wscale_per ? rc : 0];
+      row_b[i] = p.row_bias ? p.row_bias[rc] : 0;
+    }
+  }
   constexpr int aflip = (KIND == kI8 && AU8) ? (int)kFlip : 0;
   constexpr int bflip = (KIND == kI8 && BU8) ? (int)kFlip : 0;
 
@@ -818,14 +832,13 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       al_r = zrow[i];
     }
     // kOutQ8Row: this lane's output row (row0 + wm * 128 + 32 i + lr) scale
-    // and bias, computed with the fp32 operations of the reference
+    // and bias (loaded before the K loop), computed with the fp32 operations
+    // of the reference
     float cs_r = p.cs;
     double bias_r = 0.0;
     if constexpr (OUT == kOutQ8Row) {
-      const int64_t row = row0 + wm * 128 + i * 32 + lr;
-      const int64_t rc = row < M ? row : 0;
-      cs_r = p.row_xs * p.row_wscale[p.row_wscale_per ? rc : 0] / p.row_ys;
-      bias_r = p.row_bias ? (double)p.row_bias[rc] : 0.0;
+      cs_r = p.row_xs * row_ws[i] / p.row_ys;
+      bias_r = (double)row_b[i];
     }
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
