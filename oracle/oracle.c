@@ -1180,3 +1180,141 @@ int orc_ort_nbits_decode(const uint8_t *B, const double *scales, int zp_kind, co
     }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* AWQ weights (onnx_core/runtime/awq.cc:185-247, Code and Reconstructed).
+ * variant 0 "gemm": qweight INT32 [K, N * bits / 32]; 4 bits: column n of
+ *   row k at nibble inv[n % 8] of word k * (N / 8) + n / 8 with inv =
+ *   {0, 4, 1, 5, 2, 6, 3, 7}; 8 bits: byte n % 4 of word k * (N / 4) + n / 4;
+ *   qzeros INT32 [groups, N * bits / 32] the zero of (group, n) the same way;
+ *   scales [groups, N].
+ * variant 1 "gemv" (4 bits): qweight [N, K / 8], row k at nibble k % 8 of
+ *   word n * (K / 8) + k / 8; qzeros [N, padded / 8], group g at nibble g % 8
+ *   of word n * (padded / 8) + g / 8; scales [N, padded].
+ * variant 2 "gemv_fast" / "llm-awq" (4 bits): qweight INT16 [N / 4, K], the
+ *   inverse of the two 32-code permutations and the 4-row / 64-code
+ *   interleave of awq.cc:198-206; float zero terms and scales [padded, N].
+ * value: variants 0 and 1 (code - zero) * scale in fp32 (exact); variant 2
+ * code * scale rounded to fp32, plus the zero term.  Writes codes [N, K],
+ * zeros [N, groups] (variants 0 and 1; 0 for variant 2) and the FLOAT values
+ * [N, K]; scales and zero terms are decoded fp16 / bf16 values.  Returns 0,
+ * or 1 for an unknown variant or bit width. */
+int orc_awq_decode(int variant, int bits, const void *qweight, const void *qzeros, const float *zero_terms,
+                   const float *scales, int64_t K, int64_t N, int64_t group, int64_t padded, uint8_t *codes,
+                   uint8_t *zeros, float *out) {
+  static const int inv[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  if (variant < 0 || variant > 2 || !(bits == 4 || (bits == 8 && variant == 0))) return 1;
+  const uint32_t *qw = (const uint32_t *)qweight, *qz = (const uint32_t *)qzeros;
+  const uint16_t *qh = (const uint16_t *)qweight;
+  const int64_t eff = group == -1 ? K : group, groups = K / eff;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t g = 0; g < groups; ++g) {
+      uint32_t z = 0;
+      if (variant == 0 && bits == 4) z = qz[g * (N / 8) + n / 8] >> (4 * inv[n % 8]);
+      else if (variant == 0) z = qz[g * (N / 4) + n / 4] >> (8 * (n % 4));
+      else if (variant == 1) z = qz[n * (padded / 8) + g / 8] >> (4 * (g % 8));
+      zeros[n * groups + g] = (uint8_t)(z & mask);
+    }
+    for (int64_t k = 0; k < K; ++k) {
+      uint32_t c;
+      if (variant == 0 && bits == 4) c = qw[k * (N / 8) + n / 8] >> (4 * inv[n % 8]);
+      else if (variant == 0) c = qw[k * (N / 4) + n / 4] >> (8 * (n % 4));
+      else if (variant == 1) c = qw[n * (K / 8) + k / 8] >> (4 * (k % 8));
+      else {
+        const int64_t i = k % 32;
+        const int64_t first = ((i / 2) % 4) * 8 + (i / 8) * 2 + i % 2;
+        const int64_t second = (first / 8) * 8 + (first % 2) * 4 + (first % 8) / 2;
+        const int64_t flat = (n % 4) * 64 + (k % 64) / 32 * 32 + second;
+        c = (uint32_t)qh[(n / 4) * K + (k / 64) * 64 + flat / 4] >> (4 * (flat % 4));
+      }
+      const int64_t g = k / eff;
+      const uint8_t code = (uint8_t)(c & mask);
+      codes[n * K + k] = code;
+      if (variant == 2) {
+        volatile float product = (float)code * scales[g * N + n];
+        volatile float v = product + zero_terms[g * N + n];
+        out[n * K + k] = v;
+      } else {
+        const float scale = variant == 1 ? scales[n * padded + g] : scales[g * N + n];
+        volatile float v = ((float)code - (float)zeros[n * groups + g]) * scale;
+        out[n * K + k] = v;
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GPTQ weights (onnx_core/runtime/gptq.cc:166-228, Pieces, Code, Zero and
+ * Reconstructed).  Words of `width` bytes (1, 2, 4, 8; little-endian).
+ * Linear layouts (every format but gptq_p at 3 bits and 5-7 bits): logical
+ * code `index` occupies bits index * bits .. of a bit stream of words, split
+ * across two words where it crosses one.  Planar layouts (32-bit words):
+ * each block of 32 codes spans `bits` words, its 4-, 2- and 1-bit planes (the
+ * ones the width has, low to high) one after the other, each plane's code i
+ * at bits (i % (32 / plane)) * plane of word (i / (32 / plane)).  qweight
+ * [rows, N]: code (k, n) is index k of column n's stream (word w at
+ * w * N + n); qzeros [groups, zero_columns]: the zero of (group, n) is index
+ * n of row group's stream (word w at group * zero_columns + w), plus 1 for
+ * format 0 ("gptq"; 1 "gptq_v2", 2 "gptq_p").  value = (code - zero) *
+ * scale[g_idx[k] * N + n] in fp32 (exact).  Writes codes [N, K], zeros
+ * [N, groups] (INT16, the +1 included) and the FLOAT values [N, K].
+ * Returns 0. */
+static uint64_t gq_word(const uint8_t *p, int width) {
+  uint64_t w = 0;
+  for (int i = 0; i < width; ++i) w |= (uint64_t)p[i] << (8 * i);
+  return w;
+}
+
+static uint32_t gq_code(const uint8_t *data, int width, int bits, int planar, int64_t index, int64_t stride,
+                        int64_t other, int zeros) {
+  const int wb = 8 * width;
+  uint32_t result = 0;
+#define GQ_PIECE(word, shift, nb, off)                                                            \
+  do {                                                                                            \
+    const int64_t pos_ = zeros ? other * stride + (word) : (word) * stride + other;               \
+    result |= (uint32_t)((gq_word(data + pos_ * width, width) >> (shift)) & ((1ull << (nb)) - 1)) \
+              << (off);                                                                           \
+  } while (0)
+  if (!planar) {
+    const int64_t bit = index * bits;
+    const int shift = (int)(bit % wb);
+    const int low = bits < wb - shift ? bits : wb - shift;
+    GQ_PIECE(bit / wb, shift, low, 0);
+    if (low != bits) GQ_PIECE(bit / wb + 1, 0, bits - low, low);
+  } else {
+    int offset = 0;
+    int64_t word = (index / 32) * bits;
+    for (int plane = 4; plane >= 1; plane /= 2) {
+      if (!(bits & plane)) continue;
+      const int factor = 32 / plane;
+      GQ_PIECE(word + (index % 32) / factor, (int)((index % 32) % factor) * plane, plane, offset);
+      offset += plane;
+      word += plane;
+    }
+  }
+#undef GQ_PIECE
+  return result;
+}
+
+int orc_gptq_decode(int format, int bits, int width, const void *qweight, const void *qzeros, const float *scales,
+                    const int32_t *g_idx, int64_t K, int64_t N, int64_t group, uint8_t *codes, int16_t *zeros,
+                    float *out) {
+  const int planar = bits == 5 || bits == 6 || bits == 7 || (format == 2 && bits == 3);
+  const int64_t eff = group == -1 ? K : group, groups = (K + eff - 1) / eff;
+  const int64_t zero_columns = (N * bits + 8 * width - 1) / (8 * width);
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t g = 0; g < groups; ++g)
+      zeros[n * groups + g] = (int16_t)(gq_code((const uint8_t *)qzeros, width, bits, planar, n, zero_columns, g, 1) +
+                                        (format == 0 ? 1 : 0));
+    for (int64_t k = 0; k < K; ++k) {
+      const uint32_t code = gq_code((const uint8_t *)qweight, width, bits, planar, k, N, n, 0);
+      const int64_t g = g_idx[k];
+      codes[n * K + k] = (uint8_t)code;
+      volatile float v = ((float)code - (float)zeros[n * groups + g]) * scales[g * N + n];
+      out[n * K + k] = v;
+    }
+  }
+  return 0;
+}

@@ -184,6 +184,21 @@ int orc_qlinear_conv(const void *x, int x_dtype, const int64_t *x_shape, int x_r
                      const int64_t *kernel_shape, const int64_t *strides, const int64_t *pads,
                      const int64_t *dilations, int auto_pad, void *y);
 
+
+/* AWQ weights, awq.cc:185-247: variant 0 "gemm" (4 or 8 bits), 1 "gemv",
+ * 2 "gemv_fast" / "llm-awq"; codes [N, K], zeros [N, groups], FLOAT values
+ * [N, K]; scales and zero_terms (variant 2) are decoded values. */
+int orc_awq_decode(int variant, int bits, const void *qweight, const void *qzeros, const float *zero_terms,
+                   const float *scales, int64_t K, int64_t N, int64_t group, int64_t padded, uint8_t *codes,
+                   uint8_t *zeros, float *out);
+
+/* GPTQ weights, gptq.cc:166-228: format 0 "gptq" (zero + 1), 1 "gptq_v2",
+ * 2 "gptq_p"; words of `width` bytes; codes [N, K], zeros [N, groups] INT16,
+ * FLOAT values [N, K]; scales decoded [groups, N]; g_idx [K]. */
+int orc_gptq_decode(int format, int bits, int width, const void *qweight, const void *qzeros, const float *scales,
+                    const int32_t *g_idx, int64_t K, int64_t N, int64_t group, uint8_t *codes, int16_t *zeros,
+                    float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,6 +109,12 @@ def _declare(L):
     L.orc_ort_nbits_decode.restype = ctypes.c_int
     L.orc_ort_nbits_decode.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                        ctypes.c_int64, P]
+    L.orc_awq_decode.restype = ctypes.c_int
+    L.orc_awq_decode.argtypes = [ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int64, ctypes.c_int64,
+                                 ctypes.c_int64, ctypes.c_int64, P, P, P]
+    L.orc_gptq_decode.restype = ctypes.c_int
+    L.orc_gptq_decode.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int64,
+                                  ctypes.c_int64, ctypes.c_int64, P, P, P]
     L.orc_grouped_matmul.restype = ctypes.c_int
     L.orc_grouped_matmul.argtypes = [ctypes.c_int, P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int, P, ctypes.c_int64, P, P]
@@ -490,3 +496,58 @@ def dequantize_packed(x: np.ndarray, fmt: str, shape, output_dtype: int = FLOAT)
     if output_dtype == 11:  # DOUBLE
         return out.astype(np.float64)
     return out
+
+
+# ---- AWQ and GPTQ weights (awq.cc:185-247, gptq.cc:166-228) ------------------
+
+AWQ_VARIANTS = {"gemm": 0, "gemv": 1, "gemv_fast": 2, "llm-awq": 2}
+GPTQ_FORMATS = {"gptq": 0, "gptq_v2": 1, "gptq_p": 2}
+
+
+def awq_decode(variant: str, qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, K: int, N: int,
+               group: int, bits: int = 4):
+    """AWQ weight -> (codes uint8 [N, K], zeros uint8 [N, groups], FLOAT values
+    float32 [N, K]).  qweight / qzeros in the variant's integer layout (for
+    gemv_fast / llm-awq, qzeros is the float zero-term array [padded, N]);
+    scales float values in the variant's layout ([groups, N] gemm, [N, padded]
+    gemv, [padded, N] gemv_fast / llm-awq)."""
+    v = AWQ_VARIANTS[variant]
+    qw = np.ascontiguousarray(qweight)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    eff = K if group == -1 else group
+    groups = K // eff
+    padded = sc.shape[1] if v == 1 else 0
+    if v == 2:
+        zt = np.ascontiguousarray(qzeros, dtype=np.float32)
+        qz = np.zeros(1, np.uint32)
+    else:
+        qz = np.ascontiguousarray(qzeros)
+        zt = np.zeros(1, np.float32)
+    codes = np.empty((N, K), np.uint8)
+    zeros = np.zeros((N, groups), np.uint8)
+    out = np.empty((N, K), np.float32)
+    rc = lib().orc_awq_decode(v, bits, _ptr(qw), _ptr(qz), _ptr(zt), _ptr(sc), K, N, group, padded, _ptr(codes),
+                              _ptr(zeros), _ptr(out))
+    if rc:
+        raise ValueError(f"awq_decode error {rc}")
+    return codes, zeros, out
+
+
+def gptq_decode(fmt: str, bits: int, qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray,
+                g_idx: np.ndarray, K: int, N: int, group: int):
+    """GPTQ weight -> (codes uint8 [N, K], zeros int16 [N, groups], FLOAT
+    values float32 [N, K]).  qweight / qzeros integer words (their itemsize is
+    the word width); scales float values [groups, N]; g_idx int32 [K]."""
+    qw = np.ascontiguousarray(qweight)
+    qz = np.ascontiguousarray(qzeros)
+    assert qw.dtype.itemsize == qz.dtype.itemsize
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    gi = np.ascontiguousarray(g_idx, dtype=np.int32)
+    eff = K if group == -1 else group
+    groups = -(-K // eff)
+    codes = np.empty((N, K), np.uint8)
+    zeros = np.empty((N, groups), np.int16)
+    out = np.empty((N, K), np.float32)
+    lib().orc_gptq_decode(GPTQ_FORMATS[fmt], bits, qw.dtype.itemsize, _ptr(qw), _ptr(qz), _ptr(sc), _ptr(gi), K, N,
+                          group, _ptr(codes), _ptr(zeros), _ptr(out))
+    return codes, zeros, out
