@@ -340,6 +340,75 @@ int onnxl_amd_prepare_matmul_nbits(const onnxl_amd_tensor *B, const onnxl_amd_te
                                    int64_t block_size, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
                                    onnxl_amd_tensor *zero_point, void *stream);
 
+/* AWQ checkpoint weights (onnx_core/runtime/awq.cc; the reference imports
+ * them with ImportAwqWeights, quantization.h:724, and decodes them with
+ * ReconstructAwqWeights, quantization.h:735, awq.cc:370-387, through
+ * DequantizeTensor, quantization.cc:3121-3147).  variant "gemm" (bits 4 or
+ * 8): qweight INT32 [K, N * bits / 32] (4 bits: column n at nibble
+ * {0,4,1,5,2,6,3,7}[n % 8] of word n / 8), qzeros INT32 [groups, N * bits /
+ * 32], scales FLOAT16 / BFLOAT16 [groups, N]; "gemv" (4 bits): qweight INT32
+ * [N, K / 8], qzeros INT32 [N, padded / 8], scales FLOAT16 [N, padded];
+ * "gemv_fast" / "llm-awq" (4 bits): qweight INT16 [N / 4, K], qzeros (the
+ * float zero terms; "scaled_zeros" upstream for llm-awq) and scales FLOAT16
+ * [padded, N] (padded = the group count rounded as awq.cc:97-100 does).
+ * W [K, N] = (code - zero) * scale (gemv_fast / llm-awq: code * scale +
+ * zero term).  The format's checks raise INVALID_ARGUMENT with the
+ * reference's messages.
+ *
+ * onnxl_amd_prepare_awq writes the fused DequantizeLinear -> MatMul operands
+ * into caller-allocated device buffers of the sizes onnxl_amd_prepare_awq_size
+ * returns (16-byte aligned): weight UINT4 in the tiled layout of
+ * onnxl_amd_prepare_weight (4 bits) or UINT8 [K, N] (8 bits), zero_point UINT4
+ * / UINT8 [groups, N], scale FLOAT16 [groups, N] (FLOAT16 scales) or FLOAT
+ * (BFLOAT16 scales, widened exactly: pass cast_to = BFLOAT16), and sets their
+ * descriptors; then pass (A, weight, scale, zero_point, axis = 0, cast_to) to
+ * onnxl_amd_dequantize_linear_matmul.  gemv_fast / llm-awq return
+ * ONNXL_AMD_UNSUPPORTED there (float zero terms).
+ *
+ * onnxl_amd_dequantize_awq decodes every variant to y [N, K] (the reference's
+ * logical [out_features, in_features]) of y's dtype: FLOAT, FLOAT16,
+ * BFLOAT16 or DOUBLE, rounded to nearest even, raising the reference's
+ * "Dequantization output dtype overflow." where a value does not fit. */
+int onnxl_amd_prepare_awq_size(const char *variant, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                               int32_t scale_dtype, int64_t *weight_bytes, int64_t *scale_bytes,
+                               int64_t *zero_point_bytes);
+int onnxl_amd_prepare_awq(const char *variant, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                          const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                          onnxl_amd_tensor *weight, onnxl_amd_tensor *scale, onnxl_amd_tensor *zero_point,
+                          void *stream);
+int onnxl_amd_dequantize_awq(const char *variant, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                             const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                             onnxl_amd_tensor *y, void *stream);
+
+/* GPTQ checkpoint weights (onnx_core/runtime/gptq.cc; ImportGptqWeights,
+ * quantization.h:629, ReconstructGptqWeights, quantization.h:644, gptq.cc:399-412).  format
+ * "gptq" (stored zero + 1), "gptq_v2" or "gptq_p"; bits 2-8 (5-7 and gptq_p
+ * at 3 bits in planar 32-code blocks); words INT8 / INT16 / INT32 / INT64
+ * (qweight's dtype): qweight [ceil(K * bits / word bits), N] (column n's
+ * codes as a little-endian bit stream down the rows), qzeros [groups,
+ * ceil(N * bits / word bits)], scales FLOAT16 / BFLOAT16 / FLOAT [groups, N],
+ * g_idx INT32 [K] (the group of each row).  W [K, N] = (code - zero) *
+ * scale[g_idx[k]].  The format's checks raise INVALID_ARGUMENT with the
+ * reference's messages.
+ *
+ * onnxl_amd_prepare_gptq writes the fused operands as onnxl_amd_prepare_awq
+ * does: codes of at most 4 bits as tiled UINT4, 5-8 bits as UINT8 [K, N];
+ * scale FLOAT16 or FLOAT (BFLOAT16 widened; FLOAT / BFLOAT16 scales then take
+ * cast_to = A's dtype).  A group map other than g_idx[k] = k / group_size
+ * (act-order) and K not a multiple of group_size return ONNXL_AMD_UNSUPPORTED
+ * there.  onnxl_amd_dequantize_gptq decodes every format and group map to
+ * y [N, K] as onnxl_amd_dequantize_awq does. */
+int onnxl_amd_prepare_gptq_size(const char *format, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                                int32_t word_dtype, int32_t scale_dtype, int64_t *weight_bytes, int64_t *scale_bytes,
+                                int64_t *zero_point_bytes);
+int onnxl_amd_prepare_gptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                           const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
+                           int64_t bits, int64_t group_size, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                           onnxl_amd_tensor *zero_point, void *stream);
+int onnxl_amd_dequantize_gptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                              const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
+                              int64_t bits, int64_t group_size, onnxl_amd_tensor *y, void *stream);
+
 /* Waits for all work queued by this library on `stream`. */
 int onnxl_amd_synchronize(void *stream);
 

@@ -91,6 +91,17 @@ def lib() -> ctypes.CDLL:
                                                           ctypes.POINTER(I64), ctypes.POINTER(I64)]
         L.onnxl_amd_prepare_matmul_nbits.argtypes = [TP, TP, TP, I64, I64, I64, I64, ctypes.POINTER(Tensor),
                                                      ctypes.POINTER(Tensor), ctypes.POINTER(Tensor), ctypes.c_void_p]
+        PT = ctypes.POINTER(Tensor)
+        I32 = ctypes.c_int32
+        CS = ctypes.c_char_p
+        L.onnxl_amd_prepare_awq_size.argtypes = [CS, I64, I64, I64, I64, I32, ctypes.POINTER(I64),
+                                                 ctypes.POINTER(I64), ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_awq.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, PT, PT, PT, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_awq.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, TP, ctypes.c_void_p]
+        L.onnxl_amd_prepare_gptq_size.argtypes = [CS, I64, I64, I64, I64, I32, I32, ctypes.POINTER(I64),
+                                                  ctypes.POINTER(I64), ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_gptq.argtypes = [CS, TP, TP, TP, TP, I64, I64, I64, I64, PT, PT, PT, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_gptq.argtypes = [CS, TP, TP, TP, TP, I64, I64, I64, I64, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -232,9 +243,10 @@ def prepare_weight(x, x_dtype: int, x_shape=None) -> PreparedWeight:
 
 
 class PreparedNbits:
-    """An ORT MatMulNBits weight prepared by onnxl_amd_prepare_matmul_nbits:
-    the fused kernels' weight, scale and zero point (None without zero
-    points), each a PreparedWeight (device storage + descriptor)."""
+    """A packed-checkpoint weight prepared for the fused DequantizeLinear ->
+    MatMul kernels (onnxl_amd_prepare_matmul_nbits / _awq / _gptq): weight,
+    scale and zero point (None without zero points), each a PreparedWeight
+    (device storage + descriptor)."""
 
     def __init__(self, weight, scale, zero_point, K, N):
         self.weight, self.scale, self.zero_point = weight, scale, zero_point
@@ -264,10 +276,85 @@ def prepare_matmul_nbits(B, scales, zero_points, K: int, N: int, bits: int, bloc
 
 
 def matmul_nbits(a, prepared: PreparedNbits, out=None):
-    """MatMul(a, W) for a prepared ORT MatMulNBits weight W [K, N] through the
-    fused DequantizeLinear -> MatMul entry point (blocked scales, axis 0)."""
-    return dequantize_linear_matmul(a, prepared.weight, prepared.scale, prepared.zero_point, 0, 0,
+    """MatMul(a, W) for a prepared weight W [K, N] through the fused
+    DequantizeLinear -> MatMul entry point (blocked scales, axis 0); FLOAT
+    scales take a Cast to a's dtype."""
+    cast_to = _torch_code(a.dtype) if prepared.scale.desc.data_type == FLOAT else 0
+    return dequantize_linear_matmul(a, prepared.weight, prepared.scale, prepared.zero_point, 0, cast_to,
                                     x_shape=prepared.shape, out=out)
+
+
+def _prepared_triplet(sizes, run) -> tuple:
+    torch = _torch()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    bufs = [torch.empty(max(n.value, 16), dtype=torch.uint8, device=dev) for n in sizes]
+    descs = [describe(b) for b in bufs]
+    _check(run(*(ctypes.byref(d) for d in descs), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    for d, b in zip(descs, bufs):
+        d._keep = b
+    return tuple(PreparedWeight(b, d) for b, d in zip(bufs, descs))
+
+
+def _scale_code(scales) -> int:
+    if isinstance(scales, np.ndarray) and scales.dtype == np.uint16:
+        raise InvalidArgument("pass FLOAT16 / BFLOAT16 scales as float16 arrays or torch tensors")
+    return _NP_CODES[scales.dtype] if isinstance(scales, np.ndarray) else _torch_code(scales.dtype)
+
+
+def prepare_awq(variant: str, qweight, qzeros, scales, K: int, N: int, group_size: int, bits: int = 4) -> PreparedNbits:
+    """onnxl_amd_prepare_awq: an AWQ checkpoint (awq.cc layouts) as the fused
+    kernels' UINT4 / UINT8 weight, zero points and scales."""
+    sizes = [ctypes.c_int64(0) for _ in range(3)]
+    _check(lib().onnxl_amd_prepare_awq_size(variant.encode(), K, N, bits, group_size, _scale_code(scales),
+                                            *(ctypes.byref(x) for x in sizes)))
+    w, s, z = _prepared_triplet(sizes, lambda pw, ps, pz, st: lib().onnxl_amd_prepare_awq(
+        variant.encode(), describe(qweight), describe(qzeros), describe(scales), K, N, bits, group_size, pw, ps, pz,
+        st))
+    return PreparedNbits(w, s, z, K, N)
+
+
+def prepare_gptq(fmt: str, qweight, qzeros, scales, g_idx, K: int, N: int, bits: int,
+                 group_size: int) -> PreparedNbits:
+    """onnxl_amd_prepare_gptq: a GPTQ checkpoint (gptq.cc layouts) as the
+    fused kernels' UINT4 / UINT8 weight, zero points and scales."""
+    sizes = [ctypes.c_int64(0) for _ in range(3)]
+    word = _NP_CODES[qweight.dtype] if isinstance(qweight, np.ndarray) else _torch_code(qweight.dtype)
+    _check(lib().onnxl_amd_prepare_gptq_size(fmt.encode(), K, N, bits, group_size, word, _scale_code(scales),
+                                             *(ctypes.byref(x) for x in sizes)))
+    w, s, z = _prepared_triplet(sizes, lambda pw, ps, pz, st: lib().onnxl_amd_prepare_gptq(
+        fmt.encode(), describe(qweight), describe(qzeros), describe(scales), describe(g_idx), K, N, bits,
+        group_size, pw, ps, pz, st))
+    return PreparedNbits(w, s, z, K, N)
+
+
+
+def _decode_out(K, N, output_dtype, like, out):
+    torch = _torch()
+    if out is None:
+        tdt = {FLOAT: torch.float32, FLOAT16: torch.float16, BFLOAT16: torch.bfloat16,
+               DOUBLE: torch.float64}.get(output_dtype, torch.float32)
+        out = _empty((N, K), tdt, _device_of(*like))
+    return out
+
+
+def dequantize_awq(variant: str, qweight, qzeros, scales, K: int, N: int, group_size: int, bits: int = 4,
+                   output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_awq: the AWQ weight as [N, K] values."""
+    out = _decode_out(K, N, output_dtype, (qweight, qzeros, scales), out)
+    _check(lib().onnxl_amd_dequantize_awq(variant.encode(), describe(qweight), describe(qzeros), describe(scales),
+                                          K, N, bits, group_size, describe(out),
+                                          _stream_of(qweight, qzeros, scales, out)))
+    return out
+
+
+def dequantize_gptq(fmt: str, qweight, qzeros, scales, g_idx, K: int, N: int, bits: int, group_size: int,
+                    output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_gptq: the GPTQ weight as [N, K] values."""
+    out = _decode_out(K, N, output_dtype, (qweight, qzeros, scales, g_idx), out)
+    _check(lib().onnxl_amd_dequantize_gptq(fmt.encode(), describe(qweight), describe(qzeros), describe(scales),
+                                           describe(g_idx), K, N, bits, group_size, describe(out),
+                                           _stream_of(qweight, qzeros, scales, g_idx, out)))
+    return out
 
 
 class ConvAttrs(ctypes.Structure):

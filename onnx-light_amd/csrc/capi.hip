@@ -12,6 +12,7 @@
 #include <memory>
 #include <mutex>
 
+#include "checkpoint_layout.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -1590,6 +1591,377 @@ int PrepareMatMulNbits(const onnxl_amd_tensor *B, const onnxl_amd_tensor *scales
   return ONNXL_AMD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// AWQ and GPTQ checkpoint weights (onnx_core/runtime/awq.cc:47-246,
+// onnx_core/runtime/gptq.cc:49-253): the formats' geometry and value checks
+// with the reference's messages, then either preparation into the fused
+// DequantizeLinear -> MatMul operands or a dense decode to [N, K].  Value
+// checks run on host copies (one-time work per weight).
+
+struct CkptPlan {
+  CkptLayout L{};                 // qweight / qzeros pointers set per use
+  const char *fmt = "AWQ";        // message prefix
+  int32_t word_type = kInt32, zeros_type = kInt32, scale_type = kFloat16;
+  const char *zeros_name = "qzeros";
+  Shape qweight_shape, qzeros_shape, scales_shape;
+  bool trivial_groups = true;     // GPTQ: g_idx[k] == k / group (set after reading g_idx)
+};
+
+// awq.cc:64-118 (Geometry), in the reference's order of checks.
+CkptPlan PlanAwq(const char *variant, int64_t K, int64_t N, int64_t bits, int64_t group, int32_t scale_type) {
+  const std::string v = variant ? variant : "";
+  OLA_ENFORCE(K > 0 && N > 0 && (bits == 4 || (bits == 8 && v == "gemm")),
+              "AWQ requires positive dimensions, supported bits and group_axis=1.");
+  OLA_ENFORCE(v == "gemm" || v == "gemv" || v == "gemv_fast" || v == "llm-awq", "AWQ unsupported variant.");
+  OLA_ENFORCE(group == -1 || group > 0, "AWQ unsupported group size.");
+  const int64_t eff = group == -1 ? K : group;
+  OLA_ENFORCE(K % eff == 0, "AWQ requires complete groups.");
+  CkptPlan p;
+  CkptLayout &L = p.L;
+  L.K = K, L.N = N, L.bits = (int)bits, L.group = eff, L.groups = K / eff, L.width = 4;
+  p.scale_type = scale_type;
+  if (v == "gemm") {
+    OLA_ENFORCE(N % (32 / bits) == 0 && (scale_type == kFloat16 || scale_type == kBfloat16),
+                "AWQ GEMM requires complete INT32 words and FP16/BF16 scales.");
+    L.kind = kAwqGemm;
+    p.qweight_shape = {K, N / (32 / bits)};
+    p.qzeros_shape = {L.groups, N / (32 / bits)};
+    p.scales_shape = {L.groups, N};
+    return p;
+  }
+  OLA_ENFORCE(eff >= 128 || eff == 16 || eff == 32 || eff == 64, "AWQ invalid effective group size.");
+  OLA_ENFORCE(scale_type == kFloat16, "AWQ GEMV requires FLOAT16 parameters.");
+  const int64_t multiplier = eff >= 128 ? 1 : 128 / eff;
+  const int64_t words = L.groups / 8 + (L.groups % 8 != 0);
+  L.padded = (words / multiplier + (words % multiplier != 0)) * multiplier * 8;
+  if (v == "gemv") {
+    OLA_ENFORCE(K % 8 == 0, "AWQ GEMV requires K divisible by eight.");
+    L.kind = kAwqGemv;
+    p.qweight_shape = {N, K / 8};
+    p.qzeros_shape = {N, L.padded / 8};
+    p.scales_shape = {N, L.padded};
+  } else {
+    OLA_ENFORCE(K % 64 == 0 && N % 4 == 0, "AWQ GEMV_FAST requires K divisible by 64 and N by four.");
+    L.kind = kAwqFast;
+    L.width = 2;
+    p.word_type = kInt16;
+    p.zeros_type = kFloat16;
+    p.zeros_name = v == "llm-awq" ? "scaled_zeros" : "qzeros";
+    p.qweight_shape = {N / 4, K};
+    p.qzeros_shape = {L.padded, N};
+    p.scales_shape = {L.padded, N};
+  }
+  return p;
+}
+
+// gptq.cc:67-123 (Geometry), in the reference's order of checks; the word
+// dtype is qweight's.
+CkptPlan PlanGptq(const char *format, int64_t K, int64_t N, int64_t bits, int64_t group, int32_t word_type,
+                  int32_t scale_type) {
+  const std::string f = format ? format : "";
+  OLA_ENFORCE(f == "gptq" || f == "gptq_v2" || f == "gptq_p", "GPTQ unsupported format.");
+  OLA_ENFORCE(K > 0 && N > 0 && bits >= 2 && bits <= 8, "GPTQ invalid dimensions, bits or group axis.");
+  OLA_ENFORCE(group == -1 || group > 0, "GPTQ invalid group size.");
+  OLA_ENFORCE(word_type == kInt8 || word_type == kInt16 || word_type == kInt32 || word_type == kInt64,
+              "GPTQ unsupported packed word dtype.");
+  const int width = (int)ElementSize(word_type);
+  OLA_ENFORCE(f != "gptq_p" || width == 4, "GPTQ planar checkpoint format requires INT32 words.");
+  OLA_ENFORCE(f == "gptq_p" || bits == 2 || bits == 3 || bits == 4 || bits == 8,
+              "GPTQ five-, six- and seven-bit codes require the gptq_p format.");
+  const bool planar = bits == 5 || bits == 6 || bits == 7 || (f == "gptq_p" && bits == 3);
+  if (bits == 3 || planar)
+    OLA_ENFORCE(width == 4 && K % 32 == 0 && N % 32 == 0,
+                "GPTQ three-bit and planar layouts require INT32 and 32-code blocks.");
+  OLA_ENFORCE(scale_type == kFloat16 || scale_type == kBfloat16 || scale_type == kFloat,
+              "GPTQ unsupported scales dtype.");
+  CkptPlan p;
+  p.fmt = "GPTQ";
+  CkptLayout &L = p.L;
+  L.kind = kGptq, L.K = K, L.N = N, L.bits = (int)bits, L.width = width, L.planar = planar;
+  L.zero_add = f == "gptq" ? 1 : 0;
+  L.group = group == -1 ? K : group;
+  L.groups = (K + L.group - 1) / L.group;
+  const int64_t wb = 8 * width;
+  L.zero_columns = (N * bits + wb - 1) / wb;
+  p.word_type = p.zeros_type = word_type;
+  p.scale_type = scale_type;
+  p.qweight_shape = {(K * bits + wb - 1) / wb, N};
+  p.qzeros_shape = {L.groups, L.zero_columns};
+  p.scales_shape = {L.groups, N};
+  return p;
+}
+
+void CheckCkptTensor(const CkptPlan &p, const onnxl_amd_tensor *t, int32_t type, const Shape &shape,
+                     const char *name) {
+  OLA_ENFORCE(!Absent(t) && t->data_type == type && ShapeOf(*t) == shape &&
+                  t->size_bytes >= NumElements(shape) * ElementSize(type) && t->data != nullptr,
+              p.fmt, " invalid tensor type, shape or byte extent: ", name, ".");
+  CheckDescriptor(t, name);
+  OLA_ENFORCE(reinterpret_cast<uintptr_t>(t->data) % ElementSize(type) == 0, p.fmt, ": ", name,
+              " must be aligned to its ", ElementSize(type), "-byte elements.");
+}
+
+float Bf16BitsToFloat(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// Host copies of a checkpoint's parameters, then the formats' value checks.
+struct CkptHost {
+  std::vector<float> scales, zero_terms;  // decoded; zero_terms: AWQ gemv_fast / llm-awq
+  std::vector<uint8_t> qzeros, qweight;   // raw words (qweight read only when a scan needs it)
+  std::vector<int32_t> g_idx;             // GPTQ
+};
+
+std::vector<float> ReadFloats(const onnxl_amd_tensor &t) {
+  const int64_t n = NumElements(t);
+  std::vector<float> out((size_t)n);
+  if (t.data_type == kFloat) {
+    ReadBytes(t, 0, out.data(), (size_t)n * 4);
+    return out;
+  }
+  std::vector<uint16_t> h((size_t)n);
+  ReadBytes(t, 0, h.data(), (size_t)n * 2);
+  for (int64_t i = 0; i < n; ++i) out[i] = t.data_type == kFloat16 ? HalfBitsToFloat(h[i]) : Bf16BitsToFloat(h[i]);
+  return out;
+}
+
+// The value of weight (k, n) of group g as the kernels compute it.
+float CkptValue(const CkptLayout &L, const CkptHost &h, int64_t g, int64_t k, int64_t n) {
+  const int64_t si = CkptScaleIndex(L, g, n);
+  const double code = (double)CkptCode(L, k, n);
+  if (L.kind == kAwqFast) {
+    const float product = (float)(code * (double)h.scales[si]);  // exact in double, one rounding
+    volatile float sum = product + h.zero_terms[si];
+    return sum;
+  }
+  return (float)((code - (double)CkptZero(L, g, n)) * (double)h.scales[si]);
+}
+
+// Throws `msg` when some value reaches `limit` in magnitude (or is not
+// finite).  A (group, column) pair whose bound max|code - zero| * |scale|
+// (+ |zero term|) stays below the limit needs no scan; the others are
+// scanned exactly over their rows, reading qweight on first need.
+void CheckCkptMagnitudes(const CkptPlan &p, const onnxl_amd_tensor *qweight, CkptHost &h, double limit,
+                         const std::string &msg) {
+  CkptLayout L = p.L;
+  L.qzeros = h.qzeros.data();
+  const double maxq = (double)((1u << L.bits) - 1);
+  for (int64_t g = 0; g < L.groups; ++g)
+    for (int64_t n = 0; n < L.N; ++n) {
+      const int64_t si = CkptScaleIndex(L, g, n);
+      double bound;
+      if (L.kind == kAwqFast) {
+        bound = maxq * std::fabs((double)h.scales[si]) + std::fabs((double)h.zero_terms[si]);
+      } else {
+        const double z = (double)CkptZero(L, g, n);
+        bound = std::max(z, maxq - z) * std::fabs((double)h.scales[si]);
+      }
+      if (bound < limit * 0.999) continue;
+      if (h.qweight.empty()) {
+        h.qweight.resize((size_t)(NumElements(*qweight) * ElementSize(qweight->data_type)));
+        ReadBytes(*qweight, 0, h.qweight.data(), h.qweight.size());
+      }
+      L.qweight = h.qweight.data();
+      for (int64_t k = 0; k < L.K; ++k) {
+        const int64_t gk = h.g_idx.empty() ? k / L.group : (int64_t)h.g_idx[(size_t)k];
+        if (gk != g) continue;
+        const float v = CkptValue(L, h, g, k, n);
+        OLA_ENFORCE(std::isfinite(v) && std::fabs((double)v) < limit, msg);
+      }
+    }
+}
+
+constexpr double kFloatOverflow = 3.4028235677973366e38 * (1.0 + 1.0 / (1 << 25));  // FLT_MAX + half an ulp
+
+// awq.cc:156-183 and :232-245 (CheckParameter, CheckReconstruction).
+CkptHost CheckAwqValues(CkptPlan &p, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                        const onnxl_amd_tensor *scales) {
+  CkptHost h;
+  CkptLayout &L = p.L;
+  if (L.kind == kAwqFast) {
+    h.zero_terms = ReadFloats(*qzeros);
+    for (float z : h.zero_terms) OLA_ENFORCE(std::isfinite(z), "AWQ nonfinite parameter.");
+  } else {
+    h.qzeros.resize((size_t)(NumElements(*qzeros) * 4));
+    ReadBytes(*qzeros, 0, h.qzeros.data(), h.qzeros.size());
+  }
+  h.scales = ReadFloats(*scales);
+  for (size_t i = 0; i < h.scales.size(); ++i) {
+    OLA_ENFORCE(std::isfinite(h.scales[i]), "AWQ nonfinite parameter.");
+    const int64_t g = L.kind == kAwqGemv ? (int64_t)i % L.padded : (int64_t)i / L.N;
+    OLA_ENFORCE(g >= L.groups || h.scales[i] > 0, "AWQ nonpositive used scale.");
+  }
+  if (p.scale_type != kFloat16)  // finite FP16 parameters cannot overflow FLOAT with these codes
+    CheckCkptMagnitudes(p, qweight, h, kFloatOverflow, "AWQ FLOAT reconstruction overflow.");
+  return h;
+}
+
+// gptq.cc:230-253 (CheckData).
+CkptHost CheckGptqValues(CkptPlan &p, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                         const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx) {
+  CkptHost h;
+  CkptLayout &L = p.L;
+  h.g_idx.resize((size_t)L.K);
+  ReadBytes(*g_idx, 0, h.g_idx.data(), h.g_idx.size() * 4);
+  for (int64_t k = 0; k < L.K; ++k) {
+    OLA_ENFORCE(h.g_idx[k] >= 0 && h.g_idx[k] < L.groups, "GPTQ invalid group map index.");
+    if (h.g_idx[k] != k / L.group) p.trivial_groups = false;
+  }
+  h.qzeros.resize((size_t)(NumElements(*qzeros) * L.width));
+  ReadBytes(*qzeros, 0, h.qzeros.data(), h.qzeros.size());
+  h.scales = ReadFloats(*scales);
+  CkptLayout Lz = L;
+  Lz.qzeros = h.qzeros.data();
+  const uint32_t maxq = (1u << L.bits) - 1;
+  for (size_t i = 0; i < h.scales.size(); ++i) {
+    OLA_ENFORCE(std::isfinite(h.scales[i]) && h.scales[i] > 0, "GPTQ nonfinite or nonpositive scale.");
+    if (L.zero_add)
+      OLA_ENFORCE(GptqField(Lz, Lz.qzeros, (int64_t)i % L.N, (int64_t)i / L.N, true) != maxq,
+                  "GPTQ v1 all-ones zero field has ambiguous upstream conversion semantics.");
+  }
+  if (p.scale_type != kFloat16)
+    CheckCkptMagnitudes(p, qweight, h, kFloatOverflow, "GPTQ FLOAT reconstruction overflow.");
+  return h;
+}
+
+struct CkptSizes {
+  int64_t weight, scale, zp;
+};
+
+CkptSizes CkptPreparedSizes(const CkptPlan &p) {
+  const CkptLayout &L = p.L;
+  const bool four = L.bits <= 4;
+  return {four ? TiledInt4Bytes(L.K, L.N) : L.K * L.N, L.groups * L.N * (p.scale_type == kFloat16 ? 2 : 4),
+          four ? (L.groups * L.N + 1) / 2 : L.groups * L.N};
+}
+
+// Writes the fused kernels' operands (see LaunchCkptPrepare) and sets the
+// output descriptors: weight UINT4 tiled (bits <= 4) or UINT8 [K, N], zero
+// point UINT4 / UINT8 [groups, N], scale FLOAT16 [groups, N] for FLOAT16
+// scales, else FLOAT (BFLOAT16 widened exactly).
+int PrepareCkpt(const char *what, CkptPlan &p, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                const onnxl_amd_tensor *scales, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                onnxl_amd_tensor *zero_point, hipStream_t stream) {
+  OLA_ENFORCE(weight && scale && zero_point, what, ": weight, scale and zero_point are required.");
+  const CkptSizes sz = CkptPreparedSizes(p);
+  auto out_ok = [&](onnxl_amd_tensor *t, int64_t need, const char *name) {
+    OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE, what, ": ", name, " must be device memory.");
+    OLA_ENFORCE(t->size_bytes >= need, what, ": ", name, " holds ", t->size_bytes, " bytes, needs ", need);
+    OLA_ENFORCE(need == 0 || (t->data != nullptr && reinterpret_cast<uintptr_t>(t->data) % 16 == 0), what, ": ",
+                name, " must be a 16-byte aligned device buffer.");
+  };
+  out_ok(weight, sz.weight, "weight");
+  out_ok(scale, sz.scale, "scale");
+  out_ok(zero_point, sz.zp, "zero_point");
+  Ctx();
+  Staging st(stream, 0, {qweight, qzeros, scales}, {});
+  CkptLayout L = p.L;
+  L.qweight = static_cast<const uint8_t *>(st.In(qweight));
+  L.qzeros = static_cast<const uint8_t *>(st.In(qzeros));
+  LaunchCkptPrepare(L, st.In(scales), p.scale_type, weight->data, scale->data, zero_point->data, stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  const bool four = L.bits <= 4;
+  auto set = [](onnxl_amd_tensor *t, int32_t dt, int64_t d0, int64_t d1, int32_t layout) {
+    t->data_type = dt;
+    t->rank = 2;
+    for (int i = 0; i < ONNXL_AMD_MAX_RANK; ++i) t->dims[i] = i == 0 ? d0 : (i == 1 ? d1 : 0);
+    t->layout = layout;
+  };
+  set(weight, four ? kUint4 : kUint8, L.K, L.N, four ? ONNXL_AMD_LAYOUT_TILED_INT4 : ONNXL_AMD_LAYOUT_ONNX);
+  set(scale, p.scale_type == kFloat16 ? kFloat16 : kFloat, L.groups, L.N, ONNXL_AMD_LAYOUT_ONNX);
+  set(zero_point, four ? kUint4 : kUint8, L.groups, L.N, ONNXL_AMD_LAYOUT_ONNX);
+  return ONNXL_AMD_OK;
+}
+
+// The dense decode: y [N, K] of y's dtype, then the reference's output
+// checks (quantization.cc:184-200, WriteFloat).
+int DecodeCkpt(CkptPlan &p, CkptHost &h, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+               const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, onnxl_amd_tensor *y,
+               hipStream_t stream) {
+  const CkptLayout &L0 = p.L;
+  OLA_ENFORCE(y != nullptr, p.fmt, ": y is required.");
+  CheckDescriptor(y, "y");
+  const int32_t odt = y->data_type;
+  OLA_ENFORCE(odt == kFloat || odt == kDouble || odt == kFloat16 || odt == kBfloat16,
+              "Quantization requires FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == L0.N && y->dims[1] == L0.K, p.fmt, ": y must be [N, K] = [", L0.N,
+              ", ", L0.K, "].");
+  if (odt == kFloat16 || odt == kBfloat16) {
+    // the largest magnitude that rounds to a finite value, plus the tie that rounds away
+    const double limit = odt == kFloat16 ? 65520.0 : std::ldexp(1.99609375, 127);
+    CheckCkptMagnitudes(p, qweight, h, limit, "Dequantization output dtype overflow.");
+  }
+  Ctx();
+  Staging st(stream, 0, {qweight, qzeros, scales, g_idx}, {y});
+  CkptLayout L = L0;
+  L.qweight = static_cast<const uint8_t *>(st.In(qweight));
+  L.qzeros = static_cast<const uint8_t *>(st.In(qzeros));
+  LaunchCkptDecode(L, st.In(scales), p.scale_type,
+                   L.kind == kAwqFast ? static_cast<const uint16_t *>(st.In(qzeros)) : nullptr,
+                   g_idx && p.trivial_groups == false ? static_cast<const int32_t *>(st.In(g_idx)) : nullptr, odt,
+                   st.Out(y), stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+void CheckAwqTensors(const CkptPlan &p, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                     const onnxl_amd_tensor *scales) {
+  CheckCkptTensor(p, qweight, p.word_type, p.qweight_shape, "qweight");
+  CheckCkptTensor(p, qzeros, p.zeros_type, p.qzeros_shape, p.zeros_name);
+  CheckCkptTensor(p, scales, p.scale_type, p.scales_shape, "scales");
+}
+
+CkptPlan AwqFromTensors(const char *variant, const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits,
+                        int64_t group) {
+  OLA_ENFORCE(!Absent(scales), "AWQ missing scales.");
+  return PlanAwq(variant, K, N, bits, group, scales->data_type);
+}
+
+CkptPlan GptqFromTensors(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                         const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
+                         int64_t bits, int64_t group) {
+  OLA_ENFORCE(!Absent(scales), "GPTQ missing scales.");
+  OLA_ENFORCE(!Absent(qweight), "GPTQ missing tensor qweight.");
+  CkptPlan p = PlanGptq(format, K, N, bits, group, qweight->data_type, scales->data_type);
+  CheckCkptTensor(p, qweight, p.word_type, p.qweight_shape, "qweight");
+  CheckCkptTensor(p, qzeros, p.zeros_type, p.qzeros_shape, "qzeros");
+  CheckCkptTensor(p, scales, p.scale_type, p.scales_shape, "scales");
+  CheckCkptTensor(p, g_idx, kInt32, {K}, "g_idx");
+  return p;
+}
+
+int PrepareAwq(const char *variant, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+               const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits, int64_t group,
+               onnxl_amd_tensor *weight, onnxl_amd_tensor *scale, onnxl_amd_tensor *zero_point, hipStream_t stream) {
+  CkptPlan p = AwqFromTensors(variant, scales, K, N, bits, group);
+  CheckAwqTensors(p, qweight, qzeros, scales);
+  CheckAwqValues(p, qweight, qzeros, scales);
+  if (p.L.kind == kAwqFast)
+    throw Unsupported("AWQ gemv_fast / llm-awq: float zero terms have no fused DequantizeLinear kernel "
+                      "(onnxl_amd_dequantize_awq decodes them)");
+  return PrepareCkpt("prepare_awq", p, qweight, qzeros, scales, weight, scale, zero_point, stream);
+}
+
+int PrepareGptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N, int64_t bits,
+                int64_t group, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale, onnxl_amd_tensor *zero_point,
+                hipStream_t stream) {
+  CkptPlan p = GptqFromTensors(format, qweight, qzeros, scales, g_idx, K, N, bits, group);
+  CheckGptqValues(p, qweight, qzeros, scales, g_idx);
+  if (K % p.L.group != 0)
+    throw Unsupported(Cat("GPTQ: K = ", K, " is not a multiple of group_size ", group,
+                          " (a partial last group has no fused kernel)"));
+  if (!p.trivial_groups)
+    throw Unsupported("GPTQ: a group map other than g_idx[k] = k / group_size (act-order) has no fused kernel "
+                      "(onnxl_amd_dequantize_gptq decodes it)");
+  return PrepareCkpt("prepare_gptq", p, qweight, qzeros, scales, weight, scale, zero_point, stream);
+}
+
 // Validation runs before any device work, so argument errors are reported
 // even before onnxl_amd_init (the first device access then raises
 // NotInitialized).
@@ -1815,6 +2187,73 @@ int onnxl_amd_prepare_matmul_nbits(const onnxl_amd_tensor *B, const onnxl_amd_te
   return Guard([&] {
     return PrepareMatMulNbits(B, scales, zero_points, K, N, bits, block_size, weight, scale, zero_point,
                               static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_awq_size(const char *variant, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                               int32_t scale_dtype, int64_t *weight_bytes, int64_t *scale_bytes,
+                               int64_t *zero_point_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(weight_bytes && scale_bytes && zero_point_bytes, "prepare_awq_size: null output");
+    const CkptSizes sz = CkptPreparedSizes(PlanAwq(variant, K, N, bits, group_size, scale_dtype));
+    *weight_bytes = sz.weight;
+    *scale_bytes = sz.scale;
+    *zero_point_bytes = sz.zp;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_awq(const char *variant, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                          const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                          onnxl_amd_tensor *weight, onnxl_amd_tensor *scale, onnxl_amd_tensor *zero_point,
+                          void *stream) {
+  return Guard([&] {
+    return PrepareAwq(variant, qweight, qzeros, scales, K, N, bits, group_size, weight, scale, zero_point,
+                      static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_awq(const char *variant, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                             const onnxl_amd_tensor *scales, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                             onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    CkptPlan p = AwqFromTensors(variant, scales, K, N, bits, group_size);
+    CheckAwqTensors(p, qweight, qzeros, scales);
+    CkptHost h = CheckAwqValues(p, qweight, qzeros, scales);
+    return DecodeCkpt(p, h, qweight, qzeros, scales, nullptr, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_gptq_size(const char *format, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                                int32_t word_dtype, int32_t scale_dtype, int64_t *weight_bytes, int64_t *scale_bytes,
+                                int64_t *zero_point_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(weight_bytes && scale_bytes && zero_point_bytes, "prepare_gptq_size: null output");
+    const CkptSizes sz = CkptPreparedSizes(PlanGptq(format, K, N, bits, group_size, word_dtype, scale_dtype));
+    *weight_bytes = sz.weight;
+    *scale_bytes = sz.scale;
+    *zero_point_bytes = sz.zp;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_gptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                           const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
+                           int64_t bits, int64_t group_size, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                           onnxl_amd_tensor *zero_point, void *stream) {
+  return Guard([&] {
+    return PrepareGptq(format, qweight, qzeros, scales, g_idx, K, N, bits, group_size, weight, scale, zero_point,
+                       static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_gptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *qzeros,
+                              const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
+                              int64_t bits, int64_t group_size, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    CkptPlan p = GptqFromTensors(format, qweight, qzeros, scales, g_idx, K, N, bits, group_size);
+    CkptHost h = CheckGptqValues(p, qweight, qzeros, scales, g_idx);
+    return DecodeCkpt(p, h, qweight, qzeros, scales, g_idx, y, static_cast<hipStream_t>(stream));
   });
 }
 

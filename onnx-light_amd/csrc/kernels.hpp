@@ -292,4 +292,17 @@ struct NbitsPrepParams {
 };
 void LaunchPrepareNbits(const NbitsPrepParams &p, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// AWQ / GPTQ checkpoint weights (checkpoints.hip; layouts in
+// checkpoint_layout.hpp).
+struct CkptLayout;
+// weight: tiled UINT4 (bits <= 4) or UINT8 [K, N]; zp_out: UINT4 / UINT8
+// [groups, N]; scale_out: [groups, N] FLOAT16 (scale_dtype FLOAT16) or FLOAT
+void LaunchCkptPrepare(const CkptLayout &L, const void *scales, int scale_dtype, void *weight, void *scale_out,
+                       void *zp_out, hipStream_t stream);
+// y [N, K] of out_dtype (FLOAT, FLOAT16, BFLOAT16, DOUBLE); zero_terms: AWQ
+// gemv_fast / llm-awq FLOAT16 [padded, N]; g_idx: GPTQ group map [K] or null
+void LaunchCkptDecode(const CkptLayout &L, const void *scales, int scale_dtype, const uint16_t *zero_terms,
+                      const int32_t *g_idx, int out_dtype, void *y, hipStream_t stream);
+
 }  // namespace onnxl_amd

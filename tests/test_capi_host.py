@@ -351,3 +351,137 @@ def test_dequantize_packed_validation(olamd):
     # a format of the reference with no GPU kernel here (a codebook format)
     rc, _ = run(x=np.zeros(66, np.uint8), fmt=b"gguf:iq2_xxs", shape=(256,), y=np.zeros(256, np.float32))
     assert rc == olamd.UNSUPPORTED
+
+
+def test_awq_validation(olamd):
+    """The AWQ format's checks and messages (onnx_core/runtime/awq.cc:64-118
+    Geometry, :156-183 CheckParameter, :232-245 CheckReconstruction, :263-268
+    tensor checks) on host payloads; valid arguments stop at NOT_INITIALIZED."""
+    import torch
+    from awq_gptq_cases import awq_fixture
+    L = olamd.lib()
+    d = olamd.describe
+
+    def run(variant="gemm", fx=None, K=128, N=8, bits=4, group=64, y=None, **over):
+        fx = dict(awq_fixture(variant if variant in ("gemm", "gemv", "gemv_fast", "llm-awq") else "gemm", 64)
+                  if fx is None else fx)
+        fx.update(over)
+        y = np.zeros((N, K), np.float32) if y is None else y
+        rc = L.onnxl_amd_dequantize_awq(variant.encode(), d(fx["qweight"]), d(fx["qzeros"]), d(fx["scales"]), K, N,
+                                        bits, group, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(K=0), "AWQ requires positive dimensions, supported bits and group_axis=1."),
+                    (dict(bits=8, variant="gemv"), "AWQ requires positive dimensions, supported bits and group_axis=1."),
+                    (dict(variant="marlin"), "AWQ unsupported variant."),
+                    (dict(group=0), "AWQ unsupported group size."),
+                    (dict(group=48), "AWQ requires complete groups."),
+                    (dict(N=12), "AWQ GEMM requires complete INT32 words and FP16/BF16 scales."),
+                    (dict(scales=np.ones((2, 8), np.float32)),
+                     "AWQ GEMM requires complete INT32 words and FP16/BF16 scales."),
+                    (dict(qweight=np.zeros((128, 2), np.int32)), "AWQ invalid tensor type, shape or byte extent: qweight."),
+                    (dict(qzeros=np.zeros((2, 1), np.int64)), "AWQ invalid tensor type, shape or byte extent: qzeros."),
+                    (dict(y=np.zeros((8, 128), np.int32)), "Quantization requires FLOAT, DOUBLE, FLOAT16 or BFLOAT16.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    gemv = awq_fixture("gemv", 64)
+    for kw, msg in ((dict(group=8), "AWQ invalid effective group size."),
+                    (dict(scales=gemv["scales"].astype(np.float32)), "AWQ GEMV requires FLOAT16 parameters."),
+                    (dict(K=132, group=-1), "AWQ GEMV requires K divisible by eight.")):
+        rc, err = run("gemv", gemv, **kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    rc, err = run("gemv_fast", awq_fixture("gemv_fast", 64), K=96, group=32)
+    assert rc == olamd.INVALID_ARGUMENT and "AWQ GEMV_FAST requires K divisible by 64 and N by four." in err
+    rc, err = run("llm-awq", awq_fixture("llm-awq", 64), qzeros=np.zeros((16, 8), np.float32))
+    assert "AWQ invalid tensor type, shape or byte extent: scaled_zeros." in err
+    # value checks: nonfinite anywhere, nonpositive where used (the gemv padding is not used)
+    fx = awq_fixture("gemm", 64)
+    bad = fx["scales"].copy()
+    bad[1, 3] = np.inf
+    assert "AWQ nonfinite parameter." in run(scales=bad)[1]
+    bad = fx["scales"].copy()
+    bad[0, 0] = 0
+    assert "AWQ nonpositive used scale." in run(scales=bad)[1]
+    sc = gemv["scales"].copy()
+    sc[:, 2:] = -3  # padding groups
+    assert run("gemv", gemv, scales=sc)[0] == olamd.NOT_INITIALIZED
+    terms = awq_fixture("gemv_fast", 64)
+    tz = terms["qzeros"].copy()
+    tz[5, 1] = np.nan
+    assert "AWQ nonfinite parameter." in run("gemv_fast", terms, qzeros=tz)[1]
+    # BFLOAT16 scales: the FLOAT reconstruction must stay finite
+    big = torch.full((2, 8), 3.0e38, dtype=torch.bfloat16)
+    assert "AWQ FLOAT reconstruction overflow." in run(scales=big)[1]
+    # FLOAT16 output: values that round past 65504 (15 * 8192 here)
+    sc = fx["scales"].copy()
+    sc[0, 1] = 8192
+    y16 = np.zeros((8, 128), np.float16)
+    assert "Dequantization output dtype overflow." in run(scales=sc, y=y16)[1]
+    assert run(scales=sc)[0] == olamd.NOT_INITIALIZED  # FLOAT output holds it
+    # valid arguments reach the device step; prepare checks its output buffers first
+    assert run()[0] == olamd.NOT_INITIALIZED
+    o = [olamd.Tensor() for _ in range(3)]
+    rc = L.onnxl_amd_prepare_awq(b"gemm", d(fx["qweight"]), d(fx["qzeros"]), d(fx["scales"]), 128, 8, 4, 64,
+                                 *(ctypes.byref(t) for t in o), None)
+    assert rc == olamd.INVALID_ARGUMENT and "prepare_awq: weight holds 0 bytes, needs 1024" in L.onnxl_amd_last_error().decode()
+    w, s, z = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    assert L.onnxl_amd_prepare_awq_size(b"gemv", 4096, 11008, 4, 128, olamd.FLOAT16, ctypes.byref(w),
+                                        ctypes.byref(s), ctypes.byref(z)) == olamd.OK
+    assert (s.value, z.value) == (32 * 11008 * 2, 32 * 11008 // 2) and w.value >= 4096 * 11008 // 2
+    assert L.onnxl_amd_prepare_awq_size(b"gemm", 256, 64, 8, 128, olamd.BFLOAT16, ctypes.byref(w),
+                                        ctypes.byref(s), ctypes.byref(z)) == olamd.OK
+    assert (w.value, s.value, z.value) == (256 * 64, 2 * 64 * 4, 2 * 64)
+
+
+def test_gptq_validation(olamd):
+    """The GPTQ format's checks and messages (onnx_core/runtime/gptq.cc:67-123
+    Geometry, :230-253 CheckData, :158-166 tensor checks)."""
+    from awq_gptq_cases import gptq_fixture
+    L = olamd.lib()
+    d = olamd.describe
+
+    def run(fmt="gptq_v2", bits=4, width=4, K=32, N=32, group=16, fx=None, y=None, **over):
+        fx = dict(gptq_fixture(bits, fmt if fmt in ("gptq", "gptq_v2", "gptq_p") else "gptq_v2", width)
+                  if fx is None else fx)
+        fx.update(over)
+        y = np.zeros((N, K), np.float32) if y is None else y
+        rc = L.onnxl_amd_dequantize_gptq(fmt.encode(), d(fx["qweight"]), d(fx["qzeros"]), d(fx["scales"]),
+                                         d(fx["g_idx"]), K, N, bits, group, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    fx4 = gptq_fixture(4)
+    for kw, msg in ((dict(fmt="gptq_v3"), "GPTQ unsupported format."),
+                    (dict(bits=9, fx=fx4), "GPTQ invalid dimensions, bits or group axis."),
+                    (dict(group=-2), "GPTQ invalid group size."),
+                    (dict(qweight=fx4["qweight"].astype(np.uint8)), "GPTQ unsupported packed word dtype."),
+                    (dict(fmt="gptq_p", width=2, fx=gptq_fixture(4, "gptq_v2", 2)),
+                     "GPTQ planar checkpoint format requires INT32 words."),
+                    (dict(bits=5, fx=fx4), "GPTQ five-, six- and seven-bit codes require the gptq_p format."),
+                    (dict(bits=3, K=48, fx=gptq_fixture(3)),
+                     "GPTQ three-bit and planar layouts require INT32 and 32-code blocks."),
+                    (dict(scales=fx4["scales"].astype(np.float64)), "GPTQ unsupported scales dtype."),
+                    (dict(qzeros=fx4["qzeros"][:1]), "GPTQ invalid tensor type, shape or byte extent: qzeros."),
+                    (dict(g_idx=fx4["g_idx"].astype(np.int64)), "GPTQ invalid tensor type, shape or byte extent: g_idx."),
+                    (dict(g_idx=np.full(32, 2, np.int32)), "GPTQ invalid group map index."),
+                    (dict(scales=np.zeros((2, 32), np.float16)), "GPTQ nonfinite or nonpositive scale.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    # v1 all-ones zero fields are ambiguous (test_gptq.cc:314-330)
+    v1 = gptq_fixture(4, "gptq")
+    rc, err = run("gptq", fx=v1, qzeros=np.full_like(v1["qzeros"], -1))
+    assert "GPTQ v1 all-ones zero field has ambiguous upstream conversion semantics." in err
+    assert run("gptq", fx=v1)[0] == olamd.NOT_INITIALIZED
+    # FLOAT scales: the FLOAT reconstruction must stay finite
+    big = np.full((2, 32), 3.0e37, np.float32)
+    assert "GPTQ FLOAT reconstruction overflow." in run(scales=big)[1]
+    # every format, bit width and word width of the reference's fixtures passes the checks
+    for fmt in ("gptq", "gptq_v2", "gptq_p"):
+        for bits in range(2, 9):
+            if fmt != "gptq_p" and bits in (5, 6, 7):
+                continue
+            for width in ((4,) if fmt == "gptq_p" or bits in (3, 5, 6, 7) else (1, 2, 4, 8)):
+                assert run(fmt, bits, width)[0] == olamd.NOT_INITIALIZED, (fmt, bits, width)
+    w, s, z = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    assert L.onnxl_amd_prepare_gptq_size(b"gptq_p", 4096, 4096, 6, 128, olamd.INT32, olamd.FLOAT,
+                                         ctypes.byref(w), ctypes.byref(s), ctypes.byref(z)) == olamd.OK
+    assert (w.value, s.value, z.value) == (4096 * 4096, 32 * 4096 * 4, 32 * 4096)
