@@ -13,9 +13,12 @@
 //  - one KernelBase subclass per operator of the quantized-matmul path
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
-//    GroupedMatMul, and com.microsoft:MatMulNBits on ORT-packed weights)
-//    and for the two fused nodes the GPU patterns produce
-//    (ai.rt.amd:DequantizeLinearMatMul, ai.rt.amd:DequantizePackedMatMul),
+//    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
+//    ai.rt:Dequantize on AWQ / GPTQ encoded weights), for the two fused
+//    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
+//    ai.rt.amd:DequantizePackedMatMul), and for
+//    ai.rt.amd:DequantizeEncodedMatMul (MatMul on an AWQ / GPTQ encoded
+//    weight, written by an exporter: no pattern produces it yet),
 //    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
 //    the plain key the built-ins use (examples/register_custom_kernel/
 //    main.cc:105-114): a kGPU key would need RuntimeContextOptions.device =
@@ -37,6 +40,7 @@
 #include "onnx_core/runtime/kernels/kernel_dispatch_table.h"
 #include "onnx_core/runtime/kernels/node_helpers.h"
 #include "onnx_core/runtime/memory/simple_tensor.h"
+#include "onnx_core/runtime/quantization.h"
 #include "onnx_core/runtime/runtime_context.h"
 #include "onnx_core/symbolic/sym_tensor.h"
 #include "onnx_proto/onnx.h"
@@ -64,7 +68,7 @@ using ONNX_LIGHT_NAMESPACE::NodeProto;
 namespace mi355x {
 
 // ONNX TensorProto data types used below.
-constexpr int32_t kFloat = 1, kUint8 = 2, kInt8 = 3, kInt32 = 6, kFloat16 = 10, kBfloat16 = 16,
+constexpr int32_t kFloat = 1, kUint8 = 2, kInt8 = 3, kInt32 = 6, kFloat16 = 10, kDouble = 11, kBfloat16 = 16,
                   kUint4 = 21, kInt4 = 22;
 constexpr const char *kFusedDomain = "ai.rt.amd";
 
@@ -685,6 +689,80 @@ private:
   std::shared_ptr<Prepared> weight_;
 };
 
+// AWQ and GPTQ weights carried as encoded values (EncodedValueProto with the
+// struct types "onnx_light.awq_weights.v1" / "onnx_light.gptq_weights.v1").
+// The native tensors come from the reference's own exporters
+// (ExportAwqWeights / ExportGptqWeights, onnx_core/runtime/quantization.h:632,
+// :727), which validate the encoding and its schema; the library then takes
+// them as host descriptors.
+struct Checkpoint {
+  bool awq = false;
+  std::string kind;  // AWQ variant or GPTQ format
+  int64_t K = 0, N = 0, bits = 0, group = 0;
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  onnxl_amd_tensor T(const char *name) const {
+    auto it = tensors.find(name);
+    return it == tensors.end() ? Absent() : Describe(&it->second);
+  }
+};
+
+// False when the encoded value is neither AWQ nor GPTQ.
+template <typename Catalogue>
+bool ExportCheckpoint(const rt::RuntimeValue &value, const Catalogue &catalogue, Checkpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  const std::string type = catalogue.Resolve(enc.struct_type()).name().value();
+  if (type == "onnx_light.awq_weights.v1") {
+    rt::AwqWeights w = rt::ExportAwqWeights(enc, size_t{1} << 30, catalogue);
+    out = Checkpoint{true, w.variant, w.in_features, w.out_features, w.bits, w.group_size, std::move(w.tensors)};
+    return true;
+  }
+  if (type == "onnx_light.gptq_weights.v1") {
+    rt::GptqWeights w = rt::ExportGptqWeights(enc, size_t{1} << 30, catalogue);
+    out = Checkpoint{false, w.format, w.in_features, w.out_features, w.bits, w.group_size, std::move(w.tensors)};
+    return true;
+  }
+  return false;
+}
+
+// ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
+// kernel_dequantize.cc:18-43): AWQ and GPTQ encodings decode on the GPU to
+// [out_features, in_features] of dtype (onnxl_amd_dequantize_awq / _gptq);
+// every other encoding, and values that reference shared parameters, run on
+// the built-in kernel.
+class Mi355xDequantize : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.rt:Dequantize";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 1);
+    rt::RequireOutputCount(node, 1);
+    const int64_t dtype = rt::GetRequiredAttributeInt(node, "dtype");
+    if (dtype != kFloat && dtype != kDouble && dtype != kFloat16 && dtype != kBfloat16)
+      throw std::invalid_argument("Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+    const auto value = ctx.values().find(node.input(0));
+    Checkpoint c;
+    if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ");
+      return;
+    }
+    const rt::Shape shape{c.N, c.K};
+    rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                        ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
+    const onnxl_amd_tensor qz = c.T(c.kind == "llm-awq" ? "scaled_zeros" : "qzeros");
+    const int rc = c.awq ? onnxl_amd_dequantize_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group, &dy,
+                                                    nullptr)
+                         : onnxl_amd_dequantize_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group,
+                                                     &dy, nullptr);
+    if (Call(rc, ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Fused nodes.  They exist only in graphs rewritten by the GPU patterns, so
 // there is no built-in kernel: the adapter computes their chain itself when
@@ -840,6 +918,132 @@ protected:
   std::vector<int> ConstantInputs() const override { return {1}; }
 };
 
+// ai.rt.amd:DequantizeEncodedMatMul(A, Q) = MatMul(A, Transpose(Dequantize(Q,
+// dtype = A's dtype))) for an AWQ or GPTQ encoded weight Q of logical shape
+// [N, K]: the weight is prepared once (onnxl_amd_prepare_awq / _gptq) into
+// the fused DequantizeLinear -> MatMul operands when Q is a session constant,
+// else before each run; then one fused call.  Encodings and layouts the
+// preparation does not take (AWQ gemv_fast / llm-awq, GPTQ act-order group
+// maps and partial groups) decode to a dense [N, K] weight on the GPU and run
+// the MatMul there.
+class Mi355xDequantizeEncodedMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizeEncodedMatMul";
+  using Mi355xKernel::Mi355xKernel;
+
+  bool HasPreparations(const std::unordered_set<std::string> &immutable_inputs) const override {
+    return node_->input_size() >= 2 && immutable_inputs.count(node_->input(1)) != 0;
+  }
+  void DeclarePreparations(const std::unordered_set<std::string> &immutable_inputs,
+                           std::vector<rt::KernelPreparation> &preparations) override {
+    if (!HasPreparations(immutable_inputs)) return;
+    rt::KernelPreparation p;
+    p.info.source_inputs = {node_->input(1)};
+    p.info.representation = "mi355x:encoded-weight-prepared-v1";
+    p.info.output_slots = {node_->input(1) + ":" + p.info.representation};
+    p.estimate_memory = [](const rt::RuntimeContext &) { return rt::KernelPreparationMemory{0, 0, 0}; };
+    p.execute = [this](rt::RuntimeContext &ctx) {
+      auto w = PrepareWeight(ctx);
+      std::lock_guard<std::mutex> lock(mu_);
+      weight_ = std::move(w);
+    };
+    preparations.push_back(std::move(p));
+  }
+
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireInputCount(node, 2);
+    rt::RequireOutputCount(node, 1);
+    const onnxl_amd_tensor a = In(0, ctx);
+    std::shared_ptr<Prepared> w = weight_ ? weight_ : PrepareWeight(ctx);
+    if (!w->fused) {  // the decoded weight [K, N] in HBM, MatMul on the GPU
+      const rt::Shape shape = MatMulShape(a, w->dense_t.desc);
+      rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      Check(onnxl_amd_matmul(&a, &w->dense_t.desc, &dy, nullptr));
+      rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
+    const rt::Shape shape = MatMulShape(a, w->weight.desc);
+    rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const int32_t cast_to = w->scale.desc.data_type == kFloat ? a.data_type : 0;
+    Check(onnxl_amd_dequantize_linear_matmul(&a, &w->weight.desc, &w->scale.desc, &w->zero_point.desc, /*axis=*/0,
+                                             cast_to, &dy, nullptr));
+    rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+private:
+  struct Prepared {
+    bool fused = false;
+    DeviceTensor weight, scale, zero_point;  // fused operands
+    DeviceTensor dense_t;                    // the decoded weight, transposed to [K, N]
+  };
+
+  std::shared_ptr<Prepared> PrepareWeight(rt::RuntimeContext &ctx) const {
+    const auto value = ctx.values().find(node_->input(1));
+    Checkpoint c;
+    if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c))
+      throw std::invalid_argument("mi355x: DequantizeEncodedMatMul takes an AWQ or GPTQ encoded weight.");
+    const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
+    const onnxl_amd_tensor qz = c.T(c.kind == "llm-awq" ? "scaled_zeros" : "qzeros");
+    auto w = std::make_shared<Prepared>();
+    int64_t wb = 0, sb = 0, zb = 0;
+    Check(c.awq ? onnxl_amd_prepare_awq_size(c.kind.c_str(), c.K, c.N, c.bits, c.group, sc.data_type, &wb, &sb, &zb)
+                : onnxl_amd_prepare_gptq_size(c.kind.c_str(), c.K, c.N, c.bits, c.group, qw.data_type, sc.data_type,
+                                              &wb, &sb, &zb));
+    w->weight.Allocate(wb);
+    w->scale.Allocate(sb);
+    w->zero_point.Allocate(zb);
+    const int64_t sizes[3] = {wb, sb, zb};
+    DeviceTensor *outs[3] = {&w->weight, &w->scale, &w->zero_point};
+    for (int i = 0; i < 3; ++i) {
+      outs[i]->desc = onnxl_amd_tensor{};
+      outs[i]->desc.data = outs[i]->ptr;
+      outs[i]->desc.location = ONNXL_AMD_DEVICE;
+      outs[i]->desc.size_bytes = sizes[i];
+    }
+    const int rc = c.awq ? onnxl_amd_prepare_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group,
+                                                 &w->weight.desc, &w->scale.desc, &w->zero_point.desc, nullptr)
+                         : onnxl_amd_prepare_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group,
+                                                  &w->weight.desc, &w->scale.desc, &w->zero_point.desc, nullptr);
+    if (rc != ONNXL_AMD_UNSUPPORTED) {
+      Check(rc);
+      Check(onnxl_amd_synchronize(nullptr));
+      w->fused = true;
+      return w;
+    }
+    // dense decode [N, K] in the activations' dtype (GPU, copied back), its
+    // transpose [K, N] on the host, then one upload; once per weight
+    const onnxl_amd_tensor a = In(0, ctx);
+    const size_t count = static_cast<size_t>(c.N * c.K);
+    std::vector<uint16_t> nk(count), kn(count);
+    onnxl_amd_tensor host{};
+    host.data_type = a.data_type;
+    host.rank = 2;
+    host.dims[0] = c.N;
+    host.dims[1] = c.K;
+    host.data = nk.data();
+    host.size_bytes = static_cast<int64_t>(count * 2);
+    host.location = ONNXL_AMD_HOST;
+    Check(c.awq ? onnxl_amd_dequantize_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group, &host, nullptr)
+                : onnxl_amd_dequantize_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group, &host,
+                                            nullptr));
+    for (int64_t n = 0; n < c.N; ++n)
+      for (int64_t k = 0; k < c.K; ++k) kn[static_cast<size_t>(k * c.N + n)] = nk[static_cast<size_t>(n * c.K + k)];
+    w->dense_t.Allocate(host.size_bytes);
+    CheckHip(hipMemcpy(w->dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    w->dense_t.desc = host;
+    w->dense_t.desc.dims[0] = c.K;
+    w->dense_t.desc.dims[1] = c.N;
+    w->dense_t.desc.data = w->dense_t.ptr;
+    w->dense_t.desc.location = ONNXL_AMD_DEVICE;
+    return w;
+  }
+
+  std::shared_ptr<Prepared> weight_;
+};
+
 // ---------------------------------------------------------------------------
 // Registration.
 
@@ -889,6 +1093,8 @@ const char *RegisterMi355xKernelFunctions(int device_ordinal = 0) {
     Register<Mi355xMatMulNBits>("com.microsoft", "MatMulNBits");
     Register<Mi355xDequantizeLinearMatMul>(kFusedDomain, "DequantizeLinearMatMul");
     Register<Mi355xDequantizePackedMatMul>(kFusedDomain, "DequantizePackedMatMul");
+    Register<Mi355xDequantize>("ai.rt", "Dequantize");
+    Register<Mi355xDequantizeEncodedMatMul>(kFusedDomain, "DequantizeEncodedMatMul");
   });
   return onnxl_amd_version();
 }

@@ -19,7 +19,8 @@ REFERENCE = "/root/reference/onnx_light"
 
 OPERATORS = ["MatMulInteger", "QLinearMatMul", "DequantizeLinear", "MatMul", "QuantizeLinear",
              "DynamicQuantizeLinear", "ConvInteger", "QLinearConv", "Cast", "DequantizePacked",
-             "GroupedMatMul", "MatMulNBits", "DequantizeLinearMatMul", "DequantizePackedMatMul"]
+             "GroupedMatMul", "MatMulNBits", "DequantizeLinearMatMul", "DequantizePackedMatMul", "Dequantize",
+             "DequantizeEncodedMatMul"]
 
 
 def _strip_comments(text):
@@ -89,7 +90,7 @@ def test_operator_has_registered_kernel_class(op):
     assert re.search(rf'static constexpr const char \*name = "onnxl_amd:CPU:[\w.]+:{op}";', text), cls
     assert re.search(rf"void Run\(rt::RuntimeContext &ctx\) override", text)
     domain = ("kFusedDomain" if op.endswith("MatMul") and op.startswith("Dequantize")
-              else '"com.microsoft"' if op == "MatMulNBits" else '""')
+              else '"com.microsoft"' if op == "MatMulNBits" else '"ai.rt"' if op == "Dequantize" else '""')
     assert re.search(rf'Register<{cls}>\({re.escape(domain)}, "{op}"\);', text), cls
 
 
@@ -154,7 +155,8 @@ def test_reference_names_exist():
     headers = ""
     for rel in ["onnx_core/runtime/kernels/node_helpers.h", "onnx_core/runtime/kernels/kernel_dispatch_table.h",
                 "onnx_core/runtime/kernels/kernel_context.h", "onnx_core/runtime/memory/simple_tensor.h",
-                "onnx_core/runtime/runtime_context.h"]:
+                "onnx_core/runtime/runtime_context.h", "onnx_core/runtime/quantization.h",
+                "onnx_core/runtime/runtime_value.h"]:
         headers += open(os.path.join(REFERENCE, rel)).read()
     text = _adapter()
     used = set(re.findall(r"\brt::(\w+)", text))
