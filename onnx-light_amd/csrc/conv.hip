@@ -250,47 +250,104 @@ constexpr int64_t kCvMaxLds = 65536;  // staged input row (C * W) or weight row 
 int64_t PaddedRows(const ConvGeom &g) { return (g.out[1] - 1) * g.s[1] + (g.k[1] - 1) * g.d[1] + 1; }
 int64_t PaddedCols(const ConvGeom &g) { return (g.out[2] - 1) * g.s[2] + (g.k[2] - 1) * g.d[2] + 1; }
 
+// LDS layout of one staged input row on the dword path: channel row c (W / 4
+// dwords) at dword c * ts + ((c >> 6) & 3), with ts odd and at least
+// W / 4 + 3, so that the 64 lanes of a wavefront reading channel rows
+// 4 qd + i (qd = 0..63, i fixed) hit 64 distinct banks.
+__host__ __device__ inline int64_t RowTileStride(int64_t W) { return (W / 4 + 3) | 1; }  // dwords
+int64_t RowTileBytes(int64_t C, int64_t W) { return W % 4 == 0 ? (C * RowTileStride(W) + 4) * 4 : C * W; }
+
 // One launch builds both operands.  Blocks 0 .. N * Hp - 1 write padded row
 // hp of image n: xh[n, hp, wp, c] = x[n, c, hp - pt, wp - pl], or x's zero
-// point outside the input; the C input rows of W bytes are staged in LDS
-// (dword loads when W % 4 == 0 and x is dword aligned), then written as Wp
-// pixels of C bytes, one
-// dword of four channels per thread.  The remaining M blocks write one row of
-// the tap-major weight each, wr[m, tap, c] = w[m, c, tap], from the row
-// staged in LDS.
+// point outside the input; the C input rows of W bytes are staged in LDS,
+// then written as Wp pixels of C bytes.  Dword path (W % 4 == 0, x dword
+// aligned): loads of eight dwords in flight per thread; then each thread
+// reads the 4 x 4 byte block of channels 4 qd .. 4 qd + 3 and pixels
+// 4 q .. 4 q + 3 (four dword reads), transposes it with byte permutes, and
+// writes the four pixels' channel dwords, a wavefront's 64 lanes on 64
+// consecutive channel quads (256 contiguous bytes per store).  Otherwise
+// byte reads, one channel dword per thread.  The remaining M blocks write
+// one row of the tap-major weight each, wr[m, tap, c] = w[m, c, tap], from
+// the row staged in LDS.
 __global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom g, int64_t Hp, int64_t Wp,
-                                                                  const uint8_t *x, uint8_t x_zp, const uint8_t *w,
-                                                                  uint8_t *xh, uint8_t *wr) {
-  extern __shared__ uint8_t tile[];  // C * W (input row) or Kc (weight row) bytes, below 2^16
+                                                                  int dwords, const uint8_t *x, uint8_t x_zp,
+                                                                  const uint8_t *w, uint8_t *xh, uint8_t *wr) {
+  extern __shared__ uint8_t tile[];  // one staged input row or one weight row (Kc bytes), below 2^16
   // 32-bit index arithmetic inside the loops (64-bit division is a long
   // software sequence): every per-block count is below 2^16
   const uint32_t H = (uint32_t)g.in[1], W = (uint32_t)g.in[2], C = (uint32_t)g.C;
   const int64_t b = blockIdx.x;
-  if (b < g.N * Hp) {
+  const uint32_t cq = C / 4, pl = (uint32_t)g.pb[2];
+  const uint32_t zp4 = x_zp * 0x01010101u;
+  if (b < g.N * Hp && dwords) {
     const int64_t n = b / Hp, hp = b - n * Hp, h = hp - g.pb[1];
-    const bool row_in = h >= 0 && h < (int64_t)H;
-    if (row_in) {
-      const uint8_t *src = x + (n * C * H + h) * W;  // channel c at + c * H * W
-      if (W % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 4 == 0) {
-        // consecutive threads on consecutive dwords of the channel rows
-        const uint32_t wd = W / 4;
-        for (uint32_t e = threadIdx.x; e < C * wd; e += kCBlock) {
-          const uint32_t c = e / wd, q = e - c * wd;
-          reinterpret_cast<uint32_t *>(tile)[e] = reinterpret_cast<const uint32_t *>(src + (size_t)c * H * W)[q];
+    uint32_t *dst = reinterpret_cast<uint32_t *>(xh + (n * Hp + hp) * Wp * C);
+    const uint32_t wpad = (uint32_t)Wp;
+    if (h < 0 || h >= (int64_t)H) {
+      for (uint32_t e = threadIdx.x; e < wpad * cq; e += kCBlock) dst[e] = zp4;
+      return;
+    }
+    const uint32_t wd = W / 4, ts = (uint32_t)RowTileStride(W);
+    uint32_t *t32 = reinterpret_cast<uint32_t *>(tile);
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(x + (n * C * H + h) * W);
+    const uint32_t plane = H * W / 4, total = C * wd;
+    for (uint32_t e0 = threadIdx.x; e0 < total; e0 += 8 * kCBlock) {
+      uint32_t v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t e = e0 + k * kCBlock;
+        if (e < total) {
+          const uint32_t c = e / wd;
+          v[k] = src[c * plane + (e - c * wd)];
         }
-      } else {
-        for (uint32_t e = threadIdx.x; e < C * W; e += kCBlock) {
-          const uint32_t c = e / W;
-          tile[e] = src[(size_t)c * H * W + (e - c * W)];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t e = e0 + k * kCBlock;
+        if (e < total) {
+          const uint32_t c = e / wd;
+          t32[c * ts + ((c >> 6) & 3) + (e - c * wd)] = v[k];
         }
       }
     }
     __syncthreads();
+    for (uint32_t t = threadIdx.x; t < wd * cq; t += kCBlock) {
+      const uint32_t q = t / cq, qd = t - q * cq;
+      const uint32_t *r0 = t32 + (4 * qd) * ts + ((qd >> 4) & 3) + q;
+      const uint32_t a0 = r0[0], a1 = r0[ts], a2 = r0[2 * ts], a3 = r0[3 * ts];  // channels 4qd + i
+      const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+      const uint32_t px[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                              __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wp = 4 * q + j + pl;  // input columns past Wp are never read
+        if (wp < wpad) dst[wp * cq + qd] = px[j];
+      }
+    }
+    // the padding columns [0, pl) and [pl + W, Wp): x's zero point
+    const uint32_t left = pl < wpad ? pl : wpad, right0 = pl + W;
+    const uint32_t pads = left + (wpad > right0 ? wpad - right0 : 0u);
+    for (uint32_t e = threadIdx.x; e < pads * cq; e += kCBlock) {
+      const uint32_t k = e / cq, wp = k < left ? k : right0 + (k - left);
+      dst[wp * cq + (e - k * cq)] = zp4;
+    }
+  } else if (b < g.N * Hp) {
+    // one padded row, byte loads: xh[n, hp, wp, c] from the staged C x W bytes
+    const int64_t n = b / Hp, hp = b - n * Hp, h = hp - g.pb[1];
+    const bool row_in = h >= 0 && h < (int64_t)H;
+    if (row_in) {
+      const uint8_t *src = x + (n * C * H + h) * W;  // channel c at + c * H * W
+      for (uint32_t e = threadIdx.x; e < C * W; e += kCBlock) {
+        const uint32_t c = e / W;
+        tile[e] = src[(size_t)c * H * W + (e - c * W)];
+      }
+    }
+    __syncthreads();
     uint32_t *dst = reinterpret_cast<uint32_t *>(xh + (n * Hp + hp) * Wp * C);
-    const uint32_t cq = C / 4, pl = (uint32_t)g.pb[2];
     auto quad = [&](uint32_t wp, uint32_t qd) __attribute__((always_inline)) {
       const uint32_t wi = wp - pl;  // wraps above W when wp < pl
-      uint32_t v = x_zp * 0x01010101u;
+      uint32_t v = zp4;
       if (row_in && wp >= pl && wi < W) {
         const uint8_t *t = tile + (4 * qd) * W + wi;
         v = (uint32_t)t[0] | (uint32_t)t[W] << 8 | (uint32_t)t[2 * W] << 16 | (uint32_t)t[3 * W] << 24;
@@ -334,7 +391,7 @@ bool ConvImplicitEligible(const ConvGeom &g) {
   const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
   if (g.G != 1 || g.in[0] != 1 || g.k[0] != 1 || g.C % kCvChannels != 0 || g.P % 16 != 0 || g.P == 0) return false;
   const int64_t Hp = PaddedRows(g), Wp = PaddedCols(g);
-  return g.C * g.in[2] <= kCvMaxLds && g.Kc <= kCvMaxLds && g.N * Hp + g.M < (int64_t(1) << 31) &&
+  return RowTileBytes(g.C, g.in[2]) <= kCvMaxLds && g.Kc <= kCvMaxLds && g.N * Hp + g.M < (int64_t(1) << 31) &&
          Hp * Wp * g.C < lim && g.M * g.Kc < lim && g.M * g.P * 4 < lim;
 }
 
@@ -359,11 +416,12 @@ ImplicitConv ConvImplicitDesc(const ConvGeom &g) {
 void LaunchConvImplicitOperands(const ConvGeom &g, const uint8_t *x, uint8_t x_zp, const uint8_t *w, uint8_t *xh,
                                 uint8_t *wr, hipStream_t s) {
   const int64_t Hp = PaddedRows(g), Wp = PaddedCols(g);
+  const bool dwords = g.in[2] % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 4 == 0;
   const int64_t blocks = g.N * Hp + g.M;
-  const unsigned lds = (unsigned)std::max<int64_t>(g.C * g.in[2], g.Kc);
+  const unsigned lds = (unsigned)std::max<int64_t>(dwords ? RowTileBytes(g.C, g.in[2]) : g.C * g.in[2], g.Kc);
   if (blocks > 0)
-    hipLaunchKernelGGL(ImplicitOperandsKernel, dim3((unsigned)blocks), dim3(kCBlock), lds, s, g, Hp, Wp, x, x_zp, w,
-                       xh, wr);
+    hipLaunchKernelGGL(ImplicitOperandsKernel, dim3((unsigned)blocks), dim3(kCBlock), lds, s, g, Hp, Wp, (int)dwords,
+                       x, x_zp, w, xh, wr);
 }
 
 bool ConvColIsInput(const ConvGeom &g) {
