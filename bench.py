@@ -273,6 +273,35 @@ def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
     return w
 
 
+def make_awq(olamd, dev, replicas):
+    """AWQ gemm checkpoint (4 bits, group 128) of configuration 3's weight
+    shape, prepared once by onnxl_amd_prepare_awq, then the fused decode GEMV
+    fp16[8,4096] x W[4096,11008] -> fp16[8,11008] per call.  Random qweight /
+    qzeros words are valid codes; scales fp16."""
+    import torch
+    w = Workload()
+    K, N, group = 4096, 11008, 128
+    w.name = ("AWQ gemm 4-bit (group 128) fp16[8,4096] x W[4096,11008] -> fp16[8,11008], weight prepared once "
+              "into the fused DequantizeLinear -> MatMul operands")
+    w.key, w.unit, w.dtype, w.bound = "awq", "GB/s", "fp16 x uint4 (fp32 accumulate)", "hbm"
+    groups = K // group
+    w.nbytes = K * N // 2 + groups * N * 2 + groups * N // 2 + 8 * K * 2 + 8 * N * 2
+    w.work = float(w.nbytes)
+    rng = np.random.default_rng(43)
+    a = _t(np.float16(rng.standard_normal((8, K))), dev)
+    w.calls = []
+    for _ in range(replicas):
+        qweight = _t(rng.integers(-2**31, 2**31, (K, N // 8), dtype=np.int64).astype(np.int32), dev)
+        qzeros = _t(rng.integers(-2**31, 2**31, (groups, N // 8), dtype=np.int64).astype(np.int32), dev)
+        scales = _t(np.float16(rng.uniform(0.002, 0.02, (groups, N))), dev)
+        prep = olamd.prepare_awq("gemm", qweight, qzeros, scales, K, N, group)
+        del qweight, qzeros, scales
+        y = torch.empty((8, N), dtype=torch.float16, device=dev)
+        w.calls.append(olamd.prepare("dequantize_linear_matmul", a, prep.weight, prep.scale, prep.zero_point, 0, 0,
+                                     y))
+    return w
+
+
 def make_q8(olamd, dev, replicas):
     """QuantizeLinear of configuration 2's activation: fp32[2048,4096] -> u8
     with a scalar scale and zero point (the producer of QLinearMatMul's A)."""
@@ -622,7 +651,7 @@ def value_of(w, ms):
 
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
-             "pkgemv8", "pkgemv_q4k", "pkgemv_q6k", "moe")
+             "pkgemv8", "pkgemv_q4k", "pkgemv_q6k", "awq", "moe")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
                  "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
 
@@ -675,6 +704,8 @@ def main():
         if key in ("pkgemv_q4k", "pkgemv_q6k"):
             fmt = "q4_k" if key == "pkgemv_q4k" else "q6_k"
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 256 * PK_BLOCK[fmt][1]), fmt)
+        if key == "awq":
+            return make_awq(olamd, dev, args.replicas or 24)
         if key == "moe":
             return make_moe(olamd, dev)
         if key == "c3_stream_ceiling":

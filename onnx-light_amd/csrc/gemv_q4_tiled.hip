@@ -89,8 +89,11 @@ template <int J> __device__ __forceinline__ uint32_t RowPair(uint32_t w, uint32_
 // (0x6400 + offset + zp as fp16 bits): the integer moves to bits 4-7.
 __device__ __forceinline__ uint32_t OddBias(uint32_t b) { return 0x5400u + ((b - 0x6400u) << 4); }
 
+// MODE: 0 per-tensor, 1 per-column, 2 blocked along K, 3 blocked with blocks
+// of 128 rows or more (one scale row per 128-row group, loaded once).
 template <int T, bool HAS_ZP, bool SIGNED, int MODE>
 __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p) {
+  constexpr bool kBlocked = MODE >= 2;
   constexpr int kPitch = 16 * T + 4;  // floats per activation row of a wave's partial sums
   __shared__ __attribute__((aligned(16))) float red[kWaves][16][kPitch];
   const int lane = threadIdx.x & 63;
@@ -101,13 +104,13 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
   const int gb = wave * p.ngroups / kWaves;
   const int ng = (wave + 1) * p.ngroups / kWaves - gb;
   const int64_t tile_bytes = (int64_t)p.ngroups * kGroupBytes;
-  const int64_t s_rows = MODE == 2 ? p.K >> p.blk_shift : 1;
+  const int64_t s_rows = kBlocked ? p.K >> p.blk_shift : 1;
 
   const __amdgpu_buffer_rsrc_t rsW = Rsrc(p.W, p.ntiles * tile_bytes);
   const __amdgpu_buffer_rsrc_t rsA = Rsrc(p.A, (int64_t)p.M * p.K * 2);
-  const __amdgpu_buffer_rsrc_t rsS = Rsrc(p.scale, MODE == 2 ? s_rows * p.N * 2 : (MODE == 1 ? p.N * 2 : 2));
+  const __amdgpu_buffer_rsrc_t rsS = Rsrc(p.scale, kBlocked ? s_rows * p.N * 2 : (MODE == 1 ? p.N * 2 : 2));
   const __amdgpu_buffer_rsrc_t rsZ =
-      Rsrc(p.zp, HAS_ZP ? (MODE == 2 ? (s_rows * p.N + 1) / 2 : (MODE == 1 ? (p.N + 1) / 2 : 1)) : 0);
+      Rsrc(p.zp, HAS_ZP ? (kBlocked ? (s_rows * p.N + 1) / 2 : (MODE == 1 ? (p.N + 1) / 2 : 1)) : 0);
 
   int col[T];
   unsigned w_lane[T];
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
   for (int t = 0; t < T; ++t) {
     sfix[t] = 0;
     bfix[t] = p.bias2;
-    if constexpr (MODE != 2) {
+    if constexpr (!kBlocked) {
       const unsigned so = MODE == 1 ? (unsigned)min(col[t], p.N - 1) * 2u : 0u;
       const uint32_t s = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsS, so, 0, 0);
       sfix[t] = s | (s << 16);
@@ -183,10 +186,15 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
       const bool in_k = live && rb < p.K;      // wave-uniform
       act[s][c] = __builtin_bit_cast(
           v8h, __builtin_amdgcn_raw_buffer_load_b128(rsA, in_k ? a_lane : kOob, in_k ? 2 * rb : 0, 0));
-      if constexpr (MODE == 2) {
+      if constexpr (kBlocked) {
         const int su = min(rb >> p.blk_shift, su_max);  // wave-uniform
 #pragma unroll
         for (int t = 0; t < T; ++t) {
+          if (MODE == 3 && c > 0) {  // the group's one scale row (c is an unrolled constant)
+            sc[s][t][c] = sc[s][t][0];
+            if constexpr (HAS_ZP) zq[s][t][c] = zq[s][t][0];
+            continue;
+          }
           sc[s][t][c] = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsS, s_lane[t], 2 * p.N * su, 0);
           if constexpr (HAS_ZP)
             zq[s][t][c] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rsZ, z_lane[t], (p.N * su) >> 1, 0);
@@ -202,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
       for (int c = 0; c < 4; ++c) {
         // scale and bias enter the packed fp16 ops as broadcast low halves
         uint32_t s1 = sfix[t], b1 = bfix[t];
-        if constexpr (MODE == 2) {
+        if constexpr (kBlocked) {
           s1 = sc[s][t][c];
           if constexpr (HAS_ZP) {
             const uint32_t z = (zq[s][t][c] >> zsh) & 15u;
@@ -354,13 +362,15 @@ void LaunchGemvQ4Tiled(const DqMatMulParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((g.ntiles + T - 1) / T));
   const bool zp = p.zp != nullptr;
   auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, stream, g); };
-  auto by_mode = [&](auto k0, auto k1, auto k2) {
+  auto by_mode = [&](auto k0, auto k1, auto k2, auto k3) {
     if (p.mode == 0) go(k0);
     else if (p.mode == 1) go(k1);
-    else go(k2);
+    else if (g.blk_shift < 7) go(k2);
+    else go(k3);
   };
-#define OLA_TILED(TT, ZP, SG) \
-  by_mode(GemvQ4TiledKernel<TT, ZP, SG, 0>, GemvQ4TiledKernel<TT, ZP, SG, 1>, GemvQ4TiledKernel<TT, ZP, SG, 2>)
+#define OLA_TILED(TT, ZP, SG)                                                                    \
+  by_mode(GemvQ4TiledKernel<TT, ZP, SG, 0>, GemvQ4TiledKernel<TT, ZP, SG, 1>, GemvQ4TiledKernel<TT, ZP, SG, 2>, \
+          GemvQ4TiledKernel<TT, ZP, SG, 3>)
   auto by_zp = [&](auto tag) {
     constexpr int TT = decltype(tag)::value;
     if (!zp) OLA_TILED(TT, false, false);
