@@ -366,6 +366,56 @@ constexpr int kGvRows = 4 * kGvCols;              // outputs per workgroup
 constexpr int kGvChunkK = 4096;                   // values per row per chunk: 64 block pairs, one per lane
 constexpr int kGvRowBytes = kGvChunkK / 32 * 18;  // 2304
 
+// Stages `rows` rows of `bytes` bytes (row r at src + r * stride) into LDS at
+// r * bytes, with up to eight loads in flight per thread before their LDS
+// stores: 16-byte pieces when every row start is 16-byte aligned, else dwords.
+__device__ __forceinline__ void StageRows(uint32_t *stage, const uint8_t *src, int64_t stride, int rows, int bytes) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  if ((bytes & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (stride & 15) == 0) {
+    const int per_row = bytes / 16, total = rows * per_row;
+    for (int i0 = threadIdx.x; i0 < total; i0 += 8 * 256) {
+      v4i v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 256 * k;
+        if (i < total) {
+          const int r = i / per_row;
+          v[k] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + r * stride) + (i - r * per_row));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 256 * k;
+        if (i < total) {
+          const int r = i / per_row;
+          reinterpret_cast<v4i *>(stage)[(r * bytes) / 16 + (i - r * per_row)] = v[k];
+        }
+      }
+    }
+  } else {
+    const int per_row = bytes / 4, total = rows * per_row;
+    for (int i0 = threadIdx.x; i0 < total; i0 += 8 * 256) {
+      uint32_t v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 256 * k;
+        if (i < total) {
+          const int r = i / per_row;
+          v[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src + r * stride) + (i - r * per_row));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 256 * k;
+        if (i < total) {
+          const int r = i / per_row;
+          stage[(r * bytes) / 4 + (i - r * per_row)] = v[k];
+        }
+      }
+    }
+  }
+}
+
 template <int M>
 __global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
                                                      int64_t N, int64_t K, uint16_t *__restrict__ y) {
@@ -385,22 +435,7 @@ __global__ __launch_bounds__(256) void GemvQ40Kernel(const uint16_t *__restrict_
     const int chunk_bytes = (int)(chunk_k / 32 * 18);  // a multiple of 36
     // stage rows [n0, n0 + rows) of this chunk: row r at stage byte r * chunk_bytes
     const uint8_t *src = w + n0 * row_bytes + kc / 32 * 18;
-    if ((chunk_bytes & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (row_bytes & 15) == 0) {
-      const int per_row = chunk_bytes / 16;
-      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
-        const int r = i / per_row, c = i - r * per_row;
-        typedef int v4i __attribute__((ext_vector_type(4)));
-        const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + r * row_bytes) + c);
-        reinterpret_cast<v4i *>(stage)[(r * chunk_bytes) / 16 + c] = v;
-      }
-    } else {
-      const int per_row = chunk_bytes / 4;
-      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
-        const int r = i / per_row, c = i - r * per_row;
-        stage[(r * chunk_bytes) / 4 + c] =
-            __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src + r * row_bytes) + c);
-      }
-    }
+    StageRows(stage, src, row_bytes, rows, chunk_bytes);
     __syncthreads();
     for (int64_t jj = lane; jj < chunk_k / 64; jj += 64) {
 #pragma unroll
@@ -506,21 +541,7 @@ __global__ __launch_bounds__(256) void GemvQ80Kernel(const uint16_t *__restrict_
     const int64_t chunk_k = std::min<int64_t>(kGv8ChunkK, K - kc);
     const int cb = (int)(chunk_k / 32 * 34);  // a multiple of 68
     const uint8_t *src = w + n0 * row_bytes + kc / 32 * 34;
-    if ((cb & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (row_bytes & 15) == 0) {
-      const int per_row = cb / 16;
-      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
-        const int r = i / per_row, c = i - r * per_row;
-        typedef int v4i __attribute__((ext_vector_type(4)));
-        const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + r * row_bytes) + c);
-        reinterpret_cast<v4i *>(stage)[(r * cb) / 16 + c] = v;
-      }
-    } else {
-      const int per_row = cb / 4;
-      for (int i = threadIdx.x; i < rows * per_row; i += 256) {
-        const int r = i / per_row, c = i - r * per_row;
-        stage[(r * cb) / 4 + c] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(src + r * row_bytes) + c);
-      }
-    }
+    StageRows(stage, src, row_bytes, rows, cb);
     __syncthreads();
     const int64_t jb = lane;  // block of this lane within the chunk
     if (jb < chunk_k / 32) {
