@@ -253,9 +253,60 @@ public:
   }
 };
 
+// ---------------------------------------------------------------------------
+// ai.rt:Dequantize(Q; dtype) over a constant encoded weight Q (logical
+// [N, K]) -> Transpose(perm = [1, 0]) -> MatMul(A, .), A of the same FLOAT16 /
+// BFLOAT16 dtype -> ai.rt.amd:DequantizeEncodedMatMul(A, Q).  The encoding
+// (AWQ, GPTQ or another) is resolved by the session kernel.
+class DequantizeEncodedMatMulGpuPattern : public builder::PatternOptimization {
+public:
+  DequantizeEncodedMatMulGpuPattern()
+      : builder::PatternOptimization(1, "DequantizeEncodedMatMulGpu", sym::Device::kGPU0) {}
+
+  std::set<std::string> FastOpType() const override { return {"MatMul"}; }
+
+  builder::MatchResult Match(builder::GraphGraph &graph, const NodeProto &candidate) const override {
+    if (!IsOnnxOp(candidate, "MatMul") || candidate.input_size() != 2) return NoMatch(candidate, "not a MatMul");
+    const NodeProto *tr = graph.NodeBefore(In(candidate, 1));
+    if (tr == nullptr || !IsOnnxOp(*tr, "Transpose"))
+      return NoMatch(candidate, "MatMul's second input is not a Transpose output");
+    std::vector<int64_t> perm;
+    if (ol::GetAttributeInts(*tr, "perm", perm) && perm != std::vector<int64_t>{1, 0})
+      return NoMatch(candidate, "Transpose is not a 2-D transpose");
+    if (!SingleUse(graph, Out(*tr, 0), candidate)) return NoMatch(candidate, "Transpose output has another consumer");
+    const NodeProto *dq = graph.NodeBefore(In(*tr, 0));
+    if (dq == nullptr || dq->op_type().value() != "Dequantize" || dq->domain().value() != "ai.rt")
+      return NoMatch(candidate, "Transpose input is not an ai.rt Dequantize output");
+    if (!SingleUse(graph, Out(*dq, 0), *tr)) return NoMatch(candidate, "Dequantize output has another consumer");
+    if (!graph.IsConstant(In(*dq, 0))) return NoMatch(candidate, "encoded weight is not an initializer");
+    const int64_t dtype = ol::GetAttributeOr<int64_t>(*dq, "dtype", 0);
+    if (dtype != kFloat16 && dtype != kBfloat16) return NoMatch(candidate, "Dequantize dtype is not FLOAT16 or BFLOAT16");
+    if (!graph.HasType(In(candidate, 0))) return NoMatch(candidate, "type of A unknown");
+    const TensorType a_type = graph.GetType(In(candidate, 0));
+    if ((dtype == kFloat16 && a_type != TensorType::kFloat16) || (dtype == kBfloat16 && a_type != TensorType::kBfloat16))
+      return NoMatch(candidate, "type of A differs from the Dequantize dtype");
+    return builder::MatchResult{this, {dq, tr, &candidate}, &candidate};
+  }
+
+  ol::utils::RepeatedProtoField<NodeProto> Apply(builder::GraphGraph &graph,
+                                                 const std::vector<const NodeProto *> &nodes) const override {
+    const builder::MatchResult verified =
+        nodes.size() != 3 || nodes[2] == nullptr ? builder::MatchResult{} : Match(graph, *nodes[2]);
+    if (verified.pattern == nullptr || verified.nodes != nodes)
+      throw builder::BuilderError("DequantizeEncodedMatMulGpuPattern::Apply received an unsafe or inconsistent match.");
+    const NodeProto &dq = *nodes[0], &matmul = *nodes[2];
+    const std::string name = "DequantizeEncodedMatMulGpu--" + std::string(matmul.name().value());
+    NodeProto fused = ol::MakeNode("DequantizeEncodedMatMul", {In(matmul, 0), In(dq, 0)}, Outputs(matmul),
+                                   kFusedDomain, name.c_str());
+    ol::utils::RepeatedProtoField<NodeProto> out;
+    out.push_back(std::move(fused));
+    return out;
+  }
+};
+
 }  // namespace mi355x_patterns
 
-// Makes both rewrites available by name; neither is enabled by default.
+// Makes the three rewrites available by name; none is enabled by default.
 void RegisterMi355xPatterns() {
   namespace builder = ONNX_LIGHT_NAMESPACE::core::builder;
   builder::RegisterPattern(
@@ -268,6 +319,12 @@ void RegisterMi355xPatterns() {
       "DequantizePackedMatMulGpu",
       []() -> std::unique_ptr<builder::PatternOptimization> {
         return std::make_unique<mi355x_patterns::DequantizePackedMatMulGpuPattern>();
+      },
+      /*enabled_by_default=*/false);
+  builder::RegisterPattern(
+      "DequantizeEncodedMatMulGpu",
+      []() -> std::unique_ptr<builder::PatternOptimization> {
+        return std::make_unique<mi355x_patterns::DequantizeEncodedMatMulGpuPattern>();
       },
       /*enabled_by_default=*/false);
 }

@@ -17,8 +17,8 @@
 //    ai.rt:Dequantize on AWQ / GPTQ encoded weights), for the two fused
 //    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul), and for
-//    ai.rt.amd:DequantizeEncodedMatMul (MatMul on an AWQ / GPTQ encoded
-//    weight, written by an exporter: no pattern produces it yet),
+//    ai.rt.amd:DequantizeEncodedMatMul (MatMul on an encoded weight, which
+//    the DequantizeEncodedMatMulGpu pattern produces),
 //    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
 //    the plain key the built-ins use (examples/register_custom_kernel/
 //    main.cc:105-114): a kGPU key would need RuntimeContextOptions.device =
@@ -919,13 +919,15 @@ protected:
 };
 
 // ai.rt.amd:DequantizeEncodedMatMul(A, Q) = MatMul(A, Transpose(Dequantize(Q,
-// dtype = A's dtype))) for an AWQ or GPTQ encoded weight Q of logical shape
-// [N, K]: the weight is prepared once (onnxl_amd_prepare_awq / _gptq) into
-// the fused DequantizeLinear -> MatMul operands when Q is a session constant,
-// else before each run; then one fused call.  Encodings and layouts the
-// preparation does not take (AWQ gemv_fast / llm-awq, GPTQ act-order group
-// maps and partial groups) decode to a dense [N, K] weight on the GPU and run
-// the MatMul there.
+// dtype = A's dtype))) for an encoded weight Q of logical shape [N, K] (the
+// node the DequantizeEncodedMatMulGpu pattern writes): an AWQ or GPTQ weight
+// is prepared once (onnxl_amd_prepare_awq / _gptq) into the fused
+// DequantizeLinear -> MatMul operands when Q is a session constant, else
+// before each run; then one fused call.  What the preparation does not take
+// (AWQ gemv_fast / llm-awq, GPTQ act-order group maps and partial groups)
+// decodes to a dense weight on the GPU, and any other encoding through the
+// reference's DequantizeTensor; the dense weight is transposed once and the
+// MatMul runs on the GPU.
 class Mi355xDequantizeEncodedMatMul : public Mi355xKernel {
 public:
   static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizeEncodedMatMul";
@@ -982,9 +984,10 @@ private:
 
   std::shared_ptr<Prepared> PrepareWeight(rt::RuntimeContext &ctx) const {
     const auto value = ctx.values().find(node_->input(1));
+    if (value == ctx.values().end() || value->second.kind != rt::RuntimeValue::Kind::kEncoded)
+      throw std::invalid_argument("Dequantize requires an EncodedValueProto input.");
     Checkpoint c;
-    if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c))
-      throw std::invalid_argument("mi355x: DequantizeEncodedMatMul takes an AWQ or GPTQ encoded weight.");
+    if (!ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) return DenseOther(ctx, value->second);
     const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
     const onnxl_amd_tensor qz = c.T(c.kind == "llm-awq" ? "scaled_zeros" : "qzeros");
     auto w = std::make_shared<Prepared>();
@@ -1037,6 +1040,38 @@ private:
     w->dense_t.desc.dims[0] = c.K;
     w->dense_t.desc.dims[1] = c.N;
     w->dense_t.desc.data = w->dense_t.ptr;
+    w->dense_t.desc.location = ONNXL_AMD_DEVICE;
+    return w;
+  }
+
+  // Any other encoding: the reference's decode in A's dtype (materializing a
+  // shared-parameter reference first, as kernel_dequantize.cc:28-36 does),
+  // transposed to [K, N] and uploaded once.
+  std::shared_ptr<Prepared> DenseOther(rt::RuntimeContext &ctx, const rt::RuntimeValue &value) const {
+    const onnxl_amd_tensor a = In(0, ctx);
+    const auto &catalogue = ctx.struct_type_catalogue();
+    const rt::Tensor nk = value.Encoded().has_parameter_ref()
+                              ? rt::DequantizeTensor(rt::MaterializeQuantizedValue(value, catalogue), {}, nullptr,
+                                                     a.data_type)
+                              : rt::DequantizeTensor(value.Encoded(), catalogue, nullptr, a.data_type);
+    if (nk.shape.size() != 2 || nk.data_type != a.data_type)
+      throw std::invalid_argument("mi355x: DequantizeEncodedMatMul takes a 2-D encoded weight.");
+    const int64_t N = nk.shape[0], K = nk.shape[1];
+    const size_t count = static_cast<size_t>(N * K);
+    std::vector<uint16_t> kn(count);
+    const auto *src = reinterpret_cast<const uint16_t *>(nk.bytes());
+    for (int64_t n = 0; n < N; ++n)
+      for (int64_t k = 0; k < K; ++k) kn[static_cast<size_t>(k * N + n)] = src[static_cast<size_t>(n * K + k)];
+    auto w = std::make_shared<Prepared>();
+    w->dense_t.Allocate(static_cast<int64_t>(count * 2));
+    if (count > 0) CheckHip(hipMemcpy(w->dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    w->dense_t.desc = onnxl_amd_tensor{};
+    w->dense_t.desc.data_type = a.data_type;
+    w->dense_t.desc.rank = 2;
+    w->dense_t.desc.dims[0] = K;
+    w->dense_t.desc.dims[1] = N;
+    w->dense_t.desc.data = w->dense_t.ptr;
+    w->dense_t.desc.size_bytes = static_cast<int64_t>(count * 2);
     w->dense_t.desc.location = ONNXL_AMD_DEVICE;
     return w;
   }

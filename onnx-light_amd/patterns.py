@@ -45,6 +45,7 @@ from typing import Callable, Dict, List, Optional, Sequence
 FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
 PACKED_FUSED_OP = "DequantizePackedMatMul"
+ENCODED_FUSED_OP = "DequantizeEncodedMatMul"
 _PACKED_FORMATS = {"gguf:q4_0": 64, "gguf:q8_0": 64, "gguf:q4_k": 256, "gguf:q6_k": 256}  # format: K multiple
 _ONNX_DOMAINS = ("", "ai.onnx")
 _CAST_TARGETS = (10, 16)  # FLOAT16, BFLOAT16: the types the fused kernel rounds to
@@ -272,6 +273,52 @@ class DequantizePackedMatMulPattern(PatternOptimization):
                      matmul.name or dp.name)]
 
 
+class DequantizeEncodedMatMulPattern(PatternOptimization):
+    """ai.rt:Dequantize(Q; dtype) over a constant encoded weight Q (logical
+    [N, K]) -> Transpose(perm = [1, 0]) -> MatMul's second input, with A of
+    the same FLOAT16 / BFLOAT16 dtype -> one fused node
+    ``ai.rt.amd:DequantizeEncodedMatMul(A, Q)``.  The session kernel prepares
+    an AWQ or GPTQ weight once for the fused DequantizeLinear -> MatMul
+    kernels and computes the chain for any other encoding (the encoding is
+    resolved from the model's struct types at run time, not here)."""
+    device = "gpu"
+
+    def fast_op_type(self) -> set:
+        return {"MatMul"}
+
+    def match(self, graph: Graph, candidate: Node) -> MatchResult:
+        if not _is_onnx(candidate, "MatMul") or len(candidate.inputs) != 2:
+            return self.no_match("not a MatMul")
+        tr = graph.producer(candidate.inputs[1])
+        if tr is None or not _is_onnx(tr, "Transpose"):
+            return self.no_match("MatMul's second input is not a Transpose output")
+        if [int(p) for p in tr.attrs.get("perm", [1, 0])] != [1, 0]:
+            return self.no_match("Transpose is not a 2-D transpose")
+        if not DequantizeLinearMatMulPattern._single_use(graph, tr.outputs[0], candidate):
+            return self.no_match("Transpose output has another consumer")
+        dq = graph.producer(tr.inputs[0])
+        if dq is None or dq.op_type != "Dequantize" or dq.domain != "ai.rt":
+            return self.no_match("Transpose input is not an ai.rt Dequantize output")
+        if not DequantizeLinearMatMulPattern._single_use(graph, dq.outputs[0], tr):
+            return self.no_match("Dequantize output has another consumer")
+        if dq.inputs[0] not in graph.initializers:
+            return self.no_match("encoded weight is not an initializer")
+        dtype = int(dq.attrs.get("dtype", 0))
+        if dtype not in (FLOAT16, BFLOAT16):
+            return self.no_match("Dequantize dtype is not FLOAT16 or BFLOAT16")
+        a_info = graph.value_info.get(candidate.inputs[0])
+        if a_info is None:
+            return self.no_match("type of A unknown")
+        if a_info[0] != dtype:
+            return self.no_match("type of A differs from the Dequantize dtype")
+        return MatchResult([dq, tr, candidate])
+
+    def apply(self, graph: Graph, nodes: Sequence[Node]) -> List[Node]:
+        dq, _, matmul = nodes
+        return [Node(ENCODED_FUSED_OP, [matmul.inputs[0], dq.inputs[0]], list(matmul.outputs), FUSED_DOMAIN, {},
+                     matmul.name or dq.name)]
+
+
 # ---- registry --------------------------------------------------------------
 
 _REGISTRY: Dict[str, tuple] = {}
@@ -308,6 +355,7 @@ def create_registered_patterns(device: Optional[str] = None) -> List[PatternOpti
 
 register_pattern("DequantizeLinearMatMulGpu", DequantizeLinearMatMulPattern, enabled_by_default=False)
 register_pattern("DequantizePackedMatMulGpu", DequantizePackedMatMulPattern, enabled_by_default=False)
+register_pattern("DequantizeEncodedMatMulGpu", DequantizeEncodedMatMulPattern, enabled_by_default=False)
 
 
 def optimize(graph: Graph, patterns: Sequence[PatternOptimization]) -> int:

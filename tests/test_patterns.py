@@ -210,3 +210,43 @@ def test_packed_shared_intermediate_is_left_alone(pt):
 def test_packed_registry(pt):
     assert "DequantizePackedMatMulGpu" in pt.registered_pattern_names()
     assert "DequantizePackedMatMulGpu" not in pt.registered_pattern_names(include_opt_in=False)
+
+
+# ---- ai.rt:Dequantize (encoded weight) -> Transpose -> MatMul ----------------
+
+def _encoded_graph(pt, dtype=10, a_type=10, perm=(1, 0), q_const=True, extra_use=False, domain="ai.rt"):
+    N = pt.Node
+    nodes = [N("Dequantize", ["Q"], ["Wd"], domain=domain, attrs={"dtype": dtype}, name="dq"),
+             N("Transpose", ["Wd"], ["Wt"], attrs={"perm": list(perm)}, name="tr"),
+             N("MatMul", ["A", "Wt"], ["Y"], name="mm")]
+    if extra_use:
+        nodes.append(N("Relu", ["Wd"], ["R"], name="relu"))
+    outs = ["Y"] + (["R"] if extra_use else [])
+    info = {} if a_type is None else {"A": (a_type, (8, 4096))}
+    return pt.Graph(nodes, {"Q"} if q_const else set(), ["A"] + ([] if q_const else ["Q"]), outs, info)
+
+
+@pytest.mark.parametrize("dtype", [10, 16])
+def test_encoded_rewrite(pt, dtype):
+    g = _encoded_graph(pt, dtype, dtype)
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizeEncodedMatMulGpu")]) == 1
+    assert len(g.nodes) == 1
+    n = g.nodes[0]
+    assert (n.domain, n.op_type, n.inputs, n.outputs) == (pt.FUSED_DOMAIN, pt.ENCODED_FUSED_OP, ["A", "Q"], ["Y"])
+
+
+@pytest.mark.parametrize("kw,reason", [
+    (dict(dtype=1, a_type=1), "Dequantize dtype is not FLOAT16 or BFLOAT16"),
+    (dict(a_type=16), "type of A differs from the Dequantize dtype"),
+    (dict(a_type=None), "type of A unknown"),
+    (dict(perm=(0, 1)), "Transpose is not a 2-D transpose"),
+    (dict(q_const=False), "encoded weight is not an initializer"),
+    (dict(extra_use=True), "Dequantize output has another consumer"),
+    (dict(domain=""), "Transpose input is not an ai.rt Dequantize output"),
+])
+def test_encoded_no_match(pt, kw, reason):
+    g = _encoded_graph(pt, **kw)
+    mm = next(n for n in g.nodes if n.op_type == "MatMul")
+    m = pt.create_registered_pattern("DequantizeEncodedMatMulGpu").match(g, mm)
+    assert not m and m.reason == reason
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizeEncodedMatMulGpu")]) == 0
