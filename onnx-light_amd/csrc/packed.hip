@@ -662,9 +662,12 @@ __device__ __forceinline__ void DecodeK(const KRaw<12> &r, int i0, h2_t wp[4]) {
   float f[8];
   NibbleFloats(r.q[0], 4 * (g & 1), f);
   NibbleFloats(r.q[1], 4 * (g & 1), f + 4);
+  // ds * q is exact in fp32 (ds = d * scale has at most 17 significant
+  // bits, q at most 4), so one fused multiply-add rounds (ds * q) - dm
+  // exactly as the reference's rounded product and rounded difference do
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float v0 = ds * f[2 * e] - dm, v1 = ds * f[2 * e + 1] - dm;
+    const float v0 = __builtin_fmaf(ds, f[2 * e], -dm), v1 = __builtin_fmaf(ds, f[2 * e + 1], -dm);
     wp[e] = h2_t{(_Float16)v0, (_Float16)v1};
   }
 }
