@@ -17,15 +17,16 @@ oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
-                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q4k|pkgemv_q6k|moe]
+                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q4k|pkgemv_q6k|awq|moe]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
 GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q4_k / q6_k GEMVs
-(`pkgemv`, `pkgemv8`, `pkgemv_q4k`, `pkgemv_q6k`) and a Mixtral-shaped MoE
-GroupedMatMul (`moe`) are timed too and
+(`pkgemv`, `pkgemv8`, `pkgemv_q4k`, `pkgemv_q6k`), an AWQ gemm 4-bit
+checkpoint prepared for the fused decode GEMV (`awq`) and a Mixtral-shaped
+MoE GroupedMatMul (`moe`) are timed too and
 reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
 25,604,096 bytes with the same replica rotation (libonnxl_amd_bench.so): the
 rate a kernel that only reads those bytes reaches, beside which the GEMV's
