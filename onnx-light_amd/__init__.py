@@ -406,11 +406,11 @@ def _device_of(*ts):
 
 
 def _describe_zp(zp, x_dtype, x_scale):
-    """Zero point descriptor: 4-bit zero points are packed storage whose
-    logical shape is the scale's shape."""
+    """Zero point descriptor: sub-byte zero points (4-, 2- and 6-bit types)
+    are packed storage whose logical shape is the scale's shape."""
     if zp is None:
         return describe(None)
-    if x_dtype in (INT4, UINT4):
+    if x_dtype in (INT4, UINT4, 23, 25, 26, 27, 28):
         return describe(zp, x_dtype, tuple(x_scale.shape))
     return describe(zp, x_dtype)
 

@@ -476,8 +476,9 @@ bool IsSupportedScaleDType(int32_t dt) { return dt == kFloat || dt == kFloat16; 
 
 bool DqGpuDtype(int32_t dt) {
   switch (dt) {
-  case kUint8: case kInt8: case kUint16: case kInt16: case kInt32: case kFloat8E4M3FN:
-  case kInt4: case kUint4:
+  case kUint8: case kInt8: case kUint16: case kInt16: case kInt32: case kFloat8E4M3FN: case kFloat8E4M3FNUZ:
+  case kFloat8E5M2: case kFloat8E5M2FNUZ: case kInt4: case kUint4: case kFloat4E2M1: case kUint2: case kInt2:
+  case kFloat6E2M3: case kFloat6E3M2:
     return true;
   default:
     return false;
@@ -485,13 +486,6 @@ bool DqGpuDtype(int32_t dt) {
 }
 
 void CheckDqDtype(int32_t dt) {
-  // Types the reference accepts but this GPU path does not decode.
-  switch (dt) {
-  case 18: case 19: case 20: case 23: case 24: case 25: case 26: case 27:
-    throw Unsupported(Cat("DequantizeLinear: input dtype ", dt, " has no GPU kernel"));
-  default:
-    break;
-  }
   if (!DqGpuDtype(dt)) throw InvalidArgument(Cat("unsupported data type ", dt, ", ", kDqSupportedMsg));
 }
 

@@ -19,7 +19,9 @@ namespace onnxl_amd {
 // ONNX TensorProto.DataType codes used on this path.
 enum DType : int32_t {
   kFloat = 1, kUint8 = 2, kInt8 = 3, kUint16 = 4, kInt16 = 5, kInt32 = 6, kInt64 = 7,
-  kFloat16 = 10, kDouble = 11, kBfloat16 = 16, kFloat8E4M3FN = 17, kUint4 = 21, kInt4 = 22
+  kFloat16 = 10, kDouble = 11, kBfloat16 = 16, kFloat8E4M3FN = 17, kFloat8E4M3FNUZ = 18, kFloat8E5M2 = 19,
+  kFloat8E5M2FNUZ = 20, kUint4 = 21, kInt4 = 22, kFloat4E2M1 = 23, kFloat8E8M0 = 24, kUint2 = 25, kInt2 = 26,
+  kFloat6E2M3 = 27, kFloat6E3M2 = 28
 };
 
 // Validation failure, mapped to ONNXL_AMD_INVALID_ARGUMENT (the reference
@@ -75,7 +77,9 @@ inline int64_t NumElements(const onnxl_amd_tensor &t) { return NumElements(Shape
 // Bytes per element; 4-bit types return 0 (use PackedBytes).
 inline int64_t ElementSize(int32_t dt) {
   switch (dt) {
-  case kUint8: case kInt8: case kFloat8E4M3FN: return 1;
+  case kUint8: case kInt8: case kFloat8E4M3FN: case kFloat8E4M3FNUZ: case kFloat8E5M2: case kFloat8E5M2FNUZ:
+  case kFloat8E8M0:
+    return 1;
   case kUint16: case kInt16: case kFloat16: case kBfloat16: return 2;
   case kFloat: case kInt32: return 4;
   case kInt64: case kDouble: return 8;
@@ -83,9 +87,20 @@ inline int64_t ElementSize(int32_t dt) {
   }
 }
 inline bool IsFourBit(int32_t dt) { return dt == kInt4 || dt == kUint4; }
-// Payload bytes of n elements (4-bit types: ceil(n/2), core/runtime/memory/simple_tensor.h:949).
+// Bits per element of the packed sub-byte types (0 for byte-sized ones).
+inline int SubByteBits(int32_t dt) {
+  switch (dt) {
+  case kInt4: case kUint4: case kFloat4E2M1: return 4;
+  case kInt2: case kUint2: return 2;
+  case kFloat6E2M3: case kFloat6E3M2: return 6;
+  default: return 0;
+  }
+}
+// Payload bytes of n elements (sub-byte types: ceil(n * bits / 8),
+// core/runtime/memory/simple_tensor.h:949).
 inline int64_t PackedBytes(int32_t dt, int64_t n) {
-  return IsFourBit(dt) ? (n + 1) / 2 : n * ElementSize(dt);
+  const int bits = SubByteBits(dt);
+  return bits ? (n * bits + 7) / 8 : n * ElementSize(dt);
 }
 
 inline const char *DTypeName(int32_t dt) {

@@ -72,4 +72,53 @@ __device__ __forceinline__ int Int4ToInt(uint32_t nibble) {
   return (int)((nibble & 0xfu) ^ 8u) - 8;
 }
 
+// The NaN an fp32 step produces in the reference's x86-64 build, whose SSE
+// arithmetic returns the first operand (quieted) when both are NaN, else the
+// NaN one, and the negative default NaN 0xffc00000 for inf * 0 and inf - inf;
+// the GPU's own choice of operand and default NaN is replaced by that.
+__device__ __forceinline__ float SseNaN(float r, float a, float b) {
+  if (r == r) return r;
+  const uint32_t bits = a != a   ? __builtin_bit_cast(uint32_t, a) | 0x00400000u
+                        : b != b ? __builtin_bit_cast(uint32_t, b) | 0x00400000u
+                                 : 0xffc00000u;
+  return __builtin_bit_cast(float, bits);
+}
+__device__ __forceinline__ float SseMul(float a, float b) { return SseNaN(a * b, a, b); }
+__device__ __forceinline__ float SseSub(float a, float b) { return SseNaN(a - b, a, b); }
+
+// FLOAT8E4M3FNUZ / FLOAT8E5M2FNUZ bits -> float, exact (cast_float8.cc:
+// 174-215, 347-380): exponent bias 8 / 16, 0x80 the only NaN (0xffc00000).
+template <int MB, int BIAS> __device__ __forceinline__ float Fp8FnuzToF32(uint8_t c) {
+  if (c == 0x80u) return __builtin_bit_cast(float, 0xffc00000u);
+  constexpr int EB = 7 - MB;
+  const uint32_t e = (c >> MB) & ((1u << EB) - 1u), m = c & ((1u << MB) - 1u);
+  const float mag = e == 0 ? (float)m * __builtin_bit_cast(float, (uint32_t)(128 - BIAS - MB) << 23)
+                           : __builtin_bit_cast(float, ((e + 127u - BIAS) << 23) | (m << (23 - MB)));
+  return (c & 0x80u) ? -mag : mag;
+}
+
+// FLOAT8E5M2 bits -> float, exact (cast_float8.cc:263-300): the fp16 layout's
+// top byte; 0x7d-0x7f decode to 0x7fc00000 and 0xfd-0xff to 0xffc00000.
+__device__ __forceinline__ float Fp8E5M2ToF32(uint8_t c) {
+  if ((c & 0x7fu) > 0x7cu) return __builtin_bit_cast(float, (c & 0x80u) ? 0xffc00000u : 0x7fc00000u);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((uint32_t)c << 8));
+}
+
+// FLOAT4E2M1 nibble -> float (cast_helper.cc:161-166): +-{0, .5, 1, 1.5, 2, 3, 4, 6}.
+__device__ __forceinline__ float Fp4E2M1ToF32(uint32_t nib) {
+  const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
+  const float mag = e == 0 ? 0.5f * (float)m : __builtin_bit_cast(float, ((e + 126u) << 23) | (m << 22));
+  return (nib & 8u) ? -mag : mag;
+}
+
+// FLOAT6E2M3 (MB = 3) / FLOAT6E3M2 (MB = 2) bits -> float (cast_helper.cc:
+// 208-219): bias 2^(E-1) - 1, subnormals at exponent 0, sign bit 5.
+template <int MB> __device__ __forceinline__ float Fp6ToF32(uint32_t bits) {
+  constexpr int EB = 5 - MB, BIAS = (1 << (EB - 1)) - 1;
+  const uint32_t e = (bits >> MB) & ((1u << EB) - 1u), m = bits & ((1u << MB) - 1u);
+  const float mag = e == 0 ? (float)m * __builtin_bit_cast(float, (uint32_t)(128 - BIAS - MB) << 23)
+                           : __builtin_bit_cast(float, ((e + 127u - BIAS) << 23) | (m << (23 - MB)));
+  return (bits & 0x20u) ? -mag : mag;
+}
+
 }  // namespace onnxl_amd

@@ -143,19 +143,8 @@ __global__ __launch_bounds__(kPkThreads) void DequantPackedKernel(const uint8_t 
 //   (i / 32) % 4; int8 scale per 16 values at byte 192 + i / 16; fp16 d at
 //   byte 208; value = (d * scale) * (q - 32).
 //
-// The NaN a step produces follows the reference's x86-64 build, whose SSE
-// arithmetic returns the first operand (quieted) when both are NaN, else the
-// NaN one, and the negative default NaN 0xffc00000 for inf * 0 and inf - inf;
-// the GPU's own choice of operand and default NaN is replaced by that.
-__device__ __forceinline__ float SseNaN(float r, float a, float b) {
-  if (r == r) return r;
-  const uint32_t bits = a != a   ? __builtin_bit_cast(uint32_t, a) | 0x00400000u
-                        : b != b ? __builtin_bit_cast(uint32_t, b) | 0x00400000u
-                                 : 0xffc00000u;
-  return __builtin_bit_cast(float, bits);
-}
-__device__ __forceinline__ float SseMul(float a, float b) { return SseNaN(a * b, a, b); }
-__device__ __forceinline__ float SseSub(float a, float b) { return SseNaN(a - b, a, b); }
+// The NaN a step produces follows the reference's x86-64 build (SseMul,
+// SseSub of device_codecs.hpp).
 
 __device__ __forceinline__ void DecodeQ4K8(const uint8_t *p, int i0, float v[8]) {
   const float d = Half2(p), dmin = Half2(p + 2);

@@ -373,25 +373,120 @@ static int64_t numel(const int64_t *s, int r) {
   return n;
 }
 
-/* Decoded (float) quantized element i of x. */
-static float dq_decode(const void *x, int dtype, int64_t i) {
+static float f32_bits(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* FLOAT8E4M3FNUZ (cast_float8.cc:174-215): bias 8, no infinities, 0x80 the
+ * only NaN (decoded as 0xffc00000), no negative zero. */
+float orc_f8e4m3fnuz_to_f32(uint8_t v) {
+  if (v == 0x80) return f32_bits(0xffc00000u);
+  const uint32_t sign = (uint32_t)(v & 0x80u) << 24, e = (v >> 3) & 15u, m = v & 7u;
+  if (e == 0) {
+    if (m == 0) return f32_bits(sign);
+    uint32_t ee = 127u - 8u, mm = m;  /* normalise the subnormal: 1.f x 2^(ee - 127) */
+    while (!(mm & 4u)) { mm = (mm & 3u) << 1; --ee; }
+    return f32_bits(sign | ee << 23 | (mm & 3u) << 21);
+  }
+  return f32_bits(sign | (e + 127u - 8u) << 23 | m << 20);
+}
+
+/* FLOAT8E5M2 (cast_float8.cc:263-300): the fp16 layout's top byte, with
+ * 0x7c / 0xfc infinities, 0x7d-0x7f decoded as 0x7fc00000 and 0xfd-0xff as
+ * 0xffc00000. */
+float orc_f8e5m2_to_f32(uint8_t v) {
+  if (v >= 253) return f32_bits(0xffc00000u);
+  if (v >= 125 && v <= 127) return f32_bits(0x7fc00000u);
+  if (v == 252) return f32_bits(0xff800000u);
+  if (v == 124) return f32_bits(0x7f800000u);
+  const uint32_t sign = (uint32_t)(v & 0x80u) << 24, e = (v >> 2) & 31u, m = v & 3u;
+  if (e == 0) {
+    if (m == 0) return f32_bits(sign);
+    uint32_t ee = 127u - 15u, mm = m;
+    while (!(mm & 2u)) { mm = (mm & 1u) << 1; --ee; }
+    return f32_bits(sign | ee << 23 | (mm & 1u) << 22);
+  }
+  return f32_bits(sign | (e + 127u - 15u) << 23 | m << 21);
+}
+
+/* FLOAT8E5M2FNUZ (cast_float8.cc:347-380): bias 16, 0x80 the only NaN. */
+float orc_f8e5m2fnuz_to_f32(uint8_t v) {
+  if (v == 0x80) return f32_bits(0xffc00000u);
+  const uint32_t sign = (uint32_t)(v & 0x80u) << 24, e = (v >> 2) & 31u, m = v & 3u;
+  if (e == 0) {
+    if (m == 0) return f32_bits(sign);
+    uint32_t ee = 127u - 16u, mm = m;
+    while (!(mm & 2u)) { mm = (mm & 1u) << 1; --ee; }
+    return f32_bits(sign | ee << 23 | (mm & 1u) << 22);
+  }
+  return f32_bits(sign | (e + 127u - 16u) << 23 | m << 21);
+}
+
+/* FLOAT4E2M1 (cast_helper.cc:161-166): +-{0, 0.5, 1, 1.5, 2, 3, 4, 6}. */
+float orc_f4e2m1_to_f32(uint8_t nibble) {
+  static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const float v = mag[nibble & 7u];
+  return (nibble & 8u) ? -v : v;
+}
+
+/* FLOAT6E2M3 / FLOAT6E3M2 (cast_helper.cc:208-219): sign bit 5, bias
+ * 2^(E-1) - 1, subnormals at exponent 0, no infinities or NaN. */
+float orc_f6_to_f32(uint8_t bits, int dtype) {
+  const int mb = dtype == ORC_FLOAT6E2M3 ? 3 : 2, eb = 5 - mb, bias = (1 << (eb - 1)) - 1;
+  const int e = (bits >> mb) & ((1 << eb) - 1), m = bits & ((1 << mb) - 1);
+  const float v = e == 0 ? ldexpf((float)m, 1 - bias - mb) : ldexpf(1.0f + (float)m / (float)(1 << mb), e - bias);
+  return (bits & 0x20u) ? -v : v;
+}
+
+/* two-bit elements, four per byte from the low bits (cast_sub_byte.h:71-75) */
+uint8_t orc_read_2bit(const uint8_t *data, int64_t i) { return (uint8_t)((data[i / 4] >> (2 * (i % 4))) & 3u); }
+
+/* six-bit elements as a little-endian bit stream (cast_helper.cc:247-256) */
+uint8_t orc_read_6bit(const uint8_t *data, int64_t i) {
+  const int64_t bit = i * 6, byte = bit / 8;
+  const int sh = (int)(bit % 8);
+  uint32_t v = (uint32_t)data[byte] >> sh;
+  if (sh > 2) v |= (uint32_t)data[byte + 1] << (8 - sh);
+  return (uint8_t)(v & 63u);
+}
+
+/* Decoded (float) quantized element i of x (kernel_dequantizelinear.cc:
+ * 85-155). */
+float orc_dq_decode(const void *x, int dtype, int64_t i) {
+  const uint8_t *b = (const uint8_t *)x;
   switch (dtype) {
-  case ORC_UINT8: return (float)((const uint8_t *)x)[i];
+  case ORC_UINT8: return (float)b[i];
   case ORC_INT8: return (float)((const int8_t *)x)[i];
   case ORC_UINT16: return (float)((const uint16_t *)x)[i];
   case ORC_INT16: return (float)((const int16_t *)x)[i];
   case ORC_INT32: return (float)((const int32_t *)x)[i];
-  case ORC_FLOAT8E4M3FN: return orc_f8e4m3fn_to_f32(((const uint8_t *)x)[i]);
-  case ORC_INT4: return (float)orc_int4_to_i8(orc_read_4bit((const uint8_t *)x, i));
-  case ORC_UINT4: return (float)orc_read_4bit((const uint8_t *)x, i);
+  case ORC_FLOAT8E4M3FN: return orc_f8e4m3fn_to_f32(b[i]);
+  case ORC_FLOAT8E4M3FNUZ: return orc_f8e4m3fnuz_to_f32(b[i]);
+  case ORC_FLOAT8E5M2: return orc_f8e5m2_to_f32(b[i]);
+  case ORC_FLOAT8E5M2FNUZ: return orc_f8e5m2fnuz_to_f32(b[i]);
+  case ORC_INT4: return (float)orc_int4_to_i8(orc_read_4bit(b, i));
+  case ORC_UINT4: return (float)orc_read_4bit(b, i);
+  case ORC_FLOAT4E2M1: return orc_f4e2m1_to_f32(orc_read_4bit(b, i));
+  case ORC_UINT2: return (float)orc_read_2bit(b, i);
+  case ORC_INT2: return (float)(((int)orc_read_2bit(b, i) ^ 2) - 2);
+  case ORC_FLOAT6E2M3: case ORC_FLOAT6E3M2: return orc_f6_to_f32(orc_read_6bit(b, i), dtype);
   default: return 0.0f;
   }
+}
+#define dq_decode orc_dq_decode
+
+void orc_dq_decode_n(const void *x, int dtype, int64_t n, float *out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_dq_decode(x, dtype, i);
 }
 
 static int dq_supported(int dtype) {
   switch (dtype) {
   case ORC_UINT8: case ORC_INT8: case ORC_UINT16: case ORC_INT16: case ORC_INT32:
-  case ORC_FLOAT8E4M3FN: case ORC_INT4: case ORC_UINT4:
+  case ORC_FLOAT8E4M3FN: case ORC_FLOAT8E4M3FNUZ: case ORC_FLOAT8E5M2: case ORC_FLOAT8E5M2FNUZ:
+  case ORC_INT4: case ORC_UINT4: case ORC_FLOAT4E2M1: case ORC_UINT2: case ORC_INT2:
+  case ORC_FLOAT6E2M3: case ORC_FLOAT6E3M2:
     return 1;
   default:
     return 0;

@@ -44,7 +44,8 @@ extern "C" {
 enum {
   ORC_FLOAT = 1, ORC_UINT8 = 2, ORC_INT8 = 3, ORC_UINT16 = 4, ORC_INT16 = 5,
   ORC_INT32 = 6, ORC_FLOAT16 = 10, ORC_BFLOAT16 = 16, ORC_FLOAT8E4M3FN = 17,
-  ORC_UINT4 = 21, ORC_INT4 = 22
+  ORC_FLOAT8E4M3FNUZ = 18, ORC_FLOAT8E5M2 = 19, ORC_FLOAT8E5M2FNUZ = 20, ORC_UINT4 = 21, ORC_INT4 = 22,
+  ORC_FLOAT4E2M1 = 23, ORC_UINT2 = 25, ORC_INT2 = 26, ORC_FLOAT6E2M3 = 27, ORC_FLOAT6E3M2 = 28
 };
 
 /* ---- scalar codecs ---- */
@@ -55,6 +56,19 @@ float orc_bf16_to_f32(uint16_t b);      /* rk/cast_helper.cc:136-141 */
 uint8_t orc_f32_to_f8e4m3fn(float v);   /* rk/cast_float8.cc:27-81  */
 float orc_f8e4m3fn_to_f32(uint8_t v);   /* rk/cast_float8.cc:83-118 */
 uint8_t orc_read_4bit(const uint8_t *data, int64_t i); /* rk/cast_sub_byte.h:57-60 */
+/* The further DequantizeLinear input codecs (rk/cast_float8.cc:174-380,
+ * rk/cast_helper.cc:161-256, rk/cast_sub_byte.h:71-75): element i of a packed
+ * buffer decoded to float. */
+float orc_f8e4m3fnuz_to_f32(uint8_t v);
+float orc_f8e5m2_to_f32(uint8_t v);
+float orc_f8e5m2fnuz_to_f32(uint8_t v);
+float orc_f4e2m1_to_f32(uint8_t nibble);
+float orc_f6_to_f32(uint8_t bits, int dtype);
+uint8_t orc_read_2bit(const uint8_t *data, int64_t i);
+uint8_t orc_read_6bit(const uint8_t *data, int64_t i);
+/* the decoded value of element i of x in dtype (every DequantizeLinear input) */
+float orc_dq_decode(const void *x, int dtype, int64_t i);
+void orc_dq_decode_n(const void *x, int dtype, int64_t n, float *out);
 int8_t orc_int4_to_i8(uint8_t nibble);  /* rk/cast_sub_byte.cc:81-88 */
 
 /* Bulk codec helpers (same semantics as the scalar ones). */

@@ -17,6 +17,8 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 FLOAT, UINT8, INT8, UINT16, INT16, INT32 = 1, 2, 3, 4, 5, 6
 FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 10, 16, 17, 21, 22
+FLOAT8E4M3FNUZ, FLOAT8E5M2, FLOAT8E5M2FNUZ, FLOAT4E2M1, UINT2, INT2, FLOAT6E2M3, FLOAT6E3M2 = (
+    18, 19, 20, 23, 25, 26, 27, 28)
 
 _NP_OF = {UINT8: np.uint8, INT8: np.int8, UINT16: np.uint16, INT16: np.int16, INT32: np.int32,
           FLOAT: np.float32, FLOAT16: np.uint16, BFLOAT16: np.uint16, FLOAT8E4M3FN: np.uint8,
@@ -109,6 +111,8 @@ def _declare(L):
     L.orc_ort_nbits_decode.restype = ctypes.c_int
     L.orc_ort_nbits_decode.argtypes = [P, P, ctypes.c_int, P, P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                        ctypes.c_int64, P]
+    L.orc_dq_decode_n.restype = None
+    L.orc_dq_decode_n.argtypes = [P, ctypes.c_int, ctypes.c_int64, P]
     L.orc_awq_decode.restype = ctypes.c_int
     L.orc_awq_decode.argtypes = [ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int64, ctypes.c_int64,
                                  ctypes.c_int64, ctypes.c_int64, P, P, P]
@@ -551,3 +555,28 @@ def gptq_decode(fmt: str, bits: int, qweight: np.ndarray, qzeros: np.ndarray, sc
     lib().orc_gptq_decode(GPTQ_FORMATS[fmt], bits, qw.dtype.itemsize, _ptr(qw), _ptr(qz), _ptr(sc), _ptr(gi), K, N,
                           group, _ptr(codes), _ptr(zeros), _ptr(out))
     return codes, zeros, out
+
+
+# ---- sub-byte and further float8 DequantizeLinear inputs ---------------------
+
+def dq_decode(raw: np.ndarray, dtype: int, n: int) -> np.ndarray:
+    """The n decoded float32 elements of a DequantizeLinear input buffer of
+    `dtype` (packed storage for the sub-byte types)."""
+    raw = np.ascontiguousarray(raw)
+    out = np.empty(n, np.float32)
+    lib().orc_dq_decode_n(_ptr(raw), dtype, n, _ptr(out))
+    return out
+
+
+def pack_bits(codes, bits: int) -> np.ndarray:
+    """Codes of `bits` bits (2, 4 or 6) as the packed little-endian bit stream
+    of ONNX sub-byte tensors: element i at bits i * bits onwards."""
+    codes = np.asarray(codes, np.uint64).reshape(-1)
+    n = codes.size
+    out = np.zeros((n * bits + 7) // 8 + 1, np.uint8)
+    for i, c in enumerate(codes.tolist()):
+        bit = i * bits
+        v = (int(c) & ((1 << bits) - 1)) << (bit % 8)
+        out[bit // 8] |= v & 0xFF
+        out[bit // 8 + 1] |= (v >> 8) & 0xFF
+    return out[:(n * bits + 7) // 8].copy()

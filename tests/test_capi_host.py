@@ -169,9 +169,14 @@ def test_dequantize_validation(olamd):
     assert rc == olamd.INVALID_ARGUMENT and "preallocated output shape must match x shape." in err
     rc, _ = run()
     assert rc == olamd.NOT_INITIALIZED
-    # a dtype the reference decodes but this GPU path does not (FLOAT8E5M2)
-    rc = L.onnxl_amd_dequantize_linear(d(x, 19), d(np.array(1.0, np.float32)), d(None), 1, d(y), None)
-    assert rc == olamd.UNSUPPORTED
+    # every input dtype the reference decodes reaches the device step; FLOAT8E8M0 is not one of them
+    for dt in (18, 19, 20, 23, 25, 26, 27, 28):
+        rc = L.onnxl_amd_dequantize_linear(d(np.zeros(8, np.uint8), dt, (2, 3)), d(np.array(1.0, np.float32)),
+                                           d(None), 1, d(y), None)
+        assert rc == olamd.NOT_INITIALIZED, dt
+    rc = L.onnxl_amd_dequantize_linear(d(x, 24), d(np.array(1.0, np.float32)), d(None), 1, d(y), None)
+    err = L.onnxl_amd_last_error().decode()
+    assert rc == olamd.INVALID_ARGUMENT and "unsupported data type 24, kernel::DequantizeLinear: only" in err
 
 
 def test_matmul_shape_rules(olamd, golden):

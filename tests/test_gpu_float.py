@@ -115,7 +115,27 @@ DQ_CASES = [
     ("int4", (33,), "tensor", 0, None),
     ("fp8", (128, 24), "axis", 1, None),
     ("fp8", (2, 64, 8), "blocked", 1, 16),
+    # every code of the further types (NaN and infinity codes included)
+    ("e4m3fnuz", (64, 24), "axis", 1, None),
+    ("e5m2", (2, 64, 8), "blocked", 1, 16),
+    ("e5m2fnuz", (37, 20), "tensor", 1, None),
+    ("fp4", (64, 48), "blocked", 0, 32),
+    ("uint2", (5, 7, 12), "axis", 2, None),
+    ("int2", (33, 4), "tensor", 0, None),
+    ("fp6e2m3", (32, 16), "axis", 0, None),
+    ("fp6e3m2", (8, 64), "blocked", 1, 32),
 ]
+# the further DequantizeLinear input types: oracle dtype name, bits per code
+SUB_KINDS = {"e4m3fnuz": ("FLOAT8E4M3FNUZ", 8), "e5m2": ("FLOAT8E5M2", 8), "e5m2fnuz": ("FLOAT8E5M2FNUZ", 8),
+             "fp4": ("FLOAT4E2M1", 4), "uint2": ("UINT2", 2), "int2": ("INT2", 2), "fp6e2m3": ("FLOAT6E2M3", 6),
+             "fp6e3m2": ("FLOAT6E3M2", 6)}
+
+
+def _codes(oracle, rng, kind, count, shape):
+    name, bits = SUB_KINDS[kind]
+    q = rng.integers(0, 1 << bits, count)
+    raw = q.astype(np.uint8).reshape(shape) if bits == 8 else oracle.pack_bits(q, bits)
+    return raw, getattr(oracle, name)
 
 
 @pytest.mark.parametrize("case", DQ_CASES, ids=[f"{c[0]}-{c[2]}-ax{c[3]}" for c in DQ_CASES])
@@ -125,7 +145,9 @@ def test_dequantize_vs_oracle(olamd, oracle, dev, case, s16, with_zp):
     kind, shape, skind, axis, block = case
     rng = np.random.default_rng(zlib.crc32(repr((case, s16, with_zp)).encode()))
     n = int(np.prod(shape))
-    if kind in ("int4", "uint4"):
+    if kind in SUB_KINDS:
+        x, code = _codes(oracle, rng, kind, n, shape)
+    elif kind in ("int4", "uint4"):
         lo, hi = (-8, 8) if kind == "int4" else (0, 16)
         q = rng.integers(lo, hi, n)
         x, code = oracle.pack_int4(q), oracle.INT4 if kind == "int4" else oracle.UINT4
@@ -150,7 +172,9 @@ def test_dequantize_vs_oracle(olamd, oracle, dev, case, s16, with_zp):
     zp = None
     if with_zp:
         m = int(np.prod(s_shape)) if s_shape else 1
-        if kind in ("int4", "uint4"):
+        if kind in SUB_KINDS:
+            zp = _codes(oracle, rng, kind, m, s_shape)[0]
+        elif kind in ("int4", "uint4"):
             lo, hi = (-8, 8) if kind == "int4" else (0, 16)
             zp = oracle.pack_int4(rng.integers(lo, hi, m))
         elif kind == "fp8":  # finite fp8 zero points, signed and fractional

@@ -142,3 +142,67 @@ def test_rng_samplers(oracle):
     assert abs(n.mean()) < 0.01 and abs(n.std() - 1.0) < 0.01 and np.abs(n).max() <= 6.0
     with pytest.raises(ValueError):
         oracle.rand_int(3, 3, 0, 1)
+
+
+# ---- the further DequantizeLinear inputs (cast_float8.cc, cast_helper.cc,
+# cast_sub_byte.h), pinned by numpy's fp16 (E5M2 is its top byte), the
+# formats' published maxima and subnormal steps, and hand-packed bytes ------
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def test_float8e5m2_is_the_fp16_top_byte(oracle):
+    codes = np.arange(256, dtype=np.uint8)
+    got = oracle.dq_decode(codes, oracle.FLOAT8E5M2, 256)
+    half = (codes.astype(np.uint16) << 8).view(np.float16).astype(np.float32)
+    special = {124: 0x7F800000, 252: 0xFF800000, 125: 0x7FC00000, 126: 0x7FC00000, 127: 0x7FC00000,
+               253: 0xFFC00000, 254: 0xFFC00000, 255: 0xFFC00000}
+    for c in range(256):
+        if c in special:
+            assert _bits(got[c]) == special[c], c
+        else:
+            assert _bits(got[c]) == _bits(half[c]), c
+    assert got[0x7B] == 57344.0 and got[1] == 2.0 ** -16
+
+
+@pytest.mark.parametrize("dtype,bias,mbits,maxv,tiny", [("FLOAT8E4M3FNUZ", 8, 3, 240.0, 2.0 ** -10),
+                                                         ("FLOAT8E5M2FNUZ", 16, 2, 57344.0, 2.0 ** -17)])
+def test_float8_fnuz(oracle, dtype, bias, mbits, maxv, tiny):
+    codes = np.arange(256, dtype=np.uint8)
+    got = oracle.dq_decode(codes, getattr(oracle, dtype), 256)
+    eb = 7 - mbits
+    for c in range(256):
+        if c == 0x80:
+            assert _bits(got[c]) == 0xFFC00000  # the only NaN
+            continue
+        e, m = (c >> mbits) & ((1 << eb) - 1), c & ((1 << mbits) - 1)
+        mag = m * 2.0 ** (1 - bias - mbits) if e == 0 else (1 + m / 2 ** mbits) * 2.0 ** (e - bias)
+        assert got[c] == (-mag if c & 0x80 else mag), c
+    assert np.nanmax(got) == maxv and got[1] == tiny and _bits(got[0]) == 0
+
+
+def test_float4e2m1_and_float6(oracle):
+    # FLOAT4E2M1: the OCP MX element values; two per byte, low nibble first
+    packed = oracle.pack_int4(np.arange(16))
+    assert oracle.dq_decode(packed, oracle.FLOAT4E2M1, 16).tolist() == [
+        0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    # FLOAT6E2M3 / FLOAT6E3M2: the OCP MX maxima 7.5 / 28 and subnormal steps 1/8 / 1/16
+    raw = oracle.pack_bits(np.arange(64), 6)
+    for dtype, maxv, step, mb in (("FLOAT6E2M3", 7.5, 0.125, 3), ("FLOAT6E3M2", 28.0, 0.0625, 2)):
+        v = oracle.dq_decode(raw, getattr(oracle, dtype), 64)
+        assert v[31] == maxv and v[63] == -maxv and v[1] == step and v[32] == 0.0 and np.signbit(v[32])
+        pos = v[:32]
+        assert np.all(np.diff(pos) > 0)                         # monotone magnitudes
+        assert np.array_equal(pos[:(1 << mb)], step * np.arange(1 << mb))  # evenly spaced subnormals
+        assert np.array_equal(v[32:], -pos)
+
+
+def test_two_and_six_bit_packing(oracle):
+    # four 2-bit elements per byte from the low bits; INT2 is two's complement
+    assert oracle.dq_decode(np.array([0b11100100], np.uint8), oracle.UINT2, 4).tolist() == [0, 1, 2, 3]
+    assert oracle.dq_decode(np.array([0b11100100], np.uint8), oracle.INT2, 4).tolist() == [0, 1, -2, -1]
+    # six-bit elements as one little-endian bit stream: codes 1, 2, 3, 4 -> 0x103081
+    raw = np.array([0x81, 0x30, 0x10], np.uint8)
+    assert np.array_equal(oracle.pack_bits([1, 2, 3, 4], 6), raw)
+    assert oracle.dq_decode(raw, oracle.FLOAT6E3M2, 4).tolist() == [0.0625, 0.125, 0.1875, 0.25]
