@@ -118,15 +118,19 @@ int onnxl_amd_dequantize_linear(const onnxl_amd_tensor *x, const onnxl_amd_tenso
                                 onnxl_amd_tensor *y, void *stream);
 
 /* QuantizeLinear: y = saturate(nearbyint(x / y_scale) + y_zero_point), the
- * division in IEEE fp32; FLOAT8E4M3FN outputs take the saturating fp8 cast of
- * x / y_scale + y_zero_point.  x and y_scale: FLOAT or FLOAT16.  The output
- * dtype follows the reference's node dispatch (kq/kernel_quantizelinear.cc:
- * 917-941): y_zero_point's dtype when it is given (per-tensor, per-axis or
- * blocked; UINT8, INT8, UINT16, INT16, UINT4, INT4, FLOAT8E4M3FN), else
- * output_dtype when non-zero (UINT8, INT8, UINT16, INT16), else UINT8 with a
- * scalar y_scale.  y must already carry that dtype.  Output types the
- * reference quantizes but this library does not (the other fp8 formats, 2-bit,
- * FLOAT4E2M1, FLOAT6) return ONNXL_AMD_UNSUPPORTED.  axis may be negative.
+ * division in IEEE fp32, for the integer outputs; the float outputs take the
+ * reference's saturating cast of x / y_scale + y_zero_point (fp8: round to
+ * nearest even; FLOAT4E2M1 and FLOAT6: nearest code, ties to even; without a
+ * zero point nothing is added, so -0 stays -0).  x and y_scale: FLOAT or
+ * FLOAT16.  The output dtype follows the reference's node dispatch
+ * (kq/kernel_quantizelinear.cc:917-941): y_zero_point's dtype when it is
+ * given (per-tensor, per-axis or blocked; UINT8, INT8, UINT16, INT16, UINT4,
+ * INT4, UINT2, INT2, FLOAT8E4M3FN, FLOAT8E4M3FNUZ, FLOAT8E5M2,
+ * FLOAT8E5M2FNUZ, FLOAT4E2M1, FLOAT6E2M3, FLOAT6E3M2), else output_dtype when
+ * non-zero (UINT8, INT8, UINT16, INT16; FLOAT4E2M1 and FLOAT6 with a scalar
+ * y_scale), else UINT8 with a scalar y_scale.  y must already carry that
+ * dtype; sub-byte outputs are packed little-endian bit streams (element i at
+ * bits i * bits onwards).  axis may be negative.
  * Replaces kernel::QuantizeLinear::operator(), kq/kernel_quantizelinear.cc:
  * 485-532 (per tensor), :543-648 (per tensor with zero point), :664-822 (per
  * axis and blocked with zero point), :833-916 (output_dtype). */

@@ -556,10 +556,11 @@ def quantize_linear(x, y_scale, y_zero_point=None, axis: int = 1, output_dtype: 
                     y_dtype=None, out=None):
     """kernel::QuantizeLinear with the node dispatch of QuantizeLinear::Run
     (kq/kernel_quantizelinear.cc:917-941): the output dtype is y_zero_point's
-    (``y_dtype`` names it for packed 4-bit zero points), else output_dtype,
-    else UINT8.  4-bit outputs are returned as packed uint8 storage
-    (element 2k in the low nibble of byte k), FLOAT8E4M3FN as
-    torch.float8_e4m3fn."""
+    (``y_dtype`` names it for packed sub-byte and uint8-held fp8 zero
+    points), else output_dtype, else UINT8.  Sub-byte outputs (UINT4, INT4,
+    FLOAT4E2M1, UINT2, INT2, FLOAT6E2M3, FLOAT6E3M2) are returned as packed
+    uint8 storage (element i at bits i * bits onwards), FLOAT8E4M3FN as
+    torch.float8_e4m3fn, the other fp8 types as their uint8 bits."""
     torch = _torch()
     shape = _shape_of(x)
     if y_dtype is None:
@@ -567,8 +568,9 @@ def quantize_linear(x, y_scale, y_zero_point=None, axis: int = 1, output_dtype: 
                    else output_dtype if output_dtype else UINT8)
     n = int(np.prod(shape, dtype=np.int64))
     if out is None:
-        if y_dtype in (INT4, UINT4):
-            out = _empty(((n + 1) // 2,), torch.uint8, _device_of(x))
+        bits = {INT4: 4, UINT4: 4, 23: 4, 25: 2, 26: 2, 27: 6, 28: 6}.get(y_dtype)
+        if bits:
+            out = _empty(((n * bits + 7) // 8,), torch.uint8, _device_of(x))
         else:
             tdt = {UINT8: torch.uint8, INT8: torch.int8, UINT16: torch.uint16, INT16: torch.int16,
                    FLOAT8E4M3FN: torch.float8_e4m3fn}.get(y_dtype, torch.uint8)

@@ -583,9 +583,12 @@ int DequantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
 // a zero point fixes the output dtype; otherwise output_dtype does; otherwise
 // the output is UINT8 and the scale must be a scalar.
 
+// Output types with a zero point: every type of :543-648 and :700-822 (all
+// of DequantizeLinear's inputs but INT32 and FLOAT8E8M0).
 bool QlGpuOutput(int32_t dt) {
   return dt == kUint8 || dt == kInt8 || dt == kUint16 || dt == kInt16 || dt == kInt4 || dt == kUint4 ||
-         dt == kFloat8E4M3FN;
+         dt == kFloat8E4M3FN || dt == kFloat8E4M3FNUZ || dt == kFloat8E5M2 || dt == kFloat8E5M2FNUZ ||
+         dt == kFloat4E2M1 || dt == kUint2 || dt == kInt2 || dt == kFloat6E2M3 || dt == kFloat6E3M2;
 }
 
 int QuantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zp,
@@ -653,15 +656,10 @@ int QuantizeLinear(const onnxl_amd_tensor *x, const onnxl_amd_tensor *y_scale, c
   }
   // Output types: the no-zero-point overloads take 8- and 16-bit integers
   // (:485-532 adds FLOAT4E2M1 and FLOAT6 per tensor; :891-915 per axis and
-  // blocked); with a zero point every type of :543-648 and :700-822.  Types
-  // the reference quantizes but this path has no kernel for are reported as
-  // unsupported, so an adapter can hand them back to the reference.
-  const bool eight_sixteen = yt == kUint8 || yt == kInt8 || yt == kUint16 || yt == kInt16;
-  const bool ref_only = has_zp ? (yt == 18 || yt == 19 || yt == 20 || yt == 23 || yt == 25 || yt == 26 ||
-                                  yt == 27 || yt == 28)
-                               : (scalar && (yt == 23 || yt == 27 || yt == 28));
-  if (ref_only) throw Unsupported(Cat("QuantizeLinear: output dtype ", yt, " has no GPU kernel"));
-  if (has_zp ? !QlGpuOutput(yt) : !eight_sixteen)
+  // blocked); with a zero point every type of :543-648 and :700-822.
+  const bool no_zp_ok = yt == kUint8 || yt == kInt8 || yt == kUint16 || yt == kInt16 ||
+                        (scalar && (yt == kFloat4E2M1 || yt == kFloat6E2M3 || yt == kFloat6E3M2));
+  if (has_zp ? !QlGpuOutput(yt) : !no_zp_ok)
     throw InvalidArgument(Cat("unsupported data type ", yt, ", kernel::QuantizeLinear: unsupported output dtype."));
   OLA_ENFORCE(y->size_bytes == PackedBytes(yt, n),
               "kernel::QuantizeLinear preallocated output buffer has unexpected size in bytes.");

@@ -13,39 +13,6 @@ namespace {
 constexpr int kPerThread = 8;
 constexpr int kBlock = 256;
 
-// Element i of a DequantizeLinear input (kernel_dequantizelinear.cc:85-155):
-// 4-bit types two per byte (low nibble first), 2-bit four per byte from the
-// low bits, 6-bit a little-endian bit stream.
-template <int XT>
-__device__ __forceinline__ float Decode(const void *base, int64_t i) {
-  const uint8_t *b = static_cast<const uint8_t *>(base);
-  if constexpr (XT == kUint8) return (float)b[i];
-  else if constexpr (XT == kInt8) return (float)static_cast<const int8_t *>(base)[i];
-  else if constexpr (XT == kUint16) return (float)static_cast<const uint16_t *>(base)[i];
-  else if constexpr (XT == kInt16) return (float)static_cast<const int16_t *>(base)[i];
-  else if constexpr (XT == kInt32) return (float)static_cast<const int32_t *>(base)[i];
-  else if constexpr (XT == kFloat8E4M3FN) return Fp8E4M3ToF32(b[i]);
-  else if constexpr (XT == kFloat8E4M3FNUZ) return Fp8FnuzToF32<3, 8>(b[i]);
-  else if constexpr (XT == kFloat8E5M2) return Fp8E5M2ToF32(b[i]);
-  else if constexpr (XT == kFloat8E5M2FNUZ) return Fp8FnuzToF32<2, 16>(b[i]);
-  else if constexpr (XT == kUint2 || XT == kInt2) {
-    const uint32_t c = (b[i >> 2] >> (2 * (i & 3))) & 3u;
-    return XT == kInt2 ? (float)((int)(c ^ 2u) - 2) : (float)c;
-  } else if constexpr (XT == kFloat6E2M3 || XT == kFloat6E3M2) {
-    const int64_t bit = 6 * i, byte = bit >> 3;
-    const int sh = (int)(bit & 7);
-    uint32_t v = (uint32_t)b[byte] >> sh;
-    if (sh > 2) v |= (uint32_t)b[byte + 1] << (8 - sh);
-    return Fp6ToF32<XT == kFloat6E2M3 ? 3 : 2>(v & 63u);
-  } else {
-    const uint8_t byte = b[i >> 1];
-    const uint32_t nib = (i & 1) ? (byte >> 4) : (byte & 0xfu);
-    if constexpr (XT == kInt4) return (float)Int4ToInt(nib);
-    else if constexpr (XT == kFloat4E2M1) return Fp4E2M1ToF32(nib);
-    else return (float)nib;  // kUint4
-  }
-}
-
 template <int XT, int MODE, bool F16S>
 __global__ __launch_bounds__(kBlock) void DequantKernel(const DequantParams p) {
   const int64_t first = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * kPerThread;
@@ -63,8 +30,8 @@ __global__ __launch_bounds__(kBlock) void DequantKernel(const DequantParams p) {
     }
     const float s = F16S ? F16ToF32(static_cast<const uint16_t *>(p.scale)[si])
                          : static_cast<const float *>(p.scale)[si];
-    const float z = p.zp ? Decode<XT>(p.zp, si) : 0.0f;
-    const float v = SseMul(SseSub(Decode<XT>(p.x, i), z), s);  // NaNs as the reference's x86-64 build
+    const float z = p.zp ? DecodeElement<XT>(p.zp, si) : 0.0f;
+    const float v = SseMul(SseSub(DecodeElement<XT>(p.x, i), z), s);  // NaNs as the reference's x86-64 build
     if (F16S) {
       static_cast<uint16_t *>(p.y)[i] = F32ToF16(v);
     } else {

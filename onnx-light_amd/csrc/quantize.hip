@@ -53,29 +53,38 @@ template <> struct Bounds<kUint16> { static constexpr float lo = 0.f, hi = 65535
 template <> struct Bounds<kInt16> { static constexpr float lo = -32768.f, hi = 32767.f; };
 template <> struct Bounds<kUint4> { static constexpr float lo = 0.f, hi = 15.f; };
 template <> struct Bounds<kInt4> { static constexpr float lo = -8.f, hi = 7.f; };
+template <> struct Bounds<kUint2> { static constexpr float lo = 0.f, hi = 3.f; };
+template <> struct Bounds<kInt2> { static constexpr float lo = -2.f, hi = 1.f; };
+
+// Float outputs: the four fp8 types, FLOAT4E2M1 and the two FLOAT6 types.
+template <int YT>
+constexpr bool kFloatCode = YT == kFloat8E4M3FN || YT == kFloat8E4M3FNUZ || YT == kFloat8E5M2 ||
+                            YT == kFloat8E5M2FNUZ || YT == kFloat4E2M1 || YT == kFloat6E2M3 || YT == kFloat6E3M2;
+
+// Bits per stored element.
+template <int YT>
+constexpr int kYBitsOf = YT == kUint4 || YT == kInt4 || YT == kFloat4E2M1 ? 4
+                         : YT == kUint2 || YT == kInt2                    ? 2
+                         : YT == kFloat6E2M3 || YT == kFloat6E3M2         ? 6
+                         : YT == kUint16 || YT == kInt16                  ? 16
+                                                                          : 8;
 
 // Zero point of scale index si (y's storage type) as a float.
 template <int YT> __device__ __forceinline__ float ZeroPoint(const void *zp, int64_t si) {
-  if constexpr (YT == kUint8) return (float)static_cast<const uint8_t *>(zp)[si];
-  if constexpr (YT == kInt8) return (float)static_cast<const int8_t *>(zp)[si];
-  if constexpr (YT == kUint16) return (float)static_cast<const uint16_t *>(zp)[si];
-  if constexpr (YT == kInt16) return (float)static_cast<const int16_t *>(zp)[si];
-  if constexpr (YT == kFloat8E4M3FN) return Fp8E4M3ToF32(static_cast<const uint8_t *>(zp)[si]);
-  const uint8_t byte = static_cast<const uint8_t *>(zp)[si >> 1];
-  const uint32_t nib = (si & 1) ? (byte >> 4) : (byte & 0xfu);
-  if constexpr (YT == kInt4) return (float)Int4ToInt(nib);
-  return (float)nib;  // kUint4
+  return DecodeElement<YT>(zp, si);
 }
 
 // The stored code of one element: the saturated integer (two's complement,
-// narrowed by the store) or the fp8 bits.  NaN lands as 0, which is what the
-// x86-64 float-to-int conversion of the reference build leaves after its two
-// comparisons let NaN through (:75-80).
+// narrowed by the store) or the float code.  NaN lands as 0 for the integer
+// types, which is what the x86-64 float-to-int conversion of the reference
+// build leaves after its two comparisons let NaN through (:75-80, :216-222).
+// Float codes take x / scale + zero point (:228-268); without a zero point
+// the caller passes z = -0, which adds nothing (-0 stays -0, :508-511).
 template <int YT> __device__ __forceinline__ uint32_t QuantOne(float x, float s, float z) {
   const float q = x / s;  // IEEE division, as the reference divides
-  if constexpr (YT == kFloat8E4M3FN) {
+  if constexpr (kFloatCode<YT>) {
     const float v = q + z;
-    if (v != v) {
+    if ((YT == kFloat8E4M3FN || YT == kFloat8E5M2) && v != v) {
       // The fp8 NaN keeps the fp32 NaN's sign, which the GPU and an x86-64
       // build set differently.  SSE returns its destination operand when both
       // are NaN, else the NaN one, and a negative default NaN for 0/0 and
@@ -85,9 +94,14 @@ template <int YT> __device__ __forceinline__ uint32_t QuantOne(float x, float s,
                             : x != x ? __builtin_bit_cast(uint32_t, x)
                             : s != s ? __builtin_bit_cast(uint32_t, s)
                                      : 0xffc00000u;
-      return bits >> 31 ? 0xffu : 0x7fu;
+      return (bits >> 31 ? 0x80u : 0u) | (YT == kFloat8E4M3FN ? 0x7fu : 0x7eu);
     }
-    return F32ToFp8E4M3Sat(v);
+    if constexpr (YT == kFloat8E4M3FN) return F32ToFp8E4M3Sat(v);
+    else if constexpr (YT == kFloat8E4M3FNUZ) return F32ToFp8Sat<3, 8, true>(v);
+    else if constexpr (YT == kFloat8E5M2) return F32ToFp8Sat<2, 15, false>(v);
+    else if constexpr (YT == kFloat8E5M2FNUZ) return F32ToFp8Sat<2, 16, true>(v);
+    else if constexpr (YT == kFloat4E2M1) return F32ToFp4E2M1(v);
+    else return F32ToFp6<YT == kFloat6E2M3 ? 3 : 2>(v);
   } else {
     const float r = __builtin_rintf(q) + z;
     if (r != r) return 0u;
@@ -123,7 +137,7 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
   uint32_t code[kQPer];
   if constexpr (MODE == 0) {
     const float s = p.scale_f16 ? LoadF<true>(p.scale, 0) : LoadF<false>(p.scale, 0);
-    const float z = p.zp ? ZeroPoint<YT>(p.zp, 0) : 0.f;
+    const float z = p.zp ? ZeroPoint<YT>(p.zp, 0) : -0.f;
 #pragma unroll
     for (int e = 0; e < kQPer; ++e) code[e] = QuantOne<YT>(xv[e], s, z);
   } else {
@@ -141,7 +155,7 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
       const int64_t si = MODE == 1 ? a : (outer * p.s_axis + ab) * p.inner + r;
       if (full || i0 + e < p.n) {
         const float s = p.scale_f16 ? LoadF<true>(p.scale, si) : LoadF<false>(p.scale, si);
-        const float z = p.zp ? ZeroPoint<YT>(p.zp, si) : 0.f;
+        const float z = p.zp ? ZeroPoint<YT>(p.zp, si) : -0.f;
         code[e] = QuantOne<YT>(xv[e], s, z);
       } else {
         code[e] = 0;
@@ -164,10 +178,23 @@ __global__ __launch_bounds__(kQBlock) void QuantKernel(const QuantParams p) {
   }
 
   // full vector stores go through the workgroup's buffer descriptor
-  constexpr int kYBits = YT == kUint4 || YT == kInt4 ? 4 : YT == kUint16 || YT == kInt16 ? 16 : 8;
+  constexpr int kYBits = kYBitsOf<YT>;
   constexpr int kShare = kQBlock * kQPer * kYBits / 8;
   const unsigned off = threadIdx.x * (kQPer * kYBits / 8);
-  if constexpr (YT == kUint4 || YT == kInt4) {
+  if constexpr (kYBits == 2 || kYBits == 6) {
+    // element i at bits kYBits * i of a little-endian bit stream (2-bit: four
+    // per byte from the low bits; rk/cast_sub_byte.h); a thread's 8 elements
+    // fill 2 or 6 whole bytes, stored one by one
+    uint64_t word = 0;
+#pragma unroll
+    for (int e = 0; e < kQPer; ++e)
+      word |= (uint64_t)(i0 + e < p.n ? (code[e] & ((1u << kYBits) - 1u)) : 0u) << (kYBits * e);
+    uint8_t *y = static_cast<uint8_t *>(p.y) + i0 * kYBits / 8;
+    const int64_t bytes = ((full ? kQPer : p.n - i0) * kYBits + 7) / 8;
+#pragma unroll
+    for (int k = 0; k < kQPer * kYBits / 8; ++k)
+      if (k < bytes) y[k] = (uint8_t)(word >> (8 * k));
+  } else if constexpr (kYBits == 4) {
     // element 2k in the low nibble of byte k (rk/cast_sub_byte.h:50-60)
     uint32_t word = 0;
 #pragma unroll
@@ -224,6 +251,26 @@ void LaunchQY(const QuantParams &p, dim3 g, hipStream_t s) {
   case kInt4: hipLaunchKernelGGL((QuantKernel<XF16, MODE, kInt4>), g, dim3(kQBlock), 0, s, p); break;
   case kFloat8E4M3FN:
     hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat8E4M3FN>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kFloat8E4M3FNUZ:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat8E4M3FNUZ>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kFloat8E5M2:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat8E5M2>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kFloat8E5M2FNUZ:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat8E5M2FNUZ>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kFloat4E2M1:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat4E2M1>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kUint2: hipLaunchKernelGGL((QuantKernel<XF16, MODE, kUint2>), g, dim3(kQBlock), 0, s, p); break;
+  case kInt2: hipLaunchKernelGGL((QuantKernel<XF16, MODE, kInt2>), g, dim3(kQBlock), 0, s, p); break;
+  case kFloat6E2M3:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat6E2M3>), g, dim3(kQBlock), 0, s, p);
+    break;
+  case kFloat6E3M2:
+    hipLaunchKernelGGL((QuantKernel<XF16, MODE, kFloat6E3M2>), g, dim3(kQBlock), 0, s, p);
     break;
   default: throw Unsupported("QuantizeLinear: no GPU kernel for this output dtype");
   }

@@ -565,20 +565,106 @@ static float ql_load(const void *x, int dtype, int64_t i) {
   return dtype == ORC_FLOAT16 ? orc_f16_to_f32(((const uint16_t *)x)[i]) : ((const float *)x)[i];
 }
 
-/* Zero point of scale index si as fp32: the integer value (4-bit nibbles
- * sign- or zero-extended, :186-188) or the fp8 decode (:93-107). */
+/* Zero point of scale index si as fp32: the integer value (sub-byte codes
+ * sign- or zero-extended, :186-188) or the float decode (:93-107). */
 static float ql_zero_point(const void *zp, int dtype, int64_t si) {
   if (!zp) return 0.0f;
-  switch (dtype) {
-  case ORC_UINT8: return (float)((const uint8_t *)zp)[si];
-  case ORC_INT8: return (float)((const int8_t *)zp)[si];
-  case ORC_UINT16: return (float)((const uint16_t *)zp)[si];
-  case ORC_INT16: return (float)((const int16_t *)zp)[si];
-  case ORC_UINT4: return (float)orc_read_4bit((const uint8_t *)zp, si);
-  case ORC_INT4: return (float)orc_int4_to_i8(orc_read_4bit((const uint8_t *)zp, si));
-  case ORC_FLOAT8E4M3FN: return orc_f8e4m3fn_to_f32(((const uint8_t *)zp)[si]);
-  default: return 0.0f;
+  return orc_dq_decode(zp, dtype, si);
+}
+
+/* The saturating fp8 encoders of rk/cast_float8.cc:124-173 (E4M3FNUZ),
+ * :214-262 (E5M2) and :303-346 (E5M2FNUZ), restated: round to nearest even
+ * on the fp32 bits; infinities saturate to the largest finite code; NaN is
+ * 0x80 for the FNUZ types and sign|0x7e for E5M2; FNUZ results that round to
+ * zero are +0 (0x80 is NaN). */
+static uint8_t fp8_encode(float v, int mbits, int bias, int fnuz) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  const uint8_t sign = (uint8_t)((b >> 24) & 0x80u);
+  const uint8_t maxc = fnuz ? 0x7f : 0x7b;  /* E4M3FNUZ 240, E5M2 / E5M2FNUZ 57344 */
+  if ((b & 0x7fffffffu) == 0x7f800000u) return (uint8_t)(sign | maxc);
+  if ((b & 0x7f800000u) == 0x7f800000u) return fnuz ? 0x80 : (uint8_t)(sign | 0x7e);
+  const int e = (int)((b >> 23) & 0xff);
+  const uint32_t m = b & 0x7fffffu;
+  if (e == 0) return fnuz ? 0 : sign;  /* fp32 zeros and subnormals */
+  const int E = e - 127 + bias;         /* biased exponent of a normal result */
+  uint32_t mag;
+  if (E >= 1) {
+    const uint32_t full = ((uint32_t)E << 23) | m, sh = 23 - mbits;
+    const uint32_t q = full >> sh, rem = full & ((1u << sh) - 1), half = 1u << (sh - 1);
+    mag = q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+  } else {
+    const int sh = 24 - mbits - E;       /* value / 2^(1 - bias - mbits), a 24-bit significand */
+    if (sh > 25) {
+      mag = 0;
+    } else {
+      const uint32_t full = m | 0x800000u;
+      const uint32_t q = full >> sh, rem = full & ((1u << sh) - 1), half = 1u << (sh - 1);
+      mag = q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+    }
   }
+  if (mag > maxc) mag = maxc;
+  if (fnuz && mag == 0) return 0;
+  return (uint8_t)(sign | mag);
+}
+
+/* FLOAT4E2M1 nearest code (cast_helper.cc:168-203): NaN -> 0, beyond +-6
+ * saturates, distances in fp32 over the same-sign codes, ties to the even
+ * code. */
+static uint8_t fp4_encode(float v) {
+  static const float pos[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  if (isnan(v)) return 0;
+  if (v > 6.0f) return 7;
+  if (v < -6.0f) return 15;
+  if (v == 0.0f) return signbit(v) ? 8 : 0;
+  const int neg = !(v > 0.0f);
+  uint8_t best = neg ? 8 : 0;
+  float bd = fabsf(v - (neg ? -0.0f : 0.0f));
+  for (int i = 1; i < 8; ++i) {
+    const float d = fabsf(v - (neg ? -pos[i] : pos[i]));
+    const uint8_t code = (uint8_t)(neg ? 8 + i : i);
+    if (d < bd || (d == bd && !(code & 1u) && (best & 1u))) {
+      best = code;
+      bd = d;
+    }
+  }
+  return best;
+}
+
+/* FLOAT6 nearest code (cast_helper.cc:220-246): NaN -> 0, +-inf -> +-max,
+ * the first magnitude code not below |v| and the one before it compared by
+ * fp32 distance, ties to the even code; beyond the largest, the largest. */
+static uint8_t fp6_encode(float v, int dtype) {
+  if (isnan(v)) return 0;
+  const uint8_t s = signbit(v) ? 0x20 : 0;
+  if (isinf(v)) return (uint8_t)(0x1f | s);
+  const float mag = fabsf(v);
+  int up = 0;
+  while (up < 32 && orc_f6_to_f32((uint8_t)up, dtype) < mag) ++up;
+  uint8_t best = up == 32 ? 0x1f : (uint8_t)up;
+  if (up != 0 && up != 32) {
+    const float ld = mag - orc_f6_to_f32((uint8_t)(up - 1), dtype), ud = orc_f6_to_f32((uint8_t)up, dtype) - mag;
+    if (ld < ud || (ld == ud && !((up - 1) & 1))) best = (uint8_t)(up - 1);
+  }
+  return (uint8_t)(best | s);
+}
+
+uint8_t orc_f32_to_float_code(float v, int dtype) {
+  switch (dtype) {
+  case ORC_FLOAT8E4M3FN: return orc_f32_to_f8e4m3fn(v);
+  case ORC_FLOAT8E4M3FNUZ: return fp8_encode(v, 3, 8, 1);
+  case ORC_FLOAT8E5M2: return fp8_encode(v, 2, 15, 0);
+  case ORC_FLOAT8E5M2FNUZ: return fp8_encode(v, 2, 16, 1);
+  case ORC_FLOAT4E2M1: return fp4_encode(v);
+  default: return fp6_encode(v, dtype);
+  }
+}
+
+static void put_bits(uint8_t *y, int64_t i, int bits, uint32_t code) {
+  const int64_t bit = i * bits;
+  uint32_t v = (code & ((1u << bits) - 1u)) << (bit % 8);
+  y[bit / 8] |= (uint8_t)v;
+  if ((bit % 8) + bits > 8) y[bit / 8 + 1] |= (uint8_t)(v >> 8);
 }
 
 /* Integer result of nearbyint(v) + zp clamped to [lo, hi] by the
@@ -605,9 +691,18 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
   case ORC_INT16: lo = -32768.0f; hi = 32767.0f; break;
   case ORC_UINT4: lo = 0.0f; hi = 15.0f; break;
   case ORC_INT4: lo = -8.0f; hi = 7.0f; break;
-  case ORC_FLOAT8E4M3FN: lo = hi = 0.0f; break;
+  case ORC_UINT2: lo = 0.0f; hi = 3.0f; break;
+  case ORC_INT2: lo = -2.0f; hi = 1.0f; break;
+  case ORC_FLOAT8E4M3FN: case ORC_FLOAT8E4M3FNUZ: case ORC_FLOAT8E5M2: case ORC_FLOAT8E5M2FNUZ:
+  case ORC_FLOAT4E2M1: case ORC_FLOAT6E2M3: case ORC_FLOAT6E3M2:
+    lo = hi = 0.0f;
+    break;
   default: return 1;
   }
+  const int sub_bits = y_dtype == ORC_UINT4 || y_dtype == ORC_INT4 || y_dtype == ORC_FLOAT4E2M1 ? 4
+                       : y_dtype == ORC_UINT2 || y_dtype == ORC_INT2                          ? 2
+                       : y_dtype == ORC_FLOAT6E2M3 || y_dtype == ORC_FLOAT6E3M2              ? 6
+                                                                                            : 0;
   const int64_t n = numel(x_shape, x_rank);
   const int64_t ns = numel(s_shape, s_rank);
   int64_t repeats[ORC_MAX_RANK], sstr[ORC_MAX_RANK], coord[ORC_MAX_RANK];
@@ -628,7 +723,7 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
       axis_size = x_shape[axis];
     }
   }
-  if (y_dtype == ORC_UINT4 || y_dtype == ORC_INT4) memset(y, 0, (size_t)((n + 1) / 2));
+  if (sub_bits) memset(y, 0, (size_t)((n * sub_bits + 7) / 8));
   for (int64_t i = 0; i < n; ++i) {
     int64_t si = 0;
     if (ns != 1) {
@@ -644,11 +739,25 @@ int orc_quantize_linear(const void *x, int x_dtype, const int64_t *x_shape, int 
     }
     const float q = ql_load(x, x_dtype, i) / ql_load(scale, scale_dtype, si);
     const float z = ql_zero_point(zp, y_dtype, si);
-    if (y_dtype == ORC_FLOAT8E4M3FN) {
-      ((uint8_t *)y)[i] = orc_f32_to_f8e4m3fn(q + z);
+    if (y_dtype == ORC_FLOAT8E4M3FN || y_dtype == ORC_FLOAT8E4M3FNUZ || y_dtype == ORC_FLOAT8E5M2 ||
+        y_dtype == ORC_FLOAT8E5M2FNUZ) {
+      /* both NaN: x86-64 returns the destination operand, which gcc -O2
+       * makes the zero point in the reference's `x / scale + zp`; stated
+       * here so that this file's own register choice does not decide it */
+      const float v = (isnan(q) && isnan(z)) ? z : q + z;
+      ((uint8_t *)y)[i] = orc_f32_to_float_code(v, y_dtype);
+      continue;
+    }
+    if (y_dtype == ORC_FLOAT4E2M1 || y_dtype == ORC_FLOAT6E2M3 || y_dtype == ORC_FLOAT6E3M2) {
+      /* no zero point: nothing is added, so -0 stays -0 (:508-511) */
+      put_bits((uint8_t *)y, i, sub_bits, orc_f32_to_float_code(zp ? q + z : q, y_dtype));
       continue;
     }
     const int32_t v = ql_saturate(nearbyintf(q) + z, lo, hi);
+    if (y_dtype == ORC_UINT2 || y_dtype == ORC_INT2) {
+      put_bits((uint8_t *)y, i, 2, (uint32_t)v);
+      continue;
+    }
     switch (y_dtype) {
     case ORC_UINT8: ((uint8_t *)y)[i] = (uint8_t)v; break;
     case ORC_INT8: ((int8_t *)y)[i] = (int8_t)v; break;

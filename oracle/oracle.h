@@ -69,6 +69,9 @@ uint8_t orc_read_6bit(const uint8_t *data, int64_t i);
 /* the decoded value of element i of x in dtype (every DequantizeLinear input) */
 float orc_dq_decode(const void *x, int dtype, int64_t i);
 void orc_dq_decode_n(const void *x, int dtype, int64_t n, float *out);
+/* the QuantizeLinear float encoders (rk/cast_float8.cc, rk/cast_helper.cc):
+ * fp32 -> FLOAT8E4M3FN / FNUZ / E5M2 / E5M2FNUZ, FLOAT4E2M1, FLOAT6 code */
+uint8_t orc_f32_to_float_code(float v, int dtype);
 int8_t orc_int4_to_i8(uint8_t nibble);  /* rk/cast_sub_byte.cc:81-88 */
 
 /* Bulk codec helpers (same semantics as the scalar ones). */

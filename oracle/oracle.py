@@ -57,6 +57,8 @@ def _declare(L):
     L.orc_f32_to_f8e4m3fn.argtypes = [ctypes.c_float]
     L.orc_f8e4m3fn_to_f32.restype = ctypes.c_float
     L.orc_f8e4m3fn_to_f32.argtypes = [ctypes.c_uint8]
+    L.orc_f32_to_float_code.restype = ctypes.c_uint8
+    L.orc_f32_to_float_code.argtypes = [ctypes.c_float, ctypes.c_int]
     for name in ("orc_f32_to_f16_n", "orc_f16_to_f32_n", "orc_f32_to_bf16_n", "orc_bf16_to_f32_n",
                  "orc_f32_to_f8e4m3fn_n", "orc_f8e4m3fn_to_f32_n"):
         getattr(L, name).restype = None
@@ -291,16 +293,19 @@ def quantize_linear(x: np.ndarray, x_dtype: int, scale: np.ndarray, scale_dtype:
     """QuantizeLinear.  x holds FLOAT values or FLOAT16 bit patterns (its shape
     is x's shape); scale likewise; zp holds the raw storage of the y dtype
     (bytes for 4-bit types).  Returns the raw y storage: a uint8 / int8 /
-    uint16 / int16 array of x's shape, or packed bytes for 4-bit types."""
+    uint16 / int16 / fp8-bits uint8 array of x's shape, or the packed bytes
+    of the sub-byte types."""
     x = np.ascontiguousarray(x)
     scale = np.ascontiguousarray(scale)
     zp_arr = None if zp is None else np.ascontiguousarray(zp)
     n = x.size
-    if y_dtype in (UINT4, INT4):
-        y = np.zeros((n + 1) // 2, np.uint8)
+    sub = {UINT4: 4, INT4: 4, FLOAT4E2M1: 4, UINT2: 2, INT2: 2, FLOAT6E2M3: 6, FLOAT6E3M2: 6}
+    if y_dtype in sub:
+        y = np.zeros((n * sub[y_dtype] + 7) // 8, np.uint8)
     else:
         y = np.empty(x.shape, {UINT8: np.uint8, INT8: np.int8, UINT16: np.uint16, INT16: np.int16,
-                               FLOAT8E4M3FN: np.uint8}[y_dtype])
+                               FLOAT8E4M3FN: np.uint8, FLOAT8E4M3FNUZ: np.uint8, FLOAT8E5M2: np.uint8,
+                               FLOAT8E5M2FNUZ: np.uint8}[y_dtype])
     rc = lib().orc_quantize_linear(_ptr(x), x_dtype, _ptr(_shape(x.shape)), x.ndim, _ptr(scale),
                                    scale_dtype, _ptr(_shape(scale.shape)), scale.ndim,
                                    None if zp_arr is None else _ptr(zp_arr), y_dtype, axis, _ptr(y))
@@ -566,6 +571,13 @@ def dq_decode(raw: np.ndarray, dtype: int, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().orc_dq_decode_n(_ptr(raw), dtype, n, _ptr(out))
     return out
+
+
+def float_code(values, dtype: int) -> np.ndarray:
+    """QuantizeLinear's float encoders element by element: fp32 values ->
+    FLOAT8E4M3FN / FNUZ / E5M2 / E5M2FNUZ bytes, FLOAT4E2M1 or FLOAT6 codes."""
+    v = np.asarray(values, np.float32).reshape(-1)
+    return np.array([lib().orc_f32_to_float_code(float(f), dtype) for f in v], np.uint8)
 
 
 def pack_bits(codes, bits: int) -> np.ndarray:

@@ -239,13 +239,23 @@ def test_quantize_validation(olamd):
     assert rc == olamd.NOT_INITIALIZED
     rc, _ = run(s=np.array(1.0, np.float32))
     assert rc == olamd.NOT_INITIALIZED
-    # output types the reference quantizes and this library has no kernel for
-    for dt in (18, 19, 20, 25, 26):
-        rc, _ = run(s=np.array(1.0, np.float32), z=np.zeros(1, np.uint8), zdt=dt,
-                    y=np.zeros(6 if dt < 25 else 2, np.uint8), ydt=dt)
-        assert rc == olamd.UNSUPPORTED, dt
-    rc, _ = run(s=np.array(1.0, np.float32), odt=23, y=np.zeros(3, np.uint8), ydt=23)
-    assert rc == olamd.UNSUPPORTED
+    # the fp8 variants, FLOAT4E2M1, UINT2 / INT2 and FLOAT6 with a zero point
+    # (packed sizes: 6 elements in 6, 3, 2 and 5 bytes) pass validation
+    for dt, nbytes in ((18, 6), (19, 6), (20, 6), (23, 3), (25, 2), (26, 2), (27, 5), (28, 5)):
+        rc, err = run(s=np.array(1.0, np.float32), z=np.zeros(1, np.uint8), zdt=dt,
+                      y=np.zeros(nbytes, np.uint8), ydt=dt)
+        assert rc == olamd.NOT_INITIALIZED, (dt, err)
+    # without one: FLOAT4E2M1 and FLOAT6 per tensor only (:485-532)
+    for dt, nbytes in ((23, 3), (27, 5), (28, 5)):
+        rc, _ = run(s=np.array(1.0, np.float32), odt=dt, y=np.zeros(nbytes, np.uint8), ydt=dt)
+        assert rc == olamd.NOT_INITIALIZED, dt
+        rc, err = run(odt=dt, y=np.zeros(nbytes, np.uint8), ydt=dt)
+        assert rc == olamd.INVALID_ARGUMENT and "unsupported output dtype." in err, dt
+    for dt in (18, 25):
+        rc, err = run(s=np.array(1.0, np.float32), odt=dt, y=np.zeros(6, np.uint8), ydt=dt)
+        assert rc == olamd.INVALID_ARGUMENT and "unsupported output dtype." in err, dt
+    rc, err = run(s=np.array(1.0, np.float32), z=np.zeros(1, np.uint8), zdt=24, y=np.zeros(6, np.uint8), ydt=24)
+    assert rc == olamd.INVALID_ARGUMENT and "unsupported data type 24" in err
 
 
 def test_dynamic_quantize_validation(olamd):

@@ -179,6 +179,111 @@ def test_special_values(olamd, oracle, dev):
         assert np.array_equal(got, want), ("float8e4m3fn", sv, zv, np.flatnonzero(got != want)[:5])
 
 
+# ---- the other output types of the reference: three fp8 variants,
+# FLOAT4E2M1, UINT2 / INT2 and the two FLOAT6 types (raw codes throughout) ----
+CODES = {"float8e4m3fnuz": 18, "float8e5m2": 19, "float8e5m2fnuz": 20, "float4e2m1": 23, "uint2": 25,
+         "int2": 26, "float6e2m3": 27, "float6e3m2": 28}
+BITS = {23: 4, 25: 2, 26: 2, 27: 6, 28: 6}
+ZP_VALUES = {18: [0.0, 1.0, -2.0, 0.5, 3.5], 19: [0.0, 1.0, -2.0, 0.5, 3.5], 20: [0.0, 1.0, -2.0, 0.5, 3.5],
+             23: [0.0, 0.5, -1.0, 1.5], 27: [0.0, 0.25, -1.0, 2.0], 28: [0.0, 0.25, -1.0, 2.0]}
+
+
+def _zp_raw(oracle, codes, code, s_shape):
+    """Zero point codes -> the raw storage QuantizeLinear takes."""
+    c = np.asarray(codes).reshape(-1)
+    if code in BITS:
+        return oracle.pack_bits(c, BITS[code])
+    return c.astype(np.uint8).reshape(s_shape)
+
+
+def _random_zp(oracle, rng, code, s_shape):
+    n = int(np.prod(s_shape, dtype=np.int64))
+    if code in (25, 26):
+        return _zp_raw(oracle, rng.integers(0, 4, n), code, s_shape)
+    vals = rng.choice(ZP_VALUES[code], n).astype(np.float32)
+    return _zp_raw(oracle, oracle.float_code(vals, code), code, s_shape)
+
+
+def _run_code(olamd, oracle, dev, xv, x_dtype, sv, code, zp_raw, axis=1, offset=0):
+    """GPU and oracle raw outputs of one QuantizeLinear to output type `code`
+    (with zp_raw None: no zero point, output_dtype = code)."""
+    x_o, x_t = _xs(oracle, xv, x_dtype, dev)
+    s_o, s_t = _xs(oracle, sv, x_dtype, dev)
+    zp_t = None if zp_raw is None else _dev_tensor(zp_raw, dev)
+    shape = x_o.shape
+    n = int(np.prod(shape, dtype=np.int64))
+    out = None
+    if offset:
+        flat = torch.empty(x_t.numel() + offset, dtype=x_t.dtype, device=dev)
+        flat[offset:] = x_t.reshape(-1)
+        x_t = flat[offset:].view(shape)
+        nbytes = (n * BITS[code] + 7) // 8 if code in BITS else n
+        raw = torch.empty(nbytes + 1, dtype=torch.uint8, device=dev)
+        out = raw[1:] if code in BITS else raw[1:].view(shape)
+    y = olamd.quantize_linear(x_t, s_t, zp_t, axis, 0 if zp_raw is not None else code, y_dtype=code, out=out)
+    torch.cuda.synchronize()
+    got = y.view(torch.uint8).cpu().numpy().reshape(-1)
+    oaxis = axis + len(shape) if axis < 0 else axis
+    want = oracle.quantize_linear(x_o, DT[x_dtype], s_o, DT[x_dtype], code, zp_raw, oaxis).reshape(-1)
+    return got, want
+
+
+@pytest.mark.parametrize("y_name", sorted(CODES))
+@pytest.mark.parametrize("x_dtype", ["float", "float16"])
+def test_other_outputs_random_vs_oracle(olamd, oracle, dev, y_name, x_dtype):
+    """Every scale layout, with a zero point (and without one for the per
+    tensor FLOAT4E2M1 / FLOAT6 cases the reference allows), aligned and
+    misaligned, at magnitudes inside and far past each type's range."""
+    code = CODES[y_name]
+    rng = np.random.default_rng(zlib.crc32(repr((y_name, x_dtype)).encode()))
+    for shape, axis, s_shape in LAYOUTS:
+        xv = (rng.standard_normal(shape) * rng.choice([0.3, 2.0, 30.0, 500.0])).astype(np.float32)
+        sv = rng.uniform(0.03, 3.0, s_shape).astype(np.float32)
+        zps = [_random_zp(oracle, rng, code, s_shape)]
+        if s_shape == () and code in (23, 27, 28):
+            zps.append(None)
+        for zp in zps:
+            for offset in (0, 1):
+                got, want = _run_code(olamd, oracle, dev, xv, x_dtype, sv, code, zp, axis, offset)
+                bad = np.flatnonzero(got != want)
+                assert bad.size == 0, (y_name, x_dtype, shape, axis, s_shape, zp is None, offset,
+                                       bad[:5], got[bad[:5]], want[bad[:5]])
+
+
+@pytest.mark.parametrize("y_name", sorted(CODES))
+def test_other_outputs_special_values(olamd, oracle, dev, y_name):
+    """Each code's midpoints with its neighbours (ties to even) and the
+    points either side, signed zeros, NaN, infinities, overflow, subnormal
+    inputs and scales, x / 0, NaN scales and NaN zero points (the fp8
+    types' NaN sign as x86-64 gives it)."""
+    code = CODES[y_name]
+    n = {23: 16, 27: 64, 28: 64, 25: 4, 26: 4}.get(code, 256)
+    if code in (25, 26):
+        mids = np.arange(-4.5, 4.5, 0.5, dtype=np.float32)
+    else:
+        raw = np.arange(n, dtype=np.uint8) if code not in BITS else oracle.pack_bits(np.arange(n), BITS[code])
+        vals = oracle.dq_decode(raw, code, n).astype(np.float64)
+        vals = np.unique(vals[np.isfinite(vals)])
+        mids = ((vals[1:] + vals[:-1]) / 2).astype(np.float32)
+        mids = np.concatenate([vals.astype(np.float32), mids, np.nextafter(mids, np.float32(np.inf)),
+                               np.nextafter(mids, np.float32(-np.inf))])
+    tiny = np.float32(1.5e-39)
+    xv = np.concatenate([mids, np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30, tiny, -tiny,
+                                         3e-45, 1e9, -1e9], np.float32)])
+    zero = _zp_raw(oracle, [0], code, ())
+    cases = [(1.0, zero), (2.0 ** -130, zero), (0.0, zero), (np.inf, zero), (-1.0, zero), (np.nan, zero),
+             (-np.nan, zero), (3.0, _random_zp(oracle, np.random.default_rng(code), code, ()))]
+    if code in (23, 27, 28):
+        cases += [(1.0, None), (-1.0, None), (0.0, None)]
+    nan_codes = {18: [0x80], 19: [0x7E, 0xFE, 0x7F, 0xFD], 20: [0x80]}.get(code, [])
+    cases += [(sv, _zp_raw(oracle, [c], code, ())) for c in nan_codes for sv in (1.0, 0.0, np.nan)]
+    for sv, zp in cases:
+        got, want = _run_code(olamd, oracle, dev, xv, "float", np.array(sv, np.float32), code, zp)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, (y_name, sv, None if zp is None else zp.tolist(), bad[:5], got[bad[:5]],
+                               want[bad[:5]])
+
+
 def test_activation_shape(olamd, oracle, dev):
     """The BASELINE activation [2048, 4096] in both fp32 -> uint8 (scalar
     scale and zero point, the QLinearMatMul producer) and fp16 -> int8 per
@@ -192,12 +297,13 @@ def test_activation_shape(olamd, oracle, dev):
     assert np.array_equal(got, want)
 
 
-def test_unsupported_output_reported(olamd, dev):
+def test_unsupported_output_rejected(olamd, dev):
+    """FLOAT8E8M0 has no QuantizeLinear path in the reference either."""
     x = torch.zeros(8, device=dev)
     s = torch.ones((), device=dev)
     z = torch.zeros(1, dtype=torch.uint8, device=dev)
-    with pytest.raises(olamd.Unsupported):
-        olamd.quantize_linear(x, s, z, y_dtype=19, out=torch.empty(8, dtype=torch.uint8, device=dev))
+    with pytest.raises(olamd.InvalidArgument):
+        olamd.quantize_linear(x, s, z, y_dtype=24, out=torch.empty(8, dtype=torch.uint8, device=dev))
 
 
 # ---- DynamicQuantizeLinear ---------------------------------------------------

@@ -5,6 +5,7 @@ tests hold (tests/golden/reference_known_answers.json), and a numpy float32
 closed form (IEEE true division, np.rint ties-to-even, saturation) over random
 inputs in every scale layout and output type."""
 import zlib
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -156,3 +157,125 @@ def test_fp8_nan_sign_follows_x86(oracle):
     y = oracle.quantize_linear(np.array([1.0, -np.nan], np.float32), 1, np.array(1.0, np.float32), 1,
                                DT["float8e4m3fn"], nan_zp, 1)
     assert y.tolist() == [0x7f, 0x7f]
+
+
+# ---- the float and 2-bit output types ---------------------------------------
+# Codes per type and whether the type is FNUZ (no negative zero, one NaN).
+FLOAT_CODES = {18: (256, True), 19: (256, False), 20: (256, True), 23: (16, False), 27: (64, False),
+               28: (64, False)}
+
+
+def _table(oracle, dtype):
+    """Decoded value of every code (the decoders are pinned against numpy's
+    fp16, the formats' maxima and subnormal steps in test_oracle_codecs)."""
+    n, _ = FLOAT_CODES[dtype]
+    bits = {16: 4, 64: 6}.get(n, 8)
+    raw = np.arange(n, dtype=np.uint8) if bits == 8 else oracle.pack_bits(np.arange(n), bits)
+    return oracle.dq_decode(raw, dtype, n).astype(np.float64)
+
+
+def _nearest(oracle, dtype, v):
+    """Brute-force nearest finite code to v among the codes of v's sign (the
+    FNUZ types' single zero included), exact rational distances, ties to the
+    even code; what every encoder of the reference computes, stated without
+    its bit manipulations."""
+    n, fnuz = FLOAT_CODES[dtype]
+    vals = _table(oracle, dtype)
+    sign_bit = {256: 0x80, 16: 8, 64: 0x20}[n]
+    neg = np.signbit(np.float32(v))
+    best = None
+    for c in range(n):
+        if not np.isfinite(vals[c]):
+            continue
+        if fnuz:
+            if c != 0 and bool(c & sign_bit) != neg:
+                continue
+        elif bool(c & sign_bit) != neg:
+            continue
+        d = abs(Fraction(float(v)) - Fraction(vals[c]))
+        if best is None or d < best[0] or (d == best[0] and c % 2 == 0 and best[1] % 2 == 1):
+            best = (d, c)
+    return best[1]
+
+
+@pytest.mark.parametrize("dtype", sorted(FLOAT_CODES))
+def test_float_encoders_round_trip(oracle, dtype):
+    """Every finite code decodes and encodes back to itself; the E5M2
+    infinities saturate to the largest finite code."""
+    n, _ = FLOAT_CODES[dtype]
+    vals = _table(oracle, dtype).astype(np.float32)
+    codes = oracle.float_code(vals, dtype)
+    for c in range(n):
+        if np.isnan(vals[c]):
+            continue
+        want = (c & 0x80) | 0x7B if np.isinf(vals[c]) else c
+        assert codes[c] == want, (dtype, c, vals[c])
+
+
+@pytest.mark.parametrize("dtype", sorted(FLOAT_CODES))
+def test_float_encoders_nearest_even(oracle, dtype):
+    """Midpoints of adjacent codes (ties, exact in fp32), points just either
+    side of them, random values across the range and beyond it: the nearest
+    code by brute force, ties to the even code, saturation past the
+    largest."""
+    vals = np.unique(_table(oracle, dtype)[np.isfinite(_table(oracle, dtype))])
+    mids = ((vals[1:] + vals[:-1]) / 2).astype(np.float32)
+    probes = [mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf))]
+    rng = np.random.default_rng(dtype)
+    top = float(vals.max())
+    probes.append((rng.uniform(-1.5, 1.5, 300) * top).astype(np.float32))
+    probes.append((rng.standard_normal(200) * float(vals[vals > 0].min()) * 4).astype(np.float32))
+    probes.append(np.array([top * 1.01, -top * 4, 1e30, -1e-30, 1e-30, -0.0, 0.0], np.float32))
+    x = np.concatenate(probes)
+    got = oracle.float_code(x, dtype)
+    want = [_nearest(oracle, dtype, v) for v in x]
+    bad = [(float(v), int(g), int(w)) for v, g, w in zip(x, got, want) if g != w]
+    assert not bad, bad[:8]
+
+
+def test_float_encoders_specials(oracle):
+    """NaN: 0x80 for the FNUZ types, sign|0x7e for E5M2 (cast_float8.cc:
+    214-262), 0 for FLOAT4E2M1 and FLOAT6 (cast_helper.cc:168-246);
+    infinities saturate."""
+    x = np.array([np.nan, -np.nan, np.inf, -np.inf], np.float32)
+    assert oracle.float_code(x, 18).tolist() == [0x80, 0x80, 0x7F, 0xFF]
+    assert oracle.float_code(x, 19).tolist() == [0x7E, 0xFE, 0x7B, 0xFB]
+    assert oracle.float_code(x, 20).tolist() == [0x80, 0x80, 0x7F, 0xFF]
+    assert oracle.float_code(x, 23).tolist() == [0, 0, 7, 15]
+    assert oracle.float_code(x, 27).tolist() == [0, 0, 0x1F, 0x3F]
+    assert oracle.float_code(x, 28).tolist() == [0, 0, 0x1F, 0x3F]
+
+
+def test_quantize_float6_and_float4_known_answers(oracle):
+    """The reference's own answers: QuantizeAndDequantizeLinearFloat6
+    (unittests/cc/onnx_extensions/kernels/kernels/test_kernels_quantization.cc:
+    136-154) and the FLOAT4E2M1 signed-zero case without a zero point
+    (unittests/cc/onnx_extensions/backend_test/cases/test_cases_quantization.cc:
+    271-287)."""
+    x = np.array([-1.0, -0.5, 0.0, 1.0, 2.0], np.float32)
+    one = np.array(1.0, np.float32)
+    for dtype, want in ((27, [40, 9, 32, 16]), (28, [44, 10, 48, 16])):
+        y = oracle.quantize_linear(x, 1, one, 1, dtype, np.zeros(1, np.uint8), 0)
+        assert y.tolist() == want, dtype
+    y = oracle.quantize_linear(np.array([-0.0, 0.0], np.float32), 1, one, 1, 23, None, 0)
+    assert y.tolist() == [0x08]
+    # a zero point of +0 turns -0 into +0 (-0 + 0 = +0)
+    y = oracle.quantize_linear(np.array([-0.0, 0.0], np.float32), 1, one, 1, 23, np.zeros(1, np.uint8), 0)
+    assert y.tolist() == [0x00]
+
+
+@pytest.mark.parametrize("dtype", [25, 26])
+def test_quantize_int2_closed_form(oracle, dtype):
+    """UINT2 / INT2 (kq/kernel_quantizelinear.cc:202-224): rint(x / scale) +
+    zero point saturated to 0..3 / -2..1, packed four per byte from the low
+    bits; per axis with a zero point per row."""
+    rng = np.random.default_rng(dtype)
+    x = (rng.standard_normal((5, 13)) * 3).astype(np.float32)
+    x[0, :4] = [0.5, 1.5, -0.5, -2.5]  # ties
+    s = rng.uniform(0.5, 2.0, 5).astype(np.float32)
+    lo, hi = (0, 3) if dtype == 25 else (-2, 1)
+    z = rng.integers(lo, hi + 1, 5)
+    y = oracle.quantize_linear(x, 1, s, 1, dtype, oracle.pack_bits(z & 3, 2), 0)
+    q = (x / s[:, None]).astype(np.float32)
+    want = np.clip(np.rint(q) + z[:, None], lo, hi).astype(np.int64) & 3
+    assert y.tolist() == oracle.pack_bits(want.reshape(-1), 2).tolist()
