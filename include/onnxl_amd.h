@@ -95,7 +95,9 @@ int onnxl_amd_matmul_integer(const onnxl_amd_tensor *a, const onnxl_amd_tensor *
 
 /* QLinearMatMul: y = saturate(rint((float)Σ(a-za)(b-zb) * (a_s*b_s/y_s)) + zy).
  * a, b: UINT8/INT8; scales: FLOAT or FLOAT16 scalars; zero points: scalars
- * with their input's dtype; y dtype = y_zero_point dtype.
+ * with their input's dtype; y dtype = y_zero_point dtype.  The sum is exact
+ * for every K, as the reference's int64 sum (past K * max|a-za| * max|b-zb|
+ * = 2^31 an int64-accumulating kernel runs instead of the MFMA GEMM).
  * Replaces kernel::QLinearMatMul::operator()(..., Tensor &output),
  * kq/kernel_qlinearmatmul.cc:242-267 (arithmetic :115-217). */
 int onnxl_amd_qlinear_matmul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,

@@ -431,8 +431,7 @@ int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
     return std::max<int64_t>(std::llabs(lo - z), std::llabs(hi - z));
   };
   const double bound = (double)plan.K * (double)span(a->data_type, za) * (double)span(b->data_type, zb);
-  if (!(bound < 2147483648.0))
-    throw Unsupported("QLinearMatMul: K too large for exact int32 accumulation on the GPU path");
+  const bool exact32 = bound < 2147483648.0;  // else the int64-accumulating kernel
 
   IGemmParams p{};
   p.M = plan.M;
@@ -459,7 +458,8 @@ int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
   p.A = static_cast<const int8_t *>(st.In(a));
   p.B = static_cast<const int8_t *>(st.In(b));
   p.Y = st.Out(y);
-  LaunchIGemm(p, stream);
+  if (exact32) LaunchIGemm(p, stream);
+  else LaunchQlmExact(p, za, zb, stream);
   st.Finish();
   return ONNXL_AMD_OK;
 }

@@ -638,4 +638,71 @@ void LaunchIGemm(const IGemmParams &p, hipStream_t stream) {
   else LaunchEpi<kEpiQuant8>(p, mode, grid, stream);
 }
 
+
+// ---------------------------------------------------------------------------
+// QLinearMatMul past the int32-exact K.  One 16x16 output tile per
+// workgroup, one output per thread; 64-deep K slices of (a - za) and
+// (b - zb) staged in LDS.  A slice's 64 products (|.| <= 255 * 255 each)
+// sum exactly in int32 and are added into an int64 total, so the sum is the
+// reference's for every K; then the same requantization as the MFMA
+// epilogue: rint((float)acc * cs) + zy, clamped, NaN -> 0.
+namespace {
+constexpr int kXT = 16, kXK = 64;
+
+__global__ __launch_bounds__(256) void QlmExactKernel(const IGemmParams p, int32_t za, int32_t zb) {
+  __shared__ int32_t as[kXT][kXK + 1];
+  __shared__ int32_t bs[kXK][kXT + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t row = (int64_t)blockIdx.y * kXT + ty, col = (int64_t)blockIdx.x * kXT + tx;
+  const int64_t batch = blockIdx.z;
+  int64_t a_off = 0, b_off = 0;
+  BatchOffsets(p.bm, batch, a_off, b_off);
+  const int8_t *A = p.A + a_off;
+  const int8_t *B = p.B + b_off;
+  int64_t acc = 0;
+  for (int64_t k0 = 0; k0 < p.K; k0 += kXK) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = (int)threadIdx.x + 256 * e;
+      const int ar = i / kXK, ak = i % kXK;  // A slice [16][64]
+      const int64_t gr = (int64_t)blockIdx.y * kXT + ar, gk = k0 + ak;
+      int32_t av = 0;
+      if (gr < p.M && gk < p.K) {
+        const int8_t v = A[gr * p.K + gk];
+        av = (p.a_u8 ? (int32_t)(uint8_t)v : (int32_t)v) - za;
+      }
+      as[ar][ak] = av;
+      const int bk = i / kXT, bc = i % kXT;  // B slice [64][16]
+      const int64_t gk2 = k0 + bk, gc = (int64_t)blockIdx.x * kXT + bc;
+      int32_t bv = 0;
+      if (gk2 < p.K && gc < p.N) {
+        const int8_t v = B[gk2 * p.N + gc];
+        bv = (p.b_u8 ? (int32_t)(uint8_t)v : (int32_t)v) - zb;
+      }
+      bs[bk][bc] = bv;
+    }
+    __syncthreads();
+    int32_t part = 0;
+#pragma unroll 16
+    for (int k = 0; k < kXK; ++k) part += as[ty][k] * bs[k][tx];
+    acc += part;
+    __syncthreads();
+  }
+  if (row < p.M && col < p.N) {
+    const float v = __builtin_rintf((float)acc * p.cs) + p.zy;
+    const uint8_t q = v != v ? 0 : (uint8_t)(int32_t)__builtin_amdgcn_fmed3f(v, p.qmin, p.qmax);
+    static_cast<uint8_t *>(p.Y)[(batch * p.M + row) * p.N + col] = q;
+  }
+}
+}  // namespace
+
+void LaunchQlmExact(const IGemmParams &p, int32_t za, int32_t zb, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0 || p.batch == 0) return;
+  const int64_t gx = (p.N + kXT - 1) / kXT, gy = (p.M + kXT - 1) / kXT;
+  if (gx > 0x7fffffff || gy > 65535 || p.batch > 65535)
+    throw Unsupported("QLinearMatMul: shape too large for the int64-exact GPU path");
+  hipLaunchKernelGGL(QlmExactKernel, dim3((unsigned)gx, (unsigned)gy, (unsigned)p.batch), dim3(256), 0, stream, p,
+                     za, zb);
+}
+
 }  // namespace onnxl_amd

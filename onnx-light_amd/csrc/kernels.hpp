@@ -94,6 +94,11 @@ struct IGemmParams {
 };
 
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
+// QLinearMatMul where the int32 MFMA sums can overflow: int64 accumulation
+// (kq/kernel_qlinearmatmul.cc:187-191) in a VALU kernel; uses p.A, p.B, p.Y,
+// M, N, K, batch, bm, a_u8, b_u8, cs, zy, qmin, qmax, y_signed and the zero
+// points za, zb given here.
+void LaunchQlmExact(const IGemmParams &p, int32_t za, int32_t zb, hipStream_t stream);
 // Whether LaunchIGemm takes the pipelined MFMA kernel for p (kEpiQuant8Row
 // requires it).
 bool IGemmFastEligible(const IGemmParams &p);

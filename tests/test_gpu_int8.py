@@ -216,3 +216,39 @@ def test_config2_qlinear_full_size(olamd, oracle, dev):
     v = torch.round(acc.float() * float(cs)) + 128.0
     ref = v.clamp(0, 255).to(torch.uint8)
     assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("shapes,centred", [(((5, 40000), (40000, 70)), False),
+                                            (((2, 3, 33100), (33100, 17)), False),
+                                            (((1, 65536), (65536, 16)), False),
+                                            (((3, 140000), (140000, 24)), True)])
+def test_qlinear_past_int32_exact(olamd, oracle, dev, shapes, centred):
+    """K * max|a - za| * max|b - zb| >= 2^31: the reference's int64 sums
+    (kq/kernel_qlinearmatmul.cc:187-191) on the int64-accumulating kernel.
+    Row 0 against column 0 sums past int32 (every a and b at the far end of
+    its range), which a wrapped int32 sum would turn negative; ragged tiles
+    and a batch.  With zero points 128 the other sums centre on 0 and y_scale
+    spreads them over many output steps, so the rounding is exercised."""
+    a_shape, b_shape = shapes
+    rng = np.random.default_rng(zlib.crc32(repr(shapes).encode()))
+    a = rng.integers(0, 256, a_shape).astype(np.uint8)
+    b = rng.integers(0, 256, b_shape).astype(np.uint8)
+    far = 0 if centred else 255
+    a.reshape(-1, a_shape[-1])[0] = far
+    b[:, 0] = far
+    za = zb = 128 if centred else 0
+    acc = np.matmul(a.astype(np.int64) - za, b.astype(np.int64) - zb)
+    assert np.abs(acc).max() >= 2 ** 31
+    a_s, b_s = np.float32(0.02), np.float32(0.01)
+    spread = float(np.std(acc.reshape(-1, acc.shape[-1])[1:, 1:])) / 8 if centred else float(np.abs(acc).max()) / 200
+    y_s = np.float32(a_s * b_s * (spread + 1.0))
+    zy = 128 if centred else 20
+    args = (T(a, dev), T(np.array(a_s), dev), T(np.array(za, np.uint8), dev), T(b, dev),
+            T(np.array(b_s), dev), T(np.array(zb, np.uint8), dev), T(np.array(y_s), dev),
+            T(np.array(zy, np.uint8), dev))
+    y = olamd.qlinear_matmul(*args).cpu().numpy()
+    ref = oracle.qlinear_matmul(a, a_s, za, b, b_s, zb, y_s, zy, y_dtype=oracle.UINT8)
+    assert np.array_equal(y, ref)
+    assert ref.reshape(-1, ref.shape[-1])[0, 0] == ref.max() > 128  # the sum past int32, the largest output
+    if centred:
+        assert len(np.unique(ref)) > 10
