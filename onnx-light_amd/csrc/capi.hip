@@ -372,25 +372,59 @@ int MatMulInteger(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
 
 constexpr const char *kQlmName = "kernel::QLinearMatMul";
 
-int32_t QReadScalarInt(const onnxl_amd_tensor &t, const char *name) {  // :35-38
-  OLA_ENFORCE(NumElements(t) == 1, kQlmName, ": '", name, "' must be a scalar.");
-  return ReadIntElem(t, 0);
-}
+// QLinearMatMul's six scalars at once: the reference's checks in its order
+// (:35-51), then every device-resident payload copied on the call's stream
+// into pinned host memory, with one synchronisation of that stream for all
+// of them (not one blocking copy per scalar, which also waits for the whole
+// device).
+struct QlmScalars {
+  int32_t za, zb, zy;
+  float as, bs, ys;
+};
 
-float QReadScalarFloat(const onnxl_amd_tensor &t, const char *name) {  // :40-51
-  OLA_ENFORCE(NumElements(t) == 1, kQlmName, ": '", name, "' must be a scalar.");
-  if (t.data_type == kFloat) {
-    float v;
-    ReadBytes(t, 0, &v, 4);
-    return v;
+QlmScalars QReadScalars(const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b_zp, const onnxl_amd_tensor *y_zp,
+                        const onnxl_amd_tensor *a_s, const onnxl_amd_tensor *b_s, const onnxl_amd_tensor *y_s,
+                        hipStream_t stream) {
+  const onnxl_amd_tensor *ts[6] = {a_zp, b_zp, y_zp, a_s, b_s, y_s};
+  const char *names[6] = {"a_zero_point", "b_zero_point", "y_zero_point", "a_scale", "b_scale", "y_scale"};
+  for (int i = 0; i < 6; ++i) {
+    OLA_ENFORCE(NumElements(*ts[i]) == 1, kQlmName, ": '", names[i], "' must be a scalar.");
+    if (i >= 3 && ts[i]->data_type != kFloat && ts[i]->data_type != kFloat16)
+      throw InvalidArgument(Cat(kQlmName, ": '", names[i],
+                                "' must be a FLOAT or FLOAT16 scalar for the reference kernel."));
   }
-  if (t.data_type == kFloat16) {
-    uint16_t h;
-    ReadBytes(t, 0, &h, 2);
-    return HalfBitsToFloat(h);
+  static thread_local uint8_t *pinned = nullptr;  // 6 slots of 8 bytes, kept for the thread's life
+  uint8_t host[6][8] = {};
+  bool any_device = false;
+  for (int i = 0; i < 6; ++i) {
+    const size_t bytes = i < 3 ? 1 : (ts[i]->data_type == kFloat ? 4 : 2);
+    if (ts[i]->location == ONNXL_AMD_HOST) {
+      std::memcpy(host[i], ts[i]->data, bytes);
+      continue;
+    }
+    if (!pinned) OLA_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), 64, hipHostMallocDefault));
+    OLA_HIP(hipMemcpyAsync(pinned + 8 * i, ts[i]->data, bytes, hipMemcpyDeviceToHost, stream));
+    any_device = true;
   }
-  throw InvalidArgument(Cat(kQlmName, ": '", name,
-                            "' must be a FLOAT or FLOAT16 scalar for the reference kernel."));
+  if (any_device) {
+    OLA_HIP(hipStreamSynchronize(stream));
+    for (int i = 0; i < 6; ++i)
+      if (ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], pinned + 8 * i, 8);
+  }
+  QlmScalars r{};
+  int32_t *zs[3] = {&r.za, &r.zb, &r.zy};
+  for (int i = 0; i < 3; ++i) *zs[i] = ts[i]->data_type == kInt8 ? (int32_t)(int8_t)host[i][0] : (int32_t)host[i][0];
+  float *fs[3] = {&r.as, &r.bs, &r.ys};
+  for (int i = 3; i < 6; ++i) {
+    if (ts[i]->data_type == kFloat) {
+      std::memcpy(fs[i - 3], host[i], 4);
+    } else {
+      uint16_t h;
+      std::memcpy(&h, host[i], 2);
+      *fs[i - 3] = HalfBitsToFloat(h);
+    }
+  }
+  return r;
 }
 
 int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
@@ -416,12 +450,9 @@ int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
   OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kQlmName, ": preallocated output has invalid shape.");
   OLA_ENFORCE(y->size_bytes >= NumElements(plan.out_shape), kQlmName,
               ": preallocated output buffer size does not match its shape.");
-  const int32_t za = QReadScalarInt(*a_zp, "a_zero_point");
-  const int32_t zb = QReadScalarInt(*b_zp, "b_zero_point");
-  const int32_t zy = QReadScalarInt(*y_zp, "y_zero_point");
-  const float as = QReadScalarFloat(*a_scale, "a_scale");
-  const float bs = QReadScalarFloat(*b_scale, "b_scale");
-  const float ys = QReadScalarFloat(*y_scale, "y_scale");
+  const QlmScalars sc = QReadScalars(a_zp, b_zp, y_zp, a_scale, b_scale, y_scale, stream);
+  const int32_t za = sc.za, zb = sc.zb, zy = sc.zy;
+  const float as = sc.as, bs = sc.bs, ys = sc.ys;
   OLA_ENFORCE(ys != 0.0f, kQlmName, ": y_scale must be non-zero.");
 
   // The reference accumulates in int64 (:187-191); the MFMA path is exact

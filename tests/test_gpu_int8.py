@@ -252,3 +252,20 @@ def test_qlinear_past_int32_exact(olamd, oracle, dev, shapes, centred):
     assert ref.reshape(-1, ref.shape[-1])[0, 0] == ref.max() > 128  # the sum past int32, the largest output
     if centred:
         assert len(np.unique(ref)) > 10
+
+
+def test_qlinear_scalars_host_device_mixed(olamd, oracle, dev):
+    """The six scalars read in one pass: device-resident ones copied on the
+    call's stream with one synchronisation, host ones read directly; every
+    mix (and an fp16 scale) gives the oracle's bytes."""
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 256, (33, 96)).astype(np.uint8)
+    b = rng.integers(-128, 128, (96, 40)).astype(np.int8)
+    vals = [np.array(0.02, np.float32), np.array(131, np.uint8), np.array(0.01, np.float16),
+            np.array(-3, np.int8), np.array(0.9, np.float32), np.array(7, np.int8)]
+    ref = oracle.qlinear_matmul(a, np.float32(0.02), 131, b, np.float32(np.float16(0.01)), -3, np.float32(0.9), 7,
+                                y_dtype=oracle.INT8)
+    for mask in (0, 0b101010, 0b010101, 0b111111, 0b100000):
+        sc = [T(v, dev) if mask >> i & 1 else v for i, v in enumerate(vals)]
+        y = olamd.qlinear_matmul(T(a, dev), sc[0], sc[1], T(b, dev), sc[2], sc[3], sc[4], sc[5]).cpu().numpy()
+        assert np.array_equal(y, ref), bin(mask)
