@@ -271,6 +271,46 @@ private:
 
 bool IsInt8OrUint8(int32_t dt) { return dt == kInt8 || dt == kUint8; }
 
+// The first bytes[i] (<= 8) bytes of each descriptor ts[i] (null: skipped)
+// into host[i]: host payloads directly, device ones by copies on `stream`
+// into pinned memory with one synchronisation of that stream for all of them
+// (not one blocking copy each, which also waits for the whole device).
+void ReadLeadingBytes(hipStream_t stream, int n, const onnxl_amd_tensor *const *ts, const size_t *bytes,
+                      uint8_t (*host)[8]) {
+  static thread_local uint8_t *pinned = nullptr;  // 8 slots of 8 bytes, kept for the thread's life
+  bool any_device = false;
+  for (int i = 0; i < n; ++i) {
+    if (!ts[i]) continue;
+    if (ts[i]->location == ONNXL_AMD_HOST) {
+      std::memcpy(host[i], ts[i]->data, bytes[i]);
+      continue;
+    }
+    if (!pinned) OLA_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), 64, hipHostMallocDefault));
+    OLA_HIP(hipMemcpyAsync(pinned + 8 * i, ts[i]->data, bytes[i], hipMemcpyDeviceToHost, stream));
+    any_device = true;
+  }
+  if (!any_device) return;
+  OLA_HIP(hipStreamSynchronize(stream));
+  for (int i = 0; i < n; ++i)
+    if (ts[i] && ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], pinned + 8 * i, bytes[i]);
+}
+
+// An INT8 / UINT8 element's value from its byte.
+int32_t ByteInt(const onnxl_amd_tensor &t, uint8_t b) {
+  return t.data_type == kInt8 ? (int32_t)(int8_t)b : (int32_t)b;
+}
+
+// Two optional scalar zero points (null: absent, 0) read together.
+void ReadTwoZeroPoints(hipStream_t stream, const onnxl_amd_tensor *z0, const onnxl_amd_tensor *z1, int32_t &v0,
+                       int32_t &v1) {
+  const onnxl_amd_tensor *ts[2] = {z0, z1};
+  const size_t one[2] = {1, 1};
+  uint8_t host[2][8] = {};
+  ReadLeadingBytes(stream, 2, ts, one, host);
+  v0 = z0 ? ByteInt(*z0, host[0][0]) : 0;
+  v1 = z1 ? ByteInt(*z1, host[1][0]) : 0;
+}
+
 int32_t ReadIntElem(const onnxl_amd_tensor &t, int64_t idx) {
   uint8_t b = 0;
   ReadBytes(t, idx, &b, 1);
@@ -350,8 +390,11 @@ int MatMulInteger(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
   // (a_per_row = a_size > 1, :118-119).
   const bool a_vec = a_present && a_count > 1;
   const bool b_vec = b_present && b_count > 1;
-  p.alpha_scalar = ca - ((a_present && !a_vec && a_count == 1) ? ReadIntElem(*a_zp, 0) : 0);
-  p.beta_scalar = cb - ((b_present && !b_vec && b_count == 1) ? ReadIntElem(*b_zp, 0) : 0);
+  int32_t za = 0, zb = 0;
+  ReadTwoZeroPoints(stream, (a_present && !a_vec && a_count == 1) ? a_zp : nullptr,
+                    (b_present && !b_vec && b_count == 1) ? b_zp : nullptr, za, zb);
+  p.alpha_scalar = ca - za;
+  p.beta_scalar = cb - zb;
   p.need_cb = a_vec || p.alpha_scalar != 0;
   p.need_ra = b_vec || p.beta_scalar != 0;
   p.epilogue = kEpiInt32;
@@ -373,10 +416,7 @@ int MatMulInteger(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
 constexpr const char *kQlmName = "kernel::QLinearMatMul";
 
 // QLinearMatMul's six scalars at once: the reference's checks in its order
-// (:35-51), then every device-resident payload copied on the call's stream
-// into pinned host memory, with one synchronisation of that stream for all
-// of them (not one blocking copy per scalar, which also waits for the whole
-// device).
+// (:35-51), then one ReadLeadingBytes for all of them.
 struct QlmScalars {
   int32_t za, zb, zy;
   float as, bs, ys;
@@ -393,27 +433,13 @@ QlmScalars QReadScalars(const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b_
       throw InvalidArgument(Cat(kQlmName, ": '", names[i],
                                 "' must be a FLOAT or FLOAT16 scalar for the reference kernel."));
   }
-  static thread_local uint8_t *pinned = nullptr;  // 6 slots of 8 bytes, kept for the thread's life
+  const size_t bytes[6] = {1, 1, 1, ts[3]->data_type == kFloat ? 4u : 2u, ts[4]->data_type == kFloat ? 4u : 2u,
+                           ts[5]->data_type == kFloat ? 4u : 2u};
   uint8_t host[6][8] = {};
-  bool any_device = false;
-  for (int i = 0; i < 6; ++i) {
-    const size_t bytes = i < 3 ? 1 : (ts[i]->data_type == kFloat ? 4 : 2);
-    if (ts[i]->location == ONNXL_AMD_HOST) {
-      std::memcpy(host[i], ts[i]->data, bytes);
-      continue;
-    }
-    if (!pinned) OLA_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), 64, hipHostMallocDefault));
-    OLA_HIP(hipMemcpyAsync(pinned + 8 * i, ts[i]->data, bytes, hipMemcpyDeviceToHost, stream));
-    any_device = true;
-  }
-  if (any_device) {
-    OLA_HIP(hipStreamSynchronize(stream));
-    for (int i = 0; i < 6; ++i)
-      if (ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], pinned + 8 * i, 8);
-  }
+  ReadLeadingBytes(stream, 6, ts, bytes, host);
   QlmScalars r{};
   int32_t *zs[3] = {&r.za, &r.zb, &r.zy};
-  for (int i = 0; i < 3; ++i) *zs[i] = ts[i]->data_type == kInt8 ? (int32_t)(int8_t)host[i][0] : (int32_t)host[i][0];
+  for (int i = 0; i < 3; ++i) *zs[i] = ByteInt(*ts[i], host[i][0]);
   float *fs[3] = {&r.as, &r.bs, &r.ys};
   for (int i = 3; i < 6; ++i) {
     if (ts[i]->data_type == kFloat) {
@@ -955,8 +981,8 @@ int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnx
   const ConvGeom g = MakeConvGeom(*x, *w, r, attrs->group, kCiName);
   // :240-246: per-channel only for a 1-D zero point of length M
   const bool w_per_channel = wz_present && w_zp->rank == 1 && w_zp->dims[0] == M;
-  const int32_t xz = xz_present ? ReadIntElem(*x_zp, 0) : 0;
-  const int32_t wz = wz_present && !w_per_channel ? ReadIntElem(*w_zp, 0) : 0;
+  int32_t xz = 0, wz = 0;
+  ReadTwoZeroPoints(stream, xz_present ? x_zp : nullptr, wz_present && !w_per_channel ? w_zp : nullptr, xz, wz);
   const bool gemm = (g.G == 1 || !w_per_channel) && g.Kc > 0;
   const bool implicit = gemm && ConvImplicit(g, *y);
   const size_t col_bytes = implicit ? ConvImplicitScratch(g) : (gemm ? ConvColBytes(g) : 0);
