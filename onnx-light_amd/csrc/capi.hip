@@ -1012,18 +1012,6 @@ int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnx
   return ONNXL_AMD_OK;
 }
 
-float QcReadFloat(const onnxl_amd_tensor &t, int64_t idx) {  // ReadFloatElem, :47-51
-  OLA_ENFORCE(t.data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
-  float v;
-  ReadBytes(t, idx * 4, &v, 4);
-  return v;
-}
-
-int32_t QcReadScalarInt(const onnxl_amd_tensor &t, const char *name) {  // ReadScalarInt, :38-45
-  OLA_ENFORCE(NumElements(t) == 1, kQcName, ": '", name, "' must be a scalar.");
-  return ReadIntElem(t, 0);
-}
-
 int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, const onnxl_amd_tensor *x_zp,
                 const onnxl_amd_tensor *w, const onnxl_amd_tensor *w_scale, const onnxl_amd_tensor *w_zp,
                 const onnxl_amd_tensor *y_scale, const onnxl_amd_tensor *y_zp, const onnxl_amd_tensor *bias,
@@ -1043,11 +1031,22 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   OLA_ENFORCE(y->data_type == y_zp->data_type, kQcName, ": output dtype must match y_zero_point.");
   OLA_ENFORCE(ShapeOf(*y) == out_shape, kQcName, ": preallocated output shape mismatch.");
   OLA_ENFORCE(y->size_bytes == NumElements(out_shape), kQcName, ": preallocated output buffer has unexpected size.");
-  const int32_t xz = QcReadScalarInt(*x_zp, "x_zero_point");  // :200-205
-  const int32_t yz = QcReadScalarInt(*y_zp, "y_zero_point");
+  // :200-211 (ReadScalarInt :38-45, ReadFloatElem :47-51): the checks in
+  // the reference's order, then the four scalars read together
+  OLA_ENFORCE(NumElements(*x_zp) == 1, kQcName, ": 'x_zero_point' must be a scalar.");
+  OLA_ENFORCE(NumElements(*y_zp) == 1, kQcName, ": 'y_zero_point' must be a scalar.");
   OLA_ENFORCE(x_zp->data_type == x->data_type, kQcName, ": x_zero_point dtype must match x.");
   OLA_ENFORCE(w_zp->data_type == w->data_type, kQcName, ": w_zero_point dtype must match w.");
-  const float xs = QcReadFloat(*x_scale, 0), ys = QcReadFloat(*y_scale, 0);  // :207-211
+  OLA_ENFORCE(x_scale->data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
+  OLA_ENFORCE(y_scale->data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
+  const onnxl_amd_tensor *sts[4] = {x_zp, y_zp, x_scale, y_scale};
+  const size_t sbytes[4] = {1, 1, 4, 4};
+  uint8_t shost[4][8] = {};
+  ReadLeadingBytes(stream, 4, sts, sbytes, shost);
+  const int32_t xz = ByteInt(*x_zp, shost[0][0]), yz = ByteInt(*y_zp, shost[1][0]);
+  float xs, ys;
+  std::memcpy(&xs, shost[2], 4);
+  std::memcpy(&ys, shost[3], 4);
   OLA_ENFORCE(ys != 0.0f, kQcName, ": y_scale must be non-zero.");
   OLA_ENFORCE(NumElements(*x_scale) == 1 && NumElements(*y_scale) == 1, kQcName,
               ": 'x_scale' and 'y_scale' must be scalar.");
