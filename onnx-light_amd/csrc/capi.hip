@@ -271,28 +271,36 @@ private:
 
 bool IsInt8OrUint8(int32_t dt) { return dt == kInt8 || dt == kUint8; }
 
+// Pinned staging for ReadLeadingBytes: 8 slots of 8 bytes, allocated on first
+// use and freed by onnxl_amd_shutdown.  Every entry point runs under g_mu, so
+// one buffer serves all threads.
+uint8_t *g_pinned = nullptr;
+
 // The first bytes[i] (<= 8) bytes of each descriptor ts[i] (null: skipped)
 // into host[i]: host payloads directly, device ones by copies on `stream`
 // into pinned memory with one synchronisation of that stream for all of them
-// (not one blocking copy each, which also waits for the whole device).
+// (not one blocking copy each, which also waits for the whole device).  A
+// payload shorter than bytes[i] (an empty scalar the caller's checks reject
+// next) is not read: host[i] stays zero.  Caller holds g_mu.
 void ReadLeadingBytes(hipStream_t stream, int n, const onnxl_amd_tensor *const *ts, const size_t *bytes,
                       uint8_t (*host)[8]) {
-  static thread_local uint8_t *pinned = nullptr;  // 8 slots of 8 bytes, kept for the thread's life
   bool any_device = false;
+  auto readable = [&](int i) { return ts[i] && ts[i]->data && (size_t)ts[i]->size_bytes >= bytes[i]; };
   for (int i = 0; i < n; ++i) {
-    if (!ts[i]) continue;
+    std::memset(host[i], 0, 8);
+    if (!readable(i)) continue;
     if (ts[i]->location == ONNXL_AMD_HOST) {
       std::memcpy(host[i], ts[i]->data, bytes[i]);
       continue;
     }
-    if (!pinned) OLA_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), 64, hipHostMallocDefault));
-    OLA_HIP(hipMemcpyAsync(pinned + 8 * i, ts[i]->data, bytes[i], hipMemcpyDeviceToHost, stream));
+    if (!g_pinned) OLA_HIP(hipHostMalloc(reinterpret_cast<void **>(&g_pinned), 64, hipHostMallocDefault));
+    OLA_HIP(hipMemcpyAsync(g_pinned + 8 * i, ts[i]->data, bytes[i], hipMemcpyDeviceToHost, stream));
     any_device = true;
   }
   if (!any_device) return;
   OLA_HIP(hipStreamSynchronize(stream));
   for (int i = 0; i < n; ++i)
-    if (ts[i] && ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], pinned + 8 * i, bytes[i]);
+    if (readable(i) && ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], g_pinned + 8 * i, bytes[i]);
 }
 
 // An INT8 / UINT8 element's value from its byte.
@@ -309,12 +317,6 @@ void ReadTwoZeroPoints(hipStream_t stream, const onnxl_amd_tensor *z0, const onn
   ReadLeadingBytes(stream, 2, ts, one, host);
   v0 = z0 ? ByteInt(*z0, host[0][0]) : 0;
   v1 = z1 ? ByteInt(*z1, host[1][0]) : 0;
-}
-
-int32_t ReadIntElem(const onnxl_amd_tensor &t, int64_t idx) {
-  uint8_t b = 0;
-  ReadBytes(t, idx, &b, 1);
-  return t.data_type == kInt8 ? (int32_t)(int8_t)b : (int32_t)b;
 }
 
 float HalfBitsToFloat(uint16_t h) {
@@ -1039,10 +1041,13 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   OLA_ENFORCE(w_zp->data_type == w->data_type, kQcName, ": w_zero_point dtype must match w.");
   OLA_ENFORCE(x_scale->data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
   OLA_ENFORCE(y_scale->data_type == kFloat, kQcName, ": scale must be FLOAT for the reference kernel.");
-  const onnxl_amd_tensor *sts[4] = {x_zp, y_zp, x_scale, y_scale};
-  const size_t sbytes[4] = {1, 1, 4, 4};
-  uint8_t shost[4][8] = {};
-  ReadLeadingBytes(stream, 4, sts, sbytes, shost);
+  // a scalar w_zero_point rides in the same batch (one synchronisation);
+  // per-channel ones are read by the kernels
+  const bool w_zp_scalar = !(NumElements(*w_zp) == w->dims[0] && w->dims[0] > 1);
+  const onnxl_amd_tensor *sts[5] = {x_zp, y_zp, x_scale, y_scale, w_zp_scalar ? w_zp : nullptr};
+  const size_t sbytes[5] = {1, 1, 4, 4, 1};
+  uint8_t shost[5][8] = {};
+  ReadLeadingBytes(stream, 5, sts, sbytes, shost);
   const int32_t xz = ByteInt(*x_zp, shost[0][0]), yz = ByteInt(*y_zp, shost[1][0]);
   float xs, ys;
   std::memcpy(&xs, shost[2], 4);
@@ -1062,7 +1067,7 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   }
   const ConvGeom g = MakeConvGeom(*x, *w, r, attrs->group, kQcName);
   const bool w_per_channel = wz_n == M && M > 1;
-  const int32_t wz = w_per_channel ? 0 : ReadIntElem(*w_zp, 0);
+  const int32_t wz = w_per_channel ? 0 : ByteInt(*w_zp, shost[4][0]);
   // The reference accumulates in int64 (:306-330).  The GEMM's int32 sums are
   // exact while Kc * max|x - x_zp| * max|w - w_zp| < 2^31; the bias is added
   // in int64 afterwards.  Otherwise, and for grouped convolutions with
@@ -2077,6 +2082,10 @@ int onnxl_amd_shutdown(void) {
     (void)hipSetDevice(g_ctx.device);
     (void)hipDeviceSynchronize();
     g_ctx.ws.Release();
+  }
+  if (g_pinned) {
+    (void)hipHostFree(g_pinned);
+    g_pinned = nullptr;
   }
   g_init.store(false);
   return ONNXL_AMD_OK;

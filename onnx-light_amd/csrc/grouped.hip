@@ -106,24 +106,31 @@ __device__ __forceinline__ uint16_t Enc(float f, bool bf16) {
   return (uint16_t)(u >> 16);
 }
 
-// One thread per output element: block b covers columns 256 (b % nb) ..
-// of pair b / nb, nb = ceil(N / 256).
+// One thread per output element: work item b covers columns 256 (b % nb) ..
+// of pair b / nb, nb = ceil(N / 256); a grid of at most kSimpleMaxBlocks
+// workgroups strides over the nb * pairs items, so any shape fits the grid.
+constexpr int64_t kSimpleMaxBlocks = int64_t(1) << 20;
+
 __global__ __launch_bounds__(256) void GroupedSimpleKernel(const GroupedParams p) {
   const int64_t nb = (p.N + 255) / 256;
-  const int64_t i = (int64_t)blockIdx.x / nb;  // pair
-  const int64_t n = ((int64_t)blockIdx.x % nb) * 256 + threadIdx.x;
-  if (n >= p.N) return;
-  const int64_t g = GroupOf(p.idx, p.idx64, i);
-  if (g < 0 || g >= p.G) return;  // NaN row written by the routing kernel
-  const uint16_t *x = static_cast<const uint16_t *>(p.A) + (i / p.S) * p.K;
-  const uint16_t *w = static_cast<const uint16_t *>(p.W) + g * p.K * p.N;
-  float v = 0.f;
-  for (int64_t l = 0; l < p.K; ++l) {
-    const uint16_t wb = p.transB ? w[n * p.K + l] : w[l * p.N + n];
-    v = __fadd_rn(v, __fmul_rn(Dec(x[l], p.bf16), Dec(wb, p.bf16)));  // in order, no contraction
+  const int64_t items = nb * p.M * p.S;
+  for (int64_t b = blockIdx.x; b < items; b += gridDim.x) {
+    const int64_t i = b / nb;  // pair
+    const int64_t n = (b % nb) * 256 + threadIdx.x;
+    if (n >= p.N) continue;
+    const int64_t g = GroupOf(p.idx, p.idx64, i);
+    if (g < 0 || g >= p.G) continue;  // NaN row written by the routing kernel
+    const uint16_t *x = static_cast<const uint16_t *>(p.A) + (i / p.S) * p.K;
+    const uint16_t *w = static_cast<const uint16_t *>(p.W) + g * p.K * p.N;
+    float v = 0.f;
+    for (int64_t l = 0; l < p.K; ++l) {
+      const uint16_t wb = p.transB ? w[n * p.K + l] : w[l * p.N + n];
+      v = __fadd_rn(v, __fmul_rn(Dec(x[l], p.bf16), Dec(wb, p.bf16)));  // in order, no contraction
+    }
+    if (p.bias)
+      v = __fadd_rn(Dec(Enc(v, p.bf16), p.bf16), Dec(static_cast<const uint16_t *>(p.bias)[g * p.N + n], p.bf16));
+    static_cast<uint16_t *>(p.Y)[i * p.N + n] = Enc(v, p.bf16);
   }
-  if (p.bias) v = __fadd_rn(Dec(Enc(v, p.bf16), p.bf16), Dec(static_cast<const uint16_t *>(p.bias)[g * p.N + n], p.bf16));
-  static_cast<uint16_t *>(p.Y)[i * p.N + n] = Enc(v, p.bf16);
 }
 
 }  // namespace
@@ -152,7 +159,9 @@ void LaunchGroupedMatMul(const GroupedParams &p, hipStream_t stream) {
   if (P == 0 || p.N == 0) return;
   hipLaunchKernelGGL(GroupRouteKernel, dim3(1), dim3(kRouteThreads), GroupedRouteLds(p.G), stream, p);
   if (p.K == 0 || !GroupedCoreEligible(p)) {
-    hipLaunchKernelGGL(GroupedSimpleKernel, dim3((unsigned)((p.N + 255) / 256 * P)), dim3(256), 0, stream, p);
+    const int64_t items = (p.N + 255) / 256 * P;
+    hipLaunchKernelGGL(GroupedSimpleKernel, dim3((unsigned)std::min(items, kSimpleMaxBlocks)), dim3(256), 0, stream,
+                       p);
     return;
   }
   mg::GemmArgs g{};

@@ -254,6 +254,36 @@ def test_qlinear_past_int32_exact(olamd, oracle, dev, shapes, centred):
         assert len(np.unique(ref)) > 10
 
 
+@pytest.mark.parametrize("a_shape,b_shape", [((6, 45000), (45000, 40)), ((45000,), (45000, 24)),
+                                             ((7, 45000), (45000,))])
+def test_qlinear_past_int32_signed_and_1d(olamd, oracle, dev, a_shape, b_shape):
+    """The int64-accumulating kernel with INT8 a and b, zero points away from
+    0 and an INT8 output (the signed clamp and narrowing), and with 1-D
+    operands: K * max|a - za| * max|b - zb| = 45000 * 228 * 217 > 2^31, and
+    the first row / column pair sums to -45000 * 228 * 217, which a wrapped
+    int32 sum would make positive."""
+    rng = np.random.default_rng(zlib.crc32(repr((a_shape, b_shape)).encode()))
+    a = rng.integers(-128, 128, a_shape).astype(np.int8)
+    b = rng.integers(-128, 128, b_shape).astype(np.int8)
+    za, zb, zy = 100, -90, -20
+    a.reshape(-1, a_shape[-1])[0] = -128
+    (b if b.ndim == 1 else b[:, 0])[...] = 127
+    a2 = a.reshape(-1, a_shape[-1]).astype(np.int64) - za
+    b2 = (b.reshape(-1, 1) if b.ndim == 1 else b).astype(np.int64) - zb
+    acc = a2 @ b2
+    assert acc[0, 0] == -45000 * 228 * 217 and acc[0, 0] < -2 ** 31
+    a_s, b_s = np.float32(0.02), np.float32(0.01)
+    y_s = np.float32(a_s * b_s * (float(np.abs(acc).max()) / 100 + 1.0))
+    args = (T(a, dev), T(np.array(a_s), dev), T(np.array(za, np.int8), dev), T(b, dev),
+            T(np.array(b_s), dev), T(np.array(zb, np.int8), dev), T(np.array(y_s), dev),
+            T(np.array(zy, np.int8), dev))
+    y = olamd.qlinear_matmul(*args).cpu().numpy()
+    ref = oracle.qlinear_matmul(a, a_s, za, b, b_s, zb, y_s, zy, y_dtype=oracle.INT8)
+    assert y.dtype == np.int8 and y.shape == ref.shape
+    assert np.array_equal(y, ref)
+    assert ref.reshape(-1)[0] == ref.min() < -100  # the sum past int32 is the most negative output
+
+
 def test_qlinear_scalars_host_device_mixed(olamd, oracle, dev):
     """The six scalars read in one pass: device-resident ones copied on the
     call's stream with one synchronisation, host ones read directly; every
