@@ -87,18 +87,31 @@ class Workload:
         self.calls[i % len(self.calls)]()
 
 
-def make_c2(olamd, dev):
+def make_c2(olamd, dev, k_depth=0):
+    """Configuration 2.  `k_depth` > 0 replaces K = 4096 by that depth (the
+    same distributions, drawn on the GPU): the K sweep that splits the GEMM's
+    time into a per-K-step and a fixed per-launch part."""
     import importlib
+    import torch
     syn = importlib.import_module("onnx_light_amd.synth")
-    x = syn.config_inputs(2)
-    w = Workload()
-    w.name = "C2 QLinearMatMul prefill u8[2048,4096] x s8[4096,4096] -> u8[2048,4096] (a_zp=128, b_zp=0, y_zp=128)"
-    w.key, w.unit, w.dtype, w.bound = "c2", "TOPS", "int8", "mfma"
     M, K, N = 2048, 4096, 4096
+    w = Workload()
+    w.key, w.unit, w.dtype, w.bound = "c2", "TOPS", "int8", "mfma"
+    if k_depth:
+        K = k_depth
+        x = syn.config_inputs(2, scale=1 / 2048)  # the scalars
+        g = torch.Generator(device=dev)
+        g.manual_seed(K)
+        a = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=g)
+        b = torch.randint(-128, 128, (K, N), dtype=torch.int8, device=dev, generator=g)
+        w.name = (f"C2 shape at K = {K}: QLinearMatMul u8[2048,{K}] x s8[{K},4096] -> u8[2048,4096] "
+                  f"(a_zp=128, b_zp=0, y_zp=128)")
+    else:
+        x = syn.config_inputs(2)
+        a, b = _t(x["a"], dev), _t(x["b"], dev)
+        w.name = "C2 QLinearMatMul prefill u8[2048,4096] x s8[4096,4096] -> u8[2048,4096] (a_zp=128, b_zp=0, y_zp=128)"
     w.work = 2.0 * M * N * K
     w.nbytes = M * K + K * N + M * N
-    a, b = _t(x["a"], dev), _t(x["b"], dev)
-    import torch
     y = torch.empty((M, N), dtype=torch.uint8, device=dev)
     w.calls = [olamd.prepare("qlinear_matmul", a, x["a_scale"], x["a_zp"], b, x["b_scale"], x["b_zp"],
                              x["y_scale"], x["y_zp"], y)]
@@ -669,7 +682,14 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--replicas", type=int, default=0,
                     help="buffer replicas for HBM-bound configs (0 = enough to exceed 512 MB)")
+    ap.add_argument("--k", type=int, default=0,
+                    help="c2 only: time the configuration-2 shape at this K instead of 4096 (the K sweep "
+                         "behind the per-K-step / per-launch cost split; implies --no-extra, no CPU baseline)")
     args = ap.parse_args()
+    if args.k:
+        if args.workload != "c2" or args.k % 64:
+            ap.error("--k applies to --workload c2 with K a multiple of 64")
+        args.extra, args.no_cpu_baseline = False, True
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the quantized-matmul kernels "
                                    "are single-device (see DESIGN.md for how they would shard)",
@@ -683,7 +703,7 @@ def main():
 
     def build(key):
         if key == "c2":
-            return make_c2(olamd, dev)
+            return make_c2(olamd, dev, args.k if key == args.workload else 0)
         if key == "c3":
             return make_c3(olamd, dev, args.replicas or 24)
         if key == "c3_onnx_layout":

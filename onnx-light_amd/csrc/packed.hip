@@ -13,6 +13,10 @@
 #include "device_codecs.hpp"
 #include "kernels.hpp"
 
+// The lattice grids of the IQ profiles, in constant memory (33 KB).
+#define GGUF_CODEBOOK_QUAL static __constant__ const
+#include "gguf_codebooks.h"
+
 // d * q + m is two roundings in the reference (each step forced through a
 // volatile fp32): no multiply-add may be fused in this file.  The operators
 // are written out here, under the pragma; __fmul_rn / __fadd_rn come from a
@@ -295,6 +299,125 @@ __global__ __launch_bounds__(kPkThreads) void DequantPackedXKernel(const uint8_t
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = DecodeX<TYPE>(p, i0 + e);
   StoreEight<OUT>(y, b * kV + i0, v, vec != 0);  // thread t writes values 8t .. 8t + 7
+}
+
+// ---------------------------------------------------------------------------
+// The codebook profiles (dequantize_packed.cc:84-170): iq2_xxs, iq2_xs,
+// iq2_s, iq3_xxs, iq3_s, iq1_s, iq1_m.  A 256-value block is 32 octets; a
+// thread decodes octet o = 4 g + l of one block (values 8 o .. 8 o + 7):
+// grid row(s) from gguf_codebooks.h, one sign bit per value (7 bits completed
+// to even parity for iq2_xxs / iq2_xs / iq3_xxs), a per-octet scale; every
+// fp32 product and sum rounded on its own, with the x86-64 NaN results.
+// Field positions are those of the oracle's pk_decode_iq.
+template <int TYPE> struct IqLayout;
+template <> struct IqLayout<16> { static constexpr int bytes = 66; };   // iq2_xxs
+template <> struct IqLayout<17> { static constexpr int bytes = 74; };   // iq2_xs
+template <> struct IqLayout<22> { static constexpr int bytes = 82; };   // iq2_s
+template <> struct IqLayout<18> { static constexpr int bytes = 98; };   // iq3_xxs
+template <> struct IqLayout<21> { static constexpr int bytes = 110; };  // iq3_s
+template <> struct IqLayout<19> { static constexpr int bytes = 50; };   // iq1_s
+template <> struct IqLayout<29> { static constexpr int bytes = 56; };   // iq1_m
+
+__device__ __forceinline__ uint32_t U16At(const uint8_t *p) { return (uint32_t)p[0] | (uint32_t)p[1] << 8; }
+__device__ __forceinline__ uint32_t U32At(const uint8_t *p) { return U16At(p) | U16At(p + 2) << 16; }
+// +-1 for sign bit j; `parity`: 7 stored bits, the eighth makes the count even
+__device__ __forceinline__ float SignBit(uint32_t bits, int j, bool parity) {
+  if (parity) bits |= (uint32_t)(__builtin_popcount(bits) & 1) << 7;
+  return (bits >> j) & 1u ? -1.f : 1.f;
+}
+// lane j of a grid row (one signed byte per lane)
+__device__ __forceinline__ float Lane(uint64_t row, int j) { return (float)(int8_t)(uint8_t)(row >> (8 * j)); }
+
+template <int TYPE> __device__ __forceinline__ void DecodeIq8(const uint8_t *p, int o, float v[8]) {
+  const int g = o >> 2, l = o & 3;
+  if constexpr (TYPE == 16 || TYPE == 17 || TYPE == 22) {
+    uint32_t index, signs;
+    float s;
+    if constexpr (TYPE == 16) {
+      const uint32_t w = U32At(p + 6 + 8 * g);
+      index = p[2 + 8 * g + l];
+      signs = (w >> (7 * l)) & 127u;
+      s = (float)(w >> 28);
+    } else if constexpr (TYPE == 17) {
+      const uint32_t w = U16At(p + 2 + 2 * o);
+      index = w & 511u;
+      signs = w >> 9;
+      s = (float)((p[66 + g] >> (4 * (l >> 1))) & 15);
+    } else {
+      index = p[2 + o] | (((uint32_t)p[66 + g] >> (2 * l)) & 3u) << 8;
+      signs = p[34 + o];
+      s = (float)((p[74 + g] >> (4 * (l >> 1))) & 15);
+    }
+    const float scale = SseMul(SseMul(Half2(p), 0.5f + s), 0.25f);
+    const uint64_t row = TYPE == 16 ? kGgufIq2xxs[index] : (TYPE == 17 ? kGgufIq2xs[index] : kGgufIq2s[index]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = SseMul(SseMul(scale, Lane(row, j)), SignBit(signs, j, TYPE != 22));
+  } else if constexpr (TYPE == 18 || TYPE == 21) {
+    uint32_t signs;
+    float scale;
+    if constexpr (TYPE == 18) {
+      const uint32_t w = U32At(p + 66 + 4 * g);
+      signs = (w >> (7 * l)) & 127u;
+      scale = SseMul(SseMul(Half2(p), 0.5f + (float)(w >> 28)), 0.5f);
+    } else {
+      signs = p[74 + o];
+      scale = SseMul(Half2(p), (float)(1 + 2 * ((p[106 + (g >> 1)] >> (4 * (g & 1))) & 15)));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t index = p[2 + 2 * o + h];
+      if constexpr (TYPE == 21) index |= (((uint32_t)p[66 + g] >> (2 * l + h)) & 1u) << 8;
+      const uint64_t row = TYPE == 18 ? kGgufIq3xxs[index] : kGgufIq3s[index];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[4 * h + j] = SseMul(SseMul(scale, Lane(row, j)), SignBit(signs, 4 * h + j, TYPE == 18));
+    }
+  } else {  // iq1_s, iq1_m
+    uint32_t index;
+    int mult;
+    float d, delta;
+    if constexpr (TYPE == 19) {
+      const uint32_t h = U16At(p + 34 + 2 * g);
+      d = Half2(p);
+      index = p[2 + o] | ((h >> (3 * l)) & 7u) << 8;
+      mult = 2 * (int)((h >> 12) & 7u) + 1;
+      delta = h & 0x8000u ? -0.125f : 0.125f;
+    } else {
+      const uint32_t w0 = U16At(p + 48), w1 = U16At(p + 50), w2 = U16At(p + 52), w3 = U16At(p + 54);
+      d = F16ToF32((uint16_t)((w0 >> 12) | (w1 >> 12) << 4 | (w2 >> 12) << 8 | (w3 >> 12) << 12));
+      const uint32_t nib = (p[32 + (o >> 1)] >> (4 * (o & 1))) & 15u;
+      index = p[o] | (nib & 7u) << 8;
+      const uint32_t ws = (g >> 1) == 0 ? w0 : (g >> 1) == 1 ? w1 : (g >> 1) == 2 ? w2 : w3;
+      mult = 2 * (int)((ws >> (6 * (g & 1) + 3 * (l >> 1))) & 7u) + 1;
+      delta = nib & 8u ? -0.125f : 0.125f;
+    }
+    const float scale = SseMul(d, (float)mult);
+    const uint64_t row = kGgufIq1s[index];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = SseMul(scale, Lane(row, j) + delta);
+  }
+}
+
+template <int TYPE, int OUT>
+__global__ __launch_bounds__(kPkThreads) void DequantPackedIqKernel(const uint8_t *__restrict__ x, int64_t nblocks,
+                                                                    void *__restrict__ y, int vec) {
+  const int64_t t = (int64_t)blockIdx.x * kPkThreads + threadIdx.x;
+  if (t >= nblocks * 32) return;
+  const int64_t b = t >> 5;
+  const int o = (int)(t & 31);
+  float v[8];
+  DecodeIq8<TYPE>(x + b * IqLayout<TYPE>::bytes, o, v);
+  StoreEight<OUT>(y, b * 256 + 8 * o, v, vec != 0);  // thread t writes values 8t .. 8t + 7
+}
+
+template <int TYPE> void LaunchPkIqOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
+  const dim3 g((unsigned)((nblocks * 32 + kPkThreads - 1) / kPkThreads));
+  switch (out) {
+  case kFloat: hipLaunchKernelGGL((DequantPackedIqKernel<TYPE, kFloat>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kFloat16: hipLaunchKernelGGL((DequantPackedIqKernel<TYPE, kFloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  case kBfloat16: hipLaunchKernelGGL((DequantPackedIqKernel<TYPE, kBfloat16>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  default: hipLaunchKernelGGL((DequantPackedIqKernel<TYPE, kDouble>), g, dim3(kPkThreads), 0, s, x, nblocks, y, vec); break;
+  }
 }
 
 template <int TYPE> void LaunchPkXOut(const uint8_t *x, int64_t nblocks, int out, void *y, int vec, hipStream_t s) {
@@ -814,9 +937,10 @@ bool PackedFormatOnGpu(int ggml_type) {
   switch (ggml_type) {
   case 2: case 3: case 6: case 7: case 8: case 9: case 20: case 12: case 14:
   case 10: case 11: case 13: case 15: case 23: case 34: case 35: case 39: case 40: case 41: case 42:
+  case 16: case 17: case 18: case 19: case 21: case 22: case 29:
     return true;
   default:
-    return false;  // the codebook formats (iq1, iq2, iq3)
+    return false;
   }
 }
 
@@ -845,6 +969,13 @@ void LaunchDequantizePacked(int ggml_type, const uint8_t *x, int64_t nblocks, in
   case 40: LaunchPkXOut<40>(x, nblocks, out_dtype, y, vec, s); break;
   case 41: LaunchPkXOut<41>(x, nblocks, out_dtype, y, vec, s); break;
   case 42: LaunchPkXOut<42>(x, nblocks, out_dtype, y, vec, s); break;
+  case 16: LaunchPkIqOut<16>(x, nblocks, out_dtype, y, vec, s); break;
+  case 17: LaunchPkIqOut<17>(x, nblocks, out_dtype, y, vec, s); break;
+  case 18: LaunchPkIqOut<18>(x, nblocks, out_dtype, y, vec, s); break;
+  case 19: LaunchPkIqOut<19>(x, nblocks, out_dtype, y, vec, s); break;
+  case 21: LaunchPkIqOut<21>(x, nblocks, out_dtype, y, vec, s); break;
+  case 22: LaunchPkIqOut<22>(x, nblocks, out_dtype, y, vec, s); break;
+  case 29: LaunchPkIqOut<29>(x, nblocks, out_dtype, y, vec, s); break;
   default: throw Unsupported("DequantizePacked: no GPU kernel for this format");
   }
 }

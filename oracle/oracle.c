@@ -8,6 +8,7 @@
  * a baseline x86-64 build of the reference (CMakeLists.txt adds no -march).
  */
 #include "oracle.h"
+#include "../onnx-light_amd/csrc/gguf_codebooks.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -836,6 +837,13 @@ int orc_packed_block_bytes(int ggml_type) {
   case 40: return 36;  /* nvfp4 */
   case 41: return 18;  /* q1_0 */
   case 42: return 18;  /* q2_0 */
+  case 16: return 66;  /* iq2_xxs */
+  case 17: return 74;  /* iq2_xs */
+  case 22: return 82;  /* iq2_s */
+  case 18: return 98;  /* iq3_xxs */
+  case 21: return 110; /* iq3_s */
+  case 19: return 50;  /* iq1_s */
+  case 29: return 56;  /* iq1_m */
   default: return 0;
   }
 }
@@ -979,9 +987,140 @@ static void pk_decode_ext(int t, const uint8_t *p, float *out) {
   }
 }
 
+/* The codebook profiles (dequantize_packed.cc:84-170, profile table :27-36;
+ * the lattice grids of ggml src/ggml-common.h, in gguf_codebooks.h).  A
+ * 256-value block is 32 octets: octet o = 4 g + l (g the 32-value group, l its
+ * lane) holds values 8 o .. 8 o + 7, lane j of one grid row (8-value rows;
+ * the iq3 grids have 4-value rows, two per octet), each value signed by one
+ * sign bit and scaled.
+ *  iq2_xxs (66 B): fp16 d; group g's 8 bytes at 2 + 8 g: four index bytes
+ *    (lane l), then a 32-bit word w: lane l's 7 sign bits at 7 l, completed to
+ *    even parity by an eighth, and scale (d * (0.5 + (w >> 28))) * 0.25;
+ *  iq2_xs (74 B): fp16 d; a 16-bit word per octet at 2 + 2 o: 9-bit index,
+ *    7 sign bits (parity as above); scale (d * (0.5 + s)) * 0.25, s nibble
+ *    l / 2 of byte 66 + g;
+ *  iq2_s (82 B): fp16 d; index byte 2 + o with bits 2 l .. 2 l + 1 of byte
+ *    66 + g above it; 8 sign bits at 34 + o; s nibble l / 2 of byte 74 + g;
+ *  iq3_xxs (98 B): fp16 d; two index bytes per octet at 2 + 2 o (4-value
+ *    rows); group word at 66 + 4 g: signs as iq2_xxs, scale
+ *    (d * (0.5 + (w >> 28))) * 0.5;
+ *  iq3_s (110 B): fp16 d; index bytes 2 + 2 o, 2 o + 3, each with a ninth bit
+ *    (bit 2 l + half of byte 66 + g); 8 sign bits at 74 + o; scale
+ *    d * (1 + 2 s), s nibble g % 2 of byte 106 + g / 2;
+ *  iq1_s (50 B): fp16 d; index byte 2 + o with 3 bits (3 l) of the 16-bit word
+ *    h at 34 + 2 g above it; value (d * (2 s + 1)) * (grid + delta), s bits
+ *    12-14 of h, delta -0.125 when bit 15 of h is set, else 0.125;
+ *  iq1_m (56 B): index byte o with the low 3 bits of nibble o % 2 of byte
+ *    32 + o / 2 above it, that nibble's bit 3 the sign of delta; d the fp16
+ *    made of the top nibbles of the four 16-bit words at 48 (word j: bits
+ *    4 j .. 4 j + 3); s the 3-bit field 6 (g % 2) + 3 (l / 2) of word g / 2.
+ * Sign bits only flip the sign (a multiply by +-1); every other fp32 product
+ * and sum is rounded on its own. */
+static float pk_add(float a, float b) { volatile float r = a + b; return r; }
+
+static int pk_u16(const uint8_t *p) { return p[0] | (p[1] << 8); }
+static uint32_t pk_u32(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+/* +-1 for bit j of 7 sign bits completed to even parity (or 8 given bits) */
+static float pk_sign(uint32_t bits, int j, int parity) {
+  if (parity) {
+    uint32_t c = bits, n = 0;
+    while (c) { n += c & 1u; c >>= 1; }
+    bits |= (n & 1u) << 7;
+  }
+  return (bits >> j) & 1u ? -1.0f : 1.0f;
+}
+static int pk_lane8(uint64_t row, int j) { return (int)(int8_t)(uint8_t)(row >> (8 * j)); }
+static int pk_lane4(uint32_t row, int j) { return (int)(int8_t)(uint8_t)(row >> (8 * j)); }
+
+static void pk_decode_iq(int t, const uint8_t *p, float *out) {
+  float d = orc_f16_to_f32((uint16_t)pk_u16(p));
+  int words[4] = {0, 0, 0, 0};
+  if (t == 29) {
+    int bits = 0;
+    for (int j = 0; j < 4; ++j) {
+      words[j] = pk_u16(p + 48 + 2 * j);
+      bits |= (words[j] >> 12) << (4 * j);
+    }
+    d = orc_f16_to_f32((uint16_t)bits);
+  }
+  for (int o = 0; o < 32; ++o) {
+    const int g = o / 4, l = o % 4;
+    float *v = out + 8 * o;
+    if (t == 16 || t == 17 || t == 22) {
+      int index;
+      uint32_t signs;
+      int parity = 1;
+      float s;
+      if (t == 16) {
+        const uint32_t w = pk_u32(p + 6 + 8 * g);
+        index = p[2 + 8 * g + l];
+        signs = (w >> (7 * l)) & 127u;
+        s = (float)(w >> 28);
+      } else if (t == 17) {
+        const int w = pk_u16(p + 2 + 2 * o);
+        index = w & 511;
+        signs = (uint32_t)(w >> 9);
+        s = (float)((p[66 + g] >> (4 * (l / 2))) & 15);
+      } else {
+        index = p[2 + o] | (((p[66 + g] >> (2 * l)) & 3) << 8);
+        signs = p[34 + o];
+        parity = 0;
+        s = (float)((p[74 + g] >> (4 * (l / 2))) & 15);
+      }
+      const float scale = pk_mul(pk_mul(d, 0.5f + s), 0.25f);
+      const uint64_t row = t == 16 ? kGgufIq2xxs[index] : t == 17 ? kGgufIq2xs[index] : kGgufIq2s[index];
+      for (int j = 0; j < 8; ++j) v[j] = pk_mul(pk_mul(scale, (float)pk_lane8(row, j)), pk_sign(signs, j, parity));
+    } else if (t == 18 || t == 21) {
+      uint32_t signs;
+      int parity;
+      float scale;
+      if (t == 18) {
+        const uint32_t w = pk_u32(p + 66 + 4 * g);
+        signs = (w >> (7 * l)) & 127u;
+        parity = 1;
+        scale = pk_mul(pk_mul(d, 0.5f + (float)(w >> 28)), 0.5f);
+      } else {
+        signs = p[74 + o];
+        parity = 0;
+        scale = pk_mul(d, (float)(1 + 2 * ((p[106 + g / 2] >> (4 * (g % 2))) & 15)));
+      }
+      for (int half = 0; half < 2; ++half) {
+        int index = p[2 + 2 * o + half];
+        if (t == 21) index |= ((p[66 + g] >> (2 * l + half)) & 1) << 8;
+        const uint32_t row = t == 18 ? kGgufIq3xxs[index] : kGgufIq3s[index];
+        for (int j = 0; j < 4; ++j)
+          v[4 * half + j] = pk_mul(pk_mul(scale, (float)pk_lane4(row, j)), pk_sign(signs, 4 * half + j, parity));
+      }
+    } else {
+      int index, mult;
+      float delta;
+      if (t == 19) {
+        const int h = pk_u16(p + 34 + 2 * g);
+        index = p[2 + o] | (((h >> (3 * l)) & 7) << 8);
+        mult = 2 * ((h >> 12) & 7) + 1;
+        delta = h & 0x8000 ? -0.125f : 0.125f;
+      } else {
+        const int nib = (p[32 + o / 2] >> (4 * (o % 2))) & 15;
+        index = p[o] | ((nib & 7) << 8);
+        mult = 2 * ((words[g / 2] >> (6 * (g % 2) + 3 * (l / 2))) & 7) + 1;
+        delta = nib & 8 ? -0.125f : 0.125f;
+      }
+      const float scale = pk_mul(d, (float)mult);
+      for (int j = 0; j < 8; ++j) v[j] = pk_mul(scale, pk_add((float)pk_lane8(kGgufIq1s[index], j), delta));
+    }
+  }
+}
+
 int orc_dequantize_packed(int ggml_type, const uint8_t *x, int64_t nblocks, float *out) {
   const int bytes = orc_packed_block_bytes(ggml_type);
   if (!bytes) return 1;
+  if (ggml_type == 16 || ggml_type == 17 || ggml_type == 18 || ggml_type == 19 || ggml_type == 21 ||
+      ggml_type == 22 || ggml_type == 29) {
+    for (int64_t b = 0; b < nblocks; ++b, x += bytes, out += 256) pk_decode_iq(ggml_type, x, out);
+    return 0;
+  }
   const int ext = ggml_type == 10 || ggml_type == 11 || ggml_type == 13 || ggml_type == 15 || ggml_type == 23 ||
                   (ggml_type >= 34 && ggml_type <= 42);
   if (ext) {

@@ -477,7 +477,8 @@ GGUF_TYPES = {"gguf:q4_0": 2, "gguf:q4_1": 3, "gguf:q5_0": 6, "gguf:q5_1": 7, "g
               "gguf:q8_1": 9, "gguf:iq4_nl": 20, "gguf:q4_k": 12, "gguf:q6_k": 14,
               "gguf:q2_k": 10, "gguf:q3_k": 11, "gguf:q5_k": 13, "gguf:q8_k": 15, "gguf:iq4_xs": 23,
               "gguf:tq1_0": 34, "gguf:tq2_0": 35, "gguf:mxfp4": 39, "gguf:nvfp4": 40, "gguf:q1_0": 41,
-              "gguf:q2_0": 42}
+              "gguf:q2_0": 42, "gguf:iq2_xxs": 16, "gguf:iq2_xs": 17, "gguf:iq3_xxs": 18, "gguf:iq1_s": 19,
+              "gguf:iq3_s": 21, "gguf:iq2_s": 22, "gguf:iq1_m": 29}
 
 
 def packed_block_bytes(fmt: str) -> int:

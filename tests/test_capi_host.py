@@ -365,9 +365,14 @@ def test_dequantize_packed_validation(olamd):
         assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
     rc, _ = run()
     assert rc == olamd.NOT_INITIALIZED
-    # a format of the reference with no GPU kernel here (a codebook format)
-    rc, _ = run(x=np.zeros(66, np.uint8), fmt=b"gguf:iq2_xxs", shape=(256,), y=np.zeros(256, np.float32))
-    assert rc == olamd.UNSUPPORTED
+    # the codebook profiles pass validation as the others do (the device work
+    # then needs onnxl_amd_init)
+    for fmt, size in ((b"gguf:iq2_xxs", 66), (b"gguf:iq2_xs", 74), (b"gguf:iq2_s", 82), (b"gguf:iq3_xxs", 98),
+                      (b"gguf:iq3_s", 110), (b"gguf:iq1_s", 50), (b"gguf:iq1_m", 56)):
+        rc, _ = run(x=np.zeros(size, np.uint8), fmt=fmt, shape=(256,), y=np.zeros(256, np.float32))
+        assert rc == olamd.NOT_INITIALIZED, fmt
+        rc, err = run(x=np.zeros(size + 1, np.uint8), fmt=fmt, shape=(256,), y=np.zeros(256, np.float32))
+        assert rc == olamd.INVALID_ARGUMENT and "packed input length must match exactly." in err, fmt
 
 
 def test_awq_validation(olamd):

@@ -1,6 +1,7 @@
-"""GPU parity of DequantizePacked for the GGUF profiles without codebooks against
-the oracle: bit-exact in all four output dtypes (FLOAT, FLOAT16, BFLOAT16,
-DOUBLE).  The reference test's corpus is checked against its GGML-C hashes
+"""GPU parity of DequantizePacked for all 27 GGUF profiles (the codebook
+profiles iq2_xxs, iq2_xs, iq2_s, iq3_xxs, iq3_s, iq1_s and iq1_m included)
+against the oracle: bit-exact in all four output dtypes (FLOAT, FLOAT16,
+BFLOAT16, DOUBLE).  The reference test's corpus is checked against its GGML-C hashes
 through the GPU too; random blocks include NaN, infinite, subnormal and
 maximal fp16 scales; outputs at unaligned addresses take the per-element
 stores."""
@@ -8,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from test_oracle_packed import FORMATS, block_values, corpus, d_offset, fnv1a64
+from test_oracle_packed import ALL_FORMATS, FORMATS, block_values, corpus, d_offset, fnv1a64
 
 pytestmark = pytest.mark.gpu
 OUT = {"float": (1, torch.float32), "float16": (10, torch.float16), "bfloat16": (16, torch.bfloat16),
@@ -28,7 +29,7 @@ def _bits(t, out):
     return c.numpy()
 
 
-@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
 def test_corpus_hashes_on_gpu(olamd, oracle, golden, dev, fmt):
     g = golden["dequantize_packed_gguf"]
     x = corpus(oracle, fmt, g["corpus_scales"])
@@ -37,9 +38,9 @@ def test_corpus_hashes_on_gpu(olamd, oracle, golden, dev, fmt):
 
 
 @pytest.mark.parametrize("out", list(OUT))
-@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
 def test_random_blocks_vs_oracle(olamd, oracle, dev, fmt, out):
-    rng = np.random.default_rng(len(fmt) * 7 + len(out) + FORMATS.index(fmt) * 101)
+    rng = np.random.default_rng(len(fmt) * 7 + len(out) + ALL_FORMATS.index(fmt) * 101)
     size = oracle.packed_block_bytes(fmt)
     bv = block_values(fmt)
     shapes = [(bv,), (3, 5, 2 * bv), (7, 4096), (1, 3 * bv)]

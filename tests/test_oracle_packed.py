@@ -8,11 +8,15 @@ import pytest
 FORMATS = ["gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1", "gguf:iq4_nl",
            "gguf:q4_k", "gguf:q6_k", "gguf:q2_k", "gguf:q3_k", "gguf:q5_k", "gguf:q8_k", "gguf:iq4_xs",
            "gguf:tq1_0", "gguf:tq2_0", "gguf:mxfp4", "gguf:nvfp4", "gguf:q1_0", "gguf:q2_0"]
+# the codebook profiles (lattice grids of ggml-common.h)
+IQ_FORMATS = ["gguf:iq2_xxs", "gguf:iq2_xs", "gguf:iq2_s", "gguf:iq3_xxs", "gguf:iq3_s", "gguf:iq1_s",
+              "gguf:iq1_m"]
+ALL_FORMATS = FORMATS + IQ_FORMATS
 AFFINE = {"gguf:q4_1", "gguf:q5_1", "gguf:q2_k", "gguf:q4_k", "gguf:q5_k"}  # a second fp16 (minimum) after d
 # byte offset of the fp16 scale d; None: no fp16 d (q8_k's is fp32, the fp4
 # formats carry scale bytes)
 D_OFFSET = {"gguf:q2_k": 80, "gguf:q3_k": 108, "gguf:q6_k": 208, "gguf:tq1_0": 52, "gguf:tq2_0": 64,
-            "gguf:q8_k": None, "gguf:mxfp4": None, "gguf:nvfp4": None}
+            "gguf:q8_k": None, "gguf:mxfp4": None, "gguf:nvfp4": None, "gguf:iq1_m": None}
 VALUES = {"gguf:nvfp4": 64, "gguf:q2_0": 64, "gguf:q1_0": 128}
 
 
@@ -33,7 +37,8 @@ def corpus(oracle, fmt, scales):
     byte j of block i is (73j + 29i + 17(j // 7) + 11(i // 3)) mod 256, then
     the fp16 scale d at its offset and, for the formats with a minimum, the
     fp16 of the next scale right after it; q8_k takes the fp32 scale / 3 in
-    its first 4 bytes, mxfp4 the scale byte (17 i) mod 256."""
+    its first 4 bytes, mxfp4 the scale byte (17 i) mod 256, iq1_m the fp16
+    scale's four nibbles in the top nibbles of its 16-bit scale words at 48."""
     size = oracle.packed_block_bytes(fmt)
     i = np.arange(64)[:, None]
     j = np.arange(size)[None, :]
@@ -51,6 +56,12 @@ def corpus(oracle, fmt, scales):
             blocks[:, b] = (bits >> (8 * b)) & 255
     elif fmt == "gguf:mxfp4":
         blocks[:, 0] = (np.arange(64) * 17) & 255
+    elif fmt == "gguf:iq1_m":
+        d = oracle.f32_to_f16_bits(np.array([scales[k % 8] for k in range(64)], np.float32)).astype(np.int64)
+        for j in range(4):
+            word = blocks[:, 48 + 2 * j].astype(np.int64) | (blocks[:, 49 + 2 * j].astype(np.int64) << 8)
+            word = (word & 0x0FFF) | (((d >> (4 * j)) & 15) << 12)
+            blocks[:, 48 + 2 * j], blocks[:, 49 + 2 * j] = word & 255, word >> 8
     return blocks.reshape(-1)
 
 
@@ -61,7 +72,7 @@ def fnv1a64(values: np.ndarray) -> str:
     return f"{h:016x}"
 
 
-@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
 def test_ggml_oracle_hashes(oracle, golden, fmt):
     g = golden["dequantize_packed_gguf"]
     x = corpus(oracle, fmt, g["corpus_scales"])
@@ -126,3 +137,46 @@ def test_k_quant_layouts_by_hand(oracle):
     y = oracle.dequantize_packed(blk, "gguf:q6_k", (256,))
     assert y[0] == 2 * -3 * (0x25 - 32)
     assert y[1] == 2 * -3 * -32
+
+
+def test_codebook_layouts_by_hand(oracle):
+    """Single octets of each codebook profile built by hand from the grids'
+    first rows (ggml-common.h: iq2xxs_grid[1] = 0x080808080808082b,
+    iq3xxs_grid[5] = 0x04040c3e, iq1s_grid[1] = 0xffffffffffffff01)."""
+    one = [0x00, 0x3C]  # fp16 1.0
+    # iq2_xxs: octet 0 index 1, w = scale nibble 2 (<< 28), lane 0 signs 0b0000001
+    # (odd count: the parity bit 7 is set too): scale (1 * 2.5) * 0.25 = 0.625
+    blk = np.zeros(66, np.uint8)
+    blk[0:2] = one
+    blk[2] = 1
+    w = (2 << 28) | 0b0000001
+    blk[6:10] = [w & 255, (w >> 8) & 255, (w >> 16) & 255, w >> 24]
+    y = oracle.dequantize_packed(blk, "gguf:iq2_xxs", (256,))
+    assert list(y[:8]) == [-0.625 * 43, 0.625 * 8, 0.625 * 8, 0.625 * 8, 0.625 * 8, 0.625 * 8, 0.625 * 8,
+                           -0.625 * 8]
+    # iq3_xxs: octet 0 indices 5 (row 0x04040c3e: 62, 12, 4, 4) and 0; scale
+    # nibble 0: (1 * 0.5) * 0.5 = 0.25; no signs
+    blk = np.zeros(98, np.uint8)
+    blk[0:2] = one
+    blk[2] = 5
+    y = oracle.dequantize_packed(blk, "gguf:iq3_xxs", (256,))
+    assert list(y[:8]) == [0.25 * 62, 0.25 * 12, 0.25 * 4, 0.25 * 4, 1.0, 1.0, 1.0, 1.0]
+    # iq1_s: octet 0 index 1 (lanes +1, -1 x 7), word at 34 = 0x8000 | (1 << 12):
+    # scale 1 * 3, delta -0.125
+    blk = np.zeros(50, np.uint8)
+    blk[0:2] = one
+    blk[2] = 1
+    blk[34:36] = [0x00, 0x90]
+    y = oracle.dequantize_packed(blk, "gguf:iq1_s", (256,))
+    assert list(y[:8]) == [3 * 0.875] + [3 * -1.125] * 7
+    # iq1_m: d from the words' top nibbles (0x3C00 = 1.0: nibbles 0, 0, 12, 3),
+    # octet 0 index 1, scale field 0 of word 0 = 2 -> 5, nibble of byte 32 = 8:
+    # delta -0.125
+    blk = np.zeros(56, np.uint8)
+    blk[0] = 1
+    blk[32] = 8
+    words = [2, 0, 0xC000, 0x3000]
+    for j, wv in enumerate(words):
+        blk[48 + 2 * j], blk[49 + 2 * j] = wv & 255, wv >> 8
+    y = oracle.dequantize_packed(blk, "gguf:iq1_m", (256,))
+    assert list(y[:8]) == [5 * 0.875] + [5 * -1.125] * 7
