@@ -31,6 +31,7 @@
 #include "onnx_proto/type_helper.h"
 
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <set>
 #include <string>
@@ -89,6 +90,21 @@ void AddInt(NodeProto &node, const char *name, int64_t value) {
   a->set_name(name);
   a->set_type(AttributeProto::AttributeType::INT);
   a->set_i(value);
+}
+
+// Values per block of the 27 GGUF profiles of DequantizePacked
+// (dequantize_packed.cc:27-36), 0 for any other format.  The fused node runs
+// all of them on the GPU.
+int64_t PackedBlockValues(const std::string &format) {
+  static const std::map<std::string, int64_t> kBlock = {
+      {"gguf:q4_0", 32},     {"gguf:q4_1", 32},    {"gguf:q5_0", 32},    {"gguf:q5_1", 32},   {"gguf:q8_0", 32},
+      {"gguf:q8_1", 32},     {"gguf:iq4_nl", 32},  {"gguf:mxfp4", 32},   {"gguf:q2_k", 256},  {"gguf:q3_k", 256},
+      {"gguf:q4_k", 256},    {"gguf:q5_k", 256},   {"gguf:q6_k", 256},   {"gguf:q8_k", 256},  {"gguf:iq2_xxs", 256},
+      {"gguf:iq2_xs", 256},  {"gguf:iq3_xxs", 256}, {"gguf:iq1_s", 256}, {"gguf:iq3_s", 256}, {"gguf:iq2_s", 256},
+      {"gguf:iq4_xs", 256},  {"gguf:iq1_m", 256},  {"gguf:tq1_0", 256},  {"gguf:tq2_0", 256}, {"gguf:nvfp4", 64},
+      {"gguf:q2_0", 64},     {"gguf:q1_0", 128}};
+  const auto it = kBlock.find(format);
+  return it == kBlock.end() ? 0 : it->second;
 }
 
 // ---------------------------------------------------------------------------
@@ -218,16 +234,14 @@ public:
     if (!SingleUse(graph, Out(*dp, 0), *tr)) return NoMatch(candidate, "DequantizePacked output has another consumer");
     if (!graph.IsConstant(In(*dp, 0))) return NoMatch(candidate, "packed weight is not an initializer");
     const std::string format = ol::GetAttributeOr<std::string>(*dp, "format", "");
-    const int64_t k_multiple = format == "gguf:q4_0" || format == "gguf:q8_0"   ? 64
-                               : format == "gguf:q4_k" || format == "gguf:q6_k" ? 256
-                                                                                : 0;
-    if (k_multiple == 0) return NoMatch(candidate, "format has no fused kernel");
+    const int64_t k_multiple = PackedBlockValues(format);
+    if (k_multiple == 0) return NoMatch(candidate, "unknown packed format");
     std::vector<int64_t> shape;
     ol::GetAttributeInts(*dp, "shape", shape);
     if (shape.size() != 2) return NoMatch(candidate, "DequantizePacked shape is not [N, K]");
     if (ol::GetAttributeOr<int64_t>(*dp, "output_dtype", kFloat) != kFloat16)
       return NoMatch(candidate, "DequantizePacked output is not FLOAT16");
-    if (shape[1] % k_multiple != 0) return NoMatch(candidate, "K does not fit the fused GEMV");
+    if (shape[1] % k_multiple != 0) return NoMatch(candidate, "K is not a whole number of blocks");
     if (!graph.HasType(In(candidate, 0))) return NoMatch(candidate, "type of A unknown");
     if (graph.GetType(In(candidate, 0)) != TensorType::kFloat16) return NoMatch(candidate, "A is not FLOAT16");
     return builder::MatchResult{this, {dp, tr, &candidate}, &candidate};

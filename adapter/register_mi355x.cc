@@ -873,8 +873,10 @@ private:
 // ai.rt.amd:DequantizePackedMatMul(A, x; format, shape = [N, K]) =
 // MatMul(A, Transpose(DequantizePacked(x, format, shape, FLOAT16))), the
 // chain onnx_core/runtime/dequantize_packed.cc:334-372 -> km/kernel_matmul.cc.
-// The fused GEMV takes q4_0 / q8_0 with M <= 8 and K % 64 == 0; other inputs
-// run the chain (GPU decode, host transpose, GPU MatMul).
+// Every GGUF profile and M runs in the one entry point: the fused decode
+// GEMVs (q4_0, q8_0, q4_k, q6_k at M <= 8), else the weight decoded to
+// FLOAT16 [N, K] on the device and multiplied by the MFMA GEMM reading its
+// rows, with no transpose written and nothing staged on the host.
 class Mi355xDequantizePackedMatMul : public Mi355xKernel {
 public:
   static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizePackedMatMul";
@@ -894,23 +896,9 @@ public:
     const rt::Shape shape = MatMulShape(a, wt);
     rt::Tensor y = ctx.MakeOutputTensor(0, kFloat16, shape, static_cast<size_t>(Count(shape)) * 2);
     onnxl_amd_tensor dy = DescribeOutput(y);
-    const int rc = onnxl_amd_dequantize_packed_matmul(&a, &x, format.c_str(), nk.data(), 2, &dy, nullptr);
-    if (rc == ONNXL_AMD_UNSUPPORTED) {
-      // W [N, K] decoded to FLOAT16 on the GPU, transposed on the host, MatMul
-      const int64_t N = nk[0], K = nk[1];
-      rt::Tensor w = ctx.MakeTemporaryTensor(kFloat16, rt::Shape{N, K}, static_cast<size_t>(N * K) * 2);
-      onnxl_amd_tensor dw = DescribeOutput(w);
-      Check(onnxl_amd_dequantize_packed(&x, format.c_str(), nk.data(), 2, kFloat16, &dw, nullptr));
-      rt::Tensor wtt = ctx.MakeTemporaryTensor(kFloat16, rt::Shape{K, N}, static_cast<size_t>(N * K) * 2);
-      const uint16_t *src = reinterpret_cast<const uint16_t *>(w.bytes());
-      uint16_t *dst = reinterpret_cast<uint16_t *>(wtt.mutable_bytes());
-      for (int64_t r = 0; r < N; ++r)
-        for (int64_t c = 0; c < K; ++c) dst[c * N + r] = src[r * K + c];
-      const onnxl_amd_tensor b = Describe(&wtt);
-      Check(onnxl_amd_matmul(&a, &b, &dy, nullptr));
-    } else {
-      Check(rc);
-    }
+    // every format and M runs on the device (decode GEMV, or the decoded
+    // weight through the MFMA GEMM): nothing comes back to the host here
+    Check(onnxl_amd_dequantize_packed_matmul(&a, &x, format.c_str(), nk.data(), 2, &dy, nullptr));
     rt::SetOutput(node, 0, std::move(y), ctx);
   }
 

@@ -171,10 +171,11 @@ int onnxl_amd_dequantize_packed(const onnxl_amd_tensor *x, const char *format, c
  * FLOAT16): a FLOAT16 [M, K], y FLOAT16 [M, N] (fp32 accumulation).  The
  * weight is in the ggml layout, each output's blocks contiguous along K; the
  * dequantized weights are rounded to FLOAT16 exactly as the unfused chain
- * rounds them, so only the fp32 summation order differs.  gguf:q4_0 and
- * gguf:q8_0 with M <= 8 and K % 64 == 0, gguf:q4_k and gguf:q6_k with
- * M <= 8 (K a multiple of their 256-value blocks); other inputs return
- * ONNXL_AMD_UNSUPPORTED.  No
+ * rounds them, so only the fp32 summation order differs.  Every one of the
+ * 27 GGUF profiles and any M: fused decode GEMVs for gguf:q4_0 / gguf:q8_0
+ * (K % 64 == 0) and gguf:q4_k / gguf:q6_k with M <= 8, otherwise the weight
+ * decoded to FLOAT16 [N, K] in the workspace and multiplied by the MFMA GEMM
+ * reading its rows (no transpose written).  No
  * single reference kernel: it computes the DequantizePacked -> Transpose ->
  * MatMul chain, onnx_core/runtime/dequantize_packed.cc:334-372 ->
  * km/kernel_matmul.cc:181-223. */

@@ -1148,8 +1148,7 @@ struct PackedProfile {
 };
 
 // The reference's 27 fixed wire profiles (ggml block sizes and bytes,
-// dequantize_packed.cc:27-36); the GPU decodes all but the 7 codebook formats
-// (iq1, iq2, iq3).
+// dequantize_packed.cc:27-36), all decoded on the GPU.
 constexpr PackedProfile kPackedProfiles[] = {
     {"gguf:q4_0", 32, 18, 2},      {"gguf:q4_1", 32, 20, 3},      {"gguf:q5_0", 32, 22, 6},
     {"gguf:q5_1", 32, 24, 7},      {"gguf:q8_0", 32, 34, 8},      {"gguf:q8_1", 32, 36, 9},
@@ -1207,10 +1206,14 @@ int DequantizePacked(const onnxl_amd_tensor *x, const char *format, const int64_
   return ONNXL_AMD_OK;
 }
 
-// Fused DequantizePacked(gguf:q4_0, shape [N, K], FLOAT16) -> MatMul with the
+// Fused DequantizePacked(format, shape [N, K], FLOAT16) -> MatMul with the
 // weight transposed: y = a @ W^T.  No single reference kernel: it computes
 // the chain dequantize_packed.cc:334-372 -> km/kernel_matmul.cc:181-223 that a
 // DequantizePacked -> Transpose -> MatMul subgraph runs node by node.
+//  - decode GEMVs (1 <= M <= 8) fused for q4_0, q8_0, q4_k and q6_k;
+//  - every other format, M or alignment: the weight decoded to FLOAT16 [N, K]
+//    in the workspace (the chain's rounding), then the 16-bit MFMA GEMM
+//    reading its rows as the B operand (no transpose is written).
 int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const char *format,
                            const int64_t *shape, int32_t rank, onnxl_amd_tensor *y, hipStream_t stream) {
   OLA_ENFORCE(a && x && y && format && shape && rank == 2, "DequantizePackedMatMul: invalid arguments.");
@@ -1224,29 +1227,50 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
   const int64_t M = a->dims[0];
   OLA_ENFORCE(y->data_type == kFloat16 && ShapeOf(*y) == Shape({M, N}) && y->size_bytes == M * N * 2,
               "DequantizePackedMatMul: y must be FLOAT16 [M, N].");
-  const bool q8 = std::strcmp(format, "gguf:q8_0") == 0;
-  const bool q4k = std::strcmp(format, "gguf:q4_k") == 0, q6k = std::strcmp(format, "gguf:q6_k") == 0;
-  if (!q8 && !q4k && !q6k && std::strcmp(format, "gguf:q4_0") != 0)
-    throw Unsupported(Cat("DequantizePackedMatMul: format ", format, " has no fused GPU kernel"));
-  const int64_t bv = q4k || q6k ? 256 : 32, bb = q8 ? 34 : (q4k ? 144 : (q6k ? 210 : 18));
+  const PackedProfile *prof = nullptr;
+  for (const auto &pp : kPackedProfiles)
+    if (std::strcmp(pp.format, format) == 0) prof = &pp;
+  if (!prof) throw InvalidArgument(Cat("DequantizePacked: unsupported format '", format, "'."));
+  const int64_t bv = prof->block_size, bb = prof->block_bytes;
   OLA_ENFORCE(K % bv == 0, "DequantizePacked: last dimension must contain complete blocks.");
   OLA_ENFORCE(x->data_type == kUint8 && x->rank == 1, "DequantizePacked: x must be a one-dimensional UINT8 tensor.");
   OLA_ENFORCE(x->dims[0] == N * (K / bv) * bb && x->size_bytes == x->dims[0],
               "DequantizePacked: packed input length must match exactly.");
   if (M == 0 || N == 0) return ONNXL_AMD_OK;  // empty [M, N] result, nothing to launch
-  Staging st(stream, 0, {a, x}, {y});
+  const int t = prof->ggml_type;
+  const bool q40 = t == 2, q80 = t == 8, q4k = t == 12, q6k = t == 14;
+  // the fused GEMVs take these when the operands are aligned (checked on the
+  // device addresses below)
+  const bool gemv_format = (q40 || q80 || q4k || q6k) && M <= 8 && K > 0;
+  const bool aligned_a = a->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(a->data) % 16 == 0;
+  const bool aligned_x = x->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(x->data) % 16 == 0;
+  const bool try_gemv = gemv_format && (q40 || q80 ? K % 64 == 0 : true) && aligned_a &&
+                        (aligned_x || (q6k && reinterpret_cast<uintptr_t>(x->data) % 2 == 0) ||
+                         ((q40 || q80) && reinterpret_cast<uintptr_t>(x->data) % 4 == 0));
+  const int64_t w_bytes = try_gemv ? 0 : N * K * 2;
+  Staging st(stream, (size_t)w_bytes, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
-  if (q4k || q6k) {
-    if (M > 8 || K == 0 || reinterpret_cast<uintptr_t>(ad) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(xd) % (q4k ? 16 : 2) != 0)
-      throw Unsupported("DequantizePackedMatMul: k-quant GEMV needs 1 <= M <= 8, K > 0, 16-byte aligned a and "
-                        "x aligned to 16 (q4_k) or 2 (q6_k) bytes");
-    LaunchGemvK(q4k ? 12 : 14, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
-                static_cast<uint16_t *>(st.Out(y)), stream);
+  uint16_t *yd = static_cast<uint16_t *>(st.Out(y));
+  if (try_gemv) {
+    if (q4k || q6k)
+      LaunchGemvK(q4k ? 12 : 14, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K, yd,
+                  stream);
+    else
+      (q80 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M,
+                                           N, K, yd, stream);
   } else {
-    if (!GemvQ40Eligible(M, K, ad, xd)) throw Unsupported("DequantizePackedMatMul: needs M <= 8 and K % 64 == 0");  // q8_0 alike
-    (q8 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K,
-                                         static_cast<uint16_t *>(st.Out(y)), stream);
+    uint16_t *w = static_cast<uint16_t *>(st.Extra());
+    LaunchDequantizePacked(t, static_cast<const uint8_t *>(xd), N * (K / bv), kFloat16, w, stream);
+    HMatMulParams h{};
+    h.A = static_cast<const uint16_t *>(ad);
+    h.B = w;
+    h.Y = yd;
+    h.M = M;
+    h.N = N;
+    h.K = K;
+    h.batch = 1;
+    h.bf16 = 0;
+    LaunchHMatMulBT(h, stream);
   }
   st.Finish();
   return ONNXL_AMD_OK;

@@ -29,8 +29,8 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Generic 16-bit MatMul for shapes the MFMA core does not take: one thread per
-// output, fp32 accumulation in k order.
-template <bool BF16>
+// output, fp32 accumulation in k order.  TB: B given transposed, [N, K].
+template <bool BF16, bool TB = false>
 __global__ __launch_bounds__(256) void HMatMulSimpleKernel(const HMatMulParams p) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t m = blockIdx.y;
@@ -39,11 +39,12 @@ __global__ __launch_bounds__(256) void HMatMulSimpleKernel(const HMatMulParams p
   int64_t ao, bo;
   BatchOffsets(p.bm, b, ao, bo);
   const uint16_t *a = p.A + ao + m * p.K;
-  const uint16_t *w = p.B + bo + n;
+  const uint16_t *w = p.B + bo + (TB ? n * p.K : n);
+  const int64_t wstep = TB ? 1 : p.N;
   float acc = 0.f;
   for (int64_t k = 0; k < p.K; ++k) {
     const float x = BF16 ? Bf16ToF32(a[k]) : F16ToF32(a[k]);
-    const float y = BF16 ? Bf16ToF32(w[k * p.N]) : F16ToF32(w[k * p.N]);
+    const float y = BF16 ? Bf16ToF32(w[k * wstep]) : F16ToF32(w[k * wstep]);
     acc += x * y;
   }
   p.Y[(b * p.M + m) * p.N + n] = BF16 ? F32ToBf16(acc) : F32ToF16(acc);
@@ -194,6 +195,23 @@ void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((p.N + 255) / 256), (unsigned)p.M, (unsigned)p.batch);
   if (p.bf16) hipLaunchKernelGGL(HMatMulSimpleKernel<true>, grid, dim3(256), 0, stream, p);
   else hipLaunchKernelGGL(HMatMulSimpleKernel<false>, grid, dim3(256), 0, stream, p);
+}
+
+// Y = A @ B^T for B given as [N, K] (batch 1): the MFMA core reading B's rows
+// like A's, else the simple kernel.
+void LaunchHMatMulBT(const HMatMulParams &p, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0) return;
+  const mg::GemmArgs g = HArgs(p);
+  if (p.batch == 1 && mg::EligibleBT(g)) {
+    if (p.bf16) mg::LaunchBT<mg::kOutBf16>(g, stream);
+    else mg::LaunchBT<mg::kOutF16>(g, stream);
+    return;
+  }
+  if (p.M > 65535 || p.batch > 65535) throw Unsupported("MatMul with B given as [N, K]: the one-thread-per-output "
+                                                       "kernel for N % 16 != 0 takes at most 65535 rows");
+  const dim3 grid((unsigned)((p.N + 255) / 256), (unsigned)p.M, (unsigned)p.batch);
+  if (p.bf16) hipLaunchKernelGGL((HMatMulSimpleKernel<true, true>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((HMatMulSimpleKernel<false, true>), grid, dim3(256), 0, stream, p);
 }
 
 size_t DqMatMulScratchBytes(const DqMatMulParams &p) {

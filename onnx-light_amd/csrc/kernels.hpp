@@ -266,6 +266,8 @@ struct HMatMulParams {
   int bf16;
 };
 void LaunchHMatMul(const HMatMulParams &p, hipStream_t stream);
+// Y = A @ B^T with B given as [N, K] row-major (batch 1).
+void LaunchHMatMulBT(const HMatMulParams &p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // GroupedMatMul (grouped.hip): Y[m, s, :] = A[m, :] @ W[idx[m, s]] (+ bias).

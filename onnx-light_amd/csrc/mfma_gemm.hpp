@@ -193,7 +193,7 @@ struct GemmArgs {
   int row_wscale_per;
   float row_xs, row_ys;
   const int32_t *row_bias;
-  // Grouped mode (GroupedMatMul; kernels with GM != 0): the rows of A are
+  // Grouped mode (GroupedMatMul; kernels with GM 1 or 2): the rows of A are
   // gathered and the rows of Y scattered through a routing table written on
   // the device, and each group of rows multiplies its own B.  M is then the
   // number of rows of A and Y has M * grp_sel rows.
@@ -217,7 +217,10 @@ __device__ __forceinline__ uint32_t DivMagic(uint32_t x, uint32_t magic) {
 // GM: 0 one GEMM per batch entry; 1 grouped with each group's B [K, N]
 // row-major; 2 grouped with each group's B given transposed, [N, K]
 // row-major (kH16 only): its stage is then loaded and read like A's, rows of
-// N with consecutive k, which is exactly the B operand of the MFMA.
+// N with consecutive k, which is exactly the B operand of the MFMA; 3 one
+// GEMM per batch entry with B given transposed like that (kH16 only: the
+// fused DequantizePacked -> Transpose -> MatMul, whose decoded weight is
+// [N, K]).
 //
 // CV: implicit convolution (int8): B is read like A, its row for output
 // position n and K step t at the byte offset of GemmArgs::cv, so the im2col
@@ -225,7 +228,8 @@ __device__ __forceinline__ uint32_t DivMagic(uint32_t x, uint32_t magic) {
 template <int KIND, int OUT, bool ZP, bool AU8, bool BU8, int WB, int GM = 0, bool CV = false>
 __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) {
   constexpr bool RA = ZP, CB = ZP;
-  constexpr bool BT = GM == 2 || CV;
+  constexpr bool GRP = GM == 1 || GM == 2;  // grouped (routing tables)
+  constexpr bool BT = GM == 2 || GM == 3 || CV;
   static_assert(GM == 0 || (KIND == kH16 && WB == 2 && !ZP), "grouped mode: 16-bit operands, 128-column tiles");
   static_assert(!CV || (KIND == kI8 && WB == 2 && GM == 0), "implicit convolution: int8, 128-column tiles");
   using T = Traits<KIND>;
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // grouped mode: this tile's group, its routed rows [rbase, rbase + rcount)
   int grp = 0;
   int64_t rbase = 0, rcount = M;
-  if constexpr (GM != 0) {
+  if constexpr (GRP) {
     // Workgroups past the routed tiles leave at once, before any load or
     // barrier (the whole workgroup takes the same branch).  The others are
     // spread as in the plain mode: each XCD a contiguous run of tiles (about
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr int kAsz = KIND == kI8 ? 1 : 2;
   constexpr int kBsz = KIND == kH16 ? 2 : 1;
   int64_t a_off = 0, b_off = 0;
-  if constexpr (GM != 0) b_off = grp * p.grp_b_stride;
+  if constexpr (GRP) b_off = grp * p.grp_b_stride;
   else BatchOffsets(p.bm, bt, a_off, b_off);
   const char *Ab = static_cast<const char *>(p.A) + a_off * kAsz;
   const char *Bb = static_cast<const char *>(p.B) + b_off * kBsz;
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // access out of range): a scalar select instead of a per-lane one
   const __amdgpu_buffer_rsrc_t rsA0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Ab), (short)0, 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsB0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(Bb), (short)0, 0, kRsrcWord3);
-  const int64_t YR = GM != 0 ? M * p.grp_sel : M;  // rows of Y
+  const int64_t YR = GRP ? M * p.grp_sel : M;  // rows of Y
   const __amdgpu_buffer_rsrc_t rsY = __builtin_amdgcn_make_buffer_rsrc(
       static_cast<char *>(p.Y) + bt * M * LDY * kOsz, (short)0, (int)(YR * LDY * kOsz), kRsrcWord3);
   const int nfull = (int)(K / T::kKStep);                  // full K steps
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   for (int q = 0; q < 8; ++q) {
     const int64_t row = row0 + 8 * (8 * wave + q) + (lane >> 3);  // 8-row block 8 * wave + q
     int64_t src = row;  // row of A
-    if constexpr (GM != 0) src = row < rcount ? p.grp_rows[rbase + row] / p.grp_sel : 0;
+    if constexpr (GRP) src = row < rcount ? p.grp_rows[rbase + row] / p.grp_sel : 0;
     a_g[q] = row < rcount ? (unsigned)(src * KA + 16 * ((lane & 7) ^ (lane >> 3) ^ (q & 1))) : kOob;
   }
   unsigned b_g[4];  // LB <= 4 (a fixed bound: a template-dependent size here
@@ -810,9 +814,9 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // (j, g) register group, the output dtype's bits).  GroupedMatMul adds it
   // as MatMul followed by Add does: the sum rounded to the output dtype, the
   // bias added in fp32, rounded again.
-  v2i gbias[GM != 0 ? WB : 1][4];
-  const bool has_gbias = GM != 0 && p.grp_bias != nullptr;
-  if constexpr (GM != 0) {
+  v2i gbias[GRP ? WB : 1][4];
+  const bool has_gbias = GRP && p.grp_bias != nullptr;
+  if constexpr (GRP) {
     const __amdgpu_buffer_rsrc_t rsBias = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void *>(p.grp_bias), (short)0, has_gbias ? (int)(p.grp_count * N * kOsz) : 0, kRsrcWord3);
 #pragma unroll
@@ -890,7 +894,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
             for (int e = 0; e < 4; ++e) a[4 * g + e] *= sc4[e];
           }
-          if constexpr (GM != 0) {
+          if constexpr (GRP) {
             if (has_gbias) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
@@ -934,7 +938,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
     for (int c = 0; c < WB * kOsz; ++c) {
       grow[c] = 0;
-      if constexpr (GM != 0) {
+      if constexpr (GRP) {
         const int rr = (c * 64 + lane) / kChunksPerRow;
         if (brow + rr < rcount)
           grow[c] = (unsigned)(((int64_t)p.grp_rows[rbase + brow + rr] * LDY + col0 + wn * kWN) * kOsz);
@@ -952,7 +956,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
       const int id = c * 64 + lane;
       const int rr = id / kChunksPerRow, cc = id % kChunksPerRow;
       const bool ok = brow + rr < rcount && cc * (16 / kOsz) < ncol;
-      const unsigned at = GM != 0 ? grow[c] + (unsigned)(cc * 16) : ybase + (unsigned)(rr * LDY * kOsz + cc * 16);
+      const unsigned at = GRP ? grow[c] + (unsigned)(cc * 16) : ybase + (unsigned)(rr * LDY * kOsz + cc * 16);
       __builtin_amdgcn_raw_buffer_store_b128(piece[c], rsY, ok ? at : kOob, 0, kStoreThrough);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -989,6 +993,23 @@ inline void Launch(const GemmArgs &p, hipStream_t s) {
   const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN) * p.batch;
   hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, ZP, AU8, BU8, WB, 0, CV>), dim3((unsigned)tiles), dim3(kThreads),
                      0, s, p);
+}
+
+// Eligibility with B given transposed ([N, K] row-major, GM == 3): K a
+// multiple of half the K step, N a multiple of 16, 16-byte aligned operands
+// and output, and each matrix's bytes (plus the look-ahead) below 2^31 - 2^24.
+inline bool EligibleBT(const GemmArgs &p) {
+  const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
+  auto al = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  return p.K > 0 && p.K % (Traits<kH16>::kKStep / 2) == 0 && p.N % 16 == 0 && p.batch == 1 && al(p.A) &&
+         al(p.B) && al(p.Y) && p.M * p.K * 2 + 4 * kStepBytes < lim && p.N * p.K * 2 + 4 * kStepBytes < lim &&
+         p.M * p.N * 2 < lim;
+}
+
+template <int OUT> inline void LaunchBT(const GemmArgs &p, hipStream_t s) {
+  const int64_t tiles = ((p.M + kBM - 1) / kBM) * ((p.N + 127) / 128);
+  hipLaunchKernelGGL((MfmaGemmKernel<kH16, OUT, false, false, false, 2, 3>), dim3((unsigned)tiles), dim3(kThreads), 0,
+                     s, p);
 }
 
 // Grouped launch: `max_tiles` workgroups, an upper bound of the tiles the

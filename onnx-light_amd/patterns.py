@@ -46,7 +46,16 @@ FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
 PACKED_FUSED_OP = "DequantizePackedMatMul"
 ENCODED_FUSED_OP = "DequantizeEncodedMatMul"
-_PACKED_FORMATS = {"gguf:q4_0": 64, "gguf:q8_0": 64, "gguf:q4_k": 256, "gguf:q6_k": 256}  # format: K multiple
+# the 27 GGUF profiles of DequantizePacked (format: values per block); the
+# fused node runs every one of them on the GPU (decode GEMVs for q4_0, q8_0,
+# q4_k and q6_k, the decoded weight through the MFMA GEMM otherwise)
+_PACKED_FORMATS = {f: 32 for f in ("gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1",
+                                   "gguf:iq4_nl", "gguf:mxfp4")}
+_PACKED_FORMATS.update({f: 256 for f in ("gguf:q2_k", "gguf:q3_k", "gguf:q4_k", "gguf:q5_k", "gguf:q6_k",
+                                         "gguf:q8_k", "gguf:iq2_xxs", "gguf:iq2_xs", "gguf:iq3_xxs", "gguf:iq1_s",
+                                         "gguf:iq3_s", "gguf:iq2_s", "gguf:iq4_xs", "gguf:iq1_m", "gguf:tq1_0",
+                                         "gguf:tq2_0")})
+_PACKED_FORMATS.update({"gguf:nvfp4": 64, "gguf:q2_0": 64, "gguf:q1_0": 128})
 _ONNX_DOMAINS = ("", "ai.onnx")
 _CAST_TARGETS = (10, 16)  # FLOAT16, BFLOAT16: the types the fused kernel rounds to
 FLOAT, UINT8, INT8, FLOAT16, BFLOAT16, FLOAT8E4M3FN, UINT4, INT4 = 1, 2, 3, 10, 16, 17, 21, 22
@@ -251,14 +260,14 @@ class DequantizePackedMatMulPattern(PatternOptimization):
             return self.no_match("packed weight is not an initializer")
         fmt = dp.attrs.get("format")
         if fmt not in _PACKED_FORMATS:
-            return self.no_match("format has no fused kernel")
+            return self.no_match("unknown packed format")
         shape = [int(d) for d in dp.attrs.get("shape", [])]
         if len(shape) != 2:
             return self.no_match("DequantizePacked shape is not [N, K]")
         if int(dp.attrs.get("output_dtype", FLOAT)) != FLOAT16:
             return self.no_match("DequantizePacked output is not FLOAT16")
         if shape[1] % _PACKED_FORMATS[fmt]:
-            return self.no_match("K does not fit the fused GEMV")
+            return self.no_match("K is not a whole number of blocks")
         a_info = graph.value_info.get(candidate.inputs[0])
         if a_info is None:
             return self.no_match("type of A unknown")

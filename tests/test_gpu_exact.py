@@ -197,8 +197,10 @@ def test_int4_gemv_one_hot_rows_all_k(olamd, oracle, dev, layout):
 # ---- packed GGUF GEMVs ------------------------------------------------------
 
 @pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0", "gguf:q4_k", "gguf:q6_k"])
-@pytest.mark.parametrize("M,N", [(1, 14336), (8, 2048)])
+@pytest.mark.parametrize("M,N", [(1, 14336), (8, 2048), (40, 512)])
 def test_packed_gemv_dyadic_bit_exact(olamd, oracle, dev, fmt, M, N):
+    """The fused GEMVs (M <= 8) and the general path (M = 40: the weight
+    decoded to FLOAT16 [N, K], the MFMA GEMM reading its rows)."""
     K = 4096
     case = dy.gguf_case(oracle, np.random.default_rng(M * N + len(fmt)), M, K, N, fmt)
     y = olamd.dequantize_packed_matmul(bits_tensor(case["a_bits"], "f16", dev), T(case["x"], dev), fmt, (N, K))

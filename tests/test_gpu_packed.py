@@ -156,17 +156,65 @@ def test_packed_gemv_vs_chain(olamd, oracle, dev, fmt, block_bytes, M, N, K):
     assert_close(got_bits, ref, mag, "f16", oracle, f"{fmt} gemv {M}x{N}x{K}")
 
 
-def test_packed_gemv_unsupported(olamd, dev):
-    a = torch.zeros((9, 64), dtype=torch.float16, device=dev)
-    x = torch.zeros(4 * 2 * 18, dtype=torch.uint8, device=dev)
-    with pytest.raises(olamd.Unsupported):
-        olamd.dequantize_packed_matmul(a, x, "gguf:q4_0", (4, 64))
-    with pytest.raises(olamd.Unsupported):
-        olamd.dequantize_packed_matmul(a[:1], torch.zeros(4 * 2 * 22, dtype=torch.uint8, device=dev),
-                                       "gguf:q5_0", (4, 64))
-    with pytest.raises(olamd.Unsupported):  # K % 64 != 0
-        olamd.dequantize_packed_matmul(a[:1, :32], torch.zeros(4 * 34, dtype=torch.uint8, device=dev),
-                                       "gguf:q8_0", (4, 32))
+def _finite_blocks(oracle, rng, fmt, nblocks):
+    """Random blocks of `fmt` with small finite scales (whatever the format
+    keeps them in): the codes random, the outputs finite."""
+    size = oracle.packed_block_bytes(fmt)
+    x = rng.integers(0, 256, (nblocks, size)).astype(np.uint8)
+    at = d_offset(fmt)
+    if at is not None:
+        d = oracle.f32_to_f16_bits(rng.uniform(0.001, 0.01, nblocks).astype(np.float32))
+        x[:, at], x[:, at + 1] = d & 255, d >> 8
+        if fmt in ("gguf:q4_1", "gguf:q5_1", "gguf:q2_k", "gguf:q4_k", "gguf:q5_k"):
+            m = oracle.f32_to_f16_bits(rng.uniform(-0.01, 0.01, nblocks).astype(np.float32))
+            x[:, at + 2], x[:, at + 3] = m & 255, m >> 8
+    elif fmt == "gguf:q8_k":
+        d = rng.uniform(0.001, 0.01, nblocks).astype(np.float32).view(np.uint32)
+        for b in range(4):
+            x[:, b] = (d >> (8 * b)) & 255
+    elif fmt == "gguf:mxfp4":
+        x[:, 0] = rng.integers(118, 124, nblocks)  # 2^-9 .. 2^-4
+    elif fmt == "gguf:nvfp4":
+        x[:, 0:4] = rng.integers(0x18, 0x28, (nblocks, 4))  # ue4m3 2^-5 .. 2^-3 range
+    elif fmt == "gguf:iq1_m":
+        d = oracle.f32_to_f16_bits(rng.uniform(0.001, 0.01, nblocks).astype(np.float32)).astype(np.int64)
+        for j in range(4):
+            w = (x[:, 48 + 2 * j].astype(np.int64) | (x[:, 49 + 2 * j].astype(np.int64) << 8)) & 0x0FFF
+            w |= ((d >> (4 * j)) & 15) << 12
+            x[:, 48 + 2 * j], x[:, 49 + 2 * j] = w & 255, w >> 8
+    return x.reshape(-1)
+
+
+def _chain_vs_gpu(olamd, oracle, dev, fmt, M, N, K, seed):
+    from test_gpu_float import assert_close
+    rng = np.random.default_rng(seed)
+    x = _finite_blocks(oracle, rng, fmt, N * K // block_values(fmt))
+    a = np.float16(rng.standard_normal((M, K)))
+    w_bits = oracle.dequantize_packed(x, fmt, (N, K), 10)
+    ref = oracle.matmul_half(a.view(np.uint16), np.ascontiguousarray(w_bits.T), 10, nthreads=8)
+    got = olamd.dequantize_packed_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(x).to(dev), fmt, (N, K))
+    got_bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    mag = np.abs(a.astype(np.float64)) @ np.abs(oracle.f16_bits_to_f32(w_bits).astype(np.float64)).T
+    assert_close(got_bits, ref, mag, "f16", oracle, f"{fmt} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
+def test_packed_matmul_prefill_every_format(olamd, oracle, dev, fmt):
+    """M = 40 (past the decode GEMVs): the weight decoded to FLOAT16 [N, K] on
+    the device, then the MFMA GEMM reading its rows as B; the oracle chain
+    DequantizePacked(FLOAT16) -> Transpose -> MatMul within the float
+    tolerance (same weight rounding, another fp32 summation order)."""
+    _chain_vs_gpu(olamd, oracle, dev, fmt, 40, 96, 512, ALL_FORMATS.index(fmt))
+
+
+@pytest.mark.parametrize("fmt,M,N,K", [("gguf:q4_0", 300, 160, 1024), ("gguf:q4_k", 257, 48, 2048),
+                                       ("gguf:iq2_xs", 9, 64, 256), ("gguf:q5_0", 1, 32, 64),
+                                       ("gguf:q8_0", 3, 40, 32), ("gguf:q6_k", 24, 37, 512),
+                                       ("gguf:mxfp4", 5, 21, 96)])
+def test_packed_matmul_general_shapes(olamd, oracle, dev, fmt, M, N, K):
+    """Ragged M tiles, a decode shape of a format without a fused GEMV, K %
+    64 != 0 for q8_0, and N % 16 != 0 (the one-thread-per-output kernel)."""
+    _chain_vs_gpu(olamd, oracle, dev, fmt, M, N, K, M * N + K)
 
 
 @pytest.mark.parametrize("fmt,bpb", [("gguf:q4_0", 18), ("gguf:q8_0", 34)])

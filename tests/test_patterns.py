@@ -180,9 +180,9 @@ def test_packed_rewrite(pt):
 
 
 @pytest.mark.parametrize("kw,reason", [
-    ({"fmt": "gguf:q5_k"}, "format has no fused kernel"),
-    ({"shape": (96, 96)}, "K does not fit the fused GEMV"),
-    ({"fmt": "gguf:q6_k", "shape": (96, 128)}, "K does not fit the fused GEMV"),
+    ({"fmt": "gguf:q9_9"}, "unknown packed format"),
+    ({"shape": (96, 48)}, "K is not a whole number of blocks"),
+    ({"fmt": "gguf:q6_k", "shape": (96, 128)}, "K is not a whole number of blocks"),
     ({"shape": (2, 96, 128)}, "DequantizePacked shape is not [N, K]"),
     ({"odt": 1}, "DequantizePacked output is not FLOAT16"),
     ({"perm": [0, 1]}, "Transpose is not a 2-D transpose"),
@@ -195,6 +195,17 @@ def test_packed_no_match(pt, kw, reason):
     m = pat.match(g, g.nodes[2])
     assert not m and m.reason == reason
     assert pt.optimize(g, [pat]) == 0
+
+
+@pytest.mark.parametrize("fmt,block", [("gguf:q5_k", 256), ("gguf:iq2_xxs", 256), ("gguf:mxfp4", 32),
+                                       ("gguf:q1_0", 128), ("gguf:nvfp4", 64), ("gguf:q4_1", 32)])
+def test_packed_rewrite_every_format(pt, fmt, block):
+    """Every GGUF profile runs fused on the GPU (the decode GEMVs or the
+    decoded weight through the MFMA GEMM): each format with K a whole number
+    of its blocks is rewritten."""
+    g = _packed_graph(pt, fmt=fmt, shape=(96, 2 * block))
+    assert pt.optimize(g, [pt.create_registered_pattern("DequantizePackedMatMulGpu")]) == 1
+    assert g.nodes[0].attrs == {"format": fmt, "shape": [96, 2 * block]}
 
 
 def test_packed_shared_intermediate_is_left_alone(pt):
