@@ -109,16 +109,18 @@ __device__ __forceinline__ v2i PackHalf4(v4f v) {
   return r;
 }
 
-// CPL / 8 dwords of packed nibbles (CPL columns) at byte offset off + soff.
+// CPL / 8 dwords of packed nibbles (CPL columns) at byte offset off + soff,
+// with the non-temporal cache policy (each weight byte is read once per call).
 template <int CPL>
 __device__ __forceinline__ void LoadNibbles(__amdgpu_buffer_rsrc_t rs, unsigned off, int soff,
                                             uint32_t (&dst)[CPL / 8]) {
+  constexpr int kNonTemporal = 2;
   if constexpr (CPL == 16) {
-    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, soff, 0);
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, soff, kNonTemporal);
     dst[0] = (uint32_t)v.x;
     dst[1] = (uint32_t)v.y;
   } else {
-    dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, 0);
+    dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, kNonTemporal);
   }
 }
 

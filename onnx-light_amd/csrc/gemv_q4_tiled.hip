@@ -56,6 +56,11 @@ constexpr int kTargetGroups = 256;   // workgroups wanted: one per CU
 
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr unsigned kOob = 0x80000000u;  // past every buffer: loads return zero, stores drop
+// Cache policy of the weight loads: non-temporal (each weight byte is read
+// once per call).  Measured on configuration 3: 8.2 us against 8.6-8.9 us
+// with the default policy; the best plain read of the same bytes also uses
+// it.
+constexpr int kStreamPolicy = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t Rsrc(const void *p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kRsrcWord3);
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void GemvQ4TiledKernel(const TiledArgs p)
     const int q = live ? gb + i : 0;
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      wq[s][t] = __builtin_amdgcn_raw_buffer_load_b128(rsW, live ? w_lane[t] : kOob, q * kGroupBytes, 0);
+      wq[s][t] = __builtin_amdgcn_raw_buffer_load_b128(rsW, live ? w_lane[t] : kOob, q * kGroupBytes, kStreamPolicy);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int rb = q * kGroupRows + 32 * c;  // first row of chunk c (wave-uniform)
