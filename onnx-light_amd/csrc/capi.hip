@@ -1573,7 +1573,6 @@ NbitsLayout PlanNbits(int64_t K, int64_t N, int64_t bits, int64_t block, bool ha
   OLA_ENFORCE(block >= 16 && block <= 0xffffffffLL && (block & (block - 1)) == 0,
               "ORT MatMulNBits block_size must be a power of two in [16, UINT32_MAX].");
   OLA_ENFORCE(bits == 2 || bits == 4 || bits == 8, "Expected an ORT MatMulNBits quantization format.");
-  if (bits == 2) throw Unsupported("MatMulNBits: 2-bit weights have no GPU kernel");
   if (K % block != 0)
     throw Unsupported(Cat("MatMulNBits: K = ", K, " is not a multiple of block_size ", block,
                           " (a partial last block has no fused kernel)"));
@@ -1581,7 +1580,7 @@ NbitsLayout PlanNbits(int64_t K, int64_t N, int64_t bits, int64_t block, bool ha
   l.groups = K / block;
   l.blob = block * bits / 8;
   l.zcol = (l.groups * bits + 7) / 8;
-  l.weight_bytes = bits == 4 ? TiledInt4Bytes(K, N) : K * N;
+  l.weight_bytes = bits <= 4 ? TiledInt4Bytes(K, N) : K * N;  // 2-bit codes as 4-bit ones
   l.scale_bytes = l.groups * N * 2;
   l.zp_bytes = !has_zp ? 0 : (bits == 8 ? l.groups * N : (l.groups * N + 1) / 2);
   return l;
@@ -1625,7 +1624,7 @@ int PrepareMatMulNbits(const onnxl_amd_tensor *B, const onnxl_amd_tensor *scales
       }
     }
   }
-  const bool four = bits == 4;
+  const bool four = bits <= 4;  // 2-bit codes are prepared as 4-bit ones
   auto out_ok = [](onnxl_amd_tensor *t, int64_t need, const char *what) {
     OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE, "prepare_matmul_nbits: ", what, " must be device memory.");
     OLA_ENFORCE(t->size_bytes >= need, "prepare_matmul_nbits: ", what, " holds ", t->size_bytes, " bytes, needs ", need);

@@ -12,6 +12,10 @@
 //    tile's K range contiguous).  Without zero points the codes are offset
 //    binary INT4 (code - 8 is the signed value, the tiled layout's own
 //    encoding); with them UINT4 codes and UINT4 zero points [groups, N];
+//  - 2 bits: the same 4-bit tiled layout (twice the bytes of the ORT blob),
+//    so the same kernels run them: without zero points INT4 codes of
+//    code - 2 (offset binary code + 6), with them UINT4 codes 0..3 and UINT4
+//    zero points;
 //  - 8 bits: [K, N] bytes, INT8 (code ^ 0x80 = code - 128) without zero
 //    points, UINT8 codes with UINT8 zero points [groups, N];
 //  - scales transposed to [groups, N] (blocked along K, axis 0).
@@ -25,12 +29,13 @@ namespace {
 
 constexpr int kGroupRows = 128;  // the tiled layout's row group (gemv_q4_tiled.hip)
 
-// Tiled 4-bit words from ORT codes: word idx = ((t * ngroups + q) * 64 + l) * 4 + c
-// holds column 16 t + l % 16, rows 128 q + 32 c + 8 (l / 16) + (0..7), row
-// 2i at bits 4i and row 2i + 1 at bits 16 + 4i.
+// Tiled 4-bit words from ORT 4- or 2-bit codes (`bits`), each plus `add`:
+// word idx = ((t * ngroups + q) * 64 + l) * 4 + c holds column 16 t + l % 16,
+// rows 128 q + 32 c + 8 (l / 16) + (0..7), row 2i at bits 4i and row 2i + 1
+// at bits 16 + 4i; `pad` fills rows past K and columns past N.
 __global__ void OrtTileInt4Kernel(const uint8_t *__restrict__ B, int64_t K, int64_t N, int64_t block,
-                                  int64_t groups, int64_t ngroups, uint32_t pad, int64_t total,
-                                  uint32_t *__restrict__ out) {
+                                  int64_t groups, int64_t ngroups, int bits, uint32_t add, uint32_t pad,
+                                  int64_t total, uint32_t *__restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
   const int c = (int)(idx & 3);
@@ -39,14 +44,15 @@ __global__ void OrtTileInt4Kernel(const uint8_t *__restrict__ B, int64_t K, int6
   const int64_t t = tq / ngroups, q = tq % ngroups;
   const int64_t col = 16 * t + (l & 15);
   const int64_t row0 = kGroupRows * q + 32 * c + 8 * (l >> 4);
-  const int64_t blob = block / 2;
+  const int64_t blob = block * bits / 8;
+  const int per = 8 / bits;
   uint32_t word = 0;
   for (int j = 0; j < 8; ++j) {
     const int64_t row = row0 + j;
     uint32_t u = pad;
     if (row < K && col < N) {
       const int64_t g = row / block, jj = row % block;
-      u = (B[(col * groups + g) * blob + jj / 2] >> (4 * (jj & 1))) & 15u;
+      u = ((B[(col * groups + g) * blob + jj / per] >> (bits * (jj % per))) & ((1u << bits) - 1u)) + add;
     }
     word |= u << ((j & 1) ? 16 + 4 * (j >> 1) : 4 * (j >> 1));
   }
@@ -71,9 +77,9 @@ __global__ void OrtScaleTransposeKernel(const uint16_t *__restrict__ s, int64_t 
   out[e] = s[n * groups + g];
 }
 
-// zero points, packed `bits`-bit codes [N, zcol] -> [groups, N]: 4-bit
-// codes two per byte, element g * N + n in the low nibble when even (ONNX
-// packing); 8-bit one per byte.  One thread per output byte.
+// zero points, packed `bits`-bit codes [N, zcol] -> [groups, N]: 4- and
+// 2-bit codes as 4-bit ones two per byte, element g * N + n in the low nibble
+// when even (ONNX packing); 8-bit one per byte.  One thread per output byte.
 __global__ void OrtZeroPointsKernel(const uint8_t *__restrict__ z, int64_t N, int64_t groups, int64_t zcol,
                                     int bits, int64_t out_bytes, uint8_t *__restrict__ out) {
   const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -88,7 +94,8 @@ __global__ void OrtZeroPointsKernel(const uint8_t *__restrict__ z, int64_t N, in
     const int64_t e = 2 * b + h;
     if (e >= groups * N) break;
     const int64_t g = e / N, n = e % N;
-    const uint8_t code = (z[n * zcol + g / 2] >> (4 * (g & 1))) & 15u;
+    const int per = 8 / bits;
+    const uint8_t code = (z[n * zcol + g / per] >> (bits * (g % per))) & ((1u << bits) - 1u);
     v |= (uint8_t)(code << (4 * h));
   }
   out[b] = v;
@@ -100,12 +107,14 @@ unsigned Blocks(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 void LaunchPrepareNbits(const NbitsPrepParams &p, hipStream_t stream) {
   const int64_t groups = p.K / p.block;
-  if (p.bits == 4) {
+  if (p.bits <= 4) {
     const int64_t ngroups = (p.K + kGroupRows - 1) / kGroupRows;
     const int64_t total = TiledInt4Bytes(p.K, p.N) / 4;
+    // without zero points: INT4 offset binary of code - 2^(bits-1)
+    const uint32_t add = p.zp ? 0u : 8u - (1u << (p.bits - 1));
     if (total > 0)
       hipLaunchKernelGGL(OrtTileInt4Kernel, dim3(Blocks(total)), dim3(256), 0, stream, p.B, p.K, p.N, p.block,
-                         groups, ngroups, p.zp ? 0u : 8u, total, static_cast<uint32_t *>(p.weight));
+                         groups, ngroups, (int)p.bits, add, p.zp ? 0u : 8u, total, static_cast<uint32_t *>(p.weight));
   } else {
     if (p.K * p.N > 0)
       hipLaunchKernelGGL(OrtBytesToRowsKernel, dim3(Blocks(p.K * p.N)), dim3(256), 0, stream, p.B, p.K, p.N,

@@ -200,17 +200,20 @@ def int4_case(oracle, rng, M, K, N, block, signed, with_zp, dt):
 def ckpt_case(oracle, rng, kind, M, K, N, group, dt):
     """Packed checkpoint weights prepared for the fused node: kind
     "awq" (AWQ gemm, 4 bits), "gptq4" / "gptq8" (GPTQ v2, 4 / 8 bits),
-    "nbits4" / "nbits8" (ORT MatMulNBits with zero points).  W = (q - z) * s
+    "nbits2" / "nbits4" / "nbits8" (ORT MatMulNBits with zero points).  W = (q - z) * s
     with power-of-two scales (FLOAT16 for fp16 activations; BFLOAT16 for AWQ /
     GPTQ with bf16 activations); 8-bit codes lie within 24 of their zero
     point.  Returns the case with the checkpoint arrays under "ckpt"."""
     from awq_gptq_cases import awq_pack, gptq_pack
     from nbits_cases import ort_pack
-    bits = 8 if kind.endswith("8") else 4
+    bits = 8 if kind.endswith("8") else (2 if kind.endswith("2") else 4)
     groups = K // group
     if bits == 8:
         z = rng.integers(120, 137, (groups, N))
         q = np.repeat(z, group, axis=0) + rng.integers(-24, 25, (K, N))
+    elif bits == 2:
+        z = rng.integers(0, 4, (groups, N))
+        q = rng.integers(0, 4, (K, N))
     else:
         z = rng.integers(0, 16, (groups, N))
         q = rng.integers(0, 16, (K, N))

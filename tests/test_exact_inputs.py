@@ -61,7 +61,8 @@ def test_gguf_case(oracle, fmt):
 
 
 @pytest.mark.parametrize("kind,dt", [("awq", "f16"), ("awq", "bf16"), ("gptq4", "bf16"), ("gptq8", "f16"),
-                                     ("gptq8", "bf16"), ("nbits4", "f16"), ("nbits8", "f16")])
+                                     ("gptq8", "bf16"), ("nbits2", "f16"), ("nbits4", "f16"),
+                                     ("nbits8", "f16")])
 def test_checkpoint_case(oracle, kind, dt):
     case = dy.ckpt_case(oracle, np.random.default_rng(6), kind, 8, 4096, 256, 128, dt)
     _check(oracle, case, 16)

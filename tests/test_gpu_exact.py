@@ -251,8 +251,8 @@ def _prepare(olamd, case, kind, K, N, group, dt, dev):
                                       T(ck["zp"], dev), K, N, ck["bits"], group)
 
 
-CKPT = [("awq", "f16"), ("awq", "bf16"), ("gptq4", "bf16"), ("gptq8", "f16"), ("gptq8", "bf16"), ("nbits4", "f16"),
-        ("nbits8", "f16")]
+CKPT = [("awq", "f16"), ("awq", "bf16"), ("gptq4", "bf16"), ("gptq8", "f16"), ("gptq8", "bf16"), ("nbits2", "f16"),
+        ("nbits4", "f16"), ("nbits8", "f16")]
 
 
 @pytest.mark.parametrize("kind,dt", CKPT)

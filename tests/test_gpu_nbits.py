@@ -1,5 +1,6 @@
-"""ORT MatMulNBits weights on the GPU: prepared by onnxl_amd_prepare_matmul_nbits
-into the fused DequantizeLinear -> MatMul operands, then MatMul(A, W) with
+"""ORT MatMulNBits weights (2, 4 and 8 bits) on the GPU: prepared by
+onnxl_amd_prepare_matmul_nbits into the fused DequantizeLinear -> MatMul
+operands (2-bit codes as 4-bit ones in the same tiled layout), then MatMul(A, W) with
 W = oracle.ort_nbits_decode rounded to FLOAT16 (the reference's decode,
 pinned by its golden test in test_oracle_nbits.py).  One-hot activations
 read single rows of W back bit for bit (one exact product per output);
@@ -32,7 +33,7 @@ def _weight(oracle, rng, K, N, bits, block, with_zp):
     return B, scale_bits, zpk, w_bits
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("with_zp", [False, True])
 @pytest.mark.parametrize("K,N,block", [(256, 96, 32), (512, 40, 128), (128, 34, 16)])
 def test_one_hot_rows_bit_exact(olamd, oracle, dev, bits, with_zp, K, N, block):
@@ -47,7 +48,7 @@ def test_one_hot_rows_bit_exact(olamd, oracle, dev, bits, with_zp, K, N, block):
     assert np.array_equal(tensor_bits(y), w_bits[rows]), "rows of W"
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("with_zp", [False, True])
 @pytest.mark.parametrize("M", [1, 8, 24])
 def test_random_vs_oracle_chain(olamd, oracle, dev, bits, with_zp, M):
@@ -80,8 +81,6 @@ def test_llama_mlp_shape_int4_with_zero_points(olamd, oracle, dev):
 def test_unsupported_and_invalid(olamd, oracle, dev):
     rng = np.random.default_rng(1)
     B, sb, zpk, _ = _weight(oracle, rng, 64, 8, 4, 16, True)
-    with pytest.raises(olamd.Unsupported, match="2-bit"):
-        olamd.prepare_matmul_nbits(np.zeros((8, 4, 4), np.uint8), sb, None, 64, 8, 2, 16)
     with pytest.raises(olamd.Unsupported, match="multiple of block_size"):  # the reference's K = 35 golden shape
         olamd.prepare_matmul_nbits(np.zeros((2, 3, 8), np.uint8), np.zeros((2, 3), np.uint16), None, 35, 2, 4, 16)
     with pytest.raises(olamd.InvalidArgument, match="power of two"):
