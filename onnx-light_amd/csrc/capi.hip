@@ -303,6 +303,31 @@ void ReadLeadingBytes(hipStream_t stream, int n, const onnxl_amd_tensor *const *
     if (readable(i) && ts[i]->location != ONNXL_AMD_HOST) std::memcpy(host[i], g_pinned + 8 * i, bytes[i]);
 }
 
+// Whether `stream` is being captured into a HIP graph: it cannot be
+// synchronised then, so device-resident scalars are left for the kernels to
+// read.
+bool Capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st == hipStreamCaptureStatusActive;
+}
+
+bool OnDevice(const onnxl_amd_tensor *t) { return t && t->data && t->location != ONNXL_AMD_HOST; }
+
+// The convolutions read their scalars on the host (they shape the padding
+// and select the kernel): under graph capture those must be host-resident.
+void RejectCapturedDeviceScalars(hipStream_t stream, std::initializer_list<const onnxl_amd_tensor *> ts,
+                                 const char *op) {
+  bool dev = false;
+  for (auto *t : ts) dev = dev || OnDevice(t);
+  if (dev && Capturing(stream))
+    throw Unsupported(Cat(op, ": device-resident scalar zero points and scales cannot be read while the stream is "
+                              "captured into a graph; pass them as host scalars."));
+}
+
 // An INT8 / UINT8 element's value from its byte.
 int32_t ByteInt(const onnxl_amd_tensor &t, uint8_t b) {
   return t.data_type == kInt8 ? (int32_t)(int8_t)b : (int32_t)b;
@@ -392,13 +417,20 @@ int MatMulInteger(const onnxl_amd_tensor *a, const onnxl_amd_tensor *b,
   // (a_per_row = a_size > 1, :118-119).
   const bool a_vec = a_present && a_count > 1;
   const bool b_vec = b_present && b_count > 1;
+  // Single zero points: read on the host, or under graph capture (no
+  // synchronisation possible) left on the device for the kernels to read.
+  const onnxl_amd_tensor *za_t = (a_present && !a_vec && a_count == 1) ? a_zp : nullptr;
+  const onnxl_amd_tensor *zb_t = (b_present && !b_vec && b_count == 1) ? b_zp : nullptr;
+  const bool in_place = Capturing(stream);
+  const bool dev_za = in_place && OnDevice(za_t), dev_zb = in_place && OnDevice(zb_t);
   int32_t za = 0, zb = 0;
-  ReadTwoZeroPoints(stream, (a_present && !a_vec && a_count == 1) ? a_zp : nullptr,
-                    (b_present && !b_vec && b_count == 1) ? b_zp : nullptr, za, zb);
+  ReadTwoZeroPoints(stream, dev_za ? nullptr : za_t, dev_zb ? nullptr : zb_t, za, zb);
   p.alpha_scalar = ca - za;
   p.beta_scalar = cb - zb;
-  p.need_cb = a_vec || p.alpha_scalar != 0;
-  p.need_ra = b_vec || p.beta_scalar != 0;
+  p.need_cb = a_vec || p.alpha_scalar != 0 || dev_za;
+  p.need_ra = b_vec || p.beta_scalar != 0 || dev_zb;
+  if (dev_za) p.dev.za = static_cast<const uint8_t *>(za_t->data);
+  if (dev_zb) p.dev.zb = static_cast<const uint8_t *>(zb_t->data);
   p.epilogue = kEpiInt32;
 
   Staging st(stream, 0, {a, b, a_vec ? a_zp : nullptr, b_vec ? b_zp : nullptr}, {y});
@@ -424,9 +456,11 @@ struct QlmScalars {
   float as, bs, ys;
 };
 
+// With `in_place`, device-resident ones are not read (their host slots stay
+// 0): the kernels read them (QDevScalars).
 QlmScalars QReadScalars(const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b_zp, const onnxl_amd_tensor *y_zp,
                         const onnxl_amd_tensor *a_s, const onnxl_amd_tensor *b_s, const onnxl_amd_tensor *y_s,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool in_place) {
   const onnxl_amd_tensor *ts[6] = {a_zp, b_zp, y_zp, a_s, b_s, y_s};
   const char *names[6] = {"a_zero_point", "b_zero_point", "y_zero_point", "a_scale", "b_scale", "y_scale"};
   for (int i = 0; i < 6; ++i) {
@@ -438,7 +472,9 @@ QlmScalars QReadScalars(const onnxl_amd_tensor *a_zp, const onnxl_amd_tensor *b_
   const size_t bytes[6] = {1, 1, 1, ts[3]->data_type == kFloat ? 4u : 2u, ts[4]->data_type == kFloat ? 4u : 2u,
                            ts[5]->data_type == kFloat ? 4u : 2u};
   uint8_t host[6][8] = {};
-  ReadLeadingBytes(stream, 6, ts, bytes, host);
+  const onnxl_amd_tensor *read[6];
+  for (int i = 0; i < 6; ++i) read[i] = in_place && OnDevice(ts[i]) ? nullptr : ts[i];
+  ReadLeadingBytes(stream, 6, read, bytes, host);
   QlmScalars r{};
   int32_t *zs[3] = {&r.za, &r.zb, &r.zy};
   for (int i = 0; i < 3; ++i) *zs[i] = ByteInt(*ts[i], host[i][0]);
@@ -478,18 +514,27 @@ int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
   OLA_ENFORCE(ShapeOf(*y) == plan.out_shape, kQlmName, ": preallocated output has invalid shape.");
   OLA_ENFORCE(y->size_bytes >= NumElements(plan.out_shape), kQlmName,
               ": preallocated output buffer size does not match its shape.");
-  const QlmScalars sc = QReadScalars(a_zp, b_zp, y_zp, a_scale, b_scale, y_scale, stream);
+  // Under graph capture the device-resident scalars are read by the kernels
+  // (no synchronisation); a zero y_scale among them is then not reported.
+  const bool in_place = Capturing(stream);
+  const QlmScalars sc = QReadScalars(a_zp, b_zp, y_zp, a_scale, b_scale, y_scale, stream, in_place);
   const int32_t za = sc.za, zb = sc.zb, zy = sc.zy;
   const float as = sc.as, bs = sc.bs, ys = sc.ys;
-  OLA_ENFORCE(ys != 0.0f, kQlmName, ": y_scale must be non-zero.");
+  const bool dev_za = in_place && OnDevice(a_zp), dev_zb = in_place && OnDevice(b_zp);
+  const bool dev_zy = in_place && OnDevice(y_zp);
+  const bool dev_scale = in_place && (OnDevice(a_scale) || OnDevice(b_scale) || OnDevice(y_scale));
+  OLA_ENFORCE(dev_scale || ys != 0.0f, kQlmName, ": y_scale must be non-zero.");
 
   // The reference accumulates in int64 (:187-191); the MFMA path is exact
-  // while |sum| < 2^31, guaranteed by K * max|a-za| * max|b-zb| < 2^31.
-  auto span = [](int32_t dt, int32_t z) -> int64_t {
+  // while |sum| < 2^31, guaranteed by K * max|a-za| * max|b-zb| < 2^31 (an
+  // unread zero point counts with its dtype's widest span, 255).
+  auto span = [](int32_t dt, int32_t z, bool unread) -> int64_t {
+    if (unread) return 255;
     const int64_t lo = dt == kInt8 ? -128 : 0, hi = dt == kInt8 ? 127 : 255;
     return std::max<int64_t>(std::llabs(lo - z), std::llabs(hi - z));
   };
-  const double bound = (double)plan.K * (double)span(a->data_type, za) * (double)span(b->data_type, zb);
+  const double bound =
+      (double)plan.K * (double)span(a->data_type, za, dev_za) * (double)span(b->data_type, zb, dev_zb);
   const bool exact32 = bound < 2147483648.0;  // else the int64-accumulating kernel
 
   IGemmParams p{};
@@ -512,6 +557,22 @@ int QLinearMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *a_scale,
   p.qmin = p.y_signed ? -128.0f : 0.0f;
   p.qmax = p.y_signed ? 127.0f : 255.0f;
   p.epilogue = kEpiQuant8;
+  if (dev_za) p.dev.za = static_cast<const uint8_t *>(a_zp->data);
+  if (dev_zb) p.dev.zb = static_cast<const uint8_t *>(b_zp->data);
+  if (dev_zy) p.dev.zy = static_cast<const uint8_t *>(y_zp->data);
+  if (dev_scale) {  // the quotient on the device, host-resident scales as values
+    p.dev.scales = 1;
+    p.dev.as = OnDevice(a_scale) ? a_scale->data : nullptr;
+    p.dev.bs = OnDevice(b_scale) ? b_scale->data : nullptr;
+    p.dev.ys = OnDevice(y_scale) ? y_scale->data : nullptr;
+    p.dev.as_f16 = a_scale->data_type == kFloat16;
+    p.dev.bs_f16 = b_scale->data_type == kFloat16;
+    p.dev.ys_f16 = y_scale->data_type == kFloat16;
+    p.dev.as_h = as;
+    p.dev.bs_h = bs;
+    p.dev.ys_h = ys;
+  }
+  if (dev_za || dev_zb) p.need_ra = p.need_cb = 1;
 
   Staging st(stream, 0, {a, b}, {y});
   p.A = static_cast<const int8_t *>(st.In(a));
@@ -984,6 +1045,8 @@ int ConvInteger(const onnxl_amd_tensor *x, const onnxl_amd_tensor *w, const onnx
   // :240-246: per-channel only for a 1-D zero point of length M
   const bool w_per_channel = wz_present && w_zp->rank == 1 && w_zp->dims[0] == M;
   int32_t xz = 0, wz = 0;
+  RejectCapturedDeviceScalars(stream, {xz_present ? x_zp : nullptr, wz_present && !w_per_channel ? w_zp : nullptr},
+                              kCiName);
   ReadTwoZeroPoints(stream, xz_present ? x_zp : nullptr, wz_present && !w_per_channel ? w_zp : nullptr, xz, wz);
   const bool gemm = (g.G == 1 || !w_per_channel) && g.Kc > 0;
   const bool implicit = gemm && ConvImplicit(g, *y);
@@ -1047,6 +1110,7 @@ int QLinearConv(const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale, cons
   const onnxl_amd_tensor *sts[5] = {x_zp, y_zp, x_scale, y_scale, w_zp_scalar ? w_zp : nullptr};
   const size_t sbytes[5] = {1, 1, 4, 4, 1};
   uint8_t shost[5][8] = {};
+  RejectCapturedDeviceScalars(stream, {sts[0], sts[1], sts[2], sts[3], sts[4]}, kQcName);
   ReadLeadingBytes(stream, 5, sts, sbytes, shost);
   const int32_t xz = ByteInt(*x_zp, shost[0][0]), yz = ByteInt(*y_zp, shost[1][0]);
   float xs, ys;

@@ -290,6 +290,7 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmKernel(const IGemmParams p) 
   // ---- epilogue: lane (lr, lg) of block (i, j) holds column j*32+lr,
   // rows (q/4)*8 + lg*4 + q%4 of register q ----
   const unsigned Ku = (unsigned)K;
+  const QResolved qv = ResolveQ(p.dev, p.a_u8, p.b_u8, p.y_signed, p.alpha_scalar, p.beta_scalar, p.cs, p.zy);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -298,14 +299,14 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmKernel(const IGemmParams p) 
       if (row >= M) continue;
       const unsigned alpha =
           p.a_zp ? (unsigned)(p.a_u8 ? 128 - (int)p.a_zp[row] : -(int)(int8_t)p.a_zp[row])
-                 : (unsigned)p.alpha_scalar;
+                 : (unsigned)qv.alpha;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int64_t col = col0 + wn * 64 + j * 32 + lr;
         if (col >= N) continue;
         const unsigned beta =
             p.b_zp ? (unsigned)(p.b_u8 ? 128 - (int)p.b_zp[col] : -(int)(int8_t)p.b_zp[col])
-                   : (unsigned)p.beta_scalar;
+                   : (unsigned)qv.beta;
         unsigned v = (unsigned)acc[i][j][q];
         if (NEED_RA) v += beta * (unsigned)ra[i][q];
         if (NEED_CB) v += alpha * (unsigned)cb[j][q];
@@ -314,8 +315,8 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmKernel(const IGemmParams p) 
         if (EPI == kEpiInt32) {
           reinterpret_cast<int32_t *>(p.Y)[yi] = (int32_t)v;
         } else {
-          float f = (float)(int32_t)v * p.cs;
-          f = __builtin_rintf(f) + p.zy;
+          float f = (float)(int32_t)v * qv.cs;
+          f = __builtin_rintf(f) + qv.zy;
           f = f < p.qmin ? p.qmin : (f > p.qmax ? p.qmax : f);
           if (p.y_signed) {
             reinterpret_cast<int8_t *>(p.Y)[yi] = (int8_t)(int)f;
@@ -523,6 +524,7 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): drain the look-ahead loads
 
   const unsigned Ku = (unsigned)K;
+  const QResolved qv = ResolveQ(p.dev, p.a_u8, p.b_u8, p.y_signed, p.alpha_scalar, p.beta_scalar, p.cs, p.zy);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -531,14 +533,14 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
       if (row >= M) continue;
       const unsigned alpha =
           p.a_zp ? (unsigned)(p.a_u8 ? 128 - (int)p.a_zp[row] : -(int)(int8_t)p.a_zp[row])
-                 : (unsigned)p.alpha_scalar;
+                 : (unsigned)qv.alpha;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int64_t col = col0 + wn * 64 + j * 32 + lr;
         if (col >= N) continue;
         const unsigned beta =
             p.b_zp ? (unsigned)(p.b_u8 ? 128 - (int)p.b_zp[col] : -(int)(int8_t)p.b_zp[col])
-                   : (unsigned)p.beta_scalar;
+                   : (unsigned)qv.beta;
         unsigned v = (unsigned)acc[i][j][q];
         if (NEED_RA) v += beta * (unsigned)ra[i][q];
         if (NEED_CB) v += alpha * (unsigned)cb[j][q];
@@ -547,8 +549,8 @@ __global__ __launch_bounds__(kThreads, 1) void IGemmLdsKernel(const IGemmParams 
         if (EPI == kEpiInt32) {
           reinterpret_cast<int32_t *>(p.Y)[yi] = (int32_t)v;
         } else {
-          float f = (float)(int32_t)v * p.cs;
-          f = __builtin_rintf(f) + p.zy;
+          float f = (float)(int32_t)v * qv.cs;
+          f = __builtin_rintf(f) + qv.zy;
           f = f < p.qmin ? p.qmin : (f > p.qmax ? p.qmax : f);
           if (p.y_signed) {
             reinterpret_cast<int8_t *>(p.Y)[yi] = (int8_t)(int)f;
@@ -650,6 +652,10 @@ namespace {
 constexpr int kXT = 16, kXK = 64;
 
 __global__ __launch_bounds__(256) void QlmExactKernel(const IGemmParams p, int32_t za, int32_t zb) {
+  // device-resident zero points and scales (p.dev) replace the host values
+  if (p.dev.za) za = p.a_u8 ? (int32_t)p.dev.za[0] : (int32_t)(int8_t)p.dev.za[0];
+  if (p.dev.zb) zb = p.b_u8 ? (int32_t)p.dev.zb[0] : (int32_t)(int8_t)p.dev.zb[0];
+  const QResolved qv = ResolveQ(p.dev, p.a_u8, p.b_u8, p.y_signed, 0, 0, p.cs, p.zy);
   __shared__ int32_t as[kXT][kXK + 1];
   __shared__ int32_t bs[kXK][kXT + 1];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -689,7 +695,7 @@ __global__ __launch_bounds__(256) void QlmExactKernel(const IGemmParams p, int32
     __syncthreads();
   }
   if (row < p.M && col < p.N) {
-    const float v = __builtin_rintf((float)acc * p.cs) + p.zy;
+    const float v = __builtin_rintf((float)acc * qv.cs) + qv.zy;
     const uint8_t q = v != v ? 0 : (uint8_t)(int32_t)__builtin_amdgcn_fmed3f(v, p.qmin, p.qmax);
     static_cast<uint8_t *>(p.Y)[(batch * p.M + row) * p.N + col] = q;
   }

@@ -26,6 +26,7 @@ inline mg::GemmArgs ToGemmArgs(const IGemmParams &p) {
   g.beta_scalar = p.beta_scalar;
   g.cs = p.cs;
   g.zy = p.zy;
+  g.dev = p.dev;
   g.qmin = p.qmin;
   g.qmax = p.qmax;
   g.y_signed = p.y_signed;

@@ -44,6 +44,49 @@ __host__ __device__ inline void BatchOffsets(const BatchMap &m, int64_t batch, i
 
 enum IGemmEpilogue : int { kEpiInt32 = 0, kEpiQuant8 = 1, kEpiQuant8Row = 2 };
 
+// Scalar zero points and scales that stay in device memory and are read by
+// the kernels themselves, so the call needs no host synchronisation (a call
+// captured in a HIP graph).  A null pointer keeps the value given on the
+// host in the launch parameters.
+struct QDevScalars {
+  const uint8_t *za, *zb, *zy;  // one byte in A's / B's / Y's dtype
+  const void *as, *bs, *ys;     // FLOAT, or FLOAT16 where the *_f16 flag is set
+  int as_f16, bs_f16, ys_f16;
+  // scales: the quotient is formed on the device, with the host value below
+  // for a scale whose pointer is null
+  int scales;
+  float as_h, bs_h, ys_h;
+};
+
+// The constants the GEMM epilogues use: alpha = ca - za, beta = cb - zb,
+// cs = (a_scale * b_scale) / y_scale in fp32 in that order
+// (kq/kernel_qlinearmatmul.cc:156) and zy as a float.
+struct QResolved {
+  int32_t alpha, beta;
+  float cs, zy;
+};
+
+__device__ inline float DevScale(const void *p, int f16) {
+  return f16 ? (float)*static_cast<const _Float16 *>(p) : *static_cast<const float *>(p);
+}
+
+// Host values (alpha, beta, cs, zy) overridden by the device-resident ones.
+__device__ inline QResolved ResolveQ(const QDevScalars &d, int a_u8, int b_u8, int y_signed, int32_t alpha,
+                                     int32_t beta, float cs, float zy) {
+  QResolved r{alpha, beta, cs, zy};
+  if (d.za) r.alpha = a_u8 ? 128 - (int32_t)d.za[0] : -(int32_t)(int8_t)d.za[0];
+  if (d.zb) r.beta = b_u8 ? 128 - (int32_t)d.zb[0] : -(int32_t)(int8_t)d.zb[0];
+  if (d.scales) {
+    const float sa = d.as ? DevScale(d.as, d.as_f16) : d.as_h;
+    const float sb = d.bs ? DevScale(d.bs, d.bs_f16) : d.bs_h;
+    const float sy = d.ys ? DevScale(d.ys, d.ys_f16) : d.ys_h;
+    const float ab = sa * sb;
+    r.cs = ab / sy;
+  }
+  if (d.zy) r.zy = (float)(y_signed ? (int32_t)(int8_t)d.zy[0] : (int32_t)d.zy[0]);
+  return r;
+}
+
 // Implicit convolution operand: B is not a [K, N] matrix but one image of the
 // zero-point-padded input in NHWC order, [Hp, Wp, C] bytes, and K runs over
 // (kernel tap, channel) with C % 128 == 0, so a K step of 128 bytes is 128
@@ -81,6 +124,9 @@ struct IGemmParams {
   float cs, zy, qmin, qmax;
   int y_signed;
   int epilogue;
+  // Device-resident scalars replacing alpha_scalar, beta_scalar, cs and zy
+  // (kEpiInt32 / kEpiQuant8); need_cb / need_ra are set when za / zb is one.
+  QDevScalars dev;
   // kEpiQuant8Row (pipelined kernel only): row r uses the scale
   // row_xs * row_wscale[r or 0] / row_ys and adds row_bias[r] (if not null)
   // to the int32 sum exactly before the conversion.
@@ -96,8 +142,8 @@ struct IGemmParams {
 void LaunchIGemm(const IGemmParams &p, hipStream_t stream);
 // QLinearMatMul where the int32 MFMA sums can overflow: int64 accumulation
 // (kq/kernel_qlinearmatmul.cc:187-191) in a VALU kernel; uses p.A, p.B, p.Y,
-// M, N, K, batch, bm, a_u8, b_u8, cs, zy, qmin, qmax, y_signed and the zero
-// points za, zb given here.
+// M, N, K, batch, bm, a_u8, b_u8, cs, zy, qmin, qmax, y_signed, dev and the
+// zero points za, zb given here (replaced by dev.za / dev.zb when set).
 void LaunchQlmExact(const IGemmParams &p, int32_t za, int32_t zb, hipStream_t stream);
 // Whether LaunchIGemm takes the pipelined MFMA kernel for p (kEpiQuant8Row
 // requires it).

@@ -178,6 +178,7 @@ struct GemmArgs {
   int32_t alpha_scalar, beta_scalar;
   float cs, zy, qmin, qmax;
   int y_signed;
+  QDevScalars dev;  // device-resident scalars replacing the four above (kI8 with ZP)
   // kBf16F8: dequantization scales (FLOAT or FLOAT16), one per column
   // (scale_per_col) or a single value
   const void *scale;
@@ -762,17 +763,21 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   // (mod 2^32); below K = 21845 every factor fits 24 signed bits, and the
   // full-rate 24-bit multiplies give the same low 32 bits.
   const bool mul24 = K < 21845;
+  // the scalar constants, read here (after the last load of the ring) when
+  // they are device-resident
+  QResolved qv{p.alpha_scalar, p.beta_scalar, p.cs, p.zy};
+  if constexpr (KIND == kI8) qv = ResolveQ(p.dev, p.a_u8, p.b_u8, p.y_signed, p.alpha_scalar, p.beta_scalar, p.cs, p.zy);
   int32_t *zc = zsum + (KIND == kI8 && ZP ? wave * 2 * kWN : 0);
   int zrow[4] = {0, 0, 0, 0};
   if constexpr (KIND == kI8 && ZP) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      zrow[i] = p.a_zp ? (p.a_u8 ? 128 - (int)za[i] : -(int)(int8_t)za[i]) : p.alpha_scalar;
+      zrow[i] = p.a_zp ? (p.a_u8 ? 128 - (int)za[i] : -(int)(int8_t)za[i]) : qv.alpha;
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
       const int v = csum[j] + __shfl_xor(csum[j], 32);
       if (lg == 0) {
-        const int be = p.b_zp ? (p.b_u8 ? 128 - (int)zb[j] : -(int)(int8_t)zb[j]) : p.beta_scalar;
+        const int be = p.b_zp ? (p.b_u8 ? 128 - (int)zb[j] : -(int)(int8_t)zb[j]) : qv.beta;
         zc[j * 32 + lr] = (int)((unsigned)v + (unsigned)K * (unsigned)be);  // CB + K beta (mod 2^32)
         zc[kWN + j * 32 + lr] = be;
       }
@@ -808,7 +813,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   char *stg = (wave >> 1 ? sa2 : sa1) + (wave & 1) * 16384;
   // QLinearMatMul requantization constants (signed outputs biased by 128)
   const float q_bias = p.y_signed ? 128.f : 0.f;
-  const float q_zy = p.zy + q_bias, q_lo = p.qmin + q_bias, q_hi = p.qmax + q_bias;
+  const float q_zy = qv.zy + q_bias, q_lo = p.qmin + q_bias, q_hi = p.qmax + q_bias;
   const unsigned q_flip = p.y_signed ? 0x80808080u : 0u;
   // Grouped mode with a bias: the bias of this lane's columns (4 per
   // (j, g) register group, the output dtype's bits).  GroupedMatMul adds it
@@ -838,7 +843,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
     // kOutQ8Row: this lane's output row (row0 + wm * 128 + 32 i + lr) scale
     // and bias (loaded before the K loop), computed with the fp32 operations
     // of the reference
-    float cs_r = p.cs;
+    float cs_r = qv.cs;
     double bias_r = 0.0;
     if constexpr (OUT == kOutQ8Row) {
       cs_r = p.row_xs * row_ws[i] / p.row_ys;
@@ -881,7 +886,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
                 f = __builtin_rintf((float)((double)(int32_t)v[e] + bias_r) * cs_r) + q_zy;
                 if (f != f) f = q_bias;
               } else {
-                f = __builtin_rintf((float)(int32_t)v[e] * p.cs) + q_zy;
+                f = __builtin_rintf((float)(int32_t)v[e] * qv.cs) + q_zy;
               }
               packed = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(f, q_lo, q_hi), e, packed);
             }
