@@ -874,7 +874,7 @@ private:
 // MatMul(A, Transpose(DequantizePacked(x, format, shape, FLOAT16))), the
 // chain onnx_core/runtime/dequantize_packed.cc:334-372 -> km/kernel_matmul.cc.
 // Every GGUF profile and M runs in the one entry point: the fused decode
-// GEMVs (q4_0, q8_0, q4_k, q6_k at M <= 8), else the weight decoded to
+// GEMVs (q4_0, q8_0, q2_k-q6_k, iq4_xs at M <= 8), else the weight decoded to
 // FLOAT16 [N, K] on the device and multiplied by the MFMA GEMM reading its
 // rows, with no transpose written and nothing staged on the host.
 class Mi355xDequantizePackedMatMul : public Mi355xKernel {

@@ -17,14 +17,16 @@ oracle (a restatement of the reference kernel, single core as the reference
 runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
-                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q4k|pkgemv_q6k|awq|moe]
+                   c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q2k|pkgemv_q3k|pkgemv_q4k|pkgemv_q5k|
+                   pkgemv_q6k|pkgemv_iq4xs|awq|moe]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
 integer GEMMs (QuantizeLinear `q8`, DynamicQuantizeLinear `dql`, both on
 configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
-GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q4_k / q6_k GEMVs
-(`pkgemv`, `pkgemv8`, `pkgemv_q4k`, `pkgemv_q6k`), an AWQ gemm 4-bit
+GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q2_k / q3_k / q4_k /
+q5_k / q6_k / iq4_xs GEMVs (`pkgemv`, `pkgemv8`, `pkgemv_q2k`, `pkgemv_q3k`,
+`pkgemv_q4k`, `pkgemv_q5k`, `pkgemv_q6k`, `pkgemv_iq4xs`), an AWQ gemm 4-bit
 checkpoint prepared for the fused decode GEMV (`awq`) and a Mixtral-shaped
 MoE GroupedMatMul (`moe`) are timed too and
 reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
@@ -249,14 +251,17 @@ def make_pk(olamd, dev, replicas):
     return w
 
 
-PKGEMV_KEYS = {"q4_0": "pkgemv", "q8_0": "pkgemv8", "q4_k": "pkgemv_q4k", "q6_k": "pkgemv_q6k"}
-PK_BLOCK = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210)}  # values, bytes
+PKGEMV_KEYS = {"q4_0": "pkgemv", "q8_0": "pkgemv8", "q2_k": "pkgemv_q2k", "q3_k": "pkgemv_q3k",
+               "q4_k": "pkgemv_q4k", "q5_k": "pkgemv_q5k", "q6_k": "pkgemv_q6k", "iq4_xs": "pkgemv_iq4xs"}
+PK_BLOCK = {"q4_0": (32, 18), "q8_0": (32, 34), "q2_k": (256, 84), "q3_k": (256, 110), "q4_k": (256, 144),
+            "q5_k": (256, 176), "q6_k": (256, 210), "iq4_xs": (256, 136)}  # values, bytes
+PK_D_AT = {"q2_k": 80, "q3_k": 108, "q6_k": 208}  # byte offset of the fp16 d (else 0)
 
 
 def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
     """Fused GEMV y[1, 14336] = a[1, 4096] @ DequantizePacked(gguf:<fmt>,
-    [14336, 4096], FLOAT16)^T: the weight's 18 (q4_0) or 34 (q8_0) bytes per
-    32 values, or 144 (q4_k) or 210 (q6_k) per 256, dominate."""
+    [14336, 4096], FLOAT16)^T: the weight's bytes per block (PK_BLOCK)
+    dominate."""
     import torch
     w = Workload()
     per, block_bytes = PK_BLOCK[fmt]
@@ -268,12 +273,12 @@ def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
     w.work = float(w.nbytes)
     rng = np.random.default_rng(41)
     blocks = rng.integers(0, 256, (N * K // per, block_bytes)).astype(np.uint8)
-    at = 208 if fmt == "q6_k" else 0  # the fp16 d
+    at = PK_D_AT.get(fmt, 0)  # the fp16 d
     d = np.float16(rng.uniform(0.001, 0.05, N * K // per)).view(np.uint16)
     blocks[:, at], blocks[:, at + 1] = d & 255, d >> 8
-    if fmt == "q4_k":  # dmin
+    if fmt in ("q2_k", "q4_k", "q5_k"):  # dmin follows d
         m = np.float16(rng.uniform(0.001, 0.05, N * K // per)).view(np.uint16)
-        blocks[:, 2], blocks[:, 3] = m & 255, m >> 8
+        blocks[:, at + 2], blocks[:, at + 3] = m & 255, m >> 8
     a = _t(np.float16(rng.standard_normal((1, K))), dev)
     w.calls = []
     for _ in range(replicas):
@@ -691,7 +696,8 @@ def value_of(w, ms):
 
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
-             "pkgemv8", "pkgemv_q4k", "pkgemv_q6k", "awq", "moe")
+             "pkgemv8", "pkgemv_q2k", "pkgemv_q3k", "pkgemv_q4k", "pkgemv_q5k", "pkgemv_q6k", "pkgemv_iq4xs", "awq",
+             "moe")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
                  "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
 
@@ -748,8 +754,8 @@ def main():
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 18))
         if key == "pkgemv8":
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 32 * 34), "q8_0")
-        if key in ("pkgemv_q4k", "pkgemv_q6k"):
-            fmt = "q4_k" if key == "pkgemv_q4k" else "q6_k"
+        if key in PKGEMV_KEYS.values():
+            fmt = next(f for f, k in PKGEMV_KEYS.items() if k == key)
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 256 * PK_BLOCK[fmt][1]), fmt)
         if key == "awq":
             return make_awq(olamd, dev, args.replicas or 24)

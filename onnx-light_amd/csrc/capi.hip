@@ -1274,7 +1274,8 @@ int DequantizePacked(const onnxl_amd_tensor *x, const char *format, const int64_
 // weight transposed: y = a @ W^T.  No single reference kernel: it computes
 // the chain dequantize_packed.cc:334-372 -> km/kernel_matmul.cc:181-223 that a
 // DequantizePacked -> Transpose -> MatMul subgraph runs node by node.
-//  - decode GEMVs (1 <= M <= 8) fused for q4_0, q8_0, q4_k and q6_k;
+//  - decode GEMVs (1 <= M <= 8) fused for q4_0, q8_0, q2_k, q3_k, q4_k, q5_k,
+//    q6_k and iq4_xs;
 //  - every other format, M or alignment: the weight decoded to FLOAT16 [N, K]
 //    in the workspace (the chain's rounding), then the 16-bit MFMA GEMM
 //    reading its rows as the B operand (no transpose is written).
@@ -1302,23 +1303,23 @@ int DequantizePackedMatMul(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x,
               "DequantizePacked: packed input length must match exactly.");
   if (M == 0 || N == 0) return ONNXL_AMD_OK;  // empty [M, N] result, nothing to launch
   const int t = prof->ggml_type;
-  const bool q40 = t == 2, q80 = t == 8, q4k = t == 12, q6k = t == 14;
-  // the fused GEMVs take these when the operands are aligned (checked on the
-  // device addresses below)
-  const bool gemv_format = (q40 || q80 || q4k || q6k) && M <= 8 && K > 0;
-  const bool aligned_a = a->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(a->data) % 16 == 0;
-  const bool aligned_x = x->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(x->data) % 16 == 0;
-  const bool try_gemv = gemv_format && (q40 || q80 ? K % 64 == 0 : true) && aligned_a &&
-                        (aligned_x || (q6k && reinterpret_cast<uintptr_t>(x->data) % 2 == 0) ||
-                         ((q40 || q80) && reinterpret_cast<uintptr_t>(x->data) % 4 == 0));
+  const bool q40 = t == 2, q80 = t == 8;
+  const int k_align = GemvKAlignment(t);  // the 256-value formats with a fused GEMV
+  // the fused GEMVs take these when the operands are aligned (host payloads
+  // are staged into aligned scratch)
+  const bool gemv_format = (q40 || q80 || k_align > 0) && M <= 8 && K > 0;
+  auto aligned = [](const onnxl_amd_tensor *t, int b) {
+    return t->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(t->data) % b == 0;
+  };
+  const bool try_gemv = gemv_format && (q40 || q80 ? K % 64 == 0 : true) && aligned(a, 16) &&
+                        aligned(x, q40 || q80 ? 4 : k_align);
   const int64_t w_bytes = try_gemv ? 0 : N * K * 2;
   Staging st(stream, (size_t)w_bytes, {a, x}, {y});
   const void *ad = st.In(a), *xd = st.In(x);
   uint16_t *yd = static_cast<uint16_t *>(st.Out(y));
   if (try_gemv) {
-    if (q4k || q6k)
-      LaunchGemvK(q4k ? 12 : 14, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K, yd,
-                  stream);
+    if (k_align > 0)
+      LaunchGemvK(t, static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M, N, K, yd, stream);
     else
       (q80 ? LaunchGemvQ80 : LaunchGemvQ40)(static_cast<const uint16_t *>(ad), static_cast<const uint8_t *>(xd), M,
                                            N, K, yd, stream);

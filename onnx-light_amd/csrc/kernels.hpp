@@ -162,9 +162,12 @@ bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w);
 void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t stream);
 // The same for gguf:q8_0 (same eligibility).
-// Fused q4_k (ggml type 12) / q6_k (14) GEMV, K % 256 == 0, M <= 8, a 16-byte aligned.
+// Fused 256-value GEMVs: q2_k (ggml type 10), q3_k (11), q4_k (12), q5_k
+// (13), q6_k (14) and iq4_xs (23); K % 256 == 0, M <= 8, a 16-byte aligned,
+// w aligned to GemvKAlignment(type) bytes (0: no fused GEMV for the type).
 void LaunchGemvK(int ggml_type, const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                  hipStream_t s);
+int GemvKAlignment(int ggml_type);
 void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t stream);
 

@@ -176,8 +176,12 @@ __device__ __forceinline__ void DecodeQ6K8(const uint8_t *p, int i0, float v[8])
 }
 
 template <int TYPE> struct KLayout;
-template <> struct KLayout<12> { static constexpr int bytes = 144; };
-template <> struct KLayout<14> { static constexpr int bytes = 210; };
+template <> struct KLayout<10> { static constexpr int bytes = 84; };   // q2_k
+template <> struct KLayout<11> { static constexpr int bytes = 110; };  // q3_k
+template <> struct KLayout<12> { static constexpr int bytes = 144; };  // q4_k
+template <> struct KLayout<13> { static constexpr int bytes = 176; };  // q5_k
+template <> struct KLayout<14> { static constexpr int bytes = 210; };  // q6_k
+template <> struct KLayout<23> { static constexpr int bytes = 136; };  // iq4_xs
 
 template <int TYPE> __device__ __forceinline__ void DecodeK8(const uint8_t *p, int i0, float v[8]) {
   if constexpr (TYPE == 12) DecodeQ4K8(p, i0, v);
@@ -805,6 +809,145 @@ __device__ __forceinline__ void DecodeK(const KRaw<14> &r, int i0, h2_t wp[4]) {
   }
 }
 
+// q2_k, q3_k, q5_k and iq4_xs (field positions of DecodeX above).  A lane's
+// 8 values share one sub-block, so each needs one scale (and minimum) and
+// 8 consecutive code bytes per plane.
+template <> struct KRaw<10> {
+  uint32_t q[2];  // 8 bytes of 2-bit codes
+  uint32_t sc;    // the dword holding the sub-block's scale / minimum byte
+  uint32_t dd;    // fp16 d, fp16 dmin
+};
+template <> struct KRaw<11> {
+  uint32_t hm[2], q[2];  // 8 high-mask bytes, 8 bytes of 2-bit codes
+  uint32_t s;            // scale low-nibble byte | 2-bit byte << 8 | fp16 d << 16
+};
+template <> struct KRaw<13> {
+  uint32_t h[4];   // d, dmin, the 12 scale bytes
+  uint32_t hb[2];  // 8 high-bit bytes
+  uint32_t q[2];   // 8 nibble bytes
+};
+template <> struct KRaw<23> {
+  uint32_t hdr[2];  // fp16 d | high scale bits << 16, the 4 low-nibble scale bytes
+  uint32_t q[2];    // 8 nibble bytes
+};
+
+__device__ __forceinline__ uint32_t ByteOf(const uint32_t w[2], int e) { return (w[e >> 2] >> (8 * (e & 3))) & 0xffu; }
+
+// q2_k blocks are 4-byte aligned (84 = 4 x 21).
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<10> &r) {
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(p);
+  const int qo = (16 + (i0 >> 7) * 32 + (i0 & 31)) >> 2;
+  r.q[0] = w[qo], r.q[1] = w[qo + 1];
+  r.sc = w[i0 >> 6];  // byte i0 / 16 of the 16 scale bytes
+  r.dd = w[20];       // bytes 80 .. 83
+}
+
+// q3_k blocks are 2-byte aligned (110 bytes).
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<11> &r) {
+  const uint16_t *h = reinterpret_cast<const uint16_t *>(p + (i0 & 31));
+  const uint16_t *q = reinterpret_cast<const uint16_t *>(p + 32 + (i0 >> 7) * 32 + (i0 & 31));
+  r.hm[0] = h[0] | (uint32_t)h[1] << 16, r.hm[1] = h[2] | (uint32_t)h[3] << 16;
+  r.q[0] = q[0] | (uint32_t)q[1] << 16, r.q[1] = q[2] | (uint32_t)q[3] << 16;
+  const int g = i0 >> 4;
+  r.s = p[96 + (g & 7)] | (uint32_t)p[104 + (g & 3)] << 8 |
+        (uint32_t)*reinterpret_cast<const uint16_t *>(p + 108) << 16;
+}
+
+// q5_k blocks are 16-byte aligned (176 = 16 x 11).
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<13> &r) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  const v4u hdr = *reinterpret_cast<const v4u *>(p);
+  const v2u hb = *reinterpret_cast<const v2u *>(p + 16 + (i0 & 31));
+  const v2u q = *reinterpret_cast<const v2u *>(p + 48 + (i0 >> 6) * 32 + (i0 & 31));
+  r.h[0] = hdr.x, r.h[1] = hdr.y, r.h[2] = hdr.z, r.h[3] = hdr.w;
+  r.hb[0] = hb.x, r.hb[1] = hb.y, r.q[0] = q.x, r.q[1] = q.y;
+}
+
+// iq4_xs blocks are 8-byte aligned (136 = 8 x 17).
+__device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<23> &r) {
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  const v2u hdr = *reinterpret_cast<const v2u *>(p);
+  const v2u q = *reinterpret_cast<const v2u *>(p + 8 + (i0 >> 5) * 16 + (i0 & 15));
+  r.hdr[0] = hdr.x, r.hdr[1] = hdr.y, r.q[0] = q.x, r.q[1] = q.y;
+}
+
+// The products below are exact in fp32 wherever the reference rounds them
+// (a 11-bit fp16 d times a scale of at most 6 bits, times a code of at most
+// 5 bits), so ds * q - dm in one fused multiply-add, or ds * q, rounds as the
+// reference's separately rounded steps do; iq4_xs's ds * value (8-bit
+// values) is one rounded product, as in the reference.
+__device__ __forceinline__ void DecodeK(const KRaw<10> &r, int i0, h2_t wp[4]) {
+  const float d = F16ToF32((uint16_t)(r.dd & 0xffffu)), dmin = F16ToF32((uint16_t)(r.dd >> 16));
+  const uint32_t b = (r.sc >> (8 * ((i0 >> 4) & 3))) & 0xffu;
+  const float ds = d * (float)(b & 15u), dm = dmin * (float)(b >> 4);
+  const int sh = 2 * ((i0 >> 5) & 3);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(ds, (float)((ByteOf(r.q, e) >> sh) & 3u), -dm);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
+}
+
+__device__ __forceinline__ void DecodeK(const KRaw<11> &r, int i0, h2_t wp[4]) {
+  const int g = i0 >> 4;
+  const int lo = (int)((r.s & 0xffu) >> (4 * ((g >> 3) & 1))) & 15;
+  const int hi = (int)(((r.s >> 8) & 0xffu) >> (2 * ((g >> 2) & 3))) & 3;
+  const float ds = F16ToF32((uint16_t)(r.s >> 16)) * (float)((lo | hi << 4) - 32);
+  const int hsh = (i0 >> 5) & 7, qsh = 2 * ((i0 >> 5) & 3);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int q = (int)((ByteOf(r.q, e) >> qsh) & 3u) - ((ByteOf(r.hm, e) >> hsh) & 1u ? 0 : 4);
+    v[e] = ds * (float)q;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
+}
+
+__device__ __forceinline__ void DecodeK(const KRaw<13> &r, int i0, h2_t wp[4]) {
+  const float d = F16ToF32((uint16_t)(r.h[0] & 0xffffu)), dmin = F16ToF32((uint16_t)(r.h[0] >> 16));
+  const int g = i0 >> 5;
+  const int sh8 = 8 * (g & 3);  // scale bytes as in q4_k
+  const uint32_t b1 = (r.h[1] >> sh8) & 0xffu, b2 = (r.h[2] >> sh8) & 0xffu, b3 = (r.h[3] >> sh8) & 0xffu;
+  const uint32_t scale = g < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
+  const uint32_t minimum = g < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+  const float ds = d * (float)scale, dm = dmin * (float)minimum;
+  const int nsh = 4 * (g & 1), hsh = g & 7;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t q = ((ByteOf(r.q, e) >> nsh) & 15u) | (((ByteOf(r.hb, e) >> hsh) & 1u) << 4);
+    v[e] = __builtin_fmaf(ds, (float)q, -dm);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
+}
+
+__device__ __forceinline__ void DecodeK(const KRaw<23> &r, int i0, h2_t wp[4]) {
+  const int g = i0 >> 5;
+  const float d = F16ToF32((uint16_t)(r.hdr[0] & 0xffffu));
+  const uint32_t high = r.hdr[0] >> 16;
+  const int lo = (int)(r.hdr[1] >> (8 * (g >> 1) + 4 * (g & 1))) & 15;
+  const float ds = d * (float)((lo | (int)(((high >> (2 * g)) & 3u) << 4)) - 32);
+  const int sh = 4 * ((i0 >> 4) & 1);
+  float v[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // the 16 codebook values as bytes; v_perm picks 4 at once (codes 0-7 from
+    // the low pair, 8-15 from the high pair, merged by bit 3)
+    const uint32_t codes = (r.q[h] >> sh) & 0x0f0f0f0fu, sel = codes & 0x07070707u;
+    const uint32_t lo4 = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);
+    const uint32_t hi4 = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);
+    const uint32_t pick = ((codes >> 3) & 0x01010101u) * 0xffu;
+    const uint32_t vals = (hi4 & pick) | (lo4 & ~pick);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * h + e] = ds * (float)(int8_t)(uint8_t)(vals >> (8 * e));
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
+}
+
 template <int TYPE, int M>
 __global__ __launch_bounds__(256) void GemvKKernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
                                                    int64_t N, int64_t K, uint16_t *__restrict__ y) {
@@ -890,8 +1033,25 @@ void LaunchGemvKType(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, 
 void LaunchGemvK(int ggml_type, const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                  hipStream_t s) {
   if (N == 0) return;
-  if (ggml_type == 12) LaunchGemvKType<12>(a, w, M, N, K, y, s);
-  else LaunchGemvKType<14>(a, w, M, N, K, y, s);
+  switch (ggml_type) {
+  case 10: LaunchGemvKType<10>(a, w, M, N, K, y, s); break;
+  case 11: LaunchGemvKType<11>(a, w, M, N, K, y, s); break;
+  case 12: LaunchGemvKType<12>(a, w, M, N, K, y, s); break;
+  case 13: LaunchGemvKType<13>(a, w, M, N, K, y, s); break;
+  case 14: LaunchGemvKType<14>(a, w, M, N, K, y, s); break;
+  case 23: LaunchGemvKType<23>(a, w, M, N, K, y, s); break;
+  default: throw DeviceError("internal: no fused GEMV for this GGUF type");
+  }
+}
+
+int GemvKAlignment(int ggml_type) {
+  switch (ggml_type) {
+  case 10: return 4;
+  case 11: case 14: return 2;
+  case 12: case 13: return 16;
+  case 23: return 8;
+  default: return 0;
+  }
 }
 
 void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,

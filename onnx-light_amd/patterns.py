@@ -48,7 +48,8 @@ PACKED_FUSED_OP = "DequantizePackedMatMul"
 ENCODED_FUSED_OP = "DequantizeEncodedMatMul"
 # the 27 GGUF profiles of DequantizePacked (format: values per block); the
 # fused node runs every one of them on the GPU (decode GEMVs for q4_0, q8_0,
-# q4_k and q6_k, the decoded weight through the MFMA GEMM otherwise)
+# q2_k, q3_k, q4_k, q5_k, q6_k and iq4_xs, the decoded weight through the
+# MFMA GEMM otherwise)
 _PACKED_FORMATS = {f: 32 for f in ("gguf:q4_0", "gguf:q4_1", "gguf:q5_0", "gguf:q5_1", "gguf:q8_0", "gguf:q8_1",
                                    "gguf:iq4_nl", "gguf:mxfp4")}
 _PACKED_FORMATS.update({f: 256 for f in ("gguf:q2_k", "gguf:q3_k", "gguf:q4_k", "gguf:q5_k", "gguf:q6_k",
@@ -231,11 +232,9 @@ class DequantizePackedMatMulPattern(PatternOptimization):
     a constant x -> Transpose(perm = [1, 0]) -> MatMul's second input, with a
     FLOAT16 A -> one fused node ``ai.rt.amd:DequantizePackedMatMul(A, x)``
     with attributes format and shape, computed by
-    ``dequantize_packed_matmul``.  Only the formats the fused GEMVs decode
-    (q4_0 and q8_0 with K % 64 == 0, q4_k and q6_k with K % 256 == 0) are
-    rewritten; the GEMV takes up to 8 rows
-    of A, and a session adapter runs the chain for taller A (the row count is
-    only known at run time)."""
+    ``dequantize_packed_matmul``, which runs every GGUF profile and row count
+    on the device (fused decode GEMVs up to 8 rows of A, the decoded weight
+    through the MFMA GEMM otherwise)."""
     device = "gpu"
 
     def fast_op_type(self) -> set:

@@ -119,10 +119,11 @@ def _f16_bytes(oracle, v):
 
 def gguf_blocks(oracle, rng, fmt, N, K):
     """Random GGUF blocks of a [N, K] weight whose values are small integers
-    times a power-of-two d (fp16 scales 2^-4 .. 2^-6; q4_k with dmin = d,
-    sub-block scales 1..3 and minima 0..7; q6_k sub-block scales +-1..+-3;
-    q8_0 codes in [-16, 16]): the chain's fp32 decode steps and its FLOAT16
-    rounding are then exact."""
+    times a power-of-two d (fp16 scales 2^-4 .. 2^-6; q2_k, q4_k and q5_k
+    with dmin = d and small sub-block scales and minima; q3_k and q6_k
+    sub-block scales +-1..+-3; iq4_xs scales +-1, +-2; q8_0 codes in
+    [-16, 16]): the chain's fp32 decode steps and its FLOAT16 rounding are
+    then exact."""
     size = oracle.packed_block_bytes(fmt)
     nb = N * K // oracle.packed_block_values(fmt)
     x = rng.integers(0, 256, (nb, size)).astype(np.uint8)
@@ -147,6 +148,42 @@ def gguf_blocks(oracle, rng, fmt, N, K):
         x[:, 208], x[:, 209] = lo, hi
         s = rng.integers(1, 4, (nb, 16)) * np.where(rng.random((nb, 16)) < 0.5, -1, 1)
         x[:, 192:208] = s.astype(np.int8).view(np.uint8)
+    elif fmt == "gguf:q2_k":
+        # d = dmin; byte g of the 16: scale 1..3 (low nibble), minimum 0..3
+        x[:, 80], x[:, 81], x[:, 82], x[:, 83] = lo, hi, lo, hi
+        x[:, :16] = (rng.integers(1, 4, (nb, 16)) | (rng.integers(0, 4, (nb, 16)) << 4)).astype(np.uint8)
+    elif fmt == "gguf:q3_k":
+        # 6-bit scales s + 32 (s = +-1..+-3) of the 16 sub-blocks: low nibble
+        # of sub-block g in byte 96 + g % 8 (bits 4 (g / 8)), its two high bits
+        # in byte 104 + g % 4 (bits 2 ((g / 4) % 4))
+        x[:, 108], x[:, 109] = lo, hi
+        s = rng.integers(1, 4, (nb, 16)) * np.where(rng.random((nb, 16)) < 0.5, -1, 1) + 32
+        x[:, 96:108] = 0
+        for g in range(16):
+            x[:, 96 + g % 8] |= ((s[:, g] & 15) << (4 * (g // 8))).astype(np.uint8)
+            x[:, 104 + g % 4] |= ((s[:, g] >> 4) << (2 * ((g // 4) % 4))).astype(np.uint8)
+    elif fmt == "gguf:q5_k":
+        x[:, 0], x[:, 1], x[:, 2], x[:, 3] = lo, hi, lo, hi  # d = dmin, scales as q4_k's
+        sc = rng.integers(1, 3, (nb, 8))
+        mn = rng.integers(0, 8, (nb, 8))
+        x[:, 4:8] = sc[:, :4]
+        x[:, 8:12] = mn[:, :4]
+        x[:, 12:16] = (sc[:, 4:] | (mn[:, 4:] << 4)).astype(np.uint8)
+    elif fmt == "gguf:iq4_xs":
+        # sub-block scales s + 32 (s = +-1, +-2): low nibbles in bytes 4..7,
+        # two high bits each in the 16-bit word at byte 2; codes restricted to
+        # the codebook values of magnitude 49..127 (a wider spread would leave
+        # a dropped small term below an output ulp)
+        x[:, 0], x[:, 1] = lo, hi
+        s = rng.integers(1, 3, (nb, 8)) * np.where(rng.random((nb, 8)) < 0.5, -1, 1) + 32
+        high = np.zeros(nb, np.int64)
+        x[:, 4:8] = 0
+        for g in range(8):
+            x[:, 4 + g // 2] |= ((s[:, g] & 15) << (4 * (g % 2))).astype(np.uint8)
+            high |= (s[:, g] >> 4) << (2 * g)
+        x[:, 2], x[:, 3] = high & 255, high >> 8
+        codes = np.array([0, 1, 2, 3, 4, 12, 13, 14, 15])[rng.integers(0, 9, (nb, 256))]
+        x[:, 8:] = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)  # any nibble order: every code is kept
     else:
         raise ValueError(fmt)
     x = x.reshape(-1)

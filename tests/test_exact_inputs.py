@@ -54,7 +54,8 @@ def test_int4_case_c3_depth(oracle, dt, signed, zp, block):
     _check(oracle, case, 13)
 
 
-@pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0", "gguf:q4_k", "gguf:q6_k"])
+@pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0", "gguf:q2_k", "gguf:q3_k", "gguf:q4_k", "gguf:q5_k",
+                                 "gguf:q6_k", "gguf:iq4_xs"])
 def test_gguf_case(oracle, fmt):
     case = dy.gguf_case(oracle, np.random.default_rng(4), 4, 4096, 256, fmt)
     _check(oracle, case, 14)

@@ -196,7 +196,8 @@ def test_int4_gemv_one_hot_rows_all_k(olamd, oracle, dev, layout):
 
 # ---- packed GGUF GEMVs ------------------------------------------------------
 
-@pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0", "gguf:q4_k", "gguf:q6_k"])
+@pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0", "gguf:q2_k", "gguf:q3_k", "gguf:q4_k", "gguf:q5_k",
+                                 "gguf:q6_k", "gguf:iq4_xs"])
 @pytest.mark.parametrize("M,N", [(1, 14336), (8, 2048), (40, 512)])
 def test_packed_gemv_dyadic_bit_exact(olamd, oracle, dev, fmt, M, N):
     """The fused GEMVs (M <= 8) and the general path (M = 40: the weight
@@ -209,8 +210,9 @@ def test_packed_gemv_dyadic_bit_exact(olamd, oracle, dev, fmt, M, N):
     _assert_exact(got, _chain_rows(oracle, case, np.arange(M)), f"{fmt} GEMV, oracle chain")
 
 
-@pytest.mark.parametrize("fmt,block_bytes", [("gguf:q4_0", 18), ("gguf:q8_0", 34), ("gguf:q4_k", 144),
-                                             ("gguf:q6_k", 210)])
+@pytest.mark.parametrize("fmt,block_bytes", [("gguf:q4_0", 18), ("gguf:q8_0", 34), ("gguf:q2_k", 84),
+                                             ("gguf:q3_k", 110), ("gguf:q4_k", 144), ("gguf:q5_k", 176),
+                                             ("gguf:q6_k", 210), ("gguf:iq4_xs", 136)])
 def test_packed_gemv_one_hot_rows_all_k(olamd, oracle, dev, fmt, block_bytes):
     """Random blocks (random finite fp16 scales), every k of K read back by
     one-hot rows, 8 per call."""
@@ -218,12 +220,12 @@ def test_packed_gemv_one_hot_rows_all_k(olamd, oracle, dev, fmt, block_bytes):
     rng = np.random.default_rng(block_bytes)
     bv = oracle.packed_block_values(fmt)
     x = rng.integers(0, 256, (N * K // bv, block_bytes)).astype(np.uint8)
-    at = 208 if fmt == "gguf:q6_k" else 0
+    at = {"gguf:q6_k": 208, "gguf:q2_k": 80, "gguf:q3_k": 108}.get(fmt, 0)
     d = np.float16(rng.uniform(0.0005, 0.004, x.shape[0])).view(np.uint16)
     x[:, at], x[:, at + 1] = d & 255, d >> 8
-    if fmt == "gguf:q4_k":
+    if fmt in ("gguf:q2_k", "gguf:q4_k", "gguf:q5_k"):  # dmin follows d
         m = np.float16(rng.uniform(0.0005, 0.004, x.shape[0])).view(np.uint16)
-        x[:, 2], x[:, 3] = m & 255, m >> 8
+        x[:, at + 2], x[:, at + 3] = m & 255, m >> 8
     x = x.reshape(-1)
     w = oracle.f16_bits_to_f32(oracle.dequantize_packed(x, fmt, (N, K), oracle.FLOAT16))  # [N, K]
     xt = T(x, dev)

@@ -115,14 +115,15 @@ def _k_weight(rng, N, K, fmt):
 _K_SHAPES = [(1, 96, 256), (3, 200, 512), (8, 64, 4096), (2, 1000, 1024), (1, 4096, 11008 // 256 * 256), (5, 37, 2304)]
 
 
-@pytest.mark.parametrize("fmt", ["gguf:q4_k", "gguf:q6_k"])
+@pytest.mark.parametrize("fmt", ["gguf:q2_k", "gguf:q3_k", "gguf:q4_k", "gguf:q5_k", "gguf:q6_k", "gguf:iq4_xs"])
 @pytest.mark.parametrize("M,N,K", _K_SHAPES)
 def test_k_quant_gemv_vs_chain(olamd, oracle, dev, fmt, M, N, K):
-    """The fused q4_k / q6_k GEMV against the chain DequantizePacked(FLOAT16)
+    """The fused 256-value GEMVs against the chain DequantizePacked(FLOAT16)
     -> MatMul(a, W^T): same weight rounding, fp32 sums in another order."""
     from test_gpu_float import assert_close
     rng = np.random.default_rng(M * 7919 + N * 31 + K + len(fmt))
-    x = _k_weight(rng, N, K, fmt)
+    x = (_k_weight(rng, N, K, fmt) if fmt in ("gguf:q4_k", "gguf:q6_k")
+         else _finite_blocks(oracle, rng, fmt, N * K // 256))
     a = np.float16(rng.standard_normal((M, K)))
     w_bits = oracle.dequantize_packed(x, fmt, (N, K), 10)
     ref = oracle.matmul_half(a.view(np.uint16), np.ascontiguousarray(w_bits.T), 10)
