@@ -1,4 +1,4 @@
-// Graph rewrites that route two quantized-weight chains to the fused MI355X
+// Graph rewrites that route the quantized-weight chains to the fused MI355X
 // kernels registered by register_mi355x.cc:
 //
 //   DequantizeLinearMatMulGpu:
@@ -9,8 +9,13 @@
 //     x (constant) -> DequantizePacked(format, shape = [N, K], FLOAT16) ->
 //     Transpose(perm = [1, 0]) -> MatMul(A, .)
 //     => ai.rt.amd:DequantizePackedMatMul(A, x; format, shape)
+//   DequantizeEncodedMatMulGpu: ai.rt:Dequantize -> Transpose -> MatMul
+//     => ai.rt.amd:DequantizeEncodedMatMul(A, Q)
+//   DequantizeLinearGroupedMatMulGpu: constant experts -> DequantizeLinear ->
+//     [Cast] -> GroupedMatMul(input, ., group_indices[, bias])
+//     => ai.rt.amd:DequantizeLinearGroupedMatMul
 //
-// Both are core::builder::PatternOptimization subclasses
+// All are core::builder::PatternOptimization subclasses
 // (onnx_core/builder/pattern_optimization.h:164-224) registered opt-in with
 // RegisterPattern(name, factory, false) (onnx_core/builder/pattern_registry.h:
 // 36-37), so the default pattern set is unchanged and a caller enables them by
@@ -318,9 +323,124 @@ public:
   }
 };
 
+// ---------------------------------------------------------------------------
+// W, s[, zp] (constant quantized experts [G, K, N] or [G, N, K]) ->
+// DequantizeLinear(axis) -> [Cast(to = FLOAT16 | BFLOAT16)] ->
+// GroupedMatMul(input, ., group_indices[, bias]; transB)
+// => ai.rt.amd:DequantizeLinearGroupedMatMul(input, W, s, zp | "",
+//    group_indices[, bias]; axis, cast_to, transB)
+class DequantizeLinearGroupedMatMulGpuPattern : public builder::PatternOptimization {
+public:
+  explicit DequantizeLinearGroupedMatMulGpuPattern(bool fp8_scaled_sums = false)
+      : builder::PatternOptimization(1, "DequantizeLinearGroupedMatMulGpu", sym::Device::kGPU0),
+        fp8_scaled_sums_(fp8_scaled_sums) {}
+
+  std::set<std::string> FastOpType() const override { return {"GroupedMatMul"}; }
+
+  builder::MatchResult Match(builder::GraphGraph &graph, const NodeProto &candidate) const override {
+    if (!IsOnnxOp(candidate, "GroupedMatMul") || candidate.input_size() < 3 || candidate.input_size() > 4)
+      return NoMatch(candidate, "not a GroupedMatMul");
+    if (!OnlyAttributes(candidate, {"transB"})) return NoMatch(candidate, "GroupedMatMul attribute other than transB");
+    const int64_t trans_b = ol::GetAttributeOr<int64_t>(candidate, "transB", 0);
+    const NodeProto *cast = nullptr;
+    const NodeProto *prod = graph.NodeBefore(In(candidate, 1));
+    int64_t cast_to = 0;
+    if (prod != nullptr && IsOnnxOp(*prod, "Cast")) {
+      cast_to = ol::GetAttributeOr<int64_t>(*prod, "to", 0);
+      if (cast_to != kFloat16 && cast_to != kBfloat16)
+        return NoMatch(candidate, "Cast target is not FLOAT16 or BFLOAT16");
+      if (!SingleUse(graph, Out(*prod, 0), candidate)) return NoMatch(candidate, "Cast output has another consumer");
+      cast = prod;
+      prod = graph.NodeBefore(In(*prod, 0));
+    }
+    if (prod == nullptr || !IsOnnxOp(*prod, "DequantizeLinear"))
+      return NoMatch(candidate, "GroupedMatMul's weights are not a DequantizeLinear output");
+    if (!OnlyAttributes(*prod, {"axis"})) return NoMatch(candidate, "DequantizeLinear attribute other than axis");
+    std::vector<const TensorProto *> meta;
+    for (int i = 0; i < prod->input_size(); ++i) {
+      if (In(*prod, i).empty()) continue;
+      if (!graph.IsConstant(In(*prod, i))) return NoMatch(candidate, "DequantizeLinear inputs are not all initializers");
+      meta.push_back(graph.GetConstantMetadata(In(*prod, i)));
+    }
+    if (meta.size() < 2) return NoMatch(candidate, "DequantizeLinear inputs are not all initializers");
+    if (!SingleUse(graph, Out(*prod, 0), cast != nullptr ? *cast : candidate))
+      return NoMatch(candidate, "DequantizeLinear output has another consumer");
+    for (const TensorProto *m : meta)
+      if (m == nullptr) return NoMatch(candidate, "type or shape of a DequantizeLinear input unknown");
+
+    // The fused entry point's checks: DequantizeLinear's rules for 3-D
+    // experts, the Cast's, and the 16-bit GroupedMatMul.
+    const int32_t w_t = meta[0]->data_type(), s_t = meta[1]->data_type();
+    const std::vector<int64_t> w = Dims(*meta[0]), s = Dims(*meta[1]);
+    if (w_t != kInt4 && w_t != kUint4 && w_t != kInt8 && w_t != kUint8 && w_t != kFloat8E4M3FN)
+      return NoMatch(candidate, "weight type has no fused kernel");
+    if (w.size() != 3) return NoMatch(candidate, "experts are not 3-D");
+    if (s_t != kFloat && s_t != kFloat16) return NoMatch(candidate, "scale is not FLOAT or FLOAT16");
+    const bool has_zp = meta.size() > 2;
+    if (has_zp && (meta[2]->data_type() != w_t || Dims(*meta[2]) != s))
+      return NoMatch(candidate, "zero point type or shape does not match");
+    const int64_t axis = ol::GetAttributeOr<int64_t>(*prod, "axis", 1);
+    int64_t count = 1;
+    for (int64_t d : s) count *= d;
+    bool along_k = false;  // the scale varies along K inside an expert
+    if (count != 1) {
+      if (axis < 0 || axis >= 3) return NoMatch(candidate, "axis out of range");
+      if (s.size() == 3) {
+        for (int d = 0; d < 3; ++d)
+          if (s[d] <= 0 || w[d] % s[d] != 0 || (d != axis && s[d] != w[d]))
+            return NoMatch(candidate, "blocked scale does not fit the weight");
+        along_k = !(axis == 1 && s[1] == 1);
+      } else if (s.size() == 1) {
+        if (count != w[axis]) return NoMatch(candidate, "scale size differs from the axis dimension");
+        along_k = axis == 1;
+      } else {
+        return NoMatch(candidate, "scale rank is neither 1 nor 3");
+      }
+    }
+    if (cast_to != 0 && s_t != kFloat) return NoMatch(candidate, "Cast of a FLOAT16 DequantizeLinear output");
+    const int64_t run_type = cast_to != 0 ? cast_to : s_t;
+    if (run_type != kFloat16 && run_type != kBfloat16) return NoMatch(candidate, "GroupedMatMul would run in FLOAT");
+    if (w_t == kFloat8E4M3FN && cast_to == kBfloat16 && s_t == kFloat && !has_zp && trans_b == 0 && !along_k &&
+        !fp8_scaled_sums_)
+      return NoMatch(candidate, "FLOAT8E4M3FN -> BFLOAT16 chain would scale the sums (fp8_scaled_sums=True allows it)");
+
+    std::vector<const NodeProto *> nodes{prod};
+    if (cast != nullptr) nodes.push_back(cast);
+    nodes.push_back(&candidate);
+    return builder::MatchResult{this, nodes, &candidate};
+  }
+
+  ol::utils::RepeatedProtoField<NodeProto> Apply(builder::GraphGraph &graph,
+                                                 const std::vector<const NodeProto *> &nodes) const override {
+    const builder::MatchResult verified = nodes.empty() || nodes.back() == nullptr
+                                              ? builder::MatchResult{}
+                                              : Match(graph, *nodes.back());
+    if (verified.pattern == nullptr || verified.nodes != nodes)
+      throw builder::BuilderError(
+          "DequantizeLinearGroupedMatMulGpuPattern::Apply received an unsafe or inconsistent match.");
+    const NodeProto &dq = *nodes.front(), &gmm = *nodes.back();
+    const int64_t cast_to = nodes.size() == 3 ? ol::GetAttributeOr<int64_t>(*nodes[1], "to", 0) : 0;
+    std::vector<std::string> inputs{In(gmm, 0), In(dq, 0), In(dq, 1), dq.input_size() > 2 ? In(dq, 2) : "",
+                                    In(gmm, 2)};
+    if (gmm.input_size() > 3) inputs.push_back(In(gmm, 3));
+    while (inputs.size() > 1 && inputs.back().empty()) inputs.pop_back();
+    const std::string name = "DequantizeLinearGroupedMatMulGpu--" + std::string(gmm.name().value());
+    NodeProto fused = ol::MakeNode("DequantizeLinearGroupedMatMul", inputs, Outputs(gmm), kFusedDomain, name.c_str());
+    AddInt(fused, "axis", ol::GetAttributeOr<int64_t>(dq, "axis", 1));
+    AddInt(fused, "cast_to", cast_to);
+    AddInt(fused, "transB", ol::GetAttributeOr<int64_t>(gmm, "transB", 0));
+    ol::utils::RepeatedProtoField<NodeProto> out;
+    out.push_back(std::move(fused));
+    return out;
+  }
+
+private:
+  bool fp8_scaled_sums_;
+};
+
 }  // namespace mi355x_patterns
 
-// Makes the three rewrites available by name; none is enabled by default.
+// Makes the four rewrites available by name; none is enabled by default.
 void RegisterMi355xPatterns() {
   namespace builder = ONNX_LIGHT_NAMESPACE::core::builder;
   builder::RegisterPattern(
@@ -339,6 +459,12 @@ void RegisterMi355xPatterns() {
       "DequantizeEncodedMatMulGpu",
       []() -> std::unique_ptr<builder::PatternOptimization> {
         return std::make_unique<mi355x_patterns::DequantizeEncodedMatMulGpuPattern>();
+      },
+      /*enabled_by_default=*/false);
+  builder::RegisterPattern(
+      "DequantizeLinearGroupedMatMulGpu",
+      []() -> std::unique_ptr<builder::PatternOptimization> {
+        return std::make_unique<mi355x_patterns::DequantizeLinearGroupedMatMulGpuPattern>();
       },
       /*enabled_by_default=*/false);
 }

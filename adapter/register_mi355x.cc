@@ -14,11 +14,11 @@
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
-//    ai.rt:Dequantize on AWQ / GPTQ encoded weights), for the two fused
+//    ai.rt:Dequantize on AWQ / GPTQ encoded weights), and for the fused
 //    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
-//    ai.rt.amd:DequantizePackedMatMul), and for
-//    ai.rt.amd:DequantizeEncodedMatMul (MatMul on an encoded weight, which
-//    the DequantizeEncodedMatMulGpu pattern produces),
+//    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
+//    an encoded weight, ai.rt.amd:DequantizeLinearGroupedMatMul on quantized
+//    MoE experts),
 //    registered with RegisterKernelFn(..., Device::kCPU, overwrite = true),
 //    the plain key the built-ins use (examples/register_custom_kernel/
 //    main.cc:105-114): a kGPU key would need RuntimeContextOptions.device =
@@ -870,6 +870,68 @@ private:
   Staging a_stage_, y_stage_;
 };
 
+// ai.rt.amd:DequantizeLinearGroupedMatMul(input, x, x_scale, x_zero_point | "",
+// group_indices[, bias]; axis, cast_to, transB) = GroupedMatMul(input,
+// [Cast(to=cast_to)](DequantizeLinear(x, x_scale, x_zero_point, axis)),
+// group_indices, bias, transB): quantized MoE experts.  The constant experts,
+// scales, zero points and bias are kept in HBM; one fused call per run (fp8
+// experts on the matrix cores, the others dequantized on the device into the
+// 16-bit grouped GEMM).
+class Mi355xDequantizeLinearGroupedMatMul : public Mi355xKernel {
+public:
+  static constexpr const char *name = "onnxl_amd:CPU:ai.rt.amd:DequantizeLinearGroupedMatMul";
+  using Mi355xKernel::Mi355xKernel;
+  void Run(rt::RuntimeContext &ctx) override {
+    const NodeProto &node = *node_;
+    rt::RequireMinInputCount(node, 5);
+    rt::RequireOutputCount(node, 1);
+    const int64_t axis = rt::GetAttributeIntOrDefault(node, "axis", 1);
+    const int32_t cast_to = static_cast<int32_t>(rt::GetAttributeIntOrDefault(node, "cast_to", 0));
+    const int64_t transB = rt::GetAttributeIntOrDefault(node, "transB", 0);
+    const onnxl_amd_tensor a = In(0, ctx), x = In(1, ctx), s = In(2, ctx), z = In(3, ctx), idx = In(4, ctx),
+                           b = In(5, ctx);
+    if (a.rank != 2 || x.rank != 3 || idx.rank != 2) {  // the library raises the reference's error
+      onnxl_amd_tensor none{};
+      Check(onnxl_amd_dequantize_linear_grouped_matmul(&a, &x, &s, &z, axis, cast_to, &idx, &b, transB, &none,
+                                                       nullptr));
+    }
+    const rt::Shape shape{a.dims[0], idx.dims[1], x.dims[transB != 0 ? 1 : 2]};
+    rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    const int rc = onnxl_amd_dequantize_linear_grouped_matmul(&a, &x, &s, &z, axis, cast_to, &idx, &b, transB, &dy,
+                                                              nullptr);
+    if (rc == ONNXL_AMD_UNSUPPORTED) RunChain(ctx, a, x, s, z, axis, cast_to, idx, b, transB, y);
+    else Check(rc);
+    rt::SetOutput(node, 0, std::move(y), ctx);
+  }
+
+protected:
+  std::vector<int> ConstantInputs() const override { return {1, 2, 3, 5}; }
+
+private:
+  // The unfused chain through the library: DequantizeLinear into x_scale's
+  // dtype, the optional Cast, then GroupedMatMul.
+  void RunChain(rt::RuntimeContext &ctx, const onnxl_amd_tensor &a, const onnxl_amd_tensor &x,
+                const onnxl_amd_tensor &s, const onnxl_amd_tensor &z, int64_t axis, int32_t cast_to,
+                const onnxl_amd_tensor &idx, const onnxl_amd_tensor &b, int64_t transB, rt::Tensor &y) {
+    const rt::Shape wshape = ShapeOf(x.dims, x.rank);
+    const int64_t n = Count(wshape);
+    rt::Tensor w = ctx.MakeTemporaryTensor(s.data_type, wshape, ByteSize(s.data_type, n));
+    onnxl_amd_tensor dw = DescribeOutput(w);
+    Check(onnxl_amd_dequantize_linear(&x, &s, &z, axis, &dw, nullptr));
+    onnxl_amd_tensor wt = dw;
+    rt::Tensor wc;
+    if (cast_to != 0) {
+      wc = ctx.MakeTemporaryTensor(cast_to, wshape, static_cast<size_t>(n) * 2);
+      onnxl_amd_tensor dwc = DescribeOutput(wc);
+      Check(onnxl_amd_cast(&dw, cast_to, &dwc, nullptr));
+      wt = dwc;
+    }
+    onnxl_amd_tensor dy = DescribeOutput(y);
+    Check(onnxl_amd_grouped_matmul(&a, &wt, &idx, &b, transB, &dy, nullptr));
+  }
+};
+
 // ai.rt.amd:DequantizePackedMatMul(A, x; format, shape = [N, K]) =
 // MatMul(A, Transpose(DequantizePacked(x, format, shape, FLOAT16))), the
 // chain onnx_core/runtime/dequantize_packed.cc:334-372 -> km/kernel_matmul.cc.
@@ -1118,6 +1180,7 @@ const char *RegisterMi355xKernelFunctions(int device_ordinal = 0) {
     Register<Mi355xDequantizePackedMatMul>(kFusedDomain, "DequantizePackedMatMul");
     Register<Mi355xDequantize>("ai.rt", "Dequantize");
     Register<Mi355xDequantizeEncodedMatMul>(kFusedDomain, "DequantizeEncodedMatMul");
+    Register<Mi355xDequantizeLinearGroupedMatMul>(kFusedDomain, "DequantizeLinearGroupedMatMul");
   });
   return onnxl_amd_version();
 }

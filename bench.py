@@ -18,7 +18,7 @@ runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
                    c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q2k|pkgemv_q3k|pkgemv_q4k|pkgemv_q5k|
-                   pkgemv_q6k|pkgemv_iq4xs|awq|moe]
+                   pkgemv_q6k|pkgemv_iq4xs|awq|moe|moe_fp8]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
@@ -28,7 +28,8 @@ GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q2_k / q3_k / q4_k /
 q5_k / q6_k / iq4_xs GEMVs (`pkgemv`, `pkgemv8`, `pkgemv_q2k`, `pkgemv_q3k`,
 `pkgemv_q4k`, `pkgemv_q5k`, `pkgemv_q6k`, `pkgemv_iq4xs`), an AWQ gemm 4-bit
 checkpoint prepared for the fused decode GEMV (`awq`) and a Mixtral-shaped
-MoE GroupedMatMul (`moe`) are timed too and
+MoE GroupedMatMul (`moe`), the same with fp8 experts fused through
+DequantizeLinear -> Cast (`moe_fp8`) are timed too and
 reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
 25,604,096 bytes with the same replica rotation (libonnxl_amd_bench.so): the
 rate a kernel that only reads those bytes reaches, beside which the GEMV's
@@ -407,6 +408,31 @@ def make_moe(olamd, dev):
     return w
 
 
+def make_moe_fp8(olamd, dev):
+    """The same Mixtral-8x7B-shaped expert contraction with quantized
+    experts: DequantizeLinear(fp8e4m3fn experts [8, 4096, 14336], fp32 scale
+    per (expert, column) [8, 1, 14336]) -> Cast(bf16) -> GroupedMatMul, fused
+    (onnxl_amd_dequantize_linear_grouped_matmul, fp8 codes as the matrix
+    cores' B operand).  Same tokens, routing and flops as `moe`."""
+    import torch
+    M, S, G, K, N = 4096, 2, 8, 4096, 14336
+    w = Workload()
+    w.name = ("MoE DequantizeLinear(fp8e4m3fn experts [8,4096,14336], fp32 scale [8,1,14336]) -> Cast(bf16) -> "
+              "GroupedMatMul bf16[4096,4096], top-2 routing -> bf16[4096,2,14336], fused")
+    w.key, w.unit, w.dtype, w.bound = "moe_fp8", "TFLOPS", "bf16 x fp8 (fp32 accumulate)", "mfma"
+    w.work = 2.0 * M * S * K * N
+    w.nbytes = M * K * 2 + G * K * N + G * N * 4 + M * S * 8 + M * S * N * 2
+    g = torch.Generator(device=dev).manual_seed(29)
+    x = (torch.randn((M, K), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    codes = torch.randn((G, K, N), device=dev, generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    scale = torch.rand((G, 1, N), device=dev, generator=g) * 0.02 + 0.002
+    idx = torch.rand((M, G), device=dev, generator=g).argsort(dim=1)[:, :S].contiguous()  # distinct experts
+    y = torch.empty((M, S, N), dtype=torch.bfloat16, device=dev)
+    w.calls = [olamd.prepare("dequantize_linear_grouped_matmul", x, codes, scale, None, 1, olamd.BFLOAT16, idx, None,
+                             0, y, descs={1: olamd.describe(codes, olamd.FLOAT8E4M3FN)})]
+    return w
+
+
 STREAM_VARIANTS = {0: "one pass, 4 16-byte loads in flight per lane", 1: "one pass, 8 loads in flight per lane",
                    2: "one pass, 16 loads in flight per lane",
                    3: "persistent, 4 workgroups per CU looping, 4 loads in flight per lane",
@@ -697,7 +723,7 @@ def value_of(w, ms):
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
              "pkgemv8", "pkgemv_q2k", "pkgemv_q3k", "pkgemv_q4k", "pkgemv_q5k", "pkgemv_q6k", "pkgemv_iq4xs", "awq",
-             "moe")
+             "moe", "moe_fp8")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
                  "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
 
@@ -761,6 +787,8 @@ def main():
             return make_awq(olamd, dev, args.replicas or 24)
         if key == "moe":
             return make_moe(olamd, dev)
+        if key == "moe_fp8":
+            return make_moe_fp8(olamd, dev)
         return make_c5(olamd, dev, args.replicas or 16)
 
     def build_and_time(key, steps, warmup):

@@ -254,6 +254,30 @@ int onnxl_amd_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tens
                              const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
                              onnxl_amd_tensor *y, void *stream);
 
+/* Fused quantized MoE experts: y = GroupedMatMul(input, [Cast(to=cast_to)]
+ * (DequantizeLinear(x, x_scale, x_zero_point, axis)), group_indices, bias,
+ * transB), with x the quantized experts [G, K, N] (or [G, N, K] with transB):
+ * INT4, UINT4, INT8, UINT8 or FLOAT8E4M3FN; per-tensor, per-axis or blocked
+ * scales (FLOAT or FLOAT16) as DequantizeLinear takes them.  cast_to = 0
+ * means no Cast node (the DequantizeLinear output dtype must then be the
+ * input's).  input, bias and y as onnxl_amd_grouped_matmul (FLOAT16 or
+ * BFLOAT16).  The experts are dequantized with the chain's roundings and
+ * multiplied as GroupedMatMul does, except FLOAT8E4M3FN experts with FLOAT
+ * scales constant along K within an expert (per tensor, per expert [G], per
+ * column [N] or [G, 1, N]), cast_to = BFLOAT16, no zero point and transB = 0:
+ * those run on the matrix cores with the fp8 codes as the B operand and the
+ * fp32 sums multiplied by the scale, skipping the rounding of each scaled
+ * weight to bfloat16 (at most 2^-9 relative per weight), as the fp8 path of
+ * onnxl_amd_dequantize_linear_matmul does.  No single reference kernel: it
+ * computes the chain kq/kernel_dequantizelinear.cc:522-693 ->
+ * kernel_cast.cc:360-370 -> math/kernel_grouped_matmul.cc:22-103 that a
+ * DequantizeLinear->[Cast]->GroupedMatMul subgraph runs node by node. */
+int onnxl_amd_dequantize_linear_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *x,
+                                               const onnxl_amd_tensor *x_scale, const onnxl_amd_tensor *x_zero_point,
+                                               int64_t axis, int32_t cast_to, const onnxl_amd_tensor *group_indices,
+                                               const onnxl_amd_tensor *bias, int64_t transB, onnxl_amd_tensor *y,
+                                               void *stream);
+
 /* Cast FLOAT -> FLOAT16 / BFLOAT16 (round-to-nearest-even), the Cast step
  * between DequantizeLinear and a bf16 MatMul.
  * Replaces the FLOAT->BFLOAT16 / FLOAT16 branch of the reference Cast kernel,

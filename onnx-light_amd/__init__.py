@@ -86,6 +86,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_matmul.argtypes = [TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_cast.argtypes = [TP, ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_grouped_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_linear_grouped_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64, ctypes.c_int32,
+                                                                 TP, TP, ctypes.c_int64, TP, ctypes.c_void_p]
         I64 = ctypes.c_int64
         L.onnxl_amd_prepare_matmul_nbits_size.argtypes = [I64, I64, I64, I64, ctypes.c_int, ctypes.POINTER(I64),
                                                           ctypes.POINTER(I64), ctypes.POINTER(I64)]
@@ -509,6 +511,26 @@ def grouped_matmul(input, weights, group_indices, bias=None, transB: int = 0, ou
     return out
 
 
+def dequantize_linear_grouped_matmul(input, x, x_scale, group_indices, x_zero_point=None, axis: int = 1,
+                                     cast_to: int = 0, bias=None, transB: int = 0, x_dtype=None, x_shape=None,
+                                     out=None):
+    """Fused GroupedMatMul(input, [Cast](DequantizeLinear(x, x_scale,
+    x_zero_point, axis)), group_indices, bias, transB): quantized MoE experts
+    x [G, K, N] ([G, N, K] with transB)."""
+    shape = _shape_of(x, x_shape)
+    M, S = (int(d) for d in _shape_of(group_indices))
+    N = int(shape[1 if transB else 2])
+    if out is None:
+        out = _empty((M, S, N), input.dtype, _device_of(input, x))
+    dz = _describe_zp(x_zero_point, x_dtype, x_scale)
+    _check(lib().onnxl_amd_dequantize_linear_grouped_matmul(describe(input), describe(x, x_dtype, shape),
+                                                            describe(x_scale), dz, axis, cast_to,
+                                                            describe(group_indices), describe(bias), int(transB),
+                                                            describe(out),
+                                                            _stream_of(input, x, group_indices, out)))
+    return out
+
+
 def cast(x, to: int, out=None):
     """FLOAT -> FLOAT16 / BFLOAT16 Cast (ext/kernels/kernels/tensor/kernel_cast.cc:360-370)."""
     torch = _torch()
@@ -782,6 +804,21 @@ class GroupedMatMul:
         return grouped_matmul(input, weights, group_indices, bias, transB, out)
 
 
+class DequantizeLinearGroupedMatMul:
+    """Kernel of the fused node that the DequantizeLinear -> [Cast] ->
+    GroupedMatMul rewrite (``patterns.DequantizeLinearGroupedMatMulPattern``)
+    produces: inputs (input, x, scale, zero_point or None, group_indices[,
+    bias]), attributes axis, cast_to and transB.  No reference kernel: it
+    computes kernel::DequantizeLinear, kernel::Cast and kernel::GroupedMatMul
+    in one pass."""
+    name = "onnxl_amd:GPU:ai.rt.amd:DequantizeLinearGroupedMatMul"
+
+    def __call__(self, input, x, x_scale, x_zero_point, group_indices, bias=None, axis=1, cast_to=0, transB=0,
+                 x_dtype=None, x_shape=None, out=None):
+        return dequantize_linear_grouped_matmul(input, x, x_scale, group_indices, x_zero_point, axis, cast_to, bias,
+                                                transB, x_dtype, x_shape, out)
+
+
 # Dispatch keys "<domain>:<op_type>" as the reference table uses them
 # (core/runtime/kernels/kernel_dispatch_table.h:148-164).
 KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLinearMatMul,
@@ -792,7 +829,8 @@ KERNELS = {"ai.onnx:MatMulInteger": MatMulInteger, "ai.onnx:QLinearMatMul": QLin
            "ai.onnx:DequantizePacked": DequantizePacked,
            "ai.onnx:GroupedMatMul": GroupedMatMul,
            "ai.rt.amd:DequantizeLinearMatMul": DequantizeLinearMatMul,
-           "ai.rt.amd:DequantizePackedMatMul": DequantizePackedMatMul}
+           "ai.rt.amd:DequantizePackedMatMul": DequantizePackedMatMul,
+           "ai.rt.amd:DequantizeLinearGroupedMatMul": DequantizeLinearGroupedMatMul}
 
 
 class Prepared:

@@ -1545,31 +1545,29 @@ int DqMatMulNoAlloc(const onnxl_amd_tensor *a, const onnxl_amd_tensor *x, const 
 constexpr const char *kGmmName = "kernel::GroupedMatMul";
 constexpr int64_t kGmmMaxGroups = 4096;  // routing counters in LDS
 
-int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights,
-                  const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
-                  onnxl_amd_tensor *y, hipStream_t stream) {
-  OLA_ENFORCE(!Absent(input) && !Absent(weights) && !Absent(group_indices) && y, kGmmName,
-              ": input, weights, group_indices and the output are required.");
-  CheckDescriptor(input, "input");
-  CheckDescriptor(weights, "weights");
-  CheckDescriptor(group_indices, "group_indices");
-  CheckDescriptor(bias, "bias");
-  CheckDescriptor(y, "output");
+// The GroupedMatMul node's checks (:48-88) for weights of shape w_shape and
+// dtype w_dtype (the weights tensor itself, or the dequantized experts of the
+// fused node), then this build's limits.  Fills the shape fields of p.
+// `weights` (null for the fused node) joins the payload checks in the
+// reference's order.
+void PlanGrouped(const onnxl_amd_tensor *input, const Shape &w_shape, int32_t w_dtype,
+                 const onnxl_amd_tensor *weights, const onnxl_amd_tensor *group_indices,
+                 const onnxl_amd_tensor *bias, int64_t transB, const onnxl_amd_tensor *y, GroupedParams &p) {
   const bool tb = transB != 0;
-  OLA_ENFORCE(input->rank == 2 && weights->rank == 3 && group_indices->rank == 2, kGmmName,
+  OLA_ENFORCE(input->rank == 2 && w_shape.size() == 3 && group_indices->rank == 2, kGmmName,
               " expects input rank 2, weights rank 3, and indices rank 2.");
-  const int64_t M = input->dims[0], K = input->dims[1], G = weights->dims[0];
-  const int64_t N = weights->dims[tb ? 1 : 2], S = group_indices->dims[1];
-  OLA_ENFORCE(K == weights->dims[tb ? 2 : 1] && M == group_indices->dims[0], kGmmName,
+  const int64_t M = input->dims[0], K = input->dims[1], G = w_shape[0];
+  const int64_t N = w_shape[tb ? 1 : 2], S = group_indices->dims[1];
+  OLA_ENFORCE(K == w_shape[tb ? 2 : 1] && M == group_indices->dims[0], kGmmName,
               " incompatible input dimensions.");
   const int32_t dt = input->data_type;
   OLA_ENFORCE(dt == kFloat || dt == kDouble || dt == kFloat16 || dt == kBfloat16, kGmmName,
               " expects floating-point inputs.");
-  OLA_ENFORCE(weights->data_type == dt, kGmmName, " weights must match the input dtype.");
+  OLA_ENFORCE(w_dtype == dt, kGmmName, " weights must match the input dtype.");
   OLA_ENFORCE(group_indices->data_type == kInt32 || group_indices->data_type == kInt64, kGmmName,
               " indices must be INT32 or INT64.");
   for (const onnxl_amd_tensor *t : {input, weights, group_indices})
-    OLA_ENFORCE(t->size_bytes == PackedBytes(t->data_type, NumElements(*t)), kGmmName,
+    OLA_ENFORCE(!t || t->size_bytes == PackedBytes(t->data_type, NumElements(*t)), kGmmName,
                 " tensor payload does not match its shape.");
   const bool has_bias = !Absent(bias);
   if (has_bias) {
@@ -1593,16 +1591,6 @@ int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights
   if (dt != kFloat16 && dt != kBfloat16) throw Unsupported("GroupedMatMul: only FLOAT16 / BFLOAT16 run on the GPU path");
   if (G > kGmmMaxGroups) throw Unsupported(Cat("GroupedMatMul: more than ", kGmmMaxGroups, " groups"));
   OLA_ENFORCE(P < (int64_t(1) << 31) - 1, kGmmName, ": more than 2^31 (token, selection) pairs");
-  if (P == 0 || N == 0) return ONNXL_AMD_OK;
-  Ctx();
-  const size_t ws = (size_t)(2 * (G + 1) + P) * sizeof(int32_t);
-  Staging st(stream, ws, {input, weights, group_indices, has_bias ? bias : nullptr}, {y});
-  GroupedParams p{};
-  p.A = st.In(input);
-  p.W = st.In(weights);
-  p.idx = st.In(group_indices);
-  p.bias = has_bias ? st.In(bias) : nullptr;
-  p.Y = st.Out(y);
   p.M = M;
   p.K = K;
   p.N = N;
@@ -1612,11 +1600,164 @@ int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights
   p.transB = tb;
   p.bf16 = dt == kBfloat16;
   p.nbn = (N + 127) / 128;
-  int32_t *w32 = static_cast<int32_t *>(st.Extra());
+}
+
+// Routing workspace of a grouped launch: row and tile offsets (G + 1 each)
+// and the routed pairs (M * S), as int32.
+size_t GroupedRouteBytes(const GroupedParams &p) { return (size_t)(2 * (p.G + 1) + p.M * p.S) * sizeof(int32_t); }
+
+void SetGroupedRoute(GroupedParams &p, void *ws) {
+  int32_t *w32 = static_cast<int32_t *>(ws);
   p.row_off = w32;
-  p.tile_off = w32 + (G + 1);
-  p.rows = w32 + 2 * (G + 1);
+  p.tile_off = w32 + (p.G + 1);
+  p.rows = w32 + 2 * (p.G + 1);
+}
+
+int GroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *weights,
+                  const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
+                  onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(input) && !Absent(weights) && !Absent(group_indices) && y, kGmmName,
+              ": input, weights, group_indices and the output are required.");
+  CheckDescriptor(input, "input");
+  CheckDescriptor(weights, "weights");
+  CheckDescriptor(group_indices, "group_indices");
+  CheckDescriptor(bias, "bias");
+  CheckDescriptor(y, "output");
+  GroupedParams p{};
+  PlanGrouped(input, ShapeOf(*weights), weights->data_type, weights, group_indices, bias, transB, y, p);
+  if (p.M * p.S == 0 || p.N == 0) return ONNXL_AMD_OK;
+  Ctx();
+  const bool has_bias = !Absent(bias);
+  Staging st(stream, GroupedRouteBytes(p), {input, weights, group_indices, has_bias ? bias : nullptr}, {y});
+  p.A = st.In(input);
+  p.W = st.In(weights);
+  p.idx = st.In(group_indices);
+  p.bias = has_bias ? st.In(bias) : nullptr;
+  p.Y = st.Out(y);
+  SetGroupedRoute(p, st.Extra());
   LaunchGroupedMatMul(p, stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused DequantizeLinear -> [Cast] -> GroupedMatMul: quantized MoE experts.
+
+constexpr const char *kDqgName = "DequantizeLinearGroupedMatMul";
+
+int DqGroupedMatMul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *x, const onnxl_amd_tensor *x_scale,
+                    const onnxl_amd_tensor *x_zp, int64_t axis, int32_t cast_to,
+                    const onnxl_amd_tensor *group_indices, const onnxl_amd_tensor *bias, int64_t transB,
+                    onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(input) && !Absent(x) && !Absent(x_scale) && !Absent(group_indices) && y, kDqgName,
+              ": input, x, x_scale, group_indices and the output are required.");
+  CheckDescriptor(input, "input");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(x_scale, "x_scale");
+  CheckDescriptor(x_zp, "x_zero_point");
+  CheckDescriptor(group_indices, "group_indices");
+  CheckDescriptor(bias, "bias");
+  CheckDescriptor(y, "output");
+  const bool has_zp = !Absent(x_zp);
+  // The DequantizeLinear node's checks (kq/kernel_dequantizelinear.cc:522-565),
+  // as onnxl_amd_dequantize_linear makes them.
+  DqGroupedParams q{};
+  OLA_ENFORCE(IsSupportedScaleDType(x_scale->data_type),
+              "kernel::DequantizeLinear: x_scale must be FLOAT or FLOAT16.");
+  if (has_zp)
+    OLA_ENFORCE(x->data_type == x_zp->data_type, "kernel::DequantizeLinear: x_zero_point data_type must match x.");
+  OLA_ENFORCE(x->rank == 3, kDqgName, ": the quantized experts must be 3-D.");
+  const Shape xs = ShapeOf(*x), ss = ShapeOf(*x_scale);
+  OLA_ENFORCE(x->size_bytes == PackedBytes(x->data_type, NumElements(*x)), kDqgName,
+              ": x payload does not match its shape.");
+  if (NumElements(*x_scale) == 1) {
+    if (has_zp)
+      OLA_ENFORCE(NumElements(*x_zp) == 1,
+                  "kernel::DequantizeLinear: x_zero_point must be a scalar (per-tensor dequantization).");
+    q.scale_kind = 0;
+  } else {
+    OLA_ENFORCE(axis >= 0 && axis < x->rank, "kernel::DequantizeLinear: axis out of range.");
+    if (has_zp)
+      OLA_ENFORCE(ShapeOf(*x_scale) == ShapeOf(*x_zp),
+                  "kernel::DequantizeLinear: x_scale and x_zero_point must have the same shape.");
+    q.inner = 1;
+    for (int d = (int)axis + 1; d < x->rank; ++d) q.inner *= xs[d];
+    q.axis_dim = xs[axis];
+    if (ss.size() == xs.size()) {
+      for (size_t d = 0; d < xs.size(); ++d) {
+        OLA_ENFORCE(ss[d] > 0 && xs[d] % ss[d] == 0,
+                    "kernel::DequantizeLinear: blocked x_scale dimension must divide the matching x dimension.");
+        OLA_ENFORCE((int64_t)d == axis || ss[d] == xs[d],
+                    "kernel::DequantizeLinear: blocked x_scale may only differ from x along the quantization axis.");
+      }
+      q.scale_kind = 2;
+      q.block = xs[axis] / ss[axis];
+    } else {
+      OLA_ENFORCE(NumElements(*x_scale) == xs[axis],
+                  "kernel::DequantizeLinear: x_scale element count must equal axis dimension.");
+      q.scale_kind = 1;
+    }
+  }
+  switch (x->data_type) {
+  case kInt4: case kUint4: case kInt8: case kUint8: case kFloat8E4M3FN: break;
+  default: throw Unsupported(Cat(kDqgName, ": weight dtype ", x->data_type, " has no GPU kernel"));
+  }
+  // the Cast node, then GroupedMatMul on the weights' final dtype
+  const int32_t dq_out = x_scale->data_type;
+  if (cast_to) {
+    OLA_ENFORCE(dq_out == kFloat, kDqgName, ": the Cast step must convert a FLOAT DequantizeLinear output.");
+    OLA_ENFORCE(cast_to == kFloat16 || cast_to == kBfloat16, kDqgName, ": Cast to FLOAT16 or BFLOAT16 only.");
+  }
+  PlanGrouped(input, xs, cast_to ? cast_to : dq_out, nullptr, group_indices, bias, transB, y, q.g);
+  q.x_dtype = x->data_type;
+  q.scale_f16 = x_scale->data_type == kFloat16;
+  q.deq_round_f16 = dq_out == kFloat16;
+  q.cast_round = cast_to == kBfloat16 ? 16 : (cast_to == kFloat16 ? 10 : 0);
+  // fp8 experts on the core: FLOAT scales constant along K within a group
+  // (per tensor, per expert [G], per column [N] or [G, 1, N]), the Cast to
+  // BFLOAT16, no zero point, weights [G, K, N]
+  if (x->data_type == kFloat8E4M3FN && dq_out == kFloat && cast_to == kBfloat16 && !has_zp && !transB) {
+    const int64_t N = xs[2];
+    if (q.scale_kind == 0) {
+      q.fused = 1;
+    } else if (q.scale_kind == 1 && axis == 0) {
+      q.fused = 1, q.scale_grp_stride = 1;
+    } else if (q.scale_kind == 1 && axis == 2) {
+      q.fused = 1, q.scale_per_col = 1;
+    } else if (q.scale_kind == 2 && axis == 1 && ss[1] == 1) {
+      q.fused = 1, q.scale_per_col = 1, q.scale_grp_stride = N;
+    }
+  }
+  const GroupedParams &g = q.g;
+  if (g.M * g.S == 0 || g.N == 0) return ONNXL_AMD_OK;
+  Ctx();
+  // the fused check needs the device addresses: staged host payloads sit in
+  // 256-byte aligned scratch, so judge on an aligned stand-in for those
+  auto addr = [](const onnxl_amd_tensor *t) -> const void * {
+    return t->location == ONNXL_AMD_HOST ? reinterpret_cast<const void *>(uintptr_t(256)) : t->data;
+  };
+  q.g.A = addr(input);
+  q.X = static_cast<const uint8_t *>(addr(x));
+  q.g.Y = const_cast<void *>(addr(y));
+  q.g.bias = Absent(bias) ? nullptr : addr(bias);
+  const bool fused = DqGroupedFusedEligible(q);
+  const size_t route = Scratch::Round(GroupedRouteBytes(g));
+  const size_t w16 = fused ? 0 : (size_t)(g.G * g.K * g.N) * 2;
+  const bool has_bias = !Absent(bias);
+  Staging st(stream, route + w16, {input, x, x_scale, has_zp ? x_zp : nullptr, group_indices,
+                                   has_bias ? bias : nullptr}, {y});
+  q.g.A = st.In(input);
+  q.X = static_cast<const uint8_t *>(st.In(x));
+  q.scale = st.In(x_scale);
+  q.zp = has_zp ? static_cast<const uint8_t *>(st.In(x_zp)) : nullptr;
+  q.g.idx = st.In(group_indices);
+  q.g.bias = has_bias ? st.In(bias) : nullptr;
+  q.g.Y = st.Out(y);
+  SetGroupedRoute(q.g, st.Extra());
+  q.w16 = fused ? nullptr : reinterpret_cast<uint16_t *>(static_cast<char *>(st.Extra()) + route);
+  if (!fused) q.fused = 0;
+  LaunchDqGroupedMatMul(q, stream);
   OLA_HIP(hipGetLastError());
   st.Finish();
   return ONNXL_AMD_OK;
@@ -2310,6 +2451,17 @@ int onnxl_amd_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tens
                              onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return GroupedMatMul(input, weights, group_indices, bias, transB, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_linear_grouped_matmul(const onnxl_amd_tensor *input, const onnxl_amd_tensor *x,
+                                               const onnxl_amd_tensor *x_scale, const onnxl_amd_tensor *x_zero_point,
+                                               int64_t axis, int32_t cast_to, const onnxl_amd_tensor *group_indices,
+                                               const onnxl_amd_tensor *bias, int64_t transB, onnxl_amd_tensor *y,
+                                               void *stream) {
+  return Guard([&] {
+    return DqGroupedMatMul(input, x, x_scale, x_zero_point, axis, cast_to, group_indices, bias, transB, y,
+                           static_cast<hipStream_t>(stream));
   });
 }
 

@@ -23,6 +23,7 @@
 // (km/kernel_grouped_matmul.cc:22-46); with a bias, the sum is rounded to the
 // output dtype, the bias added in fp32 and the result rounded again.
 #include "common.hpp"
+#include "device_codecs.hpp"
 #include "kernels.hpp"
 #include "mfma_gemm.hpp"
 
@@ -133,6 +134,37 @@ __global__ __launch_bounds__(256) void GroupedSimpleKernel(const GroupedParams p
   }
 }
 
+// The quantized experts dequantized as the unfused chain does:
+// DequantizeLinear's (x - zp) * scale in fp32, stored in the scale's dtype,
+// then the optional Cast (kq/kernel_dequantizelinear.cc:57-63,259-285;
+// kernel_cast.cc:360-370).  One thread per weight element, grid-stride.
+__device__ __forceinline__ float QuantAt(const uint8_t *w, int dt, int64_t i) {
+  switch (dt) {
+  case kInt4: return (float)Int4ToInt((w[i >> 1] >> (4 * (i & 1))) & 0xfu);
+  case kUint4: return (float)((w[i >> 1] >> (4 * (i & 1))) & 0xfu);
+  case kInt8: return (float)(int8_t)w[i];
+  case kUint8: return (float)w[i];
+  default: return Fp8E4M3ToF32(w[i]);
+  }
+}
+
+__global__ __launch_bounds__(256) void DequantExpertsKernel(const DqGroupedParams p, int64_t total) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    int64_t si = 0;
+    if (p.scale_kind == 1) {
+      si = (i / p.inner) % p.axis_dim;
+    } else if (p.scale_kind == 2) {
+      const int64_t o = i / (p.inner * p.axis_dim), a = (i / p.inner) % p.axis_dim, r = i % p.inner;
+      si = (o * (p.axis_dim / p.block) + a / p.block) * p.inner + r;
+    }
+    const float s = p.scale_f16 ? F16ToF32(static_cast<const uint16_t *>(p.scale)[si])
+                                : static_cast<const float *>(p.scale)[si];
+    const float z = p.zp ? QuantAt(p.zp, p.x_dtype, si) : 0.f;
+    const float v = (QuantAt(p.X, p.x_dtype, i) - z) * s;
+    p.w16[i] = p.deq_round_f16 || p.cast_round != 16 ? F32ToF16(v) : F32ToBf16(v);
+  }
+}
+
 }  // namespace
 
 int64_t GroupedMaxTiles(const GroupedParams &p) {
@@ -187,6 +219,63 @@ void LaunchGroupedMatMul(const GroupedParams &p, hipStream_t stream) {
     if (p.transB) mg::LaunchGrouped<mg::kOutF16, 2>(g, tiles, stream);
     else mg::LaunchGrouped<mg::kOutF16, 1>(g, tiles, stream);
   }
+}
+
+}  // namespace onnxl_amd
+
+namespace onnxl_amd {
+
+bool DqGroupedFusedEligible(const DqGroupedParams &p) {
+  mg::GemmArgs g{};
+  g.A = p.g.A;
+  g.B = p.X;
+  g.Y = p.g.Y;
+  g.M = p.g.M;
+  g.N = p.g.N;
+  g.K = p.g.K;
+  const int64_t lim = (int64_t(1) << 31) - (int64_t(1) << 24);
+  return p.fused && !p.g.transB && p.g.bf16 && p.g.K > 0 && mg::Eligible<mg::kBf16F8>(g) &&
+         p.g.M * p.g.S * p.g.N * 2 < lim && p.g.N * p.g.K < lim &&
+         (p.g.bias == nullptr || reinterpret_cast<uintptr_t>(p.g.bias) % 8 == 0);
+}
+
+void LaunchDqGroupedMatMul(const DqGroupedParams &p, hipStream_t stream) {
+  const int64_t P = p.g.M * p.g.S;
+  if (P == 0 || p.g.N == 0) return;
+  if (!DqGroupedFusedEligible(p)) {
+    // general path: the weights dequantized into the workspace, then the
+    // 16-bit grouped GEMM
+    const int64_t total = p.g.G * p.g.K * p.g.N;
+    if (total > 0) {
+      const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+      hipLaunchKernelGGL(DequantExpertsKernel, dim3(blocks), dim3(256), 0, stream, p, total);
+    }
+    GroupedParams g = p.g;
+    g.W = p.w16;
+    LaunchGroupedMatMul(g, stream);
+    return;
+  }
+  hipLaunchKernelGGL(GroupRouteKernel, dim3(1), dim3(kRouteThreads), GroupedRouteLds(p.g.G), stream, p.g);
+  mg::GemmArgs g{};
+  g.A = p.g.A;
+  g.B = p.X;
+  g.Y = p.g.Y;
+  g.M = p.g.M;
+  g.N = p.g.N;
+  g.K = p.g.K;
+  g.batch = 1;
+  g.scale = p.scale;
+  g.scale_f16 = p.scale_f16;
+  g.scale_per_col = p.scale_per_col;
+  g.scale_grp_stride = p.scale_grp_stride;
+  g.grp_tile_off = p.g.tile_off;
+  g.grp_row_off = p.g.row_off;
+  g.grp_rows = p.g.rows;
+  g.grp_count = (int)p.g.G;
+  g.grp_sel = (int)p.g.S;
+  g.grp_b_stride = p.g.K * p.g.N;
+  g.grp_bias = p.g.bias;
+  mg::LaunchGrouped<mg::kOutBf16, 1, mg::kBf16F8>(g, GroupedMaxTiles(p.g), stream);
 }
 
 }  // namespace onnxl_amd

@@ -335,6 +335,32 @@ struct GroupedParams {
 int64_t GroupedMaxTiles(const GroupedParams &p);
 void LaunchGroupedMatMul(const GroupedParams &p, hipStream_t stream);
 
+// Fused DequantizeLinear -> [Cast] -> GroupedMatMul (quantized MoE experts):
+// the GroupedMatMul of `g` over W = Cast(DequantizeLinear(X, scale, zp)).
+struct DqGroupedParams {
+  GroupedParams g;   // g.W is set by the launcher (general path: w16)
+  const uint8_t *X;  // quantized weights [G, K, N] ([G, N, K] with transB), ONNX packing
+  const void *scale; // FLOAT or FLOAT16
+  const uint8_t *zp; // storage of X's dtype, one per scale entry, or nullptr
+  int x_dtype, scale_f16;
+  // scale entry of flat weight element i: per-tensor (kind 0) 0; per-axis (1)
+  // (i / inner) % axis_dim; blocked along the axis (2)
+  // ((i / (inner * axis_dim)) * (axis_dim / block) + ((i / inner) % axis_dim) / block) * inner + i % inner
+  int scale_kind;
+  int64_t inner, axis_dim, block;
+  // the chain's roundings: to FLOAT16 when the DequantizeLinear output is
+  // FLOAT16; else the Cast's (16: BFLOAT16, 10: FLOAT16)
+  int deq_round_f16, cast_round;
+  // fp8 weights on the grouped MFMA core, sums scaled per column in fp32:
+  // group g's column n uses scale[g * scale_grp_stride + (scale_per_col ? n : 0)]
+  int fused, scale_per_col;
+  int64_t scale_grp_stride;
+  uint16_t *w16;     // general path: the dequantized weights (G * K * N), device workspace
+};
+// Whether the fused fp8 path takes these operands (shape and alignment).
+bool DqGroupedFusedEligible(const DqGroupedParams &p);
+void LaunchDqGroupedMatMul(const DqGroupedParams &p, hipStream_t stream);
+
 // ---------------------------------------------------------------------------
 // ORT MatMulNBits weight preparation (nbits.hip).
 struct NbitsPrepParams {

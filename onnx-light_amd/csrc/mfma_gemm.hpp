@@ -180,10 +180,12 @@ struct GemmArgs {
   int y_signed;
   QDevScalars dev;  // device-resident scalars replacing the four above (kI8 with ZP)
   // kBf16F8: dequantization scales (FLOAT or FLOAT16), one per column
-  // (scale_per_col) or a single value
+  // (scale_per_col) or a single value; in grouped mode group g's scales start
+  // scale_grp_stride elements after group g - 1's
   const void *scale;
   int scale_f16;
   int scale_per_col;
+  int64_t scale_grp_stride;
   // Row pitches of B and Y in elements (0: N), so a launch can cover a
   // column range of larger matrices; N stays the width computed.
   int64_t ldb, ldy;
@@ -231,7 +233,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr bool RA = ZP, CB = ZP;
   constexpr bool GRP = GM == 1 || GM == 2;  // grouped (routing tables)
   constexpr bool BT = GM == 2 || GM == 3 || CV;
-  static_assert(GM == 0 || (KIND == kH16 && WB == 2 && !ZP), "grouped mode: 16-bit operands, 128-column tiles");
+  static_assert(GM == 0 || ((KIND == kH16 || (KIND == kBf16F8 && GM == 1)) && WB == 2 && !ZP),
+                "grouped mode: 16-bit operands (or fp8 B [K, N] per group), 128-column tiles");
   static_assert(!CV || (KIND == kI8 && WB == 2 && GM == 0), "implicit convolution: int8, 128-column tiles");
   using T = Traits<KIND>;
   using Acc = typename T::Acc;
@@ -432,7 +435,7 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < WB; ++j) {
       const int64_t col = col0 + wn * kWN + j * 32 + lr;
-      const int64_t si = p.scale_per_col ? (col < N ? col : 0) : 0;
+      const int64_t si = grp * p.scale_grp_stride + (p.scale_per_col ? (col < N ? col : 0) : 0);
       bscale[j] = p.scale_f16 ? (float)static_cast<const _Float16 *>(p.scale)[si]
                               : static_cast<const float *>(p.scale)[si];
     }
@@ -1019,8 +1022,9 @@ template <int OUT> inline void LaunchBT(const GemmArgs &p, hipStream_t s) {
 
 // Grouped launch: `max_tiles` workgroups, an upper bound of the tiles the
 // routing table holds (the rest leave at once).
-template <int OUT, int GM> inline void LaunchGrouped(const GemmArgs &p, int64_t max_tiles, hipStream_t s) {
-  hipLaunchKernelGGL((MfmaGemmKernel<kH16, OUT, false, false, false, 2, GM>), dim3((unsigned)max_tiles),
+template <int OUT, int GM, int KIND = kH16>
+inline void LaunchGrouped(const GemmArgs &p, int64_t max_tiles, hipStream_t s) {
+  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, false, false, false, 2, GM>), dim3((unsigned)max_tiles),
                      dim3(kThreads), 0, s, p);
 }
 

@@ -46,6 +46,7 @@ FUSED_DOMAIN = "ai.rt.amd"
 FUSED_OP = "DequantizeLinearMatMul"
 PACKED_FUSED_OP = "DequantizePackedMatMul"
 ENCODED_FUSED_OP = "DequantizeEncodedMatMul"
+GROUPED_FUSED_OP = "DequantizeLinearGroupedMatMul"
 # the 27 GGUF profiles of DequantizePacked (format: values per block); the
 # fused node runs every one of them on the GPU (decode GEMVs for q4_0, q8_0,
 # q2_k, q3_k, q4_k, q5_k, q6_k and iq4_xs, the decoded weight through the
@@ -327,6 +328,110 @@ class DequantizeEncodedMatMulPattern(PatternOptimization):
                      matmul.name or dq.name)]
 
 
+class DequantizeLinearGroupedMatMulPattern(PatternOptimization):
+    """DequantizeLinear over constant quantized experts x [G, K, N] ([G, N, K]
+    with transB), an optional Cast to FLOAT16 or BFLOAT16, then
+    GroupedMatMul's weights -> one fused node
+    ``ai.rt.amd:DequantizeLinearGroupedMatMul(input, x, scale, zero_point,
+    group_indices[, bias])`` with attributes axis, cast_to and transB,
+    computed by ``dequantize_linear_grouped_matmul``.  As for the 2-D rewrite,
+    fp8 experts whose Cast to BFLOAT16 the fused kernel replaces by scaled
+    sums match only with ``fp8_scaled_sums``."""
+    device = "gpu"
+
+    def fast_op_type(self) -> set:
+        return {"GroupedMatMul"}
+
+    def __init__(self, fp8_scaled_sums: bool = False):
+        self.fp8_scaled_sums = fp8_scaled_sums
+
+    def _check_types(self, graph: Graph, dq: Node, cast_to: int, trans_b: int) -> str:
+        """Why the fused entry point would refuse this chain ("" if it accepts it)."""
+        info = graph.value_info
+        names = [i for i in dq.inputs if i]
+        if any(i not in info for i in names):
+            return "type or shape of a DequantizeLinear input unknown"
+        (w_t, w_shape), (s_t, s_shape) = info[names[0]], info[names[1]]
+        zp = info[names[2]] if len(names) > 2 else None
+        w_shape, s_shape = tuple(w_shape), tuple(s_shape)
+        if w_t not in _WEIGHT_TYPES:
+            return "weight type has no fused kernel"
+        if len(w_shape) != 3:
+            return "experts are not 3-D"
+        if s_t not in _SCALE_TYPES:
+            return "scale is not FLOAT or FLOAT16"
+        if zp is not None and (zp[0] != w_t or tuple(zp[1]) != s_shape):
+            return "zero point type or shape does not match"
+        axis = int(dq.attrs.get("axis", 1))
+        count = 1
+        for d in s_shape:
+            count *= d
+        per_tensor = count == 1
+        along_k = False  # the scale varies along K inside an expert
+        if not per_tensor:
+            if not 0 <= axis < 3:
+                return "axis out of range"
+            if len(s_shape) == 3:
+                if any(s_shape[d] <= 0 or w_shape[d] % s_shape[d] or (d != axis and s_shape[d] != w_shape[d])
+                       for d in range(3)):
+                    return "blocked scale does not fit the weight"
+                along_k = not (axis == 1 and s_shape[1] == 1)
+            elif len(s_shape) == 1:
+                if count != w_shape[axis]:
+                    return "scale size differs from the axis dimension"
+                along_k = axis == 1
+            else:
+                return "scale rank is neither 1 nor 3"
+        if cast_to and s_t != FLOAT:
+            return "Cast of a FLOAT16 DequantizeLinear output"
+        if (cast_to or s_t) not in (FLOAT16, BFLOAT16):
+            return "GroupedMatMul would run in FLOAT"
+        if (w_t == FLOAT8E4M3FN and cast_to == BFLOAT16 and s_t == FLOAT and zp is None and not trans_b
+                and not along_k and not self.fp8_scaled_sums):
+            return "FLOAT8E4M3FN -> BFLOAT16 chain would scale the sums (fp8_scaled_sums=True allows it)"
+        return ""
+
+    def match(self, graph: Graph, candidate: Node) -> MatchResult:
+        if not _is_onnx(candidate, "GroupedMatMul") or not 3 <= len(candidate.inputs) <= 4:
+            return self.no_match("not a GroupedMatMul")
+        if set(candidate.attrs) - {"transB"}:
+            return self.no_match("GroupedMatMul attribute other than transB")
+        cast = None
+        prod = graph.producer(candidate.inputs[1])
+        if prod is not None and _is_onnx(prod, "Cast"):
+            if int(prod.attrs.get("to", 0)) not in _CAST_TARGETS:
+                return self.no_match("Cast target is not FLOAT16 or BFLOAT16")
+            if not DequantizeLinearMatMulPattern._single_use(graph, prod.outputs[0], candidate):
+                return self.no_match("Cast output has another consumer")
+            cast, prod = prod, graph.producer(prod.inputs[0])
+        if prod is None or not _is_onnx(prod, "DequantizeLinear"):
+            return self.no_match("GroupedMatMul's weights are not a DequantizeLinear output")
+        if set(prod.attrs) - {"axis"}:
+            return self.no_match("DequantizeLinear attribute other than axis")
+        consts = [i for i in prod.inputs if i]
+        if len(consts) < 2 or any(i not in graph.initializers for i in consts):
+            return self.no_match("DequantizeLinear inputs are not all initializers")
+        if not DequantizeLinearMatMulPattern._single_use(graph, prod.outputs[0],
+                                                          cast if cast is not None else candidate):
+            return self.no_match("DequantizeLinear output has another consumer")
+        why = self._check_types(graph, prod, int(cast.attrs["to"]) if cast is not None else 0,
+                                int(candidate.attrs.get("transB", 0)))
+        if why:
+            return self.no_match(why)
+        return MatchResult([prod] + ([cast] if cast is not None else []) + [candidate])
+
+    def apply(self, graph: Graph, nodes: Sequence[Node]) -> List[Node]:
+        dq, gmm = nodes[0], nodes[-1]
+        cast_to = int(nodes[1].attrs["to"]) if len(nodes) == 3 else 0
+        zp = dq.inputs[2] if len(dq.inputs) > 2 else ""
+        inputs = [gmm.inputs[0], dq.inputs[0], dq.inputs[1], zp, gmm.inputs[2]] + list(gmm.inputs[3:4])
+        while inputs and not inputs[-1]:
+            inputs.pop()
+        return [Node(GROUPED_FUSED_OP, inputs, list(gmm.outputs), FUSED_DOMAIN,
+                     {"axis": int(dq.attrs.get("axis", 1)), "cast_to": cast_to,
+                      "transB": int(gmm.attrs.get("transB", 0))}, gmm.name or dq.name)]
+
+
 # ---- registry --------------------------------------------------------------
 
 _REGISTRY: Dict[str, tuple] = {}
@@ -364,6 +469,7 @@ def create_registered_patterns(device: Optional[str] = None) -> List[PatternOpti
 register_pattern("DequantizeLinearMatMulGpu", DequantizeLinearMatMulPattern, enabled_by_default=False)
 register_pattern("DequantizePackedMatMulGpu", DequantizePackedMatMulPattern, enabled_by_default=False)
 register_pattern("DequantizeEncodedMatMulGpu", DequantizeEncodedMatMulPattern, enabled_by_default=False)
+register_pattern("DequantizeLinearGroupedMatMulGpu", DequantizeLinearGroupedMatMulPattern, enabled_by_default=False)
 
 
 def optimize(graph: Graph, patterns: Sequence[PatternOptimization]) -> int:

@@ -20,7 +20,7 @@ REFERENCE = "/root/reference/onnx_light"
 OPERATORS = ["MatMulInteger", "QLinearMatMul", "DequantizeLinear", "MatMul", "QuantizeLinear",
              "DynamicQuantizeLinear", "ConvInteger", "QLinearConv", "Cast", "DequantizePacked",
              "GroupedMatMul", "MatMulNBits", "DequantizeLinearMatMul", "DequantizePackedMatMul", "Dequantize",
-             "DequantizeEncodedMatMul"]
+             "DequantizeEncodedMatMul", "DequantizeLinearGroupedMatMul"]
 
 
 def _strip_comments(text):
@@ -199,12 +199,15 @@ def test_cpp_patterns_registered_opt_in(olamd):
     pat = importlib.import_module("onnx_light_amd.patterns")
     text = _strip_comments(open(PATTERNS_CC).read())
     raw = open(PATTERNS_CC).read()
-    for name in ("DequantizeLinearMatMulGpu", "DequantizePackedMatMulGpu", "DequantizeEncodedMatMulGpu"):
+    for name in ("DequantizeLinearMatMulGpu", "DequantizePackedMatMulGpu", "DequantizeEncodedMatMulGpu",
+                 "DequantizeLinearGroupedMatMulGpu"):
         assert name in pat.registered_pattern_names() and name not in pat.registered_pattern_names(False)
         assert re.search(rf'builder::RegisterPattern\(\s*"{name}",', text)
-    assert raw.count("/*enabled_by_default=*/false);") == 3
-    assert f'MakeNode("{pat.ENCODED_FUSED_OP}",' in text
-    assert f'Register<Mi355x{pat.ENCODED_FUSED_OP}>(kFusedDomain, "{pat.ENCODED_FUSED_OP}");' in _adapter()
+    assert raw.count("/*enabled_by_default=*/false);") == 4
+    for op in (pat.ENCODED_FUSED_OP, pat.GROUPED_FUSED_OP):
+        assert f'MakeNode("{op}",' in text
+        assert f'Register<Mi355x{op}>(kFusedDomain, "{op}");' in _adapter()
+    assert 'AddInt(fused, "transB",' in text
     assert f'kFusedDomain = "{pat.FUSED_DOMAIN}"' in text
     assert f'MakeNode("{pat.FUSED_OP}",' in text and f'MakeNode("{pat.PACKED_FUSED_OP}",' in text
     assert 'AddInt(fused, "axis",' in text and 'AddInt(fused, "cast_to", cast_to)' in text

@@ -261,3 +261,78 @@ def test_encoded_no_match(pt, kw, reason):
     m = pt.create_registered_pattern("DequantizeEncodedMatMulGpu").match(g, mm)
     assert not m and m.reason == reason
     assert pt.optimize(g, [pt.create_registered_pattern("DequantizeEncodedMatMulGpu")]) == 0
+
+
+# ---- DequantizeLinear -> [Cast] -> GroupedMatMul ----------------------------
+
+def _grouped_graph(pt, cast_to=16, zp=False, bias=True, w_type=None, s_type=None, w_shape=(4, 64, 32),
+                   s_shape=(4, 1, 32), axis=1, trans_b=0, extra_use=False, gmm_attrs=None):
+    N = pt.Node
+    nodes = [N("DequantizeLinear", ["W", "s", "z" if zp else ""], ["Wd"], attrs={"axis": axis}, name="dq")]
+    w = "Wd"
+    if cast_to is not None:
+        nodes.append(N("Cast", ["Wd"], ["Wc"], attrs={"to": cast_to}, name="cast"))
+        w = "Wc"
+    attrs = {"transB": trans_b} if gmm_attrs is None else gmm_attrs
+    nodes.append(N("GroupedMatMul", ["X", w, "I"] + (["B"] if bias else []), ["Y"], attrs=attrs, name="gmm"))
+    if extra_use:
+        nodes.append(N("Relu", ["Wd"], ["R"], name="relu"))
+    w_type = pt.FLOAT8E4M3FN if w_type is None else w_type
+    s_type = pt.FLOAT if s_type is None else s_type
+    info = {"W": (w_type, w_shape), "s": (s_type, s_shape), "z": (w_type, s_shape)}
+    return pt.Graph(nodes, {"W", "s", "z"}, ["X", "I"] + (["B"] if bias else []),
+                    ["Y"] + (["R"] if extra_use else []), info)
+
+
+def _grouped_pattern(pt, fp8_scaled_sums=False):
+    p = pt.create_registered_pattern("DequantizeLinearGroupedMatMulGpu")
+    p.fp8_scaled_sums = fp8_scaled_sums
+    return p
+
+
+@pytest.mark.parametrize("cast_to,zp,bias,w_type,s_type,s_shape,axis,trans_b", [
+    (16, False, True, 17, 1, (4, 1, 32), 1, 0),    # fp8 experts, per (expert, column): scaled sums (opt-in)
+    (16, False, False, 17, 1, (4,), 0, 0),          # per expert
+    (None, True, True, 22, 10, (4, 2, 32), 1, 0),   # INT4 blocked along K, FLOAT16 scales
+    (10, True, False, 2, 1, (32,), 1, 1),           # UINT8 per column ([G, N, K]: axis 1), transB
+])
+def test_grouped_rewrite(pt, olamd, cast_to, zp, bias, w_type, s_type, s_shape, axis, trans_b):
+    w_shape = (4, 32, 64) if trans_b else (4, 64, 32)
+    g = _grouped_graph(pt, cast_to, zp, bias, w_type, s_type, w_shape, s_shape, axis, trans_b)
+    assert pt.optimize(g, [_grouped_pattern(pt, fp8_scaled_sums=True)]) == 1
+    (n,) = g.nodes
+    assert (n.domain, n.op_type) == (pt.FUSED_DOMAIN, pt.GROUPED_FUSED_OP)
+    assert n.inputs == ["X", "W", "s", "z" if zp else "", "I"] + (["B"] if bias else [])
+    assert n.outputs == ["Y"]
+    assert n.attrs == {"axis": axis, "cast_to": cast_to or 0, "transB": trans_b}
+    assert f"{n.domain}:{n.op_type}" in olamd.KERNELS
+
+
+@pytest.mark.parametrize("kw,reason", [
+    (dict(), "fp8_scaled_sums=True allows it"),
+    (dict(extra_use=True), "another consumer"),
+    (dict(cast_to=1), "FLOAT16 or BFLOAT16"),
+    (dict(cast_to=None), "would run in FLOAT"),
+    (dict(w_shape=(64, 32), s_shape=(32,), axis=1), "not 3-D"),
+    (dict(w_type=3, s_shape=(4, 1, 16)), "blocked scale does not fit"),
+    (dict(w_type=3, s_shape=(31,), axis=2), "differs from the axis dimension"),
+    (dict(w_type=3, s_shape=(4, 32), axis=2), "neither 1 nor 3"),
+    (dict(w_type=3, s_shape=(32,), axis=3), "axis out of range"),
+    (dict(w_type=7), "no fused kernel"),
+    (dict(s_type=10), "Cast of a FLOAT16"),
+    (dict(gmm_attrs={"transB": 0, "alpha": 1}), "attribute other than transB"),
+])
+def test_grouped_no_match(pt, kw, reason):
+    g = _grouped_graph(pt, **kw)
+    gmm = next(n for n in g.nodes if n.op_type == "GroupedMatMul")
+    m = _grouped_pattern(pt).match(g, gmm)
+    assert not m and reason in m.reason, m.reason
+
+
+def test_grouped_fp8_exact_layouts_need_no_opt_in(pt):
+    """fp8 experts whose scale varies along K, or transposed, take the
+    dequantizing path (the chain's roundings): no opt-in needed."""
+    for kw in (dict(s_shape=(4, 2, 32), axis=1), dict(s_shape=(64,), axis=1),
+               dict(w_shape=(4, 32, 64), s_shape=(4, 32, 1), axis=2, trans_b=1)):
+        g = _grouped_graph(pt, **kw)
+        assert pt.optimize(g, [_grouped_pattern(pt)]) == 1, kw
