@@ -255,7 +255,12 @@ void LaunchDqGroupedMatMul(const DqGroupedParams &p, hipStream_t stream) {
     LaunchGroupedMatMul(g, stream);
     return;
   }
-  hipLaunchKernelGGL(GroupRouteKernel, dim3(1), dim3(kRouteThreads), GroupedRouteLds(p.g.G), stream, p.g);
+  // 256 x 256 tiles (as configuration 4's fp8 GEMM) when K takes whole K
+  // steps; the routing then counts 256-column tiles
+  GroupedParams gp = p.g;
+  const bool wide = p.g.K % 64 == 0;
+  if (wide) gp.nbn = (p.g.N + 255) / 256;
+  hipLaunchKernelGGL(GroupRouteKernel, dim3(1), dim3(kRouteThreads), GroupedRouteLds(gp.G), stream, gp);
   mg::GemmArgs g{};
   g.A = p.g.A;
   g.B = p.X;
@@ -275,7 +280,8 @@ void LaunchDqGroupedMatMul(const DqGroupedParams &p, hipStream_t stream) {
   g.grp_sel = (int)p.g.S;
   g.grp_b_stride = p.g.K * p.g.N;
   g.grp_bias = p.g.bias;
-  mg::LaunchGrouped<mg::kOutBf16, 1, mg::kBf16F8>(g, GroupedMaxTiles(p.g), stream);
+  if (wide) mg::LaunchGrouped<mg::kOutBf16, 1, mg::kBf16F8, 4>(g, GroupedMaxTiles(gp), stream);
+  else mg::LaunchGrouped<mg::kOutBf16, 1, mg::kBf16F8, 2>(g, GroupedMaxTiles(gp), stream);
 }
 
 }  // namespace onnxl_amd

@@ -233,8 +233,8 @@ __global__ __launch_bounds__(kThreads, 1) void MfmaGemmKernel(const GemmArgs p) 
   constexpr bool RA = ZP, CB = ZP;
   constexpr bool GRP = GM == 1 || GM == 2;  // grouped (routing tables)
   constexpr bool BT = GM == 2 || GM == 3 || CV;
-  static_assert(GM == 0 || ((KIND == kH16 || (KIND == kBf16F8 && GM == 1)) && WB == 2 && !ZP),
-                "grouped mode: 16-bit operands (or fp8 B [K, N] per group), 128-column tiles");
+  static_assert(GM == 0 || (((KIND == kH16 && WB == 2) || (KIND == kBf16F8 && GM == 1)) && !ZP),
+                "grouped mode: 16-bit operands in 128-column tiles, or fp8 B [K, N] per group");
   static_assert(!CV || (KIND == kI8 && WB == 2 && GM == 0), "implicit convolution: int8, 128-column tiles");
   using T = Traits<KIND>;
   using Acc = typename T::Acc;
@@ -1022,9 +1022,11 @@ template <int OUT> inline void LaunchBT(const GemmArgs &p, hipStream_t s) {
 
 // Grouped launch: `max_tiles` workgroups, an upper bound of the tiles the
 // routing table holds (the rest leave at once).
-template <int OUT, int GM, int KIND = kH16>
+// WB = 4 (256-column tiles, fp8 B only) needs K % kKStep == 0 and routing
+// tables counted in 256-column tiles.
+template <int OUT, int GM, int KIND = kH16, int WB = 2>
 inline void LaunchGrouped(const GemmArgs &p, int64_t max_tiles, hipStream_t s) {
-  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, false, false, false, 2, GM>), dim3((unsigned)max_tiles),
+  hipLaunchKernelGGL((MfmaGemmKernel<KIND, OUT, false, false, false, WB, GM>), dim3((unsigned)max_tiles),
                      dim3(kThreads), 0, s, p);
 }
 

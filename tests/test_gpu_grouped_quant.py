@@ -60,10 +60,13 @@ FP8_LAYOUTS = [("tensor", 1, lambda G, K, N: ()), ("expert", 0, lambda G, K, N: 
 
 @pytest.mark.parametrize("layout", FP8_LAYOUTS, ids=[f[0] for f in FP8_LAYOUTS])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_fp8_experts_dyadic_bit_exact(olamd, oracle, dev, layout, with_bias):
+@pytest.mark.parametrize("K,N", [(1024, 384), (96, 48)], ids=["wide_tiles", "half_k_step"])
+def test_fp8_experts_dyadic_bit_exact(olamd, oracle, dev, layout, with_bias, K, N):
+    """256 x 256 tiles when K takes whole 64-deep K steps (K = 1024, with a
+    partly filled last column tile), 256 x 128 tiles otherwise (K = 96)."""
     name, axis, sshape = layout
-    G, K, N, M, S = 8, 1024, 384, 300, 2
-    rng = np.random.default_rng(zlib.crc32(f"{name}{with_bias}".encode()))
+    G, M, S = 8, 300, 2
+    rng = np.random.default_rng(zlib.crc32(f"{name}{with_bias}{K}".encode()))
     a = dy.sparse_act(rng, (M, K), dy.DENSITY["fp8"])
     codes, q = dy.fp8_codes(oracle, rng, (G, K, N))
     scale = dy.pow2(rng, sshape(G, K, N), 3, 6)
