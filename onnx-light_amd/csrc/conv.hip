@@ -257,6 +257,17 @@ int64_t PaddedCols(const ConvGeom &g) { return (g.out[2] - 1) * g.s[2] + (g.k[2]
 __host__ __device__ inline int64_t RowTileStride(int64_t W) { return (W / 4 + 3) | 1; }  // dwords
 int64_t RowTileBytes(int64_t C, int64_t W) { return W % 4 == 0 ? (C * RowTileStride(W) + 4) * 4 : C * W; }
 
+// Word stores of the operands through the XCD's L2 (the device-scope sc1
+// policy of the GEMM epilogue's stores): the kernel then ends without a
+// writeback of dirty lines, and the GEMM, whose tiles read them from other
+// XCDs, finds them in memory.  `rs` covers the block's own output row.
+__device__ __forceinline__ void PutThrough(__amdgpu_buffer_rsrc_t rs, uint32_t e, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, rs, 4 * e, 0, 16);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t RowRsrc(void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
+}
+
 // One launch builds both operands.  Blocks 0 .. N * Hp - 1 write padded row
 // hp of image n: xh[n, hp, wp, c] = x[n, c, hp - pt, wp - pl], or x's zero
 // point outside the input; the C input rows of W bytes are staged in LDS,
@@ -276,15 +287,22 @@ __global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom
   // 32-bit index arithmetic inside the loops (64-bit division is a long
   // software sequence): every per-block count is below 2^16
   const uint32_t H = (uint32_t)g.in[1], W = (uint32_t)g.in[2], C = (uint32_t)g.C;
-  const int64_t b = blockIdx.x;
+  // Workgroup i runs on XCD i % 8; logical block b is dealt so that each XCD
+  // owns a contiguous run of blocks.  Consecutive padded rows of an image read
+  // the same input cache lines (one 128-byte line holds parts of several
+  // rows), and then read them through one L2 instead of eight.
+  const int64_t nb = (int64_t)gridDim.x, pid = blockIdx.x;
+  const int64_t xcd = pid % 8, per = nb / 8, extra = nb % 8;
+  const int64_t b = xcd * per + (xcd < extra ? xcd : extra) + pid / 8;
   const uint32_t cq = C / 4, pl = (uint32_t)g.pb[2];
   const uint32_t zp4 = x_zp * 0x01010101u;
   if (b < g.N * Hp && dwords) {
     const int64_t n = b / Hp, hp = b - n * Hp, h = hp - g.pb[1];
     uint32_t *dst = reinterpret_cast<uint32_t *>(xh + (n * Hp + hp) * Wp * C);
     const uint32_t wpad = (uint32_t)Wp;
+    const __amdgpu_buffer_rsrc_t rsD = RowRsrc(dst, Wp * C);
     if (h < 0 || h >= (int64_t)H) {
-      for (uint32_t e = threadIdx.x; e < wpad * cq; e += kCBlock) dst[e] = zp4;
+      for (uint32_t e = threadIdx.x; e < wpad * cq; e += kCBlock) PutThrough(rsD, e, zp4);
       return;
     }
     const uint32_t wd = W / 4, ts = (uint32_t)RowTileStride(W);
@@ -322,7 +340,7 @@ __global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t wp = 4 * q + j + pl;  // input columns past Wp are never read
-        if (wp < wpad) dst[wp * cq + qd] = px[j];
+        if (wp < wpad) PutThrough(rsD, wp * cq + qd, px[j]);
       }
     }
     // the padding columns [0, pl) and [pl + W, Wp): x's zero point
@@ -330,7 +348,7 @@ __global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom
     const uint32_t pads = left + (wpad > right0 ? wpad - right0 : 0u);
     for (uint32_t e = threadIdx.x; e < pads * cq; e += kCBlock) {
       const uint32_t k = e / cq, wp = k < left ? k : right0 + (k - left);
-      dst[wp * cq + (e - k * cq)] = zp4;
+      PutThrough(rsD, wp * cq + (e - k * cq), zp4);
     }
   } else if (b < g.N * Hp) {
     // one padded row, byte loads: xh[n, hp, wp, c] from the staged C x W bytes
@@ -374,11 +392,11 @@ __global__ __launch_bounds__(kCBlock) void ImplicitOperandsKernel(const ConvGeom
       for (uint32_t e = threadIdx.x; e < Kc; e += kCBlock) tile[e] = w[m * Kc + e];
     }
     __syncthreads();
-    uint32_t *dst = reinterpret_cast<uint32_t *>(wr + m * Kc);
+    const __amdgpu_buffer_rsrc_t rsD = RowRsrc(wr + m * Kc, Kc);
     for (uint32_t e = threadIdx.x; e < kq; e += kCBlock) {
       const uint32_t tap = (4 * e) / C, c = 4 * e - tap * C;
       const uint8_t *t = tile + c * T + tap;
-      dst[e] = (uint32_t)t[0] | (uint32_t)t[T] << 8 | (uint32_t)t[2 * T] << 16 | (uint32_t)t[3 * T] << 24;
+      PutThrough(rsD, e, (uint32_t)t[0] | (uint32_t)t[T] << 8 | (uint32_t)t[2 * T] << 16 | (uint32_t)t[3 * T] << 24);
     }
   }
 }
