@@ -872,19 +872,68 @@ __device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<23> &r) {
   r.hdr[0] = hdr.x, r.hdr[1] = hdr.y, r.q[0] = q.x, r.q[1] = q.y;
 }
 
+// Reads of a block staged in LDS at byte offset o of the stage array s (16-
+// byte aligned).  q3_k and q6_k blocks are only 2-byte aligned, and 16-bit
+// LDS reads cost about 20 LDS cycles each there, so their fields are read as
+// the aligned dwords around them and funnel-shifted into place
+// (v_alignbit_b32); offsets stay integers into s so the reads remain LDS
+// reads.  The other formats read as LoadK does.
+__device__ __forceinline__ uint32_t LdsDword(const uint8_t *s, int o) {
+  return *reinterpret_cast<const uint32_t *>(s + o);  // o % 4 == 0
+}
+// the 8 bytes at offset o (o even): the three dwords around them
+__device__ __forceinline__ void LdsBytes8(const uint8_t *s, int o, uint32_t out[2]) {
+  const int b = o & ~3;
+  const uint32_t sh = 8u * (uint32_t)(o & 3);
+  const uint32_t d0 = LdsDword(s, b), d1 = LdsDword(s, b + 4), d2 = LdsDword(s, b + 8);
+  out[0] = __builtin_amdgcn_alignbit(d1, d0, sh);
+  out[1] = __builtin_amdgcn_alignbit(d2, d1, sh);
+}
+// the 16 bits at offset o (o even)
+__device__ __forceinline__ uint32_t LdsHalf(const uint8_t *s, int o) {
+  return (LdsDword(s, o & ~3) >> (8u * (uint32_t)(o & 3))) & 0xffffu;
+}
+template <class R> __device__ __forceinline__ void LoadKLds(const uint8_t *s, int o, int i0, R &r) {
+  LoadK(s + o, i0, r);
+}
+__device__ __forceinline__ void LoadKLds(const uint8_t *s, int o, int i0, KRaw<11> &r) {
+  LdsBytes8(s, o + (i0 & 31), r.hm);
+  LdsBytes8(s, o + 32 + (i0 >> 7) * 32 + (i0 & 31), r.q);
+  const int g = i0 >> 4;
+  r.s = s[o + 96 + (g & 7)] | (uint32_t)s[o + 104 + (g & 3)] << 8 | LdsHalf(s, o + 108) << 16;
+}
+__device__ __forceinline__ void LoadKLds(const uint8_t *s, int o, int i0, KRaw<14> &r) {
+  LdsBytes8(s, o + (i0 >> 7) * 64 + (i0 & 63), r.l);
+  LdsBytes8(s, o + 128 + (i0 >> 7) * 32 + (i0 & 31), r.hb);
+  r.d = LdsHalf(s, o + 208);
+  r.sc = s[o + 192 + (i0 >> 4)];
+}
+
 // The products below are exact in fp32 wherever the reference rounds them
 // (a 11-bit fp16 d times a scale of at most 6 bits, times a code of at most
 // 5 bits), so ds * q - dm in one fused multiply-add, or ds * q, rounds as the
 // reference's separately rounded steps do; iq4_xs's ds * value (8-bit
 // values) is one rounded product, as in the reference.
+// Four codes at a time: one shift and mask per dword leaves each code in
+// its own byte, which v_cvt_f32_ubyte0..3 converts directly.
+__device__ __forceinline__ void ByteFloats(uint32_t t, float *f) {
+  f[0] = (float)(t & 0xffu);
+  f[1] = (float)((t >> 8) & 0xffu);
+  f[2] = (float)((t >> 16) & 0xffu);
+  f[3] = (float)(t >> 24);
+}
+
 __device__ __forceinline__ void DecodeK(const KRaw<10> &r, int i0, h2_t wp[4]) {
   const float d = F16ToF32((uint16_t)(r.dd & 0xffffu)), dmin = F16ToF32((uint16_t)(r.dd >> 16));
   const uint32_t b = (r.sc >> (8 * ((i0 >> 4) & 3))) & 0xffu;
   const float ds = d * (float)(b & 15u), dm = dmin * (float)(b >> 4);
   const int sh = 2 * ((i0 >> 5) & 3);
+  float f[8];
+  ByteFloats((r.q[0] >> sh) & 0x03030303u, f);
+  ByteFloats((r.q[1] >> sh) & 0x03030303u, f + 4);
   float v[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(ds, (float)((ByteOf(r.q, e) >> sh) & 3u), -dm);
+  for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(ds, f[e], -dm);
 #pragma unroll
   for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
 }
@@ -895,11 +944,22 @@ __device__ __forceinline__ void DecodeK(const KRaw<11> &r, int i0, h2_t wp[4]) {
   const int hi = (int)(((r.s >> 8) & 0xffu) >> (2 * ((g >> 2) & 3))) & 3;
   const float ds = F16ToF32((uint16_t)(r.s >> 16)) * (float)((lo | hi << 4) - 32);
   const int hsh = (i0 >> 5) & 7, qsh = 2 * ((i0 >> 5) & 3);
-  float v[8];
+  // u = code + 4 * high-mask bit (0..7 per byte) and q = u - 4.  For a
+  // finite ds, ds * u - 4 ds in one fused step is the exact ds * q (both
+  // products are exact), rounded as the reference rounds its product; an
+  // infinite or NaN ds takes the reference's own steps (inf * 0 = NaN).
+  float f[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int q = (int)((ByteOf(r.q, e) >> qsh) & 3u) - ((ByteOf(r.hm, e) >> hsh) & 1u ? 0 : 4);
-    v[e] = ds * (float)q;
+  for (int h = 0; h < 2; ++h)
+    ByteFloats(((r.q[h] >> qsh) & 0x03030303u) | (((r.hm[h] >> hsh) & 0x01010101u) << 2), f + 4 * h);
+  float v[8];
+  if (__builtin_isfinite(ds)) {
+    const float ds4 = 4.f * ds;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(ds, f[e], -ds4);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = ds * (f[e] - 4.f);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
@@ -914,12 +974,13 @@ __device__ __forceinline__ void DecodeK(const KRaw<13> &r, int i0, h2_t wp[4]) {
   const uint32_t minimum = g < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
   const float ds = d * (float)scale, dm = dmin * (float)minimum;
   const int nsh = 4 * (g & 1), hsh = g & 7;
+  float f[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    ByteFloats(((r.q[h] >> nsh) & 0x0f0f0f0fu) | (((r.hb[h] >> hsh) & 0x01010101u) << 4), f + 4 * h);
   float v[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t q = ((ByteOf(r.q, e) >> nsh) & 15u) | (((ByteOf(r.hb, e) >> hsh) & 1u) << 4);
-    v[e] = __builtin_fmaf(ds, (float)q, -dm);
-  }
+  for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(ds, f[e], -dm);
 #pragma unroll
   for (int e = 0; e < 4; ++e) wp[e] = h2_t{(_Float16)v[2 * e], (_Float16)v[2 * e + 1]};
 }
@@ -1109,9 +1170,8 @@ __global__ __launch_bounds__(256) void GemvKLdsKernel(const uint16_t *__restrict
         for (int c = 0; c < kGvCols; ++c) {
           const int r = wave * kGvCols + c;
           const int64_t start = (row_of(r) * nb + kb0) * kBytes;
-          const uint8_t *p = &stage[buf][r * kSlot + (int)(start & 15) + bb * kBytes];
           KRaw<TYPE> raw;
-          LoadK(p, i0, raw);
+          LoadKLds(stage[buf], r * kSlot + (int)(start & 15) + bb * kBytes, i0, raw);
           DecodeK(raw, i0, wp[c]);
         }
 #pragma unroll
@@ -1147,14 +1207,12 @@ template <int TYPE, int M> constexpr int KStageBlocks() {
   return KLayout<TYPE>::bytes <= 136 && M <= 4 ? 8 : 4;
 }
 
-// q6_k stays on the direct kernel: its 2-byte aligned fields are read from
-// LDS as 16-bit words, which cost about 20 LDS cycles per instruction
-// (counters on [1, 4096] x [14336, 4096]: 31.7 us staged against 25.1 us
-// direct); every other format measured faster staged.
+// The staged kernel for every format while the weight's byte offsets fit a
+// buffer descriptor; the direct kernel past that.
 template <int TYPE, int M>
 void LaunchGemvKM(const uint16_t *a, const uint8_t *w, int64_t N, int64_t K, uint16_t *y, hipStream_t s) {
   const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
-  if (TYPE != 14 && N * (K / 256) * KLayout<TYPE>::bytes < (int64_t(1) << 31) - (int64_t(1) << 20))
+  if (N * (K / 256) * KLayout<TYPE>::bytes < (int64_t(1) << 31) - (int64_t(1) << 20))
     hipLaunchKernelGGL((GemvKLdsKernel<TYPE, M, KStageBlocks<TYPE, M>()>), g, dim3(256), 0, s, a, w, N, K, y);
   else
     hipLaunchKernelGGL((GemvKKernel<TYPE, M>), g, dim3(256), 0, s, a, w, N, K, y);
