@@ -12,6 +12,7 @@
 #include "common.hpp"
 #include "device_codecs.hpp"
 #include "kernels.hpp"
+#include <type_traits>
 
 // The lattice grids of the IQ profiles, in constant memory (33 KB).
 #define GGUF_CODEBOOK_QUAL static __constant__ const
@@ -713,6 +714,213 @@ __global__ __launch_bounds__(256) void GemvQ80Kernel(const uint16_t *__restrict_
   }
 }
 
+// Streamed q4_0 / q8_0 GEMV for K % 256 == 0 (every row starts 16-byte
+// aligned) and a weight below 2 GiB, the same sums as the two kernels above
+// in another order.  A workgroup is one wave and computes 4 consecutive
+// outputs.  It streams its 4 rows in chunks of 128 q4_0 / 64 q8_0 blocks
+// (2304 / 2176 bytes of each row): a chunk is requested at once as nine
+// 16-byte loads per lane (load j: lanes 16r .. 16r + 15 read bytes
+// 256j .. 256j + 255 of row r's chunk) and decoded in 4 steps, each as soon
+// as the loads that hold its blocks have landed.  A landed load is copied to
+// the wave's LDS window and its register is reloaded with the same piece of
+// the next chunk, so the next chunk streams while this one is decoded.  The
+// activations of a step are requested right after the weight pieces the
+// step needs: vector memory loads complete in order, so the wait for them
+// never covers a later weight piece.  The wave owns its LDS window, so no
+// workgroup barrier is needed (a wave's LDS operations execute in order).
+//
+// Per lane and output, a step decodes 8 code bytes of one block: q4_0 half a
+// block (values 8h .. 8h + 7 from the low nibbles, 16 + 8h .. 23 + 8h from
+// the high ones), q8_0 a quarter (values 8h .. 8h + 7), read as three
+// aligned LDS dwords and funnel-shifted (a block starts 0 or 2 bytes into a
+// dword).  q4_0: v_perm spreads two code bytes into the low bytes of a half
+// pair, and one AND-OR per nibble pair forms 1024 + q (low nibbles, bits
+// 0-3) or 64 + q (high nibbles, bits 4-7, where the unit step of that
+// exponent is 1); subtracting 1032 or 72 gives q - 8 exactly.  q8_0: XOR
+// 0x80 per byte gives q + 128, v_perm places two of them under a 0x64 high
+// byte (1152 + q) and subtracting 1152 gives q.  The packed multiply by d
+// then rounds d * (q - 8) or d * q to FLOAT16 as the DequantizePacked ->
+// FLOAT16 chain does.  The pairs are consecutive values, as are the fp16
+// pairs of the 16-byte activation loads, and v_dot2_f32_f16 accumulates them
+// in fp32.
+// (x & mask) | bits in one v_and_or_b32 (the compiler splits it otherwise)
+__device__ __forceinline__ uint32_t AndOr(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(bits));
+  return r;
+}
+
+// the dword at byte offset o (o % 4 == 0) of an LDS stage s
+__device__ __forceinline__ uint32_t LdsDword(const uint8_t *s, int o) {
+  return *reinterpret_cast<const uint32_t *>(s + o);
+}
+
+template <int TYPE> struct Q0Stream;
+template <> struct Q0Stream<2> { static constexpr int block = 18, lanes_per_block = 2, chunk_blocks = 128; };
+template <> struct Q0Stream<8> { static constexpr int block = 34, lanes_per_block = 4, chunk_blocks = 64; };
+
+constexpr int kQsRows = 4;    // outputs per workgroup (one wave)
+constexpr int kQsPieces = 9;  // 16-byte loads per lane per chunk: 256 bytes of each row per load
+constexpr int kQsSteps = 4;   // decode steps per chunk
+
+// the last weight piece (load index) holding bytes of decode step s
+template <int TYPE> constexpr int QsLastPiece(int s) {
+  return ((s + 1) * (64 / Q0Stream<TYPE>::lanes_per_block) * Q0Stream<TYPE>::block - 1) / 256;
+}
+
+template <int TYPE, int M>
+__global__ __launch_bounds__(64) void GemvQ0StreamKernel(const uint16_t *__restrict__ a, const uint8_t *__restrict__ w,
+                                                         int64_t N, int64_t K, uint16_t *__restrict__ y) {
+  using L = Q0Stream<TYPE>;
+  constexpr int kBB = L::block;
+  constexpr int kChunk = L::chunk_blocks * kBB;         // bytes of a row per chunk
+  constexpr int kStepBlocks = 64 / L::lanes_per_block;  // blocks of a row per step
+  constexpr int kStepBytes = kStepBlocks * kBB;
+  constexpr int kActLoads = TYPE == 2 ? 2 : 1;          // 16-byte activation loads per step and row of a
+  static_assert(kStepBlocks * kQsSteps == L::chunk_blocks, "4 steps per chunk");
+  static_assert(kChunk % 16 == 0 && kChunk <= kQsPieces * 256 && kChunk > (kQsPieces - 1) * 256, "9 loads per chunk");
+  static_assert(kStepBlocks % 2 == 0, "a lane's blocks keep one alignment in every step");
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  // +16: the third code dword of the window's last block lies past it (read, never used)
+  __shared__ __align__(16) uint8_t stage[kQsRows * kChunk + 16];
+  const int lane = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * kQsRows;
+  const int64_t nb = K / 32;
+  const int64_t row_bytes = nb * kBB;  // a multiple of 16
+  const int nchunks = (int)((nb + L::chunk_blocks - 1) / L::chunk_blocks);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), (short)0, (int)(N * row_bytes), 0x00020000);
+
+  // loads: lane -> (row lr, 16-byte word lw of each 256-byte piece); rows past N reload the last
+  const int lr = lane >> 4, lw = lane & 15;
+  const uint32_t lbase = (uint32_t)((n0 + lr < N ? n0 + lr : N - 1) * row_bytes) + 16u * (uint32_t)lw;
+  auto load = [&](int c, int j) __attribute__((always_inline)) -> v4u {
+    const int off = 256 * j + 16 * lw;
+    const bool ok = off < kChunk && (int64_t)c * kChunk + off < row_bytes;
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                       rs, ok ? lbase + (uint32_t)(c * kChunk + 256 * j) : 0x80000000u, 0, 2));
+  };
+  auto put = [&](int j, const v4u &v) __attribute__((always_inline)) {
+    const int off = 256 * j + 16 * lw;
+    if (off < kChunk) *reinterpret_cast<v4u *>(&stage[lr * kChunk + off]) = v;
+  };
+
+  // decode: lane -> (block bl of each step, part h of the block's codes)
+  const int bl = lane / L::lanes_per_block, h = lane % L::lanes_per_block;
+  const int dofs = (bl * kBB) & ~3;                // the dword holding d
+  const int cofs = (bl * kBB + 2 + 8 * h) & ~3;    // the first of the three dwords holding the 8 code bytes
+  const uint32_t dsel = bl & 1 ? 0x03020302u : 0x01000100u;  // d in the high / low half, twice
+  const uint32_t csh = bl & 1 ? 0u : 16u;
+  // activations of the lane's values for step s of chunk c (clamped in a partial chunk's idle lanes)
+  auto act = [&](int c, int s, v4u (&av)[kActLoads][M]) __attribute__((always_inline)) {
+    const int64_t b = (int64_t)c * L::chunk_blocks + s * kStepBlocks + bl;
+    const int64_t k0 = (b < nb ? b : 0) * 32 + 8 * h;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int t = 0; t < kActLoads; ++t) av[t][m] = *reinterpret_cast<const v4u *>(a + m * K + k0 + 16 * t);
+  };
+
+  float acc[kQsRows][M];
+#pragma unroll
+  for (int r = 0; r < kQsRows; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+  const h2_t kM1032 = AsH2(0xE408E408u), kM72 = AsH2(0xD480D480u), kM1152 = AsH2(0xE480E480u);
+
+  v4u wr[kQsPieces];
+  v4u av[kQsSteps][kActLoads][M];
+#pragma unroll
+  for (int s = 0; s < kQsSteps; ++s) {
+#pragma unroll
+    for (int j = s ? QsLastPiece<TYPE>(s - 1) + 1 : 0; j <= QsLastPiece<TYPE>(s); ++j) wr[j] = load(0, j);
+    act(0, s, av[s]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // chunk c; MORE: the next chunk's loads are issued as this one's land.  The
+  // last chunk is a copy of its own, so every chunk before it issues the same
+  // loads in the same order and the compiler's waits count them exactly.
+  auto chunk = [&](int c, auto more_tag) __attribute__((always_inline)) {
+    constexpr bool kMore = decltype(more_tag)::value;
+    const int64_t cblocks = nb - (int64_t)c * L::chunk_blocks;  // blocks of this chunk: all when >= chunk_blocks
+#pragma unroll
+    for (int s = 0; s < kQsSteps; ++s) {
+#pragma unroll
+      for (int j = s ? QsLastPiece<TYPE>(s - 1) + 1 : 0; j <= QsLastPiece<TYPE>(s); ++j) {
+        put(j, wr[j]);
+        if (kMore) wr[j] = load(c + 1, j);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (s * kStepBlocks + bl < cblocks) {
+#pragma unroll
+        for (int r = 0; r < kQsRows; ++r) {
+          const uint8_t *base = stage + r * kChunk + s * kStepBytes;
+          const uint32_t dw = LdsDword(base, dofs);
+          const uint32_t c0 = LdsDword(base, cofs), c1 = LdsDword(base, cofs + 4), c2 = LdsDword(base, cofs + 8);
+          const h2_t dd = AsH2(__builtin_amdgcn_perm(dw, dw, dsel));
+          const uint32_t cw[2] = {__builtin_amdgcn_alignbit(c1, c0, csh), __builtin_amdgcn_alignbit(c2, c1, csh)};
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {  // code bytes 4q + 2e, 4q + 2e + 1
+              const int p = 2 * q + e;     // activation pair of these values
+              if (TYPE == 2) {
+                const uint32_t t = __builtin_amdgcn_perm(0u, cw[q], e ? 0x0c030c02u : 0x0c010c00u);
+                const h2_t wl = (AsH2(AndOr(t, 0x000f000fu, 0x64006400u)) + kM1032) * dd;
+                const h2_t wh = (AsH2(AndOr(t, 0x00f000f0u, 0x54005400u)) + kM72) * dd;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                  acc[r][m] = __builtin_amdgcn_fdot2(AsH2(av[s][0][m][p]), wl, acc[r][m], false);
+                  acc[r][m] = __builtin_amdgcn_fdot2(AsH2(av[s][kActLoads - 1][m][p]), wh, acc[r][m], false);
+                }
+              } else {
+                const uint32_t t = __builtin_amdgcn_perm(0x64646464u, cw[q] ^ 0x80808080u, e ? 0x04030402u : 0x04010400u);
+                const h2_t wv = (AsH2(t) + kM1152) * dd;
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[r][m] = __builtin_amdgcn_fdot2(AsH2(av[s][0][m][p]), wv, acc[r][m], false);
+              }
+            }
+          }
+        }
+      }
+      if (kMore) act(c + 1, s, av[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int c = 0; c + 1 < nchunks; ++c) chunk(c, std::true_type{});
+  chunk(nchunks - 1, std::false_type{});
+#pragma unroll
+  for (int r = 0; r < kQsRows; ++r) {
+    const int64_t n = n0 + r;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float s = acc[r][m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0 && n < N) y[m * N + n] = F32ToF16(s);
+    }
+  }
+}
+
+// The streamed kernel's conditions: 16-byte aligned operands, K % 256 == 0,
+// M <= 2 (its activation registers grow with M) and byte offsets that fit a
+// buffer descriptor.
+template <int TYPE> bool GemvQ0StreamFits(int64_t M, int64_t N, int64_t K, const void *a, const void *w) {
+  return M >= 1 && M <= 2 && K % 256 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+         N * (K / 32) * Q0Stream<TYPE>::block < (int64_t(1) << 31) - (int64_t(1) << 20);
+}
+
+template <int TYPE>
+void LaunchGemvQ0Stream(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
+                        hipStream_t s) {
+  const dim3 g((unsigned)((N + kQsRows - 1) / kQsRows));
+  if (M == 1)
+    hipLaunchKernelGGL((GemvQ0StreamKernel<TYPE, 1>), g, dim3(64), 0, s, a, w, N, K, y);
+  else
+    hipLaunchKernelGGL((GemvQ0StreamKernel<TYPE, 2>), g, dim3(64), 0, s, a, w, N, K, y);
+}
+
 // Fused q4_k / q6_k GEMV: y[m, n] = sum_k a[m, k] * W[n, k] with W the
 // FLOAT16 DequantizePacked values of the [N, K] weight (ggml layout: the
 // 256-value blocks of output n contiguous along k).  A workgroup computes 16
@@ -831,8 +1039,6 @@ template <> struct KRaw<23> {
   uint32_t q[2];    // 8 nibble bytes
 };
 
-__device__ __forceinline__ uint32_t ByteOf(const uint32_t w[2], int e) { return (w[e >> 2] >> (8 * (e & 3))) & 0xffu; }
-
 // q2_k blocks are 4-byte aligned (84 = 4 x 21).
 __device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<10> &r) {
   const uint32_t *w = reinterpret_cast<const uint32_t *>(p);
@@ -876,11 +1082,8 @@ __device__ __forceinline__ void LoadK(const uint8_t *p, int i0, KRaw<23> &r) {
 // byte aligned).  q3_k and q6_k blocks are only 2-byte aligned, and 16-bit
 // LDS reads cost about 20 LDS cycles each there, so their fields are read as
 // the aligned dwords around them and funnel-shifted into place
-// (v_alignbit_b32); offsets stay integers into s so the reads remain LDS
-// reads.  The other formats read as LoadK does.
-__device__ __forceinline__ uint32_t LdsDword(const uint8_t *s, int o) {
-  return *reinterpret_cast<const uint32_t *>(s + o);  // o % 4 == 0
-}
+// (v_alignbit_b32, LdsDword above); offsets stay integers into s so the
+// reads remain LDS reads.  The other formats read as LoadK does.
 // the 8 bytes at offset o (o even): the three dwords around them
 __device__ __forceinline__ void LdsBytes8(const uint8_t *s, int o, uint32_t out[2]) {
   const int b = o & ~3;
@@ -1263,6 +1466,7 @@ int GemvKAlignment(int ggml_type) {
 void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t s) {
   if (N == 0) return;
+  if (GemvQ0StreamFits<8>(M, N, K, a, w)) return LaunchGemvQ0Stream<8>(a, w, M, N, K, y, s);
   const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
   switch (M) {
   case 1: hipLaunchKernelGGL(GemvQ80Kernel<1>, g, dim3(256), 0, s, a, w, N, K, y); break;
@@ -1285,6 +1489,7 @@ bool GemvQ40Eligible(int64_t M, int64_t K, const void *a, const void *w) {
 void LaunchGemvQ40(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, int64_t K, uint16_t *y,
                    hipStream_t s) {
   if (N == 0) return;
+  if (GemvQ0StreamFits<2>(M, N, K, a, w)) return LaunchGemvQ0Stream<2>(a, w, M, N, K, y, s);
   const dim3 g((unsigned)((N + kGvRows - 1) / kGvRows));
   switch (M) {
   case 1: hipLaunchKernelGGL(GemvQ40Kernel<1>, g, dim3(256), 0, s, a, w, N, K, y); break;

@@ -210,6 +210,18 @@ def test_packed_gemv_dyadic_bit_exact(olamd, oracle, dev, fmt, M, N):
     _assert_exact(got, _chain_rows(oracle, case, np.arange(M)), f"{fmt} GEMV, oracle chain")
 
 
+@pytest.mark.parametrize("fmt", ["gguf:q4_0", "gguf:q8_0"])
+@pytest.mark.parametrize("M,N,K", [(1, 37, 256), (2, 129, 6144), (1, 1024, 14336), (2, 6, 8448), (2, 4096, 4096)])
+def test_streamed_q0_gemv_dyadic_bit_exact(olamd, oracle, dev, fmt, M, N, K):
+    """The streamed q4_0 / q8_0 GEMV (M <= 2, K % 256 == 0): one partial
+    chunk, several chunks with a partial last one, N not a multiple of the 4
+    outputs of a workgroup."""
+    case = dy.gguf_case(oracle, np.random.default_rng(M * N + K + len(fmt)), M, K, N, fmt)
+    y = olamd.dequantize_packed_matmul(bits_tensor(case["a_bits"], "f16", dev), T(case["x"], dev), fmt, (N, K))
+    got = tensor_bits(y)
+    _assert_exact(got, dy.exact_out_bits(oracle, case["a"], case["w"], "f16"), f"{fmt} GEMV {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("fmt,block_bytes", [("gguf:q4_0", 18), ("gguf:q8_0", 34), ("gguf:q2_k", 84),
                                              ("gguf:q3_k", 110), ("gguf:q4_k", 144), ("gguf:q5_k", 176),
                                              ("gguf:q6_k", 210), ("gguf:iq4_xs", 136)])

@@ -134,7 +134,7 @@ def test_k_quant_gemv_vs_chain(olamd, oracle, dev, fmt, M, N, K):
 
 
 _GEMV_SHAPES = [(1, 96, 64), (3, 200, 256), (8, 64, 4096), (2, 1000, 1024), (1, 14336, 4096), (5, 37, 2112),
-                (4, 129, 6144)]
+                (4, 129, 6144), (1, 37, 256), (2, 129, 6144), (1, 1024, 14336), (2, 6, 8448)]
 
 
 @pytest.mark.parametrize("fmt,block_bytes", [("gguf:q4_0", 18), ("gguf:q8_0", 34)])
