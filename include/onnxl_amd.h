@@ -440,6 +440,56 @@ int onnxl_amd_dequantize_gptq(const char *format, const onnxl_amd_tensor *qweigh
                               const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
                               int64_t bits, int64_t group_size, onnxl_amd_tensor *y, void *stream);
 
+/* bitsandbytes weights (onnx_core/runtime/bitsandbytes.cc; the encoding
+ * "onnx_light.bitsandbytes_weights.v1", imported by ImportBitsAndBytesWeights
+ * and decoded by ReconstructBitsAndBytesWeights, bitsandbytes.cc:502-539,
+ * through DequantizeTensor).  The caller parses the weight's quant state
+ * (the JSON of bitsandbytes.cc:59-199) and passes its numbers: format 0 nf4,
+ * 1 fp4, 2 int8; the logical [rows, cols] = [out_features, in_features];
+ * block_size (32 .. 4096, a power of two; 0 for int8); nested_block_size 0 or
+ * 256 and its nested_offset.  4-bit: weight UINT8 with ceil(rows * cols / 2)
+ * elements (the flattened weight's codes, the even element in the high
+ * nibble), absmax FLOAT [blocks] or, nested, UINT8 [blocks] with
+ * nested_absmax FLOAT [ceil(blocks / 256)] and nested_quant_map FLOAT [256],
+ * quant_map FLOAT [16] (the format's own table); int8: weight INT8
+ * [rows, cols], absmax the FLOAT row maxima weight_scb [rows], the rest
+ * null.  The reference's checks (Geometry, CheckTensor, CheckParameters,
+ * bitsandbytes.cc:222-258, 317-379) raise INVALID_ARGUMENT with its messages.
+ *
+ * onnxl_amd_dequantize_bitsandbytes decodes to y [rows, cols] of y's dtype
+ * (FLOAT, FLOAT16 or BFLOAT16): value = fp32(table[code] * scale), scale the
+ * block's absmax, or fp32(fp32(nested_quant_map[code] * nested_absmax) +
+ * nested_offset), or the row's fp32(weight_scb / 127); rounded to nearest
+ * even, a value that is not finite raising "bitsandbytes nonfinite
+ * reconstruction.".
+ *
+ * onnxl_amd_prepare_bitsandbytes runs the same checks, reconstructs every
+ * value in reconstruction_dtype (the activations' dtype of the MatMul it
+ * feeds) to raise that error once, and writes the resolved FLOAT scale of
+ * every block (int8: every row) into a caller-allocated device buffer of
+ * onnxl_amd_prepare_bitsandbytes_size bytes.  onnxl_amd_bitsandbytes_matmul
+ * then computes MatMul(a, Transpose(Dequantize(Q, dtype = a's dtype))) per
+ * call from the unchanged weight and those scales: y [..., rows] of a's
+ * dtype (FLOAT16 or BFLOAT16) for a [..., cols]; no counterpart in the
+ * reference as one call (its chain is the Dequantize kernel,
+ * kernels/kernel_dequantize.cc:10-16, then Transpose and MatMul,
+ * km/kernel_matmul.cc:225-253). */
+int onnxl_amd_dequantize_bitsandbytes(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                      int64_t nested_block_size, float nested_offset, const onnxl_amd_tensor *weight,
+                                      const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+                                      const onnxl_amd_tensor *nested_absmax,
+                                      const onnxl_amd_tensor *nested_quant_map, onnxl_amd_tensor *y, void *stream);
+int onnxl_amd_prepare_bitsandbytes_size(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                        int64_t *scale_bytes);
+int onnxl_amd_prepare_bitsandbytes(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                   int64_t nested_block_size, float nested_offset, const onnxl_amd_tensor *weight,
+                                   const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+                                   const onnxl_amd_tensor *nested_absmax, const onnxl_amd_tensor *nested_quant_map,
+                                   int32_t reconstruction_dtype, onnxl_amd_tensor *scales, void *stream);
+int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t cols,
+                                  int64_t block_size, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales,
+                                  onnxl_amd_tensor *y, void *stream);
+
 /* Waits for all work queued by this library on `stream`. */
 int onnxl_amd_synchronize(void *stream);
 

@@ -104,6 +104,13 @@ def lib() -> ctypes.CDLL:
                                                   ctypes.POINTER(I64), ctypes.POINTER(I64)]
         L.onnxl_amd_prepare_gptq.argtypes = [CS, TP, TP, TP, TP, I64, I64, I64, I64, PT, PT, PT, ctypes.c_void_p]
         L.onnxl_amd_dequantize_gptq.argtypes = [CS, TP, TP, TP, TP, I64, I64, I64, I64, TP, ctypes.c_void_p]
+        F32 = ctypes.c_float
+        L.onnxl_amd_dequantize_bitsandbytes.argtypes = [I32, I64, I64, I64, I64, F32, TP, TP, TP, TP, TP, TP,
+                                                        ctypes.c_void_p]
+        L.onnxl_amd_prepare_bitsandbytes_size.argtypes = [I32, I64, I64, I64, ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_bitsandbytes.argtypes = [I32, I64, I64, I64, I64, F32, TP, TP, TP, TP, TP, I32, PT,
+                                                     ctypes.c_void_p]
+        L.onnxl_amd_bitsandbytes_matmul.argtypes = [TP, I32, I64, I64, I64, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -346,6 +353,72 @@ def dequantize_awq(variant: str, qweight, qzeros, scales, K: int, N: int, group_
     _check(lib().onnxl_amd_dequantize_awq(variant.encode(), describe(qweight), describe(qzeros), describe(scales),
                                           K, N, bits, group_size, describe(out),
                                           _stream_of(qweight, qzeros, scales, out)))
+    return out
+
+
+BNB_FORMATS = {"nf4": 0, "fp4": 1, "int8": 2}
+
+
+class BnbWeight:
+    """A bitsandbytes weight (bitsandbytes.cc) of logical shape [rows, cols]
+    = [out_features, in_features]: the tensors of its checkpoint and the
+    numbers of its quant state.  fmt "nf4" / "fp4": weight uint8 packed codes,
+    absmax float32 [blocks] (or uint8 codes with nested_absmax and
+    nested_quant_map, nested_block 256, nested_offset), quant_map float32
+    [16]; "int8": weight int8 [rows, cols], absmax the row maxima
+    (weight_scb)."""
+
+    def __init__(self, fmt, rows, cols, weight, absmax, quant_map=None, block=0, nested_absmax=None,
+                 nested_quant_map=None, nested_block=0, nested_offset=0.0):
+        self.fmt, self.rows, self.cols, self.block = fmt, rows, cols, block
+        self.weight, self.absmax, self.quant_map = weight, absmax, quant_map
+        self.nested_absmax, self.nested_quant_map = nested_absmax, nested_quant_map
+        self.nested_block, self.nested_offset = nested_block, nested_offset
+        self.scales = None  # set by prepare_bitsandbytes
+
+    def args(self):
+        code = UINT8 if self.fmt != "int8" else INT8
+        return (BNB_FORMATS[self.fmt], self.rows, self.cols, self.block, self.nested_block,
+                ctypes.c_float(self.nested_offset), describe(self.weight, code), describe(self.absmax),
+                describe(self.quant_map), describe(self.nested_absmax), describe(self.nested_quant_map))
+
+    def tensors(self):
+        return (self.weight, self.absmax, self.quant_map, self.nested_absmax, self.nested_quant_map)
+
+
+def dequantize_bitsandbytes(w: BnbWeight, output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_bitsandbytes: the weight as [rows, cols] values."""
+    out = _decode_out(w.cols, w.rows, output_dtype, w.tensors(), out)
+    _check(lib().onnxl_amd_dequantize_bitsandbytes(*w.args(), describe(out), _stream_of(*w.tensors(), out)))
+    return out
+
+
+def prepare_bitsandbytes(w: BnbWeight, reconstruction_dtype: int = FLOAT16) -> BnbWeight:
+    """onnxl_amd_prepare_bitsandbytes: the checks and the resolved per-block
+    scales (device float32), kept on w for bitsandbytes_matmul."""
+    torch = _torch()
+    n = ctypes.c_int64(0)
+    _check(lib().onnxl_amd_prepare_bitsandbytes_size(BNB_FORMATS[w.fmt], w.rows, w.cols, w.block, ctypes.byref(n)))
+    dev = torch.device("cuda", torch.cuda.current_device())
+    storage = torch.empty(max(n.value // 4, 4), dtype=torch.float32, device=dev)
+    d = describe(storage)
+    _check(lib().onnxl_amd_prepare_bitsandbytes(*w.args(), reconstruction_dtype, ctypes.byref(d),
+                                                ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    w.scales = storage[: n.value // 4]
+    return w
+
+
+def bitsandbytes_matmul(a, w: BnbWeight, out=None):
+    """onnxl_amd_bitsandbytes_matmul: MatMul(a, Transpose(Dequantize(w)))
+    with w prepared for a's dtype."""
+    if w.scales is None:
+        raise InvalidArgument("bitsandbytes_matmul: prepare_bitsandbytes the weight first")
+    if out is None:
+        out = _empty(tuple(a.shape[:-1]) + (w.rows,), a.dtype, _device_of(a))
+    code = UINT8 if w.fmt != "int8" else INT8
+    _check(lib().onnxl_amd_bitsandbytes_matmul(describe(a), BNB_FORMATS[w.fmt], w.rows, w.cols, w.block,
+                                               describe(w.weight, code), describe(w.scales), describe(out),
+                                               _stream_of(a, w.weight, out)))
     return out
 
 

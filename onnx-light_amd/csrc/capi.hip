@@ -2244,6 +2244,272 @@ int PrepareGptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl
   return PrepareCkpt("prepare_gptq", p, qweight, qzeros, scales, weight, scale, zero_point, stream);
 }
 
+// ---------------------------------------------------------------------------
+// bitsandbytes weights (onnx_core/runtime/bitsandbytes.cc): the geometry and
+// tensor checks of Geometry / CheckTensor (:222-258, :317-321) on the parsed
+// state, CheckParameters (:348-379), the reconstruction (:502-539) and the
+// prepared fused MatMul.
+
+struct BnbState {
+  int32_t format;
+  int64_t rows, cols, block, nested_block, count, blocks;
+  float offset;
+};
+
+// `bytes` of a descriptor's payload to host, ordered on `stream`.
+void ReadOnStream(hipStream_t stream, const onnxl_amd_tensor &t, void *dst, size_t bytes) {
+  if (bytes == 0) return;
+  if (t.location == ONNXL_AMD_HOST) {
+    std::memcpy(dst, t.data, bytes);
+    return;
+  }
+  OLA_HIP(hipMemcpyAsync(dst, t.data, bytes, hipMemcpyDeviceToHost, stream));
+  OLA_HIP(hipStreamSynchronize(stream));
+}
+
+void BnbTensor(const onnxl_amd_tensor *t, const char *name, int32_t dtype, int64_t elements, int64_t bytes) {
+  OLA_ENFORCE(!Absent(t) && t->data_type == dtype && NumElements(*t) == elements && t->size_bytes == bytes &&
+                  t->data != nullptr,
+              "bitsandbytes invalid tensor type, shape or byte extent: ", name, ".");
+  CheckDescriptor(t, name);
+}
+
+BnbState BnbGeometry(int32_t format, int64_t rows, int64_t cols, int64_t block, int64_t nested_block, float offset,
+                     const onnxl_amd_tensor *weight, const onnxl_amd_tensor *absmax,
+                     const onnxl_amd_tensor *quant_map, const onnxl_amd_tensor *nested_absmax,
+                     const onnxl_amd_tensor *nested_quant_map) {
+  BnbState g{format, rows, cols, block, nested_block, 0, 0, offset};
+  OLA_ENFORCE(rows > 0 && cols > 0 && rows <= (int64_t(1) << 40) / cols,
+              "bitsandbytes invalid dimensions or max_bytes.");
+  g.count = rows * cols;
+  if (format == 2) {
+    OLA_ENFORCE(block == 0 && nested_block == 0, "bitsandbytes invalid INT8 metadata.");
+    g.blocks = rows;
+    BnbTensor(weight, "weight", kInt8, g.count, g.count);
+    BnbTensor(absmax, "weight_scb", kFloat, rows, rows * 4);
+    return g;
+  }
+  const bool pow2 = block >= 32 && block <= 4096 && (block & (block - 1)) == 0;
+  OLA_ENFORCE((format == 0 || format == 1) && pow2 && (nested_block == 0 || nested_block == 256),
+              "bitsandbytes unsupported four-bit state.");
+  g.blocks = (g.count + block - 1) / block;
+  BnbTensor(weight, "weight", kUint8, (g.count + 1) / 2, (g.count + 1) / 2);
+  if (nested_block)
+    BnbTensor(absmax, "weight_absmax", kUint8, g.blocks, g.blocks);
+  else
+    BnbTensor(absmax, "weight_absmax", kFloat, g.blocks, g.blocks * 4);
+  BnbTensor(quant_map, "weight_quant_map", kFloat, 16, 64);
+  if (nested_block) {
+    const int64_t nb = (g.blocks + 255) / 256;
+    BnbTensor(nested_absmax, "weight_nested_absmax", kFloat, nb, nb * 4);
+    BnbTensor(nested_quant_map, "weight_nested_quant_map", kFloat, 256, 1024);
+    OLA_ENFORCE(std::isfinite(offset) && offset >= 0.f, "bitsandbytes invalid nested offset.");
+  }
+  return g;
+}
+
+// The format's 16 code values (nf4 as float, fp4 over 12), native index order.
+float BnbTableValue(int32_t format, int j) {
+  static const double nf4[16] = {-1, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+                                 -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0,
+                                 0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
+                                 0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+                                 0.7229568362236023, 1};
+  static const float fp4[16] = {0.f, 1.f / 192, 2.f / 3, 1.f,  1.f / 3,  0.5f,  1.f / 6,  0.25f,
+                                0.f, -1.f / 192, -2.f / 3, -1.f, -1.f / 3, -0.5f, -1.f / 6, -0.25f};
+  return format == 0 ? (float)nf4[j] : fp4[j];
+}
+
+// Device work of one bitsandbytes call: its staged inputs, the resolved
+// scales (in `scales`, or in the call's scratch) and the flag word.
+struct BnbRun {
+  BnbParams p{};
+  std::unique_ptr<Staging> st;
+  onnxl_amd_tensor flag_desc{};
+
+  BnbRun(hipStream_t stream, const BnbState &g, size_t extra, const onnxl_amd_tensor *weight,
+         const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *nested_absmax,
+         const onnxl_amd_tensor *nested_quant_map, onnxl_amd_tensor *y, float *scales) {
+    const size_t sc_bytes = scales ? 0 : Scratch::Round((size_t)g.blocks * 4);
+    st.reset(new Staging(stream, sc_bytes + 256 + extra, {weight, absmax, nested_absmax, nested_quant_map}, {y}));
+    char *x = static_cast<char *>(st->Extra());
+    p.scales = scales ? scales : reinterpret_cast<float *>(x);
+    p.flag = reinterpret_cast<unsigned *>(x + sc_bytes);
+    p.format = g.format;
+    p.rows = g.rows;
+    p.cols = g.cols;
+    p.block_shift = g.format == 2 ? 0 : __builtin_ctzll((unsigned long long)g.block);
+    p.nested = g.nested_block != 0;
+    p.offset = g.offset;
+    p.blocks = g.blocks;
+    p.codes = static_cast<const uint8_t *>(st->In(weight));
+    p.absmax = st->In(absmax);
+    p.nested_absmax = static_cast<const float *>(st->In(nested_absmax));
+    p.nested_map = static_cast<const float *>(st->In(nested_quant_map));
+    hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, p.flag, (size_t)1);
+    flag_desc.data_type = kInt32;
+    flag_desc.rank = 1;
+    flag_desc.dims[0] = 1;
+    flag_desc.data = p.flag;
+    flag_desc.size_bytes = 4;
+    flag_desc.location = ONNXL_AMD_DEVICE;
+  }
+  void *ExtraAfterFlag() const { return reinterpret_cast<char *>(p.flag) + 256; }
+  unsigned Flag(hipStream_t stream) {
+    unsigned v = 0;
+    ReadOnStream(stream, flag_desc, &v, 4);
+    return v;
+  }
+};
+
+// CheckParameters in the reference's order: the FLOAT maxima (absmax, or the
+// int8 row maxima) on the device, the quant map (finite, then canonical, entry
+// by entry), the nested tables, then every nested scale (the device flags).
+void BnbCheck(hipStream_t stream, const BnbState &g, BnbRun &run, const onnxl_amd_tensor *quant_map,
+              const onnxl_amd_tensor *nested_absmax, const onnxl_amd_tensor *nested_quant_map) {
+  LaunchBnbScales(run.p, stream);
+  const unsigned flag = run.Flag(stream);
+  constexpr const char *kBadTable = "bitsandbytes nonfinite table or invalid absmax.";
+  OLA_ENFORCE(!(flag & kBnbBadAbsmax), kBadTable);
+  if (g.format != 2) {
+    float qm[16];
+    ReadOnStream(stream, *quant_map, qm, 64);
+    for (int j = 0; j < 16; ++j) OLA_ENFORCE(std::isfinite(qm[j]), kBadTable);
+    if (g.nested_block) {
+      std::vector<float> na((size_t)NumElements(*nested_absmax)), nm(256);
+      ReadOnStream(stream, *nested_absmax, na.data(), na.size() * 4);
+      ReadOnStream(stream, *nested_quant_map, nm.data(), 1024);
+      for (float v : na) OLA_ENFORCE(std::isfinite(v) && v >= 0.f, kBadTable);
+      for (float v : nm) OLA_ENFORCE(std::isfinite(v), kBadTable);
+    }
+    for (int j = 0; j < 16; ++j)
+      OLA_ENFORCE(qm[j] == BnbTableValue(g.format, j), "bitsandbytes noncanonical NF4/FP4 table.");
+  }
+  OLA_ENFORCE(!(flag & kBnbBadScale), "bitsandbytes nonfinite reconstruction.");
+}
+
+int DequantizeBnb(int32_t format, int64_t rows, int64_t cols, int64_t block, int64_t nested_block, float offset,
+                  const onnxl_amd_tensor *weight, const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+                  const onnxl_amd_tensor *nested_absmax, const onnxl_amd_tensor *nested_quant_map,
+                  onnxl_amd_tensor *y, hipStream_t stream) {
+  const BnbState g =
+      BnbGeometry(format, rows, cols, block, nested_block, offset, weight, absmax, quant_map, nested_absmax,
+                  nested_quant_map);
+  OLA_ENFORCE(y && (y->data_type == kFloat || y->data_type == kFloat16 || y->data_type == kBfloat16),
+              "bitsandbytes unsupported reconstruction_dtype.");
+  CheckDescriptor(y, "y");
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == rows && y->dims[1] == cols &&
+                  y->size_bytes == g.count * (y->data_type == kFloat ? 4 : 2),
+              "bitsandbytes: y must be [rows, cols] of reconstruction_dtype.");
+  BnbRun run(stream, g, 0, weight, absmax, nested_absmax, nested_quant_map, y, nullptr);
+  BnbCheck(stream, g, run, quant_map, nested_absmax, nested_quant_map);
+  LaunchBnbDecode(run.p, y->data_type, run.st->Out(y), stream);
+  OLA_ENFORCE(!(run.Flag(stream) & kBnbBadValue), "bitsandbytes nonfinite reconstruction.");
+  run.st->Finish();
+  return ONNXL_AMD_OK;
+}
+
+int PrepareBnb(int32_t format, int64_t rows, int64_t cols, int64_t block, int64_t nested_block, float offset,
+               const onnxl_amd_tensor *weight, const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+               const onnxl_amd_tensor *nested_absmax, const onnxl_amd_tensor *nested_quant_map,
+               int32_t reconstruction_dtype, onnxl_amd_tensor *scales, hipStream_t stream) {
+  const BnbState g =
+      BnbGeometry(format, rows, cols, block, nested_block, offset, weight, absmax, quant_map, nested_absmax,
+                  nested_quant_map);
+  OLA_ENFORCE(reconstruction_dtype == kFloat || reconstruction_dtype == kFloat16 ||
+                  reconstruction_dtype == kBfloat16,
+              "bitsandbytes unsupported reconstruction_dtype.");
+  OLA_ENFORCE(scales && scales->location == ONNXL_AMD_DEVICE && scales->data != nullptr &&
+                  scales->size_bytes >= g.blocks * 4,
+              "prepare_bitsandbytes: scales must be a device buffer of ", g.blocks * 4, " bytes.");
+  BnbRun run(stream, g, 0, weight, absmax, nested_absmax, nested_quant_map, nullptr,
+             static_cast<float *>(scales->data));
+  BnbCheck(stream, g, run, quant_map, nested_absmax, nested_quant_map);
+  // every value of the weight reconstructed in the dtype, nothing written
+  BnbParams check = run.p;
+  LaunchBnbDecode(check, reconstruction_dtype, nullptr, stream);
+  OLA_ENFORCE(!(run.Flag(stream) & kBnbBadValue), "bitsandbytes nonfinite reconstruction.");
+  scales->data_type = kFloat;
+  scales->rank = 1;
+  scales->dims[0] = g.blocks;
+  run.st->Finish();
+  return ONNXL_AMD_OK;
+}
+
+int64_t BnbBlocks(int32_t format, int64_t rows, int64_t cols, int64_t block) {
+  if (format == 2) return rows;
+  return block > 0 ? (rows * cols + block - 1) / block : 0;
+}
+
+int BnbMatMul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t cols, int64_t block,
+              const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales, onnxl_amd_tensor *y,
+              hipStream_t stream) {
+  constexpr const char *kName = "bitsandbytes_matmul";
+  OLA_ENFORCE(!Absent(a) && y, kName, ": a and y are required.");
+  CheckDescriptor(a, "a");
+  CheckDescriptor(y, "y");
+  OLA_ENFORCE(a->data_type == kFloat16 || a->data_type == kBfloat16, kName, ": a must be FLOAT16 or BFLOAT16.");
+  OLA_ENFORCE(a->rank >= 1 && a->dims[a->rank - 1] == cols, kName, ": the last dimension of a must be cols.");
+  OLA_ENFORCE(format >= 0 && format <= 2 && rows > 0 && cols > 0 &&
+                  (format == 2 ? block == 0
+                               : block >= 32 && block <= 4096 && (block & (block - 1)) == 0),
+              kName, ": unsupported format or block.");
+  const int64_t count = rows * cols, blocks = BnbBlocks(format, rows, cols, block);
+  OLA_ENFORCE(!Absent(weight) && weight->size_bytes == (format == 2 ? count : (count + 1) / 2) &&
+                  (weight->data_type == (format == 2 ? kInt8 : kUint8)),
+              kName, ": weight does not match the format and shape.");
+  OLA_ENFORCE(!Absent(scales) && scales->data_type == kFloat && scales->size_bytes >= blocks * 4, kName,
+              ": scales must be the FLOAT scales onnxl_amd_prepare_bitsandbytes wrote.");
+  CheckDescriptor(weight, "weight");
+  CheckDescriptor(scales, "scales");
+  const int64_t M = NumElements(*a) / cols;
+  OLA_ENFORCE(y->data_type == a->data_type && y->rank == a->rank && y->dims[y->rank - 1] == rows &&
+                  NumElements(*y) == M * rows && y->size_bytes == M * rows * 2,
+              kName, ": y must be a's leading dims x rows, a's dtype.");
+  if (M == 0) return ONNXL_AMD_OK;
+  const bool fp16 = a->data_type == kFloat16;
+  auto aligned = [](const onnxl_amd_tensor *t) {
+    return t->location == ONNXL_AMD_HOST || reinterpret_cast<uintptr_t>(t->data) % 16 == 0;
+  };
+  const bool gemv = fp16 && (format == 0 || format == 1) && M <= 4 && cols % 32 == 0 && cols % block == 0 &&
+                    aligned(a) && aligned(weight) && count / 2 < (int64_t(1) << 40);
+  const size_t w_bytes = gemv ? 0 : (size_t)count * 2;
+  Staging st(stream, w_bytes + 256, {a, weight, scales}, {y});
+  const uint16_t *ad = static_cast<const uint16_t *>(st.In(a));
+  const uint8_t *codes = static_cast<const uint8_t *>(st.In(weight));
+  const float *sc = static_cast<const float *>(st.In(scales));
+  uint16_t *yd = static_cast<uint16_t *>(st.Out(y));
+  if (gemv) {
+    LaunchBnbGemv(format, ad, codes, sc, M, rows, cols, block, yd, stream);
+  } else {
+    // the weight decoded to [rows, cols] in a's dtype, then Y = A W^T
+    BnbParams p{};
+    p.format = format;
+    p.rows = rows;
+    p.cols = cols;
+    p.block_shift = format == 2 ? 0 : __builtin_ctzll((unsigned long long)block);
+    p.blocks = blocks;
+    p.codes = codes;
+    p.scales = const_cast<float *>(sc);
+    char *x = static_cast<char *>(st.Extra());
+    p.flag = reinterpret_cast<unsigned *>(x + w_bytes);  // values were checked by the preparation
+    uint16_t *w = reinterpret_cast<uint16_t *>(x);
+    LaunchBnbDecode(p, a->data_type, w, stream);
+    HMatMulParams h{};
+    h.A = ad;
+    h.B = w;
+    h.Y = yd;
+    h.M = M;
+    h.N = rows;
+    h.K = cols;
+    h.batch = 1;
+    h.bf16 = fp16 ? 0 : 1;
+    LaunchHMatMulBT(h, stream);
+  }
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
 // Validation runs before any device work, so argument errors are reported
 // even before onnxl_amd_init (the first device access then raises
 // NotInitialized).
@@ -2611,6 +2877,47 @@ int onnxl_amd_prepare_weight(const onnxl_amd_tensor *x, onnxl_amd_tensor *prepar
     prepared->layout = ONNXL_AMD_LAYOUT_TILED_INT4;
     st.Finish();
     return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_dequantize_bitsandbytes(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                      int64_t nested_block_size, float nested_offset, const onnxl_amd_tensor *weight,
+                                      const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+                                      const onnxl_amd_tensor *nested_absmax,
+                                      const onnxl_amd_tensor *nested_quant_map, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeBnb(format, rows, cols, block_size, nested_block_size, nested_offset, weight, absmax,
+                         quant_map, nested_absmax, nested_quant_map, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_bitsandbytes_size(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                        int64_t *scale_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(scale_bytes, "prepare_bitsandbytes_size: null output");
+    OLA_ENFORCE(rows > 0 && cols > 0 && (format == 2 || (format >= 0 && format <= 1 && block_size > 0)),
+                "prepare_bitsandbytes_size: invalid format or dimensions");
+    *scale_bytes = BnbBlocks(format, rows, cols, block_size) * 4;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_bitsandbytes(int32_t format, int64_t rows, int64_t cols, int64_t block_size,
+                                   int64_t nested_block_size, float nested_offset, const onnxl_amd_tensor *weight,
+                                   const onnxl_amd_tensor *absmax, const onnxl_amd_tensor *quant_map,
+                                   const onnxl_amd_tensor *nested_absmax, const onnxl_amd_tensor *nested_quant_map,
+                                   int32_t reconstruction_dtype, onnxl_amd_tensor *scales, void *stream) {
+  return Guard([&] {
+    return PrepareBnb(format, rows, cols, block_size, nested_block_size, nested_offset, weight, absmax, quant_map,
+                      nested_absmax, nested_quant_map, reconstruction_dtype, scales, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t cols,
+                                  int64_t block_size, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales,
+                                  onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return BnbMatMul(a, format, rows, cols, block_size, weight, scales, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -172,6 +172,38 @@ void LaunchGemvQ80(const uint16_t *a, const uint8_t *w, int64_t M, int64_t N, in
                    hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// bitsandbytes weights (bnb.hip), logical [rows, cols] row-major: format 0
+// nf4 / 1 fp4 (4-bit codes, the even element in the high nibble, one scale
+// per 2^block_shift elements) or 2 int8 (signed bytes, one scale per row).
+// Flag bits the kernels OR into *flag:
+constexpr unsigned kBnbBadAbsmax = 1;  // a FLOAT absmax not finite or negative
+constexpr unsigned kBnbBadScale = 2;   // a resolved scale not finite
+constexpr unsigned kBnbBadValue = 4;   // a value not finite in fp32 or in the output dtype
+struct BnbParams {
+  int format;
+  int64_t rows, cols;
+  int block_shift;
+  int nested;                // absmax holds UINT8 codes of the nested statistics
+  float offset;              // nested_offset
+  int64_t blocks;            // scales: ceil(rows * cols / block), or rows for int8
+  const uint8_t *codes;
+  const void *absmax;        // FLOAT [blocks] (int8: the row maxima), or UINT8 [blocks] when nested
+  const float *nested_absmax;  // [ceil(blocks / 256)]
+  const float *nested_map;     // [256]
+  float *scales;             // [blocks]: written by LaunchBnbScales (unless null), read by the others
+  unsigned *flag;
+};
+void LaunchBnbScales(const BnbParams &p, hipStream_t s);
+// out_dtype kFloat, kFloat16, kBfloat16, or 0: the finiteness check alone
+void LaunchBnbDecode(const BnbParams &p, int out_dtype, void *y, hipStream_t s);
+// y[M, N] FLOAT16 = a[M, K] x W^T, W the FLOAT16 decode of nf4 / fp4 codes
+// [N, K] with resolved scales: M <= 4, K % 32 == 0, K % block == 0,
+// 16-byte aligned a and codes.
+bool BnbGemvEligible(int format, int64_t M, int64_t N, int64_t K, int64_t block, const void *a, const void *codes);
+void LaunchBnbGemv(int format, const uint16_t *a, const uint8_t *codes, const float *scales, int64_t M, int64_t N,
+                   int64_t K, int64_t block, uint16_t *y, hipStream_t s);
+
+// ---------------------------------------------------------------------------
 // ConvInteger / QLinearConv.  Spatial dims are right-aligned into 3 slots
 // (missing leading dims have size 1, kernel 1, stride 1, dilation 1, pad 0).
 struct ConvGeom {

@@ -1661,3 +1661,119 @@ int orc_gptq_decode(int format, int bits, int width, const void *qweight, const 
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* bitsandbytes weights (onnx_core/runtime/bitsandbytes.cc), the encoding
+ * "onnx_light.bitsandbytes_weights.v1" of ai.rt:Dequantize.  A weight of
+ * logical shape [rows, cols], flattened row-major.  format 0 nf4 / 1 fp4:
+ * element i is the 4-bit code (codes[i / 2] >> (i % 2 ? 0 : 4)) & 15 (the
+ * even element in the high nibble, :495-496), its value the format's table
+ * entry (Codebook, :323-337: nf4 from quantization.cc:126-141 as float, fp4
+ * bitsandbytes' fp4 table over 12), one scale per `block` consecutive
+ * elements: absmax[b] (FLOAT), or with nested blocks of 256 the UINT8 code
+ * absmax[b] resolved as fp32(fp32(nested_map[code] * nested_absmax[b / 256])
+ * + offset) (Scale, :339-346).  format 2 int8: element (r, c) is the signed
+ * byte codes[r * cols + c], its row's scale fp32(absmax[r] / 127)
+ * (:519).  value = fp32(code value * scale) (:523-526).
+ *
+ * orc_bnb_check: CheckParameters (:348-379) on the side tensors: every FLOAT
+ * table finite, the maxima (absmax when FLOAT, nested_absmax) >= 0, the
+ * quant map equal to the format's table, every nested scale finite.
+ * Returns 0, 3 for "bitsandbytes nonfinite table or invalid absmax.", 4 for
+ * "bitsandbytes noncanonical NF4/FP4 table.", 2 for a nonfinite nested scale
+ * ("bitsandbytes nonfinite reconstruction.").
+ * orc_bnb_reconstruct: ReconstructBitsAndBytesWeights (:502-539) into FLOAT
+ * (1), FLOAT16 (10) or BFLOAT16 (16) values; returns 0, or 2 when a scale or
+ * value is not finite, or its FLOAT16 / BFLOAT16 rounding is (:527-533). */
+static const double bnb_nf4[16] = {-1, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+                                   -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0,
+                                   0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
+                                   0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+                                   0.7229568362236023, 1};
+static const float bnb_fp4[16] = {0.f, 1.f / 192, 2.f / 3, 1.f,  1.f / 3,  0.5f,  1.f / 6,  0.25f,
+                                  0.f, -1.f / 192, -2.f / 3, -1.f, -1.f / 3, -0.5f, -1.f / 6, -0.25f};
+
+float orc_bnb_table(int format, int code) {
+  return format == 0 ? (float)bnb_nf4[code & 15] : bnb_fp4[code & 15];
+}
+
+static int bnb_scale(int format, int nested, float offset, const void *absmax, const float *nested_absmax,
+                     const float *nested_map, int64_t b, float *scale) {
+  float maximum;
+  if (format == 2 || !nested) {
+    maximum = ((const float *)absmax)[b];
+  } else {
+    volatile float product = nested_map[((const uint8_t *)absmax)[b]] * nested_absmax[b / 256];
+    if (!isfinite(product)) return 2;
+    volatile float sum = product + offset;
+    if (!isfinite(sum)) return 2;
+    maximum = sum;
+  }
+  if (format == 2) {
+    volatile float q = maximum / 127.f;
+    if (!isfinite(q)) return 2;
+    maximum = q;
+  }
+  *scale = maximum;
+  return 0;
+}
+
+int orc_bnb_check(int format, int64_t rows, int64_t cols, int64_t block, int nested, float offset,
+                  const void *absmax, const float *quant_map, const float *nested_absmax, const float *nested_map) {
+  const int64_t count = rows * cols;
+  const int64_t blocks = format == 2 ? rows : (count + block - 1) / block;
+  if (format == 2 || !nested) {
+    for (int64_t b = 0; b < blocks; ++b) {
+      const float v = ((const float *)absmax)[b];
+      if (!isfinite(v) || v < 0) return 3;
+    }
+  }
+  if (format == 2) return 0;
+  for (int j = 0; j < 16; ++j)
+    if (!isfinite(quant_map[j])) return 3;
+  if (nested) {
+    for (int64_t j = 0; j < (blocks + 255) / 256; ++j)
+      if (!isfinite(nested_absmax[j]) || nested_absmax[j] < 0) return 3;
+    for (int j = 0; j < 256; ++j)
+      if (!isfinite(nested_map[j])) return 3;
+  }
+  for (int j = 0; j < 16; ++j)
+    if (quant_map[j] != orc_bnb_table(format, j)) return 4;
+  if (nested)
+    for (int64_t b = 0; b < blocks; ++b) {
+      float s;
+      if (bnb_scale(format, nested, offset, absmax, nested_absmax, nested_map, b, &s)) return 2;
+    }
+  return 0;
+}
+
+int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, int nested, float offset,
+                        const uint8_t *codes, const void *absmax, const float *nested_absmax,
+                        const float *nested_map, int out_dtype, void *out) {
+  const int64_t count = rows * cols;
+  const int64_t bs = format == 2 ? cols : block;
+  const int64_t blocks = (count + bs - 1) / bs;
+  for (int64_t b = 0; b < blocks; ++b) {
+    float scale;
+    if (bnb_scale(format, nested, offset, absmax, nested_absmax, nested_map, b, &scale)) return 2;
+    const int64_t end = count < b * bs + bs ? count : b * bs + bs;
+    for (int64_t i = b * bs; i < end; ++i) {
+      const float code = format == 2 ? (float)(int8_t)codes[i]
+                                     : orc_bnb_table(format, (codes[i / 2] >> (i % 2 ? 0 : 4)) & 15);
+      volatile float v = code * scale;
+      if (!isfinite(v)) return 2;
+      if (out_dtype == 1) {
+        ((float *)out)[i] = v;
+      } else if (out_dtype == 10) {
+        const uint16_t h = orc_f32_to_f16(v);
+        if ((h & 0x7c00u) == 0x7c00u) return 2;
+        ((uint16_t *)out)[i] = h;
+      } else {
+        const uint16_t h = orc_f32_to_bf16(v);
+        if ((h & 0x7f80u) == 0x7f80u) return 2;
+        ((uint16_t *)out)[i] = h;
+      }
+    }
+  }
+  return 0;
+}

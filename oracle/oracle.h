@@ -216,6 +216,14 @@ int orc_gptq_decode(int format, int bits, int width, const void *qweight, const 
                     const int32_t *g_idx, int64_t K, int64_t N, int64_t group, uint8_t *codes, int16_t *zeros,
                     float *out);
 
+/* bitsandbytes weights (nf4 / fp4 / int8): table entry, side-tensor checks, reconstruction */
+float orc_bnb_table(int format, int code);
+int orc_bnb_check(int format, int64_t rows, int64_t cols, int64_t block, int nested, float offset,
+                  const void *absmax, const float *quant_map, const float *nested_absmax, const float *nested_map);
+int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, int nested, float offset,
+                        const uint8_t *codes, const void *absmax, const float *nested_absmax,
+                        const float *nested_map, int out_dtype, void *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,6 +121,14 @@ def _declare(L):
     L.orc_gptq_decode.restype = ctypes.c_int
     L.orc_gptq_decode.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int64,
                                   ctypes.c_int64, ctypes.c_int64, P, P, P]
+    L.orc_bnb_table.restype = ctypes.c_float
+    L.orc_bnb_table.argtypes = [ctypes.c_int, ctypes.c_int]
+    L.orc_bnb_check.restype = ctypes.c_int
+    L.orc_bnb_check.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                ctypes.c_float, P, P, P, P]
+    L.orc_bnb_reconstruct.restype = ctypes.c_int
+    L.orc_bnb_reconstruct.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                      ctypes.c_float, P, P, P, P, ctypes.c_int, P]
     L.orc_grouped_matmul.restype = ctypes.c_int
     L.orc_grouped_matmul.argtypes = [ctypes.c_int, P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int, P, ctypes.c_int64, P, P]
@@ -593,3 +601,42 @@ def pack_bits(codes, bits: int) -> np.ndarray:
         out[bit // 8] |= v & 0xFF
         out[bit // 8 + 1] |= (v >> 8) & 0xFF
     return out[:(n * bits + 7) // 8].copy()
+
+
+# ---- bitsandbytes weights (nf4 / fp4 / int8) ---------------------------------
+
+BNB_FORMATS = {"nf4": 0, "fp4": 1, "int8": 2}
+BNB_ERRORS = {2: "bitsandbytes nonfinite reconstruction.", 3: "bitsandbytes nonfinite table or invalid absmax.",
+              4: "bitsandbytes noncanonical NF4/FP4 table."}
+
+
+def bnb_table(fmt: str) -> np.ndarray:
+    """The format's 16 code values (nf4 / fp4) as float32."""
+    return np.array([lib().orc_bnb_table(BNB_FORMATS[fmt], j) for j in range(16)], np.float32)
+
+
+def _f32(x):
+    return np.zeros(1, np.float32) if x is None else np.ascontiguousarray(x, dtype=np.float32)
+
+
+def bnb_check(fmt: str, rows: int, cols: int, block: int, absmax, quant_map=None, nested_absmax=None,
+              nested_map=None, offset: float = 0.0) -> int:
+    """The side-tensor checks: 0, or the key of BNB_ERRORS.  absmax float32
+    (or uint8 codes with nested_absmax / nested_map)."""
+    nested = nested_absmax is not None
+    am = np.ascontiguousarray(absmax)
+    return lib().orc_bnb_check(BNB_FORMATS[fmt], rows, cols, block, int(nested), offset, _ptr(am), _ptr(_f32(quant_map)),
+                               _ptr(_f32(nested_absmax)), _ptr(_f32(nested_map)))
+
+
+def bnb_reconstruct(fmt: str, rows: int, cols: int, block: int, codes, absmax, nested_absmax=None, nested_map=None,
+                    offset: float = 0.0, out_dtype: int = FLOAT):
+    """(rc, values [rows, cols]): float32 for FLOAT, uint16 bits for FLOAT16 /
+    BFLOAT16; rc 2 is the reference's nonfinite-reconstruction error."""
+    nested = nested_absmax is not None
+    cd = np.ascontiguousarray(codes).view(np.uint8)
+    am = np.ascontiguousarray(absmax)
+    out = np.zeros((rows, cols), np.float32 if out_dtype == FLOAT else np.uint16)
+    rc = lib().orc_bnb_reconstruct(BNB_FORMATS[fmt], rows, cols, block, int(nested), offset, _ptr(cd), _ptr(am),
+                                   _ptr(_f32(nested_absmax)), _ptr(_f32(nested_map)), out_dtype, _ptr(out))
+    return rc, out
