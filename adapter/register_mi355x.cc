@@ -14,7 +14,7 @@
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
-//    ai.rt:Dequantize on AWQ / GPTQ encoded weights), and for the fused
+//    ai.rt:Dequantize on AWQ / GPTQ / bitsandbytes encoded weights), and for the fused
 //    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
 //    an encoded weight, ai.rt.amd:DequantizeLinearGroupedMatMul on quantized
@@ -49,6 +49,8 @@
 
 #include "onnxl_amd.h"
 
+#include <cctype>
+#include <charconv>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -57,6 +59,8 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <system_error>
+#include <unordered_map>
 #include <unordered_set>
 #include <utility>
 #include <vector>
@@ -727,11 +731,68 @@ bool ExportCheckpoint(const rt::RuntimeValue &value, const Catalogue &catalogue,
   return false;
 }
 
+// bitsandbytes weights carried as encoded values (struct type
+// "onnx_light.bitsandbytes_weights.v1").  The native tensors come from the
+// reference's exporter (ExportBitsAndBytesWeights, quantization.h:811), which
+// validates the encoding, its schema and the JSON quant state; the state's
+// numbers are the schema's constant fields (format, out_features,
+// in_features, block_size, nested_block_size: bitsandbytes.cc:275-289) and
+// the nested offset is read from the JSON the exporter has checked.
+struct BnbCheckpoint {
+  int32_t format = 0;
+  int64_t rows = 0, cols = 0, block = 0, nested = 0;
+  float offset = 0.f;
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  onnxl_amd_tensor T(const char *name) const {
+    auto it = tensors.find(name);
+    return it == tensors.end() ? Absent() : Describe(&it->second);
+  }
+  onnxl_amd_tensor Absmax() const { return T(format == 2 ? "weight_scb" : "weight_absmax"); }
+};
+
+// The number after "nested_offset": in a checked JSON state.
+float NestedOffset(const rt::Tensor &json) {
+  const std::string text(reinterpret_cast<const char *>(json.bytes()), json.size_bytes());
+  size_t at = text.find("\"nested_offset\"");
+  if (at == std::string::npos) throw std::invalid_argument("mi355x: bitsandbytes state without nested_offset");
+  at = text.find(':', at) + 1;
+  while (at < text.size() && std::isspace(static_cast<unsigned char>(text[at]))) ++at;
+  size_t end = at;
+  while (end < text.size() && text[end] != ',' && text[end] != '}' &&
+         !std::isspace(static_cast<unsigned char>(text[end])))
+    ++end;
+  double value = 0;
+  const auto parsed = std::from_chars(text.data() + at, text.data() + end, value);
+  if (parsed.ec != std::errc{}) throw std::invalid_argument("mi355x: bitsandbytes invalid nested offset");
+  return static_cast<float>(value);
+}
+
+// False when the encoded value is not a bitsandbytes weight.
+template <typename Catalogue>
+bool ExportBitsAndBytes(const rt::RuntimeValue &value, const Catalogue &catalogue, BnbCheckpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  const auto &type = catalogue.Resolve(enc.struct_type());
+  if (type.name().value() != "onnx_light.bitsandbytes_weights.v1") return false;
+  rt::BitsAndBytesWeights w = rt::ExportBitsAndBytesWeights(enc, size_t{1} << 30, catalogue);
+  auto number = [&](int i) { return type.structure().field(i).constant().int64_data(0); };
+  out.format = static_cast<int32_t>(number(0));
+  out.rows = number(1);
+  out.cols = number(2);
+  out.block = number(3);
+  out.nested = number(4);
+  out.tensors = std::move(w.tensors);
+  if (out.nested) out.offset = NestedOffset(out.tensors.at("weight_quant_state"));
+  return true;
+}
+
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
-// kernel_dequantize.cc:18-43): AWQ and GPTQ encodings decode on the GPU to
-// [out_features, in_features] of dtype (onnxl_amd_dequantize_awq / _gptq);
-// every other encoding, and values that reference shared parameters, run on
-// the built-in kernel.
+// kernel_dequantize.cc:18-43): AWQ, GPTQ and bitsandbytes encodings decode
+// on the GPU to [out_features, in_features] of dtype
+// (onnxl_amd_dequantize_awq / _gptq / _bitsandbytes); every other encoding,
+// and values that reference shared parameters, run on the built-in kernel.
 class Mi355xDequantize : public Mi355xKernel {
 public:
   static constexpr const char *name = "onnxl_amd:CPU:ai.rt:Dequantize";
@@ -744,9 +805,23 @@ public:
     if (dtype != kFloat && dtype != kDouble && dtype != kFloat16 && dtype != kBfloat16)
       throw std::invalid_argument("Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
     const auto value = ctx.values().find(node.input(0));
+    BnbCheckpoint b;
+    if (value != ctx.values().end() && ExportBitsAndBytes(value->second, ctx.struct_type_catalogue(), b)) {
+      const rt::Shape shape{b.rows, b.cols};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      const onnxl_amd_tensor w = b.T("weight"), am = b.Absmax(), qm = b.T("weight_quant_map");
+      const onnxl_amd_tensor na = b.T("weight_nested_absmax"), nm = b.T("weight_nested_quant_map");
+      if (Call(onnxl_amd_dequantize_bitsandbytes(b.format, b.rows, b.cols, b.block, b.nested, b.offset, &w, &am, &qm,
+                                                 &na, &nm, &dy, nullptr),
+               ctx))
+        rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / bitsandbytes");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1008,6 +1083,18 @@ public:
     rt::RequireOutputCount(node, 1);
     const onnxl_amd_tensor a = In(0, ctx);
     std::shared_ptr<Prepared> w = weight_ ? weight_ : PrepareWeight(ctx);
+    if (w->bnb) {  // the bitsandbytes codes and resolved scales in HBM, one fused call
+      rt::Shape shape(a.dims, a.dims + a.rank);
+      if (shape.empty() || shape.back() != w->cols)
+        throw std::invalid_argument("mi355x: DequantizeEncodedMatMul: A's last dimension must be in_features.");
+      shape.back() = w->rows;
+      rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      Check(onnxl_amd_bitsandbytes_matmul(&a, w->format, w->rows, w->cols, w->block, &w->weight.desc,
+                                          &w->scale.desc, &dy, nullptr));
+      rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     if (!w->fused) {  // the decoded weight [K, N] in HBM, MatMul on the GPU
       const rt::Shape shape = MatMulShape(a, w->dense_t.desc);
       rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
@@ -1028,14 +1115,52 @@ public:
 private:
   struct Prepared {
     bool fused = false;
-    DeviceTensor weight, scale, zero_point;  // fused operands
+    DeviceTensor weight, scale, zero_point;  // fused operands (bitsandbytes: codes and resolved scales)
     DeviceTensor dense_t;                    // the decoded weight, transposed to [K, N]
+    bool bnb = false;
+    int32_t format = 0;
+    int64_t rows = 0, cols = 0, block = 0;
   };
+
+  // A bitsandbytes weight: its codes uploaded once, the reference's checks
+  // and the nonfinite-reconstruction check in A's dtype once, the block scales
+  // resolved once (onnxl_amd_prepare_bitsandbytes).
+  std::shared_ptr<Prepared> PrepareBitsAndBytes(rt::RuntimeContext &ctx, const BnbCheckpoint &b) const {
+    const onnxl_amd_tensor a = In(0, ctx);
+    auto w = std::make_shared<Prepared>();
+    w->bnb = true;
+    w->format = b.format;
+    w->rows = b.rows;
+    w->cols = b.cols;
+    w->block = b.block;
+    const onnxl_amd_tensor codes = b.T("weight"), am = b.Absmax(), qm = b.T("weight_quant_map");
+    const onnxl_amd_tensor na = b.T("weight_nested_absmax"), nm = b.T("weight_nested_quant_map");
+    w->weight.Allocate(codes.size_bytes);
+    if (codes.size_bytes > 0)
+      CheckHip(hipMemcpy(w->weight.ptr, codes.data, static_cast<size_t>(codes.size_bytes), hipMemcpyHostToDevice),
+               "hipMemcpy");
+    w->weight.desc = codes;
+    w->weight.desc.data = w->weight.ptr;
+    w->weight.desc.location = ONNXL_AMD_DEVICE;
+    int64_t sb = 0;
+    Check(onnxl_amd_prepare_bitsandbytes_size(b.format, b.rows, b.cols, b.block, &sb));
+    w->scale.Allocate(sb);
+    w->scale.desc = onnxl_amd_tensor{};
+    w->scale.desc.data = w->scale.ptr;
+    w->scale.desc.location = ONNXL_AMD_DEVICE;
+    w->scale.desc.size_bytes = sb;
+    Check(onnxl_amd_prepare_bitsandbytes(b.format, b.rows, b.cols, b.block, b.nested, b.offset, &w->weight.desc, &am,
+                                         &qm, &na, &nm, a.data_type, &w->scale.desc, nullptr));
+    Check(onnxl_amd_synchronize(nullptr));
+    return w;
+  }
 
   std::shared_ptr<Prepared> PrepareWeight(rt::RuntimeContext &ctx) const {
     const auto value = ctx.values().find(node_->input(1));
     if (value == ctx.values().end() || value->second.kind != rt::RuntimeValue::Kind::kEncoded)
       throw std::invalid_argument("Dequantize requires an EncodedValueProto input.");
+    BnbCheckpoint b;
+    if (ExportBitsAndBytes(value->second, ctx.struct_type_catalogue(), b)) return PrepareBitsAndBytes(ctx, b);
     Checkpoint c;
     if (!ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) return DenseOther(ctx, value->second);
     const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
