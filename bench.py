@@ -18,7 +18,7 @@ runs it) on a bounded row sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c3_onnx_layout|c3_stream_ceiling|
                    c4|c5|q8|dql|qconv|pk|pkgemv|pkgemv8|pkgemv_q2k|pkgemv_q3k|pkgemv_q4k|pkgemv_q5k|
-                   pkgemv_q6k|pkgemv_iq4xs|awq|moe|moe_fp8]
+                   pkgemv_q6k|pkgemv_iq4xs|awq|bnb|moe|moe_fp8]
                   [--no-extra] [--no-cpu-baseline]
 
 The other configurations (3, 4, 5) and the quantizers in front of the
@@ -27,7 +27,8 @@ configuration 2's fp32 activation), a QLinearConv layer (`qconv`), a
 GGUF q4_0 weight decode (`pk`), the fused q4_0 / q8_0 / q2_k / q3_k / q4_k /
 q5_k / q6_k / iq4_xs GEMVs (`pkgemv`, `pkgemv8`, `pkgemv_q2k`, `pkgemv_q3k`,
 `pkgemv_q4k`, `pkgemv_q5k`, `pkgemv_q6k`, `pkgemv_iq4xs`), an AWQ gemm 4-bit
-checkpoint prepared for the fused decode GEMV (`awq`) and a Mixtral-shaped
+checkpoint prepared for the fused decode GEMV (`awq`), a bitsandbytes nf4
+weight prepared for its fused GEMV (`bnb`) and a Mixtral-shaped
 MoE GroupedMatMul (`moe`), the same with fp8 experts fused through
 DequantizeLinear -> Cast (`moe_fp8`) are timed too and
 reported under `extra` unless --no-extra is given.  `c3_stream_ceiling` is a plain streaming read of configuration 3's
@@ -290,6 +291,39 @@ def make_pkgemv(olamd, dev, replicas, fmt="q4_0"):
                                       [olamd.describe(a), olamd.describe(x), f"gguf:{fmt}".encode(), dims, 2,
                                        olamd.describe(y)],
                                       (a, x, y, dims), olamd._stream_of(x)))
+    return w
+
+
+def make_bnb(olamd, dev, replicas):
+    """bitsandbytes nf4 (block 64, nested statistics) weight of configuration
+    3's shape [11008, 4096], prepared once (checks, resolved block scales),
+    then the fused GEMV fp16[1,4096] x W^T -> fp16[1,11008] per call: the
+    codes and the scales dominate.  Random codes are valid nf4 codes."""
+    import torch
+    w = Workload()
+    rows, cols, block = 11008, 4096, 64
+    w.name = ("bitsandbytes nf4 (block 64, nested statistics) fp16[1,4096] x W[11008,4096]^T -> fp16[1,11008], "
+              "weight prepared once (resolved block scales)")
+    w.key, w.unit, w.dtype, w.bound = "bnb", "GB/s", "fp16 x nf4 (fp32 accumulate)", "hbm"
+    blocks = rows * cols // block
+    w.nbytes = rows * cols // 2 + blocks * 4 + cols * 2 + rows * 2
+    w.work = float(w.nbytes)
+    rng = np.random.default_rng(47)
+    table = olamd.BNB_NF4_TABLE
+    a = _t(np.float16(rng.standard_normal((1, cols))), dev)
+    w.calls = []
+    for _ in range(replicas):
+        codes = _t(rng.integers(0, 256, rows * cols // 2).astype(np.uint8), dev)
+        absmax = _t(rng.integers(0, 256, blocks).astype(np.uint8), dev)
+        nested = _t(np.float32(rng.uniform(0.01, 0.1, -(-blocks // 256))), dev)
+        nmap = _t(np.sort(np.float32(rng.uniform(-1, 1, 256))), dev)
+        bw = olamd.prepare_bitsandbytes(olamd.BnbWeight("nf4", rows, cols, codes, absmax, _t(table, dev), block,
+                                                        nested, nmap, 256, 0.05), olamd.FLOAT16)
+        y = torch.empty((1, rows), dtype=torch.float16, device=dev)
+        w.calls.append(olamd.Prepared("onnxl_amd_bitsandbytes_matmul",
+                                      [olamd.describe(a), 0, rows, cols, block, olamd.describe(codes, olamd.UINT8),
+                                       olamd.describe(bw.scales), olamd.describe(y)],
+                                      (a, codes, bw.scales, y), olamd._stream_of(codes)))
     return w
 
 
@@ -722,7 +756,7 @@ def value_of(w, ms):
 
 
 WORKLOADS = ("c2", "c3", "c3_onnx_layout", "c3_stream_ceiling", "c4", "c5", "q8", "dql", "qconv", "pk", "pkgemv",
-             "pkgemv8", "pkgemv_q2k", "pkgemv_q3k", "pkgemv_q4k", "pkgemv_q5k", "pkgemv_q6k", "pkgemv_iq4xs", "awq",
+             "pkgemv8", "pkgemv_q2k", "pkgemv_q3k", "pkgemv_q4k", "pkgemv_q5k", "pkgemv_q6k", "pkgemv_iq4xs", "awq", "bnb",
              "moe", "moe_fp8")
 CPU_BASELINES = {"c3": cpu_baseline_c3, "c3_onnx_layout": cpu_baseline_c3, "c4": cpu_baseline_c4,
                  "c5": cpu_baseline_c5, "moe": cpu_baseline_moe}
@@ -785,6 +819,8 @@ def main():
             return make_pkgemv(olamd, dev, args.replicas or replicas_for(14336 * 4096 // 256 * PK_BLOCK[fmt][1]), fmt)
         if key == "awq":
             return make_awq(olamd, dev, args.replicas or 24)
+        if key == "bnb":
+            return make_bnb(olamd, dev, args.replicas or 24)
         if key == "moe":
             return make_moe(olamd, dev)
         if key == "moe_fp8":

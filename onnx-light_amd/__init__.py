@@ -357,6 +357,11 @@ def dequantize_awq(variant: str, qweight, qzeros, scales, K: int, N: int, group_
 
 
 BNB_FORMATS = {"nf4": 0, "fp4": 1, "int8": 2}
+# bitsandbytes' nf4 table (the canonical weight_quant_map), float32
+BNB_NF4_TABLE = np.array([-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+                          -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+                          0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+                          0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0], np.float32)
 
 
 class BnbWeight:

@@ -190,13 +190,16 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2_t AsH2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 
 // The 16 FLOAT16 weights of a block with scale s as byte planes: lo[d] holds
-// the low bytes of entries 4d .. 4d+3, hi[d] their high bytes.
+// the low bytes of entries 4d .. 4d+3, hi[d] their high bytes.  The prepared
+// weight's values are finite in FLOAT16, so the hardware conversion (round
+// to nearest even, v_cvt_pk_f16_f32 on pairs) needs no NaN handling.
 template <int FMT> __device__ __forceinline__ void BuildPlanes(float s, uint32_t lo[4], uint32_t hi[4]) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
   uint32_t pr[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t h0 = F32ToF16(BnbCode<FMT>(2 * i) * s), h1 = F32ToF16(BnbCode<FMT>(2 * i + 1) * s);
-    pr[i] = h0 | h1 << 16;
+    const f2_t v = {BnbCode<FMT>(2 * i) * s, BnbCode<FMT>(2 * i + 1) * s};
+    pr[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2_t));
   }
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
@@ -205,12 +208,18 @@ template <int FMT> __device__ __forceinline__ void BuildPlanes(float s, uint32_t
   }
 }
 
-// Four codes (one per byte, 0..15) -> the low and high bytes of their weights.
-__device__ __forceinline__ void Lookup4(uint32_t x, const uint32_t lo[4], const uint32_t hi[4], uint32_t &l,
-                                        uint32_t &h) {
-  const uint32_t sel = x & 0x07070707u;
-  // byte j of the final pick: byte j of the entries 0-7 lookup, or of the 8-15 one (selector j + 4)
-  const uint32_t pick = 0x03020100u + (((x >> 3) & 0x01010101u) << 2);
+// (x & mask) | bits in one v_and_or_b32 (the compiler splits it otherwise)
+__device__ __forceinline__ uint32_t AndOr(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(bits));
+  return r;
+}
+
+// Four codes -> the low and high bytes of their weights.  sel: each code's
+// bits 0-2 (one per byte); pick: byte j is j, plus 4 when the code's bit 3
+// is set (the entries 8-15 lookup).
+__device__ __forceinline__ void Lookup4(uint32_t sel, uint32_t pick, const uint32_t lo[4], const uint32_t hi[4],
+                                        uint32_t &l, uint32_t &h) {
   const uint32_t la = __builtin_amdgcn_perm(lo[1], lo[0], sel), lb = __builtin_amdgcn_perm(lo[3], lo[2], sel);
   const uint32_t ha = __builtin_amdgcn_perm(hi[1], hi[0], sel), hb = __builtin_amdgcn_perm(hi[3], hi[2], sel);
   l = __builtin_amdgcn_perm(lb, la, pick);
@@ -274,8 +283,9 @@ __global__ __launch_bounds__(256) void BnbGemvKernel(const uint16_t *__restrict_
         for (int q = 0; q < 4; ++q) {  // 8 values: byte j holds element 2j (high nibble) and 2j + 1 (low)
           const uint32_t w = cw[r][q];
           uint32_t el, eh, ol, oh;
-          Lookup4((w >> 4) & 0x0f0f0f0fu, lo, hi, el, eh);
-          Lookup4(w & 0x0f0f0f0fu, lo, hi, ol, oh);
+          // high nibbles: bits 4-6 and 7 of each byte; low nibbles: bits 0-2 and 3
+          Lookup4((w >> 4) & 0x07070707u, AndOr(w >> 5, 0x04040404u, 0x03020100u), lo, hi, el, eh);
+          Lookup4(w & 0x07070707u, AndOr(w >> 1, 0x04040404u, 0x03020100u), lo, hi, ol, oh);
           const uint32_t e01 = __builtin_amdgcn_perm(eh, el, 0x05010400u);  // (w[0], w[2])
           const uint32_t e23 = __builtin_amdgcn_perm(eh, el, 0x07030602u);  // (w[4], w[6])
           const uint32_t o01 = __builtin_amdgcn_perm(oh, ol, 0x05010400u);  // (w[1], w[3])
