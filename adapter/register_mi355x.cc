@@ -14,7 +14,7 @@
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
-//    ai.rt:Dequantize on AWQ / GPTQ / bitsandbytes encoded weights), and for the fused
+//    ai.rt:Dequantize on AWQ / GPTQ / bitsandbytes / QQQ encoded weights), and for the fused
 //    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
 //    an encoded weight, ai.rt.amd:DequantizeLinearGroupedMatMul on quantized
@@ -788,11 +788,42 @@ bool ExportBitsAndBytes(const rt::RuntimeValue &value, const Catalogue &catalogu
   return true;
 }
 
+// QQQ weights carried as encoded values (struct type
+// "onnx_light.qqq_weights.v1").  The native tensors (B, s_channel, s_group)
+// and numbers come from the reference's exporter (ExportQqqWeights,
+// quantization.h:697), which validates the encoding and its schema.
+struct QqqCheckpoint {
+  int64_t k = 0, n = 0, group = -1, bits = 4;
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  onnxl_amd_tensor T(const char *name) const {
+    auto it = tensors.find(name);
+    return it == tensors.end() ? Absent() : Describe(&it->second);
+  }
+};
+
+// False when the encoded value is not a QQQ weight.
+template <typename Catalogue>
+bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqCheckpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  if (catalogue.Resolve(enc.struct_type()).name().value() != "onnx_light.qqq_weights.v1") return false;
+  rt::QqqWeights w = rt::ExportQqqWeights(enc, size_t{1} << 30, catalogue);
+  out.k = w.in_features;
+  out.n = w.out_features;
+  out.group = w.group_size;
+  out.bits = static_cast<int64_t>(w.bits);
+  out.tensors = std::move(w.tensors);
+  return true;
+}
+
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
-// kernel_dequantize.cc:18-43): AWQ, GPTQ and bitsandbytes encodings decode
-// on the GPU to [out_features, in_features] of dtype
-// (onnxl_amd_dequantize_awq / _gptq / _bitsandbytes); every other encoding,
-// and values that reference shared parameters, run on the built-in kernel.
+// kernel_dequantize.cc:18-43): AWQ, GPTQ, bitsandbytes and QQQ encodings
+// decode on the GPU to [out_features, in_features] of dtype
+// (onnxl_amd_dequantize_awq / _gptq / _bitsandbytes / _qqq); every other
+// encoding, and values that reference shared parameters, run on the built-in
+// kernel.
 class Mi355xDequantize : public Mi355xKernel {
 public:
   static constexpr const char *name = "onnxl_amd:CPU:ai.rt:Dequantize";
@@ -819,9 +850,20 @@ public:
         rt::SetOutput(node, 0, std::move(y), ctx);
       return;
     }
+    QqqCheckpoint q;
+    if (value != ctx.values().end() && ExportQqq(value->second, ctx.struct_type_catalogue(), q)) {
+      const rt::Shape shape{q.n, q.k};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      const onnxl_amd_tensor qb = q.T("B"), qc = q.T("s_channel"), qg = q.T("s_group");
+      if (Call(onnxl_amd_dequantize_qqq(q.k, q.n, q.group, q.bits, &qb, &qc, &qg, &dy, nullptr), ctx))
+        rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / bitsandbytes");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / bitsandbytes / QQQ");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1045,9 +1087,9 @@ protected:
 
 // ai.rt.amd:DequantizeEncodedMatMul(A, Q) = MatMul(A, Transpose(Dequantize(Q,
 // dtype = A's dtype))) for an encoded weight Q of logical shape [N, K] (the
-// node the DequantizeEncodedMatMulGpu pattern writes): an AWQ or GPTQ weight
-// is prepared once (onnxl_amd_prepare_awq / _gptq) into the fused
-// DequantizeLinear -> MatMul operands when Q is a session constant, else
+// node the DequantizeEncodedMatMulGpu pattern writes): an AWQ, GPTQ or QQQ
+// weight is prepared once (onnxl_amd_prepare_awq / _gptq / _qqq) into the
+// fused DequantizeLinear -> MatMul operands when Q is a session constant, else
 // before each run; then one fused call.  What the preparation does not take
 // (AWQ gemv_fast / llm-awq, GPTQ act-order group maps and partial groups)
 // decodes to a dense weight on the GPU, and any other encoding through the
@@ -1107,7 +1149,8 @@ public:
     rt::Tensor y = ctx.MakeOutputTensor(0, a.data_type, shape, static_cast<size_t>(Count(shape)) * 2);
     onnxl_amd_tensor dy = DescribeOutput(y);
     const int32_t cast_to = w->scale.desc.data_type == kFloat ? a.data_type : 0;
-    Check(onnxl_amd_dequantize_linear_matmul(&a, &w->weight.desc, &w->scale.desc, &w->zero_point.desc, /*axis=*/0,
+    const int64_t axis = w->scale.desc.rank == 1 ? 1 : 0;  // per-column (QQQ) or blocked along K
+    Check(onnxl_amd_dequantize_linear_matmul(&a, &w->weight.desc, &w->scale.desc, &w->zero_point.desc, axis,
                                              cast_to, &dy, nullptr));
     rt::SetOutput(node, 0, std::move(y), ctx);
   }
@@ -1155,12 +1198,47 @@ private:
     return w;
   }
 
+  // A QQQ weight: the reference's checks in A's dtype once, then the fused
+  // operands (tiled INT4 codes with 16 x channel scales, or INT8 integers with
+  // the channel scales) for onnxl_amd_dequantize_linear_matmul; null when
+  // the library has no such operand for it (UNSUPPORTED).
+  std::shared_ptr<Prepared> PrepareQqq(rt::RuntimeContext &ctx, const QqqCheckpoint &q) const {
+    const onnxl_amd_tensor a = In(0, ctx);
+    int64_t wb = 0, sb = 0;
+    Check(onnxl_amd_prepare_qqq_size(q.k, q.n, q.group, q.bits, &wb, &sb));
+    auto w = std::make_shared<Prepared>();
+    w->weight.Allocate(wb);
+    w->scale.Allocate(sb);
+    DeviceTensor *outs[2] = {&w->weight, &w->scale};
+    const int64_t sizes[2] = {wb, sb};
+    for (int i = 0; i < 2; ++i) {
+      outs[i]->desc = onnxl_amd_tensor{};
+      outs[i]->desc.data = outs[i]->ptr;
+      outs[i]->desc.location = ONNXL_AMD_DEVICE;
+      outs[i]->desc.size_bytes = sizes[i];
+    }
+    w->zero_point.desc = Absent();
+    const onnxl_amd_tensor qb = q.T("B"), qc = q.T("s_channel"), qg = q.T("s_group");
+    const int rc = onnxl_amd_prepare_qqq(q.k, q.n, q.group, q.bits, &qb, &qc, &qg, a.data_type, &w->weight.desc,
+                                         &w->scale.desc, nullptr);
+    if (rc == ONNXL_AMD_UNSUPPORTED) return nullptr;
+    Check(rc);
+    Check(onnxl_amd_synchronize(nullptr));
+    w->fused = true;
+    return w;
+  }
+
   std::shared_ptr<Prepared> PrepareWeight(rt::RuntimeContext &ctx) const {
     const auto value = ctx.values().find(node_->input(1));
     if (value == ctx.values().end() || value->second.kind != rt::RuntimeValue::Kind::kEncoded)
       throw std::invalid_argument("Dequantize requires an EncodedValueProto input.");
     BnbCheckpoint b;
     if (ExportBitsAndBytes(value->second, ctx.struct_type_catalogue(), b)) return PrepareBitsAndBytes(ctx, b);
+    QqqCheckpoint q;
+    if (ExportQqq(value->second, ctx.struct_type_catalogue(), q)) {
+      auto w = PrepareQqq(ctx, q);
+      return w ? w : DenseOther(ctx, value->second);
+    }
     Checkpoint c;
     if (!ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) return DenseOther(ctx, value->second);
     const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");

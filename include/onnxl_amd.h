@@ -490,6 +490,46 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   int64_t block_size, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales,
                                   onnxl_amd_tensor *y, void *stream);
 
+/* QQQ weights (the encoding "onnx_light.qqq_weights.v1" of ai.rt:Dequantize:
+ * ImportQqqWeights / ExportQqqWeights, quantization.h, decoded by
+ * ReconstructQqqWeights, qqq.cc:346-358, through DequantizeTensor).  The
+ * caller passes the exported numbers and tensors: in_features k and
+ * out_features n (multiples of 64), group_size -1 or 128, bits 4; B INT32
+ * [k / 16, 2n] (the packed, permuted four-bit codes), s_channel FLOAT [1, n],
+ * s_group FLOAT16 [k / 128, n] when grouped (group 128 and k != 128), else
+ * FLOAT16 [0] or null.  The reference's checks (Geometry, CheckTensor,
+ * qqq.cc:38-56, 136-141, with DecodeValues' 1 << 30 byte limit) raise
+ * INVALID_ARGUMENT with its messages.
+ *
+ * onnxl_amd_dequantize_qqq decodes to y [n, k] of y's dtype (FLOAT, FLOAT16,
+ * BFLOAT16 or DOUBLE): value = fp32(integer * channel scale), integer =
+ * clamp(round-half-even((code - 8) * group scale), -128, 127) when grouped,
+ * else the signed code * 16 (qqq.cc:185-202), then WriteFloat's rounding
+ * (quantization.cc:184-201); CheckData's errors (qqq.cc:204-218: a channel or
+ * group scale not finite or negative, a value not finite) and WriteFloat's
+ * "Dequantization output dtype overflow." in the reference's order.
+ *
+ * onnxl_amd_prepare_qqq runs the same checks in `dtype` (the activations'
+ * dtype of the MatMul it feeds) and writes the operands of
+ * onnxl_amd_dequantize_linear_matmul into caller-allocated, 16-byte aligned
+ * device buffers of onnxl_amd_prepare_qqq_size bytes: weight INT4 [k, n] in
+ * the tiled layout with scale FLOAT [n] = 16 * channel scale (per channel),
+ * or INT8 [k, n] holding the integers with scale = the channel scales
+ * (grouped); it sets both descriptors.  MatMul(A, Transpose(Dequantize(Q,
+ * dtype = A's dtype))) is then onnxl_amd_dequantize_linear_matmul(A, weight,
+ * scale, null, axis 1, cast_to = A's dtype), value for value (x * scale
+ * rounds the same exact product once).  A per-channel weight whose 16 *
+ * channel scale overflows FLOAT returns ONNXL_AMD_UNSUPPORTED there. */
+int onnxl_amd_dequantize_qqq(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                             const onnxl_amd_tensor *B, const onnxl_amd_tensor *s_channel,
+                             const onnxl_amd_tensor *s_group, onnxl_amd_tensor *y, void *stream);
+int onnxl_amd_prepare_qqq_size(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                               int64_t *weight_bytes, int64_t *scale_bytes);
+int onnxl_amd_prepare_qqq(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                          const onnxl_amd_tensor *B, const onnxl_amd_tensor *s_channel,
+                          const onnxl_amd_tensor *s_group, int32_t dtype, onnxl_amd_tensor *weight,
+                          onnxl_amd_tensor *scale, void *stream);
+
 /* Waits for all work queued by this library on `stream`. */
 int onnxl_amd_synchronize(void *stream);
 

@@ -111,6 +111,9 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_prepare_bitsandbytes.argtypes = [I32, I64, I64, I64, I64, F32, TP, TP, TP, TP, TP, I32, PT,
                                                      ctypes.c_void_p]
         L.onnxl_amd_bitsandbytes_matmul.argtypes = [TP, I32, I64, I64, I64, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_prepare_qqq_size.argtypes = [I64, I64, I64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, I32, PT, PT, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
                                                          ctypes.c_int32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul_noalloc.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -425,6 +428,37 @@ def bitsandbytes_matmul(a, w: BnbWeight, out=None):
                                                describe(w.weight, code), describe(w.scales), describe(out),
                                                _stream_of(a, w.weight, out)))
     return out
+
+
+def dequantize_qqq(k: int, n: int, group_size: int, B, s_channel, s_group=None, output_dtype: int = FLOAT,
+                   out=None, bits: int = 4):
+    """onnxl_amd_dequantize_qqq: a QQQ weight (qqq.cc: in_features k,
+    out_features n, B int32 [k / 16, 2n], s_channel float32 [1, n], s_group
+    float16 [k / 128, n] or None) as [n, k] values."""
+    out = _decode_out(k, n, output_dtype, (B, s_channel), out)
+    _check(lib().onnxl_amd_dequantize_qqq(k, n, group_size, bits, describe(B), describe(s_channel),
+                                          describe(s_group), describe(out), _stream_of(B, s_channel, out)))
+    return out
+
+
+def prepare_qqq(k: int, n: int, group_size: int, B, s_channel, s_group=None, dtype: int = FLOAT16,
+                bits: int = 4) -> PreparedNbits:
+    """onnxl_amd_prepare_qqq: the fused kernels' weight (tiled INT4 per
+    channel, INT8 grouped) and FLOAT per-column scale, after the format's
+    checks in `dtype`; qqq_matmul multiplies with it."""
+    sizes = [ctypes.c_int64(0) for _ in range(2)]
+    _check(lib().onnxl_amd_prepare_qqq_size(k, n, group_size, bits, *(ctypes.byref(x) for x in sizes)))
+    w, s = _prepared_triplet(sizes, lambda pw, ps, st: lib().onnxl_amd_prepare_qqq(
+        k, n, group_size, bits, describe(B), describe(s_channel), describe(s_group), dtype, pw, ps, st))
+    return PreparedNbits(w, s, None, k, n)
+
+
+def qqq_matmul(a, prepared: PreparedNbits, out=None):
+    """MatMul(a, Transpose(Dequantize(Q, dtype = a's dtype))) for a QQQ weight
+    prepared by prepare_qqq: the fused DequantizeLinear -> Cast -> MatMul
+    entry point with the per-column scale (axis 1)."""
+    return dequantize_linear_matmul(a, prepared.weight, prepared.scale, None, 1, _torch_code(a.dtype),
+                                    x_shape=prepared.shape, out=out)
 
 
 def dequantize_gptq(fmt: str, qweight, qzeros, scales, g_idx, K: int, N: int, bits: int, group_size: int,

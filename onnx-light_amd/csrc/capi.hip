@@ -2510,6 +2510,150 @@ int BnbMatMul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t c
   return ONNXL_AMD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// QQQ weights (onnx_core/runtime/qqq.cc): the geometry and tensor checks of
+// Geometry / CheckTensor (:38-56, :136-141) with limit 1 << 30 (DecodeValues,
+// quantization.cc:2002-2008), CheckData (:204-218) and the reconstruction
+// (:185-202) on the device, WriteFloat's output check
+// (quantization.cc:184-201), and the fused operands.
+
+struct QqqGeometry {
+  int64_t k, n;
+  bool grouped;
+};
+
+void QqqTensor(const onnxl_amd_tensor *t, const char *name, int32_t dtype, std::initializer_list<int64_t> shape,
+               int64_t bytes) {
+  bool ok = !Absent(t) && t->data_type == dtype && t->rank == (int32_t)shape.size() && t->size_bytes == bytes &&
+            (bytes == 0 || t->data != nullptr);
+  int d = 0;
+  for (int64_t v : shape) ok = ok && t->dims[d++] == v;
+  OLA_ENFORCE(ok, "QQQ invalid tensor type, shape or byte extent: ", name, ".");
+  CheckDescriptor(t, name);
+}
+
+QqqGeometry QqqCheck(int64_t k, int64_t n, int64_t group, int64_t bits, const onnxl_amd_tensor *B,
+                     const onnxl_amd_tensor *s_channel, const onnxl_amd_tensor *s_group) {
+  constexpr int64_t kLimit = int64_t(1) << 30;
+  OLA_ENFORCE(k > 0 && n > 0 && k % 64 == 0 && n % 64 == 0 && bits == 4 && (group == -1 || group == 128),
+              "QQQ requires four-bit, unpadded dimensions divisible by 64 and group -1/128.");
+  QqqGeometry g{k, n, group == 128 && k != 128};
+  OLA_ENFORCE(!g.grouped || k % 128 == 0, "QQQ incomplete 128-element group.");
+  OLA_ENFORCE(k <= kLimit / 4 / n, "QQQ logical FLOAT weights exceed max_bytes.");
+  const int64_t gb = g.grouped ? k / 128 * n * 2 : 0;
+  OLA_ENFORCE(k * n / 2 + 4 * n + gb <= kLimit, "QQQ checkpoint exceeds max_bytes.");
+  QqqTensor(B, "B", kInt32, {k / 16, 2 * n}, k * n / 2);
+  QqqTensor(s_channel, "s_channel", kFloat, {1, n}, 4 * n);
+  if (g.grouped || !Absent(s_group)) {
+    if (g.grouped)
+      QqqTensor(s_group, "s_group", kFloat16, {k / 128, n}, gb);
+    else
+      QqqTensor(s_group, "s_group", kFloat16, {0}, 0);
+  }
+  return g;
+}
+
+// The device work of one QQQ call: staged inputs, the flag word and `extra`
+// bytes of scratch after it.
+struct QqqRun {
+  QqqParams p{};
+  std::unique_ptr<Staging> st;
+  onnxl_amd_tensor flag_desc{};
+
+  QqqRun(hipStream_t stream, const QqqGeometry &g, size_t extra, const onnxl_amd_tensor *B,
+         const onnxl_amd_tensor *s_channel, const onnxl_amd_tensor *s_group, onnxl_amd_tensor *y) {
+    st.reset(new Staging(stream, 256 + extra, {B, s_channel, s_group}, {y}));
+    p.k = g.k;
+    p.n = g.n;
+    p.grouped = g.grouped ? 1 : 0;
+    p.codes = static_cast<const uint8_t *>(st->In(B));
+    p.channel = static_cast<const float *>(st->In(s_channel));
+    p.group = g.grouped ? static_cast<const uint16_t *>(st->In(s_group)) : nullptr;
+    p.flag = static_cast<unsigned *>(st->Extra());
+    hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, p.flag, (size_t)1);
+    flag_desc.data_type = kInt32;
+    flag_desc.rank = 1;
+    flag_desc.dims[0] = 1;
+    flag_desc.data = p.flag;
+    flag_desc.size_bytes = 4;
+    flag_desc.location = ONNXL_AMD_DEVICE;
+  }
+  void *Extra() const { return static_cast<char *>(st->Extra()) + 256; }
+  unsigned Flag(hipStream_t stream) {
+    unsigned v = 0;
+    ReadOnStream(stream, flag_desc, &v, 4);
+    return v;
+  }
+  // CheckData's failures, then WriteFloat's, in the reference's order
+  static void Raise(unsigned flag) {
+    OLA_ENFORCE(!(flag & kQqqBadChannel), "QQQ nonfinite or negative channel scale.");
+    OLA_ENFORCE(!(flag & kQqqBadGroup), "QQQ nonfinite or negative group scale.");
+    OLA_ENFORCE(!(flag & kQqqBadValue), "QQQ FLOAT reconstruction overflow.");
+    OLA_ENFORCE(!(flag & kQqqBadOutput), "Dequantization output dtype overflow.");
+  }
+};
+
+bool QqqDtype(int32_t dt) { return dt == kFloat || dt == kFloat16 || dt == kBfloat16 || dt == kDouble; }
+
+int DequantizeQqq(int64_t k, int64_t n, int64_t group, int64_t bits, const onnxl_amd_tensor *B,
+                  const onnxl_amd_tensor *s_channel, const onnxl_amd_tensor *s_group, onnxl_amd_tensor *y,
+                  hipStream_t stream) {
+  const QqqGeometry g = QqqCheck(k, n, group, bits, B, s_channel, s_group);
+  OLA_ENFORCE(y != nullptr && QqqDtype(y->data_type), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  CheckDescriptor(y, "y");
+  const int64_t width = y->data_type == kDouble ? 8 : (y->data_type == kFloat ? 4 : 2);
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == n && y->dims[1] == k && y->size_bytes == n * k * width,
+              "QQQ: y must be [out_features, in_features] of its dtype.");
+  OLA_ENFORCE(y->data != nullptr, "QQQ: y has no data.");
+  Ctx();
+  QqqRun run(stream, g, 0, B, s_channel, s_group, y);
+  LaunchQqqDecode(run.p, y->data_type, run.st->Out(y), stream);
+  OLA_HIP(hipGetLastError());
+  QqqRun::Raise(run.Flag(stream));
+  run.st->Finish();
+  return ONNXL_AMD_OK;
+}
+
+int64_t QqqWeightBytes(const QqqGeometry &g) { return g.grouped ? g.k * g.n : TiledInt4Bytes(g.k, g.n); }
+
+int PrepareQqq(int64_t k, int64_t n, int64_t group, int64_t bits, const onnxl_amd_tensor *B,
+               const onnxl_amd_tensor *s_channel, const onnxl_amd_tensor *s_group, int32_t dtype,
+               onnxl_amd_tensor *weight, onnxl_amd_tensor *scale, hipStream_t stream) {
+  const QqqGeometry g = QqqCheck(k, n, group, bits, B, s_channel, s_group);
+  OLA_ENFORCE(QqqDtype(dtype), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  OLA_ENFORCE(weight && scale, "prepare_qqq: weight and scale are required.");
+  const int64_t wb = QqqWeightBytes(g);
+  for (const onnxl_amd_tensor *t : {static_cast<const onnxl_amd_tensor *>(weight),
+                                    static_cast<const onnxl_amd_tensor *>(scale)})
+    OLA_ENFORCE(t->location == ONNXL_AMD_DEVICE && t->data != nullptr &&
+                    reinterpret_cast<uintptr_t>(t->data) % 16 == 0,
+                "prepare_qqq: weight and scale must be 16-byte aligned device buffers.");
+  OLA_ENFORCE(weight->size_bytes >= wb && scale->size_bytes >= 4 * n, "prepare_qqq: weight holds ",
+              weight->size_bytes, " bytes and scale ", scale->size_bytes, "; they need ", wb, " and ", 4 * n);
+  Ctx();
+  QqqRun run(stream, g, g.grouped ? 0 : (size_t)(k * n / 2), B, s_channel, s_group, nullptr);
+  LaunchQqqDecode(run.p, dtype, nullptr, stream);  // the checks alone, in the Dequantize dtype
+  OLA_HIP(hipGetLastError());
+  QqqRun::Raise(run.Flag(stream));
+  uint8_t *packed = g.grouped ? static_cast<uint8_t *>(weight->data) : static_cast<uint8_t *>(run.Extra());
+  LaunchQqqPack(run.p, packed, static_cast<float *>(scale->data), stream);
+  if (!g.grouped) LaunchTileInt4(packed, k, n, 1, static_cast<uint32_t *>(weight->data), stream);
+  OLA_HIP(hipGetLastError());
+  if (run.Flag(stream) & kQqqBadPrepared)
+    throw Unsupported("QQQ: 16 x a channel scale overflows FLOAT, so the INT4 operand has no finite scale "
+                      "(onnxl_amd_dequantize_qqq decodes such a weight)");
+  run.st->Finish();
+  weight->data_type = g.grouped ? kInt8 : kInt4;
+  weight->rank = 2;
+  for (int i = 0; i < ONNXL_AMD_MAX_RANK; ++i) weight->dims[i] = i == 0 ? k : (i == 1 ? n : 0);
+  weight->layout = g.grouped ? ONNXL_AMD_LAYOUT_ONNX : ONNXL_AMD_LAYOUT_TILED_INT4;
+  scale->data_type = kFloat;
+  scale->rank = 1;
+  for (int i = 0; i < ONNXL_AMD_MAX_RANK; ++i) scale->dims[i] = i == 0 ? n : 0;
+  scale->layout = ONNXL_AMD_LAYOUT_ONNX;
+  return ONNXL_AMD_OK;
+}
+
 // Validation runs before any device work, so argument errors are reported
 // even before onnxl_amd_init (the first device access then raises
 // NotInitialized).
@@ -2918,6 +3062,39 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return BnbMatMul(a, format, rows, cols, block_size, weight, scales, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_qqq(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                             const onnxl_amd_tensor *B, const onnxl_amd_tensor *s_channel,
+                             const onnxl_amd_tensor *s_group, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeQqq(in_features, out_features, group_size, bits, B, s_channel, s_group, y,
+                         static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_qqq_size(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                               int64_t *weight_bytes, int64_t *scale_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(weight_bytes && scale_bytes, "prepare_qqq_size: null output");
+    OLA_ENFORCE(in_features > 0 && out_features > 0 && in_features % 64 == 0 && out_features % 64 == 0 &&
+                    bits == 4 && (group_size == -1 || group_size == 128),
+                "QQQ requires four-bit, unpadded dimensions divisible by 64 and group -1/128.");
+    const QqqGeometry g{in_features, out_features, group_size == 128 && in_features != 128};
+    *weight_bytes = QqqWeightBytes(g);
+    *scale_bytes = 4 * out_features;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_qqq(int64_t in_features, int64_t out_features, int64_t group_size, int64_t bits,
+                          const onnxl_amd_tensor *B, const onnxl_amd_tensor *s_channel,
+                          const onnxl_amd_tensor *s_group, int32_t dtype, onnxl_amd_tensor *weight,
+                          onnxl_amd_tensor *scale, void *stream) {
+  return Guard([&] {
+    return PrepareQqq(in_features, out_features, group_size, bits, B, s_channel, s_group, dtype, weight, scale,
+                      static_cast<hipStream_t>(stream));
   });
 }
 

@@ -194,6 +194,26 @@ struct BnbParams {
   unsigned *flag;
 };
 void LaunchBnbScales(const BnbParams &p, hipStream_t s);
+
+// QQQ weights (qqq.hip): flag bits of a decode / preparation, in the order
+// the reference raises them.
+constexpr unsigned kQqqBadChannel = 1;   // a channel scale not finite or negative
+constexpr unsigned kQqqBadGroup = 2;     // a group scale not finite or negative
+constexpr unsigned kQqqBadValue = 4;     // a value not finite in fp32
+constexpr unsigned kQqqBadOutput = 8;    // a value past the output dtype's range
+constexpr unsigned kQqqBadPrepared = 16; // 16 * a channel scale overflows fp32 (no INT4 operand)
+struct QqqParams {
+  int64_t k, n;              // in_features, out_features (multiples of 64)
+  int grouped;               // group 128 with k != 128
+  const uint8_t *codes;      // B [k / 16, 2n] int32 words, as bytes
+  const float *channel;      // s_channel [n] (stored order)
+  const uint16_t *group;     // s_group [k / 128, n] fp16 (stored order), grouped only
+  unsigned *flag;
+};
+// out_dtype kFloat, kFloat16, kBfloat16 or kDouble; y [n, k] or null (checks alone)
+void LaunchQqqDecode(const QqqParams &p, int out_dtype, void *y, hipStream_t s);
+// weight: INT4 [k, n] ONNX packing (per channel) or INT8 [k, n] (grouped); scale FLOAT [n]
+void LaunchQqqPack(const QqqParams &p, uint8_t *weight, float *scale, hipStream_t s);
 // out_dtype kFloat, kFloat16, kBfloat16, or 0: the finiteness check alone
 void LaunchBnbDecode(const BnbParams &p, int out_dtype, void *y, hipStream_t s);
 // y[M, N] FLOAT16 = a[M, K] x W^T, W the FLOAT16 decode of nf4 / fp4 codes

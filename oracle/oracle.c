@@ -1777,3 +1777,106 @@ int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, i
   }
   return 0;
 }
+
+/* ---- QQQ weights, onnx_core/runtime/qqq.cc ----------------------------------
+ * TEST INFRASTRUCTURE (the checker of the GPU decode, never the product).
+ * Geometry (:38-68): k rows (in_features), n columns (out_features), both
+ * multiples of 64; grouped when group == 128 and k != 128.  The packed words
+ * B [k / 16, 2n] hold 16x16 tiles of codes, (k / 16, n / 16) in row-major
+ * tile order, each tile row-major, and every 1024-code block permuted by
+ * _get_perms (:57-67): permutation[i * 32 + j * 8 + lane] = 256 j +
+ * 16 (4 (i % 4) + p % 4) + i / 4 + 8 (p / 4) with p = order[lane] (order
+ * {0,2,4,6,1,3,5,7} grouped, {4,0,5,1,6,2,7,3} per channel); the code of
+ * (n, k) is nibble inverse[tiled % 1024] of its block (Position, :80-85;
+ * Code, :166-169: nibble p at bits 4 (p % 2) of byte p / 2).
+ * Scales (ScalePosition, :144-149): channel n at storage index (n / 32) 32 +
+ * ((n % 32 % 8) / 2) 8 + (n % 32 / 8) 2 + n % 2; group scale (k / 128, n),
+ * index i = (k / 128) n_total + n, at (i / 64) 64 + (i % 8) 8 + (i % 64) / 8.
+ * Reconstructed (:185-202): grouped, integer = (code - 8) * group scale
+ * rounded half to even in double, clamped to [-128, 127], a zero keeping the
+ * product's sign; per channel, integer = signed nibble * 16; value =
+ * fp32(integer * channel scale) rounded to nearest even (RoundFloat,
+ * :162-183, is IEEE double -> float rounding).
+ * orc_qqq_reconstruct returns CheckData's first failure (:204-218) -- 1
+ * "QQQ nonfinite or negative channel scale.", 2 "... group scale.", 3 "QQQ
+ * FLOAT reconstruction overflow." -- or 4 when a value does not fit
+ * out_dtype (WriteFloat, quantization.cc:184-201: "Dequantization output
+ * dtype overflow."), else 0; values [n, k] in FLOAT (1), FLOAT16 (10),
+ * BFLOAT16 (16) or DOUBLE (11); codes [n, k] when not NULL. */
+static void qqq_permutation(int grouped, int32_t *perm, int32_t *inverse) {
+  static const int channel_order[8] = {4, 0, 5, 1, 6, 2, 7, 3};
+  static const int grouped_order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  const int *order = grouped ? grouped_order : channel_order;
+  for (int i = 0; i < 32; ++i)
+    for (int j = 0; j < 4; ++j)
+      for (int lane = 0; lane < 8; ++lane) {
+        const int p = order[lane];
+        const int index = i * 32 + j * 8 + lane;
+        perm[index] = 256 * j + 16 * (4 * (i % 4) + p % 4) + i / 4 + 8 * (p / 4);
+        inverse[perm[index]] = index;
+      }
+}
+
+static int qqq_grouped(int64_t k, int64_t group) { return group == 128 && k != 128; }
+
+int64_t orc_qqq_position(int64_t k, int64_t n, int64_t group, int64_t n_index, int64_t k_index) {
+  int32_t perm[1024], inverse[1024];
+  qqq_permutation(qqq_grouped(k, group), perm, inverse);
+  const int64_t tiled = (k_index / 16) * n * 16 + (n_index / 16) * 256 + (k_index % 16) * 16 + n_index % 16;
+  return (tiled / 1024) * 1024 + inverse[tiled % 1024];
+}
+
+int64_t orc_qqq_scale_position(int64_t index, int channel) {
+  if (!channel) return (index / 64) * 64 + (index % 8) * 8 + (index % 64) / 8;
+  const int64_t local = index % 32;
+  return (index / 32) * 32 + ((local % 8) / 2) * 8 + (local / 8) * 2 + local % 2;
+}
+
+int orc_qqq_reconstruct(int64_t k, int64_t n, int64_t group, const uint8_t *words, const float *s_channel,
+                        const uint16_t *s_group, int out_dtype, void *out, uint8_t *codes) {
+  const int grouped = qqq_grouped(k, group);
+  int32_t perm[1024], inverse[1024];
+  qqq_permutation(grouped, perm, inverse);
+  for (int64_t c = 0; c < n; ++c) {
+    const float s = s_channel[orc_qqq_scale_position(c, 1)];
+    if (!isfinite(s) || s < 0) return 1;
+  }
+  if (grouped)
+    for (int64_t i = 0; i < (k / 128) * n; ++i) {
+      const float s = orc_f16_to_f32(s_group[i]);
+      if (!isfinite(s) || s < 0) return 2;
+    }
+  int rc = 0;
+  for (int64_t c = 0; c < n; ++c)
+    for (int64_t r = 0; r < k; ++r) {
+      const int64_t tiled = (r / 16) * n * 16 + (c / 16) * 256 + (r % 16) * 16 + c % 16;
+      const int64_t pos = (tiled / 1024) * 1024 + inverse[tiled % 1024];
+      const int code = (words[pos / 2] >> ((pos % 2) * 4)) & 15;
+      if (codes) codes[c * k + r] = (uint8_t)code;
+      float integer;
+      if (grouped) {
+        const double gs = orc_f16_to_f32(s_group[orc_qqq_scale_position((r / 128) * n + c, 0)]);
+        const double scaled = (double)(code - 8) * gs;
+        const double lower = floor(scaled), fraction = scaled - lower;
+        const double rounded = lower + ((fraction > 0.5 || (fraction == 0.5 && fmod(lower, 2) != 0)) ? 1 : 0);
+        integer = rounded == 0 ? copysignf(0.0f, (float)scaled)
+                               : (float)(rounded < -128 ? -128 : (rounded > 127 ? 127 : rounded));
+      } else {
+        integer = (float)((code >= 8 ? code - 16 : code) * 16);
+      }
+      const float v = (float)((double)integer * (double)s_channel[orc_qqq_scale_position(c, 1)]);
+      if (!isfinite(v)) return 3;
+      const int64_t e = c * k + r;
+      if (out_dtype == 1) {
+        ((float *)out)[e] = v;
+      } else if (out_dtype == 11) {
+        ((double *)out)[e] = (double)v;
+      } else {
+        const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+        const int inf = out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u;
+        if (inf && rc == 0) rc = 4;
+        ((uint16_t *)out)[e] = h;
+      }
+    }
+  return rc;
+}

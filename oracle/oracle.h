@@ -224,6 +224,14 @@ int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, i
                         const uint8_t *codes, const void *absmax, const float *nested_absmax,
                         const float *nested_map, int out_dtype, void *out);
 
+/* QQQ weights (four-bit, group -1 / 128): nibble position of (n, k) in the
+ * packed words, storage index of a channel / group scale, and the
+ * reconstruction with the format's checks. */
+int64_t orc_qqq_position(int64_t k, int64_t n, int64_t group, int64_t n_index, int64_t k_index);
+int64_t orc_qqq_scale_position(int64_t index, int channel);
+int orc_qqq_reconstruct(int64_t k, int64_t n, int64_t group, const uint8_t *words, const float *s_channel,
+                        const uint16_t *s_group, int out_dtype, void *out, uint8_t *codes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,6 +126,12 @@ def _declare(L):
     L.orc_bnb_check.restype = ctypes.c_int
     L.orc_bnb_check.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                 ctypes.c_float, P, P, P, P]
+    L.orc_qqq_position.restype = ctypes.c_int64
+    L.orc_qqq_position.argtypes = [ctypes.c_int64] * 5
+    L.orc_qqq_scale_position.restype = ctypes.c_int64
+    L.orc_qqq_scale_position.argtypes = [ctypes.c_int64, ctypes.c_int]
+    L.orc_qqq_reconstruct.restype = ctypes.c_int
+    L.orc_qqq_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, P, P, P, ctypes.c_int, P, P]
     L.orc_bnb_reconstruct.restype = ctypes.c_int
     L.orc_bnb_reconstruct.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                       ctypes.c_float, P, P, P, P, ctypes.c_int, P]
@@ -640,3 +646,34 @@ def bnb_reconstruct(fmt: str, rows: int, cols: int, block: int, codes, absmax, n
     rc = lib().orc_bnb_reconstruct(BNB_FORMATS[fmt], rows, cols, block, int(nested), offset, _ptr(cd), _ptr(am),
                                    _ptr(_f32(nested_absmax)), _ptr(_f32(nested_map)), out_dtype, _ptr(out))
     return rc, out
+
+
+# ---- QQQ weights (four-bit, group -1 / 128) ------------------------------------
+
+QQQ_ERRORS = {1: "QQQ nonfinite or negative channel scale.", 2: "QQQ nonfinite or negative group scale.",
+              3: "QQQ FLOAT reconstruction overflow.", 4: "Dequantization output dtype overflow."}
+
+
+def qqq_position(k: int, n: int, group: int, n_index: int, k_index: int) -> int:
+    """Nibble index of code (n_index, k_index) in the packed words."""
+    return lib().orc_qqq_position(k, n, group, n_index, k_index)
+
+
+def qqq_scale_position(index: int, channel: bool) -> int:
+    """Storage index of logical channel scale `index` (or group-scale index)."""
+    return lib().orc_qqq_scale_position(index, int(channel))
+
+
+def qqq_reconstruct(k: int, n: int, group: int, words, s_channel, s_group, out_dtype: int = FLOAT):
+    """(rc, values [n, k], codes [n, k]): float32 (FLOAT), float64 (DOUBLE) or
+    uint16 bits (FLOAT16 / BFLOAT16); rc is 0 or a key of QQQ_ERRORS.  words:
+    the int32 B tensor; s_channel float32 [1, n]; s_group float16 [k/128, n]
+    (or empty)."""
+    w = np.ascontiguousarray(words).view(np.uint8)
+    sc = np.ascontiguousarray(s_channel, dtype=np.float32)
+    sg = np.ascontiguousarray(s_group).view(np.uint16) if np.size(s_group) else np.zeros(1, np.uint16)
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((n, k), dt)
+    codes = np.zeros((n, k), np.uint8)
+    rc = lib().orc_qqq_reconstruct(k, n, group, _ptr(w), _ptr(sc), _ptr(sg), out_dtype, _ptr(out), _ptr(codes))
+    return rc, out, codes

@@ -507,3 +507,47 @@ def test_gptq_validation(olamd):
     assert L.onnxl_amd_prepare_gptq_size(b"gptq_p", 4096, 4096, 6, 128, olamd.INT32, olamd.FLOAT,
                                          ctypes.byref(w), ctypes.byref(s), ctypes.byref(z)) == olamd.OK
     assert (w.value, s.value, z.value) == (4096 * 4096, 32 * 4096 * 4, 32 * 4096)
+
+
+def test_qqq_validation(olamd):
+    """The QQQ format's geometry and tensor checks and messages
+    (onnx_core/runtime/qqq.cc:38-56 Geometry, :136-141 CheckTensor) on host
+    payloads; valid arguments stop at NOT_INITIALIZED.  CheckData's scale and
+    overflow errors need the device (test_gpu_qqq.py)."""
+    L = olamd.lib()
+    d = olamd.describe
+    k, n = 256, 64
+    B = np.zeros((k // 16, 2 * n), np.int32)
+    sc = np.ones((1, n), np.float32)
+    sg = np.ones((k // 128, n), np.float16)
+
+    def run(k=k, n=n, group=128, bits=4, B=B, sc=sc, sg=sg, y=None):
+        y = np.zeros((n, k), np.float32) if y is None else y
+        rc = L.onnxl_amd_dequantize_qqq(k, n, group, bits, d(B), d(sc), d(sg), d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    geo = "QQQ requires four-bit, unpadded dimensions divisible by 64 and group -1/128."
+    for kw, msg in ((dict(k=96), geo), (dict(n=0), geo), (dict(bits=8), geo), (dict(group=64), geo),
+                    (dict(k=192, B=B[:12], sg=sg[:1]), "QQQ incomplete 128-element group."),
+                    (dict(B=B.astype(np.int64)), "QQQ invalid tensor type, shape or byte extent: B."),
+                    (dict(B=B[:8]), "QQQ invalid tensor type, shape or byte extent: B."),
+                    (dict(sc=sc.reshape(-1)), "QQQ invalid tensor type, shape or byte extent: s_channel."),
+                    (dict(sc=sc.astype(np.float16)), "QQQ invalid tensor type, shape or byte extent: s_channel."),
+                    (dict(sg=sg[:1]), "QQQ invalid tensor type, shape or byte extent: s_group."),
+                    (dict(sg=None), "QQQ invalid tensor type, shape or byte extent: s_group."),
+                    (dict(group=-1), "QQQ invalid tensor type, shape or byte extent: s_group."),
+                    (dict(k=32768, n=16384, B=None), "QQQ logical FLOAT weights exceed max_bytes."),
+                    (dict(y=np.zeros((n, k), np.int32)), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16."),
+                    (dict(y=np.zeros((k, n), np.float32)), "QQQ: y must be [out_features, in_features]")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    assert run()[0] == olamd.NOT_INITIALIZED
+    # per channel (and group 128 with k == 128): s_group empty or absent
+    assert run(group=-1, sg=np.zeros(0, np.float16))[0] == olamd.NOT_INITIALIZED
+    assert run(group=-1, sg=None)[0] == olamd.NOT_INITIALIZED
+    assert run(k=128, B=B[:8], sg=None, y=np.zeros((n, 128), np.float32))[0] == olamd.NOT_INITIALIZED
+    w, s = ctypes.c_int64(), ctypes.c_int64()
+    assert L.onnxl_amd_prepare_qqq_size(4096, 11008, 128, 4, ctypes.byref(w), ctypes.byref(s)) == olamd.OK
+    assert (w.value, s.value) == (4096 * 11008, 11008 * 4)
+    assert L.onnxl_amd_prepare_qqq_size(4096, 11008, -1, 4, ctypes.byref(w), ctypes.byref(s)) == olamd.OK
+    assert w.value == 4096 * 11008 // 2
