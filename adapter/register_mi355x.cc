@@ -14,8 +14,9 @@
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
-//    ai.rt:Dequantize on AWQ / GPTQ / bitsandbytes / QQQ encoded weights), and for the fused
-//    nodes the GPU patterns produce (ai.rt.amd:DequantizeLinearMatMul,
+//    ai.rt:Dequantize on AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ encoded
+//    weights), and for the fused nodes the GPU patterns produce
+//    (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
 //    an encoded weight, ai.rt.amd:DequantizeLinearGroupedMatMul on quantized
 //    MoE experts),
@@ -700,17 +701,40 @@ private:
 // :727), which validate the encoding and its schema; the library then takes
 // them as host descriptors.
 struct Checkpoint {
-  bool awq = false;
-  std::string kind;  // AWQ variant or GPTQ format
+  bool awq = false, bitblas = false;
+  std::string kind;  // AWQ variant, GPTQ format or BitBLAS originating method
   int64_t K = 0, N = 0, bits = 0, group = 0;
+  int32_t symmetric = 0;  // BitBLAS
   std::unordered_map<std::string, rt::Tensor> tensors;
   onnxl_amd_tensor T(const char *name) const {
     auto it = tensors.find(name);
     return it == tensors.end() ? Absent() : Describe(&it->second);
   }
+  onnxl_amd_tensor Zeros() const { return T(kind == "llm-awq" ? "scaled_zeros" : "qzeros"); }
+  // The dense decode y [N, K] through the encoding's entry point.
+  int Decode(onnxl_amd_tensor *y) const {
+    const onnxl_amd_tensor qw = T("qweight"), sc = T("scales"), gi = T("g_idx"), qz = Zeros();
+    if (bitblas)
+      return onnxl_amd_dequantize_bitblas(kind.c_str(), &qw, &sc, &qz, K, N, bits, group, symmetric, y, nullptr);
+    return awq ? onnxl_amd_dequantize_awq(kind.c_str(), &qw, &qz, &sc, K, N, bits, group, y, nullptr)
+               : onnxl_amd_dequantize_gptq(kind.c_str(), &qw, &qz, &sc, &gi, K, N, bits, group, y, nullptr);
+  }
+  int PreparedSizes(int64_t *wb, int64_t *sb, int64_t *zb) const {
+    const onnxl_amd_tensor qw = T("qweight"), sc = T("scales");
+    if (bitblas) return onnxl_amd_prepare_bitblas_size(kind.c_str(), K, N, bits, group, symmetric, wb, sb, zb);
+    return awq ? onnxl_amd_prepare_awq_size(kind.c_str(), K, N, bits, group, sc.data_type, wb, sb, zb)
+               : onnxl_amd_prepare_gptq_size(kind.c_str(), K, N, bits, group, qw.data_type, sc.data_type, wb, sb, zb);
+  }
+  int Prepare(onnxl_amd_tensor *w, onnxl_amd_tensor *s, onnxl_amd_tensor *z) const {
+    const onnxl_amd_tensor qw = T("qweight"), sc = T("scales"), gi = T("g_idx"), qz = Zeros();
+    if (bitblas)
+      return onnxl_amd_prepare_bitblas(kind.c_str(), &qw, &sc, &qz, K, N, bits, group, symmetric, w, s, z, nullptr);
+    return awq ? onnxl_amd_prepare_awq(kind.c_str(), &qw, &qz, &sc, K, N, bits, group, w, s, z, nullptr)
+               : onnxl_amd_prepare_gptq(kind.c_str(), &qw, &qz, &sc, &gi, K, N, bits, group, w, s, z, nullptr);
+  }
 };
 
-// False when the encoded value is neither AWQ nor GPTQ.
+// False when the encoded value is none of AWQ, GPTQ and BitBLAS.
 template <typename Catalogue>
 bool ExportCheckpoint(const rt::RuntimeValue &value, const Catalogue &catalogue, Checkpoint &out) {
   if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
@@ -720,12 +744,26 @@ bool ExportCheckpoint(const rt::RuntimeValue &value, const Catalogue &catalogue,
   const std::string type = catalogue.Resolve(enc.struct_type()).name().value();
   if (type == "onnx_light.awq_weights.v1") {
     rt::AwqWeights w = rt::ExportAwqWeights(enc, size_t{1} << 30, catalogue);
-    out = Checkpoint{true, w.variant, w.in_features, w.out_features, w.bits, w.group_size, std::move(w.tensors)};
+    out.awq = true;
+    out.kind = w.variant;
+    out.K = w.in_features, out.N = w.out_features, out.bits = w.bits, out.group = w.group_size;
+    out.tensors = std::move(w.tensors);
     return true;
   }
   if (type == "onnx_light.gptq_weights.v1") {
     rt::GptqWeights w = rt::ExportGptqWeights(enc, size_t{1} << 30, catalogue);
-    out = Checkpoint{false, w.format, w.in_features, w.out_features, w.bits, w.group_size, std::move(w.tensors)};
+    out.kind = w.format;
+    out.K = w.in_features, out.N = w.out_features, out.bits = w.bits, out.group = w.group_size;
+    out.tensors = std::move(w.tensors);
+    return true;
+  }
+  if (type == "onnx_light.bitblas_weights.v1") {  // layout and revision checked by the exporter
+    rt::BitblasWeights w = rt::ExportBitblasWeights(enc, size_t{1} << 30, catalogue);
+    out.bitblas = true;
+    out.kind = w.method;
+    out.K = w.in_features, out.N = w.out_features, out.bits = w.bits, out.group = w.group_size;
+    out.symmetric = w.symmetric ? 1 : 0;
+    out.tensors = std::move(w.tensors);
     return true;
   }
   return false;
@@ -819,9 +857,9 @@ bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqChe
 }
 
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
-// kernel_dequantize.cc:18-43): AWQ, GPTQ, bitsandbytes and QQQ encodings
-// decode on the GPU to [out_features, in_features] of dtype
-// (onnxl_amd_dequantize_awq / _gptq / _bitsandbytes / _qqq); every other
+// kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes and QQQ
+// encodings decode on the GPU to [out_features, in_features] of dtype
+// (onnxl_amd_dequantize_awq / _gptq / _bitblas / _bitsandbytes / _qqq); every other
 // encoding, and values that reference shared parameters, run on the built-in
 // kernel.
 class Mi355xDequantize : public Mi355xKernel {
@@ -863,20 +901,14 @@ public:
     }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / bitsandbytes / QQQ");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ");
       return;
     }
     const rt::Shape shape{c.N, c.K};
     rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
                                         ByteSize(static_cast<int32_t>(dtype), Count(shape)));
     onnxl_amd_tensor dy = DescribeOutput(y);
-    const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
-    const onnxl_amd_tensor qz = c.T(c.kind == "llm-awq" ? "scaled_zeros" : "qzeros");
-    const int rc = c.awq ? onnxl_amd_dequantize_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group, &dy,
-                                                    nullptr)
-                         : onnxl_amd_dequantize_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group,
-                                                     &dy, nullptr);
-    if (Call(rc, ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+    if (Call(c.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
   }
 };
 
@@ -1087,10 +1119,10 @@ protected:
 
 // ai.rt.amd:DequantizeEncodedMatMul(A, Q) = MatMul(A, Transpose(Dequantize(Q,
 // dtype = A's dtype))) for an encoded weight Q of logical shape [N, K] (the
-// node the DequantizeEncodedMatMulGpu pattern writes): an AWQ, GPTQ or QQQ
-// weight is prepared once (onnxl_amd_prepare_awq / _gptq / _qqq) into the
-// fused DequantizeLinear -> MatMul operands when Q is a session constant, else
-// before each run; then one fused call.  What the preparation does not take
+// node the DequantizeEncodedMatMulGpu pattern writes): an AWQ, GPTQ, BitBLAS
+// or QQQ weight is prepared once (onnxl_amd_prepare_awq / _gptq / _bitblas /
+// _qqq) into the fused DequantizeLinear -> MatMul operands when Q is a
+// session constant, else before each run; then one fused call.  What the preparation does not take
 // (AWQ gemv_fast / llm-awq, GPTQ act-order group maps and partial groups)
 // decodes to a dense weight on the GPU, and any other encoding through the
 // reference's DequantizeTensor; the dense weight is transposed once and the
@@ -1241,13 +1273,9 @@ private:
     }
     Checkpoint c;
     if (!ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) return DenseOther(ctx, value->second);
-    const onnxl_amd_tensor qw = c.T("qweight"), sc = c.T("scales"), gi = c.T("g_idx");
-    const onnxl_amd_tensor qz = c.T(c.kind == "llm-awq" ? "scaled_zeros" : "qzeros");
     auto w = std::make_shared<Prepared>();
     int64_t wb = 0, sb = 0, zb = 0;
-    Check(c.awq ? onnxl_amd_prepare_awq_size(c.kind.c_str(), c.K, c.N, c.bits, c.group, sc.data_type, &wb, &sb, &zb)
-                : onnxl_amd_prepare_gptq_size(c.kind.c_str(), c.K, c.N, c.bits, c.group, qw.data_type, sc.data_type,
-                                              &wb, &sb, &zb));
+    Check(c.PreparedSizes(&wb, &sb, &zb));
     w->weight.Allocate(wb);
     w->scale.Allocate(sb);
     w->zero_point.Allocate(zb);
@@ -1259,10 +1287,7 @@ private:
       outs[i]->desc.location = ONNXL_AMD_DEVICE;
       outs[i]->desc.size_bytes = sizes[i];
     }
-    const int rc = c.awq ? onnxl_amd_prepare_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group,
-                                                 &w->weight.desc, &w->scale.desc, &w->zero_point.desc, nullptr)
-                         : onnxl_amd_prepare_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group,
-                                                  &w->weight.desc, &w->scale.desc, &w->zero_point.desc, nullptr);
+    const int rc = c.Prepare(&w->weight.desc, &w->scale.desc, &w->zero_point.desc);
     if (rc != ONNXL_AMD_UNSUPPORTED) {
       Check(rc);
       Check(onnxl_amd_synchronize(nullptr));
@@ -1282,9 +1307,7 @@ private:
     host.data = nk.data();
     host.size_bytes = static_cast<int64_t>(count * 2);
     host.location = ONNXL_AMD_HOST;
-    Check(c.awq ? onnxl_amd_dequantize_awq(c.kind.c_str(), &qw, &qz, &sc, c.K, c.N, c.bits, c.group, &host, nullptr)
-                : onnxl_amd_dequantize_gptq(c.kind.c_str(), &qw, &qz, &sc, &gi, c.K, c.N, c.bits, c.group, &host,
-                                            nullptr));
+    Check(c.Decode(&host));
     for (int64_t n = 0; n < c.N; ++n)
       for (int64_t k = 0; k < c.K; ++k) kn[static_cast<size_t>(k * c.N + n)] = nk[static_cast<size_t>(n * c.K + k)];
     w->dense_t.Allocate(host.size_bytes);

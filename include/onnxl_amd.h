@@ -440,6 +440,38 @@ int onnxl_amd_dequantize_gptq(const char *format, const onnxl_amd_tensor *qweigh
                               const onnxl_amd_tensor *scales, const onnxl_amd_tensor *g_idx, int64_t K, int64_t N,
                               int64_t bits, int64_t group_size, onnxl_amd_tensor *y, void *stream);
 
+/* BitBLAS row-packed weights (the encoding "onnx_light.bitblas_weights.v1":
+ * ImportBitblasWeights / ExportBitblasWeights, quantization.h:664-670,
+ * decoded by ReconstructBitblasWeights, bitblas.cc:341-347, which goes through
+ * the GPTQ affine reconstruction, gptq.cc:222-228).  method "gptq" or "awq"
+ * (the originating quantizer), K = in_features (a multiple of 32), N =
+ * out_features (a multiple of 32 for gptq, 16 for awq), bits 2-8 (gptq: 2, 4
+ * or 8), group_size -1, K, 32, 64 or 128, symmetric (codes from symmetric
+ * GPTQ are stored signed and have no qzeros).  qweight INT8 [N, K * bits / 8]
+ * (row n: its K codes as a little-endian bit stream), scales FLOAT16
+ * [N, groups], qzeros INT8 [groups, N * bits / 8] (row g: N zero fields) or
+ * empty / null when symmetric GPTQ.  W[n, k] = (code - zero) * scale in fp32
+ * (exact: a code difference of at most 8 bits times an fp16 scale), the
+ * signed codes XOR the midpoint with the midpoint as zero.  The format's
+ * checks (Geometry, CheckTensor, CheckScales, bitblas.cc:38-106, 228-237)
+ * raise INVALID_ARGUMENT with the reference's messages.
+ *
+ * onnxl_amd_dequantize_bitblas decodes to y [N, K] as onnxl_amd_dequantize_awq
+ * does.  onnxl_amd_prepare_bitblas writes the fused operands as
+ * onnxl_amd_prepare_awq does (codes of at most 4 bits tiled UINT4, else UINT8
+ * [K, N]; zero points UINT4 / UINT8 [groups, N]; scales FLOAT16 [groups, N]);
+ * pass them to onnxl_amd_dequantize_linear_matmul with axis 0. */
+int onnxl_amd_dequantize_bitblas(const char *method, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *scales,
+                                 const onnxl_amd_tensor *qzeros, int64_t K, int64_t N, int64_t bits,
+                                 int64_t group_size, int32_t symmetric, onnxl_amd_tensor *y, void *stream);
+int onnxl_amd_prepare_bitblas_size(const char *method, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                                   int32_t symmetric, int64_t *weight_bytes, int64_t *scale_bytes,
+                                   int64_t *zero_point_bytes);
+int onnxl_amd_prepare_bitblas(const char *method, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *scales,
+                              const onnxl_amd_tensor *qzeros, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                              int32_t symmetric, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                              onnxl_amd_tensor *zero_point, void *stream);
+
 /* bitsandbytes weights (onnx_core/runtime/bitsandbytes.cc; the encoding
  * "onnx_light.bitsandbytes_weights.v1", imported by ImportBitsAndBytesWeights
  * and decoded by ReconstructBitsAndBytesWeights, bitsandbytes.cc:502-539,

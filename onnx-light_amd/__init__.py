@@ -112,6 +112,11 @@ def lib() -> ctypes.CDLL:
                                                      ctypes.c_void_p]
         L.onnxl_amd_bitsandbytes_matmul.argtypes = [TP, I32, I64, I64, I64, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_bitblas.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, I32, TP, ctypes.c_void_p]
+        L.onnxl_amd_prepare_bitblas_size.argtypes = [CS, I64, I64, I64, I64, I32, ctypes.POINTER(I64),
+                                                     ctypes.POINTER(I64), ctypes.POINTER(I64)]
+        L.onnxl_amd_prepare_bitblas.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, I32, PT, PT, PT,
+                                                ctypes.c_void_p]
         L.onnxl_amd_prepare_qqq_size.argtypes = [I64, I64, I64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)]
         L.onnxl_amd_prepare_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, I32, PT, PT, ctypes.c_void_p]
         L.onnxl_amd_dequantize_linear_matmul.argtypes = [TP, TP, TP, TP, ctypes.c_int64,
@@ -428,6 +433,31 @@ def bitsandbytes_matmul(a, w: BnbWeight, out=None):
                                                describe(w.weight, code), describe(w.scales), describe(out),
                                                _stream_of(a, w.weight, out)))
     return out
+
+
+def dequantize_bitblas(method: str, qweight, scales, qzeros, K: int, N: int, bits: int, group_size: int,
+                       symmetric: bool = False, output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_bitblas: a BitBLAS row-packed weight (bitblas.cc;
+    qweight int8 [N, K * bits / 8], scales float16 [N, groups], qzeros int8
+    [groups, N * bits / 8] or None for symmetric GPTQ) as [N, K] values."""
+    out = _decode_out(K, N, output_dtype, (qweight, scales), out)
+    _check(lib().onnxl_amd_dequantize_bitblas(method.encode(), describe(qweight), describe(scales), describe(qzeros),
+                                              K, N, bits, group_size, int(symmetric), describe(out),
+                                              _stream_of(qweight, scales, out)))
+    return out
+
+
+def prepare_bitblas(method: str, qweight, scales, qzeros, K: int, N: int, bits: int, group_size: int,
+                    symmetric: bool = False) -> PreparedNbits:
+    """onnxl_amd_prepare_bitblas: the fused kernels' UINT4 / UINT8 weight,
+    zero points and FLOAT16 scales (matmul_nbits multiplies with them)."""
+    sizes = [ctypes.c_int64(0) for _ in range(3)]
+    _check(lib().onnxl_amd_prepare_bitblas_size(method.encode(), K, N, bits, group_size, int(symmetric),
+                                                *(ctypes.byref(x) for x in sizes)))
+    w, s, z = _prepared_triplet(sizes, lambda pw, ps, pz, st: lib().onnxl_amd_prepare_bitblas(
+        method.encode(), describe(qweight), describe(scales), describe(qzeros), K, N, bits, group_size,
+        int(symmetric), pw, ps, pz, st))
+    return PreparedNbits(w, s, z, K, N)
 
 
 def dequantize_qqq(k: int, n: int, group_size: int, B, s_channel, s_group=None, output_dtype: int = FLOAT,

@@ -2245,6 +2245,78 @@ int PrepareGptq(const char *format, const onnxl_amd_tensor *qweight, const onnxl
 }
 
 // ---------------------------------------------------------------------------
+// BitBLAS row-packed weights (onnx_core/runtime/bitblas.cc): the geometry of
+// Geometry (:38-84) in the reference's order, CheckTensor (:101-106),
+// CheckScales (:228-237), then the GPTQ affine values the reference
+// reconstructs through (Affine, :251-290; gptq.cc:222-228): code (k, n) the
+// k-th `bits`-bit field of row n of qweight (XOR the midpoint for codes from
+// symmetric GPTQ, whose zero is the midpoint), zero (g, n) the n-th field of
+// qzeros row g, scale (g, n) = scales[n, g].
+
+CkptPlan PlanBitblas(const char *method, int64_t K, int64_t N, int64_t bits, int64_t group, int32_t symmetric,
+                     int32_t scale_type) {
+  const std::string m = method ? method : "";
+  OLA_ENFORCE(m == "gptq" || m == "awq", "BitBLAS requires an explicit GPTQ/AWQ originating method.");
+  OLA_ENFORCE(K > 0 && N > 0 && K % 32 == 0 && N % (m == "gptq" ? 32 : 16) == 0,
+              "BitBLAS row-packed checkpoint requires aligned, unpadded dimensions.");
+  OLA_ENFORCE(bits >= 2 && bits <= 8 && (m == "awq" || bits == 2 || bits == 4 || bits == 8),
+              "BitBLAS unsupported bit width for the originating method.");
+  OLA_ENFORCE(group == -1 || group == K || group == 32 || group == 64 || group == 128,
+              "BitBLAS unsupported group size.");
+  const int64_t eff = group == -1 ? K : group;
+  OLA_ENFORCE(K % eff == 0, "BitBLAS incomplete group.");
+  constexpr int64_t kLimit = int64_t(1) << 30;
+  OLA_ENFORCE(K <= kLimit / 4 / N, "BitBLAS logical FLOAT weights exceed max_bytes.");
+  OLA_ENFORCE(scale_type == kFloat16, "BitBLAS row-packed checkpoint reader requires FP16 scales.");
+  CkptPlan p;
+  p.fmt = "BitBLAS";
+  CkptLayout &L = p.L;
+  L.kind = kBitblas, L.K = K, L.N = N, L.bits = (int)bits, L.width = 1;
+  L.group = eff, L.groups = K / eff, L.padded = L.groups;
+  L.signed_codes = m == "gptq" && symmetric != 0;
+  p.word_type = p.zeros_type = kInt8;
+  p.scale_type = kFloat16;
+  p.qweight_shape = {N, K / 8 * bits};
+  p.scales_shape = {N, L.groups};
+  p.qzeros_shape = L.signed_codes ? Shape{0} : Shape{L.groups, N / 8 * bits};
+  const int64_t zb = L.signed_codes ? 0 : L.groups * (N / 8 * bits);
+  OLA_ENFORCE(N * (K / 8 * bits) + 2 * N * L.groups + zb <= kLimit, "BitBLAS checkpoint exceeds max_bytes.");
+  return p;
+}
+
+CkptPlan BitblasFromTensors(const char *method, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *scales,
+                            const onnxl_amd_tensor *qzeros, int64_t K, int64_t N, int64_t bits, int64_t group,
+                            int32_t symmetric) {
+  OLA_ENFORCE(!Absent(scales), "BitBLAS missing scales.");
+  CkptPlan p = PlanBitblas(method, K, N, bits, group, symmetric, scales->data_type);
+  auto check = [&](const onnxl_amd_tensor *t, int32_t type, const Shape &shape, const char *name) {
+    const int64_t bytes = NumElements(shape) * ElementSize(type);
+    const bool empty_ok = bytes == 0 && Absent(t);
+    OLA_ENFORCE(empty_ok || (!Absent(t) && t->data_type == type && ShapeOf(*t) == shape && t->size_bytes == bytes &&
+                             (bytes == 0 || t->data != nullptr)),
+                "BitBLAS invalid tensor type, shape or extent: ", name, ".");
+    if (!Absent(t)) CheckDescriptor(t, name);
+  };
+  check(qweight, kInt8, p.qweight_shape, "qweight");
+  check(scales, kFloat16, p.scales_shape, "scales");
+  check(qzeros, kInt8, p.qzeros_shape, "qzeros");
+  return p;
+}
+
+// CheckScales: every FP16 scale finite and positive (the stored [N, groups]
+// order); the zero fields read for the output-range scan.
+CkptHost CheckBitblasValues(CkptPlan &p, const onnxl_amd_tensor *qzeros, const onnxl_amd_tensor *scales) {
+  CkptHost h;
+  h.scales = ReadFloats(*scales);
+  for (float v : h.scales) OLA_ENFORCE(std::isfinite(v) && v > 0.f, "BitBLAS nonfinite or nonpositive scale.");
+  if (!p.L.signed_codes) {
+    h.qzeros.resize((size_t)NumElements(*qzeros));
+    ReadBytes(*qzeros, 0, h.qzeros.data(), h.qzeros.size());
+  }
+  return h;
+}
+
+// ---------------------------------------------------------------------------
 // bitsandbytes weights (onnx_core/runtime/bitsandbytes.cc): the geometry and
 // tensor checks of Geometry / CheckTensor (:222-258, :317-321) on the parsed
 // state, CheckParameters (:348-379), the reconstruction (:502-539) and the
@@ -2961,6 +3033,42 @@ int onnxl_amd_dequantize_gptq(const char *format, const onnxl_amd_tensor *qweigh
     CkptPlan p = GptqFromTensors(format, qweight, qzeros, scales, g_idx, K, N, bits, group_size);
     CkptHost h = CheckGptqValues(p, qweight, qzeros, scales, g_idx);
     return DecodeCkpt(p, h, qweight, qzeros, scales, g_idx, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_bitblas(const char *method, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *scales,
+                                 const onnxl_amd_tensor *qzeros, int64_t K, int64_t N, int64_t bits,
+                                 int64_t group_size, int32_t symmetric, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    CkptPlan p = BitblasFromTensors(method, qweight, scales, qzeros, K, N, bits, group_size, symmetric);
+    CkptHost h = CheckBitblasValues(p, qzeros, scales);
+    return DecodeCkpt(p, h, qweight, p.L.signed_codes ? nullptr : qzeros, scales, nullptr, y,
+                      static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_prepare_bitblas_size(const char *method, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                                   int32_t symmetric, int64_t *weight_bytes, int64_t *scale_bytes,
+                                   int64_t *zero_point_bytes) {
+  return Guard([&] {
+    OLA_ENFORCE(weight_bytes && scale_bytes && zero_point_bytes, "prepare_bitblas_size: null output");
+    const CkptSizes sz = CkptPreparedSizes(PlanBitblas(method, K, N, bits, group_size, symmetric, kFloat16));
+    *weight_bytes = sz.weight;
+    *scale_bytes = sz.scale;
+    *zero_point_bytes = sz.zp;
+    return ONNXL_AMD_OK;
+  });
+}
+
+int onnxl_amd_prepare_bitblas(const char *method, const onnxl_amd_tensor *qweight, const onnxl_amd_tensor *scales,
+                              const onnxl_amd_tensor *qzeros, int64_t K, int64_t N, int64_t bits, int64_t group_size,
+                              int32_t symmetric, onnxl_amd_tensor *weight, onnxl_amd_tensor *scale,
+                              onnxl_amd_tensor *zero_point, void *stream) {
+  return Guard([&] {
+    CkptPlan p = BitblasFromTensors(method, qweight, scales, qzeros, K, N, bits, group_size, symmetric);
+    CheckBitblasValues(p, qzeros, scales);
+    return PrepareCkpt("prepare_bitblas", p, qweight, p.L.signed_codes ? nullptr : qzeros, scales, weight, scale,
+                       zero_point, static_cast<hipStream_t>(stream));
   });
 }
 

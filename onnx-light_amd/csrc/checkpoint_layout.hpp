@@ -1,7 +1,8 @@
-// AWQ and GPTQ checkpoint layouts: where the code of weight (k, n) and the
-// zero point of (group, n) sit in the packed words
+// AWQ, GPTQ and BitBLAS checkpoint layouts: where the code of weight (k, n)
+// and the zero point of (group, n) sit in the packed words
 // (onnx_core/runtime/awq.cc:185-230 Code / Reconstructed,
-// onnx_core/runtime/gptq.cc:166-205 Pieces / Code / Zero).  The functions
+// onnx_core/runtime/gptq.cc:166-205 Pieces / Code / Zero,
+// onnx_core/runtime/bitblas.cc:239-290 Codes / Affine).  The functions
 // are __host__ __device__: the host runs them for the formats' value checks
 // on the few (group, column) pairs that need an exact scan, the preparation
 // and decode kernels for every code.  Words are little-endian on both sides.
@@ -18,15 +19,17 @@ enum CkptKind : int {
   kAwqGemv = 1,   // AWQ "gemv": qweight INT32 [N, K / 8]
   kAwqFast = 2,   // AWQ "gemv_fast" / "llm-awq": qweight INT16 [N / 4, K], float zero terms
   kGptq = 3,      // GPTQ "gptq", "gptq_v2", "gptq_p"
+  kBitblas = 4,   // BitBLAS "row-packed-v1": qweight INT8 [N, K * bits / 8], scales [N, groups]
 };
 
 struct CkptLayout {
   int kind, bits, width;   // width: bytes per packed word (GPTQ 1, 2, 4, 8)
   int planar;              // GPTQ: 32-code blocks split into 4-, 2- and 1-bit planes
   int zero_add;            // GPTQ "gptq" (v1): the stored zero field plus 1
+  int signed_codes;        // BitBLAS from symmetric GPTQ: codes XOR the midpoint, zero = the midpoint
   int64_t K, N, group;     // group: rows per group (K for group_size -1)
   int64_t groups;          // scale / zero rows
-  int64_t padded;          // AWQ gemv, gemv_fast: padded group count
+  int64_t padded;          // AWQ gemv, gemv_fast: padded group count; BitBLAS: groups
   int64_t zero_columns;    // GPTQ: words per qzeros row
   const uint8_t *qweight, *qzeros;
 };
@@ -86,9 +89,23 @@ __host__ __device__ inline uint32_t GptqField(const CkptLayout &L, const uint8_t
   return r;
 }
 
+// A BitBLAS field: `bits` bits from bit `index * bits` of a little-endian
+// byte stream (a code may span two bytes; bits <= 8).
+__host__ __device__ inline uint32_t BitblasField(const uint8_t *data, int64_t index, int bits) {
+  const int64_t bit = index * bits;
+  const int s = (int)(bit & 7);
+  uint32_t v = (uint32_t)data[bit >> 3] >> s;
+  if (s + bits > 8) v |= (uint32_t)data[(bit >> 3) + 1] << (8 - s);
+  return v & ((1u << bits) - 1);
+}
+
 // The code of weight row k, column n.
 __host__ __device__ inline uint32_t CkptCode(const CkptLayout &L, int64_t k, int64_t n) {
   switch (L.kind) {
+  case kBitblas: {  // row n of the [N, K] code matrix, K codes a row
+    const uint32_t c = BitblasField(L.qweight, n * L.K + k, L.bits);
+    return L.signed_codes ? c ^ (1u << (L.bits - 1)) : c;
+  }
   case kAwqGemm:
     if (L.bits == 4)
       return (uint32_t)(CkptWord(L.qweight, k * (L.N / 8) + n / 8, 4) >> (4 * AwqNibble(n))) & 15u;
@@ -120,6 +137,8 @@ __host__ __device__ inline uint32_t CkptZero(const CkptLayout &L, int64_t g, int
     return (uint32_t)(CkptWord(L.qzeros, n * (L.padded / 8) + g / 8, 4) >> (4 * (g % 8))) & 15u;
   case kAwqFast:
     return 0;
+  case kBitblas:  // qzeros [groups, N * bits / 8]: N codes a group row
+    return L.signed_codes ? 1u << (L.bits - 1) : BitblasField(L.qzeros, g * L.N + n, L.bits);
   default:
     return GptqField(L, L.qzeros, n, g, true) + (uint32_t)L.zero_add;
   }
@@ -127,7 +146,7 @@ __host__ __device__ inline uint32_t CkptZero(const CkptLayout &L, int64_t g, int
 
 // Index of the scale (and AWQ fast zero term) of (group g, column n).
 __host__ __device__ inline int64_t CkptScaleIndex(const CkptLayout &L, int64_t g, int64_t n) {
-  return L.kind == kAwqGemv ? n * L.padded + g : g * L.N + n;
+  return L.kind == kAwqGemv || L.kind == kBitblas ? n * L.padded + g : g * L.N + n;
 }
 
 }  // namespace onnxl_amd

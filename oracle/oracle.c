@@ -1880,3 +1880,54 @@ int orc_qqq_reconstruct(int64_t k, int64_t n, int64_t group, const uint8_t *word
     }
   return rc;
 }
+
+/* ---- BitBLAS row-packed weights, onnx_core/runtime/bitblas.cc --------------
+ * TEST INFRASTRUCTURE.  Codes (:239-249): row n of qweight INT8 [n, k * bits
+ * / 8] holds its k codes as one little-endian bit stream
+ * (UnpackQuantizationCodes, compressed_tensor_packing.cc:58-74, masked to
+ * the raw unsigned field); Affine (:251-290): codes from symmetric GPTQ
+ * XOR the midpoint 2^(bits-1) with zero = the midpoint, otherwise zero (g, n)
+ * is field n of qzeros row g; scale (g, n) = scales[n, g] (FP16); the value
+ * is GPTQ's (float(code) - float(zero)) * scale (gptq.cc:222-228; exact in
+ * fp32 here).  Returns 1 for a scale not finite or not positive (CheckScales,
+ * :228-237: "BitBLAS nonfinite or nonpositive scale."), 4 when a value does
+ * not fit out_dtype (WriteFloat), else 0; values [n, k] as in
+ * orc_qqq_reconstruct; raw codes [n, k] when `codes` is not NULL. */
+static uint32_t bitblas_field(const uint8_t *data, int64_t index, int bits) {
+  const int64_t bit = index * bits;
+  uint32_t v = (uint32_t)data[bit / 8] >> (bit % 8);
+  if (bit % 8 + bits > 8) v |= (uint32_t)data[bit / 8 + 1] << (8 - bit % 8);
+  return v & ((1u << bits) - 1);
+}
+
+int orc_bitblas_reconstruct(int64_t k, int64_t n, int64_t group, int bits, int signed_codes, const uint8_t *qweight,
+                            const uint16_t *scales, const uint8_t *qzeros, int out_dtype, void *out, uint8_t *codes) {
+  const int64_t eff = group == -1 ? k : group, groups = k / eff;
+  for (int64_t i = 0; i < n * groups; ++i) {
+    const float s = orc_f16_to_f32(scales[i]);
+    if (!isfinite(s) || !(s > 0)) return 1;
+  }
+  const uint32_t mid = 1u << (bits - 1);
+  int rc = 0;
+  for (int64_t c = 0; c < n; ++c)
+    for (int64_t r = 0; r < k; ++r) {
+      const uint32_t raw = bitblas_field(qweight, c * k + r, bits);
+      if (codes) codes[c * k + r] = (uint8_t)raw;
+      const int64_t g = r / eff;
+      const uint32_t code = signed_codes ? raw ^ mid : raw;
+      const uint32_t zero = signed_codes ? mid : bitblas_field(qzeros, g * n + c, bits);
+      const float v = ((float)code - (float)zero) * orc_f16_to_f32(scales[c * groups + g]);
+      const int64_t e = c * k + r;
+      if (out_dtype == 1) {
+        ((float *)out)[e] = v;
+      } else if (out_dtype == 11) {
+        ((double *)out)[e] = (double)v;
+      } else {
+        const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+        const int inf = out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u;
+        if (inf && rc == 0) rc = 4;
+        ((uint16_t *)out)[e] = h;
+      }
+    }
+  return rc;
+}

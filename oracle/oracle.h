@@ -224,6 +224,10 @@ int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, i
                         const uint8_t *codes, const void *absmax, const float *nested_absmax,
                         const float *nested_map, int out_dtype, void *out);
 
+/* BitBLAS row-packed weights: raw codes [n, k] and the GPTQ affine values. */
+int orc_bitblas_reconstruct(int64_t k, int64_t n, int64_t group, int bits, int signed_codes, const uint8_t *qweight,
+                            const uint16_t *scales, const uint8_t *qzeros, int out_dtype, void *out, uint8_t *codes);
+
 /* QQQ weights (four-bit, group -1 / 128): nibble position of (n, k) in the
  * packed words, storage index of a channel / group scale, and the
  * reconstruction with the format's checks. */

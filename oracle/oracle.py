@@ -126,6 +126,9 @@ def _declare(L):
     L.orc_bnb_check.restype = ctypes.c_int
     L.orc_bnb_check.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                 ctypes.c_float, P, P, P, P]
+    L.orc_bitblas_reconstruct.restype = ctypes.c_int
+    L.orc_bitblas_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                          P, P, P, ctypes.c_int, P, P]
     L.orc_qqq_position.restype = ctypes.c_int64
     L.orc_qqq_position.argtypes = [ctypes.c_int64] * 5
     L.orc_qqq_scale_position.restype = ctypes.c_int64
@@ -676,4 +679,25 @@ def qqq_reconstruct(k: int, n: int, group: int, words, s_channel, s_group, out_d
     out = np.zeros((n, k), dt)
     codes = np.zeros((n, k), np.uint8)
     rc = lib().orc_qqq_reconstruct(k, n, group, _ptr(w), _ptr(sc), _ptr(sg), out_dtype, _ptr(out), _ptr(codes))
+    return rc, out, codes
+
+
+# ---- BitBLAS row-packed weights ------------------------------------------------
+
+BITBLAS_ERRORS = {1: "BitBLAS nonfinite or nonpositive scale.", 4: "Dequantization output dtype overflow."}
+
+
+def bitblas_reconstruct(k: int, n: int, group: int, bits: int, signed_codes: bool, qweight, scales, qzeros=None,
+                        out_dtype: int = FLOAT):
+    """(rc, values [n, k], raw codes [n, k]) of a BitBLAS row-packed weight:
+    qweight int8 [n, k * bits / 8], scales float16 [n, groups], qzeros int8
+    [groups, n * bits / 8] (None for symmetric GPTQ codes)."""
+    qw = np.ascontiguousarray(qweight).view(np.uint8)
+    sc = np.ascontiguousarray(scales).view(np.uint16)
+    qz = np.zeros(1, np.uint8) if qzeros is None or np.size(qzeros) == 0 else np.ascontiguousarray(qzeros).view(np.uint8)
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((n, k), dt)
+    codes = np.zeros((n, k), np.uint8)
+    rc = lib().orc_bitblas_reconstruct(k, n, group, bits, int(signed_codes), _ptr(qw), _ptr(sc), _ptr(qz), out_dtype,
+                                       _ptr(out), _ptr(codes))
     return rc, out, codes

@@ -551,3 +551,46 @@ def test_qqq_validation(olamd):
     assert (w.value, s.value) == (4096 * 11008, 11008 * 4)
     assert L.onnxl_amd_prepare_qqq_size(4096, 11008, -1, 4, ctypes.byref(w), ctypes.byref(s)) == olamd.OK
     assert w.value == 4096 * 11008 // 2
+
+
+def test_bitblas_validation(olamd):
+    """BitBLAS's geometry and tensor checks and messages (onnx_core/runtime/
+    bitblas.cc:38-84 Geometry, :101-106 CheckTensor) on host payloads; valid
+    arguments stop at NOT_INITIALIZED.  CheckScales runs on the host copy of
+    the scales before any device work."""
+    L = olamd.lib()
+    d = olamd.describe
+    K, N = 64, 32
+    qw = np.zeros((N, K // 8 * 4), np.int8)
+    sc = np.ones((N, 2), np.float16)
+    qz = np.zeros((2, N // 8 * 4), np.int8)
+
+    def run(method="gptq", qw=qw, sc=sc, qz=qz, K=K, N=N, bits=4, group=32, sym=0, y=None):
+        y = np.zeros((N, K), np.float32) if y is None else y
+        rc = L.onnxl_amd_dequantize_bitblas(method.encode(), d(qw), d(sc), d(qz), K, N, bits, group, sym, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    dims = "BitBLAS row-packed checkpoint requires aligned, unpadded dimensions."
+    for kw, msg in ((dict(sc=None), "BitBLAS missing scales."),
+                    (dict(method="marlin"), "BitBLAS requires an explicit GPTQ/AWQ originating method."),
+                    (dict(K=48), dims), (dict(N=16), dims), (dict(N=0), dims),
+                    (dict(bits=3), "BitBLAS unsupported bit width for the originating method."),
+                    (dict(bits=9, method="awq"), "BitBLAS unsupported bit width for the originating method."),
+                    (dict(group=16), "BitBLAS unsupported group size."),
+                    (dict(K=96, group=64), "BitBLAS incomplete group."),
+                    (dict(sc=sc.astype(np.float32)), "BitBLAS row-packed checkpoint reader requires FP16 scales."),
+                    (dict(qw=qw[:16]), "BitBLAS invalid tensor type, shape or extent: qweight."),
+                    (dict(sc=sc[:, :1]), "BitBLAS invalid tensor type, shape or extent: scales."),
+                    (dict(qz=None), "BitBLAS invalid tensor type, shape or extent: qzeros."),
+                    (dict(sym=1), "BitBLAS invalid tensor type, shape or extent: qzeros."),
+                    (dict(sc=np.zeros((N, 2), np.float16)), "BitBLAS nonfinite or nonpositive scale."),
+                    (dict(sc=-sc), "BitBLAS nonfinite or nonpositive scale.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    assert run()[0] == olamd.NOT_INITIALIZED
+    assert run(sym=1, qz=None)[0] == olamd.NOT_INITIALIZED  # symmetric GPTQ: no qzeros
+    assert run(method="awq", sym=1, N=16, qw=qw[:16], sc=sc[:16], qz=qz[:, :8])[0] == olamd.NOT_INITIALIZED
+    w, s, z = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    assert L.onnxl_amd_prepare_bitblas_size(b"awq", 4096, 11008, 6, 128, 0, ctypes.byref(w), ctypes.byref(s),
+                                            ctypes.byref(z)) == olamd.OK
+    assert (w.value, s.value, z.value) == (4096 * 11008, 32 * 11008 * 2, 32 * 11008)
