@@ -37,6 +37,7 @@
 //    ONNXL_AMD_UNSUPPORTED) run on the built-in kernel that was registered
 //    for the operator before this one; library errors become the reference's
 //    exception types (std::invalid_argument / std::runtime_error).
+#include "onnx_core/runtime/kernels/cast_helper.h"
 #include "onnx_core/runtime/kernels/kernel_context.h"
 #include "onnx_core/runtime/kernels/kernel_dispatch_table.h"
 #include "onnx_core/runtime/kernels/node_helpers.h"
@@ -1230,6 +1231,27 @@ private:
     return w;
   }
 
+  // FLOAT16 scales widened to FLOAT (exactly), once per weight: with BFLOAT16
+  // activations the fused node then runs DequantizeLinear in FLOAT and casts
+  // each weight to BFLOAT16, which is the reference's one rounding of the
+  // FLOAT value (Dequantize with dtype = BFLOAT16); a FLOAT16 DequantizeLinear
+  // output could not feed a BFLOAT16 MatMul.
+  static void WidenScales(DeviceTensor &scale) {
+    const size_t count = static_cast<size_t>(scale.desc.size_bytes / 2);
+    std::vector<uint16_t> h(count);
+    std::vector<float> f(count);
+    CheckHip(hipMemcpy(h.data(), scale.ptr, count * 2, hipMemcpyDeviceToHost), "hipMemcpy");
+    for (size_t i = 0; i < count; ++i) f[i] = rt::Float16BitsToFloat(h[i]);
+    void *wide = nullptr;
+    CheckHip(hipMalloc(&wide, count * 4 > 0 ? count * 4 : 16), "hipMalloc");
+    CheckHip(hipMemcpy(wide, f.data(), count * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    CheckHip(hipFree(scale.ptr), "hipFree");
+    scale.ptr = wide;
+    scale.desc.data = wide;
+    scale.desc.data_type = kFloat;
+    scale.desc.size_bytes = static_cast<int64_t>(count * 4);
+  }
+
   // A QQQ weight: the reference's checks in A's dtype once, then the fused
   // operands (tiled INT4 codes with 16 x channel scales, or INT8 integers with
   // the channel scales) for onnxl_amd_dequantize_linear_matmul; null when
@@ -1292,6 +1314,7 @@ private:
       Check(rc);
       Check(onnxl_amd_synchronize(nullptr));
       w->fused = true;
+      if (In(0, ctx).data_type == kBfloat16 && w->scale.desc.data_type == kFloat16) WidenScales(w->scale);
       return w;
     }
     // dense decode [N, K] in the activations' dtype (GPU, copied back), its

@@ -177,3 +177,27 @@ def test_prepared_matmul_one_hot_rows_all_k(olamd, oracle, dev, M, m, bits, sym)
         y = olamd.matmul_nbits(torch.from_numpy(a).to(dev, torch.float16), p)
         want = w_f[:, k0:k0 + M].T * coef[:, None]
         assert np.array_equal(tensor_bits(y), oracle.f32_to_f16_bits(want + np.float32(0.0))), (m, bits, k0)
+
+
+def test_prepared_fp16_scales_widened_for_bf16_activations(olamd, oracle, dev):
+    """With BFLOAT16 activations the adapter widens the prepared FLOAT16
+    scales to FLOAT and runs DequantizeLinear in FLOAT with a Cast to
+    BFLOAT16: every weight is then the reference's BFLOAT16 rounding of the
+    FLOAT value (Dequantize with dtype = BFLOAT16), read back bit for bit
+    through one-hot rows."""
+    k, n, g, bits, M = 256, 64, 64, 4, 4
+    rng = np.random.default_rng(21)
+    qw, sc, qz = _random(rng, "gptq", k, n, bits, g, False)
+    p = olamd.prepare_bitblas("gptq", T(qw, dev), T(sc, dev), T(qz, dev), k, n, bits, g)
+    wide = p.scale.storage[: p.scale.desc.size_bytes].view(torch.float16).float().contiguous()
+    rc, w_bits, _ = oracle.bitblas_reconstruct(k, n, g, bits, False, qw, sc, qz, out_dtype=16)
+    assert rc == 0
+    w_f = oracle.bf16_bits_to_f32(w_bits)
+    coef = np.where(np.arange(M) % 2 == 0, 1.0, -2.0).astype(np.float32)
+    for k0 in range(0, k, M):
+        a = np.zeros((M, k), np.float32)
+        a[np.arange(M), k0 + np.arange(M)] = coef
+        y = olamd.dequantize_linear_matmul(torch.from_numpy(a).to(dev, torch.bfloat16), p.weight,
+                                           wide.view(k // g, n), p.zero_point, 0, 16, x_shape=(k, n))
+        want = (w_f[:, k0:k0 + M].T * coef[:, None]).astype(np.float32) + np.float32(0.0)
+        assert np.array_equal(tensor_bits(y), (want.view(np.uint32) >> 16).astype(np.uint16)), k0
