@@ -14,8 +14,9 @@
 //    (MatMulInteger, QLinearMatMul, DequantizeLinear, MatMul, QuantizeLinear,
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
-//    ai.rt:Dequantize on AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ encoded
-//    weights), and for the fused nodes the GPU patterns produce
+//    ai.rt:Dequantize on AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ /
+//    GPTQModel FP8 encoded weights), and for the fused nodes the GPU
+//    patterns produce
 //    (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
 //    an encoded weight, ai.rt.amd:DequantizeLinearGroupedMatMul on quantized
@@ -827,6 +828,40 @@ bool ExportBitsAndBytes(const rt::RuntimeValue &value, const Catalogue &catalogu
   return true;
 }
 
+// GPTQModel FP8 weights carried as encoded values (struct type
+// "onnx_light.gptqmodel_fp8_weights.v1"): the FP8 codes and inverse scales
+// from the reference's exporter (ExportGptqModelFp8Weights,
+// quantization.h:607), which validates the encoding, its schema and the
+// inverse-scale semantics.
+struct GptqFp8Checkpoint {
+  int64_t k = 0, n = 0;
+  std::string method;
+  std::vector<int64_t> block;
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  int Decode(onnxl_amd_tensor *y) const {
+    const onnxl_amd_tensor w = Describe(&tensors.at("weight")), s = Describe(&tensors.at("weight_scale_inv"));
+    return onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.c_str(), block.empty() ? nullptr : block.data(),
+                                              static_cast<int32_t>(block.size()), &w, &s, y, nullptr);
+  }
+};
+
+// False when the encoded value is not a GPTQModel FP8 weight.
+template <typename Catalogue>
+bool ExportGptqFp8(const rt::RuntimeValue &value, const Catalogue &catalogue, GptqFp8Checkpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  if (catalogue.Resolve(enc.struct_type()).name().value() != "onnx_light.gptqmodel_fp8_weights.v1") return false;
+  rt::GptqModelFp8Weights w = rt::ExportGptqModelFp8Weights(enc, size_t{1} << 30, catalogue);
+  out.k = w.in_features;
+  out.n = w.out_features;
+  out.method = w.weight_scale_method;
+  out.block.assign(w.weight_block_size.begin(), w.weight_block_size.end());
+  out.tensors = std::move(w.tensors);
+  return true;
+}
+
 // QQQ weights carried as encoded values (struct type
 // "onnx_light.qqq_weights.v1").  The native tensors (B, s_channel, s_group)
 // and numbers come from the reference's exporter (ExportQqqWeights,
@@ -858,9 +893,10 @@ bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqChe
 }
 
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
-// kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes and QQQ
-// encodings decode on the GPU to [out_features, in_features] of dtype
-// (onnxl_amd_dequantize_awq / _gptq / _bitblas / _bitsandbytes / _qqq); every other
+// kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes, QQQ and
+// GPTQModel FP8 encodings decode on the GPU to [out_features, in_features]
+// of dtype (onnxl_amd_dequantize_awq / _gptq / _bitblas / _bitsandbytes /
+// _qqq / _gptqmodel_fp8); every other
 // encoding, and values that reference shared parameters, run on the built-in
 // kernel.
 class Mi355xDequantize : public Mi355xKernel {
@@ -889,6 +925,15 @@ public:
         rt::SetOutput(node, 0, std::move(y), ctx);
       return;
     }
+    GptqFp8Checkpoint f;
+    if (value != ctx.values().end() && ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {
+      const rt::Shape shape{f.n, f.k};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      if (Call(f.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     QqqCheckpoint q;
     if (value != ctx.values().end() && ExportQqq(value->second, ctx.struct_type_catalogue(), q)) {
       const rt::Shape shape{q.n, q.k};
@@ -902,7 +947,7 @@ public:
     }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1293,6 +1338,12 @@ private:
       auto w = PrepareQqq(ctx, q);
       return w ? w : DenseOther(ctx, value->second);
     }
+    GptqFp8Checkpoint f;
+    if (ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {  // a division per weight: dense
+      auto w = std::make_shared<Prepared>();
+      DenseFromDevice(In(0, ctx), f.n, f.k, [&](onnxl_amd_tensor *y) { return f.Decode(y); }, *w);
+      return w;
+    }
     Checkpoint c;
     if (!ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) return DenseOther(ctx, value->second);
     auto w = std::make_shared<Prepared>();
@@ -1317,30 +1368,35 @@ private:
       if (In(0, ctx).data_type == kBfloat16 && w->scale.desc.data_type == kFloat16) WidenScales(w->scale);
       return w;
     }
-    // dense decode [N, K] in the activations' dtype (GPU, copied back), its
-    // transpose [K, N] on the host, then one upload; once per weight
-    const onnxl_amd_tensor a = In(0, ctx);
-    const size_t count = static_cast<size_t>(c.N * c.K);
+    DenseFromDevice(In(0, ctx), c.N, c.K, [&](onnxl_amd_tensor *y) { return c.Decode(y); }, *w);
+    return w;
+  }
+
+  // A weight [N, K] decoded on the GPU in the activations' dtype by `decode`
+  // (copied back), transposed to [K, N] on the host and uploaded; once per
+  // weight.
+  template <typename Decode>
+  static void DenseFromDevice(const onnxl_amd_tensor &a, int64_t N, int64_t K, Decode &&decode, Prepared &w) {
+    const size_t count = static_cast<size_t>(N * K);
     std::vector<uint16_t> nk(count), kn(count);
     onnxl_amd_tensor host{};
     host.data_type = a.data_type;
     host.rank = 2;
-    host.dims[0] = c.N;
-    host.dims[1] = c.K;
+    host.dims[0] = N;
+    host.dims[1] = K;
     host.data = nk.data();
     host.size_bytes = static_cast<int64_t>(count * 2);
     host.location = ONNXL_AMD_HOST;
-    Check(c.Decode(&host));
-    for (int64_t n = 0; n < c.N; ++n)
-      for (int64_t k = 0; k < c.K; ++k) kn[static_cast<size_t>(k * c.N + n)] = nk[static_cast<size_t>(n * c.K + k)];
-    w->dense_t.Allocate(host.size_bytes);
-    CheckHip(hipMemcpy(w->dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
-    w->dense_t.desc = host;
-    w->dense_t.desc.dims[0] = c.K;
-    w->dense_t.desc.dims[1] = c.N;
-    w->dense_t.desc.data = w->dense_t.ptr;
-    w->dense_t.desc.location = ONNXL_AMD_DEVICE;
-    return w;
+    Check(decode(&host));
+    for (int64_t n = 0; n < N; ++n)
+      for (int64_t k = 0; k < K; ++k) kn[static_cast<size_t>(k * N + n)] = nk[static_cast<size_t>(n * K + k)];
+    w.dense_t.Allocate(host.size_bytes);
+    CheckHip(hipMemcpy(w.dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    w.dense_t.desc = host;
+    w.dense_t.desc.dims[0] = K;
+    w.dense_t.desc.dims[1] = N;
+    w.dense_t.desc.data = w.dense_t.ptr;
+    w.dense_t.desc.location = ONNXL_AMD_DEVICE;
   }
 
   // Any other encoding: the reference's decode in A's dtype (materializing a

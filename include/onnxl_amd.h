@@ -522,6 +522,25 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   int64_t block_size, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales,
                                   onnxl_amd_tensor *y, void *stream);
 
+/* GPTQModel FP8 weights (the encoding "onnx_light.gptqmodel_fp8_weights.v1"
+ * of ai.rt:Dequantize: ImportGptqModelFp8Weights / ExportGptqModelFp8Weights,
+ * quantization.h:603-612, decoded by ReconstructGptqModelFp8Weights,
+ * gptqmodel_fp8.cc:284-300, through DequantizeTensor).  weight [N, K] =
+ * [out_features, in_features] of FP8 codes whose data_type names the format
+ * (FLOAT8E4M3FN, FLOAT8E4M3FNUZ, FLOAT8E5M2, FLOAT8E5M2FNUZ or FLOAT8E8M0),
+ * weight_scale_inv FLOAT: [] for weight_scale_method "tensor", [N] for
+ * "row", [N / b0, K / b1] for "block" with weight_block_size {b0, b1}
+ * (block_rank 2; 0 otherwise).  Decodes to y [N, K] of y's dtype (FLOAT,
+ * FLOAT16, BFLOAT16 or DOUBLE): value = float(code) / inverse scale,
+ * correctly rounded (gptqmodel_fp8.cc:160-162), then WriteFloat's rounding.
+ * The reference's checks (Geometry, the import's tensor check, CheckData:
+ * :58-101, 246-254, 164-173) and WriteFloat's range check raise
+ * INVALID_ARGUMENT with its messages, in its order. */
+int onnxl_amd_dequantize_gptqmodel_fp8(int64_t in_features, int64_t out_features, const char *weight_scale_method,
+                                       const int64_t *weight_block_size, int32_t block_rank,
+                                       const onnxl_amd_tensor *weight, const onnxl_amd_tensor *weight_scale_inv,
+                                       onnxl_amd_tensor *y, void *stream);
+
 /* QQQ weights (the encoding "onnx_light.qqq_weights.v1" of ai.rt:Dequantize:
  * ImportQqqWeights / ExportQqqWeights, quantization.h, decoded by
  * ReconstructQqqWeights, qqq.cc:346-358, through DequantizeTensor).  The

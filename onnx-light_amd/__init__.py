@@ -112,6 +112,8 @@ def lib() -> ctypes.CDLL:
                                                      ctypes.c_void_p]
         L.onnxl_amd_bitsandbytes_matmul.argtypes = [TP, I32, I64, I64, I64, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
+        L.onnxl_amd_dequantize_gptqmodel_fp8.argtypes = [I64, I64, CS, ctypes.POINTER(I64), I32, TP, TP, TP,
+                                                         ctypes.c_void_p]
         L.onnxl_amd_dequantize_bitblas.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, I32, TP, ctypes.c_void_p]
         L.onnxl_amd_prepare_bitblas_size.argtypes = [CS, I64, I64, I64, I64, I32, ctypes.POINTER(I64),
                                                      ctypes.POINTER(I64), ctypes.POINTER(I64)]
@@ -432,6 +434,20 @@ def bitsandbytes_matmul(a, w: BnbWeight, out=None):
     _check(lib().onnxl_amd_bitsandbytes_matmul(describe(a), BNB_FORMATS[w.fmt], w.rows, w.cols, w.block,
                                                describe(w.weight, code), describe(w.scales), describe(out),
                                                _stream_of(a, w.weight, out)))
+    return out
+
+
+def dequantize_gptqmodel_fp8(weight, weight_scale_inv, method: str, block=(), code: int | None = None,
+                             output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_gptqmodel_fp8: FP8 codes [N, K] (`code` the FP8
+    data_type when `weight` holds raw uint8 bytes) over FLOAT inverse scales
+    (method "tensor", "row" or "block" with block (b0, b1)) as [N, K]."""
+    n, k = _shape_of(weight)
+    out = _decode_out(k, n, output_dtype, (weight, weight_scale_inv), out)
+    blk = (ctypes.c_int64 * 2)(*block) if block else None
+    _check(lib().onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.encode(), blk, len(block),
+                                                    describe(weight, code), describe(weight_scale_inv),
+                                                    describe(out), _stream_of(weight, weight_scale_inv, out)))
     return out
 
 

@@ -2583,6 +2583,78 @@ int BnbMatMul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t c
 }
 
 // ---------------------------------------------------------------------------
+// GPTQModel FP8 weights (onnx_core/runtime/gptqmodel_fp8.cc): Geometry
+// (:58-101) in the reference's order with DecodeValues' 1 << 30 byte limit,
+// the tensor check of ImportGptqModelFp8Weights (:246-254), CheckData
+// (:164-173) and the reconstruction (:160-162) on the device, WriteFloat's
+// output check.
+
+bool QqqDtype(int32_t dt);
+
+int DequantizeGptqFp8(int64_t k, int64_t n, const char *method_name, const int64_t *block, int32_t block_rank,
+                      const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scale, onnxl_amd_tensor *y,
+                      hipStream_t stream) {
+  constexpr int64_t kLimit = int64_t(1) << 30;
+  OLA_ENFORCE(k > 0 && n > 0, "GPTQModel FP8 requires nonempty [N,K] weights and positive max_bytes.");
+  OLA_ENFORCE(k <= kLimit / 4 / n, "GPTQModel FP8 logical FLOAT weights exceed max_bytes.");
+  OLA_ENFORCE(!Absent(weight) && (weight->data_type == kFloat8E4M3FN || weight->data_type == kFloat8E4M3FNUZ ||
+                                  weight->data_type == kFloat8E5M2 || weight->data_type == kFloat8E5M2FNUZ ||
+                                  weight->data_type == kFloat8E8M0),
+              "GPTQModel FP8 unsupported scalar format.");
+  const std::string method = method_name ? method_name : "";
+  OLA_ENFORCE(block_rank == 0 || (block_rank == 2 && block && block[0] > 0 && block[1] > 0),
+              "GPTQModel FP8 invalid weight_block_size.");
+  OLA_ENFORCE(method == "block" || block_rank == 0, "GPTQModel FP8 non-block scaling forbids weight_block_size.");
+  GptqFp8Params p{};
+  p.n = n, p.k = k, p.b0 = 1, p.b1 = 1;
+  Shape scale_shape;
+  if (method == "tensor") {
+    p.method = 0;
+  } else if (method == "row") {
+    p.method = 1;
+    scale_shape = {n};
+  } else {
+    OLA_ENFORCE(method == "block" && block_rank == 2 && n % block[0] == 0 && k % block[1] == 0,
+                "GPTQModel FP8 requires divisible two-axis blocks.");
+    p.method = 2;
+    p.b0 = block[0], p.b1 = block[1], p.scale_cols = k / block[1];
+    scale_shape = {n / block[0], k / block[1]};
+  }
+  const int64_t scales = NumElements(scale_shape);
+  OLA_ENFORCE(n * k <= kLimit && scales * 4 <= kLimit - n * k, "GPTQModel FP8 checkpoint exceeds max_bytes.");
+  OLA_ENFORCE(weight->rank == 2 && weight->dims[0] == n && weight->dims[1] == k && weight->size_bytes == n * k &&
+                  weight->data != nullptr && !Absent(scale) && scale->data_type == kFloat &&
+                  ShapeOf(*scale) == scale_shape && scale->size_bytes == scales * 4 && scale->data != nullptr,
+              "GPTQModel FP8 invalid tensor dtype, shape or byte extent.");
+  CheckDescriptor(weight, "weight");
+  CheckDescriptor(scale, "weight_scale_inv");
+  OLA_ENFORCE(y != nullptr && QqqDtype(y->data_type), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  CheckDescriptor(y, "y");
+  const int64_t width = y->data_type == kDouble ? 8 : (y->data_type == kFloat ? 4 : 2);
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == n && y->dims[1] == k && y->size_bytes == n * k * width &&
+                  y->data != nullptr,
+              "GPTQModel FP8: y must be [out_features, in_features] of its dtype.");
+  Ctx();
+  Staging st(stream, 256, {weight, scale}, {y});
+  p.codes = static_cast<const uint8_t *>(st.In(weight));
+  p.scales = static_cast<const float *>(st.In(scale));
+  p.flag = static_cast<unsigned *>(st.Extra());
+  hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, p.flag, (size_t)1);
+  LaunchGptqFp8Decode(p, weight->data_type, y->data_type, st.Out(y), stream);
+  OLA_HIP(hipGetLastError());
+  onnxl_amd_tensor fd{};
+  fd.data_type = kInt32, fd.rank = 1, fd.dims[0] = 1, fd.data = p.flag, fd.size_bytes = 4;
+  fd.location = ONNXL_AMD_DEVICE;
+  unsigned flag = 0;
+  ReadOnStream(stream, fd, &flag, 4);
+  OLA_ENFORCE(!(flag & kGptqFp8BadScale), "GPTQModel FP8 inverse scales must be finite and positive.");
+  OLA_ENFORCE(!(flag & kGptqFp8BadValue), "GPTQModel FP8 nonfinite weight or reconstruction.");
+  OLA_ENFORCE(!(flag & kGptqFp8BadOutput), "Dequantization output dtype overflow.");
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // QQQ weights (onnx_core/runtime/qqq.cc): the geometry and tensor checks of
 // Geometry / CheckTensor (:38-56, :136-141) with limit 1 << 30 (DecodeValues,
 // quantization.cc:2002-2008), CheckData (:204-218) and the reconstruction
@@ -3170,6 +3242,16 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return BnbMatMul(a, format, rows, cols, block_size, weight, scales, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_gptqmodel_fp8(int64_t in_features, int64_t out_features, const char *weight_scale_method,
+                                       const int64_t *weight_block_size, int32_t block_rank,
+                                       const onnxl_amd_tensor *weight, const onnxl_amd_tensor *weight_scale_inv,
+                                       onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeGptqFp8(in_features, out_features, weight_scale_method, weight_block_size, block_rank, weight,
+                             weight_scale_inv, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -195,6 +195,22 @@ struct BnbParams {
 };
 void LaunchBnbScales(const BnbParams &p, hipStream_t s);
 
+// GPTQModel FP8 weights (gptqmodel_fp8.hip): flag bits in the reference's order.
+constexpr unsigned kGptqFp8BadScale = 1;   // an inverse scale not finite or not positive
+constexpr unsigned kGptqFp8BadValue = 2;   // a value not finite in fp32
+constexpr unsigned kGptqFp8BadOutput = 4;  // a value past the output dtype's range
+struct GptqFp8Params {
+  int64_t n, k;              // out_features, in_features
+  int method;                // 0 tensor, 1 row, 2 block
+  int64_t b0, b1, scale_cols;  // block rows / columns, scale columns (block)
+  const uint8_t *codes;      // [n, k]
+  const float *scales;       // weight_scale_inv
+  unsigned *flag;
+};
+// code_dtype: one of the five FP8 types; out_dtype kFloat, kFloat16,
+// kBfloat16 or kDouble; y [n, k] or null (the checks alone)
+void LaunchGptqFp8Decode(const GptqFp8Params &p, int code_dtype, int out_dtype, void *y, hipStream_t s);
+
 // QQQ weights (qqq.hip): flag bits of a decode / preparation, in the order
 // the reference raises them.
 constexpr unsigned kQqqBadChannel = 1;   // a channel scale not finite or negative

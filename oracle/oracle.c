@@ -1931,3 +1931,53 @@ int orc_bitblas_reconstruct(int64_t k, int64_t n, int64_t group, int bits, int s
     }
   return rc;
 }
+
+/* ---- GPTQModel FP8 weights, onnx_core/runtime/gptqmodel_fp8.cc -----------
+ * TEST INFRASTRUCTURE.  Reconstructed (:160-162): float(code) / the inverse
+ * scale of the element's tensor / row / (b0 x b1) block (ScaleIndex,
+ * :94-103), one IEEE division.  CheckData (:164-173) returns 1 for a scale
+ * not finite or not positive, 2 for a value not finite; 4 when a value does
+ * not fit out_dtype (WriteFloat); else 0.  E8M0 as cast_float8.cc:451-461:
+ * 2^(bits - 127), 0 is 2^-127, 0xFF the quiet NaN. */
+float orc_f8e8m0_to_f32(uint8_t v) {
+  uint32_t u = v == 0 ? 0x00400000u : (v == 0xFF ? 0x7FC00000u : (uint32_t)v << 23);
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float gptq_fp8_decode(uint8_t c, int type) {
+  switch (type) {
+  case 17: return orc_f8e4m3fn_to_f32(c);
+  case 18: return orc_f8e4m3fnuz_to_f32(c);
+  case 19: return orc_f8e5m2_to_f32(c);
+  case 20: return orc_f8e5m2fnuz_to_f32(c);
+  default: return orc_f8e8m0_to_f32(c);
+  }
+}
+
+int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, int64_t b0, int64_t b1,
+                             const uint8_t *codes, const float *scales, int out_dtype, void *out) {
+  const int64_t cols = method == 2 ? k / b1 : 0;
+  const int64_t count = method == 0 ? 1 : (method == 1 ? n : (n / b0) * cols);
+  for (int64_t i = 0; i < count; ++i)
+    if (!isfinite(scales[i]) || !(scales[i] > 0)) return 1;
+  int rc = 0;
+  for (int64_t i = 0; i < n * k; ++i) {
+    const int64_t r = i / k, c = i % k;
+    const int64_t si = method == 0 ? 0 : (method == 1 ? r : (r / b0) * cols + c / b1);
+    volatile float v = gptq_fp8_decode(codes[i], code_type) / scales[si];
+    if (!isfinite(v)) return 2;
+    if (out_dtype == 1) {
+      ((float *)out)[i] = v;
+    } else if (out_dtype == 11) {
+      ((double *)out)[i] = (double)v;
+    } else {
+      const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+      const int inf = out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u;
+      if (inf && rc == 0) rc = 4;
+      ((uint16_t *)out)[i] = h;
+    }
+  }
+  return rc;
+}

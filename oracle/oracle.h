@@ -224,6 +224,12 @@ int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, i
                         const uint8_t *codes, const void *absmax, const float *nested_absmax,
                         const float *nested_map, int out_dtype, void *out);
 
+/* GPTQModel FP8 weights: code_type one of the five FP8 data types; method 0
+ * tensor, 1 row, 2 block (b0 x b1); values [n, k]. */
+float orc_f8e8m0_to_f32(uint8_t v);
+int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, int64_t b0, int64_t b1,
+                             const uint8_t *codes, const float *scales, int out_dtype, void *out);
+
 /* BitBLAS row-packed weights: raw codes [n, k] and the GPTQ affine values. */
 int orc_bitblas_reconstruct(int64_t k, int64_t n, int64_t group, int bits, int signed_codes, const uint8_t *qweight,
                             const uint16_t *scales, const uint8_t *qzeros, int out_dtype, void *out, uint8_t *codes);

@@ -126,6 +126,11 @@ def _declare(L):
     L.orc_bnb_check.restype = ctypes.c_int
     L.orc_bnb_check.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                 ctypes.c_float, P, P, P, P]
+    L.orc_f8e8m0_to_f32.restype = ctypes.c_float
+    L.orc_f8e8m0_to_f32.argtypes = [ctypes.c_uint8]
+    L.orc_gptq_fp8_reconstruct.restype = ctypes.c_int
+    L.orc_gptq_fp8_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int64, ctypes.c_int64, P, P, ctypes.c_int, P]
     L.orc_bitblas_reconstruct.restype = ctypes.c_int
     L.orc_bitblas_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                           P, P, P, ctypes.c_int, P, P]
@@ -701,3 +706,22 @@ def bitblas_reconstruct(k: int, n: int, group: int, bits: int, signed_codes: boo
     rc = lib().orc_bitblas_reconstruct(k, n, group, bits, int(signed_codes), _ptr(qw), _ptr(sc), _ptr(qz), out_dtype,
                                        _ptr(out), _ptr(codes))
     return rc, out, codes
+
+
+# ---- GPTQModel FP8 weights -------------------------------------------------------
+
+GPTQ_FP8_METHODS = {"tensor": 0, "row": 1, "block": 2}
+GPTQ_FP8_ERRORS = {1: "GPTQModel FP8 inverse scales must be finite and positive.",
+                   2: "GPTQModel FP8 nonfinite weight or reconstruction.", 4: "Dequantization output dtype overflow."}
+
+
+def gptq_fp8_reconstruct(codes, code_type: int, scales, method: str, block=(1, 1), out_dtype: int = FLOAT):
+    """(rc, values [n, k]) of FP8 codes [n, k] over FLOAT inverse scales."""
+    c = np.ascontiguousarray(codes).view(np.uint8)
+    n, k = c.shape
+    s = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((n, k), dt)
+    rc = lib().orc_gptq_fp8_reconstruct(n, k, code_type, GPTQ_FP8_METHODS[method], block[0], block[1], _ptr(c),
+                                        _ptr(s), out_dtype, _ptr(out))
+    return rc, out

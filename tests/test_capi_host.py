@@ -594,3 +594,40 @@ def test_bitblas_validation(olamd):
     assert L.onnxl_amd_prepare_bitblas_size(b"awq", 4096, 11008, 6, 128, 0, ctypes.byref(w), ctypes.byref(s),
                                             ctypes.byref(z)) == olamd.OK
     assert (w.value, s.value, z.value) == (4096 * 11008, 32 * 11008 * 2, 32 * 11008)
+
+
+def test_gptqmodel_fp8_validation(olamd):
+    """GPTQModel FP8's geometry and tensor checks and messages
+    (onnx_core/runtime/gptqmodel_fp8.cc:58-101 Geometry, :246-254 the
+    import's tensor check) on host payloads; valid arguments stop at
+    NOT_INITIALIZED."""
+    L = olamd.lib()
+    d = olamd.describe
+    w = np.zeros((4, 8), np.uint8)
+    s = np.ones(4, np.float32)
+
+    def run(method="row", block=(), w=w, s=s, code=17, n=4, k=8, y=None):
+        y = np.zeros((n, k), np.float32) if y is None else y
+        blk = (ctypes.c_int64 * 2)(*block) if block else None
+        rc = L.onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.encode(), blk, len(block), d(w, code), d(s), d(y),
+                                                  None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(n=0), "GPTQModel FP8 requires nonempty [N,K] weights and positive max_bytes."),
+                    (dict(n=1 << 14, k=1 << 15), "GPTQModel FP8 logical FLOAT weights exceed max_bytes."),
+                    (dict(code=3), "GPTQModel FP8 unsupported scalar format."),
+                    (dict(method="block", block=(0, 2)), "GPTQModel FP8 invalid weight_block_size."),
+                    (dict(block=(2, 2)), "GPTQModel FP8 non-block scaling forbids weight_block_size."),
+                    (dict(method="block", block=(3, 2)), "GPTQModel FP8 requires divisible two-axis blocks."),
+                    (dict(method="channel"), "GPTQModel FP8 requires divisible two-axis blocks."),
+                    (dict(s=s[:3]), "GPTQModel FP8 invalid tensor dtype, shape or byte extent."),
+                    (dict(method="tensor"), "GPTQModel FP8 invalid tensor dtype, shape or byte extent."),
+                    (dict(w=w[:2]), "GPTQModel FP8 invalid tensor dtype, shape or byte extent."),
+                    (dict(y=np.zeros((4, 8), np.int8)), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    assert run()[0] == olamd.NOT_INITIALIZED
+    assert run(method="tensor", s=np.ones((), np.float32))[0] == olamd.NOT_INITIALIZED
+    assert run(method="block", block=(2, 4), s=np.ones((2, 2), np.float32))[0] == olamd.NOT_INITIALIZED
+    for code in (18, 19, 20, 24):
+        assert run(code=code)[0] == olamd.NOT_INITIALIZED
