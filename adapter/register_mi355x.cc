@@ -15,7 +15,7 @@
 //    DynamicQuantizeLinear, ConvInteger, QLinearConv, Cast, DequantizePacked,
 //    GroupedMatMul, com.microsoft:MatMulNBits on ORT-packed weights, and
 //    ai.rt:Dequantize on AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ /
-//    GPTQModel FP8 encoded weights), and for the fused nodes the GPU
+//    GPTQModel FP8 / VPTQ encoded weights), and for the fused nodes the GPU
 //    patterns produce
 //    (ai.rt.amd:DequantizeLinearMatMul,
 //    ai.rt.amd:DequantizePackedMatMul, ai.rt.amd:DequantizeEncodedMatMul on
@@ -828,6 +828,54 @@ bool ExportBitsAndBytes(const rt::RuntimeValue &value, const Catalogue &catalogu
   return true;
 }
 
+// VPTQ weights carried as encoded values (struct type
+// "onnx_light.vptq_weights.v1"): the constructor metadata and native tensors
+// from the reference's exporter (ExportVptqWeights, quantization.h:901),
+// which validates the encoding and its canonical schema.
+struct VptqCheckpoint {
+  onnxl_amd_vptq_config config{};
+  int32_t dtype = 0;
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  int Decode(onnxl_amd_tensor *y) const {
+    auto t = [&](const char *name) {
+      auto it = tensors.find(name);
+      return it == tensors.end() ? Absent() : Describe(&it->second);
+    };
+    const onnxl_amd_tensor ix = t("indices"), c = t("centroids.weight"), rc = t("res_centroids.weight");
+    const onnxl_amd_tensor oc = t("outlier_centroids.weight"), oi = t("outlier_indices");
+    const onnxl_amd_tensor sc = t("weight_scale"), bi = t("weight_bias"), pm = t("perm");
+    return onnxl_amd_dequantize_vptq(&config, &ix, &c, &rc, &oc, &oi, &sc, &bi, &pm, y, nullptr);
+  }
+};
+
+// False when the encoded value is not a VPTQ weight.
+template <typename Catalogue>
+bool ExportVptq(const rt::RuntimeValue &value, const Catalogue &catalogue, VptqCheckpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  if (catalogue.Resolve(enc.struct_type()).name().value() != "onnx_light.vptq_weights.v1") return false;
+  rt::VptqWeights w = rt::ExportVptqWeights(enc, size_t{1} << 30, catalogue);
+  onnxl_amd_vptq_config &c = out.config;
+  c.in_features = w.in_features;
+  c.out_features = w.out_features;
+  c.bits = w.bits;
+  for (int i = 0; i < 2; ++i) {
+    c.vector_lens[i] = w.vector_lens[i];
+    c.num_centroids[i] = w.num_centroids[i];
+    c.num_res_centroids[i] = w.num_res_centroids[i];
+  }
+  c.npercent = w.npercent;
+  c.group_size = w.group_size;
+  c.group_num = w.group_num;
+  c.enable_norm = w.enable_norm ? 1 : 0;
+  c.norm_dim = static_cast<int32_t>(w.norm_dim);
+  c.enable_perm = w.enable_perm ? 1 : 0;
+  out.tensors = std::move(w.tensors);
+  return true;
+}
+
 // GPTQModel FP8 weights carried as encoded values (struct type
 // "onnx_light.gptqmodel_fp8_weights.v1"): the FP8 codes and inverse scales
 // from the reference's exporter (ExportGptqModelFp8Weights,
@@ -893,10 +941,10 @@ bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqChe
 }
 
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
-// kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes, QQQ and
-// GPTQModel FP8 encodings decode on the GPU to [out_features, in_features]
-// of dtype (onnxl_amd_dequantize_awq / _gptq / _bitblas / _bitsandbytes /
-// _qqq / _gptqmodel_fp8); every other
+// kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes, QQQ,
+// GPTQModel FP8 and VPTQ encodings decode on the GPU to [out_features,
+// in_features] of dtype (onnxl_amd_dequantize_awq / _gptq / _bitblas /
+// _bitsandbytes / _qqq / _gptqmodel_fp8 / _vptq); every other
 // encoding, and values that reference shared parameters, run on the built-in
 // kernel.
 class Mi355xDequantize : public Mi355xKernel {
@@ -925,6 +973,15 @@ public:
         rt::SetOutput(node, 0, std::move(y), ctx);
       return;
     }
+    VptqCheckpoint v;
+    if (value != ctx.values().end() && ExportVptq(value->second, ctx.struct_type_catalogue(), v)) {
+      const rt::Shape shape{v.config.out_features, v.config.in_features};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      if (Call(v.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     GptqFp8Checkpoint f;
     if (value != ctx.values().end() && ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {
       const rt::Shape shape{f.n, f.k};
@@ -947,7 +1004,7 @@ public:
     }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8 / VPTQ");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1337,6 +1394,13 @@ private:
     if (ExportQqq(value->second, ctx.struct_type_catalogue(), q)) {
       auto w = PrepareQqq(ctx, q);
       return w ? w : DenseOther(ctx, value->second);
+    }
+    VptqCheckpoint v;
+    if (ExportVptq(value->second, ctx.struct_type_catalogue(), v)) {  // codebook lookups: dense
+      auto w = std::make_shared<Prepared>();
+      DenseFromDevice(In(0, ctx), v.config.out_features, v.config.in_features,
+                      [&](onnxl_amd_tensor *y) { return v.Decode(y); }, *w);
+      return w;
     }
     GptqFp8Checkpoint f;
     if (ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {  // a division per weight: dense

@@ -522,6 +522,37 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   int64_t block_size, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scales,
                                   onnxl_amd_tensor *y, void *stream);
 
+/* VPTQ weights (the encoding "onnx_light.vptq_weights.v1" of ai.rt:Dequantize:
+ * ImportVptqWeights / ExportVptqWeights, quantization.h:898-902, decoded by
+ * ReconstructVptqWeights, vptq.cc:401-443, through DequantizeTensor).  The
+ * constructor metadata the layout depends on (VptqWeights,
+ * quantization.h:884-895; index 0 of the pairs is the outlier codebook's,
+ * 1 the main one's): */
+typedef struct onnxl_amd_vptq_config {
+  int64_t in_features, out_features, bits;
+  int64_t vector_lens[2], num_centroids[2], num_res_centroids[2];
+  double npercent;
+  int64_t group_size, group_num;
+  int32_t enable_norm, norm_dim, enable_perm;
+} onnxl_amd_vptq_config;
+/* Tensors (the checkpoint's names): indices INT32 [groups, vectors, words],
+ * centroids ("centroids.weight") of the codebook dtype (FLOAT, FLOAT16 or
+ * BFLOAT16) [groups, num_centroids[1] * vector_lens[1]]; res_centroids when
+ * num_res_centroids[1] > 1; outlier_centroids and outlier_indices when
+ * npercent > 0; weight_scale and weight_bias with enable_norm; perm INT32 [k]
+ * with enable_perm; absent ones null.  The layout (outlier columns, groups,
+ * index widths: Layout, vptq.cc:52-129) and the tensor, index, outlier-index
+ * and permutation checks (CheckData, :203-240) raise INVALID_ARGUMENT with
+ * the reference's messages.  Decodes to y [out_features, in_features] of y's
+ * dtype (FLOAT, FLOAT16, BFLOAT16 or DOUBLE): the codebook values with the
+ * residual and norm steps rounded to the codebook dtype, then WriteFloat
+ * (quantization.cc:184-201, its nonfinite and range errors). */
+int onnxl_amd_dequantize_vptq(const onnxl_amd_vptq_config *config, const onnxl_amd_tensor *indices,
+                              const onnxl_amd_tensor *centroids, const onnxl_amd_tensor *res_centroids,
+                              const onnxl_amd_tensor *outlier_centroids, const onnxl_amd_tensor *outlier_indices,
+                              const onnxl_amd_tensor *weight_scale, const onnxl_amd_tensor *weight_bias,
+                              const onnxl_amd_tensor *perm, onnxl_amd_tensor *y, void *stream);
+
 /* GPTQModel FP8 weights (the encoding "onnx_light.gptqmodel_fp8_weights.v1"
  * of ai.rt:Dequantize: ImportGptqModelFp8Weights / ExportGptqModelFp8Weights,
  * quantization.h:603-612, decoded by ReconstructGptqModelFp8Weights,

@@ -114,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_gptqmodel_fp8.argtypes = [I64, I64, CS, ctypes.POINTER(I64), I32, TP, TP, TP,
                                                          ctypes.c_void_p]
+        L.onnxl_amd_dequantize_vptq.argtypes = [ctypes.POINTER(VptqConfig), TP, TP, TP, TP, TP, TP, TP, TP, TP,
+                                                ctypes.c_void_p]
         L.onnxl_amd_dequantize_bitblas.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, I32, TP, ctypes.c_void_p]
         L.onnxl_amd_prepare_bitblas_size.argtypes = [CS, I64, I64, I64, I64, I32, ctypes.POINTER(I64),
                                                      ctypes.POINTER(I64), ctypes.POINTER(I64)]
@@ -434,6 +436,44 @@ def bitsandbytes_matmul(a, w: BnbWeight, out=None):
     _check(lib().onnxl_amd_bitsandbytes_matmul(describe(a), BNB_FORMATS[w.fmt], w.rows, w.cols, w.block,
                                                describe(w.weight, code), describe(w.scales), describe(out),
                                                _stream_of(a, w.weight, out)))
+    return out
+
+
+class VptqConfig(ctypes.Structure):
+    """onnxl_amd_vptq_config: the VPTQ constructor metadata the layout uses."""
+    _fields_ = [("in_features", ctypes.c_int64), ("out_features", ctypes.c_int64), ("bits", ctypes.c_int64),
+                ("vector_lens", ctypes.c_int64 * 2), ("num_centroids", ctypes.c_int64 * 2),
+                ("num_res_centroids", ctypes.c_int64 * 2), ("npercent", ctypes.c_double),
+                ("group_size", ctypes.c_int64), ("group_num", ctypes.c_int64), ("enable_norm", ctypes.c_int32),
+                ("norm_dim", ctypes.c_int32), ("enable_perm", ctypes.c_int32)]
+
+    @classmethod
+    def of(cls, params: dict, bits: int = 4):
+        c = cls()
+        c.in_features, c.out_features, c.bits = params["in_features"], params["out_features"], bits
+        for name in ("vector_lens", "num_centroids", "num_res_centroids"):
+            getattr(c, name)[0], getattr(c, name)[1] = params[name]
+        c.npercent = params["npercent"]
+        c.group_size, c.group_num = params["group_size"], params["group_num"]
+        c.enable_norm, c.norm_dim = int(params["enable_norm"]), params["norm_dim"]
+        c.enable_perm = int(params["enable_perm"])
+        return c
+
+
+VPTQ_TENSORS = ("indices", "centroids.weight", "res_centroids.weight", "outlier_centroids.weight",
+                "outlier_indices", "weight_scale", "weight_bias", "perm")
+
+
+def dequantize_vptq(config: VptqConfig, tensors: dict, codebook_dtype: int, output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_vptq: a VPTQ weight (tensors by the checkpoint's
+    names; BFLOAT16 / FLOAT16 codebooks may be uint16 bit patterns, typed by
+    codebook_dtype) as [out_features, in_features] values."""
+    out = _decode_out(config.in_features, config.out_features, output_dtype, tuple(tensors.values()), out)
+    cb = {"centroids.weight", "res_centroids.weight", "outlier_centroids.weight", "weight_scale", "weight_bias"}
+    descs = [describe(tensors.get(n), codebook_dtype if n in cb and tensors.get(n) is not None else None)
+             for n in VPTQ_TENSORS]
+    _check(lib().onnxl_amd_dequantize_vptq(ctypes.byref(config), *descs, describe(out),
+                                           _stream_of(*tensors.values(), out)))
     return out
 
 

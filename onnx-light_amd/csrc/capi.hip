@@ -2591,6 +2591,161 @@ int BnbMatMul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t c
 
 bool QqqDtype(int32_t dt);
 
+// ---------------------------------------------------------------------------
+// VPTQ weights (onnx_core/runtime/vptq.cc): Layout (:52-129) in the
+// reference's order with DecodeValues' 1 << 30 byte limit, the tensor checks
+// of ImportVptqWeights (:359-367), CheckData (:203-240: the indices on the
+// device, the outlier indices and the permutation on the host), the
+// reconstruction on the device and WriteFloat's checks.
+
+int64_t VptqPositive(int64_t v) {
+  OLA_ENFORCE(v > 0, "VPTQ invalid positive dimension.");
+  return v;
+}
+
+int DequantizeVptq(const onnxl_amd_vptq_config *cfg, const onnxl_amd_tensor *indices,
+                   const onnxl_amd_tensor *centroids, const onnxl_amd_tensor *res_centroids,
+                   const onnxl_amd_tensor *outlier_centroids, const onnxl_amd_tensor *outlier_indices,
+                   const onnxl_amd_tensor *weight_scale, const onnxl_amd_tensor *weight_bias,
+                   const onnxl_amd_tensor *perm, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(cfg != nullptr, "VPTQ: config is required.");
+  const onnxl_amd_vptq_config &w = *cfg;
+  OLA_ENFORCE(!Absent(centroids), "VPTQ missing centroids.weight.");
+  constexpr int64_t kLimit = int64_t(1) << 30;
+  VptqParams p{};
+  p.k = VptqPositive(w.in_features);
+  p.n = VptqPositive(w.out_features);
+  OLA_ENFORCE(p.k <= kLimit / 4 / p.n, "VPTQ FLOAT output exceeds max_bytes.");
+  OLA_ENFORCE(!w.enable_perm || p.k <= int64_t(std::numeric_limits<int32_t>::max()) + 1,
+              "VPTQ permutation exceeds INT32 channel range.");
+  OLA_ENFORCE(w.bits >= 1 && w.bits <= 8 && w.vector_lens[1] > 0 && w.num_centroids[1] > 1 &&
+                  w.num_res_centroids[1] != 1 && w.num_res_centroids[0] <= 1,
+              "VPTQ unsupported codebook or outlier residual configuration.");
+  const int32_t dtype = centroids->data_type;
+  OLA_ENFORCE(dtype == kFloat || dtype == kFloat16 || dtype == kBfloat16, "VPTQ unsupported codebook dtype.");
+  OLA_ENFORCE(std::isfinite(w.npercent) && w.npercent >= 0 && w.npercent < 100 && (w.norm_dim == 0 || w.norm_dim == 1),
+              "VPTQ invalid constructor metadata.");
+  const bool outlier = w.npercent > 0 && w.vector_lens[0] > 0 && w.num_centroids[0] > 1;
+  OLA_ENFORCE(w.npercent == 0 || outlier, "VPTQ unusable outlier codebook.");
+  const double initial = std::ceil((w.npercent / 100.0) * double(p.k));
+  OLA_ENFORCE(initial >= 0 && initial < double(p.k), "VPTQ empty grouped layout.");
+  p.outliers = outlier ? static_cast<int64_t>(initial) : 0;
+  OLA_ENFORCE((w.group_size == -1 || w.group_size > 0) && (w.group_num == -1 || w.group_num > 0) &&
+                  (w.group_size == -1 || w.group_num == -1),
+              "VPTQ grouping knobs must be mutually exclusive.");
+  if (w.group_num != -1) {
+    p.groups = VptqPositive(w.group_num);
+    OLA_ENFORCE(p.groups <= p.k - p.outliers, "VPTQ empty groups.");
+    if (outlier) p.outliers += (p.k - p.outliers) % p.groups;
+    p.columns = outlier ? (p.k - p.outliers) / p.groups : (p.k + p.groups - 1) / p.groups;
+  } else {
+    p.columns = w.group_size == -1 ? p.k - p.outliers : VptqPositive(w.group_size);
+    p.groups = (p.k - p.outliers + p.columns - 1) / p.columns;
+  }
+  OLA_ENFORCE(p.groups > 0 && p.columns > 0 && p.groups * p.columns >= p.k - p.outliers,
+              "VPTQ incomplete grouped layout.");
+  auto bit_width = [](int64_t entries) {
+    int b = 0;
+    for (uint64_t v = (uint64_t)(entries - 1); v; v >>= 1) ++b;
+    return b;
+  };
+  p.main_bits = bit_width(w.num_centroids[1]);
+  p.residual_bits = w.num_res_centroids[1] > 1 ? bit_width(w.num_res_centroids[1]) : 0;
+  OLA_ENFORCE(p.main_bits + p.residual_bits <= 32, "VPTQ index width exceeds INT32.");
+  p.len1 = w.vector_lens[1];
+  p.len0 = outlier ? w.vector_lens[0] : 1;
+  p.nc1 = w.num_centroids[1];
+  p.nr1 = w.num_res_centroids[1];
+  p.vectors = (p.n + p.len1 - 1) / p.len1;
+  p.words = (p.columns * (p.main_bits + p.residual_bits) + 31) / 32;
+  p.dtype = dtype;
+  p.norm_dim = (int)w.norm_dim;
+  int64_t total = 0;
+  auto spec = [&](const onnxl_amd_tensor *t, const char *name, int32_t dt, std::initializer_list<int64_t> shape) {
+    int64_t bytes = dt == kInt32 || dt == kFloat ? 4 : 2;
+    for (int64_t d : shape) bytes *= VptqPositive(d);
+    OLA_ENFORCE(total <= kLimit && bytes <= kLimit - total, "VPTQ checkpoint exceeds max_bytes.");
+    total += bytes;
+    OLA_ENFORCE(!Absent(t), "VPTQ missing tensor ", name, ".");
+    bool ok = t->data_type == dt && t->rank == (int32_t)shape.size() && t->size_bytes == bytes &&
+              t->data != nullptr;
+    int i = 0;
+    for (int64_t d : shape) ok = ok && t->dims[i++] == d;
+    OLA_ENFORCE(ok, "VPTQ invalid tensor type, shape or bytes: ", name, ".");
+    CheckDescriptor(t, name);
+  };
+  spec(indices, "indices", kInt32, {p.groups, p.vectors, p.words});
+  spec(centroids, "centroids.weight", dtype, {p.groups, p.nc1 * p.len1});
+  if (p.residual_bits) spec(res_centroids, "res_centroids.weight", dtype, {p.groups, p.nr1 * p.len1});
+  if (outlier) {
+    spec(outlier_centroids, "outlier_centroids.weight", dtype, {1, w.num_centroids[0] * w.vector_lens[0]});
+    spec(outlier_indices, "outlier_indices", kInt32, {1, (p.n + p.len0 - 1) / p.len0, p.outliers});
+  }
+  if (w.enable_norm) {
+    spec(weight_scale, "weight_scale", dtype, {w.norm_dim == 0 ? p.k : p.n});
+    spec(weight_bias, "weight_bias", dtype, {w.norm_dim == 0 ? p.k : p.n});
+  }
+  if (w.enable_perm) spec(perm, "perm", kInt32, {p.k});
+  OLA_ENFORCE(y != nullptr && QqqDtype(y->data_type), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  CheckDescriptor(y, "y");
+  const int64_t yw = y->data_type == kDouble ? 8 : (y->data_type == kFloat ? 4 : 2);
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == p.n && y->dims[1] == p.k && y->size_bytes == p.n * p.k * yw &&
+                  y->data != nullptr,
+              "VPTQ: y must be [out_features, in_features] of its dtype.");
+  Ctx();
+  Staging st(stream, 256,
+             {indices, centroids, p.residual_bits ? res_centroids : nullptr, outlier ? outlier_centroids : nullptr,
+              outlier ? outlier_indices : nullptr, w.enable_norm ? weight_scale : nullptr,
+              w.enable_norm ? weight_bias : nullptr, w.enable_perm ? perm : nullptr},
+             {y});
+  p.indices = static_cast<const uint32_t *>(st.In(indices));
+  p.centroids = st.In(centroids);
+  p.res_centroids = p.residual_bits ? st.In(res_centroids) : nullptr;
+  p.outlier_centroids = outlier ? st.In(outlier_centroids) : nullptr;
+  p.outlier_indices = outlier ? static_cast<const int32_t *>(st.In(outlier_indices)) : nullptr;
+  p.scale = w.enable_norm ? st.In(weight_scale) : nullptr;
+  p.bias = w.enable_norm ? st.In(weight_bias) : nullptr;
+  p.perm = w.enable_perm ? static_cast<const int32_t *>(st.In(perm)) : nullptr;
+  p.flag = static_cast<unsigned *>(st.Extra());
+  hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, p.flag, (size_t)3);
+  onnxl_amd_tensor fd{};
+  fd.data_type = kInt32, fd.rank = 1, fd.dims[0] = 3, fd.data = p.flag, fd.size_bytes = 12;
+  fd.location = ONNXL_AMD_DEVICE;
+  LaunchVptqIndexCheck(p, stream);
+  OLA_HIP(hipGetLastError());
+  unsigned flag = 0;
+  ReadOnStream(stream, fd, &flag, 4);
+  OLA_ENFORCE(!(flag & kVptqBadIndex), "VPTQ index exceeds codebook.");
+  if (outlier) {
+    std::vector<uint32_t> oi((size_t)NumElements(*outlier_indices));
+    ReadOnStream(stream, *outlier_indices, oi.data(), oi.size() * 4);
+    for (uint32_t v : oi)
+      OLA_ENFORCE(v <= (uint32_t)std::numeric_limits<int32_t>::max() && (int64_t)v < w.num_centroids[0],
+                  "VPTQ outlier index exceeds codebook.");
+  }
+  if (w.enable_perm) {
+    std::vector<uint32_t> pv((size_t)p.k);
+    ReadOnStream(stream, *perm, pv.data(), pv.size() * 4);
+    std::vector<uint8_t> seen((size_t)p.k, 0);
+    for (uint32_t v : pv) {
+      OLA_ENFORCE(v <= (uint32_t)std::numeric_limits<int32_t>::max() && (int64_t)v < p.k && !seen[v],
+                  "VPTQ invalid permutation.");
+      seen[v] = 1;
+    }
+  }
+  LaunchVptqDecode(p, y->data_type, st.Out(y), stream);
+  OLA_HIP(hipGetLastError());
+  unsigned first[3] = {0, 0, 0};  // WriteFloat's first failure in output order
+  ReadOnStream(stream, fd, first, 12);
+  if (first[1] || first[2]) {
+    const bool nonfinite = first[1] && (!first[2] || ~first[1] < ~first[2]);
+    OLA_ENFORCE(!nonfinite, "Dequantization produced a nonfinite value.");
+    OLA_ENFORCE(false, "Dequantization output dtype overflow.");
+  }
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
 int DequantizeGptqFp8(int64_t k, int64_t n, const char *method_name, const int64_t *block, int32_t block_rank,
                       const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scale, onnxl_amd_tensor *y,
                       hipStream_t stream) {
@@ -3242,6 +3397,17 @@ int onnxl_amd_bitsandbytes_matmul(const onnxl_amd_tensor *a, int32_t format, int
                                   onnxl_amd_tensor *y, void *stream) {
   return Guard([&] {
     return BnbMatMul(a, format, rows, cols, block_size, weight, scales, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_vptq(const onnxl_amd_vptq_config *config, const onnxl_amd_tensor *indices,
+                              const onnxl_amd_tensor *centroids, const onnxl_amd_tensor *res_centroids,
+                              const onnxl_amd_tensor *outlier_centroids, const onnxl_amd_tensor *outlier_indices,
+                              const onnxl_amd_tensor *weight_scale, const onnxl_amd_tensor *weight_bias,
+                              const onnxl_amd_tensor *perm, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeVptq(config, indices, centroids, res_centroids, outlier_centroids, outlier_indices,
+                          weight_scale, weight_bias, perm, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -195,6 +195,28 @@ struct BnbParams {
 };
 void LaunchBnbScales(const BnbParams &p, hipStream_t s);
 
+// VPTQ weights (vptq.hip): flag words and the decoded layout.  flag[0] bit
+// kVptqBadIndex: an index past its codebook; flag[1] / flag[2]: the
+// complement of the first output index whose value is not finite / past
+// the output dtype's range (0: none).
+constexpr unsigned kVptqBadIndex = 1;
+struct VptqParams {
+  int64_t k, n;                      // in_features, out_features
+  int64_t outliers, columns, groups, vectors, words;
+  int main_bits, residual_bits;
+  int64_t len0, len1, nc1, nr1;      // vector lengths, codebook sizes
+  int dtype;                         // codebook dtype: kFloat, kFloat16, kBfloat16
+  int norm_dim;
+  const uint32_t *indices;           // [groups, vectors, words]
+  const void *centroids, *res_centroids, *outlier_centroids;
+  const int32_t *outlier_indices;    // [1, ceil(n / len0), outliers]
+  const void *scale, *bias;          // norm (null without)
+  const int32_t *perm;               // null without
+  unsigned *flag;                    // 3 words
+};
+void LaunchVptqIndexCheck(const VptqParams &p, hipStream_t s);
+void LaunchVptqDecode(const VptqParams &p, int out_dtype, void *y, hipStream_t s);
+
 // GPTQModel FP8 weights (gptqmodel_fp8.hip): flag bits in the reference's order.
 constexpr unsigned kGptqFp8BadScale = 1;   // an inverse scale not finite or not positive
 constexpr unsigned kGptqFp8BadValue = 2;   // a value not finite in fp32

@@ -1981,3 +1981,142 @@ int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, in
   }
   return rc;
 }
+
+/* ---- VPTQ weights, onnx_core/runtime/vptq.cc --------------------------------
+ * TEST INFRASTRUCTURE.  Layout (:52-129): the outlier columns
+ * ceil(npercent / 100 * k) (plus the remainder (k - outliers) % groups with
+ * group_num and an outlier codebook), the groups and their columns, index
+ * widths bit_width(num_centroids - 1) (+ the residual's), vectors
+ * ceil(n / vector_len), words ceil(columns * width / 32).  Index (:194-202):
+ * bits [j * width, +width) of row (g, v) of the INT32 words.  CheckData
+ * (:203-240): every index of every column (padding included) inside its
+ * codebooks (1), outlier indices inside theirs (2), perm a permutation (3).
+ * Reconstruct (:401-443) as described for the device decode; Round
+ * (:344-351) rounds to the codebook dtype.  Returns -1 for a layout the
+ * reference rejects, the CheckData codes above, 5 for a nonfinite value
+ * and 4 for a value past out_dtype (WriteFloat), else 0. */
+static float vptq_load(const void *p, int dtype, int64_t i) {
+  if (dtype == 1) return ((const float *)p)[i];
+  const uint16_t h = ((const uint16_t *)p)[i];
+  if (dtype == 10) return orc_f16_to_f32(h);
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float vptq_round(float v, int dtype) {
+  volatile float r = v;
+  if (dtype == 10) return orc_f16_to_f32(orc_f32_to_f16(r));
+  if (dtype == 16) {
+    uint32_t u = (uint32_t)orc_f32_to_bf16(r) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+  }
+  return r;
+}
+
+static int vptq_bit_width(int64_t entries) {
+  int b = 0;
+  for (uint64_t v = (uint64_t)(entries - 1); v; v >>= 1) ++b;
+  return b;
+}
+
+int orc_vptq_reconstruct(const orc_vptq_config *c, const uint32_t *indices, const void *centroids,
+                         const void *res_centroids, const void *outlier_centroids, const int32_t *outlier_indices,
+                         const void *scale, const void *bias, const int32_t *perm, int out_dtype, void *out) {
+  const int64_t k = c->k, n = c->n;
+  const int outlier = c->npercent > 0 && c->vector_lens[0] > 0 && c->num_centroids[0] > 1;
+  if (c->npercent != 0 && !outlier) return -1;
+  const double initial = ceil((c->npercent / 100.0) * (double)k);
+  if (!(initial >= 0 && initial < (double)k)) return -1;
+  int64_t outliers = outlier ? (int64_t)initial : 0, groups, columns;
+  if (c->group_num != -1) {
+    groups = c->group_num;
+    if (groups > k - outliers) return -1;
+    if (outlier) outliers += (k - outliers) % groups;
+    columns = outlier ? (k - outliers) / groups : (k + groups - 1) / groups;
+  } else {
+    columns = c->group_size == -1 ? k - outliers : c->group_size;
+    groups = (k - outliers + columns - 1) / columns;
+  }
+  if (!(groups > 0 && columns > 0 && groups * columns >= k - outliers)) return -1;
+  const int mb = vptq_bit_width(c->num_centroids[1]);
+  const int rb = c->num_res_centroids[1] > 1 ? vptq_bit_width(c->num_res_centroids[1]) : 0;
+  const int width = mb + rb;
+  const int64_t len0 = c->vector_lens[0], len1 = c->vector_lens[1];
+  const int64_t vectors = (n + len1 - 1) / len1, words = (columns * width + 31) / 32;
+  const uint32_t mask = (uint32_t)((1ull << mb) - 1);
+#define VPTQ_INDEX(g, v, j)                                                                      \
+  ((uint32_t)(((((uint64_t)indices[((g) * vectors + (v)) * words + (j) * width / 32]) |           \
+               ((j) * width % 32 + width > 32                                                    \
+                    ? (uint64_t)indices[((g) * vectors + (v)) * words + (j) * width / 32 + 1] << 32 \
+                    : 0)) >>                                                                     \
+              ((j) * width % 32)) &                                                              \
+             ((1ull << width) - 1)))
+  for (int64_t g = 0; g < groups; ++g)
+    for (int64_t v = 0; v < vectors; ++v)
+      for (int64_t j = 0; j < columns; ++j) {
+        const uint32_t index = VPTQ_INDEX(g, v, j);
+        if ((int64_t)(index & mask) >= c->num_centroids[1]) return 1;
+        if (rb && (int64_t)(index >> mb) >= c->num_res_centroids[1]) return 1;
+      }
+  if (outliers)
+    for (int64_t i = 0; i < ((n + len0 - 1) / len0) * outliers; ++i)
+      if (outlier_indices[i] < 0 || outlier_indices[i] >= c->num_centroids[0]) return 2;
+  if (c->enable_perm) {
+    unsigned char *seen = (unsigned char *)calloc((size_t)k, 1);
+    for (int64_t i = 0; i < k; ++i) {
+      if (perm[i] < 0 || perm[i] >= k || seen[perm[i]]) {
+        free(seen);
+        return 3;
+      }
+      seen[perm[i]] = 1;
+    }
+    free(seen);
+  }
+  float *vals = (float *)malloc((size_t)(n * k) * sizeof(float));
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t col = 0; col < k; ++col) {
+      float value;
+      if (col < outliers) {
+        const int64_t index = outlier_indices[(r / len0) * outliers + col];
+        value = vptq_load(outlier_centroids, c->dtype, index * len0 + r % len0);
+      } else {
+        const int64_t g = (col - outliers) / columns, j = (col - outliers) % columns;
+        const uint32_t index = VPTQ_INDEX(g, r / len1, j);
+        value = vptq_load(centroids, c->dtype, (g * c->num_centroids[1] + (index & mask)) * len1 + r % len1);
+        if (rb)
+          value = vptq_round(value + vptq_load(res_centroids, c->dtype,
+                                               (g * c->num_res_centroids[1] + (index >> mb)) * len1 + r % len1),
+                             c->dtype);
+      }
+      const int64_t dest = c->enable_perm ? perm[col] : col;
+      if (c->enable_norm) {
+        const int64_t i = c->norm_dim == 0 ? dest : r;
+        value = vptq_round(value * vptq_load(scale, c->dtype, i), c->dtype);
+        value = vptq_round(value + vptq_load(bias, c->dtype, i), c->dtype);
+      }
+      vals[r * k + dest] = value;
+    }
+#undef VPTQ_INDEX
+  /* WriteFloat in output order: the first nonfinite or out-of-range value raises */
+  int rc = 0;
+  for (int64_t e = 0; e < n * k && rc == 0; ++e) {
+    const float value = vals[e];
+    if (!isfinite(value)) {
+      rc = 5;
+    } else if (out_dtype == 1) {
+      ((float *)out)[e] = value;
+    } else if (out_dtype == 11) {
+      ((double *)out)[e] = (double)value;
+    } else {
+      const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(value) : orc_f32_to_bf16(value);
+      if (out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u) rc = 4;
+      ((uint16_t *)out)[e] = h;
+    }
+  }
+  free(vals);
+  return rc;
+}

@@ -224,6 +224,19 @@ int orc_bnb_reconstruct(int format, int64_t rows, int64_t cols, int64_t block, i
                         const uint8_t *codes, const void *absmax, const float *nested_absmax,
                         const float *nested_map, int out_dtype, void *out);
 
+/* VPTQ weights: the constructor metadata of the layout and the
+ * reconstruction into values [n, k]. */
+typedef struct orc_vptq_config {
+  int64_t k, n, bits;
+  int64_t vector_lens[2], num_centroids[2], num_res_centroids[2];
+  double npercent;
+  int64_t group_size, group_num;
+  int32_t enable_norm, norm_dim, enable_perm, dtype;
+} orc_vptq_config;
+int orc_vptq_reconstruct(const orc_vptq_config *c, const uint32_t *indices, const void *centroids,
+                         const void *res_centroids, const void *outlier_centroids, const int32_t *outlier_indices,
+                         const void *scale, const void *bias, const int32_t *perm, int out_dtype, void *out);
+
 /* GPTQModel FP8 weights: code_type one of the five FP8 data types; method 0
  * tensor, 1 row, 2 block (b0 x b1); values [n, k]. */
 float orc_f8e8m0_to_f32(uint8_t v);

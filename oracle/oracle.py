@@ -46,6 +46,15 @@ P = ctypes.c_void_p
 I64P = ctypes.POINTER(ctypes.c_int64)
 
 
+class VptqConfig(ctypes.Structure):
+    """orc_vptq_config (oracle.h)."""
+    _fields_ = [("k", ctypes.c_int64), ("n", ctypes.c_int64), ("bits", ctypes.c_int64),
+                ("vector_lens", ctypes.c_int64 * 2), ("num_centroids", ctypes.c_int64 * 2),
+                ("num_res_centroids", ctypes.c_int64 * 2), ("npercent", ctypes.c_double),
+                ("group_size", ctypes.c_int64), ("group_num", ctypes.c_int64), ("enable_norm", ctypes.c_int32),
+                ("norm_dim", ctypes.c_int32), ("enable_perm", ctypes.c_int32), ("dtype", ctypes.c_int32)]
+
+
 def _declare(L):
     L.orc_f32_to_f16.restype = ctypes.c_uint16
     L.orc_f32_to_f16.argtypes = [ctypes.c_float]
@@ -126,6 +135,8 @@ def _declare(L):
     L.orc_bnb_check.restype = ctypes.c_int
     L.orc_bnb_check.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                 ctypes.c_float, P, P, P, P]
+    L.orc_vptq_reconstruct.restype = ctypes.c_int
+    L.orc_vptq_reconstruct.argtypes = [ctypes.POINTER(VptqConfig), P, P, P, P, P, P, P, P, ctypes.c_int, P]
     L.orc_f8e8m0_to_f32.restype = ctypes.c_float
     L.orc_f8e8m0_to_f32.argtypes = [ctypes.c_uint8]
     L.orc_gptq_fp8_reconstruct.restype = ctypes.c_int
@@ -724,4 +735,41 @@ def gptq_fp8_reconstruct(codes, code_type: int, scales, method: str, block=(1, 1
     out = np.zeros((n, k), dt)
     rc = lib().orc_gptq_fp8_reconstruct(n, k, code_type, GPTQ_FP8_METHODS[method], block[0], block[1], _ptr(c),
                                         _ptr(s), out_dtype, _ptr(out))
+    return rc, out
+
+
+# ---- VPTQ weights ------------------------------------------------------------------
+
+VPTQ_ERRORS = {1: "VPTQ index exceeds codebook.", 2: "VPTQ outlier index exceeds codebook.",
+               3: "VPTQ invalid permutation.", 5: "Dequantization produced a nonfinite value.",
+               4: "Dequantization output dtype overflow."}
+
+
+def vptq_config(params: dict, dtype: int, bits: int = 4) -> VptqConfig:
+    """A VptqConfig from the checkpoint parameters (the reference fixture's names)."""
+    c = VptqConfig()
+    c.k, c.n, c.bits = params["in_features"], params["out_features"], bits
+    for name in ("vector_lens", "num_centroids", "num_res_centroids"):
+        getattr(c, name)[0], getattr(c, name)[1] = params[name]
+    c.npercent = params["npercent"]
+    c.group_size, c.group_num = params["group_size"], params["group_num"]
+    c.enable_norm, c.norm_dim, c.enable_perm = int(params["enable_norm"]), params["norm_dim"], int(params["enable_perm"])
+    c.dtype = dtype
+    return c
+
+
+def vptq_reconstruct(cfg: VptqConfig, tensors: dict, out_dtype: int = FLOAT):
+    """(rc, values [n, k]); tensors by the checkpoint's names, codebooks as
+    float32 arrays or uint16 bit patterns of the codebook dtype."""
+    def arr(name, dt):
+        t = tensors.get(name)
+        return np.zeros(1, dt) if t is None else np.ascontiguousarray(t).view(dt)
+    cb = np.float32 if cfg.dtype == FLOAT else np.uint16
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((cfg.n, cfg.k), dt)
+    rc = lib().orc_vptq_reconstruct(ctypes.byref(cfg), _ptr(arr("indices", np.uint32)),
+                                    _ptr(arr("centroids.weight", cb)), _ptr(arr("res_centroids.weight", cb)),
+                                    _ptr(arr("outlier_centroids.weight", cb)), _ptr(arr("outlier_indices", np.int32)),
+                                    _ptr(arr("weight_scale", cb)), _ptr(arr("weight_bias", cb)),
+                                    _ptr(arr("perm", np.int32)), out_dtype, _ptr(out))
     return rc, out

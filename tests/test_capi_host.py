@@ -631,3 +631,41 @@ def test_gptqmodel_fp8_validation(olamd):
     assert run(method="block", block=(2, 4), s=np.ones((2, 2), np.float32))[0] == olamd.NOT_INITIALIZED
     for code in (18, 19, 20, 24):
         assert run(code=code)[0] == olamd.NOT_INITIALIZED
+
+
+def test_vptq_validation(olamd):
+    """VPTQ's layout and tensor checks and messages (onnx_core/runtime/
+    vptq.cc:52-129 Layout, :359-367 the import's tensor checks) on the
+    reference's golden fixture; valid arguments stop at NOT_INITIALIZED."""
+    from test_oracle_vptq import vptq_cases, _arr
+    L = olamd.lib()
+    f = next(f for f in vptq_cases() if f["name"] == "combined_float16_norm0_perm_tails")
+    tensors = {k: _arr(v) for k, v in f["tensors"].items()}
+
+    def run(params=None, t=None, y=None, dtype=10):
+        cfg = olamd.VptqConfig.of(dict(f["parameters"], **(params or {})))
+        tt = dict(tensors, **(t or {}))
+        y = np.zeros((cfg.out_features, cfg.in_features), np.float32) if y is None else y
+        descs = [olamd.describe(tt.get(n), dtype if n not in ("indices", "outlier_indices", "perm") and
+                                tt.get(n) is not None else None) for n in olamd.VPTQ_TENSORS]
+        rc = L.onnxl_amd_dequantize_vptq(ctypes.byref(cfg), *descs, olamd.describe(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    for kw, msg in ((dict(params=dict(in_features=0)), "VPTQ invalid positive dimension."),
+                    (dict(params=dict(num_centroids=[5, 1])), "VPTQ unsupported codebook or outlier residual"),
+                    (dict(params=dict(num_res_centroids=[-1, 1])), "VPTQ unsupported codebook or outlier residual"),
+                    (dict(dtype=11), "VPTQ unsupported codebook dtype."),
+                    (dict(params=dict(npercent=100.0)), "VPTQ invalid constructor metadata."),
+                    (dict(params=dict(norm_dim=2)), "VPTQ invalid constructor metadata."),
+                    (dict(params=dict(vector_lens=[-1, 3])), "VPTQ unusable outlier codebook."),
+                    (dict(params=dict(group_num=2)), "VPTQ grouping knobs must be mutually exclusive."),
+                    (dict(params=dict(group_size=-1, group_num=99)), "VPTQ empty groups."),
+                    (dict(t={"indices": tensors["indices"][:2]}), "VPTQ invalid tensor type, shape or bytes: indices."),
+                    (dict(t={"perm": None}), "VPTQ missing tensor perm."),
+                    (dict(t={"weight_bias": tensors["weight_bias"][:3]}),
+                     "VPTQ invalid tensor type, shape or bytes: weight_bias."),
+                    (dict(y=np.zeros((7, 17), np.int8)), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16."),
+                    (dict(y=np.zeros((17, 7), np.float32)), "VPTQ: y must be [out_features, in_features]")):
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
+    assert run()[0] == olamd.NOT_INITIALIZED
