@@ -940,11 +940,61 @@ bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqChe
   return true;
 }
 
+// MX and NVFP4 weights carried as encoded values (struct types
+// "onnx_light.mxfp4_weights.v1", "onnx_light.mxfp6_e2m3_weights.v1",
+// "onnx_light.mxfp8_weights.v1", "onnx_light.nvfp4_weights.v1"): the native
+// tensors from the reference's exporters (ExportMxfp4Weights /
+// ExportMxfp6E2m3Weights / ExportMxfp8Weights / ExportNvfp4Weights,
+// quantization.h:943-1012), which validate the encoding and its schema.
+struct MxCheckpoint {
+  std::string format;
+  rt::Tensor weight, scale;
+  float global = 0.f;
+  int64_t rows = 0, cols = 0;
+  int Decode(onnxl_amd_tensor *y) const {
+    const onnxl_amd_tensor w = Describe(&weight), s = Describe(&scale);
+    return onnxl_amd_dequantize_mx_weights(format.c_str(), &w, &s, global, y, nullptr);
+  }
+};
+
+// False when the encoded value is not an MX / NVFP4 weight.
+template <typename Catalogue>
+bool ExportMx(const rt::RuntimeValue &value, const Catalogue &catalogue, MxCheckpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  const std::string type = catalogue.Resolve(enc.struct_type()).name().value();
+  if (type == "onnx_light.mxfp4_weights.v1") {
+    rt::Mxfp4Weights w = rt::ExportMxfp4Weights(enc, catalogue);
+    out.format = "mxfp4", out.weight = std::move(w.weight_packed), out.scale = std::move(w.weight_scale);
+    out.cols = out.weight.shape[1] * 2;
+  } else if (type == "onnx_light.mxfp6_e2m3_weights.v1") {
+    rt::Mxfp6E2m3Weights w = rt::ExportMxfp6E2m3Weights(enc, catalogue);
+    out.format = "mxfp6_e2m3", out.weight = std::move(w.weight_packed), out.scale = std::move(w.weight_scale);
+    out.cols = out.weight.shape[1] / 3 * 4;
+  } else if (type == "onnx_light.mxfp8_weights.v1") {
+    rt::Mxfp8Weights w = rt::ExportMxfp8Weights(enc, catalogue);
+    out.format = "mxfp8", out.weight = std::move(w.weight), out.scale = std::move(w.weight_scale);
+    out.cols = out.weight.shape[1];
+  } else if (type == "onnx_light.nvfp4_weights.v1") {
+    rt::Nvfp4Weights w = rt::ExportNvfp4Weights(enc, catalogue);
+    out.format = "nvfp4", out.weight = std::move(w.weight_packed), out.scale = std::move(w.weight_scale);
+    out.global = w.weight_global_scale;
+    out.cols = out.weight.shape[1] * 2;
+  } else {
+    return false;
+  }
+  out.rows = out.weight.shape[0];
+  return true;
+}
+
 // ai.rt:Dequantize(Q; dtype) (onnx_extensions/kernels/kernels/quantization/
 // kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes, QQQ,
 // GPTQModel FP8 and VPTQ encodings decode on the GPU to [out_features,
 // in_features] of dtype (onnxl_amd_dequantize_awq / _gptq / _bitblas /
-// _bitsandbytes / _qqq / _gptqmodel_fp8 / _vptq); every other
+// _bitsandbytes / _qqq / _gptqmodel_fp8 / _vptq), and the MX / NVFP4
+// weights to their [rows, cols] (onnxl_amd_dequantize_mx_weights); every other
 // encoding, and values that reference shared parameters, run on the built-in
 // kernel.
 class Mi355xDequantize : public Mi355xKernel {
@@ -991,6 +1041,15 @@ public:
       if (Call(f.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
       return;
     }
+    MxCheckpoint mx;
+    if (value != ctx.values().end() && ExportMx(value->second, ctx.struct_type_catalogue(), mx)) {
+      const rt::Shape shape{mx.rows, mx.cols};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      if (Call(mx.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     QqqCheckpoint q;
     if (value != ctx.values().end() && ExportQqq(value->second, ctx.struct_type_catalogue(), q)) {
       const rt::Shape shape{q.n, q.k};
@@ -1004,7 +1063,7 @@ public:
     }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8 / VPTQ");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8 / VPTQ / MX");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1406,6 +1465,12 @@ private:
     if (ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {  // a division per weight: dense
       auto w = std::make_shared<Prepared>();
       DenseFromDevice(In(0, ctx), f.n, f.k, [&](onnxl_amd_tensor *y) { return f.Decode(y); }, *w);
+      return w;
+    }
+    MxCheckpoint mx;
+    if (ExportMx(value->second, ctx.struct_type_catalogue(), mx)) {  // [rows, cols] = [N, K]: dense
+      auto w = std::make_shared<Prepared>();
+      DenseFromDevice(In(0, ctx), mx.rows, mx.cols, [&](onnxl_amd_tensor *y) { return mx.Decode(y); }, *w);
       return w;
     }
     Checkpoint c;

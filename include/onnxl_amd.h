@@ -572,6 +572,27 @@ int onnxl_amd_dequantize_gptqmodel_fp8(int64_t in_features, int64_t out_features
                                        const onnxl_amd_tensor *weight, const onnxl_amd_tensor *weight_scale_inv,
                                        onnxl_amd_tensor *y, void *stream);
 
+/* MX and NVFP4 weights (the encodings "onnx_light.mxfp4_weights.v1",
+ * "onnx_light.mxfp6_e2m3_weights.v1", "onnx_light.mxfp8_weights.v1" and
+ * "onnx_light.nvfp4_weights.v1" of ai.rt:Dequantize: ImportMxfp4Weights /
+ * ImportMxfp6E2m3Weights / ImportMxfp8Weights / ImportNvfp4Weights and their
+ * exporters, quantization.h:943-1012, decoded through DequantizeTensor,
+ * quantization.cc:2032-2085).  format "mxfp4": weight UINT8 [rows, cols / 2]
+ * (E2M1 codes, low nibble first), weight_scale UINT8 [rows, cols / 32] (E8M0);
+ * "mxfp6_e2m3": weight UINT8 [rows, cols / 4 * 3] (E2M3 codes, LSB first),
+ * weight_scale UINT8 [rows, cols / 32]; "mxfp8": weight FLOAT8E4M3FN
+ * [rows, cols], weight_scale UINT8 [rows, cols / 32]; "nvfp4": weight UINT8
+ * [rows, cols / 2], weight_scale FLOAT8E4M3FN [rows, cols / 16] and
+ * weight_global_scale (ignored by the other formats).  Decodes to y
+ * [rows, cols] of y's dtype (FLOAT, FLOAT16, BFLOAT16 or DOUBLE): code value
+ * x 2^(e - 127) (NVFP4: x (local / global), the quotient rounded once), one
+ * fp32 rounding, then WriteFloat's rounding.  The import's checks and the
+ * reconstruction walk raise INVALID_ARGUMENT with the reference's messages,
+ * the first failing group and element in the reference's order. */
+int onnxl_amd_dequantize_mx_weights(const char *format, const onnxl_amd_tensor *weight,
+                                    const onnxl_amd_tensor *weight_scale, float weight_global_scale,
+                                    onnxl_amd_tensor *y, void *stream);
+
 /* QQQ weights (the encoding "onnx_light.qqq_weights.v1" of ai.rt:Dequantize:
  * ImportQqqWeights / ExportQqqWeights, quantization.h, decoded by
  * ReconstructQqqWeights, qqq.cc:346-358, through DequantizeTensor).  The

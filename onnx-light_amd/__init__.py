@@ -114,6 +114,7 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_gptqmodel_fp8.argtypes = [I64, I64, CS, ctypes.POINTER(I64), I32, TP, TP, TP,
                                                          ctypes.c_void_p]
+        L.onnxl_amd_dequantize_mx_weights.argtypes = [CS, TP, TP, F32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_vptq.argtypes = [ctypes.POINTER(VptqConfig), TP, TP, TP, TP, TP, TP, TP, TP, TP,
                                                 ctypes.c_void_p]
         L.onnxl_amd_dequantize_bitblas.argtypes = [CS, TP, TP, TP, I64, I64, I64, I64, I32, TP, ctypes.c_void_p]
@@ -488,6 +489,24 @@ def dequantize_gptqmodel_fp8(weight, weight_scale_inv, method: str, block=(), co
     _check(lib().onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.encode(), blk, len(block),
                                                     describe(weight, code), describe(weight_scale_inv),
                                                     describe(out), _stream_of(weight, weight_scale_inv, out)))
+    return out
+
+
+MX_FORMATS = ("mxfp4", "mxfp6_e2m3", "mxfp8", "nvfp4")
+
+
+def dequantize_mx_weights(fmt: str, weight, weight_scale, global_scale: float = 0.0, code: int | None = None,
+                          scale_code: int | None = None, output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_mx_weights: an MX / NVFP4 weight (`fmt` one of
+    MX_FORMATS; `code` / `scale_code` the data_types when the tensors hold raw
+    uint8 bytes: FLOAT8E4M3FN for the mxfp8 weight and the nvfp4 scales) as
+    [rows, cols] values."""
+    rows, wcols = _shape_of(weight)
+    cols = wcols if fmt == "mxfp8" else (wcols // 3 * 4 if fmt == "mxfp6_e2m3" else wcols * 2)
+    out = _decode_out(cols, rows, output_dtype, (weight, weight_scale), out)
+    _check(lib().onnxl_amd_dequantize_mx_weights(fmt.encode(), describe(weight, code),
+                                                 describe(weight_scale, scale_code), float(global_scale),
+                                                 describe(out), _stream_of(weight, weight_scale, out)))
     return out
 
 

@@ -2592,6 +2592,117 @@ int BnbMatMul(const onnxl_amd_tensor *a, int32_t format, int64_t rows, int64_t c
 bool QqqDtype(int32_t dt);
 
 // ---------------------------------------------------------------------------
+// MX and NVFP4 weights (onnx_core/runtime/quantization.cc): the checks of
+// ImportMxfp4Weights (:2193-2212), ImportMxfp8Weights (:2214-2229),
+// ImportMxfp6E2m3Weights (:2279-2298) and ImportNvfp4Weights (:2099-2118)
+// in their order (matrix, packed columns, Geometry, the two tensors), then
+// the Validate*Reconstruction walks (:1350-1359, :1477-1486, :1608-1613,
+// :1714-1720) on the device with the first failing group and element
+// raised as the reference words it, then WriteFloat's output range.
+
+int DequantizeMx(const char *format_name, const onnxl_amd_tensor *weight, const onnxl_amd_tensor *scale,
+                 float global, onnxl_amd_tensor *y, hipStream_t stream) {
+  const std::string f = format_name ? format_name : "";
+  int fmt;
+  if (f == "mxfp4") fmt = kMxFp4;
+  else if (f == "mxfp6_e2m3") fmt = kMxFp6E2M3;
+  else if (f == "mxfp8") fmt = kMxFp8;
+  else if (f == "nvfp4") fmt = kMxNvfp4;
+  else throw Unsupported(Cat("MX weights: unknown format '", f, "' (mxfp4, mxfp6_e2m3, mxfp8 or nvfp4)."));
+  // the reference's names for the format in its messages
+  const char *tag = fmt == kMxFp4 ? "MXFP4 WEIGHT" : (fmt == kMxNvfp4 ? "NVFP4 WEIGHT"
+                                                     : (fmt == kMxFp8 ? "MXFP8" : "MXFP6 E2M3"));
+  const int group = fmt == kMxNvfp4 ? 16 : 32;
+  constexpr int64_t kMax = std::numeric_limits<int64_t>::max();
+  OLA_ENFORCE(!Absent(weight) && weight->rank == 2, tag,
+              fmt == kMxFp8 ? " weights must be a matrix." : " packed weights must be a matrix.");
+  const int64_t rows = weight->dims[0], wcols = weight->dims[1];
+  int64_t cols;
+  if (fmt == kMxFp8) {
+    cols = wcols;
+  } else if (fmt == kMxFp6E2M3) {
+    OLA_ENFORCE(wcols > 0 && wcols % 3 == 0 && wcols / 3 <= kMax / 4, "Invalid MXFP6 E2M3 packed columns.");
+    cols = wcols / 3 * 4;
+  } else {
+    OLA_ENFORCE(wcols > 0 && wcols <= kMax / 2, tag, " packed columns overflow.");
+    cols = wcols * 2;
+  }
+  // Geometry
+  OLA_ENFORCE(rows > 0 && cols > 0 && cols % group == 0, tag, " requires positive [rows,cols] with cols divisible by ",
+              group, ".");
+  OLA_ENFORCE(rows <= kMax / cols, tag, " element count exceeds INT64.");
+  const int64_t count = rows * cols;
+  const int64_t code_bytes = fmt == kMxFp8 ? count : (fmt == kMxFp6E2M3 ? count / 4 * 3 : count / 2);
+  const int64_t scale_bytes = count / group;
+  // ValidateMxfp4Tensor / ValidateNvfp4Tensor / ValidateMxTensor
+  const std::string bad = fmt == kMxFp4 || fmt == kMxNvfp4 ? Cat("Invalid ", tag, " tensor type, shape or storage.")
+                                                          : std::string("Invalid MX tensor type, shape or storage.");
+  const int32_t code_type = fmt == kMxFp8 ? kFloat8E4M3FN : kUint8;
+  OLA_ENFORCE(weight->data_type == code_type && weight->size_bytes == code_bytes && weight->data != nullptr, bad);
+  const int32_t scale_type = fmt == kMxNvfp4 ? kFloat8E4M3FN : kUint8;
+  OLA_ENFORCE(!Absent(scale) && scale->data_type == scale_type && scale->rank == 2 && scale->dims[0] == rows &&
+                  scale->dims[1] == cols / group && scale->size_bytes == scale_bytes && scale->data != nullptr,
+              bad);
+  CheckDescriptor(weight, "weight");
+  CheckDescriptor(scale, "weight_scale");
+  OLA_ENFORCE(y != nullptr && QqqDtype(y->data_type), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  CheckDescriptor(y, "y");
+  const int64_t width = y->data_type == kDouble ? 8 : (y->data_type == kFloat ? 4 : 2);
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == rows && y->dims[1] == cols && y->size_bytes == count * width &&
+                  y->data != nullptr,
+              "MX weights: y must be [rows, cols] of its dtype.");
+  Ctx();
+  Staging st(stream, 256, {weight, scale}, {y});
+  MxParams p{};
+  p.count = count;
+  p.codes = static_cast<const uint8_t *>(st.In(weight));
+  p.scales = static_cast<const uint8_t *>(st.In(scale));
+  p.global = global;
+  void *out = st.Out(y);
+  p.aligned = (reinterpret_cast<uintptr_t>(p.codes) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0) ? 1 : 0;
+  p.first = static_cast<uint64_t *>(st.Extra());
+  p.flag = reinterpret_cast<unsigned *>(p.first + 1);
+  hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, reinterpret_cast<unsigned *>(p.first), (size_t)3);
+  LaunchMxDecode(p, fmt, y->data_type, out, stream);
+  OLA_HIP(hipGetLastError());
+  onnxl_amd_tensor fd{};
+  fd.data_type = kInt32, fd.rank = 1, fd.dims[0] = 3, fd.data = p.first, fd.size_bytes = 12;
+  fd.location = ONNXL_AMD_DEVICE;
+  uint32_t words[3] = {};
+  ReadOnStream(stream, fd, words, 12);
+  const uint64_t first = (uint64_t)words[0] | ((uint64_t)words[1] << 32);
+  if (first != 0) {
+    const uint64_t key = ~first;
+    const int64_t g = (int64_t)(key / 128);
+    const int step = (int)(key % 128), e = (step - 3) / 2;
+    const bool code = step >= 3 && (step - 3) % 2 == 0;
+    switch (fmt) {
+    case kMxFp4:  // Mxfp4Scale :1458-1461, Mxfp4Reconstruct :1463-1470
+      OLA_ENFORCE(step != 0, "MXFP4 WEIGHT E8M0 scale is NaN in group ", g, ".");
+      OLA_ENFORCE(false, "MXFP4 WEIGHT reconstruction overflow or nonfinite value in group ", g, ", element ", e, ".");
+      break;
+    case kMxNvfp4:  // Nvfp4EffectiveScale :1322-1333, Nvfp4Reconstruct :1335-1342
+      OLA_ENFORCE(step != 0, "NVFP4 WEIGHT scales must be positive and finite in group ", g, ".");
+      OLA_ENFORCE(step != 1, "NVFP4 WEIGHT effective scale overflow or nonfinite value in group ", g, ".");
+      OLA_ENFORCE(step != 2, "NVFP4 WEIGHT effective scale rounds to zero in group ", g, ".");
+      OLA_ENFORCE(false, "NVFP4 WEIGHT reconstruction overflow or nonfinite value in group ", g, ", element ", e, ".");
+      break;
+    case kMxFp8:  // Mxfp8Scale :1591-1595, Mxfp8Reconstruct :1597-1600, RoundFloat :41-45
+      OLA_ENFORCE(step != 0, "MXFP8 E8M0 scale must not be NaN.");
+      OLA_ENFORCE(!code, "MXFP8 E4M3FN weight must not be NaN.");
+      OLA_ENFORCE(false, "FLOAT reconstruction overflow or nonfinite value.");
+      break;
+    default:  // Mxfp6E2m3Scale :1700-1703, RoundFloat :41-45
+      OLA_ENFORCE(step != 0, "MXFP6 E2M3 E8M0 scale byte 255 is invalid.");
+      OLA_ENFORCE(false, "FLOAT reconstruction overflow or nonfinite value.");
+    }
+  }
+  OLA_ENFORCE(!(words[2] & kMxBadOutput), "Dequantization output dtype overflow.");
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // VPTQ weights (onnx_core/runtime/vptq.cc): Layout (:52-129) in the
 // reference's order with DecodeValues' 1 << 30 byte limit, the tensor checks
 // of ImportVptqWeights (:359-367), CheckData (:203-240: the indices on the
@@ -3408,6 +3519,14 @@ int onnxl_amd_dequantize_vptq(const onnxl_amd_vptq_config *config, const onnxl_a
   return Guard([&] {
     return DequantizeVptq(config, indices, centroids, res_centroids, outlier_centroids, outlier_indices,
                           weight_scale, weight_bias, perm, y, static_cast<hipStream_t>(stream));
+  });
+}
+
+int onnxl_amd_dequantize_mx_weights(const char *format, const onnxl_amd_tensor *weight,
+                                    const onnxl_amd_tensor *weight_scale, float weight_global_scale,
+                                    onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] {
+    return DequantizeMx(format, weight, weight_scale, weight_global_scale, y, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -233,6 +233,25 @@ struct GptqFp8Params {
 // kBfloat16 or kDouble; y [n, k] or null (the checks alone)
 void LaunchGptqFp8Decode(const GptqFp8Params &p, int code_dtype, int out_dtype, void *y, hipStream_t s);
 
+// MX / NVFP4 weights (mx_weights.hip).  `first` (zeroed by the caller)
+// receives the complement of the smallest failure key group * 128 + step
+// (step 0 a group's scale, 1 / 2 NVFP4's quotient not finite / zero, 3 + 2e
+// element e's NaN code, 4 + 2e its value not finite), 0 when none; `flag`
+// the output range bit.
+enum MxFormat { kMxFp4 = 0, kMxFp6E2M3 = 1, kMxFp8 = 2, kMxNvfp4 = 3 };
+constexpr unsigned kMxBadOutput = 1;  // a value past the output dtype's range
+struct MxParams {
+  int64_t count;          // rows * cols, a multiple of the group size
+  const uint8_t *codes;   // packed codes (MXFP4 / NVFP4 nibbles, MXFP6 6-bit, MXFP8 bytes)
+  const uint8_t *scales;  // one byte per group
+  float global;           // NVFP4's global scale
+  int aligned;            // codes and y 16-byte aligned: vector loads and stores
+  uint64_t *first;
+  unsigned *flag;
+};
+// y [rows, cols] of out_dtype (kFloat, kFloat16, kBfloat16, kDouble) or null
+void LaunchMxDecode(const MxParams &p, int format, int out_dtype, void *y, hipStream_t s);
+
 // QQQ weights (qqq.hip): flag bits of a decode / preparation, in the order
 // the reference raises them.
 constexpr unsigned kQqqBadChannel = 1;   // a channel scale not finite or negative

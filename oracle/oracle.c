@@ -1982,6 +1982,68 @@ int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, in
   return rc;
 }
 
+/* ---- MX and NVFP4 weights, onnx_core/runtime/quantization.cc ------------
+ * TEST INFRASTRUCTURE.  format 0 MXFP4, 1 MXFP6 E2M3, 2 MXFP8, 3 NVFP4; count
+ * = rows * cols, groups of 32 (16 for NVFP4) consecutive values, one scale
+ * byte each.  Validate*Reconstruction (:1350-1359, :1477-1486, :1608-1613,
+ * :1714-1720) walk the groups in order: the scale (Mxfp4Scale :1458,
+ * Mxfp8Scale :1591, Mxfp6E2m3Scale :1700: byte 255 rejected, 2^(e - 127)
+ * with byte 0 = 2^-127; Nvfp4EffectiveScale :1322: E4M3FN local / global,
+ * both finite and positive, the quotient finite and nonzero), then each
+ * element (MXFP8: a NaN code rejected first) as one fp32 product, finite.
+ * Returns 0, or 1 a bad scale, 2 NVFP4's quotient not finite, 3 it is zero,
+ * 4 a NaN code, 5 a value not finite (group / element of the first), 6 a
+ * value past out_dtype's range (WriteFloat, after every check). */
+int orc_mx_reconstruct(int format, int64_t count, const uint8_t *codes, const uint8_t *scales, float global,
+                       int out_dtype, void *out, int64_t *fail_group, int64_t *fail_element) {
+  const int64_t g = format == 3 ? 16 : 32;
+  int rc = 0;
+  *fail_group = *fail_element = -1;
+  for (int64_t grp = 0; grp < count / g; ++grp) {
+    float scale;
+    if (format == 3) {
+      const float local = orc_f8e4m3fn_to_f32(scales[grp]);
+      if (!(isfinite(global) && global > 0 && isfinite(local) && local > 0)) { *fail_group = grp; return 1; }
+      volatile float eff = local / global;
+      if (!isfinite(eff)) { *fail_group = grp; return 2; }
+      if (!(eff > 0)) { *fail_group = grp; return 3; }
+      scale = eff;
+    } else {
+      if (scales[grp] == 255) { *fail_group = grp; return 1; }
+      scale = ldexpf(1.0f, (int)scales[grp] - 127);
+    }
+    for (int64_t j = 0; j < g; ++j) {
+      const int64_t i = grp * g + j;
+      float level;
+      if (format == 0 || format == 3) {
+        level = orc_f4e2m1_to_f32((uint8_t)(j % 2 ? codes[i / 2] >> 4 : codes[i / 2] & 15));
+      } else if (format == 1) {
+        const int64_t bit = j * 6;
+        const uint8_t *b = codes + grp * 24 + bit / 8;
+        unsigned v = b[0] >> (bit % 8);
+        if (bit % 8 > 2) v |= (unsigned)b[1] << (8 - bit % 8);
+        level = orc_f6_to_f32((uint8_t)(v & 63u), ORC_FLOAT6E2M3);
+      } else {
+        level = orc_f8e4m3fn_to_f32(codes[i]);
+        if (!isfinite(level)) { *fail_group = grp, *fail_element = j; return 4; }
+      }
+      volatile float v = level * scale;
+      if (!isfinite(v)) { *fail_group = grp, *fail_element = j; return 5; }
+      if (out_dtype == 1) {
+        ((float *)out)[i] = v;
+      } else if (out_dtype == 11) {
+        ((double *)out)[i] = (double)v;
+      } else {
+        const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+        const int inf = out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u;
+        if (inf) rc = 6;
+        ((uint16_t *)out)[i] = h;
+      }
+    }
+  }
+  return rc;
+}
+
 /* ---- VPTQ weights, onnx_core/runtime/vptq.cc --------------------------------
  * TEST INFRASTRUCTURE.  Layout (:52-129): the outlier columns
  * ceil(npercent / 100 * k) (plus the remainder (k - outliers) % groups with

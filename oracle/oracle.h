@@ -243,6 +243,11 @@ float orc_f8e8m0_to_f32(uint8_t v);
 int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, int64_t b0, int64_t b1,
                              const uint8_t *codes, const float *scales, int out_dtype, void *out);
 
+/* MX / NVFP4 weights: format 0 MXFP4, 1 MXFP6 E2M3, 2 MXFP8, 3 NVFP4; values
+ * [count] and the first failure's group / element. */
+int orc_mx_reconstruct(int format, int64_t count, const uint8_t *codes, const uint8_t *scales, float global,
+                       int out_dtype, void *out, int64_t *fail_group, int64_t *fail_element);
+
 /* BitBLAS row-packed weights: raw codes [n, k] and the GPTQ affine values. */
 int orc_bitblas_reconstruct(int64_t k, int64_t n, int64_t group, int bits, int signed_codes, const uint8_t *qweight,
                             const uint16_t *scales, const uint8_t *qzeros, int out_dtype, void *out, uint8_t *codes);

@@ -139,6 +139,10 @@ def _declare(L):
     L.orc_vptq_reconstruct.argtypes = [ctypes.POINTER(VptqConfig), P, P, P, P, P, P, P, P, ctypes.c_int, P]
     L.orc_f8e8m0_to_f32.restype = ctypes.c_float
     L.orc_f8e8m0_to_f32.argtypes = [ctypes.c_uint8]
+    L.orc_mx_reconstruct.restype = ctypes.c_int
+    L.orc_mx_reconstruct.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+                                     ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
+                                     ctypes.POINTER(ctypes.c_int64)]
     L.orc_gptq_fp8_reconstruct.restype = ctypes.c_int
     L.orc_gptq_fp8_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int64, ctypes.c_int64, P, P, ctypes.c_int, P]
@@ -736,6 +740,44 @@ def gptq_fp8_reconstruct(codes, code_type: int, scales, method: str, block=(1, 1
     rc = lib().orc_gptq_fp8_reconstruct(n, k, code_type, GPTQ_FP8_METHODS[method], block[0], block[1], _ptr(c),
                                         _ptr(s), out_dtype, _ptr(out))
     return rc, out
+
+
+# ---- MX and NVFP4 weights -----------------------------------------------------------
+
+MX_FORMATS = {"mxfp4": 0, "mxfp6_e2m3": 1, "mxfp8": 2, "nvfp4": 3}
+
+
+def mx_error(fmt: str, rc: int, group: int, element: int) -> str:
+    """The reference's message for orc_mx_reconstruct's failure `rc`
+    (quantization.cc:1322-1342, 1458-1470, 1591-1600, 1700-1707, RoundFloat
+    :41-45, WriteFloat :184-201)."""
+    if rc == 6:
+        return "Dequantization output dtype overflow."
+    if fmt == "mxfp4":
+        return {1: f"MXFP4 WEIGHT E8M0 scale is NaN in group {group}.",
+                5: f"MXFP4 WEIGHT reconstruction overflow or nonfinite value in group {group}, element {element}."}[rc]
+    if fmt == "nvfp4":
+        return {1: f"NVFP4 WEIGHT scales must be positive and finite in group {group}.",
+                2: f"NVFP4 WEIGHT effective scale overflow or nonfinite value in group {group}.",
+                3: f"NVFP4 WEIGHT effective scale rounds to zero in group {group}.",
+                5: f"NVFP4 WEIGHT reconstruction overflow or nonfinite value in group {group}, element {element}."}[rc]
+    if fmt == "mxfp8":
+        return {1: "MXFP8 E8M0 scale must not be NaN.", 4: "MXFP8 E4M3FN weight must not be NaN.",
+                5: "FLOAT reconstruction overflow or nonfinite value."}[rc]
+    return {1: "MXFP6 E2M3 E8M0 scale byte 255 is invalid.", 5: "FLOAT reconstruction overflow or nonfinite value."}[rc]
+
+
+def mx_reconstruct(fmt: str, rows: int, cols: int, codes, scales, global_scale: float = 0.0,
+                   out_dtype: int = FLOAT):
+    """(rc, group, element, values [rows, cols]) of an MX / NVFP4 weight."""
+    c = np.ascontiguousarray(codes).view(np.uint8).reshape(-1)
+    s = np.ascontiguousarray(scales).view(np.uint8).reshape(-1)
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((rows, cols), dt)
+    g, e = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib().orc_mx_reconstruct(MX_FORMATS[fmt], rows * cols, _ptr(c), _ptr(s), float(global_scale), out_dtype,
+                                  _ptr(out), ctypes.byref(g), ctypes.byref(e))
+    return rc, g.value, e.value, out
 
 
 # ---- VPTQ weights ------------------------------------------------------------------

@@ -669,3 +669,54 @@ def test_vptq_validation(olamd):
         rc, err = run(**kw)
         assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw, err)
     assert run()[0] == olamd.NOT_INITIALIZED
+
+
+def test_mx_weights_validation(olamd):
+    """The MX / NVFP4 imports' checks and messages (quantization.cc:2099-2118,
+    2193-2229, 2279-2298: matrix, packed columns, Geometry, the two tensors)
+    on host payloads, in that order; valid arguments stop at
+    NOT_INITIALIZED."""
+    L = olamd.lib()
+    d = olamd.describe
+
+    def run(fmt, w, s, code=None, scode=None, y=None, g=1.0):
+        rows = w.shape[0] if w.ndim else 1
+        y = np.zeros((rows, 32), np.float32) if y is None else y
+        rc = L.onnxl_amd_dequantize_mx_weights(fmt.encode(), d(w, code), d(s, scode), g, d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    u8 = np.uint8
+    cases = [
+        ("mxfp4", np.zeros(16, u8), np.zeros((1, 1), u8), None, None, "MXFP4 WEIGHT packed weights must be a matrix."),
+        ("mxfp4", np.zeros((1, 0), u8), np.zeros((1, 1), u8), None, None, "MXFP4 WEIGHT packed columns overflow."),
+        ("mxfp4", np.zeros((1, 8), u8), np.zeros((1, 1), u8), None, None,
+         "MXFP4 WEIGHT requires positive [rows,cols] with cols divisible by 32."),
+        ("mxfp4", np.zeros((0, 16), u8), np.zeros((0, 1), u8), None, None,
+         "MXFP4 WEIGHT requires positive [rows,cols] with cols divisible by 32."),
+        ("mxfp4", np.zeros((1, 16), np.int8), np.zeros((1, 1), u8), None, None,
+         "Invalid MXFP4 WEIGHT tensor type, shape or storage."),
+        ("mxfp4", np.zeros((1, 16), u8), np.zeros((1, 2), u8), None, None,
+         "Invalid MXFP4 WEIGHT tensor type, shape or storage."),
+        ("nvfp4", np.zeros((1, 16), u8), np.zeros((1, 2), u8), None, None,
+         "Invalid NVFP4 WEIGHT tensor type, shape or storage."),
+        ("nvfp4", np.zeros((1, 12), u8), np.zeros((1, 2), u8), None, 17,
+         "NVFP4 WEIGHT requires positive [rows,cols] with cols divisible by 16."),
+        ("mxfp8", np.zeros(32, u8), np.zeros((1, 1), u8), 17, None, "MXFP8 weights must be a matrix."),
+        ("mxfp8", np.zeros((1, 32), u8), np.zeros((1, 1), u8), None, None, "Invalid MX tensor type, shape or storage."),
+        ("mxfp8", np.zeros((1, 48), u8), np.zeros((1, 1), u8), 17, None,
+         "MXFP8 requires positive [rows,cols] with cols divisible by 32."),
+        ("mxfp6_e2m3", np.zeros((1, 25), u8), np.zeros((1, 1), u8), None, None, "Invalid MXFP6 E2M3 packed columns."),
+        ("mxfp6_e2m3", np.zeros((1, 24), u8), np.zeros((1, 1), np.int8), None, None,
+         "Invalid MX tensor type, shape or storage."),
+    ]
+    for fmt, w, s, code, scode, msg in cases:
+        rc, err = run(fmt, w, s, code, scode)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (fmt, w.shape, err)
+    rc, err = run("mxfp5", np.zeros((1, 16), u8), np.zeros((1, 1), u8))
+    assert rc == olamd.UNSUPPORTED and "unknown format" in err
+    for fmt, w, s, code, scode in (("mxfp4", np.zeros((1, 16), u8), np.zeros((1, 1), u8), None, None),
+                                   ("mxfp6_e2m3", np.zeros((1, 24), u8), np.zeros((1, 1), u8), None, None),
+                                   ("mxfp8", np.zeros((1, 32), u8), np.zeros((1, 1), u8), 17, None),
+                                   ("nvfp4", np.zeros((1, 16), u8), np.zeros((1, 2), u8), None, 17)):
+        rc, err = run(fmt, w, s, code, scode)
+        assert rc == olamd.NOT_INITIALIZED, (fmt, err)
