@@ -940,6 +940,39 @@ bool ExportQqq(const rt::RuntimeValue &value, const Catalogue &catalogue, QqqChe
   return true;
 }
 
+// EXL3 weights carried as encoded values (struct type
+// "onnx_light.exl3_weights.v1"): the trellis, suh, svh and codebook marker
+// from the reference's exporter (ExportExl3Weights, quantization.h:851),
+// which validates the encoding, its schema and the upstream revision.
+struct Exl3Checkpoint {
+  std::unordered_map<std::string, rt::Tensor> tensors;
+  int64_t k = 0, n = 0;
+  onnxl_amd_tensor T(const char *name) const {
+    auto it = tensors.find(name);
+    return it == tensors.end() ? Absent() : Describe(&it->second);
+  }
+  int Decode(onnxl_amd_tensor *y) const {
+    const onnxl_amd_tensor t = T("trellis"), u = T("suh"), v = T("svh"), m1 = T("mcg"), m2 = T("mul1");
+    return onnxl_amd_dequantize_exl3(&t, &u, &v, &m1, &m2, y, nullptr);
+  }
+};
+
+// False when the encoded value is not an EXL3 weight.
+template <typename Catalogue>
+bool ExportExl3(const rt::RuntimeValue &value, const Catalogue &catalogue, Exl3Checkpoint &out) {
+  if (value.kind != rt::RuntimeValue::Kind::kEncoded || value.Encoded().has_parameter_ref() ||
+      !value.Encoded().has_struct_type())
+    return false;
+  const auto &enc = value.Encoded();
+  if (catalogue.Resolve(enc.struct_type()).name().value() != "onnx_light.exl3_weights.v1") return false;
+  rt::Exl3Weights w = rt::ExportExl3Weights(enc, size_t{1} << 30, catalogue);
+  out.tensors = std::move(w.tensors);
+  const rt::Tensor &trellis = out.tensors.at("trellis");
+  out.k = trellis.shape[0] * 16;
+  out.n = trellis.shape[1] * 16;
+  return true;
+}
+
 // MX and NVFP4 weights carried as encoded values (struct types
 // "onnx_light.mxfp4_weights.v1", "onnx_light.mxfp6_e2m3_weights.v1",
 // "onnx_light.mxfp8_weights.v1", "onnx_light.nvfp4_weights.v1"): the native
@@ -993,8 +1026,9 @@ bool ExportMx(const rt::RuntimeValue &value, const Catalogue &catalogue, MxCheck
 // kernel_dequantize.cc:18-43): AWQ, GPTQ, BitBLAS, bitsandbytes, QQQ,
 // GPTQModel FP8 and VPTQ encodings decode on the GPU to [out_features,
 // in_features] of dtype (onnxl_amd_dequantize_awq / _gptq / _bitblas /
-// _bitsandbytes / _qqq / _gptqmodel_fp8 / _vptq), and the MX / NVFP4
-// weights to their [rows, cols] (onnxl_amd_dequantize_mx_weights); every other
+// _bitsandbytes / _qqq / _gptqmodel_fp8 / _vptq), the MX / NVFP4 weights to
+// their [rows, cols] (onnxl_amd_dequantize_mx_weights) and EXL3 weights to
+// their [k, n] (onnxl_amd_dequantize_exl3); every other
 // encoding, and values that reference shared parameters, run on the built-in
 // kernel.
 class Mi355xDequantize : public Mi355xKernel {
@@ -1041,6 +1075,15 @@ public:
       if (Call(f.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
       return;
     }
+    Exl3Checkpoint x3;
+    if (value != ctx.values().end() && ExportExl3(value->second, ctx.struct_type_catalogue(), x3)) {
+      const rt::Shape shape{x3.k, x3.n};
+      rt::Tensor y = ctx.MakeOutputTensor(0, static_cast<int32_t>(dtype), shape,
+                                          ByteSize(static_cast<int32_t>(dtype), Count(shape)));
+      onnxl_amd_tensor dy = DescribeOutput(y);
+      if (Call(x3.Decode(&dy), ctx)) rt::SetOutput(node, 0, std::move(y), ctx);
+      return;
+    }
     MxCheckpoint mx;
     if (value != ctx.values().end() && ExportMx(value->second, ctx.struct_type_catalogue(), mx)) {
       const rt::Shape shape{mx.rows, mx.cols};
@@ -1063,7 +1106,7 @@ public:
     }
     Checkpoint c;
     if (value == ctx.values().end() || !ExportCheckpoint(value->second, ctx.struct_type_catalogue(), c)) {
-      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8 / VPTQ / MX");
+      RunBuiltin(ctx, "encoding other than AWQ / GPTQ / BitBLAS / bitsandbytes / QQQ / GPTQModel FP8 / VPTQ / MX / EXL3");
       return;
     }
     const rt::Shape shape{c.N, c.K};
@@ -1465,6 +1508,12 @@ private:
     if (ExportGptqFp8(value->second, ctx.struct_type_catalogue(), f)) {  // a division per weight: dense
       auto w = std::make_shared<Prepared>();
       DenseFromDevice(In(0, ctx), f.n, f.k, [&](onnxl_amd_tensor *y) { return f.Decode(y); }, *w);
+      return w;
+    }
+    Exl3Checkpoint x3;
+    if (ExportExl3(value->second, ctx.struct_type_catalogue(), x3)) {  // [k, n] = [N, K]: dense
+      auto w = std::make_shared<Prepared>();
+      DenseFromDevice(In(0, ctx), x3.k, x3.n, [&](onnxl_amd_tensor *y) { return x3.Decode(y); }, *w);
       return w;
     }
     MxCheckpoint mx;

@@ -593,6 +593,23 @@ int onnxl_amd_dequantize_mx_weights(const char *format, const onnxl_amd_tensor *
                                     const onnxl_amd_tensor *weight_scale, float weight_global_scale,
                                     onnxl_amd_tensor *y, void *stream);
 
+/* EXL3 weights (the encoding "onnx_light.exl3_weights.v1" of ai.rt:Dequantize,
+ * GPTQModel's EXL3 module: ImportExl3Weights / ExportExl3Weights,
+ * quantization.h:847-852, decoded by ReconstructExl3Weights, exl3.cc:309-357,
+ * through DequantizeTensor).  trellis INT16 [k / 16, n / 16, 16 * bits]
+ * (bits 1..8), suh FLOAT16 [k], svh FLOAT16 [n], and at most one codebook
+ * marker, an INT32 scalar: mcg (0xCBAC1FED) or mul1 (0x83DCD12D); neither
+ * selects the 3INST codebook.  Decodes to y [k, n] of y's dtype (FLOAT,
+ * FLOAT16, BFLOAT16 or DOUBLE): trellis states through the codebook (binary16),
+ * normalised 128-point Hadamard butterflies down the columns, x suh, the same
+ * along the rows, x svh, every step one fp32 rounding, then WriteFloat's
+ * rounding.  Validate's checks (exl3.cc:136-165; the upstream revision is the
+ * exporter's) raise INVALID_ARGUMENT with the reference's messages, in its
+ * order. */
+int onnxl_amd_dequantize_exl3(const onnxl_amd_tensor *trellis, const onnxl_amd_tensor *suh,
+                              const onnxl_amd_tensor *svh, const onnxl_amd_tensor *mcg, const onnxl_amd_tensor *mul1,
+                              onnxl_amd_tensor *y, void *stream);
+
 /* QQQ weights (the encoding "onnx_light.qqq_weights.v1" of ai.rt:Dequantize:
  * ImportQqqWeights / ExportQqqWeights, quantization.h, decoded by
  * ReconstructQqqWeights, qqq.cc:346-358, through DequantizeTensor).  The

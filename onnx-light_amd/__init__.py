@@ -114,6 +114,7 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_gptqmodel_fp8.argtypes = [I64, I64, CS, ctypes.POINTER(I64), I32, TP, TP, TP,
                                                          ctypes.c_void_p]
+        L.onnxl_amd_dequantize_exl3.argtypes = [TP, TP, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_mx_weights.argtypes = [CS, TP, TP, F32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_vptq.argtypes = [ctypes.POINTER(VptqConfig), TP, TP, TP, TP, TP, TP, TP, TP, TP,
                                                 ctypes.c_void_p]
@@ -489,6 +490,17 @@ def dequantize_gptqmodel_fp8(weight, weight_scale_inv, method: str, block=(), co
     _check(lib().onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.encode(), blk, len(block),
                                                     describe(weight, code), describe(weight_scale_inv),
                                                     describe(out), _stream_of(weight, weight_scale_inv, out)))
+    return out
+
+
+def dequantize_exl3(trellis, suh, svh, mcg=None, mul1=None, output_dtype: int = FLOAT, out=None):
+    """onnxl_amd_dequantize_exl3: an EXL3 weight (trellis int16 [k / 16,
+    n / 16, 16 * bits], suh / svh float16 [k] / [n], the optional int32
+    codebook marker mcg or mul1) as [k, n] values."""
+    d0, d1, _ = _shape_of(trellis)
+    out = _decode_out(d1 * 16, d0 * 16, output_dtype, (trellis, suh, svh), out)
+    _check(lib().onnxl_amd_dequantize_exl3(describe(trellis), describe(suh), describe(svh), describe(mcg),
+                                           describe(mul1), describe(out), _stream_of(trellis, suh, svh, out)))
     return out
 
 

@@ -2703,6 +2703,92 @@ int DequantizeMx(const char *format_name, const onnxl_amd_tensor *weight, const 
 }
 
 // ---------------------------------------------------------------------------
+// EXL3 weights (onnx_core/runtime/exl3.cc): Validate (:136-165) in the
+// reference's order with its 1 << 30 byte limit (Geometry :45-69, CheckTensor
+// :111-115, CheckScales :117-124 on the host, CheckMarker :126-134), then the
+// reconstruction (:309-357) on the device and WriteFloat's range check.
+
+int DequantizeExl3(const onnxl_amd_tensor *trellis, const onnxl_amd_tensor *suh, const onnxl_amd_tensor *svh,
+                   const onnxl_amd_tensor *mcg, const onnxl_amd_tensor *mul1, onnxl_amd_tensor *y,
+                   hipStream_t stream) {
+  constexpr int64_t kLimit = int64_t(1) << 30, kMax = std::numeric_limits<int64_t>::max();
+  OLA_ENFORCE(!Absent(trellis), "EXL3 missing tensor trellis.");
+  OLA_ENFORCE(trellis->rank == 3 && trellis->dims[0] > 0 && trellis->dims[1] > 0 && trellis->dims[0] <= kMax / 16 &&
+                  trellis->dims[1] <= kMax / 16 && trellis->dims[2] % 16 == 0,
+              "EXL3 invalid trellis dimensions.");
+  const int book = !Absent(mcg) ? 1 : (!Absent(mul1) ? 2 : 0);
+  const int64_t k = trellis->dims[0] * 16, n = trellis->dims[1] * 16, rate = trellis->dims[2] / 16;
+  // Geometry
+  OLA_ENFORCE(k % 128 == 0 && n % 128 == 0, "EXL3 dimensions must be positive multiples of 128.");
+  OLA_ENFORCE(rate >= 1 && rate <= 8, "EXL3 unsupported trellis rate.");
+  OLA_ENFORCE(k <= kLimit / 4 / n, "EXL3 logical FLOAT weights exceed max_bytes.");
+  const int64_t count = k * n, packed = count / 8 * rate, scales = 2 * k + 2 * n;
+  OLA_ENFORCE(packed <= kLimit && scales <= kLimit - packed && (book == 0 || kLimit - packed - scales >= 4),
+              "EXL3 checkpoint exceeds max_bytes.");
+  OLA_ENFORCE(!(book == 1 && !Absent(mul1)), "EXL3 unexpected side tensors or conflicting codebooks.");
+  OLA_ENFORCE(trellis->data_type == kInt16 && trellis->size_bytes == packed && trellis->data != nullptr,
+              "EXL3 invalid tensor type, shape or byte extent.");
+  CheckDescriptor(trellis, "trellis");
+  // suh then svh: each tensor's check, then its values finite
+  const onnxl_amd_tensor *side[2] = {suh, svh};
+  const char *side_name[2] = {"suh", "svh"};
+  const int64_t side_count[2] = {k, n};
+  for (int i = 0; i < 2; ++i) {
+    const onnxl_amd_tensor *t = side[i];
+    OLA_ENFORCE(!Absent(t), "EXL3 missing tensor ", side_name[i], ".");
+    OLA_ENFORCE(t->data_type == kFloat16 && t->rank == 1 && t->dims[0] == side_count[i] &&
+                    t->size_bytes == side_count[i] * 2 && t->data != nullptr,
+                "EXL3 invalid tensor type, shape or byte extent.");
+    CheckDescriptor(t, side_name[i]);
+    std::vector<uint16_t> h((size_t)side_count[i]);
+    if (t->location != ONNXL_AMD_HOST) Ctx();
+    ReadOnStream(stream, *t, h.data(), h.size() * 2);
+    for (uint16_t b : h) OLA_ENFORCE((b & 0x7c00u) != 0x7c00u, "EXL3 nonfinite scale.");
+  }
+  if (book) {
+    const onnxl_amd_tensor *m = book == 1 ? mcg : mul1;
+    OLA_ENFORCE(m->data_type == kInt32 && m->rank == 0 && m->size_bytes == 4 && m->data != nullptr,
+                "EXL3 invalid tensor type, shape or byte extent.");
+    CheckDescriptor(m, book == 1 ? "mcg" : "mul1");
+    uint32_t marker = 0;
+    if (m->location != ONNXL_AMD_HOST) Ctx();
+    ReadOnStream(stream, *m, &marker, 4);
+    OLA_ENFORCE(marker == (book == 1 ? 0xcbac1fedu : 0x83dcd12du), "EXL3 invalid codebook marker.");
+  }
+  OLA_ENFORCE(y != nullptr && QqqDtype(y->data_type), "Dequantize dtype must be FLOAT, DOUBLE, FLOAT16 or BFLOAT16.");
+  CheckDescriptor(y, "y");
+  const int64_t width = y->data_type == kDouble ? 8 : (y->data_type == kFloat ? 4 : 2);
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == k && y->dims[1] == n && y->size_bytes == count * width &&
+                  y->data != nullptr,
+              "EXL3: y must be [k, n] of its dtype.");
+  Ctx();
+  Staging st(stream, 256, {trellis, suh, svh}, {y});
+  Exl3Params p{};
+  p.k = k, p.n = n, p.bits = (int)rate, p.book = book;
+  p.trellis = static_cast<const uint16_t *>(st.In(trellis));
+  p.suh = static_cast<const uint16_t *>(st.In(suh));
+  p.svh = static_cast<const uint16_t *>(st.In(svh));
+  p.flag = static_cast<unsigned *>(st.Extra());
+  OLA_ENFORCE(reinterpret_cast<uintptr_t>(p.trellis) % 2 == 0 && reinterpret_cast<uintptr_t>(p.suh) % 2 == 0 &&
+                  reinterpret_cast<uintptr_t>(p.svh) % 2 == 0,
+              "EXL3: trellis, suh and svh must be 2-byte aligned.");
+  void *out = st.Out(y);
+  OLA_ENFORCE(reinterpret_cast<uintptr_t>(out) % width == 0, "EXL3: y must be aligned to its element size.");
+  hipLaunchKernelGGL(ZeroWordsKernel, dim3(1), dim3(256), 0, stream, p.flag, (size_t)1);
+  LaunchExl3Decode(p, y->data_type, out, stream);
+  OLA_HIP(hipGetLastError());
+  onnxl_amd_tensor fd{};
+  fd.data_type = kInt32, fd.rank = 1, fd.dims[0] = 1, fd.data = p.flag, fd.size_bytes = 4;
+  fd.location = ONNXL_AMD_DEVICE;
+  unsigned flag = 0;
+  ReadOnStream(stream, fd, &flag, 4);
+  OLA_ENFORCE(!(flag & kExl3BadValue), "EXL3 nonfinite reconstruction.");
+  OLA_ENFORCE(!(flag & kExl3BadOutput), "Dequantization output dtype overflow.");
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // VPTQ weights (onnx_core/runtime/vptq.cc): Layout (:52-129) in the
 // reference's order with DecodeValues' 1 << 30 byte limit, the tensor checks
 // of ImportVptqWeights (:359-367), CheckData (:203-240: the indices on the
@@ -3528,6 +3614,12 @@ int onnxl_amd_dequantize_mx_weights(const char *format, const onnxl_amd_tensor *
   return Guard([&] {
     return DequantizeMx(format, weight, weight_scale, weight_global_scale, y, static_cast<hipStream_t>(stream));
   });
+}
+
+int onnxl_amd_dequantize_exl3(const onnxl_amd_tensor *trellis, const onnxl_amd_tensor *suh,
+                              const onnxl_amd_tensor *svh, const onnxl_amd_tensor *mcg, const onnxl_amd_tensor *mul1,
+                              onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] { return DequantizeExl3(trellis, suh, svh, mcg, mul1, y, static_cast<hipStream_t>(stream)); });
 }
 
 int onnxl_amd_dequantize_gptqmodel_fp8(int64_t in_features, int64_t out_features, const char *weight_scale_method,

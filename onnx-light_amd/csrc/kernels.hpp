@@ -252,6 +252,20 @@ struct MxParams {
 // y [rows, cols] of out_dtype (kFloat, kFloat16, kBfloat16, kDouble) or null
 void LaunchMxDecode(const MxParams &p, int format, int out_dtype, void *y, hipStream_t s);
 
+// EXL3 weights (exl3.hip): flag bits after the host's checks.
+constexpr unsigned kExl3BadValue = 1;   // a reconstructed value not finite
+constexpr unsigned kExl3BadOutput = 2;  // a value past the output dtype's range
+struct Exl3Params {
+  int64_t k, n;             // rows, columns (multiples of 128)
+  int bits, book;           // trellis rate 1..8; codebook 0 3INST, 1 MCG, 2 MUL1
+  const uint16_t *trellis;  // [k / 16, n / 16, 16 * bits]
+  const uint16_t *suh;      // binary16 [k]
+  const uint16_t *svh;      // binary16 [n]
+  unsigned *flag;
+};
+// y [k, n] of out_dtype (kFloat, kFloat16, kBfloat16, kDouble)
+void LaunchExl3Decode(const Exl3Params &p, int out_dtype, void *y, hipStream_t s);
+
 // QQQ weights (qqq.hip): flag bits of a decode / preparation, in the order
 // the reference raises them.
 constexpr unsigned kQqqBadChannel = 1;   // a channel scale not finite or negative

@@ -1982,6 +1982,102 @@ int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, in
   return rc;
 }
 
+/* ---- EXL3 weights, onnx_core/runtime/exl3.cc --------------------------------
+ * TEST INFRASTRUCTURE.  ReconstructExl3Weights (:309-357) in FLOAT: for
+ * every 16 x 16 tile and position, State (:222-231, the words taken at
+ * index ^ 1) through Codebook (:205-220, rounded to binary16) into the MMA
+ * fragment place (:331-334); then per 128-row block and column the
+ * Hadamard butterflies (:233-245, ascending widths, then x fp32(1 / sqrt
+ * 128)), per row x suh, the butterflies per 128-column block, x svh; every
+ * step one fp32 rounding.  Returns 0, 1 for a nonfinite value (Rounded :36),
+ * 4 for a value past out_dtype's range (WriteFloat). */
+static float exl3_codebook(uint32_t state, int book) {
+  float r;
+  if (book < 2) {
+    uint32_t raw = book == 0 ? state * 89226354u + 64248484u : state * 0xcbac1fedu;
+    raw = 0x3b603b60u ^ (raw & 0x8fff8fffu);
+    volatile float sum = orc_f16_to_f32((uint16_t)raw) + orc_f16_to_f32((uint16_t)(raw >> 16));
+    r = sum;
+  } else {
+    const uint32_t raw = state * 0x83dcd12du;
+    const uint32_t sum = (raw & 255u) + ((raw >> 8) & 255u) + ((raw >> 16) & 255u) + (raw >> 24);
+    r = fmaf(orc_f16_to_f32((uint16_t)(sum + 0x6400u)), orc_f16_to_f32(0x1eee), orc_f16_to_f32(0xc931));
+  }
+  return orc_f16_to_f32(orc_f32_to_f16(r));
+}
+
+static uint16_t exl3_state(const uint16_t *stream, uint32_t bits, uint32_t position) {
+  const uint32_t words = 16u * bits, span = 256u * bits;
+  const uint32_t start = ((position + 1u) * bits + span - 16u) % span;
+  const uint32_t word = start / 16u, shift = start % 16u;
+  uint32_t state = stream[word ^ 1u];
+  if (shift) state = ((state << shift) | ((uint32_t)stream[((word + 1u) % words) ^ 1u] >> (16u - shift))) & 65535u;
+  return (uint16_t)state;
+}
+
+static int exl3_hadamard(float *v, int64_t stride) {
+  int bad = 0;
+  for (int64_t w = 1; w < 128; w *= 2)
+    for (int64_t base = 0; base < 128; base += 2 * w)
+      for (int64_t j = base; j < base + w; ++j) {
+        const float a = v[j * stride], b = v[(j + w) * stride];
+        volatile float s = a + b, d = a - b;
+        v[j * stride] = s, v[(j + w) * stride] = d;
+        bad |= !isfinite(s) || !isfinite(d);
+      }
+  for (int64_t i = 0; i < 128; ++i) {
+    volatile float x = v[i * stride] * 0.08838834764831845f;
+    v[i * stride] = x;
+    bad |= !isfinite(x);
+  }
+  return bad;
+}
+
+int orc_exl3_reconstruct(int64_t k, int64_t n, int bits, int book, const uint16_t *trellis, const uint16_t *suh,
+                         const uint16_t *svh, int out_dtype, void *out) {
+  float *v = (float *)malloc((size_t)(k * n) * sizeof(float));
+  if (!v) return -1;
+  const int64_t words = 16 * bits;
+  for (int64_t tile = 0; tile < k * n / 256; ++tile)
+    for (uint32_t p = 0; p < 256; ++p) {
+      const uint32_t lane = p / 8, item = p % 8;
+      const int64_t row = (tile / (n / 16)) * 16 + (lane % 4) * 2 + (item & 1) + ((item & 2) ? 8 : 0);
+      const int64_t col = (tile % (n / 16)) * 16 + lane / 4 + ((item & 4) ? 8 : 0);
+      v[row * n + col] = exl3_codebook(exl3_state(trellis + tile * words, (uint32_t)bits, p), book);
+    }
+  int bad = 0;
+  for (int64_t r = 0; r < k; r += 128)
+    for (int64_t c = 0; c < n; ++c) bad |= exl3_hadamard(v + r * n + c, n);
+  for (int64_t r = 0; r < k; ++r) {
+    const float s = orc_f16_to_f32(suh[r]);
+    for (int64_t c = 0; c < n; ++c) {
+      volatile float x = v[r * n + c] * s;
+      v[r * n + c] = x;
+      bad |= !isfinite(x);
+    }
+    for (int64_t c = 0; c < n; c += 128) bad |= exl3_hadamard(v + r * n + c, 1);
+    for (int64_t c = 0; c < n; ++c) {
+      volatile float x = v[r * n + c] * orc_f16_to_f32(svh[c]);
+      v[r * n + c] = x;
+      bad |= !isfinite(x);
+    }
+  }
+  int rc = bad ? 1 : 0;
+  for (int64_t i = 0; i < k * n && !rc; ++i) {
+    if (out_dtype == 1) {
+      ((float *)out)[i] = v[i];
+    } else if (out_dtype == 11) {
+      ((double *)out)[i] = (double)v[i];
+    } else {
+      const uint16_t h = out_dtype == 10 ? orc_f32_to_f16(v[i]) : orc_f32_to_bf16(v[i]);
+      if (out_dtype == 10 ? (h & 0x7c00u) == 0x7c00u : (h & 0x7f80u) == 0x7f80u) rc = 4;
+      ((uint16_t *)out)[i] = h;
+    }
+  }
+  free(v);
+  return rc;
+}
+
 /* ---- MX and NVFP4 weights, onnx_core/runtime/quantization.cc ------------
  * TEST INFRASTRUCTURE.  format 0 MXFP4, 1 MXFP6 E2M3, 2 MXFP8, 3 NVFP4; count
  * = rows * cols, groups of 32 (16 for NVFP4) consecutive values, one scale

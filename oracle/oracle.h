@@ -243,6 +243,11 @@ float orc_f8e8m0_to_f32(uint8_t v);
 int orc_gptq_fp8_reconstruct(int64_t n, int64_t k, int code_type, int method, int64_t b0, int64_t b1,
                              const uint8_t *codes, const float *scales, int out_dtype, void *out);
 
+/* EXL3 weights: trellis [k / 16, n / 16, 16 * bits] words, book 0 3INST, 1
+ * MCG, 2 MUL1; values [k, n]. */
+int orc_exl3_reconstruct(int64_t k, int64_t n, int bits, int book, const uint16_t *trellis, const uint16_t *suh,
+                         const uint16_t *svh, int out_dtype, void *out);
+
 /* MX / NVFP4 weights: format 0 MXFP4, 1 MXFP6 E2M3, 2 MXFP8, 3 NVFP4; values
  * [count] and the first failure's group / element. */
 int orc_mx_reconstruct(int format, int64_t count, const uint8_t *codes, const uint8_t *scales, float global,

@@ -139,6 +139,9 @@ def _declare(L):
     L.orc_vptq_reconstruct.argtypes = [ctypes.POINTER(VptqConfig), P, P, P, P, P, P, P, P, ctypes.c_int, P]
     L.orc_f8e8m0_to_f32.restype = ctypes.c_float
     L.orc_f8e8m0_to_f32.argtypes = [ctypes.c_uint8]
+    L.orc_exl3_reconstruct.restype = ctypes.c_int
+    L.orc_exl3_reconstruct.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     L.orc_mx_reconstruct.restype = ctypes.c_int
     L.orc_mx_reconstruct.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
                                      ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
@@ -739,6 +742,24 @@ def gptq_fp8_reconstruct(codes, code_type: int, scales, method: str, block=(1, 1
     out = np.zeros((n, k), dt)
     rc = lib().orc_gptq_fp8_reconstruct(n, k, code_type, GPTQ_FP8_METHODS[method], block[0], block[1], _ptr(c),
                                         _ptr(s), out_dtype, _ptr(out))
+    return rc, out
+
+
+# ---- EXL3 weights ----------------------------------------------------------------------
+
+EXL3_ERRORS = {1: "EXL3 nonfinite reconstruction.", 4: "Dequantization output dtype overflow."}
+
+
+def exl3_reconstruct(trellis, suh, svh, book: int = 0, out_dtype: int = FLOAT):
+    """(rc, values [k, n]) of an EXL3 weight: trellis int16 [k / 16, n / 16,
+    16 * bits], suh / svh binary16 [k] / [n], book 0 3INST, 1 MCG, 2 MUL1."""
+    t = np.ascontiguousarray(trellis).view(np.uint16)
+    k, n, bits = t.shape[0] * 16, t.shape[1] * 16, t.shape[2] // 16
+    u = np.ascontiguousarray(suh).view(np.uint16)
+    v = np.ascontiguousarray(svh).view(np.uint16)
+    dt = {FLOAT: np.float32, DOUBLE: np.float64}.get(out_dtype, np.uint16)
+    out = np.zeros((k, n), dt)
+    rc = lib().orc_exl3_reconstruct(k, n, bits, book, _ptr(t), _ptr(u), _ptr(v), out_dtype, _ptr(out))
     return rc, out
 
 

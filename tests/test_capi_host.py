@@ -720,3 +720,43 @@ def test_mx_weights_validation(olamd):
                                    ("nvfp4", np.zeros((1, 16), u8), np.zeros((1, 2), u8), None, 17)):
         rc, err = run(fmt, w, s, code, scode)
         assert rc == olamd.NOT_INITIALIZED, (fmt, err)
+
+
+def test_exl3_validation(olamd):
+    """EXL3's Validate checks and messages (exl3.cc:136-165: trellis
+    dimensions, Geometry, the codebook count, each tensor then its scales'
+    finiteness, the marker) on host payloads, in that order; valid arguments
+    stop at NOT_INITIALIZED."""
+    L = olamd.lib()
+    d = olamd.describe
+    tr = np.zeros((8, 8, 48), np.int16)
+    suh, svh = np.ones(128, np.float16), np.ones(128, np.float16)
+    mcg = np.array(0xCBAC1FED, np.uint32).view(np.int32).reshape(())
+    mul1 = np.array(0x83DCD12D, np.uint32).view(np.int32).reshape(())
+
+    def run(t=tr, u=suh, v=svh, m1=None, m2=None):
+        y = np.zeros((t.shape[0] * 16 if t.ndim == 3 else 1, t.shape[1] * 16 if t.ndim == 3 else 1), np.float32)
+        rc = L.onnxl_amd_dequantize_exl3(d(t), d(u), d(v), d(m1), d(m2), d(y), None)
+        return rc, L.onnxl_amd_last_error().decode()
+
+    inf = suh.copy()
+    inf[3] = np.float16(np.inf)
+    cases = [(dict(t=np.zeros((8, 8), np.int16)), "EXL3 invalid trellis dimensions."),
+             (dict(t=np.zeros((8, 8, 17), np.int16)), "EXL3 invalid trellis dimensions."),
+             (dict(t=np.zeros((4, 8, 48), np.int16)), "EXL3 dimensions must be positive multiples of 128."),
+             (dict(t=np.zeros((8, 8, 0), np.int16)), "EXL3 unsupported trellis rate."),
+             (dict(t=np.zeros((8, 8, 144), np.int16)), "EXL3 unsupported trellis rate."),
+             (dict(t=np.zeros((2048, 2048, 16), np.int16)), "EXL3 logical FLOAT weights exceed max_bytes."),
+             (dict(m1=mcg, m2=mul1), "EXL3 unexpected side tensors or conflicting codebooks."),
+             (dict(t=np.zeros((8, 8, 48), np.uint16)), "EXL3 invalid tensor type, shape or byte extent."),
+             (dict(u=inf, v=svh[:5]), "EXL3 nonfinite scale."),
+             (dict(v=svh[:5]), "EXL3 invalid tensor type, shape or byte extent."),
+             (dict(u=suh.astype(np.float32)), "EXL3 invalid tensor type, shape or byte extent."),
+             (dict(m1=np.array(mcg ^ 1)), "EXL3 invalid codebook marker."),
+             (dict(m2=mcg), "EXL3 invalid codebook marker.")]
+    for kw, msg in cases:
+        rc, err = run(**kw)
+        assert rc == olamd.INVALID_ARGUMENT and msg in err, (kw.keys(), err)
+    for kw in (dict(), dict(m1=mcg), dict(m2=mul1)):
+        rc, err = run(**kw)
+        assert rc == olamd.NOT_INITIALIZED, err
