@@ -936,13 +936,28 @@ void LaunchGemvQ0Stream(const uint16_t *a, const uint8_t *w, int64_t M, int64_t 
 // bytes; every block starts 16-byte aligned as 144 = 9 x 16) and one 8-byte
 // run of codes; q6_k (210-byte blocks, 2-byte aligned) four 16-bit loads of
 // low nibbles, four of high bits, the sub-block's scale byte and d.
-__device__ __forceinline__ void NibbleFloats(uint32_t dw, int sh, float *f) {
-  const uint32_t t = (dw >> sh) & 0x0f0f0f0fu;
-  f[0] = (float)(t & 0xffu);
-  f[1] = (float)((t >> 8) & 0xffu);
-  f[2] = (float)((t >> 16) & 0xffu);
-  f[3] = (float)((t >> 24) & 0xffu);
+// Byte B of a dword as a float in one v_cvt_f32_ubyteB.  Written as
+// (float)((t >> 8B) & 0xff) the compiler folds the byte masks into the
+// mask that isolated the codes and emits a bit-field extract plus
+// v_cvt_f32_ubyte0: two instructions per value instead of one.
+template <int B> __device__ __forceinline__ float UbyteF32(uint32_t t) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(t));
+  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(t));
+  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(t));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(t));
+  return r;
 }
+
+// Four codes, one per byte of t, as floats.
+__device__ __forceinline__ void ByteFloats(uint32_t t, float *f) {
+  f[0] = UbyteF32<0>(t);
+  f[1] = UbyteF32<1>(t);
+  f[2] = UbyteF32<2>(t);
+  f[3] = UbyteF32<3>(t);
+}
+
+__device__ __forceinline__ void NibbleFloats(uint32_t dw, int sh, float *f) { ByteFloats((dw >> sh) & 0x0f0f0f0fu, f); }
 
 // The raw bytes one lane needs from one block, loaded a block ahead of use.
 template <int TYPE> struct KRaw;
@@ -1003,11 +1018,7 @@ __device__ __forceinline__ void DecodeK(const KRaw<14> &r, int i0, h2_t wp[4]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     // q = low nibble | (2 high bits << 4), as the bytes of a dword
-    const uint32_t q = ((r.l[h] >> shl) & 0x0f0f0f0fu) | (((r.hb[h] >> shh) & 0x03030303u) << 4);
-    f[4 * h] = (float)(q & 0xffu);
-    f[4 * h + 1] = (float)((q >> 8) & 0xffu);
-    f[4 * h + 2] = (float)((q >> 16) & 0xffu);
-    f[4 * h + 3] = (float)((q >> 24) & 0xffu);
+    ByteFloats(((r.l[h] >> shl) & 0x0f0f0f0fu) | (((r.hb[h] >> shh) & 0x03030303u) << 4), f + 4 * h);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -1118,13 +1129,7 @@ __device__ __forceinline__ void LoadKLds(const uint8_t *s, int o, int i0, KRaw<1
 // reference's separately rounded steps do; iq4_xs's ds * value (8-bit
 // values) is one rounded product, as in the reference.
 // Four codes at a time: one shift and mask per dword leaves each code in
-// its own byte, which v_cvt_f32_ubyte0..3 converts directly.
-__device__ __forceinline__ void ByteFloats(uint32_t t, float *f) {
-  f[0] = (float)(t & 0xffu);
-  f[1] = (float)((t >> 8) & 0xffu);
-  f[2] = (float)((t >> 16) & 0xffu);
-  f[3] = (float)(t >> 24);
-}
+// its own byte, which v_cvt_f32_ubyte0..3 converts directly (ByteFloats).
 
 __device__ __forceinline__ void DecodeK(const KRaw<10> &r, int i0, h2_t wp[4]) {
   const float d = F16ToF32((uint16_t)(r.dd & 0xffffu)), dmin = F16ToF32((uint16_t)(r.dd >> 16));
