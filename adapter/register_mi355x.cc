@@ -1551,30 +1551,34 @@ private:
   }
 
   // A weight [N, K] decoded on the GPU in the activations' dtype by `decode`
-  // (copied back), transposed to [K, N] on the host and uploaded; once per
-  // weight.
+  // into device memory and transposed to [K, N] there; once per weight, with
+  // no host copy.
   template <typename Decode>
   static void DenseFromDevice(const onnxl_amd_tensor &a, int64_t N, int64_t K, Decode &&decode, Prepared &w) {
-    const size_t count = static_cast<size_t>(N * K);
-    std::vector<uint16_t> nk(count), kn(count);
-    onnxl_amd_tensor host{};
-    host.data_type = a.data_type;
-    host.rank = 2;
-    host.dims[0] = N;
-    host.dims[1] = K;
-    host.data = nk.data();
-    host.size_bytes = static_cast<int64_t>(count * 2);
-    host.location = ONNXL_AMD_HOST;
-    Check(decode(&host));
-    for (int64_t n = 0; n < N; ++n)
-      for (int64_t k = 0; k < K; ++k) kn[static_cast<size_t>(k * N + n)] = nk[static_cast<size_t>(n * K + k)];
-    w.dense_t.Allocate(host.size_bytes);
-    CheckHip(hipMemcpy(w.dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
-    w.dense_t.desc = host;
-    w.dense_t.desc.dims[0] = K;
-    w.dense_t.desc.dims[1] = N;
+    const int64_t bytes = N * K * 2;
+    DeviceTensor nk;  // the decoded [N, K], freed once transposed
+    nk.Allocate(bytes);
+    nk.desc.data_type = a.data_type;
+    nk.desc.rank = 2;
+    nk.desc.dims[0] = N;
+    nk.desc.dims[1] = K;
+    nk.desc.data = nk.ptr;
+    nk.desc.size_bytes = bytes;
+    nk.desc.location = ONNXL_AMD_DEVICE;
+    Check(decode(&nk.desc));
+    TransposeOnDevice(nk.desc, w);
+  }
+
+  // w.dense_t = the [K, N] transpose of the device tensor nk [N, K], on the
+  // GPU (onnxl_amd_transpose_2d), complete on return.
+  static void TransposeOnDevice(const onnxl_amd_tensor &nk, Prepared &w) {
+    w.dense_t.Allocate(nk.size_bytes);
+    w.dense_t.desc = nk;
+    w.dense_t.desc.dims[0] = nk.dims[1];
+    w.dense_t.desc.dims[1] = nk.dims[0];
     w.dense_t.desc.data = w.dense_t.ptr;
-    w.dense_t.desc.location = ONNXL_AMD_DEVICE;
+    Check(onnxl_amd_transpose_2d(&nk, &w.dense_t.desc, nullptr));
+    Check(onnxl_amd_synchronize(nullptr));
   }
 
   // Any other encoding: the reference's decode in A's dtype (materializing a
@@ -1589,23 +1593,9 @@ private:
                               : rt::DequantizeTensor(value.Encoded(), catalogue, nullptr, a.data_type);
     if (nk.shape.size() != 2 || nk.data_type != a.data_type)
       throw std::invalid_argument("mi355x: DequantizeEncodedMatMul takes a 2-D encoded weight.");
-    const int64_t N = nk.shape[0], K = nk.shape[1];
-    const size_t count = static_cast<size_t>(N * K);
-    std::vector<uint16_t> kn(count);
-    const auto *src = reinterpret_cast<const uint16_t *>(nk.bytes());
-    for (int64_t n = 0; n < N; ++n)
-      for (int64_t k = 0; k < K; ++k) kn[static_cast<size_t>(k * N + n)] = src[static_cast<size_t>(n * K + k)];
     auto w = std::make_shared<Prepared>();
-    w->dense_t.Allocate(static_cast<int64_t>(count * 2));
-    if (count > 0) CheckHip(hipMemcpy(w->dense_t.ptr, kn.data(), count * 2, hipMemcpyHostToDevice), "hipMemcpy");
-    w->dense_t.desc = onnxl_amd_tensor{};
-    w->dense_t.desc.data_type = a.data_type;
-    w->dense_t.desc.rank = 2;
-    w->dense_t.desc.dims[0] = K;
-    w->dense_t.desc.dims[1] = N;
-    w->dense_t.desc.data = w->dense_t.ptr;
-    w->dense_t.desc.size_bytes = static_cast<int64_t>(count * 2);
-    w->dense_t.desc.location = ONNXL_AMD_DEVICE;
+    const auto up = UploadToHbm(nk);  // [N, K], transposed on the GPU
+    TransposeOnDevice(up->desc, *w);
     return w;
   }
 

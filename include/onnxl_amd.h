@@ -284,6 +284,14 @@ int onnxl_amd_dequantize_linear_grouped_matmul(const onnxl_amd_tensor *input, co
  * ext/kernels/kernels/tensor/kernel_cast.cc:360-370. */
 int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, void *stream);
 
+/* Transpose(x, perm = [1, 0]) of a 2-D tensor whose elements take 1, 2, 4 or
+ * 8 bytes, into the preallocated y [x.dims[1], x.dims[0]].  Replaces the 2-D
+ * case of the reference Transpose kernel, tensor/kernel_transpose.cc:98-111
+ * (its preallocated-output checks and messages); other ranks and sub-byte
+ * types return ONNXL_AMD_UNSUPPORTED.  The adapter uses it to lay a weight
+ * decoded on the GPU as [N, K] out as [K, N] without a host round trip. */
+int onnxl_amd_transpose_2d(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, void *stream);
+
 /* Fused Y = MatMul(A, [Cast(to=cast_to)](DequantizeLinear(x, x_scale,
  * x_zero_point, axis))) for a 2-D quantized weight x [K, N].  A: FLOAT16 or
  * BFLOAT16 [..., M, K]; the dequantized weight is rounded exactly as the

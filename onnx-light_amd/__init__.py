@@ -114,6 +114,7 @@ def lib() -> ctypes.CDLL:
         L.onnxl_amd_dequantize_qqq.argtypes = [I64, I64, I64, I64, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_gptqmodel_fp8.argtypes = [I64, I64, CS, ctypes.POINTER(I64), I32, TP, TP, TP,
                                                          ctypes.c_void_p]
+        L.onnxl_amd_transpose_2d.argtypes = [TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_exl3.argtypes = [TP, TP, TP, TP, TP, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_mx_weights.argtypes = [CS, TP, TP, F32, TP, ctypes.c_void_p]
         L.onnxl_amd_dequantize_vptq.argtypes = [ctypes.POINTER(VptqConfig), TP, TP, TP, TP, TP, TP, TP, TP, TP,
@@ -490,6 +491,16 @@ def dequantize_gptqmodel_fp8(weight, weight_scale_inv, method: str, block=(), co
     _check(lib().onnxl_amd_dequantize_gptqmodel_fp8(k, n, method.encode(), blk, len(block),
                                                     describe(weight, code), describe(weight_scale_inv),
                                                     describe(out), _stream_of(weight, weight_scale_inv, out)))
+    return out
+
+
+def transpose_2d(x, out=None):
+    """onnxl_amd_transpose_2d: Transpose(x, perm=[1, 0]) of a 2-D tensor."""
+    torch = _torch()
+    if out is None:
+        dt = torch.from_numpy(x[:0]).dtype if isinstance(x, np.ndarray) else x.dtype
+        out = _empty(tuple(x.shape)[::-1], dt, _device_of(x))
+    _check(lib().onnxl_amd_transpose_2d(describe(x), describe(out), _stream_of(x, out)))
     return out
 
 

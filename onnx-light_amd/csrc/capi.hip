@@ -1361,6 +1361,33 @@ int Cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, hipStream_t
 }
 
 // ---------------------------------------------------------------------------
+// Transpose of a 2-D tensor (perm [1, 0]), tensor/kernel_transpose.cc:98-111
+// (the preallocated output's checks with the reference's messages).
+
+int Transpose2d(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, hipStream_t stream) {
+  OLA_ENFORCE(!Absent(x) && y, "kernel::Transpose: input and output are required.");
+  CheckDescriptor(x, "x");
+  CheckDescriptor(y, "y");
+  if (x->rank != 2) throw Unsupported("Transpose: the GPU path transposes 2-D tensors (perm [1, 0]).");
+  const int64_t width = PackedBytes(x->data_type, 1);
+  if (PackedBytes(x->data_type, 2) != 2 * width || !(width == 1 || width == 2 || width == 4 || width == 8))
+    throw Unsupported("Transpose: the GPU path takes 1, 2, 4 or 8-byte elements.");
+  OLA_ENFORCE(y->data_type == x->data_type, "kernel::Transpose: preallocated output dtype must match input dtype.");
+  OLA_ENFORCE(y->rank == 2 && y->dims[0] == x->dims[1] && y->dims[1] == x->dims[0],
+              "kernel::Transpose: preallocated output shape mismatch.");
+  OLA_ENFORCE(y->size_bytes >= NumElements(*x) * width && y->data != nullptr,
+              "kernel::Transpose: preallocated output buffer is too small.");
+  if ((x->dims[0] + 63) / 64 > 65535 || (x->dims[1] + 63) / 64 > (int64_t(1) << 31) - 1)
+    throw Unsupported("Transpose: more than 65535 row blocks of 64.");
+  Ctx();
+  Staging st(stream, 0, {x}, {y});
+  LaunchTranspose2d(st.In(x), st.Out(y), x->dims[0], x->dims[1], (int)width, stream);
+  OLA_HIP(hipGetLastError());
+  st.Finish();
+  return ONNXL_AMD_OK;
+}
+
+// ---------------------------------------------------------------------------
 // MatMul FLOAT16 / BFLOAT16, km/kernel_matmul.cc:225-253.
 
 constexpr const char *kMmName = "kernel::MatMul";
@@ -3494,6 +3521,10 @@ int onnxl_amd_prepare_bitblas(const char *method, const onnxl_amd_tensor *qweigh
     return PrepareCkpt("prepare_bitblas", p, qweight, p.L.signed_codes ? nullptr : qzeros, scales, weight, scale,
                        zero_point, static_cast<hipStream_t>(stream));
   });
+}
+
+int onnxl_amd_transpose_2d(const onnxl_amd_tensor *x, onnxl_amd_tensor *y, void *stream) {
+  return Guard([&] { return Transpose2d(x, y, static_cast<hipStream_t>(stream)); });
 }
 
 int onnxl_amd_cast(const onnxl_amd_tensor *x, int32_t to, onnxl_amd_tensor *y, void *stream) {

@@ -90,6 +90,53 @@ void LaunchDequantize(const DequantParams &p, hipStream_t s) {
   }
 }
 
+// Transpose of a [R, C] matrix of T (1, 2, 4 or 8 bytes): one 64 x 64 tile
+// per 256-thread workgroup, read row-wise (consecutive threads on
+// consecutive columns), held in LDS with a padded pitch, written row-wise
+// in the output's order.  Tiles are dealt in row-major order over
+// (row blocks, column blocks) with the row block in blockIdx.y.
+template <typename T>
+__global__ __launch_bounds__(256) void Transpose2dKernel(const T *__restrict__ x, T *__restrict__ y, int64_t R,
+                                                         int64_t C) {
+  __shared__ T tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rr = ty + 4 * i;
+    if (r0 + rr < R && c0 + tx < C) tile[rr][tx] = x[(r0 + rr) * C + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int cc = ty + 4 * i;  // output row c0 + cc, output column r0 + tx
+    if (c0 + cc < C && r0 + tx < R) y[(c0 + cc) * R + r0 + tx] = tile[tx][cc];
+  }
+}
+
+void LaunchTranspose2d(const void *x, void *y, int64_t R, int64_t C, int elem_bytes, hipStream_t s) {
+  if (R == 0 || C == 0) return;
+  const dim3 g((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64)), b(256);
+  switch (elem_bytes) {
+  case 1:
+    hipLaunchKernelGGL(Transpose2dKernel<uint8_t>, g, b, 0, s, static_cast<const uint8_t *>(x),
+                       static_cast<uint8_t *>(y), R, C);
+    break;
+  case 2:
+    hipLaunchKernelGGL(Transpose2dKernel<uint16_t>, g, b, 0, s, static_cast<const uint16_t *>(x),
+                       static_cast<uint16_t *>(y), R, C);
+    break;
+  case 4:
+    hipLaunchKernelGGL(Transpose2dKernel<uint32_t>, g, b, 0, s, static_cast<const uint32_t *>(x),
+                       static_cast<uint32_t *>(y), R, C);
+    break;
+  default:
+    hipLaunchKernelGGL(Transpose2dKernel<uint64_t>, g, b, 0, s, static_cast<const uint64_t *>(x),
+                       static_cast<uint64_t *>(y), R, C);
+    break;
+  }
+}
+
 void LaunchCastF32(const float *x, void *y, int64_t n, int to_bf16, hipStream_t s) {
   if (n == 0) return;
   const dim3 g((unsigned)((n + (int64_t)kBlock * kPerThread - 1) / ((int64_t)kBlock * kPerThread)));

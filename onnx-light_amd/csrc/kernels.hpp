@@ -381,6 +381,8 @@ void LaunchDynamicQuantize(const float *x, int64_t n, uint8_t *y, float *y_scale
 
 // Cast FLOAT -> FLOAT16 / BFLOAT16 (round to nearest even).
 void LaunchCastF32(const float *x, void *y, int64_t n, int to_bf16, hipStream_t stream);
+// y [C, R] = x [R, C]^T, elements of 1, 2, 4 or 8 bytes (elementwise.hip)
+void LaunchTranspose2d(const void *x, void *y, int64_t R, int64_t C, int elem_bytes, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Dequantize-fused MatMul: Y[M,N] = A[M,K] @ W[K,N], W = round(deq(x)).
