@@ -1208,7 +1208,12 @@ __device__ __forceinline__ void DecodeK(const KRaw<23> &r, int i0, h2_t wp[4]) {
     const uint32_t codes = (r.q[h] >> sh) & 0x0f0f0f0fu, sel = codes & 0x07070707u;
     const uint32_t lo4 = __builtin_amdgcn_perm(0xf6eaddcfu, 0xbfad9881u, sel);
     const uint32_t hi4 = __builtin_amdgcn_perm(0x71594535u, 0x26190d01u, sel);
-    const uint32_t pick = ((codes >> 3) & 0x01010101u) * 0xffu;
+    // 0xff in each byte whose code has bit 3: (m << 8) - m, the subtraction
+    // written as one instruction (the compiler folds the pair into a
+    // quarter-rate v_mul_lo_u32 by 255)
+    const uint32_t m = (codes >> 3) & 0x01010101u;
+    uint32_t pick;
+    asm("v_sub_u32 %0, %1, %2" : "=v"(pick) : "v"(m << 8), "v"(m));
     const uint32_t vals = (hi4 & pick) | (lo4 & ~pick);
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[4 * h + e] = ds * (float)(int8_t)(uint8_t)(vals >> (8 * e));
@@ -1305,7 +1310,9 @@ __global__ __launch_bounds__(256) void GemvKLdsKernel(const uint16_t *__restrict
   constexpr int kPer = (kStageWords + 255) / 256;  // words per thread per stage
   typedef unsigned v4u __attribute__((ext_vector_type(4)));
   __shared__ __align__(16) uint8_t stage[2][kGvRows * kSlot];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index as a scalar: the per-row offsets below are then scalar
+  // work, not 64-bit vector multiplies in the decode loop
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, i0 = (lane & 31) * 8;
   const int64_t nb = K / 256;
   const int64_t n0 = (int64_t)blockIdx.x * kGvRows;
@@ -1321,20 +1328,27 @@ __global__ __launch_bounds__(256) void GemvKLdsKernel(const uint16_t *__restrict
 
   // per thread: the row and word of each of its stage words (fixed over the stages)
   int wrow[kPer], wword[kPer];
+  auto row_of = [&](int r) -> int64_t { return n0 + r < N ? n0 + r : N - 1; };  // rows past N decode the last
+  int64_t wbase[kPer];  // byte offset of the row of each stage word
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int idx = tid + 256 * j;
     wrow[j] = idx / kWords;
     wword[j] = idx - wrow[j] * kWords;
+    wbase[j] = row_of(wrow[j]) * nb * kBytes;
   }
-  auto row_of = [&](int r) -> int64_t { return n0 + r < N ? n0 + r : N - 1; };  // rows past N decode the last
+  // a decoding row's block offsets modulo 16 (its window keeps the global
+  // alignment): (row * nb * bytes) mod 16, plus the stage's part
+  int rmod[kGvCols];
+#pragma unroll
+  for (int c = 0; c < kGvCols; ++c) rmod[c] = (int)((row_of(wave * kGvCols + c) * nb * kBytes) & 15);
   v4u regs[kPer];
   auto load = [&](int s) __attribute__((always_inline)) {
     const int64_t kb0 = (int64_t)s * CB;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const bool ok = tid + 256 * j < kStageWords;
-      const int64_t start = (row_of(wrow[j]) * nb + kb0) * kBytes;
+      const int64_t start = wbase[j] + kb0 * kBytes;
       const int64_t off = (start & ~int64_t(15)) + 16 * wword[j];
       regs[j] = __builtin_bit_cast(
           v4u, __builtin_amdgcn_raw_buffer_load_b128(rsW, ok ? (unsigned)off : 0x80000000u, 0, 2));
@@ -1377,9 +1391,9 @@ __global__ __launch_bounds__(256) void GemvKLdsKernel(const uint16_t *__restrict
 #pragma unroll
         for (int c = 0; c < kGvCols; ++c) {
           const int r = wave * kGvCols + c;
-          const int64_t start = (row_of(r) * nb + kb0) * kBytes;
+          const int sm = (rmod[c] + (int)((kb0 * kBytes) & 15)) & 15;  // (row * nb + kb0) * bytes mod 16
           KRaw<TYPE> raw;
-          LoadKLds(stage[buf], r * kSlot + (int)(start & 15) + bb * kBytes, i0, raw);
+          LoadKLds(stage[buf], r * kSlot + sm + bb * kBytes, i0, raw);
           DecodeK(raw, i0, wp[c]);
         }
 #pragma unroll
